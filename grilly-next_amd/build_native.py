@@ -1,0 +1,84 @@
+"""Builds the native libraries of this package, in-tree, for gfx950.
+
+  libgn_bwd.so          HIP kernels + the C ABI declared in include/gn_bwd.h
+  grilly_core*.so       pybind11 module: tape engine (TensorRef, OpType, Node, TapeArena,
+                        BackwardEngine, TapeContext) calling libgn_bwd through the C ABI
+
+Usage: python grilly-next_amd/build_native.py   (also called by __graft_entry__.build()).
+Compiles every time it is called; objects go to grilly-next_amd/_build/.
+"""
+import os
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+INCLUDE = os.path.join(ROOT, "include")
+ARCH = os.environ.get("GN_OFFLOAD_ARCH", "gfx950")
+
+KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip",
+                  "gn_vsa.hip", "gn_attn.hip"]
+TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "bindings.cpp"]
+
+# -packed-fp32-ops off: packed fp32 VALU forms are kept out of the generated code.
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INCLUDE, "-I", CSRC,
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
+             "-Wno-unused-function", "-Wno-unused-variable"]
+
+
+def _run(cmd):
+    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in p.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if p.returncode != 0:
+        raise RuntimeError("build failed: " + " ".join(cmd) + "\n" + out)
+    return out
+
+
+def _obj(src):
+    return os.path.join(BUILD, src.replace("/", "_").rsplit(".", 1)[0] + ".o")
+
+
+def build_kernels(jobs=8):
+    os.makedirs(BUILD, exist_ok=True)
+    cmds = [["hipcc", *HIP_FLAGS, "-c", os.path.join(CSRC, s), "-o", _obj(s)]
+            for s in KERNEL_SOURCES]
+    with ThreadPoolExecutor(jobs) as ex:
+        list(ex.map(_run, cmds))
+    out = os.path.join(HERE, "libgn_bwd.so")
+    _run(["hipcc", "-shared", f"--offload-arch={ARCH}", "-o", out + ".tmp",
+          *[_obj(s) for s in KERNEL_SOURCES]])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_tape(jobs=8):
+    import pybind11
+    os.makedirs(BUILD, exist_ok=True)
+    py_inc = sysconfig.get_paths()["include"]
+    ext = sysconfig.get_config_var("EXT_SUFFIX")
+    flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I", INCLUDE, "-I", CSRC,
+             "-I", os.path.join(CSRC, "tape"), "-I", pybind11.get_include(), "-I", py_inc,
+             "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-fvisibility=hidden"]
+    cmds = [["g++", *flags, "-c", os.path.join(CSRC, s), "-o", _obj(s)] for s in TAPE_SOURCES]
+    with ThreadPoolExecutor(jobs) as ex:
+        list(ex.map(_run, cmds))
+    out = os.path.join(HERE, "grilly_core" + ext)
+    _run(["g++", "-shared", "-o", out + ".tmp", *[_obj(s) for s in TAPE_SOURCES],
+          "-L", HERE, "-lgn_bwd", "-Wl,-rpath,$ORIGIN", "-L/opt/rocm/lib", "-lamdhip64",
+          "-Wl,-rpath,/opt/rocm/lib"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def main():
+    print(build_kernels())
+    if all(os.path.exists(os.path.join(CSRC, s)) for s in TAPE_SOURCES):
+        print(build_tape())
+
+
+if __name__ == "__main__":
+    sys.exit(main())

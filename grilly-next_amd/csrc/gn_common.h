@@ -1,0 +1,119 @@
+// gn_common.h — shared device/host helpers for libgn_bwd (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <cstdio>
+#include <string>
+
+#include "gn_bwd.h"
+
+namespace gn {
+
+// ---- error reporting (thread-local message behind gn_last_error) --------------------
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define GN_REQUIRE(cond, ...)                  \
+    do {                                       \
+        if (!(cond)) {                         \
+            ::gn::set_error(__VA_ARGS__);      \
+            return GN_E_INVALID;               \
+        }                                      \
+    } while (0)
+
+#define GN_LAUNCH_CHECK(what)                                                          \
+    do {                                                                               \
+        hipError_t e_ = hipGetLastError();                                             \
+        if (e_ != hipSuccess) {                                                        \
+            ::gn::set_error("%s: launch failed: %s", what, hipGetErrorString(e_));       \
+            return GN_E_HIP;                                                           \
+        }                                                                              \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- bf16 storage helpers -------------------------------------------------------------
+typedef uint16_t bf16_t;  // raw bf16 bits in memory
+
+__device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// round-to-nearest-even float -> bf16 (NaN stays NaN)
+__device__ __forceinline__ bf16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+// pack two floats into one dword of bf16 (lo = a, hi = b)
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+template <typename T> struct io;
+template <> struct io<float> {
+    static __device__ __forceinline__ float ld(const float* p, size_t i) { return p[i]; }
+    static __device__ __forceinline__ void st(float* p, size_t i, float v) { p[i] = v; }
+};
+template <> struct io<bf16_t> {
+    static __device__ __forceinline__ float ld(const bf16_t* p, size_t i) { return bf2f(p[i]); }
+    static __device__ __forceinline__ void st(bf16_t* p, size_t i, float v) { p[i] = f2bf(v); }
+};
+
+// ---- small math (fast hardware exp; formulas from the op definitions) ----------------
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float tanhf_(float z) {
+    // tanh(z) = 1 - 2 / (exp(2z) + 1); saturates cleanly for |z| large
+    float e = __expf(2.0f * z);
+    return 1.0f - 2.0f / (e + 1.0f);
+}
+
+// ---- wave / block reductions (wave64) -------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum over a block of NW waves; `sh` must hold NW floats. Result broadcast to all threads.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) sh[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += sh[i];
+    return t;
+}
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* sh) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) sh[w] = v;
+    __syncthreads();
+    float t = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t = fmaxf(t, sh[i]);
+    return t;
+}
+
+inline unsigned grid_for(int64_t n, int per_block, unsigned cap = 65535u * 16u) {
+    int64_t g = (n + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > (int64_t)cap) g = cap;
+    return (unsigned)g;
+}
+
+}  // namespace gn

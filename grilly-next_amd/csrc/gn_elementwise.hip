@@ -1,0 +1,351 @@
+// gn_elementwise.hip — single-pass, HBM-bound gradient kernels:
+//   activation backward, GLU local gradients, fan-out accumulation, VSA surrogate loss.
+// Each thread moves 16-byte vectors; the grid is sized to ~4 waves per SIMD and strides.
+#include "gn_common.h"
+
+namespace gn {
+namespace {
+
+// ---- vector load/store of V consecutive elements as float -------------------------------
+template <typename T, int V> struct vec;
+template <> struct vec<float, 4> {
+    static __device__ __forceinline__ void ld(const float* p, float (&v)[4]) {
+        float4 x = *reinterpret_cast<const float4*>(p);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    }
+    static __device__ __forceinline__ void st(float* p, const float (&v)[4]) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+};
+template <> struct vec<bf16_t, 8> {
+    static __device__ __forceinline__ void ld(const bf16_t* p, float (&v)[8]) {
+        uint4 x = *reinterpret_cast<const uint4*>(p);
+        uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+    static __device__ __forceinline__ void st(bf16_t* p, const float (&v)[8]) {
+        uint4 x;
+        x.x = pack_bf2(v[0], v[1]);
+        x.y = pack_bf2(v[2], v[3]);
+        x.z = pack_bf2(v[4], v[5]);
+        x.w = pack_bf2(v[6], v[7]);
+        *reinterpret_cast<uint4*>(p) = x;
+    }
+};
+template <typename T, int V> struct vec {  // scalar fallback (V == 1)
+    static __device__ __forceinline__ void ld(const T* p, float (&v)[V]) {
+        for (int i = 0; i < V; ++i) v[i] = io<T>::ld(p, i);
+    }
+    static __device__ __forceinline__ void st(T* p, const float (&v)[V]) {
+        for (int i = 0; i < V; ++i) io<T>::st(p, i, v[i]);
+    }
+};
+
+// ---- activation derivatives --------------------------------------------------------------
+constexpr float kSqrt2OverPi = 0.7978845608028654f;
+constexpr float kGeluC = 0.044715f;
+
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+    return 0.5f * x * (1.0f + tanhf_(kSqrt2OverPi * (x + kGeluC * x * x * x)));
+}
+// activation-gelu-backward.glsl:38-50: 0.5 (1 + tanh z + x sech^2 z dz/dx)
+__device__ __forceinline__ float gelu_tanh_grad_f(float x) {
+    float z = kSqrt2OverPi * (x + kGeluC * x * x * x);
+    float t = tanhf_(z);
+    return 0.5f * (1.0f + t + x * (1.0f - t * t) * kSqrt2OverPi * (1.0f + 3.0f * kGeluC * x * x));
+}
+// erf form (autograd_core.py:529-542): Phi(x) + x phi(x)
+__device__ __forceinline__ float gelu_erf_grad_f(float x) {
+    return 0.5f * (1.0f + erff(x * 0.70710678118654752f)) +
+           x * 0.3989422804014327f * __expf(-0.5f * x * x);
+}
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoidf_(x); }
+__device__ __forceinline__ float silu_grad_f(float x) {
+    float s = sigmoidf_(x);
+    return s * (1.0f + x * (1.0f - s));
+}
+
+template <int KIND>
+__device__ __forceinline__ float act_grad(float x) {
+    if constexpr (KIND == GN_ACT_RELU) return x > 0.0f ? 1.0f : 0.0f;
+    else if constexpr (KIND == GN_ACT_GELU_TANH) return gelu_tanh_grad_f(x);
+    else if constexpr (KIND == GN_ACT_GELU_ERF) return gelu_erf_grad_f(x);
+    else if constexpr (KIND == GN_ACT_SILU) return silu_grad_f(x);
+    else if constexpr (KIND == GN_ACT_TANH) return 1.0f - x * x;  // x = saved tanh output
+    else return x * (1.0f - x);                                    // x = saved sigmoid output
+}
+
+template <int KIND, typename T, int V>
+__global__ __launch_bounds__(256) void act_bwd_kernel(const T* __restrict__ dY,
+                                                      const T* __restrict__ X,
+                                                      T* __restrict__ dX, int64_t nvec,
+                                                      int accumulate) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float dy[V], x[V], o[V];
+        vec<T, V>::ld(dY + i * V, dy);
+        vec<T, V>::ld(X + i * V, x);
+        if (accumulate) vec<T, V>::ld(dX + i * V, o);
+#pragma unroll
+        for (int j = 0; j < V; ++j) o[j] = (accumulate ? o[j] : 0.0f) + dy[j] * act_grad<KIND>(x[j]);
+        vec<T, V>::st(dX + i * V, o);
+    }
+}
+
+// ---- GLU local gradients (fused-{swiglu,geglu,reglu}-backward.glsl local terms) ---------
+template <int KIND>
+__device__ __forceinline__ void glu_grad(float d, float g, float u, float& dg, float& du) {
+    if constexpr (KIND == GN_GLU_SWIGLU_UP) {
+        float s = sigmoidf_(u);
+        dg = d * u * s;
+        du = d * g * s * (1.0f + u * (1.0f - s));
+    } else if constexpr (KIND == GN_GLU_SWIGLU_GATE) {
+        float s = sigmoidf_(g);
+        dg = d * u * s * (1.0f + g * (1.0f - s));
+        du = d * g * s;
+    } else if constexpr (KIND == GN_GLU_GEGLU_UP) {
+        dg = d * gelu_tanh_f(u);
+        du = d * g * gelu_tanh_grad_f(u);
+    } else if constexpr (KIND == GN_GLU_GEGLU_GATE) {
+        dg = d * u * gelu_tanh_grad_f(g);
+        du = d * gelu_tanh_f(g);
+    } else {  // REGLU_UP
+        dg = d * (u > 0.0f ? u : 0.0f);
+        du = d * g * (u > 0.0f ? 1.0f : 0.0f);
+    }
+}
+
+template <int KIND, typename T, int V>
+__global__ __launch_bounds__(256) void glu_bwd_kernel(const T* __restrict__ dO,
+                                                      const T* __restrict__ G,
+                                                      const T* __restrict__ U,
+                                                      T* __restrict__ dG, T* __restrict__ dU,
+                                                      int64_t nvec) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float d[V], g[V], u[V], og[V], ou[V];
+        vec<T, V>::ld(dO + i * V, d);
+        vec<T, V>::ld(G + i * V, g);
+        vec<T, V>::ld(U + i * V, u);
+#pragma unroll
+        for (int j = 0; j < V; ++j) glu_grad<KIND>(d[j], g[j], u[j], og[j], ou[j]);
+        vec<T, V>::st(dG + i * V, og);
+        vec<T, V>::st(dU + i * V, ou);
+    }
+}
+
+template <typename T, int V>
+__global__ __launch_bounds__(256) void add_kernel(T* __restrict__ out, const T* __restrict__ a,
+                                                  int64_t nvec) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float x[V], y[V];
+        vec<T, V>::ld(out + i * V, x);
+        vec<T, V>::ld(a + i * V, y);
+#pragma unroll
+        for (int j = 0; j < V; ++j) x[j] += y[j];
+        vec<T, V>::st(out + i * V, x);
+    }
+}
+
+// ---- VSA surrogate loss backward (vsa-surrogate-loss-backward.glsl:50-88) ---------------
+// grid (ceil(D / (256*4)), Bn); each thread owns 4 consecutive dims i (one u32 word).
+__global__ __launch_bounds__(256) void surrogate_bwd_kernel(
+    const float* __restrict__ preds, const uint32_t* __restrict__ bits,
+    const uint32_t* __restrict__ results, const float* __restrict__ weights,
+    float* __restrict__ dP, int K, int D, int words, float gamma, float delta, float lambda_c,
+    float scale, int accumulate, int vec4) {
+    const int b = blockIdx.y;
+    const int i0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= D) return;
+    const uint32_t win = results[b * 4 + 0], run = results[b * 4 + 1];
+    const float dwin = __uint_as_float(results[b * 4 + 2]);
+    const float drun = __uint_as_float(results[b * 4 + 3]);
+    const bool contrast = (win != run) && (delta - (dwin - drun) > 0.0f);
+    const float invD = 1.0f / (float)D;
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int i = i0 + j;
+        uint32_t w = (i < D) ? bits[(size_t)b * words + (i >> 5)] : 0u;
+        y[j] = ((w >> (i & 31)) & 1u) ? 1.0f : -1.0f;
+    }
+    for (int k = 0; k < K; ++k) {
+        const size_t base = ((size_t)b * K + k) * D + i0;
+        const float wk = weights[(size_t)b * K + k] * scale;
+        const float cterm = (contrast && (uint32_t)k == run) ? lambda_c * scale * invD : 0.0f;
+        float z[4], g[4];
+        if (vec4) {
+            float4 t = *reinterpret_cast<const float4*>(preds + base);
+            z[0] = t.x; z[1] = t.y; z[2] = t.z; z[3] = t.w;
+            if (accumulate) {
+                float4 a = *reinterpret_cast<const float4*>(dP + base);
+                g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
+            } else {
+                g[0] = g[1] = g[2] = g[3] = 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                z[j] = (i0 + j < D) ? preds[base + j] : 0.0f;
+                g[j] = (accumulate && i0 + j < D) ? dP[base + j] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (gamma - y[j] * z[j] > 0.0f) g[j] += (-y[j] * invD) * wk;
+            g[j] += y[j] * cterm;
+        }
+        if (vec4) {
+            *reinterpret_cast<float4*>(dP + base) = make_float4(g[0], g[1], g[2], g[3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (i0 + j < D) dP[base + j] = g[j];
+        }
+    }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int KIND, typename T>
+int launch_act(const void* dY, const void* X, void* dX, int64_t n, bool acc, hipStream_t s) {
+    constexpr int V = sizeof(T) == 4 ? 4 : 8;
+    const bool fast = (n % V == 0) && aligned16(dY) && aligned16(X) && aligned16(dX);
+    if (fast) {
+        int64_t nv = n / V;
+        act_bwd_kernel<KIND, T, V><<<grid_for(nv, 256, 8192), 256, 0, s>>>(
+            (const T*)dY, (const T*)X, (T*)dX, nv, acc ? 1 : 0);
+    } else {
+        act_bwd_kernel<KIND, T, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>(
+            (const T*)dY, (const T*)X, (T*)dX, n, acc ? 1 : 0);
+    }
+    GN_LAUNCH_CHECK("gn_act_bwd");
+    return GN_OK;
+}
+
+template <int KIND, typename T>
+int launch_glu(const void* dO, const void* g, const void* u, void* dg, void* du, int64_t n,
+               hipStream_t s) {
+    constexpr int V = sizeof(T) == 4 ? 4 : 8;
+    const bool fast = (n % V == 0) && aligned16(dO) && aligned16(g) && aligned16(u) &&
+                      aligned16(dg) && aligned16(du);
+    if (fast) {
+        int64_t nv = n / V;
+        glu_bwd_kernel<KIND, T, V><<<grid_for(nv, 256, 8192), 256, 0, s>>>(
+            (const T*)dO, (const T*)g, (const T*)u, (T*)dg, (T*)du, nv);
+    } else {
+        glu_bwd_kernel<KIND, T, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>(
+            (const T*)dO, (const T*)g, (const T*)u, (T*)dg, (T*)du, n);
+    }
+    GN_LAUNCH_CHECK("gn_glu_bwd");
+    return GN_OK;
+}
+
+template <typename T>
+int dispatch_act(int kind, const void* dY, const void* X, void* dX, int64_t n, bool acc,
+                 hipStream_t s) {
+    switch (kind) {
+        case GN_ACT_RELU: return launch_act<GN_ACT_RELU, T>(dY, X, dX, n, acc, s);
+        case GN_ACT_GELU_TANH: return launch_act<GN_ACT_GELU_TANH, T>(dY, X, dX, n, acc, s);
+        case GN_ACT_GELU_ERF: return launch_act<GN_ACT_GELU_ERF, T>(dY, X, dX, n, acc, s);
+        case GN_ACT_SILU: return launch_act<GN_ACT_SILU, T>(dY, X, dX, n, acc, s);
+        case GN_ACT_TANH: return launch_act<GN_ACT_TANH, T>(dY, X, dX, n, acc, s);
+        case GN_ACT_SIGMOID: return launch_act<GN_ACT_SIGMOID, T>(dY, X, dX, n, acc, s);
+        default: set_error("gn_act_bwd: unknown activation kind %d", kind); return GN_E_INVALID;
+    }
+}
+
+template <typename T>
+int dispatch_glu(int kind, const void* dO, const void* g, const void* u, void* dg, void* du,
+                 int64_t n, hipStream_t s) {
+    switch (kind) {
+        case GN_GLU_SWIGLU_UP: return launch_glu<GN_GLU_SWIGLU_UP, T>(dO, g, u, dg, du, n, s);
+        case GN_GLU_SWIGLU_GATE: return launch_glu<GN_GLU_SWIGLU_GATE, T>(dO, g, u, dg, du, n, s);
+        case GN_GLU_GEGLU_UP: return launch_glu<GN_GLU_GEGLU_UP, T>(dO, g, u, dg, du, n, s);
+        case GN_GLU_GEGLU_GATE: return launch_glu<GN_GLU_GEGLU_GATE, T>(dO, g, u, dg, du, n, s);
+        case GN_GLU_REGLU_UP: return launch_glu<GN_GLU_REGLU_UP, T>(dO, g, u, dg, du, n, s);
+        default: set_error("gn_glu_bwd: unknown GLU kind %d", kind); return GN_E_INVALID;
+    }
+}
+
+}  // namespace
+}  // namespace gn
+
+using namespace gn;
+
+extern "C" int gn_act_bwd(int kind, const void* dY, const void* X, void* dX, int64_t n,
+                          int dtype, unsigned flags, void* stream) {
+    clear_error();
+    GN_REQUIRE(n >= 0, "gn_act_bwd: negative n");
+    if (n == 0) return GN_OK;
+    GN_REQUIRE(dY && X && dX, "gn_act_bwd: null pointer");
+    const bool acc = flags & GN_ACCUMULATE;
+    if (dtype == GN_F32) return dispatch_act<float>(kind, dY, X, dX, n, acc, as_stream(stream));
+    if (dtype == GN_BF16) return dispatch_act<bf16_t>(kind, dY, X, dX, n, acc, as_stream(stream));
+    set_error("gn_act_bwd: dtype %d not supported (f32, bf16)", dtype);
+    return GN_E_INVALID;
+}
+
+extern "C" int gn_glu_bwd(int kind, const void* dO, const void* gate, const void* up,
+                          void* dGate, void* dUp, int64_t n, int dtype, void* stream) {
+    clear_error();
+    GN_REQUIRE(n >= 0, "gn_glu_bwd: negative n");
+    if (n == 0) return GN_OK;
+    GN_REQUIRE(dO && gate && up && dGate && dUp, "gn_glu_bwd: null pointer");
+    if (dtype == GN_F32)
+        return dispatch_glu<float>(kind, dO, gate, up, dGate, dUp, n, as_stream(stream));
+    if (dtype == GN_BF16)
+        return dispatch_glu<bf16_t>(kind, dO, gate, up, dGate, dUp, n, as_stream(stream));
+    set_error("gn_glu_bwd: dtype %d not supported (f32, bf16)", dtype);
+    return GN_E_INVALID;
+}
+
+extern "C" int gn_add_inplace(void* out, const void* a, int64_t n, int dtype, void* stream) {
+    clear_error();
+    GN_REQUIRE(n >= 0, "gn_add_inplace: negative n");
+    if (n == 0) return GN_OK;
+    GN_REQUIRE(out && a, "gn_add_inplace: null pointer");
+    hipStream_t s = as_stream(stream);
+    const bool al = aligned16(out) && aligned16(a);
+    if (dtype == GN_F32) {
+        if (al && n % 4 == 0)
+            add_kernel<float, 4><<<grid_for(n / 4, 256, 8192), 256, 0, s>>>((float*)out, (const float*)a, n / 4);
+        else
+            add_kernel<float, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>((float*)out, (const float*)a, n);
+    } else if (dtype == GN_BF16) {
+        if (al && n % 8 == 0)
+            add_kernel<bf16_t, 8><<<grid_for(n / 8, 256, 8192), 256, 0, s>>>((bf16_t*)out, (const bf16_t*)a, n / 8);
+        else
+            add_kernel<bf16_t, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>((bf16_t*)out, (const bf16_t*)a, n);
+    } else {
+        set_error("gn_add_inplace: dtype %d not supported", dtype);
+        return GN_E_INVALID;
+    }
+    GN_LAUNCH_CHECK("gn_add_inplace");
+    return GN_OK;
+}
+
+extern "C" int gn_vsa_surrogate_bwd(const float* preds, const uint32_t* bits,
+                                    const uint32_t* results, const float* weights,
+                                    float* dPreds, int Bn, int K, int D, int words, float gamma,
+                                    float delta, float lambda_c, float scale, unsigned flags,
+                                    void* stream) {
+    clear_error();
+    GN_REQUIRE(Bn >= 0 && K >= 0 && D >= 0, "gn_vsa_surrogate_bwd: negative size");
+    if (Bn == 0 || K == 0 || D == 0) return GN_OK;
+    GN_REQUIRE(preds && bits && results && weights && dPreds, "gn_vsa_surrogate_bwd: null pointer");
+    GN_REQUIRE(words >= (D + 31) / 32, "gn_vsa_surrogate_bwd: words %d < ceil(D/32)", words);
+    GN_REQUIRE(Bn <= 65535, "gn_vsa_surrogate_bwd: Bn %d exceeds grid.y limit 65535", Bn);
+    const int vec4 = (D % 4 == 0) && aligned16(preds) && aligned16(dPreds);
+    dim3 grid((D + 1023) / 1024, Bn);
+    surrogate_bwd_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+        preds, bits, results, weights, dPreds, K, D, words, gamma, delta, lambda_c, scale,
+        (flags & GN_ACCUMULATE) ? 1 : 0, vec4);
+    GN_LAUNCH_CHECK("gn_vsa_surrogate_bwd");
+    return GN_OK;
+}

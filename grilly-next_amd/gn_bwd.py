@@ -1,0 +1,326 @@
+"""Python front-end of libgn_bwd.so (the C ABI in include/gn_bwd.h).
+
+Device memory and streams come from PyTorch (ROCm build): every function takes torch
+tensors that already live on the GPU, passes their raw pointers and the current HIP
+stream to the C entry point, and raises GnError on a non-zero status.  There is no CPU
+fallback: if the library or a GPU is missing, the call fails loudly.
+
+Function names and argument meaning mirror the reference's backward ops
+(src/grilly_next/backend/autograd_core.py:486-654, VulkanBackwardOps) where they exist.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgn_bwd.so")
+
+F32, F16, U32, I32, BF16 = 0, 1, 2, 3, 4
+ACCUMULATE, LN_STAT_VAR = 1, 2
+ACT = {"relu": 0, "gelu_tanh": 1, "gelu_erf": 2, "silu": 3, "tanh": 4, "sigmoid": 5}
+GLU = {"swiglu_up": 0, "swiglu_gate": 1, "geglu_up": 2, "geglu_gate": 3, "reglu_up": 4}
+ROPE = {"none": 0, "interleaved": 1, "half": 2}
+
+# exported symbols, in the order include/gn_bwd.h declares them
+SYMBOLS = [
+    "gn_last_error", "gn_version", "gn_linear_bwd", "gn_gemm", "gn_colsum", "gn_act_bwd",
+    "gn_glu_bwd", "gn_glu_linear_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
+    "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
+    "gn_attn_workspace_bytes", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
+    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_add_inplace",
+]
+
+
+class GnError(RuntimeError):
+    pass
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_U = ctypes.c_uint
+_F = ctypes.c_float
+_L = ctypes.c_int64
+_Z = ctypes.c_size_t
+
+_SIGS = {
+    "gn_last_error": ([], ctypes.c_char_p),
+    "gn_version": ([], ctypes.c_char_p),
+    "gn_linear_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
+    "gn_gemm": ([_P, _P, _I, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _U, _P], _I),
+    "gn_colsum": ([_P, _P, _I, _I, _I, _U, _P], _I),
+    "gn_act_bwd": ([_I, _P, _P, _P, _L, _I, _U, _P], _I),
+    "gn_glu_bwd": ([_I, _P, _P, _P, _P, _P, _L, _I, _P], _I),
+    "gn_glu_linear_bwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                           _U, _P], _I),
+    "gn_layernorm_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P, _Z, _P], _I),
+    "gn_rmsnorm_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _U, _P, _Z, _P], _I),
+    "gn_norm_workspace_bytes": ([_I, _I], _Z),
+    "gn_softmax_bwd": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "gn_xent_bwd": ([_P, _P, _P, _I, _I, _F, _I, _P], _I),
+    "gn_attn_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P,
+                     _Z, _P], _I),
+    "gn_attn_workspace_bytes": ([_I, _I, _I, _I], _Z),
+    "gn_attn_fwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P, _Z, _P], _I),
+    "gn_vsa_unpack_project_bwd": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _U, _P, _Z, _P], _I),
+    "gn_vsa_workspace_bytes": ([_I, _I], _Z),
+    "gn_vsa_surrogate_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F, _U, _P], _I),
+    "gn_add_inplace": ([_P, _P, _L, _I, _P], _I),
+}
+
+
+def lib():
+    """Load libgn_bwd.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise GnError(f"{LIB_PATH} is missing: run python grilly-next_amd/build_native.py")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            fn = getattr(l, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = l
+    return _lib
+
+
+def last_error() -> str:
+    return lib().gn_last_error().decode()
+
+
+def version() -> str:
+    return lib().gn_version().decode()
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise GnError(f"{what} failed ({rc}): {last_error()}")
+
+
+# ---------------------------------------------------------------------------------------
+import torch  # noqa: E402  (plumbing: device memory and streams)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise GnError("tensor is not on the GPU")
+    if not t.is_contiguous():
+        raise GnError("tensor must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dt(t):
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise GnError(f"unsupported dtype {t.dtype}")
+
+
+def workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def linear_bwd(dY, X, W, need_dx=True, need_db=True, dX=None, dW=None, db=None, accumulate=False):
+    """(dX, dW, db) for y = X W^T + b.  bf16 inputs give bf16 dX and fp32 dW, db."""
+    M, N = dY.shape
+    K = X.shape[1]
+    dt = _dt(dY)
+    if need_dx and dX is None:
+        dX = torch.empty((M, K), dtype=dY.dtype, device=dY.device)
+    if dW is None:
+        dW = torch.empty((N, K), dtype=torch.float32, device=dY.device)
+    if need_db and db is None:
+        db = torch.empty((N,), dtype=torch.float32, device=dY.device)
+    _check(lib().gn_linear_bwd(_ptr(dY), _ptr(X), _ptr(W), _ptr(dX) if need_dx else None,
+                               _ptr(dW), _ptr(db) if need_db else None, M, N, K, dt,
+                               ACCUMULATE if accumulate else 0, _stream()), "gn_linear_bwd")
+    return (dX if need_dx else None), dW, (db if need_db else None)
+
+
+def gemm(A0, B0, transA=False, transB=False, A1=None, B1=None, out_dtype=None, C=None,
+         accumulate=False):
+    K0 = A0.shape[0] if transA else A0.shape[1]
+    M = A0.shape[1] if transA else A0.shape[0]
+    N = B0.shape[0] if transB else B0.shape[1]
+    K1 = 0
+    if A1 is not None:
+        K1 = A1.shape[0] if transA else A1.shape[1]
+    dt = _dt(A0)
+    out_dtype = out_dtype or A0.dtype
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=A0.device)
+    _check(lib().gn_gemm(_ptr(A0), _ptr(B0), K0, _ptr(A1), _ptr(B1), K1, _ptr(C), M, N,
+                         int(transA), int(transB), dt, _dt(C), ACCUMULATE if accumulate else 0,
+                         _stream()), "gn_gemm")
+    return C
+
+
+def colsum(x, out=None, accumulate=False):
+    M, N = x.shape
+    if out is None:
+        out = torch.empty((N,), dtype=torch.float32, device=x.device)
+    _check(lib().gn_colsum(_ptr(x), _ptr(out), M, N, _dt(x), ACCUMULATE if accumulate else 0,
+                           _stream()), "gn_colsum")
+    return out
+
+
+def act_bwd(kind, dY, X, dX=None, accumulate=False):
+    if dX is None:
+        dX = torch.empty_like(dY)
+    _check(lib().gn_act_bwd(ACT[kind], _ptr(dY), _ptr(X), _ptr(dX), dY.numel(), _dt(dY),
+                            ACCUMULATE if accumulate else 0, _stream()), "gn_act_bwd")
+    return dX
+
+
+def glu_bwd(kind, dO, gate, up, dGate=None, dUp=None):
+    dGate = torch.empty_like(dO) if dGate is None else dGate
+    dUp = torch.empty_like(dO) if dUp is None else dUp
+    _check(lib().gn_glu_bwd(GLU[kind], _ptr(dO), _ptr(gate), _ptr(up), _ptr(dGate), _ptr(dUp),
+                            dO.numel(), _dt(dO), _stream()), "gn_glu_bwd")
+    return dGate, dUp
+
+
+def glu_linear_bwd(kind, dO, gate, up, X, Wg, Wu, need_dx=True, need_db=False, gu_ws=None):
+    """Fused GLU-projection backward: (dX, dWg, dWu, dbg, dbu)."""
+    M, H = dO.shape
+    K = X.shape[1]
+    dev = dO.device
+    dX = torch.empty((M, K), dtype=dO.dtype, device=dev) if need_dx else None
+    dWg = torch.empty((H, K), dtype=torch.float32, device=dev)
+    dWu = torch.empty((H, K), dtype=torch.float32, device=dev)
+    dbg = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
+    dbu = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
+    if gu_ws is None:
+        gu_ws = torch.empty((2, M, H), dtype=dO.dtype, device=dev)
+    _check(lib().gn_glu_linear_bwd(GLU[kind], _ptr(dO), _ptr(gate), _ptr(up), _ptr(X), _ptr(Wg),
+                                   _ptr(Wu), _ptr(dX), _ptr(dWg), _ptr(dWu), _ptr(dbg),
+                                   _ptr(dbu), _ptr(gu_ws), M, K, H, _dt(dO), 0, _stream()),
+           "gn_glu_linear_bwd")
+    return dX, dWg, dWu, dbg, dbu
+
+
+def norm_workspace_bytes(rows, F):
+    return int(lib().gn_norm_workspace_bytes(rows, F))
+
+
+def layernorm_bwd(dY, X, gamma, mean, rstd, eps=1e-5, stat_is_var=False, ws=None,
+                  need_param=True):
+    rows, F = X.shape
+    dX = torch.empty_like(X)
+    dG = torch.empty((F,), dtype=torch.float32, device=X.device) if need_param else None
+    dB = torch.empty((F,), dtype=torch.float32, device=X.device) if need_param else None
+    if ws is None:
+        ws = workspace(norm_workspace_bytes(rows, F), X.device)
+    _check(lib().gn_layernorm_bwd(_ptr(dY), _ptr(X), _ptr(gamma), _ptr(mean), _ptr(rstd),
+                                  _ptr(dX), _ptr(dG), _ptr(dB), rows, F, eps, _dt(X),
+                                  LN_STAT_VAR if stat_is_var else 0, _ptr(ws), ws.numel(),
+                                  _stream()), "gn_layernorm_bwd")
+    return dX, dG, dB
+
+
+def rmsnorm_bwd(dY, X, w, rstd, ws=None, need_param=True, dX=None, dW=None):
+    rows, F = X.shape
+    dX = torch.empty_like(X) if dX is None else dX
+    if need_param and dW is None:
+        dW = torch.empty((F,), dtype=torch.float32, device=X.device)
+    if ws is None:
+        ws = workspace(norm_workspace_bytes(rows, F), X.device)
+    _check(lib().gn_rmsnorm_bwd(_ptr(dY), _ptr(X), _ptr(w), _ptr(rstd), _ptr(dX),
+                                _ptr(dW) if need_param else None, rows, F, _dt(X), 0, _ptr(ws),
+                                ws.numel(), _stream()), "gn_rmsnorm_bwd")
+    return dX, (dW if need_param else None)
+
+
+def softmax_bwd(dY, Y):
+    rows, C = Y.shape
+    dX = torch.empty_like(Y)
+    _check(lib().gn_softmax_bwd(_ptr(dY), _ptr(Y), _ptr(dX), rows, C, _dt(Y), _stream()),
+           "gn_softmax_bwd")
+    return dX
+
+
+def xent_bwd(logits, targets, scale=1.0, dLogits=None):
+    rows, C = logits.shape
+    dLogits = torch.empty_like(logits) if dLogits is None else dLogits
+    t = targets.to(torch.int32).contiguous()
+    _check(lib().gn_xent_bwd(_ptr(logits), _ptr(t), _ptr(dLogits), rows, C, scale, _dt(logits),
+                             _stream()), "gn_xent_bwd")
+    return dLogits
+
+
+def attn_workspace_bytes(B, H, S, D):
+    return int(lib().gn_attn_workspace_bytes(B, H, S, D))
+
+
+def attn_bwd(Q, K, V, O, dO, LSE, scale=None, causal=True, rope="interleaved", theta=10000.0,
+             ws=None, out=None):
+    B, H, S, D = Q.shape
+    scale = D ** -0.5 if scale is None else scale
+    dQ, dK, dV = out if out is not None else (torch.empty_like(Q), torch.empty_like(K),
+                                              torch.empty_like(V))
+    if ws is None:
+        ws = workspace(attn_workspace_bytes(B, H, S, D), Q.device)
+    _check(lib().gn_attn_bwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(LSE), _ptr(dQ),
+                             _ptr(dK), _ptr(dV), B, H, S, D, scale, int(causal), ROPE[rope],
+                             theta, _dt(Q), _ptr(ws), ws.numel(), _stream()), "gn_attn_bwd")
+    return dQ, dK, dV
+
+
+def attn_fwd(Q, K, V, scale=None, causal=True, rope="interleaved", theta=10000.0, ws=None):
+    B, H, S, D = Q.shape
+    scale = D ** -0.5 if scale is None else scale
+    O = torch.empty_like(Q)
+    LSE = torch.empty((B, H, S), dtype=torch.float32, device=Q.device)
+    if ws is None:
+        ws = workspace(attn_workspace_bytes(B, H, S, D), Q.device)
+    _check(lib().gn_attn_fwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(LSE), B, H, S, D, scale,
+                             int(causal), ROPE[rope], theta, _dt(Q), _ptr(ws), ws.numel(),
+                             _stream()), "gn_attn_fwd")
+    return O, LSE
+
+
+def vsa_unpack_project_bwd(dY, bits, D, need_db=True, dW=None, db=None, accumulate=False):
+    Bn, O = dY.shape
+    words = bits.shape[1]
+    if dW is None:
+        dW = torch.empty((O, D), dtype=torch.float32, device=dY.device)
+    if need_db and db is None:
+        db = torch.empty((O,), dtype=torch.float32, device=dY.device)
+    _check(lib().gn_vsa_unpack_project_bwd(_ptr(dY), _ptr(bits), _ptr(dW),
+                                           _ptr(db) if need_db else None, Bn, O, D, words,
+                                           _dt(dY), ACCUMULATE if accumulate else 0, None, 0,
+                                           _stream()), "gn_vsa_unpack_project_bwd")
+    return dW, (db if need_db else None)
+
+
+def vsa_surrogate_bwd(preds, bits, results, weights, gamma=1.0, delta=1.0, lambda_c=0.3,
+                      scale=1.0, dPreds=None, accumulate=False):
+    Bn, K, D = preds.shape
+    words = bits.shape[1]
+    dPreds = torch.empty_like(preds) if dPreds is None else dPreds
+    _check(lib().gn_vsa_surrogate_bwd(_ptr(preds), _ptr(bits), _ptr(results), _ptr(weights),
+                                      _ptr(dPreds), Bn, K, D, words, gamma, delta, lambda_c,
+                                      scale, ACCUMULATE if accumulate else 0, _stream()),
+           "gn_vsa_surrogate_bwd")
+    return dPreds
+
+
+def add_inplace(out, a):
+    _check(lib().gn_add_inplace(_ptr(out), _ptr(a), out.numel(), _dt(out), _stream()),
+           "gn_add_inplace")
+    return out
+
+
+def u32_tensor(arr, device):
+    """numpy uint32 -> device tensor holding the same bits (torch has no uint32 kernels)."""
+    import numpy as np
+    a = np.ascontiguousarray(arr, dtype=np.uint32)
+    return torch.from_numpy(a.view(np.int32)).to(device)

@@ -1,0 +1,215 @@
+/*
+ * gn_bwd.h — C ABI of the MI355X (gfx950) backward-kernel library libgn_bwd.so.
+ *
+ * This is the drop-in boundary between grilly-next's tape engine and the
+ * gradient kernels.  In the reference every per-op handler
+ * `BackwardEngine::backward_<op>(Node*)` (cpp/include/grilly/autograd/autograd.h:340-373,
+ * selected by the switch at cpp/src/autograd.cpp:95-130) binds descriptor sets and
+ * dispatches GLSL passes with a fence wait per pass.  Here the same handlers call one
+ * entry point per op, below.  Every entry point:
+ *
+ *   - takes raw device pointers (row-major, contiguous), sizes, a dtype code and a
+ *     hipStream_t passed as `void*` (NULL = the legacy default stream);
+ *   - enqueues its kernels on that stream and returns without synchronising;
+ *   - allocates nothing: scratch space is passed in by the caller (`ws`, sized by the
+ *     matching *_workspace_bytes query);
+ *   - returns GN_OK (0) or a negative GN_E* code; gn_last_error() then gives a
+ *     message (thread-local).  The library throws no C++ exceptions across this ABI.
+ *
+ * Shapes follow the reference: X [M x K], W [N x K] (y = X W^T + b), dY [M x N],
+ * dW [N x K], attention tensors [B, H, S, D], VSA dW [O x D].
+ *
+ * dtype codes extend TensorRef.dtype (autograd.h:50): 0 = f32, 1 = f16, 2 = u32,
+ * 3 = i32, 4 = bf16.  "bf16 path" below means bf16 activations/weights, fp32
+ * accumulation, bf16 activation gradients and fp32 parameter gradients.
+ */
+#ifndef GN_BWD_H
+#define GN_BWD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------- */
+#define GN_OK 0
+#define GN_E_INVALID (-1)   /* bad size, null pointer, unsupported dtype/kind */
+#define GN_E_HIP (-2)       /* a HIP runtime call or kernel launch failed */
+#define GN_E_WORKSPACE (-3) /* workspace missing or too small */
+
+/* ---- dtype codes (TensorRef.dtype, autograd.h:50, plus bf16) ------------------------ */
+#define GN_F32 0
+#define GN_F16 1
+#define GN_U32 2
+#define GN_I32 3
+#define GN_BF16 4
+
+/* ---- flags ------------------------------------------------------------------------ */
+#define GN_ACCUMULATE 1u  /* add into existing gradients (fan-out) instead of overwriting */
+#define GN_LN_STAT_VAR 2u /* layernorm: `rstd` argument holds the biased variance */
+
+/* ---- activation kinds (gn_act_bwd) ------------------------------------------------- */
+#define GN_ACT_RELU 0      /* dx = dy*[x>0]            activation-relu-backward.glsl:33-37 */
+#define GN_ACT_GELU_TANH 1 /* tanh-form GELU'(x)        activation-gelu-backward.glsl:38-50 */
+#define GN_ACT_GELU_ERF 2  /* erf-form GELU'(x)         autograd_core.py:529-542 */
+#define GN_ACT_SILU 3      /* sig(x)(1+x(1-sig(x)))     activation-silu-backward.glsl:25-42 */
+#define GN_ACT_TANH 4      /* input = saved tanh output t: dy*(1-t^2)  activation-tanh-backward.glsl:33 */
+#define GN_ACT_SIGMOID 5   /* input = saved sigmoid output s: dy*s*(1-s) */
+
+/* ---- GLU kinds (gn_glu_bwd, gn_glu_linear_bwd) -------------------------------------- */
+#define GN_GLU_SWIGLU_UP 0   /* out = gate*SiLU(up)     fused-swiglu-backward.glsl:99-100 */
+#define GN_GLU_SWIGLU_GATE 1 /* out = SiLU(gate)*up     swiglu-fused.glsl:60-64 */
+#define GN_GLU_GEGLU_UP 2    /* out = gate*GELU_tanh(up) fused-geglu-backward.glsl:101-103 */
+#define GN_GLU_GEGLU_GATE 3  /* out = GELU_tanh(gate)*up */
+#define GN_GLU_REGLU_UP 4    /* out = gate*ReLU(up)     fused-reglu-backward.glsl:83-86 */
+
+/* ---- RoPE modes (gn_attn_bwd) ------------------------------------------------------- */
+#define GN_ROPE_NONE 0
+#define GN_ROPE_INTERLEAVED 1 /* pairs (2i,2i+1)         flash-attention2-rope.glsl:101-141 */
+#define GN_ROPE_HALF 2        /* pairs (i, i+D/2)        rope.glsl:74-125 */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* gn_last_error(void);
+
+/* Library version string and the gfx target it was built for. */
+const char* gn_version(void);
+
+/* ---- linear ----------------------------------------------------------------------- */
+/* Replaces BackwardEngine::backward_linear / backward_linear_chunked
+ * (cpp/src/autograd.cpp:172-483) and fnn-linear-backward.glsl:43-89.
+ *   dX = dY W      [M x K]  (skipped when dX == NULL: input needs no grad, autograd.cpp:259)
+ *   dW = dY^T X    [N x K]
+ *   db = sum_rows dY [N]    (skipped when db == NULL)
+ * dtype GN_F32: all fp32.  GN_BF16: dY, X, W, dX bf16; dW, db fp32.
+ * flags: GN_ACCUMULATE adds into dX, dW, db. */
+int gn_linear_bwd(const void* dY, const void* X, const void* W, void* dX, void* dW, void* db,
+                  int M, int N, int K, int dtype, unsigned flags, void* stream);
+
+/* Plain GEMM entry used by the linear handler and exported for tests/benchmarks:
+ *   C[M x N] (+)= sum_s op(A_s) op(B_s), with up to two K-segments s (the second may be NULL).
+ *   transA = 0: A_s is [M x Ks] row-major;  transA = 1: A_s is stored [Ks x M] (i.e. A_s^T).
+ *   transB = 0: B_s is [Ks x N] row-major;  transB = 1: B_s is stored [N x Ks].
+ * dtype GN_BF16: A, B bf16, fp32 accumulation, C is bf16 (c_dtype GN_BF16) or fp32 (GN_F32).
+ * dtype GN_F32: all fp32. */
+int gn_gemm(const void* A0, const void* B0, int K0, const void* A1, const void* B1, int K1,
+            void* C, int M, int N, int transA, int transB, int dtype, int c_dtype,
+            unsigned flags, void* stream);
+
+/* Column sums: out[N] (+)= sum_rows in[M x N] (fp32 out; in is f32 or bf16). */
+int gn_colsum(const void* in, float* out, int M, int N, int dtype, unsigned flags, void* stream);
+
+/* ---- activations ------------------------------------------------------------------ */
+/* Replaces backward_gelu (autograd.cpp:485-537) and the relu/silu/tanh/sigmoid stubs
+ * (autograd.cpp:551-575); shaders activation-{relu,gelu,silu,tanh}-backward.glsl.
+ * dX = dY * act'(X) elementwise over n elements (dtype f32 or bf16 for all three). */
+int gn_act_bwd(int kind, const void* dY, const void* X, void* dX, int64_t n, int dtype,
+               unsigned flags, void* stream);
+
+/* ---- GLU ---------------------------------------------------------------------------- */
+/* Elementwise GLU gradient (the local-gradient part of fused-{swiglu,geglu,reglu}-
+ * backward.glsl, e.g. fused-swiglu-backward.glsl:93-100):
+ *   dGate = dO * d(out)/d(gate),  dUp = dO * d(out)/d(up),  n elements. */
+int gn_glu_bwd(int kind, const void* dO, const void* gate, const void* up, void* dGate,
+               void* dUp, int64_t n, int dtype, void* stream);
+
+/* Full fused GLU-projection backward (fused-swiglu-backward.glsl:82-160 and the GEGLU/
+ * ReGLU twins): with gate = X Wg^T (+bg), up = X Wu^T (+bu), out = glu(gate, up) [M x H]:
+ *   dGate, dUp -> written to the caller's gu_ws [2 x M x H] (dtype of the path)
+ *   dX  = dGate Wg + dUp Wu    [M x K]  (skipped when dX == NULL)
+ *   dWg = dGate^T X, dWu = dUp^T X  [H x K] (fp32 on the bf16 path)
+ *   dbg, dbu = column sums      [H]     (skipped when NULL)
+ * gu_ws must hold 2*M*H elements of `dtype`. */
+int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, const void* up,
+                      const void* X, const void* Wg, const void* Wu, void* dX, void* dWg,
+                      void* dWu, void* dbg, void* dbu, void* gu_ws, int M, int K, int H,
+                      int dtype, unsigned flags, void* stream);
+
+/* ---- normalisation ---------------------------------------------------------------- */
+/* LayerNorm backward, textbook form (autograd_core.py:591-609; fnn-layernorm-backward.glsl
+ * :58-159 restructured, with its gamma placement corrected).  mean/rstd fp32 [rows];
+ * with GN_LN_STAT_VAR the `rstd` array holds the biased variance and eps is applied.
+ * dGamma, dBeta fp32 [F] (either may be NULL). ws: gn_norm_workspace_bytes(rows, F). */
+int gn_layernorm_bwd(const void* dY, const void* X, const void* gamma, const float* mean,
+                     const float* rstd, void* dX, float* dGamma, float* dBeta, int rows,
+                     int F, float eps, int dtype, unsigned flags, void* ws, size_t ws_bytes,
+                     void* stream);
+
+/* RMSNorm backward (no handler in the reference, autograd.cpp:126-128; forward
+ * rms-norm.glsl:34-70): y = x * r * w with r = rsqrt(mean(x^2)+eps) given as rstd [rows].
+ *   dx = r*w*dy - x * r^3 * mean_j(w_j dy_j x_j);  dw = sum_rows dy * x * r. */
+int gn_rmsnorm_bwd(const void* dY, const void* X, const void* w, const float* rstd, void* dX,
+                   float* dW, int rows, int F, int dtype, unsigned flags, void* ws,
+                   size_t ws_bytes, void* stream);
+
+size_t gn_norm_workspace_bytes(int rows, int F);
+
+/* ---- softmax / cross-entropy --------------------------------------------------------- */
+/* activation-softmax-backward.glsl:27-49: dX = Y * (dY - sum_c dY*Y), per row of C. */
+int gn_softmax_bwd(const void* dY, const void* Y, void* dX, int rows, int C, int dtype,
+                   void* stream);
+
+/* cross-entropy-backward.glsl:29-84: dLogits = scale * (softmax(logits) - onehot(target)).
+ * targets int32 [rows]; scale = 1 reproduces the reference (no 1/B). A target outside
+ * [0, C) contributes no one-hot term (the row gets scale*softmax). */
+int gn_xent_bwd(const void* logits, const int32_t* targets, void* dLogits, int rows, int C,
+                float scale, int dtype, void* stream);
+
+/* ---- attention ------------------------------------------------------------------------ */
+/* Attention backward (attention-backward.glsl:73-194 semantics; RoPE of
+ * flash-attention2-rope.glsl:73-145 applied to Q and K inside; causal mask j <= i).
+ * Q, K, V, O, dO, dQ, dK, dV: [B, H, S, D]; LSE fp32 [B*H*S] = log sum_j exp(scale*q.k_j).
+ * Q and K are the *pre-rotation* tensors; dQ, dK are gradients w.r.t. them.
+ * rope_theta = base (10000); positions are 0..S-1.
+ * ws: gn_attn_workspace_bytes(B, H, S, D). D must be 64 or 128 on the bf16 path. */
+int gn_attn_bwd(const void* Q, const void* K, const void* V, const void* O, const void* dO,
+                const float* LSE, void* dQ, void* dK, void* dV, int B, int H, int S, int D,
+                float scale, int causal, int rope_mode, float rope_theta, int dtype,
+                void* ws, size_t ws_bytes, void* stream);
+
+size_t gn_attn_workspace_bytes(int B, int H, int S, int D);
+
+/* Attention forward producing the saved-tensor contract of the backward (O and the fp32
+ * row logsumexp; flash-attention2-rope.glsl:165-247 semantics plus the causal mask).
+ * Same arguments as gn_attn_bwd; ws as sized by gn_attn_workspace_bytes (needed only
+ * when rope_mode != GN_ROPE_NONE). */
+int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O, float* LSE, int B,
+                int H, int S, int D, float scale, int causal, int rope_mode,
+                float rope_theta, int dtype, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- VSA ------------------------------------------------------------------------------ */
+/* backward_vsa_unpack_project (autograd.cpp:727-815), vsa-unpack-project-backward.glsl:42-74:
+ *   s_b(j) = bit (j&31) of word X[b, j>>5] ? +1 : -1
+ *   dW[o, j] (+)= sum_b dY[b, o] * s_b(j)   [O x D] fp32
+ *   db[o]    (+)= sum_b dY[b, o]            [O] fp32 (skipped if NULL)
+ * dY fp32 [Bn x O] (dtype GN_F32, fp32-accurate via a two-term bf16 split of dY) or bf16.
+ * words = D/32 (D must be a multiple of 32). ws: gn_vsa_workspace_bytes(Bn, O). */
+int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, float* dW, float* db,
+                              int Bn, int O, int D, int words, int dtype, unsigned flags,
+                              void* ws, size_t ws_bytes, void* stream);
+
+size_t gn_vsa_workspace_bytes(int Bn, int O);
+
+/* vsa-surrogate-loss-backward.glsl:50-88 (dispatch_vsa_loss_backward_with_buf,
+ * vsa_loss_node.cpp:182-228):
+ *   for each k, i: if gamma - y_i z[b,k,i] > 0: g[b,k,i] += -y_i/D * w[b,k] * scale
+ *   if win != run and delta - (dot_win - dot_run) > 0: g[b,run,i] += y_i/D * lambda * scale
+ * preds fp32 [Bn x K x D]; bits [Bn x words]; results u32 [Bn x 4] =
+ * {win, run, f32bits(dot_win), f32bits(dot_run)}; weights fp32 [Bn x K].
+ * Without GN_ACCUMULATE the output is overwritten (no memset needed). */
+int gn_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32_t* results,
+                         const float* weights, float* dPreds, int Bn, int K, int D, int words,
+                         float gamma, float delta, float lambda_c, float scale, unsigned flags,
+                         void* stream);
+
+/* ---- misc ------------------------------------------------------------------------------ */
+/* out[i] (+)= a[i] (f32/bf16): the fan-out accumulation the reference leaves as a TODO
+ * (autograd.cpp:78-86). */
+int gn_add_inplace(void* out, const void* a, int64_t n, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GN_BWD_H */

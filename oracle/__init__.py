@@ -1,0 +1,326 @@
+"""numpy front-end of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg as the checker / CPU baseline.  The product path never imports it.
+Every function returns fresh fp32 numpy arrays; see oracle.h for the reference file:line
+each one restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+ACT = {"relu": 0, "gelu_tanh": 1, "gelu_erf": 2, "silu": 3, "tanh": 4, "sigmoid": 5}
+GLU = {"swiglu_up": 0, "swiglu_gate": 1, "geglu_up": 2, "geglu_gate": 3, "reglu_up": 4}
+ROPE = {"none": 0, "interleaved": 1, "half": 2}
+
+
+def build() -> None:
+    subprocess.check_call(["make", "-s", "-C", _HERE])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+    return _lib
+
+
+def _f(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _u(a):
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _i(a):
+    a = np.ascontiguousarray(a, dtype=np.int32)
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _out(shape):
+    a = np.empty(shape, dtype=np.float32)
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())
+
+
+def linear_bwd(dY, X, W, need_dx=True, need_db=True):
+    M, N = dY.shape
+    K = X.shape[1]
+    dY, pdy = _f(dY)
+    X, px = _f(X)
+    W, pw = _f(W)
+    dX, pdx = _out((M, K)) if need_dx else (None, None)
+    dW, pdw = _out((N, K))
+    db, pdb = _out((N,)) if need_db else (None, None)
+    lib().or_linear_bwd(pdy, px, pw, pdx, pdw, pdb, M, N, K)
+    return dX, dW, db
+
+
+def linear_fwd(X, W, b=None):
+    M, K = X.shape
+    N = W.shape[0]
+    X, px = _f(X)
+    W, pw = _f(W)
+    pb = None
+    if b is not None:
+        b, pb = _f(b)
+    Y, py = _out((M, N))
+    lib().or_linear_fwd(px, pw, pb, py, M, N, K)
+    return Y
+
+
+def act_bwd(kind, dY, X):
+    dY, pdy = _f(dY)
+    X, px = _f(X)
+    dX, pdx = _out(dY.shape)
+    lib().or_act_bwd(ACT[kind], pdy, px, pdx, ctypes.c_int64(dY.size))
+    return dX
+
+
+def act_fwd(kind, X):
+    X, px = _f(X)
+    Y, py = _out(X.shape)
+    lib().or_act_fwd(ACT[kind], px, py, ctypes.c_int64(X.size))
+    return Y
+
+
+def glu_bwd(kind, dO, gate, up):
+    dO, pd = _f(dO)
+    gate, pg = _f(gate)
+    up, pu = _f(up)
+    dG, pdg = _out(dO.shape)
+    dU, pdu = _out(dO.shape)
+    lib().or_glu_bwd(GLU[kind], pd, pg, pu, pdg, pdu, ctypes.c_int64(dO.size))
+    return dG, dU
+
+
+def glu_fwd(kind, gate, up):
+    gate, pg = _f(gate)
+    up, pu = _f(up)
+    out, po = _out(gate.shape)
+    lib().or_glu_fwd(GLU[kind], pg, pu, po, ctypes.c_int64(gate.size))
+    return out
+
+
+def layernorm_bwd(dY, X, gamma, mean, rstd, eps=1e-5, stat_is_var=False):
+    rows, F = X.shape
+    dY, pdy = _f(dY)
+    X, px = _f(X)
+    gamma, pg = _f(gamma)
+    mean, pm = _f(mean)
+    rstd, pr = _f(rstd)
+    dX, pdx = _out((rows, F))
+    dG, pdg = _out((F,))
+    dB, pdb = _out((F,))
+    lib().or_layernorm_bwd(pdy, px, pg, pm, pr, pdx, pdg, pdb, rows, F,
+                           ctypes.c_float(eps), int(stat_is_var))
+    return dX, dG, dB
+
+
+def layernorm_bwd_glsl(dY, X, gamma, mean, rstd):
+    rows, F = X.shape
+    dY, pdy = _f(dY)
+    X, px = _f(X)
+    gamma, pg = _f(gamma)
+    mean, pm = _f(mean)
+    rstd, pr = _f(rstd)
+    dX, pdx = _out((rows, F))
+    lib().or_layernorm_bwd_glsl(pdy, px, pg, pm, pr, pdx, rows, F)
+    return dX
+
+
+def layernorm_fwd(X, gamma, beta=None, eps=1e-5):
+    rows, F = X.shape
+    X, px = _f(X)
+    gamma, pg = _f(gamma)
+    pb = None
+    if beta is not None:
+        beta, pb = _f(beta)
+    Y, py = _out((rows, F))
+    mean, pm = _out((rows,))
+    rstd, pr = _out((rows,))
+    lib().or_layernorm_fwd(px, pg, pb, py, pm, pr, rows, F, ctypes.c_float(eps))
+    return Y, mean, rstd
+
+
+def rmsnorm_bwd(dY, X, w, rstd):
+    rows, F = X.shape
+    dY, pdy = _f(dY)
+    X, px = _f(X)
+    w, pw = _f(w)
+    rstd, pr = _f(rstd)
+    dX, pdx = _out((rows, F))
+    dW, pdw = _out((F,))
+    lib().or_rmsnorm_bwd(pdy, px, pw, pr, pdx, pdw, rows, F)
+    return dX, dW
+
+
+def rmsnorm_fwd(X, w, eps=1e-6):
+    rows, F = X.shape
+    X, px = _f(X)
+    w, pw = _f(w)
+    Y, py = _out((rows, F))
+    rstd, pr = _out((rows,))
+    lib().or_rmsnorm_fwd(px, pw, py, pr, rows, F, ctypes.c_float(eps))
+    return Y, rstd
+
+
+def softmax_bwd(dY, Y):
+    rows, C = Y.shape
+    dY, pdy = _f(dY)
+    Y, py = _f(Y)
+    dX, pdx = _out((rows, C))
+    lib().or_softmax_bwd(pdy, py, pdx, rows, C)
+    return dX
+
+
+def softmax_fwd(X):
+    rows, C = X.shape
+    X, px = _f(X)
+    Y, py = _out((rows, C))
+    lib().or_softmax_fwd(px, py, rows, C)
+    return Y
+
+
+def xent_bwd(logits, targets, scale=1.0):
+    rows, C = logits.shape
+    logits, pl = _f(logits)
+    targets, pt = _i(targets)
+    dL, pdl = _out((rows, C))
+    lib().or_xent_bwd(pl, pt, pdl, rows, C, ctypes.c_float(scale))
+    return dL
+
+
+def rope(X, mode="interleaved", theta=10000.0, inverse=False):
+    S, D = X.shape
+    X = np.array(X, dtype=np.float32, copy=True)
+    lib().or_rope(X.ctypes.data_as(ctypes.c_void_p), S, D, ROPE[mode], ctypes.c_float(theta),
+                  int(inverse))
+    return X
+
+
+def attn_fwd(Q, K, V, scale=None, causal=True, rope_mode="interleaved", theta=10000.0):
+    B, H, S, D = Q.shape
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    Q, pq = _f(Q)
+    K, pk = _f(K)
+    V, pv = _f(V)
+    O, po = _out((B, H, S, D))
+    LSE, pl = _out((B, H, S))
+    lib().or_attn_fwd(pq, pk, pv, po, pl, B, H, S, D, ctypes.c_float(scale), int(causal),
+                      ROPE[rope_mode], ctypes.c_float(theta))
+    return O, LSE
+
+
+def attn_bwd(Q, K, V, dO, LSE, scale=None, causal=True, rope_mode="interleaved",
+             theta=10000.0):
+    B, H, S, D = Q.shape
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    Q, pq = _f(Q)
+    K, pk = _f(K)
+    V, pv = _f(V)
+    dO, pdo = _f(dO)
+    LSE, pl = _f(LSE)
+    dQ, pdq = _out((B, H, S, D))
+    dK, pdk = _out((B, H, S, D))
+    dV, pdv = _out((B, H, S, D))
+    lib().or_attn_bwd(pq, pk, pv, pdo, pl, pdq, pdk, pdv, B, H, S, D, ctypes.c_float(scale),
+                      int(causal), ROPE[rope_mode], ctypes.c_float(theta))
+    return dQ, dK, dV
+
+
+def unpack_bits(bits, D):
+    Bn, words = bits.shape
+    bits, pb = _u(bits)
+    out, po = _out((Bn, D))
+    lib().or_unpack_bits(pb, po, Bn, D, words)
+    return out
+
+
+def vsa_unpack_project_bwd(dY, bits, D):
+    Bn, O = dY.shape
+    words = bits.shape[1]
+    dY, pdy = _f(dY)
+    bits, pb = _u(bits)
+    dW, pdw = _out((O, D))
+    db, pdb = _out((O,))
+    lib().or_vsa_unpack_project_bwd(pdy, pb, pdw, pdb, Bn, O, D, words)
+    return dW, db
+
+
+def vsa_surrogate_bwd(preds, bits, results, weights, gamma=1.0, delta=1.0, lambda_c=0.3,
+                      scale=1.0, init=None):
+    Bn, K, D = preds.shape
+    words = bits.shape[1]
+    preds, pp = _f(preds)
+    bits, pb = _u(bits)
+    results, pr = _u(results)
+    weights, pw = _f(weights)
+    if init is None:
+        dP, pdp = _out((Bn, K, D))
+        acc = 0
+    else:
+        dP, pdp = _f(np.array(init, dtype=np.float32, copy=True))
+        acc = 1
+    lib().or_vsa_surrogate_bwd(pp, pb, pr, pw, pdp, Bn, K, D, words, ctypes.c_float(gamma),
+                               ctypes.c_float(delta), ctypes.c_float(lambda_c),
+                               ctypes.c_float(scale), acc)
+    return dP
+
+
+def vsa_dots(preds, bits):
+    Bn, K, D = preds.shape
+    words = bits.shape[1]
+    preds, pp = _f(preds)
+    bits, pb = _u(bits)
+    dots, pd = _out((Bn, K))
+    lib().or_vsa_dots(pp, pb, pd, Bn, K, D, words)
+    return dots
+
+
+def vsa_results_weights(dots, temperature=1.0, rng=None):
+    """Seeded restatement of the host top-2 + softmax of vsa_loss_node.cpp:101-148.
+
+    The reference perturbs the dots with unseeded Gumbel noise (vsa_loss_node.cpp:9-14);
+    here the noise comes from `rng` (None = no noise), so the backward inputs are
+    reproducible.  Returns (results u32 [B,4], weights f32 [B,K]).
+    """
+    Bn, K = dots.shape
+    results = np.zeros((Bn, 4), dtype=np.uint32)
+    weights = np.zeros((Bn, K), dtype=np.float32)
+    for b in range(Bn):
+        adj = dots[b].astype(np.float64)
+        if rng is not None:
+            u = rng.uniform(1e-8, 1 - 1e-8, size=K)
+            adj = adj + (-np.log(-np.log(u))) * temperature
+        max1 = max2 = -1e30
+        k1 = k2 = 0
+        for k in range(K):
+            if adj[k] > max1:
+                max2, k2 = max1, k1
+                max1, k1 = adj[k], k
+            elif adj[k] > max2:
+                max2, k2 = adj[k], k
+        results[b, 0] = k1
+        results[b, 1] = k2
+        results[b, 2] = np.float32(dots[b, k1]).view(np.uint32)
+        results[b, 3] = np.float32(dots[b, k2]).view(np.uint32)
+        e = np.exp((dots[b].astype(np.float64) - dots[b].max()) / temperature)
+        weights[b] = (e / e.sum()).astype(np.float32)
+    return results, weights

@@ -1,0 +1,94 @@
+/*
+ * oracle.h — CPU restatement of grilly-next's backward formulas.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load liboracle.so, and only as the checker or as the timed CPU
+ * baseline; the product path (libgn_bwd.so, grilly_core) never links or calls it.
+ *
+ * All functions take fp32 host arrays and accumulate in fp64.  Each cites the reference
+ * file:line it restates; the pins for each function are listed in tests/test_oracle.py.
+ * Parity status: every function below is pinned (golden vectors from an independent
+ * torch-fp64 autograd restatement, closed forms, reference known-answer tests).
+ */
+#ifndef GN_ORACLE_H
+#define GN_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fnn-linear-backward.glsl:47-89; autograd_core.py:511-513 */
+void or_linear_bwd(const float* dY, const float* X, const float* W, float* dX, float* dW,
+                   float* db, int M, int N, int K);
+/* forward y = X W^T + b (fnn-linear.glsl), used to build saved tensors */
+void or_linear_fwd(const float* X, const float* W, const float* b, float* Y, int M, int N,
+                   int K);
+
+/* activation-*-backward.glsl; kinds as GN_ACT_* in include/gn_bwd.h */
+void or_act_bwd(int kind, const float* dY, const float* X, float* dX, int64_t n);
+void or_act_fwd(int kind, const float* X, float* Y, int64_t n);
+
+/* fused-{swiglu,geglu,reglu}-backward.glsl local gradients; kinds as GN_GLU_* */
+void or_glu_bwd(int kind, const float* dO, const float* gate, const float* up, float* dGate,
+                float* dUp, int64_t n);
+void or_glu_fwd(int kind, const float* gate, const float* up, float* out, int64_t n);
+
+/* Textbook LayerNorm backward (autograd_core.py:591-609). stat_is_var: rstd holds var. */
+void or_layernorm_bwd(const float* dY, const float* X, const float* gamma, const float* mean,
+                      const float* rstd, float* dX, float* dGamma, float* dBeta, int rows,
+                      int F, float eps, int stat_is_var);
+/* The reference GLSL form (fnn-layernorm-backward.glsl:124), kept to pin the gamma==1
+ * agreement with the textbook form. */
+void or_layernorm_bwd_glsl(const float* dY, const float* X, const float* gamma,
+                           const float* mean, const float* rstd, float* dX, int rows, int F);
+/* fnn-layernorm.glsl:44-102: biased variance; returns mean and rstd */
+void or_layernorm_fwd(const float* X, const float* gamma, const float* beta, float* Y,
+                      float* mean, float* rstd, int rows, int F, float eps);
+
+/* RMSNorm (rms-norm.glsl:34-70 forward; backward by closed form) */
+void or_rmsnorm_bwd(const float* dY, const float* X, const float* w, const float* rstd,
+                    float* dX, float* dW, int rows, int F);
+void or_rmsnorm_fwd(const float* X, const float* w, float* Y, float* rstd, int rows, int F,
+                    float eps);
+
+/* activation-softmax-backward.glsl:27-49 */
+void or_softmax_bwd(const float* dY, const float* Y, float* dX, int rows, int C);
+void or_softmax_fwd(const float* X, float* Y, int rows, int C);
+
+/* cross-entropy-backward.glsl:29-84 (targets as int32) */
+void or_xent_bwd(const float* logits, const int32_t* targets, float* dLogits, int rows, int C,
+                 float scale);
+
+/* RoPE rotation of one [S, D] head in place (flash-attention2-rope.glsl:74-91 interleaved,
+ * rope.glsl:74-125 rotate-half); inverse = 1 applies R^T. */
+void or_rope(float* X, int S, int D, int mode, float theta, int inverse);
+
+/* attention-backward.glsl:73-194 / autograd_core.py:638-654 with causal mask and RoPE.
+ * P is recomputed from LSE; D_i = sum_j P_ij dP_ij as in the reference pass 2. */
+void or_attn_bwd(const float* Q, const float* K, const float* V, const float* dO,
+                 const float* LSE, float* dQ, float* dK, float* dV, int B, int H, int S, int D,
+                 float scale, int causal, int rope_mode, float theta);
+void or_attn_fwd(const float* Q, const float* K, const float* V, float* O, float* LSE, int B,
+                 int H, int S, int D, float scale, int causal, int rope_mode, float theta);
+
+/* vsa-unpack-project-backward.glsl:42-74 */
+void or_unpack_bits(const uint32_t* bits, float* out, int Bn, int D, int words);
+void or_vsa_unpack_project_bwd(const float* dY, const uint32_t* bits, float* dW, float* db,
+                               int Bn, int O, int D, int words);
+
+/* vsa-surrogate-loss-backward.glsl:50-88; accumulate=0 starts from zero */
+void or_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32_t* results,
+                          const float* weights, float* dPreds, int Bn, int K, int D, int words,
+                          float gamma, float delta, float lambda_c, float scale,
+                          int accumulate);
+/* vsa-surrogate-loss-forward.glsl pass 0 (dots) */
+void or_vsa_dots(const float* preds, const uint32_t* bits, float* dots, int Bn, int K, int D,
+                 int words);
+
+int or_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,57 @@
+"""CPU checks of the C-ABI boundary: the library loads and exports every entry point that
+include/gn_bwd.h declares (no compute calls: this container has no GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT, PKG
+
+HEADER = os.path.join(ROOT, "include", "gn_bwd.h")
+LIB = os.path.join(PKG, "libgn_bwd.so")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    for n in ["gn_linear_bwd", "gn_glu_linear_bwd", "gn_rmsnorm_bwd", "gn_layernorm_bwd",
+              "gn_xent_bwd", "gn_attn_bwd", "gn_vsa_unpack_project_bwd", "gn_vsa_surrogate_bwd"]:
+        assert n in names
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_python_frontend_lists_every_symbol():
+    import gn_bwd
+    assert sorted(gn_bwd.SYMBOLS) == declared()
+    lib = gn_bwd.lib()
+    assert b"gfx950" in lib.gn_version()
+    # size queries are pure host arithmetic
+    assert lib.gn_norm_workspace_bytes(4096, 2048) == 2 * 256 * 2048 * 4
+    assert lib.gn_attn_workspace_bytes(4, 16, 2048, 128) > 0
+    assert lib.gn_attn_workspace_bytes(0, 16, 2048, 128) == 0
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_invalid_arguments_rejected_without_gpu():
+    # argument validation happens before any HIP call
+    import gn_bwd
+    lib = gn_bwd.lib()
+    assert lib.gn_act_bwd(99, None, None, None, 4, 0, 0, None) == -1  # null pointer first
+    assert "null" in gn_bwd.last_error()
+    assert lib.gn_act_bwd(0, None, None, None, 0, 0, 0, None) == 0  # empty input is a no-op
+    assert lib.gn_vsa_unpack_project_bwd(None, None, None, None, 8, 8, 100, 4, 0, 0, None, 0, None) == -1
+    assert lib.gn_attn_bwd(None, None, None, None, None, None, None, None, None, 1, 1, 8, 300,
+                           1.0, 1, 1, 1e4, 4, None, 0, None) == -1

@@ -1,0 +1,353 @@
+"""GPU parity: every libgn_bwd entry point against the CPU oracle on seeded inputs.
+
+Tolerances (normwise relative error max|gpu - ref| / max|ref|):
+  fp32 paths   <= 1e-4
+  bf16 paths   <= 2e-2 against the fp32 oracle run on the same bf16-rounded inputs
+  bit / integer work: exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import golden, rel_err
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def gn(gpu):
+    import gn_bwd
+    gn_bwd.lib()
+    return gn_bwd
+
+
+def dev(x, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def rnd(x):
+    """bf16-round a float32 numpy array (what the kernel actually sees)."""
+    return host(dev(x, torch.bfloat16))
+
+
+def rng_(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------------------- GEMM core
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("shape", [(136, 200, 72), (256, 128, 640), (8, 8, 8)])
+def test_gemm_bf16_layouts(gn, ta, tb, shape):
+    M, N, K = shape
+    r = rng_(1)
+    A = rnd(r.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = rnd(r.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    C = gn.gemm(dev(A, torch.bfloat16), dev(B, torch.bfloat16), bool(ta), bool(tb),
+                out_dtype=torch.float32)
+    assert rel_err(host(C), ref) < 1e-5
+    Cb = gn.gemm(dev(A, torch.bfloat16), dev(B, torch.bfloat16), bool(ta), bool(tb),
+                 out_dtype=torch.bfloat16)
+    assert rel_err(host(Cb), ref) < 8e-3
+
+
+def test_gemm_two_segments_and_accumulate(gn):
+    r = rng_(2)
+    M, N, K0, K1 = 64, 96, 40, 24
+    A0, A1 = (rnd(r.standard_normal((M, k)).astype(np.float32)) for k in (K0, K1))
+    B0, B1 = (rnd(r.standard_normal((k, N)).astype(np.float32)) for k in (K0, K1))
+    ref = A0.astype(np.float64) @ B0 + A1.astype(np.float64) @ B1
+    C = gn.gemm(dev(A0, torch.bfloat16), dev(B0, torch.bfloat16), A1=dev(A1, torch.bfloat16),
+                B1=dev(B1, torch.bfloat16), out_dtype=torch.float32)
+    assert rel_err(host(C), ref) < 1e-5
+    gn.gemm(dev(A0, torch.bfloat16), dev(B0, torch.bfloat16), C=C, accumulate=True)
+    assert rel_err(host(C), ref + A0.astype(np.float64) @ B0) < 1e-5
+
+
+def test_gemm_unaligned_falls_back(gn):
+    r = rng_(3)
+    A = rnd(r.standard_normal((10, 13)).astype(np.float32))
+    B = rnd(r.standard_normal((13, 7)).astype(np.float32))
+    C = gn.gemm(dev(A, torch.bfloat16), dev(B, torch.bfloat16), out_dtype=torch.float32)
+    assert rel_err(host(C), A.astype(np.float64) @ B) < 1e-5
+
+
+# ---------------------------------------------------------------------------- linear
+def test_linear_fp32_golden(gn):
+    for tag in ["small", "c1l2"]:
+        g = golden(f"linear_{tag}")
+        dX, dW, db = gn.linear_bwd(dev(g["dY"]), dev(g["X"]), dev(g["W"]))
+        assert rel_err(host(dX), g["dX"]) < FP32_TOL
+        assert rel_err(host(dW), g["dW"]) < FP32_TOL
+        assert rel_err(host(db), g["db"]) < FP32_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 384, 320), (512, 256, 1024)])
+def test_linear_bf16(gn, M, N, K):
+    r = rng_(4)
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    W = rnd((r.standard_normal((N, K)) * 0.02).astype(np.float32))
+    dY = rnd((r.standard_normal((M, N)) * 0.01).astype(np.float32))
+    dX, dW, db = gn.linear_bwd(dev(dY, torch.bfloat16), dev(X, torch.bfloat16),
+                               dev(W, torch.bfloat16))
+    rX, rW, rb = oracle.linear_bwd(dY, X, W)
+    assert dX.dtype == torch.bfloat16 and dW.dtype == torch.float32
+    assert rel_err(host(dX), rX) < BF16_TOL
+    assert rel_err(host(dW), rW) < 1e-4  # fp32 output of bf16 products: only summation order
+    assert rel_err(host(db), rb) < 1e-4
+
+
+def test_linear_no_dx_and_accumulate(gn):
+    g = golden("linear_small")
+    dY, X, W = dev(g["dY"]), dev(g["X"]), dev(g["W"])
+    dX, dW, db = gn.linear_bwd(dY, X, W, need_dx=False)
+    assert dX is None
+    gn.linear_bwd(dY, X, W, need_dx=False, dW=dW, db=db, accumulate=True)
+    assert rel_err(host(dW), 2 * g["dW"]) < FP32_TOL
+    assert rel_err(host(db), 2 * g["db"]) < FP32_TOL
+
+
+# ---------------------------------------------------------------------------- activations
+@pytest.mark.parametrize("kind", ["relu", "gelu_tanh", "gelu_erf", "silu", "tanh", "sigmoid"])
+def test_act_golden_fp32(gn, kind):
+    g = golden("act")
+    inp = g["Y_" + kind] if kind in ("tanh", "sigmoid") else g["X"]
+    dX = gn.act_bwd(kind, dev(g["dY"]), dev(inp))
+    assert rel_err(host(dX), g["dX_" + kind]) < FP32_TOL
+
+
+@pytest.mark.parametrize("kind", ["relu", "gelu_tanh", "silu"])
+@pytest.mark.parametrize("n", [4096 * 8 + 3, 1 << 20])
+def test_act_bf16(gn, kind, n):
+    r = rng_(5)
+    X = rnd((r.standard_normal(n) * 3).astype(np.float32))
+    dY = rnd(r.standard_normal(n).astype(np.float32))
+    dX = gn.act_bwd(kind, dev(dY, torch.bfloat16), dev(X, torch.bfloat16))
+    assert rel_err(host(dX), oracle.act_bwd(kind, dY, X)) < BF16_TOL
+    gn.act_bwd(kind, dev(dY, torch.bfloat16), dev(X, torch.bfloat16), dX=dX, accumulate=True)
+    assert rel_err(host(dX), 2 * oracle.act_bwd(kind, dY, X)) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------- GLU
+@pytest.mark.parametrize("kind", ["swiglu_up", "swiglu_gate", "geglu_up", "geglu_gate", "reglu_up"])
+def test_glu_golden_fp32(gn, kind):
+    g = golden("glu")
+    dG, dU = gn.glu_bwd(kind, dev(g["dO"]), dev(g["gate"]), dev(g["up"]))
+    assert rel_err(host(dG), g["dGate_" + kind]) < FP32_TOL
+    assert rel_err(host(dU), g["dUp_" + kind]) < FP32_TOL
+
+
+@pytest.mark.parametrize("kind", ["swiglu_up", "geglu_up"])
+def test_glu_linear_bf16(gn, kind):
+    r = rng_(6)
+    M, K, H = 192, 256, 320
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    Wg = rnd((r.standard_normal((H, K)) * 0.05).astype(np.float32))
+    Wu = rnd((r.standard_normal((H, K)) * 0.05).astype(np.float32))
+    gate, up = oracle.linear_fwd(X, Wg), oracle.linear_fwd(X, Wu)
+    gate, up = rnd(gate), rnd(up)
+    dO = rnd((r.standard_normal((M, H)) * 0.01).astype(np.float32))
+    dX, dWg, dWu, dbg, dbu = gn.glu_linear_bwd(kind, dev(dO, torch.bfloat16),
+                                               dev(gate, torch.bfloat16), dev(up, torch.bfloat16),
+                                               dev(X, torch.bfloat16), dev(Wg, torch.bfloat16),
+                                               dev(Wu, torch.bfloat16), need_db=True)
+    dG, dU = oracle.glu_bwd(kind, dO, gate, up)
+    rX = oracle.linear_bwd(dG, X, Wg)[0] + oracle.linear_bwd(dU, X, Wu)[0]
+    assert rel_err(host(dX), rX) < BF16_TOL
+    assert rel_err(host(dWg), oracle.linear_bwd(dG, X, Wg)[1]) < BF16_TOL
+    assert rel_err(host(dWu), oracle.linear_bwd(dU, X, Wu)[1]) < BF16_TOL
+    assert rel_err(host(dbg), dG.sum(0)) < BF16_TOL
+    assert rel_err(host(dbu), dU.sum(0)) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------- norms
+def test_layernorm_golden_fp32(gn):
+    g = golden("layernorm")
+    dX, dG, dB = gn.layernorm_bwd(dev(g["dY"]), dev(g["X"]), dev(g["gamma"]), dev(g["mean"]),
+                                  dev(g["rstd"]))
+    assert rel_err(host(dX), g["dX"]) < FP32_TOL
+    assert rel_err(host(dG), g["dGamma"]) < FP32_TOL
+    assert rel_err(host(dB), g["dBeta"]) < FP32_TOL
+    dX2, _, _ = gn.layernorm_bwd(dev(g["dY"]), dev(g["X"]), dev(g["gamma"]), dev(g["mean"]),
+                                 dev(g["var"]), eps=float(g["eps"]), stat_is_var=True)
+    assert rel_err(host(dX2), g["dX"]) < FP32_TOL
+
+
+@pytest.mark.parametrize("rows,F,dt", [(8192, 768, "bf16"), (1000, 2048, "f32"), (77, 4096, "bf16"),
+                                       (33, 100, "f32"), (5, 6000, "bf16")])
+def test_layernorm_shapes(gn, rows, F, dt):
+    r = rng_(7)
+    X = (r.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32)
+    gamma = (1 + 0.3 * r.standard_normal(F)).astype(np.float32)
+    dY = r.standard_normal((rows, F)).astype(np.float32)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    if dt == "bf16":
+        X, gamma, dY = rnd(X), rnd(gamma), rnd(dY)
+    _, mean, rstd = oracle.layernorm_fwd(X, gamma)
+    dX, dG, dB = gn.layernorm_bwd(dev(dY, tdt), dev(X, tdt), dev(gamma, tdt), dev(mean), dev(rstd))
+    rX, rG, rB = oracle.layernorm_bwd(dY, X, gamma, mean, rstd)
+    tol = BF16_TOL if dt == "bf16" else FP32_TOL
+    assert rel_err(host(dX), rX) < tol
+    assert rel_err(host(dG), rG) < FP32_TOL * 10
+    assert rel_err(host(dB), rB) < FP32_TOL * 10
+
+
+def test_rmsnorm_golden_fp32(gn):
+    g = golden("rmsnorm")
+    dX, dW = gn.rmsnorm_bwd(dev(g["dY"]), dev(g["X"]), dev(g["w"]), dev(g["rstd"]))
+    assert rel_err(host(dX), g["dX"]) < FP32_TOL
+    assert rel_err(host(dW), g["dW"]) < FP32_TOL
+
+
+@pytest.mark.parametrize("rows,F", [(4096, 2048), (300, 768), (17, 50)])
+def test_rmsnorm_bf16(gn, rows, F):
+    r = rng_(8)
+    X = rnd(r.standard_normal((rows, F)).astype(np.float32))
+    w = rnd((1 + 0.2 * r.standard_normal(F)).astype(np.float32))
+    dY = rnd((r.standard_normal((rows, F)) * 0.01).astype(np.float32))
+    _, rstd = oracle.rmsnorm_fwd(X, w)
+    dX, dW = gn.rmsnorm_bwd(dev(dY, torch.bfloat16), dev(X, torch.bfloat16),
+                            dev(w, torch.bfloat16), dev(rstd))
+    rX, rW = oracle.rmsnorm_bwd(dY, X, w, rstd)
+    assert rel_err(host(dX), rX) < BF16_TOL
+    assert rel_err(host(dW), rW) < 1e-3
+
+
+# ---------------------------------------------------------------------------- softmax / CE
+def test_softmax_and_xent_golden(gn):
+    g = golden("softmax")
+    assert rel_err(host(gn.softmax_bwd(dev(g["dY"]), dev(g["Y"]))), g["dX"]) < FP32_TOL
+    g = golden("xent")
+    dL = gn.xent_bwd(dev(g["logits"]), torch.from_numpy(g["targets"]).cuda(), 1.0)
+    assert rel_err(host(dL), g["dLogits"]) < FP32_TOL
+
+
+def test_xent_vocab_bf16(gn):
+    r = rng_(9)
+    rows, C = 64, 32000
+    Z = rnd((r.standard_normal((rows, C)) * 2).astype(np.float32))
+    t = r.integers(0, C, size=rows).astype(np.int32)
+    dL = gn.xent_bwd(dev(Z, torch.bfloat16), torch.from_numpy(t).cuda(), 1.0 / rows)
+    assert rel_err(host(dL), oracle.xent_bwd(Z, t, 1.0 / rows)) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------- attention
+@pytest.mark.parametrize("tag", ["causal_rope", "full_norope", "causal_half"])
+def test_attention_golden_fp32(gn, tag):
+    g = golden(f"attn_{tag}")
+    kw = dict(scale=float(g["scale"]), causal=bool(g["causal"]), rope=str(g["rope"]),
+              theta=float(g["theta"]))
+    O, LSE = gn.attn_fwd(dev(g["Q"]), dev(g["K"]), dev(g["V"]), **kw)
+    assert rel_err(host(O), g["O"]) < FP32_TOL and rel_err(host(LSE), g["LSE"]) < FP32_TOL
+    dQ, dK, dV = gn.attn_bwd(dev(g["Q"]), dev(g["K"]), dev(g["V"]), dev(g["O"]), dev(g["dO"]),
+                             dev(g["LSE"]), **kw)
+    assert rel_err(host(dQ), g["dQ"]) < FP32_TOL
+    assert rel_err(host(dK), g["dK"]) < FP32_TOL
+    assert rel_err(host(dV), g["dV"]) < FP32_TOL
+
+
+@pytest.mark.parametrize("S,D,causal,rope", [(256, 128, True, "interleaved"), (130, 64, True, "interleaved"),
+                                             (192, 128, False, "none"), (128, 128, True, "half")])
+def test_attention_bf16_mfma(gn, S, D, causal, rope):
+    r = rng_(10)
+    B, H = 2, 3
+    Q, K, V = (rnd(r.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    dO = rnd((r.standard_normal((B, H, S, D)) * 0.01).astype(np.float32))
+    kw = dict(causal=causal, rope_mode=rope)
+    O, LSE = oracle.attn_fwd(Q, K, V, **kw)
+    O = rnd(O)
+    rQ, rK, rV = oracle.attn_bwd(Q, K, V, dO, LSE, **kw)
+    dQ, dK, dV = gn.attn_bwd(dev(Q, torch.bfloat16), dev(K, torch.bfloat16), dev(V, torch.bfloat16),
+                             dev(O, torch.bfloat16), dev(dO, torch.bfloat16), dev(LSE),
+                             causal=causal, rope=rope)
+    assert rel_err(host(dV), rV) < BF16_TOL
+    assert rel_err(host(dQ), rQ) < BF16_TOL
+    assert rel_err(host(dK), rK) < BF16_TOL
+
+
+def test_attention_fwd_bf16_matches_oracle(gn):
+    r = rng_(11)
+    Q, K, V = (rnd(r.standard_normal((1, 2, 96, 64)).astype(np.float32)) for _ in range(3))
+    O, LSE = gn.attn_fwd(dev(Q, torch.bfloat16), dev(K, torch.bfloat16), dev(V, torch.bfloat16))
+    rO, rL = oracle.attn_fwd(Q, K, V)
+    assert rel_err(host(O), rO) < BF16_TOL and rel_err(host(LSE), rL) < 1e-3
+
+
+# ---------------------------------------------------------------------------- VSA
+def test_vsa_project_golden(gn):
+    g = golden("vsa_project")
+    D = g["W"].shape[1]
+    bits = gn.u32_tensor(g["bits"], "cuda:0")
+    dW, db = gn.vsa_unpack_project_bwd(dev(g["dY"]), bits, D)
+    assert rel_err(host(dW), g["dW"]) < FP32_TOL and rel_err(host(db), g["db"]) < FP32_TOL
+
+
+def test_vsa_project_popcount_exact(gn):
+    # integer dY: every partial sum is an exactly representable integer, so the GPU result
+    # must equal 2 * popcount - B bit for bit (pins the unpack order)
+    r = rng_(12)
+    Bn, O, D = 1000, 64, 2048
+    bits = r.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    dW, _ = gn.vsa_unpack_project_bwd(dev(np.ones((Bn, O), np.float32)), gn.u32_tensor(bits, "cuda:0"), D)
+    pop = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little").sum(0).astype(np.int64)
+    np.testing.assert_array_equal(host(dW), np.tile(2 * pop - Bn, (O, 1)).astype(np.float32))
+
+
+@pytest.mark.parametrize("Bn,O,D", [(512, 768, 1024), (333, 128, 320)])
+def test_vsa_project_fp32_split(gn, Bn, O, D):
+    r = rng_(13)
+    bits = r.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    dY = r.standard_normal((Bn, O)).astype(np.float32)
+    dW, db = gn.vsa_unpack_project_bwd(dev(dY), gn.u32_tensor(bits, "cuda:0"), D)
+    rW, rb = oracle.vsa_unpack_project_bwd(dY, bits, D)
+    assert rel_err(host(dW), rW) < FP32_TOL
+    assert rel_err(host(db), rb) < FP32_TOL
+
+
+def test_vsa_surrogate_golden_and_random(gn):
+    g = golden("vsa_surrogate")
+    dP = gn.vsa_surrogate_bwd(dev(g["preds"]), gn.u32_tensor(g["bits"], "cuda:0"),
+                              gn.u32_tensor(g["results"], "cuda:0"), dev(g["weights"]),
+                              float(g["gamma"]), float(g["delta"]), float(g["lambda_c"]),
+                              float(g["scale"]))
+    assert rel_err(host(dP), g["dPreds"]) < 1e-6
+    r = rng_(14)
+    Bn, K, D = 64, 4, 10240
+    preds = r.standard_normal((Bn, K, D)).astype(np.float32)
+    bits = r.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    res, w = oracle.vsa_results_weights(oracle.vsa_dots(preds, bits), rng=r)
+    dP = gn.vsa_surrogate_bwd(dev(preds), gn.u32_tensor(bits, "cuda:0"), gn.u32_tensor(res, "cuda:0"),
+                              dev(w))
+    ref = oracle.vsa_surrogate_bwd(preds, bits, res, w)
+    assert rel_err(host(dP), ref) < 1e-6
+    init = r.standard_normal((Bn, K, D)).astype(np.float32)
+    dP = gn.vsa_surrogate_bwd(dev(preds), gn.u32_tensor(bits, "cuda:0"), gn.u32_tensor(res, "cuda:0"),
+                              dev(w), dPreds=dev(init), accumulate=True)
+    assert rel_err(host(dP), oracle.vsa_surrogate_bwd(preds, bits, res, w, init=init)) < 1e-6
+
+
+def test_add_inplace(gn):
+    a = torch.randn(1001, device="cuda:0")
+    b = torch.randn(1001, device="cuda:0")
+    ref = (a + b).cpu()
+    gn.add_inplace(a, b)
+    assert torch.equal(a.cpu(), ref)
+
+
+def test_errors_are_reported(gn):
+    x = torch.zeros(4, device="cuda:0")
+    rc = gn.lib().gn_act_bwd(99, gn._ptr(x), gn._ptr(x), gn._ptr(x), 4, gn.F32, 0, None)
+    assert rc == -1 and "unknown activation" in gn.last_error()
+    with pytest.raises(gn.GnError, match="workspace"):
+        X = torch.zeros((8, 16), device="cuda:0")
+        gn.rmsnorm_bwd(X, X, torch.ones(16, device="cuda:0"), torch.ones(8, device="cuda:0"),
+                       ws=torch.empty(1, dtype=torch.uint8, device="cuda:0"))

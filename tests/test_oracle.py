@@ -1,0 +1,252 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each oracle function is checked against
+  * golden vectors from torch float64 autograd of the op's forward definition
+    (tests/golden/make_golden.py) — independent of the oracle's backward formulas;
+  * the reference's own known-answer tests where they exist
+    (tests/test_vsa_hypernetwork.py:151-202, tests/test_vsa_training_loop.py:131-148);
+  * closed forms and invariants chosen so a dropped term, sign or index fails.
+Tolerance: normwise relative error (max|a-b|/max|b|) <= 1e-5 (fp32 output of an fp64
+computation).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import golden, rel_err
+
+TOL = 1e-5
+
+
+def test_linear_golden():
+    for tag in ["small", "c1l2"]:
+        g = golden(f"linear_{tag}")
+        dX, dW, db = oracle.linear_bwd(g["dY"], g["X"], g["W"])
+        assert rel_err(dX, g["dX"]) < TOL
+        assert rel_err(dW, g["dW"]) < TOL
+        assert rel_err(db, g["db"]) < TOL
+
+
+def test_linear_transpose_identity():
+    # dX = dY W must equal (W^T dY^T)^T, and dW for a one-hot dY row picks that X row.
+    rng = np.random.default_rng(0)
+    X = rng.standard_normal((4, 6)).astype(np.float32)
+    W = rng.standard_normal((3, 6)).astype(np.float32)
+    dY = np.zeros((4, 3), np.float32)
+    dY[2, 1] = 1.0
+    dX, dW, db = oracle.linear_bwd(dY, X, W)
+    np.testing.assert_array_equal(dX[2], W[1])
+    np.testing.assert_array_equal(dW[1], X[2])
+    assert np.count_nonzero(dW[[0, 2]]) == 0
+    np.testing.assert_array_equal(db, [0, 1, 0])
+
+
+@pytest.mark.parametrize("kind", ["relu", "gelu_tanh", "gelu_erf", "silu", "tanh", "sigmoid"])
+def test_act_golden(kind):
+    g = golden("act")
+    # tanh/sigmoid backward take the saved forward output (activation-tanh-backward.glsl:33)
+    inp = g["Y_" + kind] if kind in ("tanh", "sigmoid") else g["X"]
+    dX = oracle.act_bwd(kind, g["dY"], inp)
+    assert rel_err(dX, g["dX_" + kind]) < TOL
+
+
+def test_relu_strict_at_zero():
+    # activation-relu-backward.glsl:35: derivative is 1 only for x > 0 (0 at x == 0)
+    dX = oracle.act_bwd("relu", np.ones(3, np.float32), np.array([0.0, -0.0, 1e-30], np.float32))
+    np.testing.assert_array_equal(dX, [0.0, 0.0, 1.0])
+
+
+@pytest.mark.parametrize("kind", ["swiglu_up", "swiglu_gate", "geglu_up", "geglu_gate", "reglu_up"])
+def test_glu_golden(kind):
+    g = golden("glu")
+    dG, dU = oracle.glu_bwd(kind, g["dO"], g["gate"], g["up"])
+    assert rel_err(dG, g["dGate_" + kind]) < TOL
+    assert rel_err(dU, g["dUp_" + kind]) < TOL
+
+
+def test_glu_orientation_differs():
+    # the two SwiGLU conventions (fused-swiglu-backward.glsl vs swiglu-fused.glsl) really differ
+    g = golden("glu")
+    a = oracle.glu_bwd("swiglu_up", g["dO"], g["gate"], g["up"])[0]
+    b = oracle.glu_bwd("swiglu_gate", g["dO"], g["gate"], g["up"])[0]
+    assert rel_err(a, b) > 0.1
+
+
+def test_layernorm_golden():
+    g = golden("layernorm")
+    dX, dG, dB = oracle.layernorm_bwd(g["dY"], g["X"], g["gamma"], g["mean"], g["rstd"])
+    assert rel_err(dX, g["dX"]) < TOL
+    assert rel_err(dG, g["dGamma"]) < TOL
+    assert rel_err(dB, g["dBeta"]) < TOL
+    # the variance form (the reference saves var, fnn-layernorm.glsl:77) gives the same
+    dX2, _, _ = oracle.layernorm_bwd(g["dY"], g["X"], g["gamma"], g["mean"], g["var"],
+                                     eps=float(g["eps"]), stat_is_var=True)
+    assert rel_err(dX2, g["dX"]) < TOL
+    # forward restatement reproduces the saved statistics
+    Y, mean, rstd = oracle.layernorm_fwd(g["X"], g["gamma"], g["beta"], eps=float(g["eps"]))
+    assert rel_err(mean, g["mean"]) < TOL and rel_err(rstd, g["rstd"]) < TOL
+    assert rel_err(Y, g["Y"]) < TOL
+
+
+def test_layernorm_glsl_form_agrees_only_at_unit_gamma():
+    # fnn-layernorm-backward.glsl:124 multiplies gamma into the mean terms.  At gamma == 1
+    # it coincides with the textbook form; with a random gamma it does not.
+    g = golden("layernorm")
+    ones = np.ones_like(g["gamma"])
+    a = oracle.layernorm_bwd(g["dY"], g["X"], ones, g["mean"], g["rstd"])[0]
+    b = oracle.layernorm_bwd_glsl(g["dY"], g["X"], ones, g["mean"], g["rstd"])
+    assert rel_err(a, b) < TOL
+    c = oracle.layernorm_bwd_glsl(g["dY"], g["X"], g["gamma"], g["mean"], g["rstd"])
+    assert rel_err(c, g["dX"]) > 1e-2
+
+
+def test_rmsnorm_golden():
+    g = golden("rmsnorm")
+    dX, dW = oracle.rmsnorm_bwd(g["dY"], g["X"], g["w"], g["rstd"])
+    assert rel_err(dX, g["dX"]) < TOL
+    assert rel_err(dW, g["dW"]) < TOL
+    Y, rstd = oracle.rmsnorm_fwd(g["X"], g["w"], eps=float(g["eps"]))
+    assert rel_err(rstd, g["rstd"]) < TOL and rel_err(Y, g["Y"]) < TOL
+
+
+def test_rmsnorm_scale_invariance():
+    # y(c x) = y(x) for c > 0 when eps -> 0, so dx . x = 0 for every row (eps = 0 case).
+    rng = np.random.default_rng(1)
+    X = rng.standard_normal((5, 16)).astype(np.float32)
+    w = rng.standard_normal(16).astype(np.float32)
+    dY = rng.standard_normal((5, 16)).astype(np.float32)
+    _, rstd = oracle.rmsnorm_fwd(X, w, eps=0.0)
+    dX, _ = oracle.rmsnorm_bwd(dY, X, w, rstd)
+    assert np.max(np.abs(np.sum(dX * X, axis=1))) < 1e-4
+
+
+def test_softmax_golden_and_invariant():
+    g = golden("softmax")
+    dX = oracle.softmax_bwd(g["dY"], g["Y"])
+    assert rel_err(dX, g["dX"]) < TOL
+    assert np.max(np.abs(dX.sum(axis=1))) < 1e-5  # shift invariance: rows sum to zero
+    assert rel_err(oracle.softmax_fwd(g["X"]), g["Y"]) < TOL
+
+
+def test_xent_golden_and_invariant():
+    g = golden("xent")
+    dL = oracle.xent_bwd(g["logits"], g["targets"], 1.0)
+    assert rel_err(dL, g["dLogits"]) < TOL
+    assert np.max(np.abs(dL.sum(axis=1))) < 1e-5
+    # scale multiplies (the reference uses scale 1: no 1/B, cross-entropy-backward.glsl:77-83)
+    assert rel_err(oracle.xent_bwd(g["logits"], g["targets"], 0.25), 0.25 * g["dLogits"]) < TOL
+    # the target column is the only negative one
+    for r, tgt in enumerate(g["targets"]):
+        assert dL[r, tgt] < 0 and np.all(np.delete(dL[r], tgt) > 0)
+
+
+def test_rope_orthogonal():
+    rng = np.random.default_rng(2)
+    X = rng.standard_normal((7, 8)).astype(np.float32)
+    for mode in ["interleaved", "half"]:
+        Y = oracle.rope(X, mode)
+        np.testing.assert_allclose(np.linalg.norm(Y, axis=1), np.linalg.norm(X, axis=1), rtol=1e-5)
+        np.testing.assert_allclose(oracle.rope(Y, mode, inverse=True), X, atol=1e-5)
+        np.testing.assert_array_equal(Y[0], X[0])  # position 0 is the identity
+    # interleaved pair 0 at position 1 rotates by exactly 1 radian
+    Y = oracle.rope(X, "interleaved")
+    c, s = np.cos(1.0), np.sin(1.0)
+    np.testing.assert_allclose(Y[1, :2], [X[1, 0] * c - X[1, 1] * s, X[1, 0] * s + X[1, 1] * c],
+                               rtol=1e-5)
+
+
+@pytest.mark.parametrize("tag", ["causal_rope", "full_norope", "causal_half"])
+def test_attention_golden(tag):
+    g = golden(f"attn_{tag}")
+    kw = dict(scale=float(g["scale"]), causal=bool(g["causal"]), rope_mode=str(g["rope"]),
+              theta=float(g["theta"]))
+    O, LSE = oracle.attn_fwd(g["Q"], g["K"], g["V"], **kw)
+    assert rel_err(O, g["O"]) < TOL and rel_err(LSE, g["LSE"]) < TOL
+    dQ, dK, dV = oracle.attn_bwd(g["Q"], g["K"], g["V"], g["dO"], g["LSE"], **kw)
+    assert rel_err(dQ, g["dQ"]) < TOL
+    assert rel_err(dK, g["dK"]) < TOL
+    assert rel_err(dV, g["dV"]) < TOL
+
+
+def test_attention_single_key_closed_form():
+    # S == 1: P == 1, so dV == dO and dS == P (dP - rowdot) == 0 -> dQ == dK == 0.
+    rng = np.random.default_rng(3)
+    Q, K, V, dO = (rng.standard_normal((1, 2, 1, 8)).astype(np.float32) for _ in range(4))
+    O, LSE = oracle.attn_fwd(Q, K, V)
+    dQ, dK, dV = oracle.attn_bwd(Q, K, V, dO, LSE)
+    np.testing.assert_allclose(dV, dO, rtol=1e-6)
+    assert np.max(np.abs(dQ)) < 1e-6 and np.max(np.abs(dK)) < 1e-6
+
+
+def test_bitunpack_reference_kat():
+    # tests/test_vsa_training_loop.py:131-148: 0xFFFFFFFF -> all +1, 0 -> all -1
+    ones = oracle.unpack_bits(np.array([[0xFFFFFFFF, 0xFFFFFFFF]], np.uint32), 64)
+    zeros = oracle.unpack_bits(np.array([[0, 0]], np.uint32), 64)
+    assert np.all(ones == 1.0) and np.all(zeros == -1.0)
+    # LSB-first little-endian order equals np.unpackbits(bitorder="little") (vsa_loop.py:170-175)
+    rng = np.random.default_rng(4)
+    bits = rng.integers(0, 2**32, size=(3, 5), dtype=np.uint64).astype(np.uint32)
+    ref = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little").astype(np.float32) * 2 - 1
+    np.testing.assert_array_equal(oracle.unpack_bits(bits, 160), ref)
+
+
+def test_vsa_project_golden():
+    g = golden("vsa_project")
+    D = g["W"].shape[1]
+    np.testing.assert_array_equal(oracle.unpack_bits(g["bits"], D), g["S"])
+    dW, db = oracle.vsa_unpack_project_bwd(g["dY"], g["bits"], D)
+    assert rel_err(dW, g["dW"]) < TOL and rel_err(db, g["db"]) < TOL
+
+
+def test_vsa_project_popcount_identity():
+    # with dY == 1: dW[o, j] = sum_b s_b(j) = 2 * popcount_j - B exactly (integer identity)
+    rng = np.random.default_rng(5)
+    Bn, O, D = 37, 3, 128
+    bits = rng.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    dW, db = oracle.vsa_unpack_project_bwd(np.ones((Bn, O), np.float32), bits, D)
+    pop = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little").sum(axis=0).astype(np.int64)
+    for o in range(O):
+        np.testing.assert_array_equal(dW[o], 2 * pop - Bn)
+    np.testing.assert_array_equal(db, Bn)
+
+
+def test_vsa_surrogate_golden():
+    g = golden("vsa_surrogate")
+    dP = oracle.vsa_surrogate_bwd(g["preds"], g["bits"], g["results"], g["weights"],
+                                  float(g["gamma"]), float(g["delta"]), float(g["lambda_c"]),
+                                  float(g["scale"]))
+    assert rel_err(dP, g["dPreds"]) < TOL
+
+
+def _surrogate_case(preds_fn, gamma, dots_win_run=None, K=4, D=256):
+    rng = np.random.default_rng(6)
+    bits = rng.integers(0, 2**32, size=(1, D // 32), dtype=np.uint64).astype(np.uint32)
+    y = oracle.unpack_bits(bits, D)[0]
+    preds = np.stack([preds_fn(y) for _ in range(K)])[None].astype(np.float32)
+    weights = np.full((1, K), 1.0 / K, np.float32)
+    res = np.zeros((1, 4), np.uint32)
+    res[0, 0], res[0, 1] = 0, 1
+    dw, dr = dots_win_run if dots_win_run else (0.0, 0.0)
+    res[0, 2] = np.float32(dw).view(np.uint32)
+    res[0, 3] = np.float32(dr).view(np.uint32)
+    return preds, bits, res, weights, y
+
+
+def test_vsa_surrogate_reference_kats():
+    K, D = 4, 256
+    # perfect prediction (test_vsa_hypernetwork.py:151-165): every hinge inactive; the
+    # contrastive margin 0.5 - (100 - 99) < 0 is inactive too -> zero gradient
+    p, bits, res, w, y = _surrogate_case(lambda y: 2.0 * y, 0.1, (100.0, 99.0))
+    dP = oracle.vsa_surrogate_bwd(p, bits, res, w, gamma=0.1, delta=0.5, lambda_c=0.3)
+    assert np.count_nonzero(dP) == 0
+    # adversarial (test_vsa_hypernetwork.py:167-178): every hinge active -> -y/D * w_k
+    p, bits, res, w, y = _surrogate_case(lambda y: -np.ones_like(y), 0.1, (100.0, 99.0))
+    p = -np.abs(p) * 0 - y[None, None, :]  # prediction opposes the target everywhere
+    dP = oracle.vsa_surrogate_bwd(p, bits, res, w, gamma=0.1, delta=0.5, lambda_c=0.3)
+    np.testing.assert_allclose(dP[0], np.tile(-y / D / K, (K, 1)), rtol=1e-6)
+    # contrastive too close (test_vsa_hypernetwork.py:192-202): 0.5 - (100 - 99.8) = 0.3 > 0
+    # -> runner-up additionally gets +lambda*y/D
+    p, bits, res, w, y = _surrogate_case(lambda y: 2.0 * y, 0.1, (100.0, 99.8))
+    dP = oracle.vsa_surrogate_bwd(p, bits, res, w, gamma=0.1, delta=0.5, lambda_c=0.3)
+    np.testing.assert_allclose(dP[0, 1], 0.3 * y / D, rtol=1e-6)
+    assert np.count_nonzero(dP[0, [0, 2, 3]]) == 0
