@@ -31,7 +31,8 @@ template <bool SPLIT>
 __global__ __launch_bounds__(256, 2) void vsa_dw_kernel(const void* __restrict__ dYv,
                                                         const uint32_t* __restrict__ bits,
                                                         float* __restrict__ dW, int Bn, int O,
-                                                        int D, int words, int accumulate) {
+                                                        int D, int words, int accumulate,
+                                                        int vec_ok) {
     __shared__ __align__(16) bf16_t sAh[2][VT];
     __shared__ __align__(16) bf16_t sAl[SPLIT ? 2 : 1][SPLIT ? VT : 8];
     __shared__ __align__(16) bf16_t sB[2][VT];
@@ -60,7 +61,17 @@ __global__ __launch_bounds__(256, 2) void vsa_dw_kernel(const void* __restrict__
         for (int r = 0; r < 2; ++r) {
             const int b = b0 + r;
             const int o = o0 + cc * 8;
-            if (SPLIT) {
+            if (!vec_ok) {  // any O: scalar loads with per-element bounds
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const size_t idx = (size_t)b * O + o + e;
+                    float v = 0.f;
+                    if (b < Bn && o + e < O)
+                        v = SPLIT ? reinterpret_cast<const float*>(dYv)[idx]
+                                  : bf2f(reinterpret_cast<const bf16_t*>(dYv)[idx]);
+                    av[r][e] = v;
+                }
+            } else if (SPLIT) {
                 const float* p = reinterpret_cast<const float*>(dYv) + (size_t)b * O + o;
                 if (b < Bn && o < O) {
                     float4 x = *reinterpret_cast<const float4*>(p);
@@ -194,16 +205,15 @@ extern "C" int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, 
     GN_REQUIRE(dY && Xbits && dW, "gn_vsa_unpack_project_bwd: null pointer");
     GN_REQUIRE(D % 32 == 0 && words >= D / 32,
                "gn_vsa_unpack_project_bwd: D=%d must be a multiple of 32 with words >= D/32", D);
-    GN_REQUIRE(O % 8 == 0 && al16(dY), "gn_vsa_unpack_project_bwd: O=%d must be a multiple of 8 "
-               "and dY 16-byte aligned", O);
     GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_vsa_unpack_project_bwd: dtype %d", dtype);
     hipStream_t s = as_stream(stream);
     const int tiles = ((O + VBM - 1) / VBM) * ((D + VBN - 1) / VBN);
     const int acc = (flags & GN_ACCUMULATE) ? 1 : 0;
+    const int vec_ok = (O % 8 == 0) && al16(dY);
     if (dtype == GN_F32)
-        vsa_dw_kernel<true><<<tiles, 256, 0, s>>>(dY, Xbits, dW, Bn, O, D, words, acc);
+        vsa_dw_kernel<true><<<tiles, 256, 0, s>>>(dY, Xbits, dW, Bn, O, D, words, acc, vec_ok);
     else
-        vsa_dw_kernel<false><<<tiles, 256, 0, s>>>(dY, Xbits, dW, Bn, O, D, words, acc);
+        vsa_dw_kernel<false><<<tiles, 256, 0, s>>>(dY, Xbits, dW, Bn, O, D, words, acc, vec_ok);
     GN_LAUNCH_CHECK("gn_vsa_unpack_project_bwd");
     if (db) return colsum_dispatch(dY, db, Bn, O, dtype, flags, s);
     return GN_OK;
