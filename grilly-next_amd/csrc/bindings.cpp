@@ -1,0 +1,204 @@
+// bindings.cpp — pybind11 module `grilly_core`: the reference's autograd API surface
+// (cpp/python/bindings.cpp:2688-2880) on the MI355X tape engine, plus a Device with
+// explicit buffer upload/download (the reference gives Python no way to create a buffer
+// id for its own data, bindings.cpp:2725).
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include "autograd.h"
+#include "device.h"
+#include "gn_bwd.h"
+
+namespace py = pybind11;
+using namespace grilly;
+using namespace grilly::autograd;
+
+namespace {
+
+py::dict stats_dict(const BackwardEngine::Stats& s) {
+    py::dict d;
+    d["nodes_visited"] = s.nodes_visited;
+    d["nodes_with_grad"] = s.nodes_with_grad;
+    d["shaders_dispatched"] = s.shaders_dispatched;
+    d["cpu_fallbacks"] = s.cpu_fallbacks;
+    d["fanout_accumulations"] = s.fanout_accumulations;
+    return d;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(grilly_core, m) {
+    m.doc() = "grilly-next tape autograd on MI355X (HIP kernels through libgn_bwd's C ABI)";
+    m.attr("__backend__") = "hip-gfx950";
+    m.def("kernel_library_version", []() { return std::string(gn_version()); });
+
+    py::class_<Device>(m, "Device")
+        .def(py::init<int>(), py::arg("index") = 0)
+        .def_property_readonly("name", &Device::name)
+        .def_property_readonly("index", &Device::index)
+        .def("use_stream", &Device::use_stream, py::arg("stream_handle"),
+             "Launch on a caller-owned HIP stream (e.g. torch.cuda.current_stream().cuda_stream); 0 = own stream")
+        .def("stream_handle", [](const Device& d) { return reinterpret_cast<uint64_t>(d.stream()); })
+        .def("alloc", &Device::acquire, py::arg("nbytes"))
+        .def("free", &Device::release, py::arg("buffer_id"))
+        .def("buffer_bytes", &Device::buffer_bytes, py::arg("buffer_id"))
+        .def("upload",
+             [](Device& d, py::array arr) {
+                 py::buffer_info bi = py::array::ensure(arr, py::array::c_style).request();
+                 const size_t bytes = (size_t)bi.size * bi.itemsize;
+                 uint64_t id = d.acquire(bytes);
+                 d.upload(id, bi.ptr, bytes);
+                 return id;
+             },
+             py::arg("array"), "Allocate a pool buffer holding a copy of `array`; returns its id")
+        .def("upload_to",
+             [](Device& d, uint64_t id, py::array arr, size_t offset) {
+                 py::buffer_info bi = py::array::ensure(arr, py::array::c_style).request();
+                 d.upload(id, bi.ptr, (size_t)bi.size * bi.itemsize, offset);
+             },
+             py::arg("buffer_id"), py::arg("array"), py::arg("offset") = 0)
+        .def("download",
+             [](Device& d, uint64_t id, std::vector<ssize_t> shape, py::dtype dtype) {
+                 py::array out(dtype, shape);
+                 d.download(id, out.mutable_data(), (size_t)out.nbytes());
+                 return out;
+             },
+             py::arg("buffer_id"), py::arg("shape"), py::arg("dtype"))
+        .def("zero", &Device::zero, py::arg("buffer_id"), py::arg("nbytes"))
+        .def("synchronize", &Device::synchronize)
+        .def("trim", &Device::trim)
+        .def("pool_stats", [](const Device& d) {
+            auto s = d.stats();
+            py::dict r;
+            r["bytes_live"] = s.bytes_live;
+            r["bytes_cached"] = s.bytes_cached;
+            r["allocs"] = s.allocs;
+            r["reuses"] = s.reuses;
+            return r;
+        });
+
+    py::enum_<OpType>(m, "OpType")
+        .value("Add", OpType::Add).value("Sub", OpType::Sub).value("Mul", OpType::Mul)
+        .value("Div", OpType::Div).value("Neg", OpType::Neg).value("Pow", OpType::Pow)
+        .value("MatMul", OpType::MatMul).value("Linear", OpType::Linear)
+        .value("ReLU", OpType::ReLU).value("GELU", OpType::GELU).value("SiLU", OpType::SiLU)
+        .value("Tanh", OpType::Tanh).value("Sigmoid", OpType::Sigmoid)
+        .value("Softmax", OpType::Softmax).value("LayerNorm", OpType::LayerNorm)
+        .value("RMSNorm", OpType::RMSNorm).value("FlashAttention2", OpType::FlashAttention2)
+        .value("Conv2d", OpType::Conv2d).value("Conv1d", OpType::Conv1d)
+        .value("Sum", OpType::Sum).value("Mean", OpType::Mean).value("Max", OpType::Max)
+        .value("Min", OpType::Min).value("Reshape", OpType::Reshape)
+        .value("Transpose", OpType::Transpose).value("Slice", OpType::Slice)
+        .value("CrossEntropy", OpType::CrossEntropy).value("MSELoss", OpType::MSELoss)
+        .value("CubeMindSurprise", OpType::CubeMindSurprise)
+        .value("TemporalSurprise", OpType::TemporalSurprise)
+        .value("VSAUnpackProject", OpType::VSAUnpackProject)
+        .value("VSASurrogateLoss", OpType::VSASurrogateLoss)
+        .value("VSALoRAExpand", OpType::VSALoRAExpand)
+        .value("VSACosineBlendLoss", OpType::VSACosineBlendLoss)
+        .value("FusedGLU", OpType::FusedGLU)
+        .export_values();
+
+    py::class_<TensorRef>(m, "TensorRef")
+        .def(py::init([]() { return TensorRef::none(); }))
+        .def_readwrite("buffer_id", &TensorRef::buffer_id)
+        .def_readwrite("ndim", &TensorRef::ndim)
+        .def_readwrite("dtype", &TensorRef::dtype)
+        .def_readwrite("requires_grad", &TensorRef::requires_grad)
+        .def("numel", &TensorRef::numel)
+        .def("size_bytes", &TensorRef::size_bytes)
+        .def("valid", &TensorRef::valid)
+        .def_static("none", &TensorRef::none)
+        .def("set_shape",
+             [](TensorRef& r, const std::vector<uint32_t>& shape) {
+                 if (shape.size() > 8) throw py::value_error("TensorRef: at most 8 dimensions");
+                 r.ndim = (uint32_t)shape.size();
+                 for (uint32_t i = 0; i < r.ndim; ++i) r.shape[i] = shape[i];
+             },
+             py::arg("shape"))
+        .def("get_shape", [](const TensorRef& r) {
+            return std::vector<uint32_t>(r.shape, r.shape + r.ndim);
+        });
+
+    py::class_<TapeContext>(m, "TapeContext")
+        .def(py::init<Device&, size_t>(), py::arg("device"),
+             py::arg("arena_capacity") = TapeArena::kDefaultCapacity, py::keep_alive<1, 2>())
+        .def("begin", &TapeContext::begin)
+        .def("record_op",
+             [](TapeContext& t, OpType op, const std::vector<TensorRef>& inputs,
+                const std::vector<TensorRef>& outputs, py::bytes params) {
+                 std::string p = params;
+                 return t.record_op(op, inputs.data(), (uint32_t)inputs.size(), outputs.data(),
+                                    (uint32_t)outputs.size(), p.empty() ? nullptr : p.data(),
+                                    (uint32_t)p.size());
+             },
+             py::arg("op"), py::arg("inputs"), py::arg("outputs"), py::arg("params") = py::bytes(),
+             py::return_value_policy::reference)
+        .def("save_for_backward",
+             [](TapeContext& t, Node* node, const std::vector<uint64_t>& ids) {
+                 t.save_for_backward(node, ids.data(), (uint32_t)ids.size());
+             },
+             py::arg("node"), py::arg("buffer_ids"))
+        .def("backward",
+             [](TapeContext& t, Node* loss, uint64_t g) { t.backward(loss, g); },
+             py::arg("loss_node"), py::arg("grad_output_buffer"))
+        .def("get_grad_buffer", &TapeContext::get_grad_buffer, py::arg("input_buffer_id"))
+        .def("record_temporal_surprise",
+             [](TapeContext& t, const TensorRef& input, const TensorRef& output, float coh,
+                float contra, uint32_t branches, uint32_t dt, float alpha) {
+                 TemporalSurpriseParams p{coh, contra, 1.0f - 2.0f * contra, alpha, branches, dt};
+                 TensorRef ins[1] = {input}, outs[1] = {output};
+                 return t.record_op(OpType::TemporalSurprise, ins, 1, outs, 1, &p, sizeof(p));
+             },
+             py::arg("input"), py::arg("output"), py::arg("avg_coherence"),
+             py::arg("avg_contradiction"), py::arg("num_branches") = 128, py::arg("dt") = 1,
+             py::arg("alpha") = 1.0f, py::return_value_policy::reference)
+        .def("end", &TapeContext::end)
+        .def("acquire_temp", &TapeContext::acquire_temp, py::arg("nbytes"))
+        .def("is_recording", &TapeContext::is_recording)
+        .def("arena_bytes_used", &TapeContext::arena_bytes_used)
+        .def("arena_utilization", &TapeContext::arena_utilization)
+        .def("last_backward_stats", [](const TapeContext& t) { return stats_dict(t.last_backward_stats()); });
+
+    py::class_<Node>(m, "AutogradNode")
+        .def_readonly("op", &Node::op)
+        .def_readonly("seq", &Node::seq)
+        .def_readonly("num_inputs", &Node::num_inputs)
+        .def_readonly("num_outputs", &Node::num_outputs)
+        .def_readonly("num_saved", &Node::num_saved)
+        .def_readonly("grad_output_buffer", &Node::grad_output_buffer)
+        .def("get_grad_input_buffer",
+             [](const Node& n, uint32_t i) -> uint64_t { return i < kMaxNodeIO ? n.grad_input_buffers[i] : 0; },
+             py::arg("index"))
+        .def("get_input",
+             [](const Node& n, uint32_t i) { return i < kMaxNodeIO ? n.inputs[i] : TensorRef::none(); },
+             py::arg("index"))
+        .def("get_output",
+             [](const Node& n, uint32_t i) { return i < kMaxNodeIO ? n.outputs[i] : TensorRef::none(); },
+             py::arg("index"))
+        .def("get_saved_buffer",
+             [](const Node& n, uint32_t i) -> uint64_t { return i < kMaxNodeIO ? n.saved_buffer_ids[i] : 0; },
+             py::arg("index"));
+
+    // Host-only view of the bump allocator, for tests of its failure behaviour.
+    py::class_<TapeArena>(m, "_TapeArena")
+        .def(py::init<size_t>(), py::arg("capacity"))
+        .def("allocate", [](TapeArena& a, size_t bytes, size_t align) {
+            return reinterpret_cast<uintptr_t>(a.allocate_bytes(bytes, align));
+        }, py::arg("nbytes"), py::arg("align") = 16)
+        .def("reset", &TapeArena::reset)
+        .def("bytes_used", &TapeArena::bytes_used)
+        .def("utilization", &TapeArena::utilization)
+        .def("save", [](const TapeArena& a) { return a.save().offset; })
+        .def("restore", [](TapeArena& a, size_t off) { a.restore({off, nullptr}); });
+    m.attr("NODE_BYTES") = sizeof(Node);
+
+    py::register_exception_translator([](std::exception_ptr p) {
+        try {
+            if (p) std::rethrow_exception(p);
+        } catch (const std::length_error& e) {
+            PyErr_SetString(PyExc_OverflowError, e.what());
+        }
+    });
+}

@@ -25,8 +25,12 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LDS_PITCH = BK + 8;  // bf16 elements per LDS row (144 bytes)
+constexpr int LDS_PITCH = BK;  // bf16 elements per LDS row (128 bytes, XOR-swizzled chunks)
 constexpr int TILE_ELEMS = 128 * LDS_PITCH;
+
+// 16-byte chunk c of row r lives at chunk c ^ swz(r).  Fragment reads (32 consecutive rows,
+// one chunk) and the transposed stores (rows 8 apart) both spread over all 8 chunk slots.
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
 
 struct GemmArgs {
     const bf16_t* A[2];
@@ -76,7 +80,8 @@ __device__ __forceinline__ void store_tile(bf16_t* __restrict__ s, const uint4 (
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = t + 256 * i;
-            *reinterpret_cast<uint4*>(s + (c >> 3) * LDS_PITCH + (c & 7) * 8) = reg[i];
+            const int r = c >> 3;
+            *reinterpret_cast<uint4*>(s + r * LDS_PITCH + (((c & 7) ^ swz(r)) * 8)) = reg[i];
         }
     } else {
         // reg[i] holds row k = kg*4+i, columns rc*8 .. rc*8+7 (two bf16 per dword).
@@ -94,8 +99,9 @@ __device__ __forceinline__ void store_tile(bf16_t* __restrict__ s, const uint4 (
             lo.y = __builtin_amdgcn_perm(w3[d], w2[d], 0x05040100u);
             hi.x = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);
             hi.y = __builtin_amdgcn_perm(w3[d], w2[d], 0x07060302u);
-            *reinterpret_cast<uint2*>(s + (rc * 8 + 2 * d) * LDS_PITCH + kg * 4) = lo;
-            *reinterpret_cast<uint2*>(s + (rc * 8 + 2 * d + 1) * LDS_PITCH + kg * 4) = hi;
+            const int r0 = rc * 8 + 2 * d, r1 = r0 + 1;
+            *reinterpret_cast<uint2*>(s + r0 * LDS_PITCH + (((kg >> 1) ^ swz(r0)) * 8) + (kg & 1) * 4) = lo;
+            *reinterpret_cast<uint2*>(s + r1 * LDS_PITCH + (((kg >> 1) ^ swz(r1)) * 8) + (kg & 1) * 4) = hi;
         }
     }
 }
@@ -163,18 +169,22 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma(GemmArgs g) {
     }
     __syncthreads();
 
-    const int frow = lane & 31, fk = (lane >> 5) * 8;
+    const int frow = lane & 31, fhalf = lane >> 5;
+    // fragment rows: a rows wm*64 + {0,32} + frow, b rows wn*64 + {0,32} + frow
+    const int ra0 = wm * 64 + frow, ra1 = ra0 + 32, rb0 = wn * 64 + frow, rb1 = rb0 + 32;
+    const int sa0 = swz(ra0), sa1 = swz(ra1), sb0 = swz(rb0), sb1 = swz(rb1);
     for (int t = 0; t < KT; ++t) {
         const int cur = t & 1;
         if (t + 1 < KT) gload(t + 1);
-        const bf16_t* a_base = sA + cur * TILE_ELEMS + (wm * 64 + frow) * LDS_PITCH + fk;
-        const bf16_t* b_base = sB + cur * TILE_ELEMS + (wn * 64 + frow) * LDS_PITCH + fk;
+        const bf16_t* As = sA + cur * TILE_ELEMS;
+        const bf16_t* Bs = sB + cur * TILE_ELEMS;
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
-            bf16x8_t a0 = lds_frag(a_base + ks * 16);
-            bf16x8_t a1 = lds_frag(a_base + 32 * LDS_PITCH + ks * 16);
-            bf16x8_t b0 = lds_frag(b_base + ks * 16);
-            bf16x8_t b1 = lds_frag(b_base + 32 * LDS_PITCH + ks * 16);
+            const int ch = ks * 2 + fhalf;
+            bf16x8_t a0 = lds_frag(As + ra0 * LDS_PITCH + ((ch ^ sa0) * 8));
+            bf16x8_t a1 = lds_frag(As + ra1 * LDS_PITCH + ((ch ^ sa1) * 8));
+            bf16x8_t b0 = lds_frag(Bs + rb0 * LDS_PITCH + ((ch ^ sb0) * 8));
+            bf16x8_t b1 = lds_frag(Bs + rb1 * LDS_PITCH + ((ch ^ sb1) * 8));
             acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
             acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc[0][1], 0, 0, 0);
             acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);

@@ -1,0 +1,451 @@
+// autograd.cpp — BackwardEngine and TapeContext (see autograd.h for the contract).
+#include "autograd.h"
+
+#include <cmath>
+#include <string>
+
+#include "gn_bwd.h"
+
+namespace grilly {
+namespace autograd {
+
+namespace {
+
+int gn_dtype(uint32_t d, const char* what) {
+    if (d == 0) return GN_F32;
+    if (d == 4) return GN_BF16;
+    throw std::invalid_argument(std::string(what) + ": tensor dtype must be f32 (0) or bf16 (4)");
+}
+
+void gn_call(int rc, const char* what) {
+    if (rc != GN_OK) throw std::runtime_error(std::string(what) + ": " + gn_last_error());
+}
+
+void* P(uint64_t id) { return reinterpret_cast<void*>(id); }
+
+template <typename T>
+T params_of(const Node* n) {
+    T p{};
+    std::memcpy(&p, n->params, std::min<size_t>(sizeof(T), n->params_size));
+    return p;
+}
+
+inline uint64_t mix(uint64_t x) {
+    x ^= x >> 33;
+    x *= 0xff51afd7ed558ccdULL;
+    x ^= x >> 33;
+    return x;
+}
+
+}  // namespace
+
+// ═════════════════════════════════════════════════════════════════════ BackwardEngine
+
+BackwardEngine::BackwardEngine(Device& dev) : dev_(dev), table_(kGradTableSize) { clear_grads(); }
+
+void BackwardEngine::clear_grads() {
+    for (auto& e : table_) e = GradEntry{};
+    count_ = 0;
+}
+
+BackwardEngine::GradEntry* BackwardEngine::find(uint64_t id) const {
+    if (id == 0) return nullptr;
+    const size_t mask = kGradTableSize - 1;
+    for (size_t i = mix(id) & mask, probes = 0; probes < kGradTableSize; i = (i + 1) & mask, ++probes) {
+        if (table_[i].buffer_id == id) return &table_[i];
+        if (table_[i].buffer_id == 0) return nullptr;
+    }
+    return nullptr;
+}
+
+BackwardEngine::GradEntry* BackwardEngine::find_or_insert(uint64_t id) {
+    if (GradEntry* e = find(id)) return e;
+    if (count_ >= kGradTableSize * 3 / 4)
+        throw std::length_error("BackwardEngine: gradient table full (more than 6144 tensors)");
+    const size_t mask = kGradTableSize - 1;
+    size_t i = mix(id) & mask;
+    while (table_[i].buffer_id != 0) i = (i + 1) & mask;
+    table_[i] = GradEntry{id, 0, 0, 0, false};
+    ++count_;
+    return &table_[i];
+}
+
+uint64_t BackwardEngine::get_grad_buffer(uint64_t id) const {
+    const GradEntry* e = find(id);
+    return e ? e->grad_id : 0ULL;
+}
+
+uint64_t BackwardEngine::alloc_grad(size_t bytes) {
+    uint64_t id = dev_.acquire(bytes);
+    backward_bufs_.push_back(id);
+    return id;
+}
+
+void BackwardEngine::contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t numel, bool owned) {
+    if (id == 0 || g == 0) return;
+    GradEntry* e = find_or_insert(id);
+    const size_t bytes = numel * TensorRef::elem_size(dtype);
+    if (e->grad_id == 0) {
+        *e = GradEntry{id, g, bytes, dtype, owned};
+        return;
+    }
+    if (e->grad_id == g) return;  // same buffer recorded twice
+    // fan-out: the second consumer's gradient is added (autograd.cpp:78-86 drops it)
+    if (e->dtype != dtype || e->grad_bytes != bytes)
+        throw std::runtime_error("BackwardEngine: fan-out gradients disagree in dtype or size");
+    if (!e->owned) {
+        uint64_t fresh = alloc_grad(bytes);
+        hip_check(hipMemcpyAsync(P(fresh), P(e->grad_id), bytes, hipMemcpyDeviceToDevice,
+                                 dev_.stream()), "fan-out copy");
+        e->grad_id = fresh;
+        e->owned = true;
+    }
+    gn_call(gn_add_inplace(P(e->grad_id), P(g), (int64_t)numel, gn_dtype(dtype, "fan-out"),
+                           dev_.stream()), "fan-out add");
+    stats_.fanout_accumulations++;
+    stats_.shaders_dispatched++;
+}
+
+const void* BackwardEngine::gout(Node* n) const {
+    if (n->grad_output_buffer <= 1)
+        throw std::invalid_argument(
+            "backward: this node needs an upstream gradient buffer (grad_output_buffer)");
+    return P(n->grad_output_buffer);
+}
+
+void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_output_buffer) {
+    stats_ = {};
+    if (!loss_node) throw std::invalid_argument("backward: loss node is None");
+    // autograd.cpp:30-31: 0 means "the loss computes its own gradient" (sentinel 1)
+    loss_node->grad_output_buffer = grad_output_buffer ? grad_output_buffer : 1ULL;
+    for (Node* cur = tape.tail<Node>(); cur != nullptr; cur = cur->prev_in_tape) {
+        stats_.nodes_visited++;
+        if (cur->grad_output_buffer == 0) {
+            for (uint32_t i = 0; i < cur->num_outputs && i < kMaxNodeIO; ++i) {
+                uint64_t g = get_grad_buffer(cur->outputs[i].buffer_id);
+                if (g) {
+                    cur->grad_output_buffer = g;
+                    break;
+                }
+            }
+        }
+        if (cur->grad_output_buffer == 0) continue;
+        stats_.nodes_with_grad++;
+        std::memset(cur->grad_input_buffers, 0, sizeof(cur->grad_input_buffers));
+        borrowed_ = 0;
+        dispatch(cur);
+        for (uint32_t i = 0; i < cur->num_inputs && i < kMaxNodeIO; ++i) {
+            const TensorRef& in = cur->inputs[i];
+            if (!in.requires_grad || cur->grad_input_buffers[i] == 0) continue;
+            contribute(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(),
+                       !((borrowed_ >> i) & 1u));
+        }
+    }
+}
+
+void BackwardEngine::dispatch(Node* n) {
+    switch (n->op) {
+        case OpType::Linear: bwd_linear(n); break;
+        case OpType::ReLU: bwd_act(n, GN_ACT_RELU, false); break;
+        case OpType::GELU:
+            bwd_act(n, params_of<GELUParams>(n).erf_form ? GN_ACT_GELU_ERF : GN_ACT_GELU_TANH, false);
+            break;
+        case OpType::SiLU: bwd_act(n, GN_ACT_SILU, false); break;
+        case OpType::Tanh: bwd_act(n, GN_ACT_TANH, true); break;
+        case OpType::Sigmoid: bwd_act(n, GN_ACT_SIGMOID, true); break;
+        case OpType::Softmax: bwd_softmax(n); break;
+        case OpType::LayerNorm: bwd_layernorm(n); break;
+        case OpType::RMSNorm: bwd_rmsnorm(n); break;
+        case OpType::FlashAttention2: bwd_attention(n); break;
+        case OpType::CrossEntropy: bwd_cross_entropy(n); break;
+        case OpType::Add: bwd_add_sub(n, false); break;
+        case OpType::Reshape: bwd_passthrough(n); break;
+        case OpType::VSAUnpackProject: bwd_vsa_unpack_project(n); break;
+        case OpType::VSASurrogateLoss: bwd_vsa_surrogate(n); break;
+        case OpType::FusedGLU: bwd_fused_glu(n); break;
+        default: stats_.cpu_fallbacks++; break;  // no handler (autograd.cpp:126-128)
+    }
+}
+
+// Linear: y = x W^T + b (autograd.cpp:172-305); saved[0] = W [N x K], saved[1] = b or 0.
+void BackwardEngine::bwd_linear(Node* n) {
+    const TensorRef& x = n->inputs[0];
+    const TensorRef& y = n->outputs[0];
+    const int M = (int)x.rows(), K = (int)x.last(), N = (int)y.last();
+    if ((size_t)M != y.rows()) throw std::invalid_argument("Linear: input/output rows differ");
+    const int dt = gn_dtype(x.dtype, "Linear");
+    const uint64_t W = n->saved_buffer_ids[0], b = n->num_saved > 1 ? n->saved_buffer_ids[1] : 0;
+    if (!W) throw std::invalid_argument("Linear: saved_buffer_ids[0] must hold W");
+    uint64_t dX = x.requires_grad ? alloc_grad(x.size_bytes()) : 0;
+    uint64_t dW = alloc_grad((size_t)N * K * 4);
+    uint64_t db = b ? alloc_grad((size_t)N * 4) : 0;
+    gn_call(gn_linear_bwd(gout(n), P(x.buffer_id), P(W), P(dX), P(dW), P(db), M, N, K, dt, 0,
+                          dev_.stream()), "Linear backward");
+    stats_.shaders_dispatched += db ? 3 : 2;
+    n->grad_input_buffers[0] = dX;
+    contribute(W, dW, 0, (size_t)N * K, true);
+    if (b) contribute(b, db, 0, (size_t)N, true);
+}
+
+// Elementwise activations; tanh/sigmoid read the saved output (activation-tanh-backward.glsl:33).
+void BackwardEngine::bwd_act(Node* n, int kind, bool uses_output) {
+    const TensorRef& x = n->inputs[0];
+    if (!x.requires_grad) return;
+    const uint64_t src = uses_output ? n->outputs[0].buffer_id : x.buffer_id;
+    uint64_t dX = alloc_grad(x.size_bytes());
+    gn_call(gn_act_bwd(kind, gout(n), P(src), P(dX), (int64_t)x.numel(), gn_dtype(x.dtype, "activation"),
+                       0, dev_.stream()), "activation backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dX;
+}
+
+void BackwardEngine::bwd_softmax(Node* n) {
+    const TensorRef& x = n->inputs[0];
+    const TensorRef& y = n->outputs[0];
+    if (!x.requires_grad) return;
+    uint64_t dX = alloc_grad(x.size_bytes());
+    gn_call(gn_softmax_bwd(gout(n), P(y.buffer_id), P(dX), (int)y.rows(), (int)y.last(),
+                           gn_dtype(y.dtype, "Softmax"), dev_.stream()), "Softmax backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dX;
+}
+
+// saved: [0] gamma, [1] beta (or 0), [2] mean, [3] rstd (or var with stat_is_var)
+void BackwardEngine::bwd_layernorm(Node* n) {
+    const TensorRef& x = n->inputs[0];
+    const int rows = (int)x.rows(), F = (int)x.last();
+    LayerNormParams p = params_of<LayerNormParams>(n);
+    if (p.eps == 0.f) p.eps = 1e-5f;
+    const uint64_t gamma = n->saved_buffer_ids[0], beta = n->saved_buffer_ids[1];
+    const uint64_t mean = n->saved_buffer_ids[2], rstd = n->saved_buffer_ids[3];
+    if (!gamma || !mean || !rstd) throw std::invalid_argument("LayerNorm: saved gamma/mean/rstd missing");
+    uint64_t dX = alloc_grad(x.size_bytes());
+    uint64_t dG = alloc_grad((size_t)F * 4);
+    uint64_t dB = beta ? alloc_grad((size_t)F * 4) : 0;
+    const size_t wsb = gn_norm_workspace_bytes(rows, F);
+    uint64_t ws = alloc_grad(wsb);
+    gn_call(gn_layernorm_bwd(gout(n), P(x.buffer_id), P(gamma), (const float*)P(mean),
+                             (const float*)P(rstd), P(dX), (float*)P(dG), (float*)P(dB), rows, F,
+                             p.eps, gn_dtype(x.dtype, "LayerNorm"), p.stat_is_var ? GN_LN_STAT_VAR : 0,
+                             P(ws), wsb, dev_.stream()), "LayerNorm backward");
+    stats_.shaders_dispatched += 2;
+    if (x.requires_grad) n->grad_input_buffers[0] = dX;
+    contribute(gamma, dG, 0, F, true);
+    if (beta) contribute(beta, dB, 0, F, true);
+}
+
+// saved: [0] w, [1] rstd (fp32 per row)
+void BackwardEngine::bwd_rmsnorm(Node* n) {
+    const TensorRef& x = n->inputs[0];
+    const int rows = (int)x.rows(), F = (int)x.last();
+    const uint64_t w = n->saved_buffer_ids[0], rstd = n->saved_buffer_ids[1];
+    if (!w || !rstd) throw std::invalid_argument("RMSNorm: saved w/rstd missing");
+    uint64_t dX = alloc_grad(x.size_bytes());
+    uint64_t dW = alloc_grad((size_t)F * 4);
+    const size_t wsb = gn_norm_workspace_bytes(rows, F);
+    uint64_t ws = alloc_grad(wsb);
+    gn_call(gn_rmsnorm_bwd(gout(n), P(x.buffer_id), P(w), (const float*)P(rstd), P(dX),
+                           (float*)P(dW), rows, F, gn_dtype(x.dtype, "RMSNorm"), 0, P(ws), wsb,
+                           dev_.stream()), "RMSNorm backward");
+    stats_.shaders_dispatched += 2;
+    if (x.requires_grad) n->grad_input_buffers[0] = dX;
+    contribute(w, dW, 0, F, true);
+}
+
+// inputs Q, K, V [B, H, S, D]; outputs[0] = O; saved[0] = LSE fp32 [B*H*S]
+void BackwardEngine::bwd_attention(Node* n) {
+    const TensorRef& q = n->inputs[0];
+    const TensorRef& k = n->inputs[1];
+    const TensorRef& v = n->inputs[2];
+    if (q.ndim < 3) throw std::invalid_argument("FlashAttention2: Q must be [B,H,S,D] or [H,S,D]");
+    const int D = (int)q.shape[q.ndim - 1], S = (int)q.shape[q.ndim - 2];
+    const int H = (int)q.shape[q.ndim - 3], B = q.ndim >= 4 ? (int)q.shape[q.ndim - 4] : 1;
+    AttentionParams p = params_of<AttentionParams>(n);
+    const float scale = p.scale != 0.f ? p.scale : 1.0f / std::sqrt((float)D);
+    const float theta = p.rope_theta != 0.f ? p.rope_theta : 10000.f;
+    const uint64_t lse = n->saved_buffer_ids[0];
+    if (!lse) throw std::invalid_argument("FlashAttention2: saved LSE missing");
+    uint64_t dQ = alloc_grad(q.size_bytes()), dK = alloc_grad(k.size_bytes()), dV = alloc_grad(v.size_bytes());
+    const size_t wsb = gn_attn_workspace_bytes(B, H, S, D);
+    uint64_t ws = alloc_grad(wsb);
+    gn_call(gn_attn_bwd(P(q.buffer_id), P(k.buffer_id), P(v.buffer_id), P(n->outputs[0].buffer_id),
+                        gout(n), (const float*)P(lse), P(dQ), P(dK), P(dV), B, H, S, D, scale,
+                        (int)p.causal, (int)p.rope_mode, theta, gn_dtype(q.dtype, "FlashAttention2"),
+                        P(ws), wsb, dev_.stream()), "attention backward");
+    stats_.shaders_dispatched += 3;
+    n->grad_input_buffers[0] = dQ;
+    n->grad_input_buffers[1] = dK;
+    n->grad_input_buffers[2] = dV;
+}
+
+// cross-entropy-backward.glsl:29-84: softmax - onehot, scaled (default 1: no 1/B).  The
+// loss is a root: like the reference shader it takes no upstream gradient.
+void BackwardEngine::bwd_cross_entropy(Node* n) {
+    const TensorRef& z = n->inputs[0];
+    const TensorRef& t = n->inputs[1];
+    if (!z.requires_grad) return;
+    CrossEntropyParams p = params_of<CrossEntropyParams>(n);
+    const float scale = p.has_scale ? p.scale : 1.0f;
+    uint64_t dZ = alloc_grad(z.size_bytes());
+    gn_call(gn_xent_bwd(P(z.buffer_id), (const int32_t*)P(t.buffer_id), P(dZ), (int)z.rows(),
+                        (int)z.last(), scale, gn_dtype(z.dtype, "CrossEntropy"), dev_.stream()),
+            "cross-entropy backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dZ;
+}
+
+// Add: both inputs receive the upstream gradient itself (borrowed, copied on fan-out).
+void BackwardEngine::bwd_add_sub(Node* n, bool /*sub*/) {
+    const uint64_t g = reinterpret_cast<uint64_t>(gout(n));
+    for (uint32_t i = 0; i < n->num_inputs && i < 2; ++i) {
+        if (!n->inputs[i].requires_grad) continue;
+        if (n->inputs[i].numel() != n->outputs[0].numel())
+            throw std::invalid_argument("Add: broadcasting inputs are not supported");
+        n->grad_input_buffers[i] = g;
+        borrowed_ |= 1u << i;
+    }
+}
+
+void BackwardEngine::bwd_passthrough(Node* n) {
+    if (!n->inputs[0].requires_grad) return;
+    n->grad_input_buffers[0] = reinterpret_cast<uint64_t>(gout(n));
+    borrowed_ |= 1u;
+}
+
+// backward_vsa_unpack_project (autograd.cpp:727-815): inputs[0] = bits [Bn, words] (or
+// [words] for one row), outputs[0] = y [Bn, O]; saved[0] = W [O x D], saved[1] = b or 0.
+void BackwardEngine::bwd_vsa_unpack_project(Node* n) {
+    const TensorRef& bits = n->inputs[0];
+    const TensorRef& y = n->outputs[0];
+    const int words = (int)bits.last();
+    const int Bn = bits.ndim >= 2 ? (int)bits.rows() : 1;
+    const int O = (int)y.last(), D = words * 32;
+    const uint64_t W = n->saved_buffer_ids[0], b = n->num_saved > 1 ? n->saved_buffer_ids[1] : 0;
+    uint64_t dW = alloc_grad((size_t)O * D * 4);
+    uint64_t db = b ? alloc_grad((size_t)O * 4) : 0;
+    gn_call(gn_vsa_unpack_project_bwd(gout(n), (const uint32_t*)P(bits.buffer_id), (float*)P(dW),
+                                      (float*)P(db), Bn, O, D, words, gn_dtype(y.dtype, "VSAUnpackProject"),
+                                      0, nullptr, 0, dev_.stream()), "VSA unpack-project backward");
+    stats_.shaders_dispatched += db ? 2 : 1;
+    n->grad_input_buffers[0] = 0;  // bitpacked input: no gradient
+    if (W) contribute(W, dW, 0, (size_t)O * D, true);
+    if (b) contribute(b, db, 0, (size_t)O, true);
+}
+
+// backward_vsa_surrogate_loss (autograd.cpp:713-725): grad scale 1; saved[n-2] = results,
+// saved[n-1] = weights (vsa_loss_node.cpp:156-159, 209-215).
+void BackwardEngine::bwd_vsa_surrogate(Node* n) {
+    VSASurrogateLossParams p = params_of<VSASurrogateLossParams>(n);
+    const TensorRef& preds = n->inputs[0];
+    const TensorRef& bits = n->inputs[1];
+    if (n->num_saved < 2) throw std::invalid_argument("VSASurrogateLoss: results/weights not saved");
+    const int Bn = (int)preds.shape[0];
+    const int words = (int)((p.D + 31) / 32);
+    uint64_t dP = alloc_grad((size_t)Bn * p.K * p.D * 4);
+    gn_call(gn_vsa_surrogate_bwd((const float*)P(preds.buffer_id), (const uint32_t*)P(bits.buffer_id),
+                                 (const uint32_t*)P(n->saved_buffer_ids[n->num_saved - 2]),
+                                 (const float*)P(n->saved_buffer_ids[n->num_saved - 1]), (float*)P(dP),
+                                 Bn, (int)p.K, (int)p.D, words, p.gamma, p.delta_margin, p.lambda,
+                                 1.0f, 0, dev_.stream()), "VSA surrogate backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dP;
+}
+
+// FusedGLU: inputs[0] = X [M x K]; outputs[0] = glu(gate, up) [M x H];
+// saved: [0] Wg, [1] Wu, [2] gate, [3] up, [4] bg or 0, [5] bu or 0.
+void BackwardEngine::bwd_fused_glu(Node* n) {
+    const TensorRef& x = n->inputs[0];
+    const TensorRef& y = n->outputs[0];
+    const int M = (int)x.rows(), K = (int)x.last(), H = (int)y.last();
+    const uint64_t* s = n->saved_buffer_ids;
+    if (!s[0] || !s[1] || !s[2] || !s[3]) throw std::invalid_argument("FusedGLU: saved Wg/Wu/gate/up missing");
+    const uint64_t bg = n->num_saved > 4 ? s[4] : 0, bu = n->num_saved > 5 ? s[5] : 0;
+    const int dt = gn_dtype(x.dtype, "FusedGLU");
+    const size_t es = TensorRef::elem_size(x.dtype);
+    uint64_t dX = x.requires_grad ? alloc_grad(x.size_bytes()) : 0;
+    uint64_t dWg = alloc_grad((size_t)H * K * 4), dWu = alloc_grad((size_t)H * K * 4);
+    uint64_t dbg = bg ? alloc_grad((size_t)H * 4) : 0, dbu = bu ? alloc_grad((size_t)H * 4) : 0;
+    uint64_t gu = alloc_grad((size_t)2 * M * H * es);
+    gn_call(gn_glu_linear_bwd((int)params_of<FusedGLUParams>(n).kind, gout(n), P(s[2]), P(s[3]),
+                              P(x.buffer_id), P(s[0]), P(s[1]), P(dX), P(dWg), P(dWu), P(dbg), P(dbu),
+                              P(gu), M, K, H, dt, 0, dev_.stream()), "FusedGLU backward");
+    stats_.shaders_dispatched += 4;
+    n->grad_input_buffers[0] = dX;
+    contribute(s[0], dWg, 0, (size_t)H * K, true);
+    contribute(s[1], dWu, 0, (size_t)H * K, true);
+    if (bg) contribute(bg, dbg, 0, H, true);
+    if (bu) contribute(bu, dbu, 0, H, true);
+}
+
+// ═════════════════════════════════════════════════════════════════════ TapeContext
+
+TapeContext::TapeContext(Device& dev, size_t arena_capacity)
+    : dev_(dev), arena_(arena_capacity), engine_(dev) {}
+
+uint64_t TapeContext::acquire_temp(size_t bytes) {
+    uint64_t id = dev_.acquire(bytes);
+    step_bufs_.push_back(id);
+    return id;
+}
+
+void TapeContext::begin() {
+    arena_.reset();
+    engine_.clear_grads();
+    seq_ = 0;
+    recording_ = true;
+}
+
+// autograd.cpp:884-917
+Node* TapeContext::record_op(OpType op, const TensorRef* inputs, uint32_t num_inputs,
+                             const TensorRef* outputs, uint32_t num_outputs, const void* params,
+                             uint32_t params_size) {
+    if (!recording_) return nullptr;
+    Node* node = arena_.allocate_node<Node>();
+    node->op = op;
+    node->seq = seq_++;
+    node->num_inputs = std::min(num_inputs, kMaxNodeIO);
+    node->num_outputs = std::min(num_outputs, kMaxNodeIO);
+    node->num_saved = 0;
+    node->grad_output_buffer = 0;
+    node->params_size = 0;
+    node->emotion[0] = node->emotion[1] = 0.f;
+    std::memset(node->inputs, 0, sizeof(node->inputs));
+    std::memset(node->outputs, 0, sizeof(node->outputs));
+    std::memset(node->saved_buffer_ids, 0, sizeof(node->saved_buffer_ids));
+    std::memset(node->grad_input_buffers, 0, sizeof(node->grad_input_buffers));
+    std::memset(node->params, 0, sizeof(node->params));
+    for (uint32_t i = 0; i < node->num_inputs; ++i) node->inputs[i] = inputs[i];
+    for (uint32_t i = 0; i < node->num_outputs; ++i) node->outputs[i] = outputs[i];
+    if (params && params_size > 0) {
+        if (params_size > sizeof(node->params))
+            throw std::invalid_argument("record_op: params larger than 64 bytes");
+        std::memcpy(node->params, params, params_size);
+        node->params_size = params_size;
+    }
+    return node;
+}
+
+void TapeContext::save_for_backward(Node* node, const uint64_t* ids, uint32_t count) {
+    if (!node) return;
+    for (uint32_t i = 0; i < count && i < kMaxNodeIO; ++i) node->saved_buffer_ids[i] = ids[i];
+    node->num_saved = std::min(count, kMaxNodeIO);
+}
+
+void TapeContext::backward(Node* loss_node, uint64_t grad_output_buffer) {
+    recording_ = false;
+    engine_.backward(arena_, loss_node, grad_output_buffer);
+}
+
+void TapeContext::end() {
+    for (uint64_t b : step_bufs_) dev_.release(b);
+    step_bufs_.clear();
+    for (uint64_t b : engine_.backward_bufs_) dev_.release(b);
+    engine_.backward_bufs_.clear();
+    arena_.reset();
+    engine_.clear_grads();
+    seq_ = 0;
+    recording_ = false;
+}
+
+}  // namespace autograd
+}  // namespace grilly

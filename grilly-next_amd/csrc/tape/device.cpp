@@ -1,0 +1,121 @@
+// device.cpp — HIP device, stream and caching buffer pool (see device.h).
+#include "device.h"
+
+#include <cstring>
+
+namespace grilly {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+Device::Device(int index) : index_(index) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        throw std::runtime_error("grilly_core.Device: no HIP device is visible");
+    if (index < 0 || index >= n) throw std::runtime_error("grilly_core.Device: bad device index");
+    hip_check(hipSetDevice(index), "hipSetDevice");
+    hipDeviceProp_t prop;
+    hip_check(hipGetDeviceProperties(&prop, index), "hipGetDeviceProperties");
+    name_ = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    // default-priority stream (work on streams of different priorities is avoided)
+    hip_check(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
+    stream_ = own_stream_;
+}
+
+Device::~Device() {
+    hipSetDevice(index_);
+    hipStreamSynchronize(stream_);
+    std::lock_guard<std::mutex> g(mu_);
+    for (auto& kv : free_) hipFree(reinterpret_cast<void*>(kv.second));
+    for (auto& kv : live_) hipFree(reinterpret_cast<void*>(kv.first));
+    if (own_stream_) hipStreamDestroy(own_stream_);
+}
+
+void Device::use_stream(uint64_t handle) {
+    stream_ = handle ? reinterpret_cast<hipStream_t>(handle) : own_stream_;
+}
+
+size_t Device::bucket(size_t bytes) {
+    size_t b = 256;
+    while (b < bytes) b <<= 1;
+    return b;
+}
+
+uint64_t Device::acquire(size_t bytes) {
+    const size_t b = bucket(bytes ? bytes : 1);
+    std::lock_guard<std::mutex> g(mu_);
+    auto it = free_.find(b);
+    uint64_t id;
+    if (it != free_.end()) {
+        id = it->second;
+        free_.erase(it);
+        stats_.bytes_cached -= b;
+        stats_.reuses++;
+    } else {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, b);
+        if (e != hipSuccess) {
+            // give cached blocks back and retry once
+            for (auto& kv : free_) hipFree(reinterpret_cast<void*>(kv.second));
+            free_.clear();
+            stats_.bytes_cached = 0;
+            hip_check(hipMalloc(&p, b), "hipMalloc");
+        }
+        id = reinterpret_cast<uint64_t>(p);
+        stats_.allocs++;
+    }
+    live_[id] = b;
+    stats_.bytes_live += b;
+    return id;
+}
+
+void Device::release(uint64_t id) {
+    std::lock_guard<std::mutex> g(mu_);
+    auto it = live_.find(id);
+    if (it == live_.end()) throw std::runtime_error("Device.release: unknown buffer id");
+    free_.emplace(it->second, id);
+    stats_.bytes_live -= it->second;
+    stats_.bytes_cached += it->second;
+    live_.erase(it);
+}
+
+size_t Device::buffer_bytes(uint64_t id) const {
+    std::lock_guard<std::mutex> g(mu_);
+    auto it = live_.find(id);
+    return it == live_.end() ? 0 : it->second;
+}
+
+void Device::upload(uint64_t id, const void* host, size_t bytes, size_t offset) {
+    hip_check(hipMemcpyAsync(reinterpret_cast<char*>(id) + offset, host, bytes,
+                             hipMemcpyHostToDevice, stream_), "upload");
+    hip_check(hipStreamSynchronize(stream_), "upload sync");
+}
+
+void Device::download(uint64_t id, void* host, size_t bytes, size_t offset) {
+    hip_check(hipMemcpyAsync(host, reinterpret_cast<const char*>(id) + offset, bytes,
+                             hipMemcpyDeviceToHost, stream_), "download");
+    hip_check(hipStreamSynchronize(stream_), "download sync");
+}
+
+void Device::zero(uint64_t id, size_t bytes) {
+    hip_check(hipMemsetAsync(reinterpret_cast<void*>(id), 0, bytes, stream_), "zero");
+}
+
+void Device::synchronize() { hip_check(hipStreamSynchronize(stream_), "synchronize"); }
+
+Device::Stats Device::stats() const {
+    std::lock_guard<std::mutex> g(mu_);
+    return stats_;
+}
+
+void Device::trim() {
+    synchronize();
+    std::lock_guard<std::mutex> g(mu_);
+    for (auto& kv : free_) hipFree(reinterpret_cast<void*>(kv.second));
+    free_.clear();
+    stats_.bytes_cached = 0;
+}
+
+}  // namespace grilly

@@ -1,0 +1,70 @@
+// device.h — HIP device, stream and caching buffer pool under the tape engine.
+//
+// Replaces the reference's Vulkan runtime (GrillyDevice, BufferPool, CommandBatch:
+// cpp/include/grilly/{device,buffer_pool,command_batch}.h).  A buffer id is the device
+// pointer cast to uint64 (the reference uses the VkBuffer handle, autograd.cpp:228-233),
+// so any device pointer — including a torch tensor's data_ptr() — is a valid buffer id.
+// Freed buffers go back to power-of-two size buckets (buffer_pool.h:99-101 uses the same
+// bucketing) and are reused without another hipMalloc.  All work is ordered on one
+// stream; nothing here synchronises except download() and synchronize().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace grilly {
+
+// hipError_t -> std::runtime_error (the role of vkCheck, command_batch.cpp:9-14)
+void hip_check(hipError_t e, const char* what);
+
+class Device {
+public:
+    explicit Device(int index = 0);
+    ~Device();
+    Device(const Device&) = delete;
+    Device& operator=(const Device&) = delete;
+
+    int index() const { return index_; }
+    std::string name() const { return name_; }
+    hipStream_t stream() const { return stream_; }
+    // Launch on a caller-owned stream (e.g. torch.cuda.current_stream().cuda_stream);
+    // 0 restores the device's own stream.
+    void use_stream(uint64_t handle);
+
+    uint64_t acquire(size_t bytes);  // from the pool; contents undefined
+    void release(uint64_t id);       // back to the pool
+    size_t buffer_bytes(uint64_t id) const;
+
+    void upload(uint64_t id, const void* host, size_t bytes, size_t offset = 0);
+    void download(uint64_t id, void* host, size_t bytes, size_t offset = 0);
+    void zero(uint64_t id, size_t bytes);  // fill kernel, stream-ordered
+    void synchronize();
+
+    struct Stats {
+        size_t bytes_live = 0, bytes_cached = 0;
+        uint64_t allocs = 0, reuses = 0;
+    };
+    Stats stats() const;
+    void trim();  // return cached blocks to HIP
+
+private:
+    static size_t bucket(size_t bytes);
+    int index_ = 0;
+    std::string name_;
+    hipStream_t own_stream_ = nullptr;
+    hipStream_t stream_ = nullptr;
+    mutable std::mutex mu_;
+    std::unordered_map<uint64_t, size_t> live_;            // id -> bucket bytes
+    std::multimap<size_t, uint64_t> free_;                 // bucket bytes -> id
+    Stats stats_;
+};
+
+}  // namespace grilly

@@ -1,0 +1,89 @@
+"""Python helpers around grilly_core, mirroring the reference's
+src/grilly_next/backend/_bridge.py (create_tape_context :260, make_tensor_ref :279), plus
+packers for the per-op parameter blocks and torch interop.
+
+A buffer id is a device pointer, so a torch tensor on the GPU is wrapped without a copy:
+`make_tensor_ref(t.data_ptr(), t.shape, dtype_code(t))`.  Use `attach_torch_stream(device)`
+so the tape launches on torch's current stream.
+"""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+
+import grilly_core
+
+DTYPE_F32, DTYPE_F16, DTYPE_U32, DTYPE_I32, DTYPE_BF16 = 0, 1, 2, 3, 4
+GLU_KIND = {"swiglu_up": 0, "swiglu_gate": 1, "geglu_up": 2, "geglu_gate": 3, "reglu_up": 4}
+ROPE_MODE = {"none": 0, "interleaved": 1, "half": 2}
+
+
+def create_tape_context(device, arena_capacity: int = 64 << 20):
+    return grilly_core.TapeContext(device, arena_capacity)
+
+
+def make_tensor_ref(buffer_id: int, shape, dtype: int = DTYPE_F32, requires_grad: bool = False):
+    ref = grilly_core.TensorRef()
+    ref.buffer_id = int(buffer_id)
+    ref.set_shape([int(s) for s in shape])
+    ref.dtype = int(dtype)
+    ref.requires_grad = bool(requires_grad)
+    return ref
+
+
+def dtype_code(t) -> int:
+    import torch
+    return {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16,
+            torch.int32: DTYPE_I32}[t.dtype]
+
+
+def tref(t, requires_grad: bool = False):
+    """TensorRef over a contiguous torch tensor on the GPU (no copy)."""
+    assert t.is_cuda and t.is_contiguous()
+    return make_tensor_ref(t.data_ptr(), t.shape, dtype_code(t), requires_grad)
+
+
+def attach_torch_stream(device):
+    import torch
+    device.use_stream(torch.cuda.current_stream().cuda_stream)
+
+
+def download(device, buffer_id: int, shape, dtype: int = DTYPE_F32) -> np.ndarray:
+    """Copy a device buffer to numpy as float32 (bf16 is widened)."""
+    if dtype == DTYPE_BF16:
+        raw = device.download(buffer_id, list(shape), np.dtype(np.uint16))
+        return (raw.astype(np.uint32) << 16).view(np.float32)
+    if dtype == DTYPE_I32:
+        return device.download(buffer_id, list(shape), np.dtype(np.int32))
+    return device.download(buffer_id, list(shape), np.dtype(np.float32))
+
+
+# ---- parameter blocks (layouts of the structs in csrc/tape/autograd.h) ------------------
+def gelu_params(erf_form: bool = False) -> bytes:
+    return struct.pack("<I", int(erf_form))
+
+
+def layernorm_params(eps: float = 1e-5, stat_is_var: bool = False) -> bytes:
+    return struct.pack("<fI", eps, int(stat_is_var))
+
+
+def attention_params(scale: float = 0.0, causal: bool = True, rope: str = "interleaved",
+                     theta: float = 10000.0) -> bytes:
+    return struct.pack("<fIIf", scale, int(causal), ROPE_MODE[rope], theta)
+
+
+def cross_entropy_params(scale: float = 1.0) -> bytes:
+    return struct.pack("<fI", scale, 1)
+
+
+def fused_glu_params(kind: str = "swiglu_up") -> bytes:
+    return struct.pack("<I", GLU_KIND[kind])
+
+
+def vsa_surrogate_params(K: int, D: int, gamma: float = 1.0, delta: float = 1.0,
+                         lambda_c: float = 0.3, temperature: float = 1.0,
+                         winning_k: int = 0, runner_up_k: int = 0) -> bytes:
+    """VSASurrogateLossParams (autograd.h:172-184); defaults as in bindings.cpp:3169-3176."""
+    return struct.pack("<fffIIIIfff", gamma, delta, lambda_c, K, D, winning_k, runner_up_k,
+                       0.0, temperature, 0.01)

@@ -1,0 +1,290 @@
+"""GPU tests of the tape engine end to end: forward values are built with torch (plumbing),
+the ops are recorded on grilly_core.TapeContext exactly as a reference model records them
+(cpp/src/models/vsa_hypernetwork.cpp:52-160), backward runs through the C-ABI kernels, and
+every gradient is compared with a composition of the CPU oracle.
+
+Tolerances: fp32 paths 1e-4, bf16 paths 2e-2 (normwise relative error)."""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def env(gpu):
+    import grilly_core
+    import grilly_bridge as gb
+    dev = grilly_core.Device(0)
+    gb.attach_torch_stream(dev)
+    return grilly_core, gb, dev
+
+
+def T(x, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0").to(dtype).contiguous()
+
+
+def grad(gb, dev, tape, t, dtype=None):
+    gid = tape.get_grad_buffer(t.data_ptr())
+    assert gid != 0, "no gradient recorded"
+    return gb.download(dev, gid, t.shape, gb.dtype_code(t) if dtype is None else dtype)
+
+
+def xavier(r, out, inp):
+    lim = np.sqrt(6.0 / (inp + out))
+    return r.uniform(-lim, lim, size=(out, inp)).astype(np.float32)
+
+
+def test_mlp_c1_through_tape(env):
+    """MLP 784->256->10, fp32, batch 64, ReLU, softmax CE."""
+    gc, gb, dev = env
+    r = np.random.default_rng(1)
+    B = 64
+    X = r.standard_normal((B, 784)).astype(np.float32)
+    y = r.integers(0, 10, size=B).astype(np.int32)
+    W1, W2 = xavier(r, 256, 784), xavier(r, 10, 256)
+    b1, b2 = np.zeros(256, np.float32), np.zeros(10, np.float32)
+    tX, tW1, tb1, tW2, tb2, ty = T(X), T(W1), T(b1), T(W2), T(b2), T(y, torch.int32)
+    Z = (tX @ tW1.t() + tb1).contiguous()
+    H = torch.relu(Z).contiguous()
+    L = (H @ tW2.t() + tb2).contiguous()
+    loss = torch.zeros(1, device="cuda:0")
+
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    n1 = tape.record_op(gc.OpType.Linear, [gb.tref(tX)], [gb.tref(Z)])
+    tape.save_for_backward(n1, [tW1.data_ptr(), tb1.data_ptr()])
+    tape.record_op(gc.OpType.ReLU, [gb.tref(Z, True)], [gb.tref(H)])
+    n3 = tape.record_op(gc.OpType.Linear, [gb.tref(H, True)], [gb.tref(L)])
+    tape.save_for_backward(n3, [tW2.data_ptr(), tb2.data_ptr()])
+    ce = tape.record_op(gc.OpType.CrossEntropy, [gb.tref(L, True), gb.tref(ty)], [gb.tref(loss)],
+                        gb.cross_entropy_params(1.0))
+    tape.backward(ce, 0)
+    stats = tape.last_backward_stats()
+    assert stats["nodes_visited"] == 4 and stats["nodes_with_grad"] == 4
+    assert stats["cpu_fallbacks"] == 0
+
+    hZ, hH, hL = Z.cpu().numpy(), H.cpu().numpy(), L.cpu().numpy()
+    dL = oracle.xent_bwd(hL, y, 1.0)
+    dH, dW2, db2 = oracle.linear_bwd(dL, hH, W2)
+    dZ = oracle.act_bwd("relu", dH, hZ)
+    _, dW1, db1 = oracle.linear_bwd(dZ, X, W1, need_dx=False)
+    assert rel_err(grad(gb, dev, tape, L), dL) < 1e-4
+    assert rel_err(grad(gb, dev, tape, H), dH) < 1e-4
+    assert rel_err(grad(gb, dev, tape, Z), dZ) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tW2), dW2) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tb2), db2) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tW1), dW1) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tb1), db1) < 1e-4
+    assert tape.get_grad_buffer(tX.data_ptr()) == 0  # input needs no grad (autograd.cpp:259)
+    live = dev.pool_stats()["bytes_live"]
+    tape.end()
+    assert dev.pool_stats()["bytes_live"] < live
+    assert not tape.is_recording()
+
+
+def test_ffn_block_bf16_through_tape(env):
+    """configs[1] structure at a small size: RMSNorm -> FusedGLU(SwiGLU) -> Linear(down)."""
+    gc, gb, dev = env
+    r = np.random.default_rng(2)
+    M, Dm, Hd = 96, 256, 384
+    bf = torch.bfloat16
+    x = T(r.standard_normal((M, Dm)), bf)
+    w = T(1 + 0.1 * r.standard_normal(Dm), bf)
+    Wg, Wu = (T(r.standard_normal((Hd, Dm)) * 0.05, bf) for _ in range(2))
+    Wd = T(r.standard_normal((Dm, Hd)) * 0.05, bf)
+    dY = T(r.standard_normal((M, Dm)) * 0.01, bf)
+    xf = x.float()
+    rstd = torch.rsqrt((xf * xf).mean(-1) + 1e-6).contiguous()
+    n = (xf * rstd[:, None] * w.float()).to(bf).contiguous()
+    gate, up = (n @ Wg.t()).contiguous(), (n @ Wu.t()).contiguous()
+    a = (gate.float() * torch.nn.functional.silu(up.float())).to(bf).contiguous()
+    y = (a @ Wd.t()).contiguous()
+
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    nn_ = tape.record_op(gc.OpType.RMSNorm, [gb.tref(x, True)], [gb.tref(n)])
+    tape.save_for_backward(nn_, [w.data_ptr(), rstd.data_ptr()])
+    ng = tape.record_op(gc.OpType.FusedGLU, [gb.tref(n, True)], [gb.tref(a)],
+                        gb.fused_glu_params("swiglu_up"))
+    tape.save_for_backward(ng, [Wg.data_ptr(), Wu.data_ptr(), gate.data_ptr(), up.data_ptr()])
+    nd = tape.record_op(gc.OpType.Linear, [gb.tref(a, True)], [gb.tref(y)])
+    tape.save_for_backward(nd, [Wd.data_ptr(), 0])
+    tape.backward(nd, dY.data_ptr())
+
+    h = lambda t: t.float().cpu().numpy()
+    dA, dWd, _ = oracle.linear_bwd(h(dY), h(a), h(Wd))
+    dG, dU = oracle.glu_bwd("swiglu_up", dA, h(gate), h(up))
+    dN = oracle.linear_bwd(dG, h(n), h(Wg))[0] + oracle.linear_bwd(dU, h(n), h(Wu))[0]
+    dWg, dWu = oracle.linear_bwd(dG, h(n), h(Wg))[1], oracle.linear_bwd(dU, h(n), h(Wu))[1]
+    dx, dw = oracle.rmsnorm_bwd(dN, h(x), h(w), h(rstd))
+    assert rel_err(grad(gb, dev, tape, a), dA) < 2e-2
+    assert rel_err(grad(gb, dev, tape, Wd, gb.DTYPE_F32), dWd) < 2e-2
+    assert rel_err(grad(gb, dev, tape, n), dN) < 2e-2
+    assert rel_err(grad(gb, dev, tape, Wg, gb.DTYPE_F32), dWg) < 2e-2
+    assert rel_err(grad(gb, dev, tape, Wu, gb.DTYPE_F32), dWu) < 2e-2
+    assert rel_err(grad(gb, dev, tape, x), dx) < 2e-2
+    assert rel_err(grad(gb, dev, tape, w, gb.DTYPE_F32), dw) < 2e-2
+    tape.end()
+
+
+def test_fanout_is_accumulated(env):
+    """Residual z = Linear(x) + x and a weight used twice: both gradients are summed
+    (the reference drops the second contribution, autograd.cpp:78-86)."""
+    gc, gb, dev = env
+    r = np.random.default_rng(3)
+    x = T(r.standard_normal((16, 32)))
+    W = T(r.standard_normal((32, 32)) * 0.1)
+    y = (x @ W.t()).contiguous()
+    z = (y + x).contiguous()
+    u = (z @ W.t()).contiguous()  # W used a second time
+    dU = T(r.standard_normal((16, 32)))
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    n1 = tape.record_op(gc.OpType.Linear, [gb.tref(x, True)], [gb.tref(y)])
+    tape.save_for_backward(n1, [W.data_ptr(), 0])
+    tape.record_op(gc.OpType.Add, [gb.tref(y, True), gb.tref(x, True)], [gb.tref(z)])
+    n3 = tape.record_op(gc.OpType.Linear, [gb.tref(z, True)], [gb.tref(u)])
+    tape.save_for_backward(n3, [W.data_ptr(), 0])
+    tape.backward(n3, dU.data_ptr())
+    hW, hx, hz, hdU = W.cpu().numpy(), x.cpu().numpy(), z.cpu().numpy(), dU.cpu().numpy()
+    dz = hdU @ hW
+    dx = dz + dz @ hW
+    dW = hdU.T @ hz + dz.T @ hx
+    assert rel_err(grad(gb, dev, tape, x), dx) < 1e-4
+    assert rel_err(grad(gb, dev, tape, W), dW) < 1e-4
+    assert tape.last_backward_stats()["fanout_accumulations"] >= 2
+    # the upstream buffer passed through Add must not have been modified
+    assert torch.equal(dU.cpu(), torch.from_numpy(hdU))
+    tape.end()
+
+
+def test_attention_and_layernorm_nodes(env):
+    gc, gb, dev = env
+    r = np.random.default_rng(4)
+    B, H, S, D = 1, 2, 128, 64
+    bf = torch.bfloat16
+    Q, K, V = (T(r.standard_normal((B, H, S, D)), bf) for _ in range(3))
+    dO = T(r.standard_normal((B, H, S, D)) * 0.01, bf)
+    h = lambda t: t.float().cpu().numpy()
+    O_, LSE_ = oracle.attn_fwd(h(Q), h(K), h(V))
+    O, LSE = T(O_, bf), T(LSE_)
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    na = tape.record_op(gc.OpType.FlashAttention2, [gb.tref(Q, True), gb.tref(K, True), gb.tref(V, True)],
+                        [gb.tref(O)], gb.attention_params(causal=True, rope="interleaved"))
+    tape.save_for_backward(na, [LSE.data_ptr()])
+    tape.backward(na, dO.data_ptr())
+    rQ, rK, rV = oracle.attn_bwd(h(Q), h(K), h(V), h(dO), LSE_)
+    assert rel_err(grad(gb, dev, tape, Q), rQ) < 2e-2
+    assert rel_err(grad(gb, dev, tape, K), rK) < 2e-2
+    assert rel_err(grad(gb, dev, tape, V), rV) < 2e-2
+    tape.end()
+
+    rows, F = 64, 768
+    X = T(r.standard_normal((rows, F)) * 2)
+    gamma, beta = T(1 + 0.2 * r.standard_normal(F)), T(r.standard_normal(F))
+    Y_, mean_, rstd_ = oracle.layernorm_fwd(h(X), h(gamma), h(beta))
+    Y, mean, rstd = T(Y_), T(mean_), T(rstd_)
+    dY = T(r.standard_normal((rows, F)))
+    tape.begin()
+    nl = tape.record_op(gc.OpType.LayerNorm, [gb.tref(X, True)], [gb.tref(Y)], gb.layernorm_params(1e-5))
+    tape.save_for_backward(nl, [gamma.data_ptr(), beta.data_ptr(), mean.data_ptr(), rstd.data_ptr()])
+    tape.backward(nl, dY.data_ptr())
+    rX, rG, rB = oracle.layernorm_bwd(h(dY), h(X), h(gamma), mean_, rstd_)
+    assert rel_err(grad(gb, dev, tape, X), rX) < 1e-4
+    assert rel_err(grad(gb, dev, tape, gamma), rG) < 1e-4
+    assert rel_err(grad(gb, dev, tape, beta), rB) < 1e-4
+    tape.end()
+
+
+def test_vsa_hypernetwork_chain(env):
+    """The reference's only taped model (vsa_hypernetwork.cpp:52-160, vsa_training_step
+    bindings.cpp:3140-3286): VSAUnpackProject -> Linear -> GELU -> Linear -> VSASurrogateLoss,
+    here with a batch of 8 and seeded winner selection."""
+    gc, gb, dev = env
+    r = np.random.default_rng(5)
+    Bn, D, d_model, hidden, K = 8, 1024, 64, 128, 4
+    words = D // 32
+    bits = r.integers(0, 2**32, size=(Bn, words), dtype=np.uint64).astype(np.uint32)
+    target = r.integers(0, 2**32, size=(Bn, words), dtype=np.uint64).astype(np.uint32)
+    Wp = (r.standard_normal((d_model, D)) / np.sqrt(D)).astype(np.float32)
+    bp = np.zeros(d_model, np.float32)
+    W1 = (r.standard_normal((hidden, d_model)) * np.sqrt(2 / (d_model + hidden))).astype(np.float32)
+    b1 = np.zeros(hidden, np.float32)
+    W2 = (r.standard_normal((K * D, hidden)) * np.sqrt(2 / (hidden + K * D))).astype(np.float32)
+    b2 = np.zeros(K * D, np.float32)
+    S = oracle.unpack_bits(bits, D)
+    h0 = S @ Wp.T + bp
+    z1 = h0 @ W1.T + b1
+    a1 = oracle.act_fwd("gelu_tanh", z1)
+    preds = (a1 @ W2.T + b2).astype(np.float32)
+    res, wts = oracle.vsa_results_weights(oracle.vsa_dots(preds.reshape(Bn, K, D), target),
+                                          rng=np.random.default_rng(6))
+    tb = {k: T(v) for k, v in dict(Wp=Wp, bp=bp, W1=W1, b1=b1, W2=W2, b2=b2, h0=h0, z1=z1,
+                                   a1=a1, preds=preds).items()}
+    tbits = torch.from_numpy(bits.view(np.int32)).cuda()
+    ttarget = torch.from_numpy(target.view(np.int32)).cuda()
+    tres = torch.from_numpy(res.view(np.int32)).cuda()
+    twts = T(wts)
+    loss = torch.zeros(1, device="cuda:0")
+
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    bits_ref = gb.make_tensor_ref(tbits.data_ptr(), (Bn, words), gb.DTYPE_U32)
+    n0 = tape.record_op(gc.OpType.VSAUnpackProject, [bits_ref], [gb.tref(tb["h0"])])
+    tape.save_for_backward(n0, [tb["Wp"].data_ptr(), tb["bp"].data_ptr()])
+    n1 = tape.record_op(gc.OpType.Linear, [gb.tref(tb["h0"], True)], [gb.tref(tb["z1"])])
+    tape.save_for_backward(n1, [tb["W1"].data_ptr(), tb["b1"].data_ptr()])
+    tape.record_op(gc.OpType.GELU, [gb.tref(tb["z1"], True)], [gb.tref(tb["a1"])])
+    n3 = tape.record_op(gc.OpType.Linear, [gb.tref(tb["a1"], True)], [gb.tref(tb["preds"])])
+    tape.save_for_backward(n3, [tb["W2"].data_ptr(), tb["b2"].data_ptr()])
+    preds_ref = gb.make_tensor_ref(tb["preds"].data_ptr(), (Bn, K, D), gb.DTYPE_F32, True)
+    tgt_ref = gb.make_tensor_ref(ttarget.data_ptr(), (Bn, words), gb.DTYPE_U32)
+    nl = tape.record_op(gc.OpType.VSASurrogateLoss, [preds_ref, tgt_ref], [gb.tref(loss)],
+                        gb.vsa_surrogate_params(K, D))
+    tape.save_for_backward(nl, [tres.data_ptr(), twts.data_ptr()])
+    tape.backward(nl, 0)
+    assert tape.last_backward_stats()["cpu_fallbacks"] == 0
+
+    dP = oracle.vsa_surrogate_bwd(preds.reshape(Bn, K, D), target, res, wts).reshape(Bn, K * D)
+    da1, dW2, db2 = oracle.linear_bwd(dP, a1, W2)
+    dz1 = oracle.act_bwd("gelu_tanh", da1, z1)
+    dh0, dW1, db1 = oracle.linear_bwd(dz1, h0, W1)
+    dWp, dbp = oracle.vsa_unpack_project_bwd(dh0, bits, D)
+    assert rel_err(grad(gb, dev, tape, tb["preds"]), dP) < 1e-5
+    assert rel_err(grad(gb, dev, tape, tb["W2"]), dW2) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tb["b2"]), db2) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tb["W1"]), dW1) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tb["b1"]), db1) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tb["Wp"]), dWp) < 1e-4
+    assert rel_err(grad(gb, dev, tape, tb["bp"]), dbp) < 1e-4
+    tape.end()
+
+
+def test_tape_error_paths(env):
+    gc, gb, dev = env
+    x = torch.zeros((4, 8), device="cuda:0")
+    W = torch.zeros((8, 8), device="cuda:0")
+    tape = gb.create_tape_context(dev, arena_capacity=1 << 20)
+    assert tape.record_op(gc.OpType.Linear, [gb.tref(x)], [gb.tref(x)]) is None  # not recording
+    tape.begin()
+    n = tape.record_op(gc.OpType.Linear, [gb.tref(x, True)], [gb.tref(x)])
+    tape.save_for_backward(n, [W.data_ptr()])
+    with pytest.raises(ValueError, match="upstream gradient"):
+        tape.backward(n, 0)  # a Linear root needs dL/dy
+    tape.end()
+    tape.begin()
+    m = tape.record_op(gc.OpType.Conv2d, [gb.tref(x, True)], [gb.tref(x)])
+    tape.backward(m, x.data_ptr())
+    assert tape.last_backward_stats()["cpu_fallbacks"] == 1  # no handler (autograd.cpp:126-128)
+    tape.end()
+    small = gb.create_tape_context(dev, arena_capacity=4096)
+    small.begin()
+    with pytest.raises(MemoryError):
+        for _ in range(10):
+            small.record_op(gc.OpType.ReLU, [gb.tref(x, True)], [gb.tref(x)])
+    small.end()
