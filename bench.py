@@ -3,9 +3,9 @@
 Workload: RMSNorm(d=2048) -> SwiGLU (gate/up 2048->5632, down 5632->2048), T = 4096 tokens
 (batch 4 x seq 1024), bf16 activations/weights, fp32 accumulation; x ~ N(0,1), weights
 N(0, 0.02), dY ~ N(0, 1e-2).  One step = the whole block backward:
-    gn_linear_bwd      (down projection: dA, dWd)
-    gn_glu_linear_bwd  (SwiGLU local grads, dN = dG Wg + dU Wu, dWg, dWu)
-    gn_rmsnorm_bwd     (dx, dw)
+    gn_ffn_down_glu_bwd  (down projection with the SwiGLU backward in its epilogue: dG|dU, dWd)
+    gn_glu_proj_bwd      (dN = dG Wg + dU Wu, dWg, dWu)
+    gn_rmsnorm_bwd       (dx, dw)
 with inputs (x, saved rstd / gate / up / activations, weights, dY) resident in HBM.
 The metric is layer-backward tokens/s; the dominant kernel's roofline fraction comes from
 HIP events around its own launches, and the CPU baseline is the oracle (C, OpenMP) timed on
@@ -66,12 +66,11 @@ class Step:
         self.gn, self.d = gn, d
         dev = d["x"].device
         f32, bf = torch.float32, torch.bfloat16
-        self.dA = torch.empty(T, HID, device=dev, dtype=bf)
         self.dWd = torch.empty(DM, HID, device=dev, dtype=f32)
         self.dN = torch.empty(T, DM, device=dev, dtype=bf)
         self.dWg = torch.empty(HID, DM, device=dev, dtype=f32)
         self.dWu = torch.empty(HID, DM, device=dev, dtype=f32)
-        self.gu = torch.empty(2, T, HID, device=dev, dtype=bf)
+        self.gu = torch.empty(T, 2 * HID, device=dev, dtype=bf)
         self.dx = torch.empty(T, DM, device=dev, dtype=bf)
         self.dw = torch.empty(DM, device=dev, dtype=f32)
         self.ws = gn.workspace(gn.norm_workspace_bytes(T, DM), dev)
@@ -79,12 +78,12 @@ class Step:
     def __call__(self):
         gn, d, P, s = self.gn, self.d, self.gn._ptr, self.gn._stream()
         L = gn.lib()
-        gn._check(L.gn_linear_bwd(P(d["dY"]), P(d["a"]), P(d["Wd"]), P(self.dA), P(self.dWd), None,
-                                  T, DM, HID, gn.BF16, 0, s), "linear_bwd")
-        gn._check(L.gn_glu_linear_bwd(gn.GLU["swiglu_up"], P(self.dA), P(d["gate"]), P(d["up"]),
-                                      P(d["n"]), P(d["Wg"]), P(d["Wu"]), P(self.dN), P(self.dWg),
-                                      P(self.dWu), None, None, P(self.gu), T, DM, HID, gn.BF16, 0,
-                                      s), "glu_linear_bwd")
+        gn._check(L.gn_ffn_down_glu_bwd(gn.GLU["swiglu_up"], P(d["dY"]), P(d["a"]), P(d["Wd"]),
+                                        P(d["gate"]), P(d["up"]), P(self.gu), P(self.dWd), None,
+                                        T, DM, HID, gn.BF16, 0, s), "ffn_down_glu_bwd")
+        gn._check(L.gn_glu_proj_bwd(P(self.gu), P(d["n"]), P(d["Wg"]), P(d["Wu"]), P(self.dN),
+                                    P(self.dWg), P(self.dWu), None, None, T, DM, HID, gn.BF16, 0,
+                                    s), "glu_proj_bwd")
         gn._check(L.gn_rmsnorm_bwd(P(self.dN), P(d["x"]), P(d["w"]), P(d["rstd"]), P(self.dx),
                                    P(self.dw), T, DM, gn.BF16, 0, P(self.ws), self.ws.numel(), s),
                   "rmsnorm_bwd")
@@ -93,7 +92,8 @@ class Step:
 def time_dominant(gn, torch, st, reps=20):
     """HIP-event timing of the dominant GEMM launch: dN = dG Wg + dU Wu (K = 2*5632)."""
     d = st.d
-    dG, dU = st.gu[0], st.gu[1]
+    dG = st.gu[:, :HID].contiguous()
+    dU = st.gu[:, HID:].contiguous()
     P, L = gn._ptr, gn.lib()
     stream = torch.cuda.current_stream()
 

@@ -20,7 +20,7 @@ BUILD = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(ROOT, "include")
 ARCH = os.environ.get("GN_OFFLOAD_ARCH", "gfx950")
 
-KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip",
+KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip", "gn_gemm_dma.hip",
                   "gn_vsa.hip", "gn_attn.hip"]
 TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "bindings.cpp"]
 

@@ -2,6 +2,7 @@
 //   activation backward, GLU local gradients, fan-out accumulation, VSA surrogate loss.
 // Each thread moves 16-byte vectors; the grid is sized to ~4 waves per SIMD and strides.
 #include "gn_common.h"
+#include "gn_math.h"
 
 namespace gn {
 namespace {
@@ -45,40 +46,6 @@ template <typename T, int V> struct vec {  // scalar fallback (V == 1)
     }
 };
 
-// ---- activation derivatives --------------------------------------------------------------
-constexpr float kSqrt2OverPi = 0.7978845608028654f;
-constexpr float kGeluC = 0.044715f;
-
-__device__ __forceinline__ float gelu_tanh_f(float x) {
-    return 0.5f * x * (1.0f + tanhf_(kSqrt2OverPi * (x + kGeluC * x * x * x)));
-}
-// activation-gelu-backward.glsl:38-50: 0.5 (1 + tanh z + x sech^2 z dz/dx)
-__device__ __forceinline__ float gelu_tanh_grad_f(float x) {
-    float z = kSqrt2OverPi * (x + kGeluC * x * x * x);
-    float t = tanhf_(z);
-    return 0.5f * (1.0f + t + x * (1.0f - t * t) * kSqrt2OverPi * (1.0f + 3.0f * kGeluC * x * x));
-}
-// erf form (autograd_core.py:529-542): Phi(x) + x phi(x)
-__device__ __forceinline__ float gelu_erf_grad_f(float x) {
-    return 0.5f * (1.0f + erff(x * 0.70710678118654752f)) +
-           x * 0.3989422804014327f * __expf(-0.5f * x * x);
-}
-__device__ __forceinline__ float silu_f(float x) { return x * sigmoidf_(x); }
-__device__ __forceinline__ float silu_grad_f(float x) {
-    float s = sigmoidf_(x);
-    return s * (1.0f + x * (1.0f - s));
-}
-
-template <int KIND>
-__device__ __forceinline__ float act_grad(float x) {
-    if constexpr (KIND == GN_ACT_RELU) return x > 0.0f ? 1.0f : 0.0f;
-    else if constexpr (KIND == GN_ACT_GELU_TANH) return gelu_tanh_grad_f(x);
-    else if constexpr (KIND == GN_ACT_GELU_ERF) return gelu_erf_grad_f(x);
-    else if constexpr (KIND == GN_ACT_SILU) return silu_grad_f(x);
-    else if constexpr (KIND == GN_ACT_TANH) return 1.0f - x * x;  // x = saved tanh output
-    else return x * (1.0f - x);                                    // x = saved sigmoid output
-}
-
 template <int KIND, typename T, int V>
 __global__ __launch_bounds__(256) void act_bwd_kernel(const T* __restrict__ dY,
                                                       const T* __restrict__ X,
@@ -93,29 +60,6 @@ __global__ __launch_bounds__(256) void act_bwd_kernel(const T* __restrict__ dY,
 #pragma unroll
         for (int j = 0; j < V; ++j) o[j] = (accumulate ? o[j] : 0.0f) + dy[j] * act_grad<KIND>(x[j]);
         vec<T, V>::st(dX + i * V, o);
-    }
-}
-
-// ---- GLU local gradients (fused-{swiglu,geglu,reglu}-backward.glsl local terms) ---------
-template <int KIND>
-__device__ __forceinline__ void glu_grad(float d, float g, float u, float& dg, float& du) {
-    if constexpr (KIND == GN_GLU_SWIGLU_UP) {
-        float s = sigmoidf_(u);
-        dg = d * u * s;
-        du = d * g * s * (1.0f + u * (1.0f - s));
-    } else if constexpr (KIND == GN_GLU_SWIGLU_GATE) {
-        float s = sigmoidf_(g);
-        dg = d * u * s * (1.0f + g * (1.0f - s));
-        du = d * g * s;
-    } else if constexpr (KIND == GN_GLU_GEGLU_UP) {
-        dg = d * gelu_tanh_f(u);
-        du = d * g * gelu_tanh_grad_f(u);
-    } else if constexpr (KIND == GN_GLU_GEGLU_GATE) {
-        dg = d * u * gelu_tanh_grad_f(g);
-        du = d * gelu_tanh_f(g);
-    } else {  // REGLU_UP
-        dg = d * (u > 0.0f ? u : 0.0f);
-        du = d * g * (u > 0.0f ? 1.0f : 0.0f);
     }
 }
 
@@ -135,6 +79,28 @@ __global__ __launch_bounds__(256) void glu_bwd_kernel(const T* __restrict__ dO,
         for (int j = 0; j < V; ++j) glu_grad<KIND>(d[j], g[j], u[j], og[j], ou[j]);
         vec<T, V>::st(dG + i * V, og);
         vec<T, V>::st(dU + i * V, ou);
+    }
+}
+
+// GLU local gradients written as gu = [dGate | dUp] rows of pitch 2H (V elements at a time
+// along h; H % V == 0 for V > 1).
+template <int KIND, typename T, int V>
+__global__ __launch_bounds__(256) void glu_bwd_gu_kernel(const T* __restrict__ dO,
+                                                         const T* __restrict__ G,
+                                                         const T* __restrict__ U,
+                                                         T* __restrict__ gu, int64_t M, int H) {
+    const int64_t hv = H / V, nvec = M * hv;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = i / hv, h = (i % hv) * V;
+        float d[V], g[V], u[V], og[V], ou[V];
+        vec<T, V>::ld(dO + m * H + h, d);
+        vec<T, V>::ld(G + m * H + h, g);
+        vec<T, V>::ld(U + m * H + h, u);
+#pragma unroll
+        for (int j = 0; j < V; ++j) glu_grad<KIND>(d[j], g[j], u[j], og[j], ou[j]);
+        vec<T, V>::st(gu + m * 2 * H + h, og);
+        vec<T, V>::st(gu + m * 2 * H + H + h, ou);
     }
 }
 
@@ -260,6 +226,35 @@ int dispatch_act(int kind, const void* dY, const void* X, void* dX, int64_t n, b
     }
 }
 
+template <int KIND, typename T>
+int launch_glu_gu(const void* dO, const void* g, const void* u, void* gu, int M, int H,
+                  hipStream_t s) {
+    constexpr int V = sizeof(T) == 4 ? 4 : 8;
+    const bool fast = (H % V == 0) && aligned16(dO) && aligned16(g) && aligned16(u) && aligned16(gu);
+    const int64_t n = (int64_t)M * H;
+    if (fast)
+        glu_bwd_gu_kernel<KIND, T, V><<<grid_for(n / V, 256, 8192), 256, 0, s>>>(
+            (const T*)dO, (const T*)g, (const T*)u, (T*)gu, M, H);
+    else
+        glu_bwd_gu_kernel<KIND, T, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>(
+            (const T*)dO, (const T*)g, (const T*)u, (T*)gu, M, H);
+    GN_LAUNCH_CHECK("glu backward (gu)");
+    return GN_OK;
+}
+
+template <typename T>
+int dispatch_glu_gu(int kind, const void* dO, const void* g, const void* u, void* gu, int M, int H,
+                    hipStream_t s) {
+    switch (kind) {
+        case GN_GLU_SWIGLU_UP: return launch_glu_gu<GN_GLU_SWIGLU_UP, T>(dO, g, u, gu, M, H, s);
+        case GN_GLU_SWIGLU_GATE: return launch_glu_gu<GN_GLU_SWIGLU_GATE, T>(dO, g, u, gu, M, H, s);
+        case GN_GLU_GEGLU_UP: return launch_glu_gu<GN_GLU_GEGLU_UP, T>(dO, g, u, gu, M, H, s);
+        case GN_GLU_GEGLU_GATE: return launch_glu_gu<GN_GLU_GEGLU_GATE, T>(dO, g, u, gu, M, H, s);
+        case GN_GLU_REGLU_UP: return launch_glu_gu<GN_GLU_REGLU_UP, T>(dO, g, u, gu, M, H, s);
+        default: set_error("glu backward: unknown GLU kind %d", kind); return GN_E_INVALID;
+    }
+}
+
 template <typename T>
 int dispatch_glu(int kind, const void* dO, const void* g, const void* u, void* dg, void* du,
                  int64_t n, hipStream_t s) {
@@ -274,6 +269,16 @@ int dispatch_glu(int kind, const void* dO, const void* g, const void* u, void* d
 }
 
 }  // namespace
+
+int glu_bwd_to_gu(int kind, const void* dO, const void* gate, const void* up, void* gu, int M,
+                  int H, int dtype, hipStream_t s) {
+    if ((int64_t)M * H == 0) return GN_OK;
+    if (dtype == GN_F32) return dispatch_glu_gu<float>(kind, dO, gate, up, gu, M, H, s);
+    if (dtype == GN_BF16) return dispatch_glu_gu<bf16_t>(kind, dO, gate, up, gu, M, H, s);
+    set_error("glu backward: dtype %d", dtype);
+    return GN_E_INVALID;
+}
+
 }  // namespace gn
 
 using namespace gn;

@@ -17,6 +17,7 @@
 #include <algorithm>
 
 #include "gn_common.h"
+#include "gn_gemm_dma.h"
 
 namespace gn {
 namespace {
@@ -31,16 +32,6 @@ constexpr int TILE_ELEMS = 128 * LDS_PITCH;
 // 16-byte chunk c of row r lives at chunk c ^ swz(r).  Fragment reads (32 consecutive rows,
 // one chunk) and the transposed stores (rows 8 apart) both spread over all 8 chunk slots.
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
-
-struct GemmArgs {
-    const bf16_t* A[2];
-    const bf16_t* B[2];
-    int Ks[2];
-    int nseg;
-    void* C;
-    int M, N;
-    int accumulate;
-};
 
 // Load one 128-row x 64-k operand tile into registers (4 x 16 bytes per thread).
 //   KCONTIG: element (r, k) at P[r * ld + k]    (r = row of the tile: m for A, n for B)
@@ -111,8 +102,8 @@ __device__ __forceinline__ bf16x8_t lds_frag(const bf16_t* p) {
     return __builtin_bit_cast(bf16x8_t, v);
 }
 
-template <bool TA, bool TB, typename CT>
-__global__ __launch_bounds__(256, 2) void gemm_bf16_mfma(GemmArgs g) {
+template <bool TA, bool TB, typename CT, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_mfma(GemmDesc g) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     bf16_t* sA = reinterpret_cast<bf16_t*>(smem_raw);  // [2][128][LDS_PITCH]
     bf16_t* sB = sA + 2 * TILE_ELEMS;                   // [2][128][LDS_PITCH]
@@ -151,12 +142,12 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma(GemmArgs g) {
         const int s = t < kt0 ? 0 : 1;
         const int k0 = (t < kt0 ? t : t - kt0) * BK;
         const int Ks = g.Ks[s];
-        // A: TA=0 -> [M x Ks] (k contiguous); TA=1 -> stored [Ks x M]
-        if (!TA) load_tile<true>(g.A[s], Ks, m0, g.M, k0, Ks, ra);
-        else load_tile<false>(g.A[s], g.M, m0, g.M, k0, Ks, ra);
-        // B: TB=1 -> stored [N x Ks] (k contiguous); TB=0 -> [Ks x N]
-        if (TB) load_tile<true>(g.B[s], Ks, n0, g.N, k0, Ks, rb);
-        else load_tile<false>(g.B[s], g.N, n0, g.N, k0, Ks, rb);
+        // A: TA=0 -> A[m*lda + k] (k contiguous); TA=1 -> A[k*lda + m]
+        if (!TA) load_tile<true>(g.A[s], g.lda[s], m0, g.M, k0, Ks, ra);
+        else load_tile<false>(g.A[s], g.lda[s], m0, g.M, k0, Ks, ra);
+        // B: TB=1 -> B[n*ldb + k] (k contiguous); TB=0 -> B[k*ldb + n]
+        if (TB) load_tile<true>(g.B[s], g.ldb[s], n0, g.N, k0, Ks, rb);
+        else load_tile<false>(g.B[s], g.ldb[s], n0, g.N, k0, Ks, rb);
     };
     auto sstore = [&](int buf) {
         store_tile<!TA>(sA + buf * TILE_ELEMS, ra);
@@ -195,51 +186,35 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_mfma(GemmArgs g) {
     }
 
     // ---- epilogue: 32x32 accumulator layout: col = lane%32, row = 8*(r/4) + 4*(lane/32) + r%4
-    CT* C = reinterpret_cast<CT*>(g.C);
-    const int col_l = lane & 31, rq = (lane >> 5) * 4;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + j * 32 + col_l;
-            if (n >= g.N) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + rq + (r & 3);
-                if (m >= g.M) continue;
-                const size_t idx = (size_t)m * g.N + n;
-                float v = acc[i][j][r];
-                if (g.accumulate) v += io<CT>::ld(C, idx);
-                io<CT>::st(C, idx, v);
-            }
-        }
+        for (int j = 0; j < 2; ++j)
+            gemm_store_tile<CT, EPI>(g, m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, acc[i][j]);
 }
 
-// ---- SIMT fallback: 64x64 tile, BK 16, 4x4 outputs per thread -------------------------
-template <typename TI, typename CT, bool TA, bool TB>
-__global__ __launch_bounds__(256) void gemm_simt(const TI* A0, const TI* B0, int K0,
-                                                 const TI* A1, const TI* B1, int K1, CT* C,
-                                                 int M, int N, int accumulate) {
+// ---- SIMT fallback: 64x64 tile, BK 16, 4x4 outputs per thread (any shape, f32 or bf16) ----
+template <typename TI, typename CT, bool TA, bool TB, int EPI>
+__global__ __launch_bounds__(256) void gemm_simt(GemmDesc g) {
     __shared__ float sA[16][64 + 4];
     __shared__ float sB[16][64 + 4];
     const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     float acc[4][4] = {};
-    for (int s = 0; s < 2; ++s) {
-        const TI* A = s ? A1 : A0;
-        const TI* B = s ? B1 : B0;
-        const int Ks = s ? K1 : K0;
-        if (!A || Ks <= 0) continue;
+    for (int s = 0; s < g.nseg; ++s) {
+        const TI* A = reinterpret_cast<const TI*>(g.A[s]);
+        const TI* B = reinterpret_cast<const TI*>(g.B[s]);
+        const int Ks = g.Ks[s], lda = g.lda[s], ldb = g.ldb[s];
         for (int k0 = 0; k0 < Ks; k0 += 16) {
             for (int e = threadIdx.x; e < 16 * 64; e += 256) {
                 const int kk = e / 64, mm = e % 64;
                 const int m = m0 + mm, k = k0 + kk;
                 float va = 0.f;
-                if (m < M && k < Ks) va = TA ? io<TI>::ld(A, (size_t)k * M + m) : io<TI>::ld(A, (size_t)m * Ks + k);
+                if (m < g.M && k < Ks) va = TA ? io<TI>::ld(A, (size_t)k * lda + m) : io<TI>::ld(A, (size_t)m * lda + k);
                 sA[kk][mm] = va;
                 const int n = n0 + mm;
                 float vb = 0.f;
-                if (n < N && k < Ks) vb = TB ? io<TI>::ld(B, (size_t)n * Ks + k) : io<TI>::ld(B, (size_t)k * N + n);
+                if (n < g.N && k < Ks) vb = TB ? io<TI>::ld(B, (size_t)n * ldb + k) : io<TI>::ld(B, (size_t)k * ldb + n);
                 sB[kk][mm] = vb;
             }
             __syncthreads();
@@ -263,24 +238,19 @@ __global__ __launch_bounds__(256) void gemm_simt(const TI* A0, const TI* B0, int
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = m0 + ty + 16 * i, n = n0 + tx + 16 * j;
-            if (m < M && n < N) {
-                const size_t idx = (size_t)m * N + n;
-                float v = acc[i][j];
-                if (accumulate) v += io<CT>::ld(C, idx);
-                io<CT>::st(C, idx, v);
-            }
+            if (m < g.M && n < g.N) gemm_store<CT, EPI>(g, m, n, acc[i][j]);
         }
 }
 
 // ---- column sums (db): thread per column, rows split over grid.y with fp32 atomics ------
 template <typename TI>
 __global__ __launch_bounds__(256) void colsum_kernel(const TI* __restrict__ in, float* out,
-                                                     int M, int N, int rows_per) {
+                                                     int M, int N, int ld, int rows_per) {
     const int n = blockIdx.x * 256 + threadIdx.x;
     if (n >= N) return;
     const int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
     float s = 0.f;
-    for (int r = r0; r < r1; ++r) s += io<TI>::ld(in, (size_t)r * N + n);
+    for (int r = r0; r < r1; ++r) s += io<TI>::ld(in, (size_t)r * ld + n);
     if (gridDim.y == 1) out[n] += s;
     else atomicAdd(out + n, s);
 }
@@ -301,93 +271,105 @@ bool allow_big_lds(F* fn, size_t bytes) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
 }
 
-template <bool TA, bool TB>
-int launch_mfma(const GemmArgs& g, int c_dtype, hipStream_t s) {
-    const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    static const bool ok_f = allow_big_lds(gemm_bf16_mfma<TA, TB, float>, kMfmaSmem);
-    static const bool ok_b = allow_big_lds(gemm_bf16_mfma<TA, TB, bf16_t>, kMfmaSmem);
-    if (!(c_dtype == GN_F32 ? ok_f : ok_b)) {
+template <bool TA, bool TB, typename CT, int EPI>
+int launch_mfma_t(const GemmDesc& g, hipStream_t s) {
+    static const bool ok = allow_big_lds(gemm_bf16_mfma<TA, TB, CT, EPI>, kMfmaSmem);
+    if (!ok) {
         set_error("gn_gemm: cannot reserve %zu B of LDS", kMfmaSmem);
         return GN_E_HIP;
     }
-    if (c_dtype == GN_F32)
-        hipLaunchKernelGGL((gemm_bf16_mfma<TA, TB, float>), dim3(tiles), dim3(256), kMfmaSmem, s, g);
-    else
-        hipLaunchKernelGGL((gemm_bf16_mfma<TA, TB, bf16_t>), dim3(tiles), dim3(256), kMfmaSmem, s, g);
+    const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    hipLaunchKernelGGL((gemm_bf16_mfma<TA, TB, CT, EPI>), dim3(tiles), dim3(256), kMfmaSmem, s, g);
     GN_LAUNCH_CHECK("gn_gemm (mfma)");
     return GN_OK;
 }
 
-template <typename TI, typename CT>
-int launch_simt_t(const void* A0, const void* B0, int K0, const void* A1, const void* B1, int K1,
-                  void* C, int M, int N, int ta, int tb, bool acc, hipStream_t s) {
-    dim3 grid((N + 63) / 64, (M + 63) / 64);
-#define GN_SIMT(TAV, TBV)                                                                     \
-    gemm_simt<TI, CT, TAV, TBV><<<grid, 256, 0, s>>>((const TI*)A0, (const TI*)B0, K0,        \
-                                                      (const TI*)A1, (const TI*)B1, K1, (CT*)C, \
-                                                      M, N, acc ? 1 : 0)
-    if (!ta && !tb) GN_SIMT(false, false);
-    else if (!ta && tb) GN_SIMT(false, true);
-    else if (ta && !tb) GN_SIMT(true, false);
-    else GN_SIMT(true, true);
-#undef GN_SIMT
+template <typename CT, int EPI>
+int launch_mfma(const GemmDesc& g, int ta, int tb, hipStream_t s) {
+    if (!ta && !tb) return launch_mfma_t<false, false, CT, EPI>(g, s);
+    if (!ta && tb) return launch_mfma_t<false, true, CT, EPI>(g, s);
+    if (ta && !tb) return launch_mfma_t<true, false, CT, EPI>(g, s);
+    return launch_mfma_t<true, true, CT, EPI>(g, s);
+}
+
+template <typename TI, typename CT, int EPI>
+int launch_simt(const GemmDesc& g, int ta, int tb, hipStream_t s) {
+    dim3 grid((g.N + 63) / 64, (g.M + 63) / 64);
+    if (!ta && !tb) gemm_simt<TI, CT, false, false, EPI><<<grid, 256, 0, s>>>(g);
+    else if (!ta && tb) gemm_simt<TI, CT, false, true, EPI><<<grid, 256, 0, s>>>(g);
+    else if (ta && !tb) gemm_simt<TI, CT, true, false, EPI><<<grid, 256, 0, s>>>(g);
+    else gemm_simt<TI, CT, true, true, EPI><<<grid, 256, 0, s>>>(g);
     GN_LAUNCH_CHECK("gn_gemm (simt)");
     return GN_OK;
 }
 
+bool mfma_applicable(const GemmDesc& g) {
+    if (g.M % 8 || g.N % 8) return false;
+    for (int s = 0; s < g.nseg; ++s)
+        if (g.Ks[s] % 8 || !al16(g.A[s]) || !al16(g.B[s]) || g.lda[s] % 8 || g.ldb[s] % 8) return false;
+    return true;
+}
+
 }  // namespace
 
-// Internal entry shared by the linear / GLU handlers (no error clearing).
+int gemm_run(const GemmDesc& d, int transA, int transB, int dtype, int c_dtype, hipStream_t s) {
+    if (d.M == 0 || d.N == 0) return GN_OK;
+    if (dtype == GN_BF16) {
+        if (gemm_dma_applicable(d)) return gemm_dma_launch(d, transA, transB, c_dtype, s);
+        if (mfma_applicable(d)) {
+            if (d.epi == 1) return launch_mfma<bf16_t, 1>(d, transA, transB, s);
+            if (c_dtype == GN_F32) return launch_mfma<float, 0>(d, transA, transB, s);
+            return launch_mfma<bf16_t, 0>(d, transA, transB, s);
+        }
+        if (d.epi == 1) return launch_simt<bf16_t, bf16_t, 1>(d, transA, transB, s);
+        if (c_dtype == GN_F32) return launch_simt<bf16_t, float, 0>(d, transA, transB, s);
+        return launch_simt<bf16_t, bf16_t, 0>(d, transA, transB, s);
+    }
+    if (dtype == GN_F32) {
+        if (d.epi == 1) {
+            set_error("gemm: the GLU epilogue needs bf16 operands");
+            return GN_E_INVALID;
+        }
+        return launch_simt<float, float, 0>(d, transA, transB, s);
+    }
+    set_error("gn_gemm: dtype %d not supported (f32, bf16)", dtype);
+    return GN_E_INVALID;
+}
+
+// Plain-argument form used by the C entry points.
 int gemm_dispatch(const void* A0, const void* B0, int K0, const void* A1, const void* B1, int K1,
                   void* C, int M, int N, int transA, int transB, int dtype, int c_dtype,
                   unsigned flags, hipStream_t s) {
     GN_REQUIRE(M >= 0 && N >= 0 && K0 >= 0 && K1 >= 0, "gn_gemm: negative size");
     if (M == 0 || N == 0) return GN_OK;
     GN_REQUIRE(C, "gn_gemm: null C");
+    GN_REQUIRE(c_dtype == GN_F32 || c_dtype == GN_BF16, "gn_gemm: c_dtype %d", c_dtype);
+    GN_REQUIRE(dtype == GN_BF16 || c_dtype == GN_F32, "gn_gemm: fp32 path writes fp32 C");
     const bool acc = flags & GN_ACCUMULATE;
     const bool seg1 = A1 && B1 && K1 > 0;
     if (K0 + (seg1 ? K1 : 0) == 0) {
         if (acc) return GN_OK;
-        GN_REQUIRE(c_dtype == GN_F32 || c_dtype == GN_BF16, "gn_gemm: bad c_dtype");
         hipError_t e = hipMemsetAsync(C, 0, (size_t)M * N * (c_dtype == GN_F32 ? 4 : 2), s);
         if (e != hipSuccess) { set_error("gn_gemm: memset failed"); return GN_E_HIP; }
         return GN_OK;
     }
     GN_REQUIRE(A0 && B0, "gn_gemm: null operand");
-    if (dtype == GN_BF16) {
-        GN_REQUIRE(c_dtype == GN_F32 || c_dtype == GN_BF16, "gn_gemm: c_dtype %d", c_dtype);
-        const bool mfma_ok = (M % 8 == 0) && (N % 8 == 0) && (K0 % 8 == 0) &&
-                             (!seg1 || K1 % 8 == 0) && al16(A0) && al16(B0) &&
-                             (!seg1 || (al16(A1) && al16(B1)));
-        if (mfma_ok) {
-            GemmArgs g{};
-            g.A[0] = (const bf16_t*)A0; g.B[0] = (const bf16_t*)B0; g.Ks[0] = K0;
-            g.A[1] = (const bf16_t*)(seg1 ? A1 : A0); g.B[1] = (const bf16_t*)(seg1 ? B1 : B0);
-            g.Ks[1] = seg1 ? K1 : 0;
-            g.nseg = seg1 ? 2 : 1;
-            g.C = C; g.M = M; g.N = N; g.accumulate = acc ? 1 : 0;
-            if (!transA && !transB) return launch_mfma<false, false>(g, c_dtype, s);
-            if (!transA && transB) return launch_mfma<false, true>(g, c_dtype, s);
-            if (transA && !transB) return launch_mfma<true, false>(g, c_dtype, s);
-            return launch_mfma<true, true>(g, c_dtype, s);
-        }
-        if (c_dtype == GN_F32)
-            return launch_simt_t<bf16_t, float>(A0, B0, K0, seg1 ? A1 : nullptr, B1, K1, C, M, N,
-                                                transA, transB, acc, s);
-        return launch_simt_t<bf16_t, bf16_t>(A0, B0, K0, seg1 ? A1 : nullptr, B1, K1, C, M, N,
-                                             transA, transB, acc, s);
+    GemmDesc d{};
+    d.A[0] = (const bf16_t*)A0; d.B[0] = (const bf16_t*)B0; d.Ks[0] = K0;
+    d.lda[0] = transA ? M : K0; d.ldb[0] = transB ? K0 : N;
+    d.nseg = seg1 ? 2 : 1;
+    if (seg1) {
+        d.A[1] = (const bf16_t*)A1; d.B[1] = (const bf16_t*)B1; d.Ks[1] = K1;
+        d.lda[1] = transA ? M : K1; d.ldb[1] = transB ? K1 : N;
     }
-    if (dtype == GN_F32) {
-        GN_REQUIRE(c_dtype == GN_F32, "gn_gemm: fp32 path writes fp32 C");
-        return launch_simt_t<float, float>(A0, B0, K0, seg1 ? A1 : nullptr, B1, K1, C, M, N,
-                                           transA, transB, acc, s);
-    }
-    set_error("gn_gemm: dtype %d not supported (f32, bf16)", dtype);
-    return GN_E_INVALID;
+    d.M = M; d.N = N; d.C = C; d.C2 = C; d.Msplit = M; d.ldc = N;
+    d.accumulate = acc ? 1 : 0;
+    return gemm_run(d, transA, transB, dtype, c_dtype, s);
 }
 
 int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigned flags,
-                    hipStream_t s) {
+                    hipStream_t s, int ld) {
+    if (ld <= 0) ld = N;
     GN_REQUIRE(M >= 0 && N >= 0, "gn_colsum: negative size");
     if (N == 0) return GN_OK;
     GN_REQUIRE(in && out, "gn_colsum: null pointer");
@@ -400,8 +382,8 @@ int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigne
     const int rows_per = (M + splits - 1) / splits;
     splits = (M + rows_per - 1) / rows_per;
     dim3 grid(cb, splits);
-    if (dtype == GN_F32) colsum_kernel<float><<<grid, 256, 0, s>>>((const float*)in, out, M, N, rows_per);
-    else if (dtype == GN_BF16) colsum_kernel<bf16_t><<<grid, 256, 0, s>>>((const bf16_t*)in, out, M, N, rows_per);
+    if (dtype == GN_F32) colsum_kernel<float><<<grid, 256, 0, s>>>((const float*)in, out, M, N, ld, rows_per);
+    else if (dtype == GN_BF16) colsum_kernel<bf16_t><<<grid, 256, 0, s>>>((const bf16_t*)in, out, M, N, ld, rows_per);
     else { set_error("gn_colsum: dtype %d", dtype); return GN_E_INVALID; }
     GN_LAUNCH_CHECK("gn_colsum");
     return GN_OK;
@@ -422,7 +404,7 @@ extern "C" int gn_gemm(const void* A0, const void* B0, int K0, const void* A1, c
 extern "C" int gn_colsum(const void* in, float* out, int M, int N, int dtype, unsigned flags,
                          void* stream) {
     clear_error();
-    return colsum_dispatch(in, out, M, N, dtype, flags, as_stream(stream));
+    return colsum_dispatch(in, out, M, N, dtype, flags, as_stream(stream), N);
 }
 
 // Linear backward (autograd.cpp:172-305): three stream-ordered launches, no host sync.
@@ -442,7 +424,51 @@ extern "C" int gn_linear_bwd(const void* dY, const void* X, const void* W, void*
     // dW[N x K] = dY^T . X  (A = dY stored [M x N] = [Ks x Mout], transposed)
     rc = gemm_dispatch(dY, X, M, nullptr, nullptr, 0, dW, N, K, 1, 0, dtype, GN_F32, flags, s);
     if (rc) return rc;
-    if (db) return colsum_dispatch(dY, (float*)db, M, N, dtype, flags, s);
+    if (db) return colsum_dispatch(dY, (float*)db, M, N, dtype, flags, s, N);
+    return GN_OK;
+}
+
+namespace gn {
+int glu_bwd_to_gu(int kind, const void* dO, const void* gate, const void* up, void* gu, int M,
+                  int H, int dtype, hipStream_t s);
+}
+
+// Projection part of the fused GLU backward, from the local gradients gu = [dGate | dUp]
+// ([M x 2H], row pitch 2H): dX = dGate Wg + dUp Wu (one GEMM over K = 2H), dWg and dWu from
+// one GEMM over the 2H rows of gu^T X (rows < H -> dWg, rows >= H -> dWu), bias sums.
+extern "C" int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, const void* Wu,
+                               void* dX, void* dWg, void* dWu, void* dbg, void* dbu, int M, int K,
+                               int H, int dtype, unsigned flags, void* stream) {
+    clear_error();
+    GN_REQUIRE(M >= 0 && K >= 0 && H >= 0, "gn_glu_proj_bwd: negative size");
+    GN_REQUIRE(gu && X && Wg && Wu && dWg && dWu, "gn_glu_proj_bwd: null pointer");
+    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_glu_proj_bwd: dtype %d", dtype);
+    hipStream_t s = as_stream(stream);
+    const size_t esz = dtype == GN_F32 ? 4 : 2;
+    const char* g0 = (const char*)gu;
+    const bool acc = flags & GN_ACCUMULATE;
+    int rc;
+    if (M == 0 || K == 0 || H == 0) return GN_OK;
+    if (dX) {
+        GemmDesc d{};
+        d.nseg = 2;
+        d.A[0] = (const bf16_t*)g0; d.lda[0] = 2 * H; d.B[0] = (const bf16_t*)Wg; d.ldb[0] = K; d.Ks[0] = H;
+        d.A[1] = (const bf16_t*)(g0 + (size_t)H * esz); d.lda[1] = 2 * H;
+        d.B[1] = (const bf16_t*)Wu; d.ldb[1] = K; d.Ks[1] = H;
+        d.M = M; d.N = K; d.C = dX; d.C2 = dX; d.Msplit = M; d.ldc = K; d.accumulate = acc;
+        if ((rc = gemm_run(d, 0, 0, dtype, dtype, s))) return rc;
+    }
+    {
+        GemmDesc d{};
+        d.nseg = 1;
+        d.A[0] = (const bf16_t*)g0; d.lda[0] = 2 * H; d.Ks[0] = M;
+        d.B[0] = (const bf16_t*)X; d.ldb[0] = K;
+        d.M = 2 * H; d.N = K; d.C = dWg; d.C2 = dWu; d.Msplit = H; d.ldc = K; d.accumulate = acc;
+        if ((rc = gemm_run(d, 1, 0, dtype, GN_F32, s))) return rc;
+    }
+    if (dbg && (rc = colsum_dispatch(g0, (float*)dbg, M, H, dtype, flags, s, 2 * H))) return rc;
+    if (dbu && (rc = colsum_dispatch(g0 + (size_t)H * esz, (float*)dbu, M, H, dtype, flags, s, 2 * H)))
+        return rc;
     return GN_OK;
 }
 
@@ -455,21 +481,38 @@ extern "C" int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, con
     GN_REQUIRE(dO && gate && up && X && Wg && Wu && dWg && dWu && gu_ws,
                "gn_glu_linear_bwd: null pointer");
     GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_glu_linear_bwd: dtype %d", dtype);
+    int rc = glu_bwd_to_gu(kind, dO, gate, up, gu_ws, M, H, dtype, as_stream(stream));
+    if (rc) return rc;
+    return gn_glu_proj_bwd(gu_ws, X, Wg, Wu, dX, dWg, dWu, dbg, dbu, M, K, H, dtype, flags, stream);
+}
+
+// Down projection backward with the GLU local gradient fused into the dA epilogue:
+//   gu = [dGate | dUp] of glu(gate, up) at dO = dA = dY Wd   (dA never written)
+//   dWd = dY^T A (fp32),  dbd = column sums of dY (optional).
+extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, const void* Wd,
+                                   const void* gate, const void* up, void* gu, void* dWd,
+                                   void* dbd, int M, int N, int H, int dtype, unsigned flags,
+                                   void* stream) {
+    clear_error();
+    GN_REQUIRE(M >= 0 && N >= 0 && H >= 0, "gn_ffn_down_glu_bwd: negative size");
+    GN_REQUIRE(dY && A && Wd && gate && up && gu && dWd, "gn_ffn_down_glu_bwd: null pointer");
+    GN_REQUIRE(dtype == GN_BF16, "gn_ffn_down_glu_bwd: bf16 only (fp32: gn_linear_bwd + gn_glu_linear_bwd)");
+    GN_REQUIRE(kind >= GN_GLU_SWIGLU_UP && kind <= GN_GLU_REGLU_UP, "gn_ffn_down_glu_bwd: kind %d", kind);
+    if (M == 0 || H == 0) return GN_OK;
     hipStream_t s = as_stream(stream);
-    const size_t esz = dtype == GN_F32 ? 4 : 2;
-    void* dG = gu_ws;
-    void* dU = (char*)gu_ws + (size_t)M * H * esz;
-    int rc = gn_glu_bwd(kind, dO, gate, up, dG, dU, (int64_t)M * H, dtype, stream);
-    if (rc) return rc;
-    if (dX) {  // dX = dG Wg + dU Wu : one GEMM over the concatenated K = 2H
-        rc = gemm_dispatch(dG, Wg, H, dU, Wu, H, dX, M, K, 0, 0, dtype, dtype, flags, s);
-        if (rc) return rc;
+    int rc;
+    {
+        GemmDesc d{};
+        d.nseg = 1;
+        d.A[0] = (const bf16_t*)dY; d.lda[0] = N; d.Ks[0] = N;
+        d.B[0] = (const bf16_t*)Wd; d.ldb[0] = H;
+        d.M = M; d.N = H; d.Msplit = M;
+        d.epi = 1; d.gate = (const bf16_t*)gate; d.up = (const bf16_t*)up; d.ldg = H;
+        d.gu = (bf16_t*)gu; d.ldgu = 2 * H; d.H = H; d.glu_kind = kind;
+        if ((rc = gemm_run(d, 0, 0, dtype, GN_BF16, s))) return rc;
     }
-    rc = gemm_dispatch(dG, X, M, nullptr, nullptr, 0, dWg, H, K, 1, 0, dtype, GN_F32, flags, s);
+    rc = gemm_dispatch(dY, A, M, nullptr, nullptr, 0, dWd, N, H, 1, 0, dtype, GN_F32, flags, s);
     if (rc) return rc;
-    rc = gemm_dispatch(dU, X, M, nullptr, nullptr, 0, dWu, H, K, 1, 0, dtype, GN_F32, flags, s);
-    if (rc) return rc;
-    if (dbg && (rc = colsum_dispatch(dG, (float*)dbg, M, H, dtype, flags, s))) return rc;
-    if (dbu && (rc = colsum_dispatch(dU, (float*)dbu, M, H, dtype, flags, s))) return rc;
+    if (dbd) return colsum_dispatch(dY, (float*)dbd, M, N, dtype, flags, s, N);
     return GN_OK;
 }

@@ -1,0 +1,114 @@
+// gn_gemm_dma.h — descriptor of the LDS-DMA GEMM core (gn_gemm_dma.hip).
+#pragma once
+
+#include "gn_common.h"
+#include "gn_math.h"
+
+namespace gn {
+
+struct GemmDesc {
+    // transA = 0: A_s[m * lda + k];  transA = 1: A_s[k * lda + m]
+    // transB = 0: B_s[k * ldb + n];  transB = 1: B_s[n * ldb + k]
+    const bf16_t* A[2];
+    int lda[2];
+    const bf16_t* B[2];
+    int ldb[2];
+    int Ks[2];
+    int nseg;
+    int M, N;
+    // plain epilogue (epi 0): rows < Msplit -> C, rows >= Msplit -> C2 (row m - Msplit)
+    void* C;
+    void* C2;
+    int Msplit;
+    int ldc;
+    int accumulate;
+    // GLU epilogue (epi 1): the GEMM result is dO of glu(gate, up); writes
+    // gu[m * ldgu + n] = dGate, gu[m * ldgu + H + n] = dUp (bf16)
+    int epi;
+    const bf16_t* gate;
+    const bf16_t* up;
+    int ldg;
+    bf16_t* gu;
+    int ldgu;
+    int H;
+    int glu_kind;
+};
+
+// Store one accumulated element (m, n) according to the descriptor's epilogue.
+template <typename CT, int EPI>
+__device__ __forceinline__ void gemm_store(const GemmDesc& g, int m, int n, float v);
+
+bool gemm_dma_applicable(const GemmDesc& g);
+int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s);
+
+template <typename CT, int EPI>
+__device__ __forceinline__ void gemm_store(const GemmDesc& g, int m, int n, float v) {
+    if constexpr (EPI == 0) {
+        CT* C = reinterpret_cast<CT*>(m < g.Msplit ? g.C : g.C2);
+        const size_t idx = (size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n;
+        io<CT>::st(C, idx, g.accumulate ? v + io<CT>::ld(C, idx) : v);
+    } else {
+        const size_t gi = (size_t)m * g.ldg + n;
+        const float gt = bf2f(g.gate[gi]), up = bf2f(g.up[gi]);
+        float dg, du;
+        switch (g.glu_kind) {
+            case GN_GLU_SWIGLU_UP: glu_grad<GN_GLU_SWIGLU_UP>(v, gt, up, dg, du); break;
+            case GN_GLU_SWIGLU_GATE: glu_grad<GN_GLU_SWIGLU_GATE>(v, gt, up, dg, du); break;
+            case GN_GLU_GEGLU_UP: glu_grad<GN_GLU_GEGLU_UP>(v, gt, up, dg, du); break;
+            case GN_GLU_GEGLU_GATE: glu_grad<GN_GLU_GEGLU_GATE>(v, gt, up, dg, du); break;
+            default: glu_grad<GN_GLU_REGLU_UP>(v, gt, up, dg, du); break;
+        }
+        g.gu[(size_t)m * g.ldgu + n] = f2bf(dg);
+        g.gu[(size_t)m * g.ldgu + g.H + n] = f2bf(du);
+    }
+}
+
+// Epilogue of one 32x32 MFMA accumulator tile (lane layout: col = lane%32, row =
+// 8(r/4) + 4(lane/32) + r%4) at (m0, n0).  For the GLU epilogue all 32 gate/up loads of
+// the tile are issued before any store, so their latencies overlap.
+template <typename CT, int EPI, typename ACC>
+__device__ __forceinline__ void gemm_store_tile(const GemmDesc& g, int m0, int n0, const ACC& a) {
+    const int lane = threadIdx.x & 63;
+    const int n = n0 + (lane & 31), rq = (lane >> 5) * 4;
+    if (n >= g.N) return;
+    if constexpr (EPI == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + 8 * (r >> 2) + rq + (r & 3);
+            if (m < g.M) gemm_store<CT, 0>(g, m, n, a[r]);
+        }
+    } else {
+        const bf16_t* __restrict__ gp = g.gate;
+        const bf16_t* __restrict__ upp = g.up;
+        bf16_t* __restrict__ gu = g.gu;
+        bf16_t gv[16], uv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = min(m0 + 8 * (r >> 2) + rq + (r & 3), g.M - 1);
+            gv[r] = gp[(size_t)m * g.ldg + n];
+            uv[r] = upp[(size_t)m * g.ldg + n];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + 8 * (r >> 2) + rq + (r & 3);
+            if (m >= g.M) continue;
+            float dg, du;
+            const float v = a[r], gt = bf2f(gv[r]), up = bf2f(uv[r]);
+            switch (g.glu_kind) {
+                case GN_GLU_SWIGLU_UP: glu_grad<GN_GLU_SWIGLU_UP>(v, gt, up, dg, du); break;
+                case GN_GLU_SWIGLU_GATE: glu_grad<GN_GLU_SWIGLU_GATE>(v, gt, up, dg, du); break;
+                case GN_GLU_GEGLU_UP: glu_grad<GN_GLU_GEGLU_UP>(v, gt, up, dg, du); break;
+                case GN_GLU_GEGLU_GATE: glu_grad<GN_GLU_GEGLU_GATE>(v, gt, up, dg, du); break;
+                default: glu_grad<GN_GLU_REGLU_UP>(v, gt, up, dg, du); break;
+            }
+            gu[(size_t)m * g.ldgu + n] = f2bf(dg);
+            gu[(size_t)m * g.ldgu + g.H + n] = f2bf(du);
+        }
+    }
+}
+
+// Run C (+)= sum_s op(A_s) op(B_s) described by `d`: the LDS-DMA kernel when the shape
+// allows it, else the register-staged MFMA kernel, else the SIMT kernel.
+int gemm_run(const GemmDesc& d, int transA, int transB, int dtype, int c_dtype, hipStream_t s);
+
+}  // namespace gn

@@ -1,0 +1,357 @@
+// gn_gemm_dma.hip — gfx950 GEMM core: LDS-DMA staging + transpose reads.
+//
+//   C[M x N] (+)= sum_s opA(A_s) opB(B_s)        (up to two K-segments, own leading dims)
+//
+// Block tile BM x BN x 64, 256 threads = 2 x 2 waves, wave tile (BM/2) x (BN/2) built from
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulators.  Global -> LDS moves use the 16-byte
+// `global_load_lds` DMA (no VGPR staging), double-buffered: the DMA of k-tile t+1 runs
+// while the MFMAs of tile t execute.  Each operand stays in LDS in its global orientation:
+//   * k-contiguous operand (rows of 64 k):   [row][k], 16-byte chunk c of row r stored at
+//     chunk c ^ swz(r); MFMA fragments are single ds_read_b128;
+//   * k-outer operand (rows of BM/BN columns): [k][col], chunk c of k-row k stored at
+//     c ^ 2(k & 3); fragments come from ds_read_b64_tr_b16, which transposes a 4(k) x 16
+//     block across each 16-lane group (lane i gets column i, four consecutive k).
+// The DMA lane -> global-address map applies the inverse swizzle, so every DMA
+// instruction still reads whole 128-byte (or longer) row segments.
+// Epilogues: plain store (bf16 or fp32, optional accumulate, optional row split into two
+// outputs) or the GLU epilogue, which turns the dA tile of the down projection straight
+// into the SwiGLU/GEGLU/ReGLU local gradients (dA never reaches HBM).
+#include <type_traits>
+
+#include "gn_common.h"
+#include "gn_math.h"
+#include "gn_gemm_dma.h"
+
+namespace gn {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+
+constexpr int BK = 64;
+
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int fko(int k) { return 2 * (k & 3); }
+
+// One 16-byte DMA per lane: lane l's bytes land at LDS byte address lds_base + 16*l.
+// Issued from inline assembly: the compiler then does not order later LDS reads of the
+// *other* stage behind this DMA (it cannot tell the two stages apart); the kernel waits
+// for its own DMA explicitly (s_waitcnt vmcnt(0) + barrier) before reading a stage.
+__device__ __forceinline__ void dma16(const bf16_t* g, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off"
+        :
+        : "s"(lds_base), "v"(g)
+        : "memory", "m0");
+}
+
+// Stage one operand tile of R rows/cols (R = BM or BN) into LDS (R*64 bf16 = R*8 chunks,
+// R/8 DMA instructions, R/32 per wave).
+//   KC (k-contiguous): element (r, k) at P[r*ld + k]; tile stored [r][64], chunk-swizzled
+//   else (k-outer):    element (r, k) at P[k*ld + r]; tile stored [64][R], chunk-swizzled
+template <int R, bool KC>
+__device__ __forceinline__ void stage(const bf16_t* __restrict__ P, int ld, int r0, int rlim,
+                                      int k0, uint32_t s) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < R / 32; ++j) {
+        const int q = wave * (R / 32) + j;  // DMA instruction index: slots [64q, 64q+64)
+        const int slot = 64 * q + lane;
+        const bf16_t* src;
+        if (KC) {
+            const int r = slot >> 3, p = slot & 7;
+            const int c = p ^ swz(r);
+            const int rr = min(r0 + r, rlim - 1);  // rows past the edge re-read a valid row
+            src = P + (size_t)rr * ld + k0 + c * 8;
+        } else {
+            constexpr int CPR = R / 8;  // chunks per k-row
+            const int k = slot / CPR, p = slot % CPR;
+            const int c = p ^ fko(k);
+            const int col = min(r0 + c * 8, rlim - 8);
+            src = P + (size_t)(k0 + k) * ld + col;
+        }
+        dma16(src, __builtin_amdgcn_readfirstlane(s + 64 * 16 * q));
+    }
+}
+
+// A-type fragment (32 rows x 16 k) for v_mfma_f32_32x32x16_bf16: lane l -> row l%32,
+// k = 8(l/32) .. +7 within k-step ks.
+template <int R, bool KC>
+__device__ __forceinline__ bf16x8_t frag(const bf16_t* s, int row0, int ks) {
+    const int lane = threadIdx.x & 63;
+    if (KC) {
+        const int r = row0 + (lane & 31);
+        const int c = ks * 2 + (lane >> 5);
+        uint4 v = *reinterpret_cast<const uint4*>(s + r * BK + ((c ^ swz(r)) * 8));
+        return __builtin_bit_cast(bf16x8_t, v);
+    } else {
+        // 16-lane group g: columns row0 + 16(g%2) .. +15, k = ks*16 + 8(g/2) + {0..3, 4..7}
+        const int g = lane >> 4, sl = lane & 15;
+        const int col = row0 + 16 * (g & 1) + 4 * (sl & 3);
+        const int k = ks * 16 + 8 * (g >> 1) + (sl >> 2);
+        const int c = col >> 3, within = col & 7;
+        const bf16_t* p0 = s + k * R + ((c ^ fko(k)) * 8) + within;
+        const bf16_t* p1 = p0 + 4 * R;  // k + 4 (same swizzle: fko(k+4) == fko(k))
+        s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+        s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
+        typedef short s16x8_t __attribute__((ext_vector_type(8)));
+        s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        return __builtin_bit_cast(bf16x8_t, v);
+    }
+}
+
+// One k-tile of MFMAs from LDS buffers (sa, sb); fragments of k-step ks+1 are requested
+// before the MFMAs of k-step ks are issued.
+template <bool TA, bool TB, int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void compute_tile(const bf16_t* sa, const bf16_t* sb, int wm, int wn,
+                                             f32x16_t (&acc)[FM][FN]) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    bf16x8_t a[2][FM], b[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) a[0][i] = frag<BM, !TA>(sa, wm * WM + i * 32, 0);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) b[0][j] = frag<BN, TB>(sb, wn * WN + j * 32, 0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+        const int cur = ks & 1, nxt = cur ^ 1;
+        if (ks + 1 < BK / 16) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) a[nxt][i] = frag<BM, !TA>(sa, wm * WM + i * 32, ks + 1);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[nxt][j] = frag<BN, TB>(sb, wn * WN + j * 32, ks + 1);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+    }
+}
+
+// GLU local gradients of 8 consecutive elements (gate/up given as 4 packed bf16 pairs).
+template <int KIND>
+__device__ __forceinline__ void glu8(const float (&v)[8], const uint32_t (&gg)[4],
+                                     const uint32_t (&uu)[4], float (&dg)[8], float (&du)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float gt = __uint_as_float((e & 1) ? (gg[e >> 1] & 0xffff0000u) : (gg[e >> 1] << 16));
+        const float up = __uint_as_float((e & 1) ? (uu[e >> 1] & 0xffff0000u) : (uu[e >> 1] << 16));
+        glu_grad<KIND>(v[e], gt, up, dg[e], du[e]);
+    }
+}
+
+// Write one staged 32 x WN strip (LDS, fp32, pitch WN+4) to global memory: lane l owns
+// row l/2 and WN/2 consecutive columns, moved 8 at a time with 16-byte accesses.
+template <typename CT, int EPI, int WN>
+__device__ __forceinline__ void epilogue_rows(const GemmDesc& g, const float* st, int mbase, int nbase,
+                                           int lane) {
+        const int rr = lane >> 1;
+        const int m = mbase + rr;
+#pragma unroll
+        for (int q = 0; q < WN / 16; ++q) {
+            const int c = (lane & 1) * (WN / 2) + q * 8;
+            const int n = nbase + c;
+            const float4 lo = *reinterpret_cast<const float4*>(st + rr * (WN + 4) + c);
+            const float4 hi = *reinterpret_cast<const float4*>(st + rr * (WN + 4) + c + 4);
+            float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            if (m >= g.M || n >= g.N) continue;
+            if constexpr (EPI == 0) {
+                CT* C = reinterpret_cast<CT*>(m < g.Msplit ? g.C : g.C2);
+                const size_t idx = (size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n;
+                if constexpr (sizeof(CT) == 4) {
+                    float4* p = reinterpret_cast<float4*>(reinterpret_cast<float*>(C) + idx);
+                    if (g.accumulate) {
+                        const float4 o0 = p[0], o1 = p[1];
+                        v[0] += o0.x; v[1] += o0.y; v[2] += o0.z; v[3] += o0.w;
+                        v[4] += o1.x; v[5] += o1.y; v[6] += o1.z; v[7] += o1.w;
+                    }
+                    p[0] = make_float4(v[0], v[1], v[2], v[3]);
+                    p[1] = make_float4(v[4], v[5], v[6], v[7]);
+                } else {
+                    uint4* p = reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(C) + idx);
+                    if (g.accumulate) {
+                        const uint4 o = *p;
+                        const uint32_t w[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            v[2 * e] += __uint_as_float(w[e] << 16);
+                            v[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+                        }
+                    }
+                    *p = make_uint4(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]),
+                                    pack_bf2(v[6], v[7]));
+                }
+            } else {
+                const size_t gi = (size_t)m * g.ldg + n;
+                const uint4 gw = *reinterpret_cast<const uint4*>(g.gate + gi);
+                const uint4 uw = *reinterpret_cast<const uint4*>(g.up + gi);
+                const uint32_t gg[4] = {gw.x, gw.y, gw.z, gw.w}, uu[4] = {uw.x, uw.y, uw.z, uw.w};
+                float dg[8], du[8];
+                switch (g.glu_kind) {
+                    case GN_GLU_SWIGLU_UP: glu8<GN_GLU_SWIGLU_UP>(v, gg, uu, dg, du); break;
+                    case GN_GLU_SWIGLU_GATE: glu8<GN_GLU_SWIGLU_GATE>(v, gg, uu, dg, du); break;
+                    case GN_GLU_GEGLU_UP: glu8<GN_GLU_GEGLU_UP>(v, gg, uu, dg, du); break;
+                    case GN_GLU_GEGLU_GATE: glu8<GN_GLU_GEGLU_GATE>(v, gg, uu, dg, du); break;
+                    default: glu8<GN_GLU_REGLU_UP>(v, gg, uu, dg, du); break;
+                }
+                bf16_t* o = g.gu + (size_t)m * g.ldgu + n;
+                *reinterpret_cast<uint4*>(o) = make_uint4(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]),
+                                                          pack_bf2(dg[4], dg[5]), pack_bf2(dg[6], dg[7]));
+                *reinterpret_cast<uint4*>(o + g.H) = make_uint4(pack_bf2(du[0], du[1]), pack_bf2(du[2], du[3]),
+                                                                pack_bf2(du[4], du[5]), pack_bf2(du[6], du[7]));
+            }
+        }
+}
+
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    bf16_t* sbase = reinterpret_cast<bf16_t*>(smem_raw);
+    constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
+    constexpr int STAGE = A_ELEMS + B_ELEMS;
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    // LDS byte address of the dynamic allocation (for the DMA's M0 operand)
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)sbase;
+
+    const int tilesM = (g.M + BM - 1) / BM, tilesN = (g.N + BN - 1) / BN;
+    const int nblk = tilesM * tilesN;
+    int pid = blockIdx.x;
+    if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);  // XCD-contiguous ranges
+    constexpr int GROUP = 8;
+    const int group_id = pid / (GROUP * tilesN);
+    const int first_m = group_id * GROUP;
+    const int gsize = min(tilesM - first_m, GROUP);
+    const int in_group = pid % (GROUP * tilesN);
+    const int m0 = (first_m + in_group % gsize) * BM;
+    const int n0 = (in_group / gsize) * BN;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    f32x16_t acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int kt0 = g.Ks[0] / BK;
+    const int KT = kt0 + (g.nseg > 1 ? g.Ks[1] / BK : 0);
+
+    auto issue = [&](int t, int buf) {
+        const int s = t < kt0 ? 0 : 1;
+        const int k0 = (t < kt0 ? t : t - kt0) * BK;
+        const uint32_t sa = lds0 + (uint32_t)(buf * STAGE) * 2u;
+        stage<BM, !TA>(g.A[s], g.lda[s], m0, g.M, k0, sa);
+        stage<BN, TB>(g.B[s], g.ldb[s], n0, g.N, k0, sa + A_ELEMS * 2u);
+    };
+
+    if (KT > 0) issue(0, 0);
+    for (int t = 0; t < KT; ++t) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA for tile t has landed
+        __syncthreads();                // ... and everyone's; the other stage is free again
+        if (t + 1 < KT) issue(t + 1, (t + 1) & 1);
+        const bf16_t* sa = sbase + (t & 1) * STAGE;
+        compute_tile<TA, TB, BM, BN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc);
+    }
+
+    // ---- epilogue: each wave stages one 32-row strip of its tile at a time in a private
+    // LDS region (fp32, rows padded by 4), then moves 8 consecutive columns per lane with
+    // 16-byte accesses (two lanes per row).  The strip index is a compile-time constant so
+    // the accumulators are never indexed dynamically (which would put them in scratch).
+    __syncthreads();  // every wave is done with the operand stages
+    float* st = reinterpret_cast<float*>(smem_raw) + wave * 32 * (WN + 4);
+    const int rq = (lane >> 5) * 4;
+    auto strip = [&](auto I_) {
+        constexpr int i = decltype(I_)::value;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        epilogue_rows<CT, EPI, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+    };
+    strip(std::integral_constant<int, 0>{});
+    if constexpr (FM > 1) strip(std::integral_constant<int, 1>{});
+    if constexpr (FM > 2) strip(std::integral_constant<int, 2>{});
+    if constexpr (FM > 3) strip(std::integral_constant<int, 3>{});
+}
+
+template <typename F>
+bool allow_lds(F* fn, size_t bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
+}
+
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
+int launch_t(const GemmDesc& g, hipStream_t s) {
+    constexpr size_t smem = (size_t)2 * (BM + BN) * BK * sizeof(bf16_t);
+    static const bool ok = allow_lds(gemm_dma<TA, TB, CT, BM, BN, EPI>, smem);
+    if (!ok) {
+        set_error("gemm: cannot reserve %zu B of LDS", smem);
+        return GN_E_HIP;
+    }
+    const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    hipLaunchKernelGGL((gemm_dma<TA, TB, CT, BM, BN, EPI>), dim3(tiles), dim3(256), smem, s, g);
+    GN_LAUNCH_CHECK("gemm (dma)");
+    return GN_OK;
+}
+
+// Tile shape: fewest "rounds" of 256 CUs, ties broken toward the larger tile.
+template <bool TA, bool TB, typename CT, int EPI>
+int launch_shape(const GemmDesc& g, hipStream_t s) {
+    auto cost = [&](int bm, int bn) {
+        const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+        const long rounds = (tiles + 255) / 256;
+        return rounds * (long)bm * bn;  // ~ time: rounds x per-tile work
+    };
+    const long c256 = cost(256, 256), c256x128 = cost(256, 128), c128x256 = cost(128, 256),
+               c128 = cost(128, 128);
+    long best = c256;
+    int pick = 0;
+    if (c256x128 < best) { best = c256x128; pick = 1; }
+    if (c128x256 < best) { best = c128x256; pick = 2; }
+    if (c128 < best) { best = c128; pick = 3; }
+    switch (pick) {
+        case 0: return launch_t<TA, TB, CT, 256, 256, EPI>(g, s);
+        case 1: return launch_t<TA, TB, CT, 256, 128, EPI>(g, s);
+        case 2: return launch_t<TA, TB, CT, 128, 256, EPI>(g, s);
+        default: return launch_t<TA, TB, CT, 128, 128, EPI>(g, s);
+    }
+}
+
+template <typename CT, int EPI>
+int launch_trans(const GemmDesc& g, int ta, int tb, hipStream_t s) {
+    if (!ta && !tb) return launch_shape<false, false, CT, EPI>(g, s);
+    if (!ta && tb) return launch_shape<false, true, CT, EPI>(g, s);
+    if (ta && !tb) return launch_shape<true, false, CT, EPI>(g, s);
+    return launch_shape<true, true, CT, EPI>(g, s);
+}
+
+}  // namespace
+
+bool gemm_dma_applicable(const GemmDesc& g) {
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (g.M % 8 || g.N % 8 || g.M < 8 || g.N < 8) return false;
+    if (g.epi == 0 && (!al(g.C) || !al(g.C2) || g.ldc % 8)) return false;
+    if (g.epi == 1 && (!al(g.gate) || !al(g.up) || !al(g.gu) || g.ldg % 8 || g.ldgu % 8 || g.H % 8))
+        return false;
+    for (int s = 0; s < g.nseg; ++s) {
+        if (g.Ks[s] % BK || !al(g.A[s]) || !al(g.B[s]) || g.lda[s] % 8 || g.ldb[s] % 8) return false;
+    }
+    return true;
+}
+
+int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s) {
+    if (g.epi == 1) return launch_trans<bf16_t, 1>(g, transA, transB, s);
+    if (c_dtype == GN_F32) return launch_trans<float, 0>(g, transA, transB, s);
+    return launch_trans<bf16_t, 0>(g, transA, transB, s);
+}
+
+}  // namespace gn

@@ -181,7 +181,7 @@ inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 }  // namespace
 
 int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigned flags,
-                    hipStream_t s);
+                    hipStream_t s, int ld);
 
 }  // namespace gn
 
@@ -215,6 +215,6 @@ extern "C" int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, 
     else
         vsa_dw_kernel<false><<<tiles, 256, 0, s>>>(dY, Xbits, dW, Bn, O, D, words, acc, vec_ok);
     GN_LAUNCH_CHECK("gn_vsa_unpack_project_bwd");
-    if (db) return colsum_dispatch(dY, db, Bn, O, dtype, flags, s);
+    if (db) return colsum_dispatch(dY, db, Bn, O, dtype, flags, s, O);
     return GN_OK;
 }

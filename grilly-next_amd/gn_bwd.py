@@ -25,7 +25,7 @@ ROPE = {"none": 0, "interleaved": 1, "half": 2}
 # exported symbols, in the order include/gn_bwd.h declares them
 SYMBOLS = [
     "gn_last_error", "gn_version", "gn_linear_bwd", "gn_gemm", "gn_colsum", "gn_act_bwd",
-    "gn_glu_bwd", "gn_glu_linear_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
+    "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_add_inplace",
@@ -54,6 +54,8 @@ _SIGS = {
     "gn_glu_bwd": ([_I, _P, _P, _P, _P, _P, _L, _I, _P], _I),
     "gn_glu_linear_bwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                            _U, _P], _I),
+    "gn_glu_proj_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
+    "gn_ffn_down_glu_bwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_layernorm_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P, _Z, _P], _I),
     "gn_rmsnorm_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _U, _P, _Z, _P], _I),
     "gn_norm_workspace_bytes": ([_I, _I], _Z),
@@ -199,12 +201,42 @@ def glu_linear_bwd(kind, dO, gate, up, X, Wg, Wu, need_dx=True, need_db=False, g
     dbg = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
     dbu = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
     if gu_ws is None:
-        gu_ws = torch.empty((2, M, H), dtype=dO.dtype, device=dev)
+        gu_ws = torch.empty((M, 2 * H), dtype=dO.dtype, device=dev)
     _check(lib().gn_glu_linear_bwd(GLU[kind], _ptr(dO), _ptr(gate), _ptr(up), _ptr(X), _ptr(Wg),
                                    _ptr(Wu), _ptr(dX), _ptr(dWg), _ptr(dWu), _ptr(dbg),
                                    _ptr(dbu), _ptr(gu_ws), M, K, H, _dt(dO), 0, _stream()),
            "gn_glu_linear_bwd")
     return dX, dWg, dWu, dbg, dbu
+
+
+def glu_proj_bwd(gu, X, Wg, Wu, need_dx=True, need_db=False):
+    """Projection half of the GLU backward from gu = [dGate | dUp] ([M, 2H])."""
+    M, H2 = gu.shape
+    H, K = H2 // 2, X.shape[1]
+    dev = gu.device
+    dX = torch.empty((M, K), dtype=gu.dtype, device=dev) if need_dx else None
+    dWg = torch.empty((H, K), dtype=torch.float32, device=dev)
+    dWu = torch.empty((H, K), dtype=torch.float32, device=dev)
+    dbg = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
+    dbu = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
+    _check(lib().gn_glu_proj_bwd(_ptr(gu), _ptr(X), _ptr(Wg), _ptr(Wu), _ptr(dX), _ptr(dWg),
+                                 _ptr(dWu), _ptr(dbg), _ptr(dbu), M, K, H, _dt(gu), 0, _stream()),
+           "gn_glu_proj_bwd")
+    return dX, dWg, dWu, dbg, dbu
+
+
+def ffn_down_glu_bwd(kind, dY, A, Wd, gate, up, need_db=False, gu=None, dWd=None):
+    """Down projection backward with the GLU local gradient fused: (gu, dWd, dbd)."""
+    M, N = dY.shape
+    H = A.shape[1]
+    dev = dY.device
+    gu = torch.empty((M, 2 * H), dtype=dY.dtype, device=dev) if gu is None else gu
+    dWd = torch.empty((N, H), dtype=torch.float32, device=dev) if dWd is None else dWd
+    dbd = torch.empty((N,), dtype=torch.float32, device=dev) if need_db else None
+    _check(lib().gn_ffn_down_glu_bwd(GLU[kind], _ptr(dY), _ptr(A), _ptr(Wd), _ptr(gate), _ptr(up),
+                                     _ptr(gu), _ptr(dWd), _ptr(dbd), M, N, H, _dt(dY), 0,
+                                     _stream()), "gn_ffn_down_glu_bwd")
+    return gu, dWd, dbd
 
 
 def norm_workspace_bytes(rows, F):

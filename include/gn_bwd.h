@@ -116,7 +116,7 @@ int gn_glu_bwd(int kind, const void* dO, const void* gate, const void* up, void*
 
 /* Full fused GLU-projection backward (fused-swiglu-backward.glsl:82-160 and the GEGLU/
  * ReGLU twins): with gate = X Wg^T (+bg), up = X Wu^T (+bu), out = glu(gate, up) [M x H]:
- *   dGate, dUp -> written to the caller's gu_ws [2 x M x H] (dtype of the path)
+ *   gu_ws = [dGate | dUp], one row of 2H per token  [M x 2H] (dtype of the path)
  *   dX  = dGate Wg + dUp Wu    [M x K]  (skipped when dX == NULL)
  *   dWg = dGate^T X, dWu = dUp^T X  [H x K] (fp32 on the bf16 path)
  *   dbg, dbu = column sums      [H]     (skipped when NULL)
@@ -125,6 +125,21 @@ int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, const void* up
                       const void* X, const void* Wg, const void* Wu, void* dX, void* dWg,
                       void* dWu, void* dbg, void* dbu, void* gu_ws, int M, int K, int H,
                       int dtype, unsigned flags, void* stream);
+
+/* The projection half of gn_glu_linear_bwd, starting from gu = [dGate | dUp] ([M x 2H])
+ * already computed (e.g. by gn_ffn_down_glu_bwd). Same outputs as gn_glu_linear_bwd. */
+int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, const void* Wu, void* dX,
+                    void* dWg, void* dWu, void* dbg, void* dbu, int M, int K, int H, int dtype,
+                    unsigned flags, void* stream);
+
+/* Down-projection backward with the GLU backward fused into its epilogue (a two-node
+ * fusion of backward_linear and the fused-*-backward.glsl local gradients):
+ *   dA = dY Wd is never stored; gu = [dGate | dUp] of glu(gate, up) at dO = dA ([M x 2H])
+ *   dWd = dY^T A [N x H] fp32;  dbd = column sums of dY [N] (skipped when NULL)
+ * dY [M x N], A = glu(gate, up) [M x H], Wd [N x H], gate/up [M x H]. bf16 only. */
+int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, const void* Wd,
+                        const void* gate, const void* up, void* gu, void* dWd, void* dbd, int M,
+                        int N, int H, int dtype, unsigned flags, void* stream);
 
 /* ---- normalisation ---------------------------------------------------------------- */
 /* LayerNorm backward, textbook form (autograd_core.py:591-609; fnn-layernorm-backward.glsl

@@ -45,7 +45,8 @@ def rng_(seed):
 
 # ---------------------------------------------------------------------------- GEMM core
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("shape", [(136, 200, 72), (256, 128, 640), (8, 8, 8)])
+@pytest.mark.parametrize("shape", [(136, 200, 72), (256, 128, 640), (8, 8, 8), (264, 136, 128),
+                                   (520, 392, 256), (1024, 768, 512)])
 def test_gemm_bf16_layouts(gn, ta, tb, shape):
     M, N, K = shape
     r = rng_(1)
@@ -71,6 +72,22 @@ def test_gemm_two_segments_and_accumulate(gn):
     assert rel_err(host(C), ref) < 1e-5
     gn.gemm(dev(A0, torch.bfloat16), dev(B0, torch.bfloat16), C=C, accumulate=True)
     assert rel_err(host(C), ref + A0.astype(np.float64) @ B0) < 1e-5
+
+
+def test_gemm_two_segments_dma_path(gn):
+    # K segments that are multiples of 64 take the LDS-DMA kernel; edge tiles in M and N
+    r = rng_(21)
+    M, N, K0, K1 = 392, 200, 128, 192
+    for ta, tb in [(0, 0), (1, 0), (0, 1)]:
+        A0 = rnd(r.standard_normal((K0, M) if ta else (M, K0)).astype(np.float32))
+        A1 = rnd(r.standard_normal((K1, M) if ta else (M, K1)).astype(np.float32))
+        B0 = rnd(r.standard_normal((N, K0) if tb else (K0, N)).astype(np.float32))
+        B1 = rnd(r.standard_normal((N, K1) if tb else (K1, N)).astype(np.float32))
+        op = lambda x, t: (x.T if t else x).astype(np.float64)
+        ref = op(A0, ta) @ op(B0, tb) + op(A1, ta) @ op(B1, tb)
+        C = gn.gemm(dev(A0, torch.bfloat16), dev(B0, torch.bfloat16), bool(ta), bool(tb),
+                    A1=dev(A1, torch.bfloat16), B1=dev(B1, torch.bfloat16), out_dtype=torch.float32)
+        assert rel_err(host(C), ref) < 1e-5, (ta, tb)
 
 
 def test_gemm_unaligned_falls_back(gn):
@@ -167,6 +184,36 @@ def test_glu_linear_bf16(gn, kind):
     assert rel_err(host(dWu), oracle.linear_bwd(dU, X, Wu)[1]) < BF16_TOL
     assert rel_err(host(dbg), dG.sum(0)) < BF16_TOL
     assert rel_err(host(dbu), dU.sum(0)) < BF16_TOL
+
+
+@pytest.mark.parametrize("M,N,H", [(256, 192, 320), (136, 200, 96), (40, 64, 100)])
+@pytest.mark.parametrize("kind", ["swiglu_up", "geglu_up", "reglu_up"])
+def test_ffn_down_glu_fused(gn, M, N, H, kind):
+    """gn_ffn_down_glu_bwd (GLU epilogue on dA = dY Wd) + gn_glu_proj_bwd against the
+    unfused oracle chain; the shapes exercise the DMA, register-staged and SIMT GEMMs."""
+    r = rng_(22)
+    K = 128
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    Wg = rnd((r.standard_normal((H, K)) * 0.05).astype(np.float32))
+    Wu = rnd((r.standard_normal((H, K)) * 0.05).astype(np.float32))
+    gate, up = rnd(oracle.linear_fwd(X, Wg)), rnd(oracle.linear_fwd(X, Wu))
+    A = rnd(oracle.glu_fwd(kind, gate, up))
+    Wd = rnd((r.standard_normal((N, H)) * 0.05).astype(np.float32))
+    dY = rnd((r.standard_normal((M, N)) * 0.01).astype(np.float32))
+    b = torch.bfloat16
+    gu, dWd, dbd = gn.ffn_down_glu_bwd(kind, dev(dY, b), dev(A, b), dev(Wd, b), dev(gate, b),
+                                       dev(up, b), need_db=True)
+    dA, rWd, rbd = oracle.linear_bwd(dY, A, Wd)
+    dG, dU = oracle.glu_bwd(kind, dA, gate, up)
+    hgu = host(gu)
+    assert rel_err(hgu[:, :H], dG) < BF16_TOL and rel_err(hgu[:, H:], dU) < BF16_TOL
+    assert rel_err(host(dWd), rWd) < 1e-4 and rel_err(host(dbd), rbd) < 1e-4
+    dX, dWg, dWu, dbg, dbu = gn.glu_proj_bwd(gu, dev(X, b), dev(Wg, b), dev(Wu, b), need_db=True)
+    gG, gU = hgu[:, :H], hgu[:, H:]
+    assert rel_err(host(dX), oracle.linear_bwd(gG, X, Wg)[0] + oracle.linear_bwd(gU, X, Wu)[0]) < BF16_TOL
+    assert rel_err(host(dWg), oracle.linear_bwd(gG, X, Wg)[1]) < 1e-4
+    assert rel_err(host(dWu), oracle.linear_bwd(gU, X, Wu)[1]) < 1e-4
+    assert rel_err(host(dbg), gG.sum(0)) < 1e-4 and rel_err(host(dbu), gU.sum(0)) < 1e-4
 
 
 # ---------------------------------------------------------------------------- norms
