@@ -1,7 +1,7 @@
 // gn_norm.hip — row-reduction gradients: LayerNorm, RMSNorm, softmax, cross-entropy.
 //
-// LayerNorm / RMSNorm: one wave per row, the row held in registers (4-element chunks,
-// chunk c = lane + 64 j), so x and dy are read once and dx written once.  Parameter
+// LayerNorm / RMSNorm: one wave per row, the row held in registers (8-element chunks of
+// 16 bytes, chunk c = lane + 64 j), so x and dy are read once and dx written once.  Parameter
 // gradients (dgamma/dbeta, dw) are accumulated per lane across the rows a wave owns,
 // reduced across the block's waves in LDS, written as one partial row per block to the
 // workspace, and summed by a small deterministic finish kernel (no atomics).
@@ -10,53 +10,79 @@
 namespace gn {
 namespace {
 
-constexpr int kNormBlocks = 256;  // partial rows in the workspace (one per block)
+constexpr int kNormBlocks = 512;  // partial rows in the workspace (one per block)
+constexpr int kNormWaves = 8;     // waves per block (512 threads)
 
-template <typename T> struct chunk4;
-template <> struct chunk4<float> {
-    static __device__ __forceinline__ void ld(const float* p, float (&v)[4]) {
-        float4 x = *reinterpret_cast<const float4*>(p);
-        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+template <typename T> struct chunk8;
+template <> struct chunk8<float> {
+    static __device__ __forceinline__ void ld(const float* p, float (&v)[8]) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     }
-    static __device__ __forceinline__ void st(float* p, const float (&v)[4]) {
-        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    static __device__ __forceinline__ void st(float* p, const float (&v)[8]) {
+        reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
 };
-template <> struct chunk4<bf16_t> {
-    static __device__ __forceinline__ void ld(const bf16_t* p, float (&v)[4]) {
-        uint2 x = *reinterpret_cast<const uint2*>(p);
-        v[0] = __uint_as_float(x.x << 16); v[1] = __uint_as_float(x.x & 0xffff0000u);
-        v[2] = __uint_as_float(x.y << 16); v[3] = __uint_as_float(x.y & 0xffff0000u);
+template <> struct chunk8<bf16_t> {
+    static __device__ __forceinline__ void ld(const bf16_t* p, float (&v)[8]) {
+        const uint4 x = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
     }
-    static __device__ __forceinline__ void st(bf16_t* p, const float (&v)[4]) {
-        uint2 x;
-        x.x = pack_bf2(v[0], v[1]);
-        x.y = pack_bf2(v[2], v[3]);
-        *reinterpret_cast<uint2*>(p) = x;
+    static __device__ __forceinline__ void st(bf16_t* p, const float (&v)[8]) {
+        *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]),
+                                                  pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7]));
     }
 };
 
-// MODE 0 = LayerNorm (two parameter grads), 1 = RMSNorm (one)
+// Register-resident 8-element chunk: bf16 stays packed (4 VGPRs) until it is used.
+template <typename T> struct raw8;
+template <> struct raw8<float> {
+    float v[8];
+    __device__ __forceinline__ void load(const float* p) { chunk8<float>::ld(p, v); }
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+    __device__ __forceinline__ float operator[](int e) const { return v[e]; }
+};
+template <> struct raw8<bf16_t> {
+    uint32_t w[4];
+    __device__ __forceinline__ void load(const bf16_t* p) {
+        const uint4 x = *reinterpret_cast<const uint4*>(p);
+        w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+    }
+    __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = 0u; }
+    __device__ __forceinline__ float operator[](int e) const {
+        return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+    }
+};
+
+// One wave per row; lane l owns 8-element chunks c = l + 64 j (j < NC).  gamma/w is
+// re-read per row (it stays in L1/L2) so that few registers are live and many waves are
+// resident.  MODE 0 = LayerNorm (dgamma, dbeta partials), 1 = RMSNorm (dw partials).
 template <int MODE, typename T, int NC>
-__global__ __launch_bounds__(256) void norm_bwd_rows(
+__global__ __launch_bounds__(512) void norm_bwd_rows(
     const T* __restrict__ dY, const T* __restrict__ X, const T* __restrict__ gamma,
     const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dX,
     float* __restrict__ part, int rows, int F, float eps, int stat_is_var, int accumulate) {
-    __shared__ float red[4][256 * NC * 4 / 4];  // 4 waves x (NC*4*64) floats
+    __shared__ float red[64 * NC * 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nchunks = F >> 2;
+    const int nchunks = F >> 3;
     const float invF = 1.0f / (float)F;
-    float gm[NC][4], pa[NC][4], pb[NC][4];
+    float pa[NC][8], pb[NC][8];
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        const int c = lane + 64 * j;
+    for (int j = 0; j < NC; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { pa[j][e] = 0.f; pb[j][e] = 0.f; gm[j][e] = 0.f; }
-        if (c < nchunks) chunk4<T>::ld(gamma + 4 * c, gm[j]);
-    }
-    for (int r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {
+        for (int e = 0; e < 8; ++e) { pa[j][e] = 0.f; pb[j][e] = 0.f; }
+    for (int r = blockIdx.x * kNormWaves + wave; r < rows; r += gridDim.x * kNormWaves) {
         const size_t off = (size_t)r * F;
-        float x[NC][4], dy[NC][4];
+        raw8<T> x[NC], dy[NC], gm[NC];
         float mu = 0.f, rs;
         if (MODE == 0) {
             mu = mean[r];
@@ -64,41 +90,45 @@ __global__ __launch_bounds__(256) void norm_bwd_rows(
         } else {
             rs = rstd[r];
         }
-        float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
             const int c = lane + 64 * j;
             if (c < nchunks) {
-                chunk4<T>::ld(X + off + 4 * c, x[j]);
-                chunk4<T>::ld(dY + off + 4 * c, dy[j]);
+                x[j].load(X + off + 8 * c);
+                dy[j].load(dY + off + 8 * c);
+                gm[j].load(gamma + 8 * c);
             } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) { x[j][e] = 0.f; dy[j][e] = 0.f; }
+                x[j].zero();
+                dy[j].zero();
+                gm[j].zero();
             }
+        }
+        float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+        for (int j = 0; j < NC; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
                 if (MODE == 0) {
-                    float xh = (x[j][e] - mu) * rs, g = dy[j][e] * gm[j][e];
+                    const float xh = (x[j][e] - mu) * rs, g = dy[j][e] * gm[j][e];
                     s1 += g;
                     s2 += g * xh;
                 } else {
                     s1 += gm[j][e] * dy[j][e] * x[j][e];
                 }
             }
-        }
         s1 = wave_sum(s1);
         if (MODE == 0) s2 = wave_sum(s2);
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
             const int c = lane + 64 * j;
             if (c >= nchunks) continue;
-            float o[4];
-            if (accumulate) chunk4<T>::ld(dX + off + 4 * c, o);
+            float o[8];
+            if (accumulate) chunk8<T>::ld(dX + off + 8 * c, o);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int e = 0; e < 8; ++e) {
                 float v;
                 if (MODE == 0) {
-                    float xh = (x[j][e] - mu) * rs, g = dy[j][e] * gm[j][e];
+                    const float xh = (x[j][e] - mu) * rs, g = dy[j][e] * gm[j][e];
                     v = rs * (g - s1 * invF - xh * s2 * invF);
                     pa[j][e] += dy[j][e] * xh;
                     pb[j][e] += dy[j][e];
@@ -108,36 +138,47 @@ __global__ __launch_bounds__(256) void norm_bwd_rows(
                 }
                 o[e] = accumulate ? o[e] + v : v;
             }
-            chunk4<T>::st(dX + off + 4 * c, o);
+            chunk8<T>::st(dX + off + 8 * c, o);
         }
     }
-    // block-level reduction of the parameter-gradient partials, one param at a time
+    // block reduction of the parameter partials (waves add into LDS in turn), then one
+    // partial row per block in the workspace
     for (int p = 0; p < (MODE == 0 ? 2 : 1); ++p) {
-        __syncthreads();
+        for (int w = 0; w < kNormWaves; ++w) {
+            __syncthreads();
+            if (wave == w) {
 #pragma unroll
-        for (int j = 0; j < NC; ++j)
+                for (int j = 0; j < NC; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) red[wave][(lane + 64 * j) * 4 + e] = p == 0 ? pa[j][e] : pb[j][e];
+                    for (int e = 0; e < 8; ++e) {
+                        const int f = (lane + 64 * j) * 8 + e;
+                        const float v = p == 0 ? pa[j][e] : pb[j][e];
+                        red[f] = w == 0 ? v : red[f] + v;
+                    }
+            }
+        }
         __syncthreads();
         float* dst = part + ((size_t)p * gridDim.x + blockIdx.x) * F;
-        for (int f = threadIdx.x; f < F; f += 256)
-            dst[f] = red[0][f] + red[1][f] + red[2][f] + red[3][f];
+        for (int f = threadIdx.x; f < F; f += 512) dst[f] = red[f];
     }
 }
 
-// out[f] (+)= sum_g part[g][f] over G partial rows; grid ceil(F/64), block 256.
+// out[f] (+)= sum_g part[g][f] over G partial rows: block = 8 columns x 32 row groups.
 __global__ __launch_bounds__(256) void colsum_partials(const float* __restrict__ part, int G,
                                                        int F, float* __restrict__ out,
                                                        int accumulate) {
-    __shared__ float sh[4][64];
-    const int c = blockIdx.x * 64 + (threadIdx.x & 63), g0 = threadIdx.x >> 6;
+    __shared__ float sh[32][8];
+    const int cl = threadIdx.x & 7, rg = threadIdx.x >> 3;
+    const int c = blockIdx.x * 8 + cl;
     float s = 0.f;
     if (c < F)
-        for (int g = g0; g < G; g += 4) s += part[(size_t)g * F + c];
-    sh[g0][threadIdx.x & 63] = s;
+        for (int g = rg; g < G; g += 32) s += part[(size_t)g * F + c];
+    sh[rg][cl] = s;
     __syncthreads();
-    if (g0 == 0 && c < F) {
-        float t = sh[0][threadIdx.x] + sh[1][threadIdx.x] + sh[2][threadIdx.x] + sh[3][threadIdx.x];
+    if (threadIdx.x < 8 && c < F) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) t += sh[i][cl];
         out[c] = accumulate ? out[c] + t : t;
     }
 }
@@ -215,18 +256,19 @@ template <int MODE, typename T>
 int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean,
              const float* rstd, void* dX, float* dA, float* dB, int rows, int F, float eps,
              int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s) {
-    const bool vec_ok = (F % 4 == 0) && F <= 4096 && aligned16(dY) && aligned16(X) &&
-                        aligned16(dX) && ((reinterpret_cast<uintptr_t>(gamma) & 7u) == 0);
+    // rows wider than 2048 would not fit in registers: they use the generic path
+    const bool vec_ok = (F % 8 == 0) && F <= 2048 && aligned16(dY) && aligned16(X) &&
+                        aligned16(dX) && aligned16(gamma);
     const bool need_param = dA || dB;
     if (vec_ok) {
-        const int G = std::min(kNormBlocks, (rows + 3) / 4);
+        const int G = std::min(kNormBlocks, (rows + kNormWaves - 1) / kNormWaves);
         const size_t need = (size_t)(MODE == 0 ? 2 : 1) * G * F * sizeof(float);
         if (need_param && (!ws || ws_bytes < need)) {
             set_error("norm backward: workspace %zu B < %zu B", ws_bytes, need);
             return GN_E_WORKSPACE;
         }
         float* part = need_param ? (float*)ws : nullptr;
-        const int nc = (F / 4 + 63) / 64;
+        const int nc = (F / 8 + 63) / 64;
         // part == nullptr is never dereferenced: without param grads the partial write is
         // redirected to a dummy path below by using the generic dx kernel instead.
         if (!need_param) {
@@ -236,17 +278,15 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
             return GN_OK;
         }
 #define GN_NORM_LAUNCH(NCV)                                                                    \
-    norm_bwd_rows<MODE, T, NCV><<<G, 256, 0, s>>>((const T*)dY, (const T*)X, (const T*)gamma,  \
+    norm_bwd_rows<MODE, T, NCV><<<G, 512, 0, s>>>((const T*)dY, (const T*)X, (const T*)gamma,  \
                                                   mean, rstd, (T*)dX, part, rows, F, eps,       \
                                                   stat_var, acc)
         if (nc <= 1) GN_NORM_LAUNCH(1);
         else if (nc <= 2) GN_NORM_LAUNCH(2);
-        else if (nc <= 4) GN_NORM_LAUNCH(4);
-        else if (nc <= 8) GN_NORM_LAUNCH(8);
-        else GN_NORM_LAUNCH(16);
+        else GN_NORM_LAUNCH(4);
 #undef GN_NORM_LAUNCH
         GN_LAUNCH_CHECK("norm backward rows");
-        const unsigned gf = (F + 63) / 64;
+        const unsigned gf = (F + 7) / 8;
         if (dA) colsum_partials<<<gf, 256, 0, s>>>(part, G, F, dA, acc);
         if (MODE == 0 && dB) colsum_partials<<<gf, 256, 0, s>>>(part + (size_t)G * F, G, F, dB, acc);
         GN_LAUNCH_CHECK("norm backward finish");
@@ -326,7 +366,7 @@ using namespace gn;
 
 extern "C" size_t gn_norm_workspace_bytes(int rows, int F) {
     if (rows <= 0 || F <= 0) return 0;
-    const int G = std::min(kNormBlocks, (rows + 3) / 4);
+    const int G = std::min(kNormBlocks, (rows + kNormWaves - 1) / kNormWaves);
     return (size_t)2 * G * F * sizeof(float);
 }
 
