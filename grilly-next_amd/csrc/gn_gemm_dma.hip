@@ -54,12 +54,12 @@ __device__ __forceinline__ void dma16(const bf16_t* g, uint32_t lds_base) {
 // R/8 DMA instructions, R/32 per wave).
 //   KC (k-contiguous): element (r, k) at P[r*ld + k]; tile stored [r][64], chunk-swizzled
 //   else (k-outer):    element (r, k) at P[k*ld + r]; tile stored [64][R], chunk-swizzled
-template <int R, bool KC>
+template <int R, bool KC, int J0 = 0, int J1 = R / 32>
 __device__ __forceinline__ void stage(const bf16_t* __restrict__ P, int ld, int r0, int rlim,
                                       int k0, uint32_t s) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < R / 32; ++j) {
+    for (int j = J0; j < J1; ++j) {
         const int q = wave * (R / 32) + j;  // DMA instruction index: slots [64q, 64q+64)
         const int slot = 64 * q + lane;
         const bf16_t* src;
@@ -107,9 +107,9 @@ __device__ __forceinline__ bf16x8_t frag(const bf16_t* s, int row0, int ks) {
 
 // One k-tile of MFMAs from LDS buffers (sa, sb); fragments of k-step ks+1 are requested
 // before the MFMAs of k-step ks are issued.
-template <bool TA, bool TB, int BM, int BN, int FM, int FN>
+template <bool TA, bool TB, int BM, int BN, int FM, int FN, typename HOOK>
 __device__ __forceinline__ void compute_tile(const bf16_t* sa, const bf16_t* sb, int wm, int wn,
-                                             f32x16_t (&acc)[FM][FN]) {
+                                             f32x16_t (&acc)[FM][FN], HOOK&& after_step) {
     constexpr int WM = BM / 2, WN = BN / 2;
     bf16x8_t a[2][FM], b[2][FN];
 #pragma unroll
@@ -130,6 +130,7 @@ __device__ __forceinline__ void compute_tile(const bf16_t* sa, const bf16_t* sb,
 #pragma unroll
             for (int j = 0; j < FN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+        after_step(std::integral_constant<int, 0>{}, ks);
     }
 }
 
@@ -208,10 +209,18 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& g, const float* st
         }
 }
 
+// Pipeline depth: three LDS stages when they fit and A is k-contiguous; with a k-outer A
+// (transpose reads for both operands) two stages measured faster on MI355X.
+template <bool TA, int BM, int BN>
+constexpr int gemm_stages() {
+    return (!TA && 3 * (BM + BN) * BK * 2 <= 160 * 1024) ? 3 : 2;
+}
+
 template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     bf16_t* sbase = reinterpret_cast<bf16_t*>(smem_raw);
+    constexpr int STAGES = gemm_stages<TA, BM, BN>();
     constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
     constexpr int STAGE = A_ELEMS + B_ELEMS;
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
@@ -244,21 +253,49 @@ __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
     const int kt0 = g.Ks[0] / BK;
     const int KT = kt0 + (g.nseg > 1 ? g.Ks[1] / BK : 0);
 
+    auto tile_base = [&](int buf) { return lds0 + (uint32_t)(buf * STAGE) * 2u; };
     auto issue = [&](int t, int buf) {
         const int s = t < kt0 ? 0 : 1;
         const int k0 = (t < kt0 ? t : t - kt0) * BK;
-        const uint32_t sa = lds0 + (uint32_t)(buf * STAGE) * 2u;
-        stage<BM, !TA>(g.A[s], g.lda[s], m0, g.M, k0, sa);
-        stage<BN, TB>(g.B[s], g.ldb[s], n0, g.N, k0, sa + A_ELEMS * 2u);
+        stage<BM, !TA>(g.A[s], g.lda[s], m0, g.M, k0, tile_base(buf));
+        stage<BN, TB>(g.B[s], g.ldb[s], n0, g.N, k0, tile_base(buf) + A_ELEMS * 2u);
+    };
+    // DMA of tile t split over the four k-steps of the current tile's MFMAs:
+    // step 0/1 carry the A halves, steps 2/3 the B halves.
+    auto issue_part = [&](int t, int buf, int step) {
+        const int s = t < kt0 ? 0 : 1;
+        const int k0 = (t < kt0 ? t : t - kt0) * BK;
+        const uint32_t base = tile_base(buf);
+        constexpr int JA = BM / 32, JB = BN / 32;
+        switch (step) {
+            case 0: stage<BM, !TA, 0, JA / 2>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
+            case 1: stage<BM, !TA, JA / 2, JA>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
+            case 2: stage<BN, TB, 0, JB / 2>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
+            default: stage<BN, TB, JB / 2, JB>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
+        }
     };
 
+    // vmcnt immediate: outstanding DMA instructions of one tile per wave
+    constexpr int DMA_PER_TILE = (BM + BN) / 32;
+    static_assert(DMA_PER_TILE < 64, "vmcnt is a 6-bit field");
+    // s_waitcnt vmcnt(N) expcnt(7) lgkmcnt(15): vmcnt bits [3:0] and [15:14]
+    constexpr unsigned WAIT_ONE_TILE =
+        0x0F70u | (DMA_PER_TILE & 15u) | ((unsigned)(DMA_PER_TILE >> 4) << 14);
+
     if (KT > 0) issue(0, 0);
+    if (STAGES > 2 && KT > 1) issue(1, 1);
     for (int t = 0; t < KT; ++t) {
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA for tile t has landed
-        __syncthreads();                // ... and everyone's; the other stage is free again
-        if (t + 1 < KT) issue(t + 1, (t + 1) & 1);
-        const bf16_t* sa = sbase + (t & 1) * STAGE;
-        compute_tile<TA, TB, BM, BN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc);
+        // tile t's DMA has landed (with 3 stages, tile t+1's may still be in flight)
+        if (STAGES > 2 && t + 1 < KT) __builtin_amdgcn_s_waitcnt(WAIT_ONE_TILE);
+        else __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // ... for every wave; the stage about to be refilled is free
+        const int nxt = t + STAGES - 1;  // tile whose DMA is issued during this compute
+        const int nbuf = nxt % STAGES;
+        const bf16_t* sa = sbase + (t % STAGES) * STAGE;
+        compute_tile<TA, TB, BM, BN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc,
+                                             [&](auto, int ks) {
+                                                 if (nxt < KT) issue_part(nxt, nbuf, ks);
+                                             });
     }
 
     // ---- epilogue: each wave stages one 32-row strip of its tile at a time in a private
@@ -291,7 +328,7 @@ bool allow_lds(F* fn, size_t bytes) {
 
 template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
 int launch_t(const GemmDesc& g, hipStream_t s) {
-    constexpr size_t smem = (size_t)2 * (BM + BN) * BK * sizeof(bf16_t);
+    constexpr size_t smem = (size_t)gemm_stages<TA, BM, BN>() * (BM + BN) * BK * sizeof(bf16_t);
     static const bool ok = allow_lds(gemm_dma<TA, TB, CT, BM, BN, EPI>, smem);
     if (!ok) {
         set_error("gemm: cannot reserve %zu B of LDS", smem);
