@@ -11,7 +11,14 @@ The metric is layer-backward tokens/s; the dominant kernel's roofline fraction c
 HIP events around its own launches, and the CPU baseline is the oracle (C, OpenMP) timed on
 a bounded token sample of the same workload on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Other BASELINE configs (parity-tested, measured with --workload):
+    attn  configs[2]: causal attention backward with RoPE, B4 H16 S2048 D128, bf16
+    vsa   configs[3]: VSA unpack-project dW (8192 x 10240 bits -> 768, fp32 dY) and the
+          surrogate-loss backward (K = 4)
+    mlp   configs[0]: MLP 784->256->10 fp32 B=64 through the tape engine (grilly_core)
+Each prints one JSON line of the same shape; the default (ffn) is the headline metric.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ffn|attn|vsa|mlp]
 """
 import argparse
 import json
@@ -36,7 +43,166 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--cpu-tokens", type=int, default=256)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--workload", default="ffn", choices=["ffn", "attn", "vsa", "mlp"])
     return p.parse_args()
+
+
+def timed(torch, fn, steps, warmup):
+    """Average ms of fn() over `steps` calls, HIP events on torch's current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def line(metric, value, unit, args, ms, dtype, config, roofline, cpu, higher=True):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": higher,
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+            "data": "synthetic (seeded)", "config": config, "roofline": roofline,
+            "cpu_baseline": cpu}
+
+
+def bench_attn(args, torch, gn):
+    """causal attention backward with RoPE (theta 1e4), B4 H16 S2048 D128."""
+    B, H, S, D = 4, 16, 2048, 128
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    bf = torch.bfloat16
+    Q, K, V = (torch.randn(B, H, S, D, device=dev, generator=g).to(bf) for _ in range(3))
+    dO = (torch.randn(B, H, S, D, device=dev, generator=g) * 1e-2).to(bf)
+    ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D), dev)
+    O, LSE = gn.attn_fwd(Q, K, V, causal=True, rope="interleaved", ws=ws)
+    out = (torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V))
+    ms = timed(torch, lambda: gn.attn_bwd(Q, K, V, O, dO, LSE, causal=True, rope="interleaved",
+                                          ws=ws, out=out), args.steps, args.warmup)
+    flops = 5 * 2.0 * S * S * D * 0.5 * B * H  # causal, algorithmic (5 GEMMs)
+    tf = flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        r = np.random.default_rng(3)
+        Hs, Ss = 16, 1024
+        q, k, v = (r.standard_normal((1, Hs, Ss, D)).astype(np.float32) for _ in range(3))
+        do = (r.standard_normal((1, Hs, Ss, D)) * 1e-2).astype(np.float32)
+        o, lse = oracle.attn_fwd(q, k, v)
+        t0 = time.perf_counter()
+        oracle.attn_bwd(q, k, v, do, lse)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(5 * 2.0 * Ss * Ss * D * 0.5 * Hs / dt / 1e12, 6), "unit": "TFLOP/s",
+               "cores": oracle.num_threads(), "kind": "port",
+               "sample": f"1 x {Hs} heads x S={Ss} (oracle C/OpenMP fp64), {dt:.2f} s"}
+    return line("causal attention backward with RoPE (algorithmic TFLOP/s)", round(tf, 2),
+                "TFLOP/s", args, ms, "bf16",
+                {"workload": "C3 causal attention bwd + RoPE(1e4), B4 H16 S2048 D128",
+                 "batch": B, "heads": H, "seq_len": S, "head_dim": D},
+                {"kernel": "gn_attn_bwd (pre-pass + dK/dV + dQ kernels)", "bound": "mfma",
+                 "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                 "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None}, cpu)
+
+
+def bench_vsa(args, torch, gn):
+    """VSA unpack-project dW/db (fp32 dY, two-term bf16 split) + surrogate bwd."""
+    Bn, D, O, K = 8192, 10240, 768, 4
+    words = D // 32
+    dev = torch.device("cuda:0")
+    r = np.random.default_rng(4)
+    bits = gn.u32_tensor(r.integers(0, 2**32, size=(Bn, words), dtype=np.uint64).astype(np.uint32), dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    dY = torch.randn(Bn, O, device=dev, generator=g)
+    dW = torch.empty(O, D, device=dev)
+    db = torch.empty(O, device=dev)
+    ms = timed(torch, lambda: gn.vsa_unpack_project_bwd(dY, bits, D, dW=dW, db=db), args.steps,
+               args.warmup)
+    flops = 2.0 * O * D * Bn
+    tf = flops / (ms * 1e-3) / 1e12
+    preds = torch.randn(Bn, K, D, device=dev, generator=g)
+    res_np, w_np = np.zeros((Bn, 4), np.uint32), np.full((Bn, K), 1.0 / K, np.float32)
+    res_np[:, 1] = 1
+    res = gn.u32_tensor(res_np, dev)
+    wts = torch.from_numpy(w_np).to(dev)
+    dP = torch.empty_like(preds)
+    ms_s = timed(torch, lambda: gn.vsa_surrogate_bwd(preds, bits, res, wts, dPreds=dP),
+                 args.steps, args.warmup)
+    bytes_s = 2.0 * Bn * K * D * 4 + Bn * words * 4
+    gbs = bytes_s / (ms_s * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        Bs = 256
+        bh = r.integers(0, 2**32, size=(Bs, words), dtype=np.uint64).astype(np.uint32)
+        dy = r.standard_normal((Bs, O)).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.vsa_unpack_project_bwd(dy, bh, D)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(2.0 * O * D * Bs / dt / 1e12, 6), "unit": "TFLOP/s",
+               "cores": oracle.num_threads(), "kind": "port",
+               "sample": f"{Bs} of {Bn} rows of the dW contraction (oracle C/OpenMP fp64), {dt:.2f} s"}
+    out = line("VSA unpack-project dW backward (algorithmic TFLOP/s)", round(tf, 2), "TFLOP/s",
+               args, ms, "f32 (bf16x2 split MFMA)",
+               {"workload": "C4 VSA unpack-project bwd: 8192 x 10240 bits -> 768, fp32 dY",
+                "rows": Bn, "vsa_dim": D, "out_dim": O},
+               {"kernel": "vsa_dw_kernel<true>", "bound": "mfma", "achieved": round(tf, 1),
+                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                "traffic": None}, cpu)
+    out["surrogate_bwd"] = {"ms": round(ms_s, 4), "GB/s": round(gbs, 1),
+                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "K": K,
+                            "bytes": bytes_s}
+    return out
+
+
+def bench_mlp(args, torch, gn):
+    """MLP 784->256->10 fp32, batch 64, ReLU, CE, one backward through the tape."""
+    import grilly_core
+    import grilly_bridge as gb
+    dev = torch.device("cuda:0")
+    r = np.random.default_rng(1)
+    Bsz = 64
+    lim1, lim2 = np.sqrt(6 / (784 + 256)), np.sqrt(6 / (256 + 10))
+    t = lambda a, dt=torch.float32: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dt)
+    X = t(r.standard_normal((Bsz, 784)).astype(np.float32))
+    y = t(r.integers(0, 10, Bsz).astype(np.int32), torch.int32)
+    W1 = t(r.uniform(-lim1, lim1, (256, 784)).astype(np.float32))
+    W2 = t(r.uniform(-lim2, lim2, (10, 256)).astype(np.float32))
+    b1, b2 = torch.zeros(256, device=dev), torch.zeros(10, device=dev)
+    Z = (X @ W1.t() + b1).contiguous()
+    Hh = torch.relu(Z).contiguous()
+    L = (Hh @ W2.t() + b2).contiguous()
+    loss = torch.zeros(1, device=dev)
+    device = grilly_core.Device(0)
+    gb.attach_torch_stream(device)
+    tape = gb.create_tape_context(device)
+
+    def step():
+        tape.begin()
+        n1 = tape.record_op(grilly_core.OpType.Linear, [gb.tref(X)], [gb.tref(Z)])
+        tape.save_for_backward(n1, [W1.data_ptr(), b1.data_ptr()])
+        tape.record_op(grilly_core.OpType.ReLU, [gb.tref(Z, True)], [gb.tref(Hh)])
+        n3 = tape.record_op(grilly_core.OpType.Linear, [gb.tref(Hh, True)], [gb.tref(L)])
+        tape.save_for_backward(n3, [W2.data_ptr(), b2.data_ptr()])
+        ce = tape.record_op(grilly_core.OpType.CrossEntropy, [gb.tref(L, True), gb.tref(y)],
+                            [gb.tref(loss)], gb.cross_entropy_params(1.0))
+        tape.backward(ce, 0)
+        tape.end()
+    ms = timed(torch, step, args.steps, args.warmup)
+    flops = 2.0 * Bsz * (784 * 256 + 256 * 10 + 256 * 10)
+    return line("MLP tape backward step time (784-256-10, B=64, fp32)", round(ms * 1e3, 2), "us",
+                args, ms, "f32",
+                {"workload": "C1 MLP 784->256->10 fp32 B=64: CE, 2x linear, ReLU bwd via the tape",
+                 "batch": Bsz},
+                {"kernel": "whole step (launch-bound)", "bound": "latency",
+                 "achieved": round(flops / (ms * 1e-3) / 1e12, 4), "peak": 157.3, "unit": "TFLOP/s",
+                 "frac": round(flops / (ms * 1e-3) / 1e12 / 157.3, 6), "traffic": None}, None,
+                higher=False)
 
 
 def make_inputs(torch, dev):
@@ -145,6 +311,10 @@ def main():
     import torch
     import gn_bwd as gn
     gn.lib()
+    if args.workload != "ffn":
+        fn = {"attn": bench_attn, "vsa": bench_vsa, "mlp": bench_mlp}[args.workload]
+        print(json.dumps(fn(args, torch, gn)))
+        return
     dev = torch.device("cuda:0")
     d = make_inputs(torch, dev)
     st = Step(gn, torch, d)
