@@ -30,6 +30,12 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INCLU
              "-Wno-unused-function", "-Wno-unused-variable"]
 
 
+# Extra flags per source.  gn_attn.hip: MFMAs in their VGPR form — the attention kernels
+# keep P and dS in VGPRs between MFMAs, and the AGPR form made the register allocator
+# shuttle every accumulator between the two files on each loop iteration.
+FILE_FLAGS = {"gn_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _run(cmd):
     p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(l for l in p.stdout.splitlines() if "packed-fp32-ops" not in l)
@@ -44,7 +50,7 @@ def _obj(src):
 
 def build_kernels(jobs=8):
     os.makedirs(BUILD, exist_ok=True)
-    cmds = [["hipcc", *HIP_FLAGS, "-c", os.path.join(CSRC, s), "-o", _obj(s)]
+    cmds = [["hipcc", *HIP_FLAGS, *FILE_FLAGS.get(s, []), "-c", os.path.join(CSRC, s), "-o", _obj(s)]
             for s in KERNEL_SOURCES]
     with ThreadPoolExecutor(jobs) as ex:
         list(ex.map(_run, cmds))

@@ -8,37 +8,26 @@
 // materialised: it is recomputed per 64x64 tile from the saved LSE, and the row dot
 // D_i = sum_j P_ij dP_ij is obtained as rowsum(dO * O) (equal for a consistent forward).
 //
-// bf16 MFMA path (D = 64 or 128): a pre-pass writes rotated Q, K (bf16) and D_i; then
-//   attn_bwd_dkdv: one block per (64-key block, b*h); loops over query blocks,
-//                  S = Q K^T and dP = dO V^T (v_mfma_f32_32x32x16_bf16), P and dS written to
-//                  LDS transposed, dV += P^T dO, dK += dS^T Q;
-//   attn_bwd_dq:   one block per (64-query block, b*h); loops over key blocks,
-//                  S^T = K Q^T, dP^T = V dO^T, dQ += dS K.
-// Both keep fp32 accumulators in registers and write bf16 through an LDS-staged epilogue
-// that applies the inverse rotation.  Two kernels (7 tile products instead of 5) keep the
-// dQ reduction free of atomics and deterministic.
+// bf16 MFMA path (D = 64 or 128): one pre-pass writes rotated Q, K (bf16), D_i and
+// L log2(e); then two kernels, both v_mfma_f32_32x32x16_bf16 with fp32 accumulators in
+// registers and operand tiles brought into LDS by DMA while the previous tile computes:
+//   attn_dkdv_mfma: one block per (b*h, 128 keys); loops over query tiles of 64;
+//   attn_dq_mfma:   one block per (b*h, 128 queries); loops over key tiles of 64.
+// P and dS go from the accumulators of one product straight into the operand registers
+// of the next (the accumulator row order is matched by the transpose reads of the other
+// operand), so neither is ever written to LDS.  Two kernels (7 tile products instead of 5)
+// keep the dQ reduction free of atomics and deterministic.  The epilogues stage each
+// wave's rows in LDS and apply the inverse rotation from a cos/sin table.
 // A SIMT path (any D <= 256, fp32 or bf16) serves other shapes and the fp32 dtype.
 #include <math.h>
 
+#include <type_traits>
+
 #include "gn_common.h"
+#include "gn_mfma.h"
 
 namespace gn {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ bf16x8_t afrag(const bf16_t* p) {
-    uint4 v = *reinterpret_cast<const uint4*>(p);
-    return __builtin_bit_cast(bf16x8_t, v);
-}
-__device__ __forceinline__ f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ void zero16(f32x16_t& a) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = 0.f;
-}
 
 // RoPE angle for pair i at position p: p * base^(-2i/D), reduced in fp64 then sincos fp32.
 __device__ __forceinline__ void rope_cs(int p, int i, int D, float theta, float& c, float& s) {
@@ -87,277 +76,485 @@ __global__ __launch_bounds__(256) void row_dot(const T* __restrict__ A, const T*
     if (lane == 0) out[r] = s;
 }
 
-// ---- tile loaders (64 rows x D, bf16) ---------------------------------------------------
-// natural: s[row][d] (pitch D+8); rows beyond `nrows` are zero
-template <int D>
-__device__ __forceinline__ void load_nat(bf16_t* s, const bf16_t* __restrict__ g, int nrows) {
-    constexpr int CPR = D / 8;  // 16-byte chunks per row
-    for (int c = threadIdx.x; c < 64 * CPR; c += 256) {
-        const int r = c / CPR, k = (c % CPR) * 8;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (r < nrows) v = *reinterpret_cast<const uint4*>(g + (size_t)r * D + k);
-        *reinterpret_cast<uint4*>(s + r * (D + 8) + k) = v;
-    }
+// ---- MFMA path (bf16, D = 64 or 128) ---------------------------------------------------
+//
+// Operand tiles are 64 rows x D bf16 kept in LDS in their global orientation (row pitch
+// 2D bytes).  The 16-byte chunk c of tile row r sits at chunk position c ^ tswz<D>(r); for
+// the two fragment reads below (ds_read_b128 of one chunk from 32 consecutive rows, and
+// the transpose read of 4 consecutive rows x 64 bytes per 32 lanes) this spreads the
+// lanes of every LDS pass over distinct banks, for 32- and 64-bank organisations alike.
+template <int D> __device__ __forceinline__ int tswz(int r);
+template <> __device__ __forceinline__ int tswz<128>(int r) {
+    return ((r & 1) * 6) ^ (((r >> 1) & 1) * 10) ^ ((r >> 2) & 1) ^ (((r >> 3) & 1) << 1);
 }
-// transposed: s[d][row] (pitch 72); 4 rows x 8 d per thread, regrouped with v_perm
+template <> __device__ __forceinline__ int tswz<64>(int r) {
+    return ((r & 3) << 1) ^ ((r >> 2) & 1) ^ (((r >> 3) & 1) << 1);
+}
+
+constexpr int tile_bytes(int D) { return 64 * D * 2; }
+
+// DMA rows row0 .. row0+63 of a [S x D] matrix into a swizzled LDS tile (rows past S
+// re-read row S-1; the kernels mask them).  D/32 DMA instructions per wave.
 template <int D>
-__device__ __forceinline__ void load_tr(bf16_t* s, const bf16_t* __restrict__ g, int nrows) {
-    constexpr int DC = D / 8;  // d chunks
-    for (int c = threadIdx.x; c < 16 * DC; c += 256) {
-        const int dc = c % DC, rg = c / DC;
-        uint32_t w[4][4];
+__device__ __forceinline__ void dma_tile(const bf16_t* __restrict__ g, int row0, int S,
+                                         uint32_t lds) {
+    constexpr int CPR = D / 8, RPI = 64 / CPR, PER_WAVE = CPR / 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = rg * 4 + i;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (r < nrows) v = *reinterpret_cast<const uint4*>(g + (size_t)r * D + dc * 8);
-            w[i][0] = v.x; w[i][1] = v.y; w[i][2] = v.z; w[i][3] = v.w;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint2 lo, hi;
-            lo.x = __builtin_amdgcn_perm(w[1][q], w[0][q], 0x05040100u);
-            lo.y = __builtin_amdgcn_perm(w[3][q], w[2][q], 0x05040100u);
-            hi.x = __builtin_amdgcn_perm(w[1][q], w[0][q], 0x07060302u);
-            hi.y = __builtin_amdgcn_perm(w[3][q], w[2][q], 0x07060302u);
-            *reinterpret_cast<uint2*>(s + (dc * 8 + 2 * q) * 72 + rg * 4) = lo;
-            *reinterpret_cast<uint2*>(s + (dc * 8 + 2 * q + 1) * 72 + rg * 4) = hi;
-        }
+    for (int j = 0; j < PER_WAVE; ++j) {
+        const int q = wave * PER_WAVE + j;  // instruction q fills tile bytes [1024q, +1024)
+        const int r = q * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ tswz<D>(r);
+        const int rr = min(row0 + r, S - 1);
+        dma16(g + (size_t)rr * D + c * 8, __builtin_amdgcn_readfirstlane(lds + q * 1024));
     }
 }
 
-// Store a 64 x D fp32 tile staged in LDS (pitch D+4) to global bf16, applying R^T per row.
+// Fragment whose 32 rows are tile rows m0 .. m0+31 and whose k runs along d:
+// lane l -> row m0 + l%32, d = 16 ks + 8(l/32) .. +7.
 template <int D>
-__device__ __forceinline__ void store_rotated(const float* st, bf16_t* __restrict__ g, int row0,
-                                              int nrows, int mode, float theta) {
-    constexpr int H = D / 2;
-    for (int idx = threadIdx.x; idx < 64 * H; idx += 256) {
-        const int r = idx / H, i = idx % H;
-        if (r >= nrows) continue;
-        int e0, e1;
-        if (mode == GN_ROPE_NONE) { e0 = 2 * i; e1 = 2 * i + 1; }
-        else rope_pair(mode, i, D, e0, e1);
-        float x0 = st[r * (D + 4) + e0], x1 = st[r * (D + 4) + e1];
-        if (mode != GN_ROPE_NONE) {
-            float c, s;
-            rope_cs(row0 + r, i, D, theta, c, s);
-            const float y0 = x0 * c + x1 * s, y1 = -x0 * s + x1 * c;  // R^T
-            x0 = y0; x1 = y1;
-        }
-        g[(size_t)r * D + e0] = f2bf(x0);
-        g[(size_t)r * D + e1] = f2bf(x1);
-    }
-}
-
-// scatter a wave's 32x32 accumulator tile (rows r0.., cols c0..) into an fp32 LDS tile
-__device__ __forceinline__ void stage_acc(float* st, int pitch, int r0, int c0, const f32x16_t& a,
-                                          float mul) {
+__device__ __forceinline__ bf16x8_t frag_rows(const bf16_t* t, int m0, int ks) {
     const int lane = threadIdx.x & 63;
-    const int col = c0 + (lane & 31), rq = (lane >> 5) * 4;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) st[(r0 + 8 * (r >> 2) + rq + (r & 3)) * pitch + col] = a[r] * mul;
+    const int r = m0 + (lane & 31);
+    return ld_frag16(t + r * D + (((2 * ks + (lane >> 5)) ^ tswz<D>(r)) << 3));
 }
 
+// Fragment whose 32 columns are d = n0 .. n0+31 and whose k runs along tile rows:
+// lane l -> column n0 + l%32, rows kb + 4(l/32) + {0..3} then kb + 8 + 4(l/32) + {0..3}.
+// With kb = 32i + 16p these are exactly the rows (queries or keys) that elements
+// 8p .. 8p+7 of a 32x32 accumulator tile i hold, so a P or dS accumulator converts to an
+// MFMA operand in registers, without going through LDS.
 template <int D>
-struct DkdvSmem {
-    bf16_t K[64 * (D + 8)], V[64 * (D + 8)];
-    union {
-        struct {
-            bf16_t Q[64 * (D + 8)], dO[64 * (D + 8)];
-        } n;
-        float stage[64 * (D + 4)];
-    } u;
-    bf16_t Qt[D * 72], dOt[D * 72];
-    bf16_t Pt[64 * 72], dSt[64 * 72];
-    float L[64], Dr[64];
+__device__ __forceinline__ bf16x8_t frag_cols(const bf16_t* t, int kb, int n0) {
+    const int lane = threadIdx.x & 63, s = lane & 15;
+    const int col = n0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+    const int r0 = kb + 4 * (lane >> 5) + (s >> 2), r1 = r0 + 8;
+    const int c = col >> 3, w = col & 7;
+    return ld_tr_pair(t + r0 * D + ((c ^ tswz<D>(r0)) << 3) + w,
+                      t + r1 * D + ((c ^ tswz<D>(r1)) << 3) + w);
+}
+
+// scatter a wave's 32 x D fp32 accumulators (NT tiles of 32 columns) into its LDS strip
+template <int D, int NT>
+__device__ __forceinline__ void strip_acc(float* st, const f32x16_t (&a)[NT]) {
+    const int lane = threadIdx.x & 63, rq = (lane >> 5) * 4;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            st[(8 * (r >> 2) + rq + (r & 3)) * (D + 4) + 32 * t + (lane & 31)] = a[t][r];
+}
+
+__device__ __forceinline__ void rot_t(float& x0, float& x1, float2 cs) {
+    const float y0 = x0 * cs.x + x1 * cs.y, y1 = x1 * cs.x - x0 * cs.y;  // R^T
+    x0 = y0;
+    x1 = y1;
+}
+
+// Store a wave's 32 staged rows (sequence positions row0 ..) as bf16, times `mul`, with
+// the inverse rotation of `mode`.  Each lane moves chunk c and its partner c + D/16
+// (8 columns each), which holds every RoPE pair of either layout.
+template <int D>
+__device__ __forceinline__ void store_rows(const float* st, bf16_t* __restrict__ g, int row0,
+                                           int S, float mul, int mode,
+                                           const float2* __restrict__ cs) {
+    constexpr int HC = D / 16, P = D + 4;
+    const int lane = threadIdx.x & 63;
+#pragma unroll 2
+    for (int idx = lane; idx < 32 * HC; idx += 64) {
+        const int r = idx / HC, c = idx % HC, row = row0 + r;
+        if (row >= S) continue;
+        float x[8], y[8];
+        const float4* sx = reinterpret_cast<const float4*>(st + r * P + 8 * c);
+        const float4* sy = reinterpret_cast<const float4*>(st + r * P + 8 * (c + HC));
+        const float4 a0 = sx[0], a1 = sx[1], b0 = sy[0], b1 = sy[1];
+        x[0] = a0.x; x[1] = a0.y; x[2] = a0.z; x[3] = a0.w;
+        x[4] = a1.x; x[5] = a1.y; x[6] = a1.z; x[7] = a1.w;
+        y[0] = b0.x; y[1] = b0.y; y[2] = b0.z; y[3] = b0.w;
+        y[4] = b1.x; y[5] = b1.y; y[6] = b1.z; y[7] = b1.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { x[e] *= mul; y[e] *= mul; }
+        const float2* t = cs + (size_t)row * (D / 2);
+        if (mode == GN_ROPE_INTERLEAVED) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                rot_t(x[2 * e], x[2 * e + 1], t[4 * c + e]);
+                rot_t(y[2 * e], y[2 * e + 1], t[4 * (c + HC) + e]);
+            }
+        } else if (mode == GN_ROPE_HALF) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) rot_t(x[e], y[e], t[8 * c + e]);
+        }
+        bf16_t* o = g + (size_t)row * D;
+        *reinterpret_cast<bf16x8_t*>(o + 8 * c) = to_bf16x8(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
+        *reinterpret_cast<bf16x8_t*>(o + 8 * (c + HC)) = to_bf16x8(y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]);
+    }
+}
+
+template <int D, int STAGES>
+struct DkdvCfg {
+    static constexpr int TB = tile_bytes(D);
+    static constexpr int STAGE = 2 * TB + 512;  // Q tile, dO tile, 64 x L, 64 x D_i
+    static constexpr int DMA_PER_TILE = 2 * (D / 32) + 1;
+    static constexpr int KV = 4 * TB;           // the block's 128 K rows and 128 V rows
+    static constexpr int EPI = 4 * 32 * (D + 4) * 4;
+    static constexpr int LDS = STAGES * STAGE + KV > EPI ? STAGES * STAGE + KV : EPI;
 };
 
-template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv(
+// dK, dV for 128 keys (four waves x 32 keys) of one (batch, head); loops over the query
+// tiles of 64 that can see those keys.  Per query tile and wave:
+//   S = Q K^T, dP = dO V^T        (A = Q / dO rows from LDS, B = K / V fragments in VGPRs)
+//   P = exp2(S scale log2e - L log2e), dS = P (dP - D_i)    (masked on edge tiles)
+//   dV += P^T dO, dK += dS^T Q    (A = P / dS straight from the accumulators,
+//                                  B = dO / Q columns by transpose reads)
+// The next tiles' Q, dO, L, D_i arrive by LDS DMA while the current one is computed.
+template <int D, int STAGES>
+__global__ __launch_bounds__(256) void attn_dkdv_mfma(
     const bf16_t* __restrict__ Qr, const bf16_t* __restrict__ Kr, const bf16_t* __restrict__ V,
-    const bf16_t* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Di,
-    bf16_t* __restrict__ dK, bf16_t* __restrict__ dV, int S, float scale, int causal,
-    int rope_mode, float theta) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    DkdvSmem<D>& sm = *reinterpret_cast<DkdvSmem<D>*>(smem_raw);
-    constexpr int NT = D / 64;  // 32-wide d tiles per wave in dK / dV
-    const int bh = blockIdx.y, j0 = blockIdx.x * 64;
+    const bf16_t* __restrict__ dO, const float* __restrict__ Lsc, const float* __restrict__ Di,
+    const float2* __restrict__ cs, bf16_t* __restrict__ dK, bf16_t* __restrict__ dV, int S,
+    int Spad, float scale, int causal, int rope_mode) {
+    using C = DkdvCfg<D, STAGES>;
+    extern __shared__ __align__(1024) unsigned char smem[];
+    constexpr int NT = D / 32, KS = D / 16;
+    const int bh = blockIdx.x, j0 = blockIdx.y * 128;
     const size_t base = (size_t)bh * S * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wr = wave >> 1, wc = wave & 1;
-    const int fr = lane & 31, fk = (lane >> 5) * 8, rq = (lane >> 5) * 4;
+    const int lane = threadIdx.x & 63, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int kw0 = j0 + wave * 32, key = kw0 + (lane & 31);
+    const float c2 = scale * 1.4426950408889634f;
 
-    load_nat<D>(sm.K, Kr + base + (size_t)j0 * D, S - j0);
-    load_nat<D>(sm.V, V + base + (size_t)j0 * D, S - j0);
-
+    // the block's K and V rows stay in LDS (after the stages) for the whole block
+    const bf16_t* sKb = reinterpret_cast<const bf16_t*>(smem + STAGES * C::STAGE);
+    const bf16_t* sVb = sKb + 128 * D;
     f32x16_t aV[NT], aK[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) { zero16(aV[t]); zero16(aK[t]); }
 
-    const int nqb = (S + 63) / 64;
-    for (int qb = causal ? blockIdx.x : 0; qb < nqb; ++qb) {
-        const int q0 = qb * 64;
-        __syncthreads();
-        load_nat<D>(sm.u.n.Q, Qr + base + (size_t)q0 * D, S - q0);
-        load_nat<D>(sm.u.n.dO, dO + base + (size_t)q0 * D, S - q0);
-        load_tr<D>(sm.Qt, Qr + base + (size_t)q0 * D, S - q0);
-        load_tr<D>(sm.dOt, dO + base + (size_t)q0 * D, S - q0);
-        if (threadIdx.x < 64) {
-            const int q = q0 + threadIdx.x;
-            sm.L[threadIdx.x] = q < S ? LSE[(size_t)bh * S + q] : 0.f;
-            sm.Dr[threadIdx.x] = q < S ? Di[(size_t)bh * S + q] : 0.f;
+    const uint32_t lds0 = lds_addr(smem);
+    const int t0 = causal ? j0 / 64 : 0;
+    const int T = (S + 63) / 64 - t0;
+    auto issue = [&](int it) {
+        const int q0 = (t0 + it) * 64;
+        const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
+        dma_tile<D>(Qr + base, q0, S, sb);
+        dma_tile<D>(dO + base, q0, S, sb + C::TB);
+        // L (waves 0, 1) and D_i (waves 2, 3): 32 floats per wave, 8 lanes x 16 bytes
+        if (lane < 8) {
+            const float* src = (wave < 2 ? Lsc : Di) + (size_t)bh * Spad + q0 + 32 * (wave & 1) + 4 * lane;
+            dma16(src, __builtin_amdgcn_readfirstlane(sb + 2 * C::TB + 128 * wave));
         }
-        __syncthreads();
-        // S and dP for this wave's 32 (q) x 32 (key) tile
-        f32x16_t s, dp;
-        zero16(s);
-        zero16(dp);
+    };
+
+    {
+        const uint32_t kv = lds0 + STAGES * C::STAGE;
+        dma_tile<D>(Kr + base, j0, S, kv);
+        dma_tile<D>(Kr + base, j0 + 64, S, kv + C::TB);
+        dma_tile<D>(V + base, j0, S, kv + 2 * C::TB);
+        dma_tile<D>(V + base, j0 + 64, S, kv + 3 * C::TB);
+    }
+    issue(0);
+    if (STAGES > 2 && T > 1) issue(1);
+    for (int it = 0; it < T; ++it) {
+        if (STAGES > 2 && it + 1 < T) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::DMA_PER_TILE));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();  // tile `it` is in LDS for every wave; the buffer refilled next is free
+        if (it + STAGES - 1 < T) issue(it + STAGES - 1);
+        const int q0 = (t0 + it) * 64;
+        const unsigned char* sb = smem + (it % STAGES) * C::STAGE;
+        const bf16_t* sQ = reinterpret_cast<const bf16_t*>(sb);
+        const bf16_t* sG = reinterpret_cast<const bf16_t*>(sb + C::TB);
+        const float* sL = reinterpret_cast<const float*>(sb + 2 * C::TB);
+        const float* sD = sL + 64;
+        if (kw0 >= S || (causal && kw0 > q0 + 63)) continue;  // every key of the wave masked
+        const bool full = kw0 + 31 < S && q0 + 63 < S && (!causal || kw0 + 31 <= q0);
+
+        // the two 32-query halves one after the other (keeps S, dP, P, dS of one half live).
+        // Masked entries get S = -inf, hence P = dS = 0 (L and D_i are finite everywhere,
+        // padding included); only tiles on the diagonal or the sequence end evaluate it.
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
-            const int k = ks * 16 + fk;
-            s = mfma(afrag(&sm.u.n.Q[(wr * 32 + fr) * (D + 8) + k]), afrag(&sm.K[(wc * 32 + fr) * (D + 8) + k]), s);
-            dp = mfma(afrag(&sm.u.n.dO[(wr * 32 + fr) * (D + 8) + k]), afrag(&sm.V[(wc * 32 + fr) * (D + 8) + k]), dp);
-        }
-        const int keyl = wc * 32 + fr, key = j0 + keyl;
+        for (int i = 0; i < 2; ++i) {
+            // S, dP: the fragments of k-step ks+1 are requested before the MFMAs of ks; the
+            // scheduling fences keep the compiler from hoisting every LDS read up front
+            f32x16_t s, dp;
+            zero16(s);
+            zero16(dp);
+            bf16x8_t fa[2][2];
+            fa[0][0] = frag_rows<D>(sQ, 32 * i, 0);
+            fa[0][1] = frag_rows<D>(sG, 32 * i, 0);
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-            float pv[4], dv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = g4 * 4 + e;
-                const int ql = wr * 32 + 8 * g4 + rq + e, q = q0 + ql;
-                const bool ok = q < S && key < S && (!causal || key <= q);
-                const float p = ok ? __expf(s[r] * scale - sm.L[ql]) : 0.f;
-                pv[e] = p;
-                dv[e] = p * (dp[r] - sm.Dr[ql]);
+            for (int ks = 0; ks < KS; ++ks) {
+                if (ks + 1 < KS) {
+                    fa[(ks + 1) & 1][0] = frag_rows<D>(sQ, 32 * i, ks + 1);
+                    fa[(ks + 1) & 1][1] = frag_rows<D>(sG, 32 * i, ks + 1);
+                }
+                s = mfma32(fa[ks & 1][0], frag_rows<D>(sKb, 32 * wave, ks), s);
+                dp = mfma32(fa[ks & 1][1], frag_rows<D>(sVb, 32 * wave, ks), dp);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            const int ql0 = wr * 32 + 8 * g4 + rq;
-            uint2 pp, dd;
-            pp.x = pack_bf2(pv[0], pv[1]); pp.y = pack_bf2(pv[2], pv[3]);
-            dd.x = pack_bf2(dv[0], dv[1]); dd.y = pack_bf2(dv[2], dv[3]);
-            *reinterpret_cast<uint2*>(&sm.Pt[keyl * 72 + ql0]) = pp;
-            *reinterpret_cast<uint2*>(&sm.dSt[keyl * 72 + ql0]) = dd;
-        }
-        __syncthreads();
-        // dV[key][d] += P^T dO ; dK[key][d] += dS^T Q   (contraction over the 64 queries)
+            // the first transpose fragments of the dV / dK step are in flight during the exp work
+            bf16x8_t fb[2][2];
+            fb[0][0] = frag_cols<D>(sG, 32 * i, 0);
+            fb[0][1] = frag_cols<D>(sQ, 32 * i, 0);
+            if (!full) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int k = ks * 16 + fk;
-            const bf16x8_t ap = afrag(&sm.Pt[(wr * 32 + fr) * 72 + k]);
-            const bf16x8_t ad = afrag(&sm.dSt[(wr * 32 + fr) * 72 + k]);
+                for (int r = 0; r < 16; ++r) {
+                    const int q = q0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const bool ok = q < S && key < S && (!causal || key <= q);
+                    s[r] = ok ? s[r] : -INFINITY;
+                }
+            }
+            float pv[16], dv[16];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const int dcol = wc * 32 + t * 64 + fr;
-                aV[t] = mfma(ap, afrag(&sm.dOt[dcol * 72 + k]), aV[t]);
-                aK[t] = mfma(ad, afrag(&sm.Qt[dcol * 72 + k]), aK[t]);
+            for (int g = 0; g < 4; ++g) {
+                const int ql = 32 * i + 8 * g + 4 * h;
+                const float4 L4 = *reinterpret_cast<const float4*>(sL + ql);
+                const float4 D4 = *reinterpret_cast<const float4*>(sD + ql);
+                const float Lv[4] = {L4.x, L4.y, L4.z, L4.w}, Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g + e;
+                    pv[r] = __builtin_amdgcn_exp2f(s[r] * c2 - Lv[e]);
+                    dv[r] = pv[r] * (dp[r] - Dv[e]);
+                }
+            }
+            bf16x8_t pa[2], da[2];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                pa[p] = to_bf16x8(pv[8 * p], pv[8 * p + 1], pv[8 * p + 2], pv[8 * p + 3],
+                                  pv[8 * p + 4], pv[8 * p + 5], pv[8 * p + 6], pv[8 * p + 7]);
+                da[p] = to_bf16x8(dv[8 * p], dv[8 * p + 1], dv[8 * p + 2], dv[8 * p + 3],
+                                  dv[8 * p + 4], dv[8 * p + 5], dv[8 * p + 6], dv[8 * p + 7]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 2 * NT; ++j) {  // step j: d tile j/2, query rows 16 (j%2)
+                if (j + 1 < 2 * NT) {
+                    const int kb = 32 * i + 16 * ((j + 1) & 1), n0 = 32 * ((j + 1) >> 1);
+                    fb[(j + 1) & 1][0] = frag_cols<D>(sG, kb, n0);
+                    fb[(j + 1) & 1][1] = frag_cols<D>(sQ, kb, n0);
+                }
+                aV[j >> 1] = mfma32(pa[j & 1], fb[j & 1][0], aV[j >> 1]);
+                aK[j >> 1] = mfma32(da[j & 1], fb[j & 1][1], aK[j >> 1]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
-    // epilogue: dV (no rotation), then dK * scale with R^T
+
+    // epilogue: each wave stages its 32 x D rows (fp32) in a private LDS strip
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < NT; ++t) stage_acc(sm.u.stage, D + 4, wr * 32, wc * 32 + t * 64, aV[t], 1.f);
+    float* st = reinterpret_cast<float*>(smem) + wave * 32 * (D + 4);
+    strip_acc<D, NT>(st, aV);
     __syncthreads();
-    store_rotated<D>(sm.u.stage, dV + base + (size_t)j0 * D, j0, S - j0, GN_ROPE_NONE, theta);
+    store_rows<D>(st, dV + base, kw0, S, 1.f, GN_ROPE_NONE, cs);
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < NT; ++t) stage_acc(sm.u.stage, D + 4, wr * 32, wc * 32 + t * 64, aK[t], scale);
+    strip_acc<D, NT>(st, aK);
     __syncthreads();
-    store_rotated<D>(sm.u.stage, dK + base + (size_t)j0 * D, j0, S - j0, rope_mode, theta);
+    store_rows<D>(st, dK + base, kw0, S, scale, rope_mode, cs);
 }
 
-template <int D>
-struct DqSmem {
-    bf16_t Q[64 * (D + 8)], dO[64 * (D + 8)];
-    union {
-        struct {
-            bf16_t K[64 * (D + 8)], V[64 * (D + 8)];
-        } n;
-        float stage[64 * (D + 4)];
-    } u;
-    bf16_t Kt[D * 72];
-    bf16_t dS[64 * 72];
-    float L[64], Dr[64];
+template <int D, int STAGES>
+struct DqCfg {
+    static constexpr int TB = tile_bytes(D);
+    static constexpr int STAGE = 2 * TB;  // K tile, V tile
+    static constexpr int DMA_PER_TILE = 2 * (D / 32);
+    static constexpr int EPI = 4 * 32 * (D + 4) * 4;
+    static constexpr int LDS = STAGES * STAGE > EPI ? STAGES * STAGE : EPI;
 };
 
-template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dq(
+// dQ for 128 queries (four waves x 32 queries) of one (batch, head); loops over the key
+// tiles of 64 those queries can see.  Per key tile and wave:
+//   S^T = K Q^T, dP^T = V dO^T    (A = K / V rows from LDS, B = Q / dO fragments in VGPRs)
+//   dS^T = P^T (dP^T - D_i)       (each lane owns one query: its L and D_i are scalars)
+//   dQ += dS K                    (A = dS from the accumulators, B = K columns by
+//                                  transpose reads)
+template <int D, int STAGES>
+__global__ __launch_bounds__(256) void attn_dq_mfma(
     const bf16_t* __restrict__ Qr, const bf16_t* __restrict__ Kr, const bf16_t* __restrict__ V,
-    const bf16_t* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Di,
-    bf16_t* __restrict__ dQ, int S, float scale, int causal, int rope_mode, float theta) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    DqSmem<D>& sm = *reinterpret_cast<DqSmem<D>*>(smem_raw);
-    constexpr int NT = D / 64;
-    const int bh = blockIdx.y, i0 = blockIdx.x * 64;
+    const bf16_t* __restrict__ dO, const float* __restrict__ Lsc, const float* __restrict__ Di,
+    const float2* __restrict__ cs, bf16_t* __restrict__ dQ, int S, int Spad, float scale,
+    int causal, int rope_mode) {
+    using C = DqCfg<D, STAGES>;
+    extern __shared__ __align__(1024) unsigned char smem[];
+    constexpr int NT = D / 32, KS = D / 16;
+    const int nqb = (S + 127) / 128;
+    const int bh = blockIdx.x, i0 = (nqb - 1 - (int)blockIdx.y) * 128;  // longest rows first
     const size_t base = (size_t)bh * S * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wr = wave >> 1, wc = wave & 1;
-    const int fr = lane & 31, fk = (lane >> 5) * 8, rq = (lane >> 5) * 4;
+    const int lane = threadIdx.x & 63, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int qw0 = i0 + wave * 32, q = qw0 + (lane & 31), qc = min(q, S - 1);
+    const float c2 = scale * 1.4426950408889634f;
 
-    load_nat<D>(sm.Q, Qr + base + (size_t)i0 * D, S - i0);
-    load_nat<D>(sm.dO, dO + base + (size_t)i0 * D, S - i0);
-    if (threadIdx.x < 64) {
-        const int q = i0 + threadIdx.x;
-        sm.L[threadIdx.x] = q < S ? LSE[(size_t)bh * S + q] : 0.f;
-        sm.Dr[threadIdx.x] = q < S ? Di[(size_t)bh * S + q] : 0.f;
+    bf16x8_t qf[KS], of[KS];
+    {
+        const size_t rq = base + (size_t)qc * D + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            qf[ks] = ld_frag16(Qr + rq + 16 * ks);
+            of[ks] = ld_frag16(dO + rq + 16 * ks);
+        }
     }
+    const float lq = Lsc[(size_t)bh * Spad + qc], dq = Di[(size_t)bh * Spad + qc];
     f32x16_t aQ[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) zero16(aQ[t]);
 
-    const int nkb = (S + 63) / 64;
-    const int kb_end = causal ? (int)blockIdx.x : nkb - 1;
-    for (int kb = 0; kb <= kb_end; ++kb) {
-        const int k0 = kb * 64;
+    const uint32_t lds0 = lds_addr(smem);
+    const int kend = causal ? min(S, i0 + 128) : S;
+    const int T = (kend + 63) / 64;
+    auto issue = [&](int it) {
+        const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
+        dma_tile<D>(Kr + base, it * 64, S, sb);
+        dma_tile<D>(V + base, it * 64, S, sb + C::TB);
+    };
+
+    issue(0);
+    if (STAGES > 2 && T > 1) issue(1);
+    for (int it = 0; it < T; ++it) {
+        if (STAGES > 2 && it + 1 < T) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::DMA_PER_TILE));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
-        load_nat<D>(sm.u.n.K, Kr + base + (size_t)k0 * D, S - k0);
-        load_nat<D>(sm.u.n.V, V + base + (size_t)k0 * D, S - k0);
-        load_tr<D>(sm.Kt, Kr + base + (size_t)k0 * D, S - k0);
-        __syncthreads();
-        // S^T and dP^T for this wave's 32 (key) x 32 (q) tile
-        f32x16_t st, dpt;
-        zero16(st);
-        zero16(dpt);
+        if (it + STAGES - 1 < T) issue(it + STAGES - 1);
+        const int k0 = it * 64;
+        const unsigned char* sb = smem + (it % STAGES) * C::STAGE;
+        const bf16_t* sK = reinterpret_cast<const bf16_t*>(sb);
+        const bf16_t* sV = reinterpret_cast<const bf16_t*>(sb + C::TB);
+        if (qw0 >= S || (causal && k0 > qw0 + 31)) continue;  // every key masked for the wave
+        const bool full = qw0 + 31 < S && k0 + 63 < S && (!causal || k0 + 63 <= qw0);
+
+        // masked entries get S = -inf, hence dS = 0
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
-            const int k = ks * 16 + fk;
-            st = mfma(afrag(&sm.u.n.K[(wr * 32 + fr) * (D + 8) + k]), afrag(&sm.Q[(wc * 32 + fr) * (D + 8) + k]), st);
-            dpt = mfma(afrag(&sm.u.n.V[(wr * 32 + fr) * (D + 8) + k]), afrag(&sm.dO[(wc * 32 + fr) * (D + 8) + k]), dpt);
-        }
-        const int ql = wc * 32 + fr, q = i0 + ql;
-        const float lq = sm.L[ql], dq = sm.Dr[ql];
+        for (int i = 0; i < 2; ++i) {
+            f32x16_t s, dp;
+            zero16(s);
+            zero16(dp);
+            bf16x8_t fa[2][2];
+            fa[0][0] = frag_rows<D>(sK, 32 * i, 0);
+            fa[0][1] = frag_rows<D>(sV, 32 * i, 0);
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-            float dv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = g4 * 4 + e;
-                const int key = k0 + wr * 32 + 8 * g4 + rq + e;
-                const bool ok = q < S && key < S && (!causal || key <= q);
-                const float p = ok ? __expf(st[r] * scale - lq) : 0.f;
-                dv[e] = p * (dpt[r] - dq);
+            for (int ks = 0; ks < KS; ++ks) {
+                if (ks + 1 < KS) {
+                    fa[(ks + 1) & 1][0] = frag_rows<D>(sK, 32 * i, ks + 1);
+                    fa[(ks + 1) & 1][1] = frag_rows<D>(sV, 32 * i, ks + 1);
+                }
+                s = mfma32(fa[ks & 1][0], qf[ks], s);
+                dp = mfma32(fa[ks & 1][1], of[ks], dp);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            uint2 dd;
-            dd.x = pack_bf2(dv[0], dv[1]);
-            dd.y = pack_bf2(dv[2], dv[3]);
-            *reinterpret_cast<uint2*>(&sm.dS[ql * 72 + wr * 32 + 8 * g4 + rq]) = dd;
-        }
-        __syncthreads();
-        // dQ[q][d] += dS[q][key] K[key][d]
+            bf16x8_t fb[2];
+            fb[0] = frag_cols<D>(sK, 32 * i, 0);
+            if (!full) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int k = ks * 16 + fk;
-            const bf16x8_t a = afrag(&sm.dS[(wr * 32 + fr) * 72 + k]);
+                for (int r = 0; r < 16; ++r) {
+                    const int kk = k0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const bool ok = q < S && kk < S && (!causal || kk <= q);
+                    s[r] = ok ? s[r] : -INFINITY;
+                }
+            }
+            float dv[16];
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-                aQ[t] = mfma(a, afrag(&sm.Kt[(wc * 32 + t * 64 + fr) * 72 + k]), aQ[t]);
+            for (int r = 0; r < 16; ++r)
+                dv[r] = __builtin_amdgcn_exp2f(s[r] * c2 - lq) * (dp[r] - dq);
+            bf16x8_t da[2];
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+                da[p] = to_bf16x8(dv[8 * p], dv[8 * p + 1], dv[8 * p + 2], dv[8 * p + 3],
+                                  dv[8 * p + 4], dv[8 * p + 5], dv[8 * p + 6], dv[8 * p + 7]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 2 * NT; ++j) {
+                if (j + 1 < 2 * NT)
+                    fb[(j + 1) & 1] = frag_cols<D>(sK, 32 * i + 16 * ((j + 1) & 1), 32 * ((j + 1) >> 1));
+                aQ[j >> 1] = mfma32(da[j & 1], fb[j & 1], aQ[j >> 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
+
     __syncthreads();
+    float* st = reinterpret_cast<float*>(smem) + wave * 32 * (D + 4);
+    strip_acc<D, NT>(st, aQ);
+    __syncthreads();
+    store_rows<D>(st, dQ + base, qw0, S, scale, rope_mode, cs);
+}
+
+// cos/sin table [S][D/2] of the RoPE angles (pair i at position p)
+__global__ __launch_bounds__(256) void rope_table(float2* __restrict__ cs, int S, int D,
+                                                  float theta) {
+    const int half = D / 2;
+    for (int64_t idx = blockIdx.x * (int64_t)256 + threadIdx.x; idx < (int64_t)S * half;
+         idx += (int64_t)gridDim.x * 256) {
+        float c, s;
+        rope_cs((int)(idx / half), (int)(idx % half), D, theta, c, s);
+        cs[idx] = make_float2(c, s);
+    }
+}
+
+// Pre-pass of the MFMA path, D/8 lanes per row: rotated Q and K (bf16), D_i = rowsum(dO*O)
+// and L log2(e), both into [B*H][Spad] arrays whose padding the kernels never unmask.
+template <int D>
+__global__ __launch_bounds__(256) void attn_prep(
+    const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ dO,
+    const bf16_t* __restrict__ O, const float* __restrict__ LSE, bf16_t* __restrict__ Qr,
+    bf16_t* __restrict__ Kr, float* __restrict__ Lsc, float* __restrict__ Di,
+    const float2* __restrict__ cs, int64_t rows, int S, int Spad, int mode) {
+    constexpr int LPR = D / 8;
+    const int64_t gid = blockIdx.x * (int64_t)256 + threadIdx.x;
+    const int64_t row = gid / LPR;
+    const int c = (int)(gid % LPR);
+    if (row >= rows) return;  // LPR divides 256: whole row groups leave together
+    const int pos = (int)(row % S);
+    const int64_t bh = row / S;
+    const size_t off = (size_t)row * D + 8 * c;
+    const uint4 o4 = *reinterpret_cast<const uint4*>(O + off);
+    const uint4 g4 = *reinterpret_cast<const uint4*>(dO + off);
+    const uint32_t ow[4] = {o4.x, o4.y, o4.z, o4.w}, gw[4] = {g4.x, g4.y, g4.z, g4.w};
+    float dot = 0.f;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) stage_acc(sm.u.stage, D + 4, wr * 32, wc * 32 + t * 64, aQ[t], scale);
-    __syncthreads();
-    store_rotated<D>(sm.u.stage, dQ + base + (size_t)i0 * D, i0, S - i0, rope_mode, theta);
+    for (int e = 0; e < 4; ++e) {
+        dot += __uint_as_float(ow[e] << 16) * __uint_as_float(gw[e] << 16);
+        dot += __uint_as_float(ow[e] & 0xffff0000u) * __uint_as_float(gw[e] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) dot += __shfl_xor(dot, m);
+    if (c == 0) {
+        Di[(size_t)bh * Spad + pos] = dot;
+        Lsc[(size_t)bh * Spad + pos] = LSE[row] * 1.4426950408889634f;
+        if (pos == S - 1)  // finite padding: masked entries compute exp2(-inf - 0) * (dP - 0)
+            for (int p = S; p < Spad; ++p) Di[(size_t)bh * Spad + p] = Lsc[(size_t)bh * Spad + p] = 0.f;
+    }
+    if (mode == GN_ROPE_NONE) return;
+    const float2* t = cs + (size_t)pos * (D / 2);
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        const uint4 v4 = *reinterpret_cast<const uint4*>((which ? K : Q) + off);
+        const uint32_t vw[4] = {v4.x, v4.y, v4.z, v4.w};
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = __uint_as_float(vw[e] << 16);
+            x[2 * e + 1] = __uint_as_float(vw[e] & 0xffff0000u);
+        }
+        if (mode == GN_ROPE_INTERLEAVED) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float2 r = t[4 * c + e];
+                const float x0 = x[2 * e], x1 = x[2 * e + 1];
+                x[2 * e] = x0 * r.x - x1 * r.y;
+                x[2 * e + 1] = x0 * r.y + x1 * r.x;
+            }
+        } else {  // GN_ROPE_HALF: element e pairs with the same element of chunk c ^ LPR/2
+            const bool lo = c < LPR / 2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float xp = __shfl_xor(x[e], LPR / 2);
+                const float2 r = t[8 * (c % (LPR / 2)) + e];
+                x[e] = lo ? x[e] * r.x - xp * r.y : xp * r.y + x[e] * r.x;
+            }
+        }
+        *reinterpret_cast<bf16x8_t*>((which ? Kr : Qr) + off) =
+            to_bf16x8(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
+    }
 }
 
 // ---- SIMT path: one wave per query row (dQ, forward) or key row (dK, dV) ----------------
@@ -509,23 +706,35 @@ struct AttnWs {
     void* Qr;
     void* Kr;
     float* Di;
-    float* acc;  // SIMT path only: fp32 [B*H*S*D]
+    float* Lsc;   // MFMA path: L log2(e), [B*H][Spad]
+    float2* cs;   // MFMA path: RoPE cos/sin table [S][D/2]
+    float* acc;   // SIMT path: fp32 [B*H*S*D]
 };
 
 inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+inline int spad_of(int S) { return (S + 63) / 64 * 64; }
 
-size_t ws_layout(int64_t BHSD, int64_t BHS, size_t esz, bool simt, void* base, AttnWs* w) {
+// mfma: bf16 Qr, Kr; Di, Lsc padded to Spad per (b, h); cos/sin table.
+// simt: esz-sized Qr, Kr; Di; fp32 accumulator.
+size_t ws_layout(int64_t BH, int S, int D, size_t esz, bool mfma, void* base, AttnWs* w) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
         void* p = base ? (char*)base + off : nullptr;
         off += align_up(bytes);
         return p;
     };
+    const int64_t BHSD = BH * S * D;
     AttnWs t{};
     t.Qr = take(BHSD * esz);
     t.Kr = take(BHSD * esz);
-    t.Di = (float*)take(BHS * 4);
-    t.acc = simt ? (float*)take(BHSD * 4) : nullptr;
+    if (mfma) {
+        t.Di = (float*)take(BH * spad_of(S) * 4);
+        t.Lsc = (float*)take(BH * spad_of(S) * 4);
+        t.cs = (float2*)take((size_t)S * (D / 2) * 8);
+    } else {
+        t.Di = (float*)take(BH * S * 4);
+        t.acc = (float*)take(BHSD * 4);
+    }
     if (w) *w = t;
     return off;
 }
@@ -536,24 +745,37 @@ bool allow_lds(F* fn, size_t bytes) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
 }
 
+constexpr int kStagesDkdv = 2, kStagesDq = 3;
+
 template <int D>
-int launch_mfma_bwd(const AttnWs& w, const void* Qp, const void* Kp, const void* V, const void* dO,
-                    const float* LSE, void* dQ, void* dK, void* dV, int BH, int S, float scale,
-                    int causal, int rope_mode, float theta, hipStream_t s) {
-    static const bool ok1 = allow_lds(attn_bwd_dkdv<D>, sizeof(DkdvSmem<D>));
-    static const bool ok2 = allow_lds(attn_bwd_dq<D>, sizeof(DqSmem<D>));
+int launch_mfma_bwd(const AttnWs& w, const void* Q, const void* K, const void* V, const void* O,
+                    const void* dO, const float* LSE, void* dQ, void* dK, void* dV, int BH, int S,
+                    float scale, int causal, int rope_mode, float theta, hipStream_t s) {
+    using C1 = DkdvCfg<D, kStagesDkdv>;
+    using C2 = DqCfg<D, kStagesDq>;
+    static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv>, C1::LDS);
+    static const bool ok2 = allow_lds(attn_dq_mfma<D, kStagesDq>, C2::LDS);
     if (!ok1 || !ok2) {
-        set_error("gn_attn_bwd: cannot reserve LDS (%zu / %zu B)", sizeof(DkdvSmem<D>), sizeof(DqSmem<D>));
+        set_error("gn_attn_bwd: cannot reserve LDS (%d / %d B)", C1::LDS, C2::LDS);
         return GN_E_HIP;
     }
-    const int nb = (S + 63) / 64;
-    dim3 grid(nb, BH);
-    hipLaunchKernelGGL(attn_bwd_dkdv<D>, grid, dim3(256), sizeof(DkdvSmem<D>), s,
-                       (const bf16_t*)Qp, (const bf16_t*)Kp, (const bf16_t*)V, (const bf16_t*)dO,
-                       LSE, w.Di, (bf16_t*)dK, (bf16_t*)dV, S, scale, causal, rope_mode, theta);
-    hipLaunchKernelGGL(attn_bwd_dq<D>, grid, dim3(256), sizeof(DqSmem<D>), s,
-                       (const bf16_t*)Qp, (const bf16_t*)Kp, (const bf16_t*)V, (const bf16_t*)dO,
-                       LSE, w.Di, (bf16_t*)dQ, S, scale, causal, rope_mode, theta);
+    const int64_t rows = (int64_t)BH * S;
+    const int Spad = spad_of(S);
+    if (rope_mode != GN_ROPE_NONE)
+        rope_table<<<grid_for((int64_t)S * (D / 2), 256, 4096), 256, 0, s>>>(w.cs, S, D, theta);
+    const int64_t threads = rows * (D / 8);
+    attn_prep<D><<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(
+        (const bf16_t*)Q, (const bf16_t*)K, (const bf16_t*)dO, (const bf16_t*)O, LSE,
+        (bf16_t*)w.Qr, (bf16_t*)w.Kr, w.Lsc, w.Di, w.cs, rows, S, Spad, rope_mode);
+    const bf16_t* Qp = (const bf16_t*)(rope_mode != GN_ROPE_NONE ? w.Qr : Q);
+    const bf16_t* Kp = (const bf16_t*)(rope_mode != GN_ROPE_NONE ? w.Kr : K);
+    const int nb = (S + 127) / 128;
+    hipLaunchKernelGGL((attn_dkdv_mfma<D, kStagesDkdv>), dim3(BH, nb), dim3(256), C1::LDS, s, Qp,
+                       Kp, (const bf16_t*)V, (const bf16_t*)dO, w.Lsc, w.Di, w.cs, (bf16_t*)dK,
+                       (bf16_t*)dV, S, Spad, scale, causal, rope_mode);
+    hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, Qp, Kp,
+                       (const bf16_t*)V, (const bf16_t*)dO, w.Lsc, w.Di, w.cs, (bf16_t*)dQ, S,
+                       Spad, scale, causal, rope_mode);
     GN_LAUNCH_CHECK("gn_attn_bwd (mfma)");
     return GN_OK;
 }
@@ -566,10 +788,17 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
     const int64_t BH = (int64_t)B * H, rows = BH * S, BHSD = rows * D;
     const bool mfma_ok = sizeof(T) == 2 && (D == 64 || D == 128);
     AttnWs w;
-    const size_t need = ws_layout(BHSD, rows, sizeof(T), !mfma_ok, ws, &w);
+    const size_t need = ws_layout(BH, S, D, sizeof(T), mfma_ok, ws, &w);
     if (!ws || ws_bytes < need) {
         set_error("gn_attn_bwd: workspace %zu B < %zu B", ws_bytes, need);
         return GN_E_WORKSPACE;
+    }
+    if (mfma_ok) {
+        if (D == 64)
+            return launch_mfma_bwd<64>(w, Q, K, V, O, dO, LSE, dQ, dK, dV, (int)BH, S, scale,
+                                       causal, rope_mode, theta, s);
+        return launch_mfma_bwd<128>(w, Q, K, V, O, dO, LSE, dQ, dK, dV, (int)BH, S, scale, causal,
+                                    rope_mode, theta, s);
     }
     const void* Qp = Q;
     const void* Kp = K;
@@ -581,14 +810,6 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
         Kp = w.Kr;
     }
     row_dot<T><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>((const T*)dO, (const T*)O, w.Di, rows, D);
-    GN_LAUNCH_CHECK("gn_attn_bwd (pre-pass)");
-    if (mfma_ok) {
-        if (D == 64)
-            return launch_mfma_bwd<64>(w, Qp, Kp, V, dO, LSE, dQ, dK, dV, (int)BH, S, scale, causal,
-                                       rope_mode, theta, s);
-        return launch_mfma_bwd<128>(w, Qp, Kp, V, dO, LSE, dQ, dK, dV, (int)BH, S, scale, causal,
-                                    rope_mode, theta, s);
-    }
     const unsigned gr = (unsigned)((rows + 3) / 4);
     const unsigned ge = grid_for(rows * (D / 2), 256, 16384);
     attn_bwd_dq_simt<T><<<gr, 256, 0, s>>>((const T*)Qp, (const T*)Kp, (const T*)V, (const T*)dO,
@@ -599,6 +820,7 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
                                              scale, causal);
     unrotate_store<T><<<ge, 256, 0, s>>>(w.acc, (T*)dK, rows, S, D, rope_mode, theta);
     GN_LAUNCH_CHECK("gn_attn_bwd (simt)");
+    (void)BHSD;
     return GN_OK;
 }
 
@@ -609,9 +831,10 @@ using namespace gn;
 
 extern "C" size_t gn_attn_workspace_bytes(int B, int H, int S, int D) {
     if (B <= 0 || H <= 0 || S <= 0 || D <= 0) return 0;
-    const int64_t rows = (int64_t)B * H * S;
-    // sized for the larger (SIMT, fp32) layout so one query covers every dtype
-    return ws_layout(rows * D, rows, 4, true, nullptr, nullptr);
+    // the larger of the two layouts, so one query covers every dtype and path
+    const size_t simt = ws_layout((int64_t)B * H, S, D, 4, false, nullptr, nullptr);
+    const size_t mfma = ws_layout((int64_t)B * H, S, D, 2, true, nullptr, nullptr);
+    return simt > mfma ? simt : mfma;
 }
 
 static int attn_check(const void* Q, const void* K, const void* V, int B, int H, int S, int D,
@@ -655,7 +878,8 @@ extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O,
     hipStream_t s = as_stream(stream);
     const size_t esz = dtype == GN_BF16 ? 2 : 4;
     AttnWs w;
-    const size_t need = ws_layout(rows * D, rows, esz, false, ws, &w);
+    ws_layout((int64_t)B * H, S, D, esz, false, ws, &w);
+    const size_t need = 2 * align_up((size_t)rows * D * esz);  // the forward uses Qr, Kr only
     if (rope_mode != GN_ROPE_NONE && (!ws || ws_bytes < need)) {
         set_error("gn_attn_fwd: workspace %zu B < %zu B", ws_bytes, need);
         return GN_E_WORKSPACE;
