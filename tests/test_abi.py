@@ -39,7 +39,9 @@ def test_python_frontend_lists_every_symbol():
     lib = gn_bwd.lib()
     assert b"gfx950" in lib.gn_version()
     # size queries are pure host arithmetic
-    assert lib.gn_norm_workspace_bytes(4096, 2048) == 2 * 256 * 2048 * 4
+    # two fp32 partial rows per block, one block per 8 rows up to 512 blocks
+    assert lib.gn_norm_workspace_bytes(4096, 2048) == 2 * 512 * 2048 * 4
+    assert lib.gn_norm_workspace_bytes(100, 64) == 2 * 13 * 64 * 4
     assert lib.gn_attn_workspace_bytes(4, 16, 2048, 128) > 0
     assert lib.gn_attn_workspace_bytes(0, 16, 2048, 128) == 0
 
