@@ -94,11 +94,12 @@ template <> __device__ __forceinline__ int tswz<64>(int r) {
 constexpr int tile_bytes(int D) { return 64 * D * 2; }
 
 // DMA rows row0 .. row0+63 of a [S x D] matrix into a swizzled LDS tile (rows past S
-// re-read row S-1; the kernels mask them).  D/32 DMA instructions per wave.
-template <int D>
+// re-read row S-1; the kernels mask them).  D/(8 NW) DMA instructions per wave.
+template <int D, int NW = 4>
 __device__ __forceinline__ void dma_tile(const bf16_t* __restrict__ g, int row0, int S,
                                          uint32_t lds) {
-    constexpr int CPR = D / 8, RPI = 64 / CPR, PER_WAVE = CPR / 4;
+    constexpr int CPR = D / 8, RPI = 64 / CPR, PER_WAVE = CPR / NW;
+    static_assert(PER_WAVE >= 1, "one DMA instruction per wave at least");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int j = 0; j < PER_WAVE; ++j) {
@@ -191,37 +192,41 @@ __device__ __forceinline__ void store_rows(const float* st, bf16_t* __restrict__
     }
 }
 
-template <int D, int STAGES>
+template <int D, int STAGES, int NW>
 struct DkdvCfg {
     static constexpr int TB = tile_bytes(D);
     static constexpr int STAGE = 2 * TB + 512;  // Q tile, dO tile, 64 x L, 64 x D_i
-    static constexpr int DMA_PER_TILE = 2 * (D / 32) + 1;
+    static constexpr int DMA_PER_TILE = 2 * (D / (8 * NW)) + 1;
     static constexpr int KV = 4 * TB;           // the block's 128 K rows and 128 V rows
     static constexpr int EPI = 4 * 32 * (D + 4) * 4;
     static constexpr int LDS = STAGES * STAGE + KV > EPI ? STAGES * STAGE + KV : EPI;
 };
 
-// dK, dV for 128 keys (four waves x 32 keys) of one (batch, head); loops over the query
-// tiles of 64 that can see those keys.  Per query tile and wave:
-//   S = Q K^T, dP = dO V^T        (A = Q / dO rows from LDS, B = K / V fragments in VGPRs)
+// dK, dV for 128 keys of one (batch, head): wave w owns keys 32 (w % 4) ..; loops over the
+// query tiles of 64 that can see those keys.  With NW = 4 each wave takes both 32-query
+// halves of a tile in turn; with NW = 8 waves w and w + 4 take one half each (two waves per
+// SIMD) and add their partial sums at the end.  Per query half and wave:
+//   S = Q K^T, dP = dO V^T        (A = Q / dO rows, B = K / V rows, all from LDS)
 //   P = exp2(S scale log2e - L log2e), dS = P (dP - D_i)    (masked on edge tiles)
 //   dV += P^T dO, dK += dS^T Q    (A = P / dS straight from the accumulators,
 //                                  B = dO / Q columns by transpose reads)
 // The next tiles' Q, dO, L, D_i arrive by LDS DMA while the current one is computed.
-template <int D, int STAGES>
-__global__ __launch_bounds__(256) void attn_dkdv_mfma(
+template <int D, int STAGES, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     const bf16_t* __restrict__ Qr, const bf16_t* __restrict__ Kr, const bf16_t* __restrict__ V,
     const bf16_t* __restrict__ dO, const float* __restrict__ Lsc, const float* __restrict__ Di,
     const float2* __restrict__ cs, bf16_t* __restrict__ dK, bf16_t* __restrict__ dV, int S,
     int Spad, float scale, int causal, int rope_mode) {
-    using C = DkdvCfg<D, STAGES>;
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
+    using C = DkdvCfg<D, STAGES, NW>;
     extern __shared__ __align__(1024) unsigned char smem[];
-    constexpr int NT = D / 32, KS = D / 16;
+    constexpr int NT = D / 32, KS = D / 16, HALVES = NW == 4 ? 2 : 1;
     const int bh = blockIdx.x, j0 = blockIdx.y * 128;
     const size_t base = (size_t)bh * S * D;
     const int lane = threadIdx.x & 63, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    const int kw0 = j0 + wave * 32, key = kw0 + (lane & 31);
+    const int kg = wave & 3, half0 = NW == 4 ? 0 : wave >> 2;
+    const int kw0 = j0 + kg * 32, key = kw0 + (lane & 31);
     const float c2 = scale * 1.4426950408889634f;
 
     // the block's K and V rows stay in LDS (after the stages) for the whole block
@@ -237,21 +242,23 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(
     auto issue = [&](int it) {
         const int q0 = (t0 + it) * 64;
         const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
-        dma_tile<D>(Qr + base, q0, S, sb);
-        dma_tile<D>(dO + base, q0, S, sb + C::TB);
-        // L (waves 0, 1) and D_i (waves 2, 3): 32 floats per wave, 8 lanes x 16 bytes
-        if (lane < 8) {
-            const float* src = (wave < 2 ? Lsc : Di) + (size_t)bh * Spad + q0 + 32 * (wave & 1) + 4 * lane;
-            dma16(src, __builtin_amdgcn_readfirstlane(sb + 2 * C::TB + 128 * wave));
+        dma_tile<D, NW>(Qr + base, q0, S, sb);
+        dma_tile<D, NW>(dO + base, q0, S, sb + C::TB);
+        // 64 L values then 64 D_i values: one DMA instruction per wave
+        constexpr int LANES = 32 / NW;  // 16-byte pieces per wave (32 pieces in all)
+        if (lane < LANES) {
+            const int piece = wave * LANES + lane;  // 0..15: L, 16..31: D_i
+            const float* src = (piece < 16 ? Lsc : Di) + (size_t)bh * Spad + q0 + 4 * (piece & 15);
+            dma16(src, __builtin_amdgcn_readfirstlane(sb + 2 * C::TB + 16 * LANES * wave));
         }
     };
 
     {
         const uint32_t kv = lds0 + STAGES * C::STAGE;
-        dma_tile<D>(Kr + base, j0, S, kv);
-        dma_tile<D>(Kr + base, j0 + 64, S, kv + C::TB);
-        dma_tile<D>(V + base, j0, S, kv + 2 * C::TB);
-        dma_tile<D>(V + base, j0 + 64, S, kv + 3 * C::TB);
+        dma_tile<D, NW>(Kr + base, j0, S, kv);
+        dma_tile<D, NW>(Kr + base, j0 + 64, S, kv + C::TB);
+        dma_tile<D, NW>(V + base, j0, S, kv + 2 * C::TB);
+        dma_tile<D, NW>(V + base, j0 + 64, S, kv + 3 * C::TB);
     }
     issue(0);
     if (STAGES > 2 && T > 1) issue(1);
@@ -269,11 +276,12 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(
         if (kw0 >= S || (causal && kw0 > q0 + 63)) continue;  // every key of the wave masked
         const bool full = kw0 + 31 < S && q0 + 63 < S && (!causal || kw0 + 31 <= q0);
 
-        // the two 32-query halves one after the other (keeps S, dP, P, dS of one half live).
-        // Masked entries get S = -inf, hence P = dS = 0 (L and D_i are finite everywhere,
-        // padding included); only tiles on the diagonal or the sequence end evaluate it.
+        // 32-query halves (keeps S, dP, P, dS of one half live).  Masked entries get
+        // S = -inf, hence P = dS = 0 (L and D_i are finite everywhere, padding included);
+        // only tiles on the diagonal or the sequence end evaluate the mask.
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int hh = 0; hh < HALVES; ++hh) {
+            const int i = half0 + hh;
             // S, dP: the fragments of k-step ks+1 are requested before the MFMAs of ks; the
             // scheduling fences keep the compiler from hoisting every LDS read up front
             f32x16_t s, dp;
@@ -288,8 +296,8 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(
                     fa[(ks + 1) & 1][0] = frag_rows<D>(sQ, 32 * i, ks + 1);
                     fa[(ks + 1) & 1][1] = frag_rows<D>(sG, 32 * i, ks + 1);
                 }
-                s = mfma32(fa[ks & 1][0], frag_rows<D>(sKb, 32 * wave, ks), s);
-                dp = mfma32(fa[ks & 1][1], frag_rows<D>(sVb, 32 * wave, ks), dp);
+                s = mfma32(fa[ks & 1][0], frag_rows<D>(sKb, 32 * kg, ks), s);
+                dp = mfma32(fa[ks & 1][1], frag_rows<D>(sVb, 32 * kg, ks), dp);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // the first transpose fragments of the dV / dK step are in flight during the exp work
@@ -341,16 +349,25 @@ __global__ __launch_bounds__(256) void attn_dkdv_mfma(
         }
     }
 
-    // epilogue: each wave stages its 32 x D rows (fp32) in a private LDS strip
-    __syncthreads();
-    float* st = reinterpret_cast<float*>(smem) + wave * 32 * (D + 4);
-    strip_acc<D, NT>(st, aV);
-    __syncthreads();
-    store_rows<D>(st, dV + base, kw0, S, 1.f, GN_ROPE_NONE, cs);
-    __syncthreads();
-    strip_acc<D, NT>(st, aK);
-    __syncthreads();
-    store_rows<D>(st, dK + base, kw0, S, scale, rope_mode, cs);
+    // epilogue: the key group's 32 x D rows (fp32) go through a private LDS strip; with
+    // eight waves the second-half wave deposits its partial sums there first
+    float* st = reinterpret_cast<float*>(smem) + kg * 32 * (D + 4);
+    auto finish = [&](f32x16_t (&acc)[NT], bf16_t* out, float mul, int mode) {
+        __syncthreads();
+        if (NW == 4 || half0 == 1) strip_acc<D, NT>(st, acc);
+        __syncthreads();
+        if (NW == 8 && half0 == 0) {
+            const int rq = (lane >> 5) * 4;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    st[(8 * (r >> 2) + rq + (r & 3)) * (D + 4) + 32 * t + (lane & 31)] += acc[t][r];
+        }
+        if (half0 == 0) store_rows<D>(st, out + base, kw0, S, mul, mode, cs);
+    };
+    finish(aV, dV, 1.f, GN_ROPE_NONE);
+    finish(aK, dK, scale, rope_mode);
 }
 
 template <int D, int STAGES>
@@ -499,15 +516,22 @@ __global__ __launch_bounds__(256) void attn_prep(
     bf16_t* __restrict__ Kr, float* __restrict__ Lsc, float* __restrict__ Di,
     const float2* __restrict__ cs, int64_t rows, int S, int Spad, int mode) {
     constexpr int LPR = D / 8;
-    const int64_t gid = blockIdx.x * (int64_t)256 + threadIdx.x;
-    const int64_t row = gid / LPR;
+    const unsigned gid = blockIdx.x * 256u + threadIdx.x;  // rows * LPR < 2^31 (host check)
+    const unsigned row = gid / LPR;
     const int c = (int)(gid % LPR);
-    if (row >= rows) return;  // LPR divides 256: whole row groups leave together
-    const int pos = (int)(row % S);
-    const int64_t bh = row / S;
+    if (row >= (unsigned)rows) return;  // LPR divides 256: whole row groups leave together
+    const int pos = (int)(row % (unsigned)S);
+    const unsigned bh = row / (unsigned)S;
     const size_t off = (size_t)row * D + 8 * c;
+    // every global load up front, so one round trip covers them all
     const uint4 o4 = *reinterpret_cast<const uint4*>(O + off);
     const uint4 g4 = *reinterpret_cast<const uint4*>(dO + off);
+    uint4 qk4[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    if (mode != GN_ROPE_NONE) {
+        qk4[0] = *reinterpret_cast<const uint4*>(Q + off);
+        qk4[1] = *reinterpret_cast<const uint4*>(K + off);
+    }
+    const float lse = c == 0 ? LSE[row] : 0.f;
     const uint32_t ow[4] = {o4.x, o4.y, o4.z, o4.w}, gw[4] = {g4.x, g4.y, g4.z, g4.w};
     float dot = 0.f;
 #pragma unroll
@@ -519,7 +543,7 @@ __global__ __launch_bounds__(256) void attn_prep(
     for (int m = LPR / 2; m >= 1; m >>= 1) dot += __shfl_xor(dot, m);
     if (c == 0) {
         Di[(size_t)bh * Spad + pos] = dot;
-        Lsc[(size_t)bh * Spad + pos] = LSE[row] * 1.4426950408889634f;
+        Lsc[(size_t)bh * Spad + pos] = lse * 1.4426950408889634f;
         if (pos == S - 1)  // finite padding: masked entries compute exp2(-inf - 0) * (dP - 0)
             for (int p = S; p < Spad; ++p) Di[(size_t)bh * Spad + p] = Lsc[(size_t)bh * Spad + p] = 0.f;
     }
@@ -527,7 +551,7 @@ __global__ __launch_bounds__(256) void attn_prep(
     const float2* t = cs + (size_t)pos * (D / 2);
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
-        const uint4 v4 = *reinterpret_cast<const uint4*>((which ? K : Q) + off);
+        const uint4 v4 = qk4[which];
         const uint32_t vw[4] = {v4.x, v4.y, v4.z, v4.w};
         float x[8];
 #pragma unroll
@@ -745,15 +769,15 @@ bool allow_lds(F* fn, size_t bytes) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
 }
 
-constexpr int kStagesDkdv = 2, kStagesDq = 3;
+constexpr int kStagesDkdv = 2, kStagesDq = 2, kWavesDkdv = 8;
 
 template <int D>
 int launch_mfma_bwd(const AttnWs& w, const void* Q, const void* K, const void* V, const void* O,
                     const void* dO, const float* LSE, void* dQ, void* dK, void* dV, int BH, int S,
                     float scale, int causal, int rope_mode, float theta, hipStream_t s) {
-    using C1 = DkdvCfg<D, kStagesDkdv>;
+    using C1 = DkdvCfg<D, kStagesDkdv, kWavesDkdv>;
     using C2 = DqCfg<D, kStagesDq>;
-    static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv>, C1::LDS);
+    static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>, C1::LDS);
     static const bool ok2 = allow_lds(attn_dq_mfma<D, kStagesDq>, C2::LDS);
     if (!ok1 || !ok2) {
         set_error("gn_attn_bwd: cannot reserve LDS (%d / %d B)", C1::LDS, C2::LDS);
@@ -761,6 +785,10 @@ int launch_mfma_bwd(const AttnWs& w, const void* Q, const void* K, const void* V
     }
     const int64_t rows = (int64_t)BH * S;
     const int Spad = spad_of(S);
+    if (rows * (D / 8) >= ((int64_t)1 << 31)) {
+        set_error("gn_attn_bwd: B*H*S = %lld rows exceeds the bf16 path's 32-bit indexing", (long long)rows);
+        return GN_E_INVALID;
+    }
     if (rope_mode != GN_ROPE_NONE)
         rope_table<<<grid_for((int64_t)S * (D / 2), 256, 4096), 256, 0, s>>>(w.cs, S, D, theta);
     const int64_t threads = rows * (D / 8);
@@ -770,7 +798,7 @@ int launch_mfma_bwd(const AttnWs& w, const void* Q, const void* K, const void* V
     const bf16_t* Qp = (const bf16_t*)(rope_mode != GN_ROPE_NONE ? w.Qr : Q);
     const bf16_t* Kp = (const bf16_t*)(rope_mode != GN_ROPE_NONE ? w.Kr : K);
     const int nb = (S + 127) / 128;
-    hipLaunchKernelGGL((attn_dkdv_mfma<D, kStagesDkdv>), dim3(BH, nb), dim3(256), C1::LDS, s, Qp,
+    hipLaunchKernelGGL((attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>), dim3(BH, nb), dim3(64 * kWavesDkdv), C1::LDS, s, Qp,
                        Kp, (const bf16_t*)V, (const bf16_t*)dO, w.Lsc, w.Di, w.cs, (bf16_t*)dK,
                        (bf16_t*)dV, S, Spad, scale, causal, rope_mode);
     hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, Qp, Kp,
