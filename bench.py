@@ -41,10 +41,86 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--cpu-tokens", type=int, default=256)
+    p.add_argument("--cpu-tokens", type=int, default=T)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--workload", default="ffn", choices=["ffn", "attn", "vsa", "mlp"])
+    p.add_argument("--calib-copy", action="store_true",
+                   help="after the timed region, launch one gn_add_inplace over 2^28 floats "
+                        "(reads 2 GiB, writes 1 GiB): the reference dispatch that scales the "
+                        "FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
+    p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                        "'bench.py --calib-copy' into the HBM traffic of the dominant kernel")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_dn_gemm_hbm_traffic.txt")
+CALIB_FLOATS = 1 << 28
+
+
+def calib_copy(torch, gn):
+    x = torch.ones(CALIB_FLOATS, device="cuda:0")
+    y = torch.zeros(CALIB_FLOATS, device="cuda:0")
+    torch.cuda.synchronize()
+    gn.add_inplace(y, x)
+    torch.cuda.synchronize()
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the dominant GEMM and of the calibration
+    add (known bytes) -> scaled HBM bytes per launch of the dominant GEMM."""
+    import csv
+    import glob
+    import re
+
+    def load(d, counter):
+        out = {}
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = (r["Kernel_Name"], r["Grid_Size"])
+                out.setdefault(key, {}).setdefault(r["Dispatch_Id"], 0.0)
+                out[key][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        return out
+
+    res = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        tab = load(d, counter)
+        calib = [v for (k, g), v in tab.items() if "add_kernel" in k]
+        # the dN GEMM: gemm_dma kernel, plain epilogue, no transposes, grid of 4096 x 2048 tiles
+        gemm = {(k, g): v for (k, g), v in tab.items()
+                if re.search(r"gemm_dma<false, false, unsigned short, \d+, \d+, 0>", k)}
+        if not calib or not gemm:
+            raise SystemExit(f"{counter}: calibration or GEMM dispatches not found in {d}")
+        cvals = [x for v in calib for x in v.values()]
+        (gk, gg), gv = max(gemm.items(), key=lambda kv: len(kv[1]))
+        gvals = list(gv.values())
+        res[counter] = (sum(cvals) / len(cvals), sum(gvals) / len(gvals), len(gvals), gk, gg)
+    known = {"FETCH_SIZE": 2.0 * CALIB_FLOATS * 4, "WRITE_SIZE": 1.0 * CALIB_FLOATS * 4}
+    total = 0.0
+    lines = []
+    for counter, (ckib, gkib, n, gk, gg) in res.items():
+        factor = known[counter] / (ckib * 1024.0)
+        b = gkib * 1024.0 * factor
+        total += b
+        lines.append(f"{counter}: calibration add {ckib:.0f} KiB/dispatch (expected "
+                     f"{known[counter] / 1024:.0f} KiB) -> factor {factor:.4f}; dominant GEMM "
+                     f"{gkib:.0f} KiB/dispatch over {n} dispatches -> {b / 1e6:.1f} MB")
+    lines.append(f"kernel: {res['FETCH_SIZE'][3][:120]} grid {res['FETCH_SIZE'][4]}")
+    lines.append(f"traffic_bytes_per_launch: {total:.0f}")
+    print("\n".join(lines))
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the dominant GEMM from the committed counter summary."""
+    try:
+        for l in open(TRAFFIC_FILE):
+            if l.startswith("traffic_bytes_per_launch:"):
+                return int(float(l.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def timed(torch, fn, steps, warmup):
@@ -90,7 +166,7 @@ def bench_attn(args, torch, gn):
     if not args.no_cpu:
         import oracle
         r = np.random.default_rng(3)
-        Hs, Ss = 16, 1024
+        Hs, Ss = H, S  # one of the four batch rows at full size (the rate is per flop)
         q, k, v = (r.standard_normal((1, Hs, Ss, D)).astype(np.float32) for _ in range(3))
         do = (r.standard_normal((1, Hs, Ss, D)) * 1e-2).astype(np.float32)
         o, lse = oracle.attn_fwd(q, k, v)
@@ -304,6 +380,9 @@ def cpu_baseline(tokens):
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the backward "
               "path has no multi-GPU code in this build", file=sys.stderr)
@@ -332,6 +411,8 @@ def main():
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
     dom_ms, dom_flops = time_dominant(gn, torch, st)
+    if args.calib_copy:
+        calib_copy(torch, gn)
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
     flops_step = 6 * 2.0 * T * DM * HID
     cpu = None
@@ -360,7 +441,8 @@ def main():
         "roofline": {"kernel": "gemm_bf16_mfma (dN = dG Wg + dU Wu, 4096x2048x11264)",
                      "bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "launch_ms": round(dom_ms, 4), "traffic": None},
+                     "launch_ms": round(dom_ms, 4), "traffic": traffic_from_profile(),
+                     "algorithmic_bytes": 2 * (2 * T * HID + 2 * HID * DM) + 2 * T * DM},
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }
