@@ -10,7 +10,8 @@
 namespace gn {
 namespace {
 
-constexpr int kNormBlocks = 512;  // partial rows in the workspace (one per block)
+constexpr int kNormBlocks = 512;  // workspace rows reserved (one partial row per block)
+constexpr int kNormGrid = 256;    // blocks the row kernel uses at most (one per CU)
 constexpr int kNormWaves = 8;     // waves per block (512 threads)
 
 template <typename T> struct chunk8;
@@ -63,46 +64,70 @@ template <> struct raw8<bf16_t> {
     }
 };
 
-// One wave per row; lane l owns 8-element chunks c = l + 64 j (j < NC).  gamma/w is
-// re-read per row (it stays in L1/L2) so that few registers are live and many waves are
-// resident.  MODE 0 = LayerNorm (dgamma, dbeta partials), 1 = RMSNorm (dw partials).
+// One wave per row; lane l owns 8-element chunks c = l + 64 j (j < NC).  Each wave walks
+// rows r, r + stride, ... and requests row r + stride before it works on row r.  gamma / w
+// stays in registers.  Parameter-gradient partials live in LDS, one row per wave (each wave
+// adds into its own row, so the order of additions is fixed); at the end the block sums
+// its waves' rows and writes one partial row to the workspace.
+// MODE 0 = LayerNorm (dgamma, dbeta partials), 1 = RMSNorm (dw partials).
 template <int MODE, typename T, int NC>
-__global__ __launch_bounds__(512) void norm_bwd_rows(
+__global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
     const T* __restrict__ dY, const T* __restrict__ X, const T* __restrict__ gamma,
     const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dX,
     float* __restrict__ part, int rows, int F, float eps, int stat_is_var, int accumulate) {
-    __shared__ float red[64 * NC * 8];
+    constexpr int NP = MODE == 0 ? 2 : 1;
+    extern __shared__ float red[];  // [kNormWaves][NP][F]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nchunks = F >> 3;
     const float invF = 1.0f / (float)F;
-    float pa[NC][8], pb[NC][8];
+    float* my = red + (size_t)wave * NP * F;
+    for (int f = 4 * lane; f < NP * F; f += 256) *reinterpret_cast<float4*>(my + f) = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    raw8<T> gm[NC];
 #pragma unroll
-    for (int j = 0; j < NC; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { pa[j][e] = 0.f; pb[j][e] = 0.f; }
-    for (int r = blockIdx.x * kNormWaves + wave; r < rows; r += gridDim.x * kNormWaves) {
+    for (int j = 0; j < NC; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunks) gm[j].load(gamma + 8 * c);
+        else gm[j].zero();
+    }
+    auto load_row = [&](int r, raw8<T> (&x)[NC], raw8<T> (&dy)[NC]) {
         const size_t off = (size_t)r * F;
-        raw8<T> x[NC], dy[NC], gm[NC];
-        float mu = 0.f, rs;
-        if (MODE == 0) {
-            mu = mean[r];
-            rs = stat_is_var ? rsqrtf(rstd[r] + eps) : rstd[r];
-        } else {
-            rs = rstd[r];
-        }
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
             const int c = lane + 64 * j;
             if (c < nchunks) {
                 x[j].load(X + off + 8 * c);
                 dy[j].load(dY + off + 8 * c);
-                gm[j].load(gamma + 8 * c);
             } else {
                 x[j].zero();
                 dy[j].zero();
-                gm[j].zero();
             }
         }
+    };
+    // row statistics travel with the row's loads, so the prefetch of the next row is the
+    // only memory traffic in flight while a row is worked on
+    auto load_stats = [&](int r, float& mu, float& rs) {
+        mu = MODE == 0 ? mean[r] : 0.f;
+        rs = rstd[r];
+    };
+    const int stride = gridDim.x * kNormWaves;
+    int r = blockIdx.x * kNormWaves + wave;
+    raw8<T> x[NC], dy[NC];
+    float mu = 0.f, rs = 0.f;
+    if (r < rows) {
+        load_stats(r, mu, rs);
+        load_row(r, x, dy);
+    }
+    while (r < rows) {
+        const int rn = r + stride;
+        raw8<T> xn[NC], dyn[NC];
+        float mun = 0.f, rsn = 0.f;
+        if (rn < rows) {
+            load_stats(rn, mun, rsn);
+            load_row(rn, xn, dyn);
+        }
+        const size_t off = (size_t)r * F;
+        if (MODE == 0 && stat_is_var) rs = rsqrtf(rs + eps);
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int j = 0; j < NC; ++j)
@@ -122,64 +147,83 @@ __global__ __launch_bounds__(512) void norm_bwd_rows(
         for (int j = 0; j < NC; ++j) {
             const int c = lane + 64 * j;
             if (c >= nchunks) continue;
-            float o[8];
+            float o[8], pa[8], pb[8];
             if (accumulate) chunk8<T>::ld(dX + off + 8 * c, o);
+            float4* qa = reinterpret_cast<float4*>(my + 8 * c);
+            float4* qb = reinterpret_cast<float4*>(my + F + 8 * c);
+            const float4 a0 = qa[0], a1 = qa[1];
+            pa[0] = a0.x; pa[1] = a0.y; pa[2] = a0.z; pa[3] = a0.w;
+            pa[4] = a1.x; pa[5] = a1.y; pa[6] = a1.z; pa[7] = a1.w;
+            if (MODE == 0) {
+                const float4 b0 = qb[0], b1 = qb[1];
+                pb[0] = b0.x; pb[1] = b0.y; pb[2] = b0.z; pb[3] = b0.w;
+                pb[4] = b1.x; pb[5] = b1.y; pb[6] = b1.z; pb[7] = b1.w;
+            }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float v;
                 if (MODE == 0) {
                     const float xh = (x[j][e] - mu) * rs, g = dy[j][e] * gm[j][e];
                     v = rs * (g - s1 * invF - xh * s2 * invF);
-                    pa[j][e] += dy[j][e] * xh;
-                    pb[j][e] += dy[j][e];
+                    pa[e] += dy[j][e] * xh;
+                    pb[e] += dy[j][e];
                 } else {
                     v = rs * gm[j][e] * dy[j][e] - x[j][e] * rs * rs * rs * s1 * invF;
-                    pa[j][e] += dy[j][e] * x[j][e] * rs;
+                    pa[e] += dy[j][e] * x[j][e] * rs;
                 }
                 o[e] = accumulate ? o[e] + v : v;
             }
             chunk8<T>::st(dX + off + 8 * c, o);
-        }
-    }
-    // block reduction of the parameter partials (waves add into LDS in turn), then one
-    // partial row per block in the workspace
-    for (int p = 0; p < (MODE == 0 ? 2 : 1); ++p) {
-        for (int w = 0; w < kNormWaves; ++w) {
-            __syncthreads();
-            if (wave == w) {
-#pragma unroll
-                for (int j = 0; j < NC; ++j)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int f = (lane + 64 * j) * 8 + e;
-                        const float v = p == 0 ? pa[j][e] : pb[j][e];
-                        red[f] = w == 0 ? v : red[f] + v;
-                    }
+            qa[0] = make_float4(pa[0], pa[1], pa[2], pa[3]);
+            qa[1] = make_float4(pa[4], pa[5], pa[6], pa[7]);
+            if (MODE == 0) {
+                qb[0] = make_float4(pb[0], pb[1], pb[2], pb[3]);
+                qb[1] = make_float4(pb[4], pb[5], pb[6], pb[7]);
             }
         }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NC; ++j) { x[j] = xn[j]; dy[j] = dyn[j]; }
+        mu = mun;
+        rs = rsn;
+        r = rn;
+    }
+    // the block's partial rows: waves summed in a fixed order
+    __syncthreads();
+    for (int p = 0; p < NP; ++p) {
         float* dst = part + ((size_t)p * gridDim.x + blockIdx.x) * F;
-        for (int f = threadIdx.x; f < F; f += 512) dst[f] = red[f];
+        for (int f = 4 * threadIdx.x; f < F; f += 4 * 64 * kNormWaves) {
+            float4 s = *reinterpret_cast<const float4*>(red + (size_t)p * F + f);
+#pragma unroll
+            for (int w = 1; w < kNormWaves; ++w) {
+                const float4 v = *reinterpret_cast<const float4*>(red + ((size_t)w * NP + p) * F + f);
+                s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+            }
+            *reinterpret_cast<float4*>(dst + f) = s;
+        }
     }
 }
 
-// out[f] (+)= sum_g part[g][f] over G partial rows: block = 8 columns x 32 row groups.
-__global__ __launch_bounds__(256) void colsum_partials(const float* __restrict__ part, int G,
-                                                       int F, float* __restrict__ out,
-                                                       int accumulate) {
-    __shared__ float sh[32][8];
-    const int cl = threadIdx.x & 7, rg = threadIdx.x >> 3;
-    const int c = blockIdx.x * 8 + cl;
+// out[f] (+)= sum_g part[g][f] over G partial rows.  Block: 16 waves x 64 columns (one per
+// lane, 256-byte rows); wave w sums rows w, w + 16, ...; the waves' sums are added in a
+// fixed order.
+__global__ __launch_bounds__(1024) void colsum_partials(const float* __restrict__ part, int G,
+                                                        int F, float* __restrict__ out,
+                                                        int accumulate) {
+    __shared__ float sh[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int f = blockIdx.x * 64 + lane;
     float s = 0.f;
-    if (c < F)
-        for (int g = rg; g < G; g += 32) s += part[(size_t)g * F + c];
-    sh[rg][cl] = s;
+    if (f < F) {
+#pragma unroll 8
+        for (int g = wave; g < G; g += 16) s += part[(size_t)g * F + f];
+    }
+    sh[wave][lane] = s;
     __syncthreads();
-    if (threadIdx.x < 8 && c < F) {
-        float t = 0.f;
+    if (wave == 0 && f < F) {
+        float t = sh[0][lane];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) t += sh[i][cl];
-        out[c] = accumulate ? out[c] + t : t;
+        for (int w = 1; w < 16; ++w) t += sh[w][lane];
+        out[f] = accumulate ? out[f] + t : t;
     }
 }
 
@@ -252,6 +296,12 @@ __global__ __launch_bounds__(256) void norm_bwd_generic_param(
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+template <typename F>
+bool allow_lds(F* fn, size_t bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
+}
+
 template <int MODE, typename T>
 int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean,
              const float* rstd, void* dX, float* dA, float* dB, int rows, int F, float eps,
@@ -261,7 +311,8 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
                         aligned16(dX) && aligned16(gamma);
     const bool need_param = dA || dB;
     if (vec_ok) {
-        const int G = std::min(kNormBlocks, (rows + kNormWaves - 1) / kNormWaves);
+        // every wave gets two rows or more where the row count allows it
+        const int G = std::max(1, std::min(kNormGrid, (rows + 2 * kNormWaves - 1) / (2 * kNormWaves)));
         const size_t need = (size_t)(MODE == 0 ? 2 : 1) * G * F * sizeof(float);
         if (need_param && (!ws || ws_bytes < need)) {
             set_error("norm backward: workspace %zu B < %zu B", ws_bytes, need);
@@ -277,18 +328,27 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
             GN_LAUNCH_CHECK("norm backward (dx only)");
             return GN_OK;
         }
+        const size_t lds = (size_t)kNormWaves * (MODE == 0 ? 2 : 1) * F * sizeof(float);
+        if (lds > 64 * 1024) {
+            static const bool ok = allow_lds(norm_bwd_rows<MODE, T, 4>, 160 * 1024) &&
+                                   allow_lds(norm_bwd_rows<MODE, T, 2>, 160 * 1024);
+            if (!ok) {
+                set_error("norm backward: cannot reserve %zu B of LDS", lds);
+                return GN_E_HIP;
+            }
+        }
 #define GN_NORM_LAUNCH(NCV)                                                                    \
-    norm_bwd_rows<MODE, T, NCV><<<G, 512, 0, s>>>((const T*)dY, (const T*)X, (const T*)gamma,  \
-                                                  mean, rstd, (T*)dX, part, rows, F, eps,       \
-                                                  stat_var, acc)
+    norm_bwd_rows<MODE, T, NCV><<<G, 64 * kNormWaves, lds, s>>>(                               \
+        (const T*)dY, (const T*)X, (const T*)gamma, mean, rstd, (T*)dX, part, rows, F, eps,   \
+        stat_var, acc)
         if (nc <= 1) GN_NORM_LAUNCH(1);
         else if (nc <= 2) GN_NORM_LAUNCH(2);
         else GN_NORM_LAUNCH(4);
 #undef GN_NORM_LAUNCH
         GN_LAUNCH_CHECK("norm backward rows");
-        const unsigned gf = (F + 7) / 8;
-        if (dA) colsum_partials<<<gf, 256, 0, s>>>(part, G, F, dA, acc);
-        if (MODE == 0 && dB) colsum_partials<<<gf, 256, 0, s>>>(part + (size_t)G * F, G, F, dB, acc);
+        const unsigned gf = (F + 63) / 64;
+        if (dA) colsum_partials<<<gf, 1024, 0, s>>>(part, G, F, dA, acc);
+        if (MODE == 0 && dB) colsum_partials<<<gf, 1024, 0, s>>>(part + (size_t)G * F, G, F, dB, acc);
         GN_LAUNCH_CHECK("norm backward finish");
         return GN_OK;
     }
