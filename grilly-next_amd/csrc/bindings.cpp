@@ -98,6 +98,7 @@ PYBIND11_MODULE(grilly_core, m) {
         .value("VSALoRAExpand", OpType::VSALoRAExpand)
         .value("VSACosineBlendLoss", OpType::VSACosineBlendLoss)
         .value("FusedGLU", OpType::FusedGLU)
+        .value("Embedding", OpType::Embedding)
         .export_values();
 
     py::class_<TensorRef>(m, "TensorRef")

@@ -93,11 +93,24 @@ template <> __device__ __forceinline__ int tswz<64>(int r) {
 
 constexpr int tile_bytes(int D) { return 64 * D * 2; }
 
+// Where the rows of one (batch, head) live: element (b, h, s, d) at p[b sb + h sh + s sr + d]
+// (strides in elements).  [B,H,S,D] is {H S D, S D, D}; a [B,S,H,D] buffer whose rows are
+// ld elements apart (a fused QKV projection, say) is {S ld, D, ld}.
+struct TDesc {
+    const void* p;
+    int64_t sb, sh, sr;
+};
+template <typename T = bf16_t>
+__device__ __forceinline__ T* head_base(const TDesc& t, int bh, int H) {
+    const int b = bh / H, h = bh - b * H;
+    return (T*)t.p + b * t.sb + h * t.sh;
+}
+
 // DMA rows row0 .. row0+63 of a [S x D] matrix into a swizzled LDS tile (rows past S
 // re-read row S-1; the kernels mask them).  D/(8 NW) DMA instructions per wave.
 template <int D, int NW = 4>
-__device__ __forceinline__ void dma_tile(const bf16_t* __restrict__ g, int row0, int S,
-                                         uint32_t lds) {
+__device__ __forceinline__ void dma_tile(const bf16_t* __restrict__ g, int64_t sr, int row0,
+                                         int S, uint32_t lds) {
     constexpr int CPR = D / 8, RPI = 64 / CPR, PER_WAVE = CPR / NW;
     static_assert(PER_WAVE >= 1, "one DMA instruction per wave at least");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -107,7 +120,7 @@ __device__ __forceinline__ void dma_tile(const bf16_t* __restrict__ g, int row0,
         const int r = q * RPI + lane / CPR;
         const int c = (lane % CPR) ^ tswz<D>(r);
         const int rr = min(row0 + r, S - 1);
-        dma16(g + (size_t)rr * D + c * 8, __builtin_amdgcn_readfirstlane(lds + q * 1024));
+        dma16(g + rr * sr + c * 8, __builtin_amdgcn_readfirstlane(lds + q * 1024));
     }
 }
 
@@ -156,8 +169,8 @@ __device__ __forceinline__ void rot_t(float& x0, float& x1, float2 cs) {
 // the inverse rotation of `mode`.  Each lane moves chunk c and its partner c + D/16
 // (8 columns each), which holds every RoPE pair of either layout.
 template <int D>
-__device__ __forceinline__ void store_rows(const float* st, bf16_t* __restrict__ g, int row0,
-                                           int S, float mul, int mode,
+__device__ __forceinline__ void store_rows(const float* st, bf16_t* __restrict__ g, int64_t sr,
+                                           int row0, int S, float mul, int mode,
                                            const float2* __restrict__ cs) {
     constexpr int HC = D / 16, P = D + 4;
     const int lane = threadIdx.x & 63;
@@ -186,7 +199,7 @@ __device__ __forceinline__ void store_rows(const float* st, bf16_t* __restrict__
 #pragma unroll
             for (int e = 0; e < 8; ++e) rot_t(x[e], y[e], t[8 * c + e]);
         }
-        bf16_t* o = g + (size_t)row * D;
+        bf16_t* o = g + row * sr;
         *reinterpret_cast<bf16x8_t*>(o + 8 * c) = to_bf16x8(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
         *reinterpret_cast<bf16x8_t*>(o + 8 * (c + HC)) = to_bf16x8(y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]);
     }
@@ -213,16 +226,18 @@ struct DkdvCfg {
 // The next tiles' Q, dO, L, D_i arrive by LDS DMA while the current one is computed.
 template <int D, int STAGES, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
-    const bf16_t* __restrict__ Qr, const bf16_t* __restrict__ Kr, const bf16_t* __restrict__ V,
-    const bf16_t* __restrict__ dO, const float* __restrict__ Lsc, const float* __restrict__ Di,
-    const float2* __restrict__ cs, bf16_t* __restrict__ dK, bf16_t* __restrict__ dV, int S,
-    int Spad, float scale, int causal, int rope_mode) {
+    TDesc tQ, TDesc tK, TDesc tV, TDesc tG, const float* __restrict__ Lsc,
+    const float* __restrict__ Di, const float2* __restrict__ cs, TDesc tdK, TDesc tdV, int H,
+    int S, int Spad, float scale, int causal, int rope_mode) {
     static_assert(NW == 4 || NW == 8, "four or eight waves");
     using C = DkdvCfg<D, STAGES, NW>;
     extern __shared__ __align__(1024) unsigned char smem[];
     constexpr int NT = D / 32, KS = D / 16, HALVES = NW == 4 ? 2 : 1;
     const int bh = blockIdx.x, j0 = blockIdx.y * 128;
-    const size_t base = (size_t)bh * S * D;
+    const bf16_t* Qr = head_base<const bf16_t>(tQ, bh, H);
+    const bf16_t* Kr = head_base<const bf16_t>(tK, bh, H);
+    const bf16_t* V = head_base<const bf16_t>(tV, bh, H);
+    const bf16_t* dO = head_base<const bf16_t>(tG, bh, H);
     const int lane = threadIdx.x & 63, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int kg = wave & 3, half0 = NW == 4 ? 0 : wave >> 2;
@@ -242,8 +257,8 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     auto issue = [&](int it) {
         const int q0 = (t0 + it) * 64;
         const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
-        dma_tile<D, NW>(Qr + base, q0, S, sb);
-        dma_tile<D, NW>(dO + base, q0, S, sb + C::TB);
+        dma_tile<D, NW>(Qr, tQ.sr, q0, S, sb);
+        dma_tile<D, NW>(dO, tG.sr, q0, S, sb + C::TB);
         // 64 L values then 64 D_i values: one DMA instruction per wave
         constexpr int LANES = 32 / NW;  // 16-byte pieces per wave (32 pieces in all)
         if (lane < LANES) {
@@ -255,10 +270,10 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
 
     {
         const uint32_t kv = lds0 + STAGES * C::STAGE;
-        dma_tile<D, NW>(Kr + base, j0, S, kv);
-        dma_tile<D, NW>(Kr + base, j0 + 64, S, kv + C::TB);
-        dma_tile<D, NW>(V + base, j0, S, kv + 2 * C::TB);
-        dma_tile<D, NW>(V + base, j0 + 64, S, kv + 3 * C::TB);
+        dma_tile<D, NW>(Kr, tK.sr, j0, S, kv);
+        dma_tile<D, NW>(Kr, tK.sr, j0 + 64, S, kv + C::TB);
+        dma_tile<D, NW>(V, tV.sr, j0, S, kv + 2 * C::TB);
+        dma_tile<D, NW>(V, tV.sr, j0 + 64, S, kv + 3 * C::TB);
     }
     issue(0);
     if (STAGES > 2 && T > 1) issue(1);
@@ -352,7 +367,7 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     // epilogue: the key group's 32 x D rows (fp32) go through a private LDS strip; with
     // eight waves the second-half wave deposits its partial sums there first
     float* st = reinterpret_cast<float*>(smem) + kg * 32 * (D + 4);
-    auto finish = [&](f32x16_t (&acc)[NT], bf16_t* out, float mul, int mode) {
+    auto finish = [&](f32x16_t (&acc)[NT], bf16_t* out, int64_t sr, float mul, int mode) {
         __syncthreads();
         if (NW == 4 || half0 == 1) strip_acc<D, NT>(st, acc);
         __syncthreads();
@@ -364,10 +379,10 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
                 for (int r = 0; r < 16; ++r)
                     st[(8 * (r >> 2) + rq + (r & 3)) * (D + 4) + 32 * t + (lane & 31)] += acc[t][r];
         }
-        if (half0 == 0) store_rows<D>(st, out + base, kw0, S, mul, mode, cs);
+        if (half0 == 0) store_rows<D>(st, out, sr, kw0, S, mul, mode, cs);
     };
-    finish(aV, dV, 1.f, GN_ROPE_NONE);
-    finish(aK, dK, scale, rope_mode);
+    finish(aV, head_base<bf16_t>(tdV, bh, H), tdV.sr, 1.f, GN_ROPE_NONE);
+    finish(aK, head_base<bf16_t>(tdK, bh, H), tdK.sr, scale, rope_mode);
 }
 
 template <int D, int STAGES>
@@ -387,29 +402,28 @@ struct DqCfg {
 //                                  transpose reads)
 template <int D, int STAGES>
 __global__ __launch_bounds__(256) void attn_dq_mfma(
-    const bf16_t* __restrict__ Qr, const bf16_t* __restrict__ Kr, const bf16_t* __restrict__ V,
-    const bf16_t* __restrict__ dO, const float* __restrict__ Lsc, const float* __restrict__ Di,
-    const float2* __restrict__ cs, bf16_t* __restrict__ dQ, int S, int Spad, float scale,
-    int causal, int rope_mode) {
+    TDesc tQ, TDesc tK, TDesc tV, TDesc tG, const float* __restrict__ Lsc,
+    const float* __restrict__ Di, const float2* __restrict__ cs, TDesc tdQ, int H, int S,
+    int Spad, float scale, int causal, int rope_mode) {
     using C = DqCfg<D, STAGES>;
     extern __shared__ __align__(1024) unsigned char smem[];
     constexpr int NT = D / 32, KS = D / 16;
     const int nqb = (S + 127) / 128;
     const int bh = blockIdx.x, i0 = (nqb - 1 - (int)blockIdx.y) * 128;  // longest rows first
-    const size_t base = (size_t)bh * S * D;
+    const bf16_t* Qr = head_base<const bf16_t>(tQ, bh, H);
+    const bf16_t* Kr = head_base<const bf16_t>(tK, bh, H);
+    const bf16_t* V = head_base<const bf16_t>(tV, bh, H);
+    const bf16_t* dO = head_base<const bf16_t>(tG, bh, H);
     const int lane = threadIdx.x & 63, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int qw0 = i0 + wave * 32, q = qw0 + (lane & 31), qc = min(q, S - 1);
     const float c2 = scale * 1.4426950408889634f;
 
     bf16x8_t qf[KS], of[KS];
-    {
-        const size_t rq = base + (size_t)qc * D + 8 * h;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            qf[ks] = ld_frag16(Qr + rq + 16 * ks);
-            of[ks] = ld_frag16(dO + rq + 16 * ks);
-        }
+    for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = ld_frag16(Qr + qc * tQ.sr + 8 * h + 16 * ks);
+        of[ks] = ld_frag16(dO + qc * tG.sr + 8 * h + 16 * ks);
     }
     const float lq = Lsc[(size_t)bh * Spad + qc], dq = Di[(size_t)bh * Spad + qc];
     f32x16_t aQ[NT];
@@ -421,8 +435,8 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(
     const int T = (kend + 63) / 64;
     auto issue = [&](int it) {
         const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
-        dma_tile<D>(Kr + base, it * 64, S, sb);
-        dma_tile<D>(V + base, it * 64, S, sb + C::TB);
+        dma_tile<D>(Kr, tK.sr, it * 64, S, sb);
+        dma_tile<D>(V, tV.sr, it * 64, S, sb + C::TB);
     };
 
     issue(0);
@@ -492,7 +506,7 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(
     float* st = reinterpret_cast<float*>(smem) + wave * 32 * (D + 4);
     strip_acc<D, NT>(st, aQ);
     __syncthreads();
-    store_rows<D>(st, dQ + base, qw0, S, scale, rope_mode, cs);
+    store_rows<D>(st, head_base<bf16_t>(tdQ, bh, H), tdQ.sr, qw0, S, scale, rope_mode, cs);
 }
 
 // cos/sin table [S][D/2] of the RoPE angles (pair i at position p)
@@ -511,10 +525,9 @@ __global__ __launch_bounds__(256) void rope_table(float2* __restrict__ cs, int S
 // and L log2(e), both into [B*H][Spad] arrays whose padding the kernels never unmask.
 template <int D>
 __global__ __launch_bounds__(256) void attn_prep(
-    const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ dO,
-    const bf16_t* __restrict__ O, const float* __restrict__ LSE, bf16_t* __restrict__ Qr,
+    TDesc tQ, TDesc tK, TDesc tG, TDesc tO, const float* __restrict__ LSE, bf16_t* __restrict__ Qr,
     bf16_t* __restrict__ Kr, float* __restrict__ Lsc, float* __restrict__ Di,
-    const float2* __restrict__ cs, int64_t rows, int S, int Spad, int mode) {
+    const float2* __restrict__ cs, int64_t rows, int H, int S, int Spad, int mode) {
     constexpr int LPR = D / 8;
     const unsigned gid = blockIdx.x * 256u + threadIdx.x;  // rows * LPR < 2^31 (host check)
     const unsigned row = gid / LPR;
@@ -522,14 +535,14 @@ __global__ __launch_bounds__(256) void attn_prep(
     if (row >= (unsigned)rows) return;  // LPR divides 256: whole row groups leave together
     const int pos = (int)(row % (unsigned)S);
     const unsigned bh = row / (unsigned)S;
-    const size_t off = (size_t)row * D + 8 * c;
+    const size_t off = (size_t)row * D + 8 * c;  // in the [B,H,S,D] Qr, Kr copies
     // every global load up front, so one round trip covers them all
-    const uint4 o4 = *reinterpret_cast<const uint4*>(O + off);
-    const uint4 g4 = *reinterpret_cast<const uint4*>(dO + off);
+    const uint4 o4 = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tO, (int)bh, H) + pos * tO.sr + 8 * c);
+    const uint4 g4 = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tG, (int)bh, H) + pos * tG.sr + 8 * c);
     uint4 qk4[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
     if (mode != GN_ROPE_NONE) {
-        qk4[0] = *reinterpret_cast<const uint4*>(Q + off);
-        qk4[1] = *reinterpret_cast<const uint4*>(K + off);
+        qk4[0] = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tQ, (int)bh, H) + pos * tQ.sr + 8 * c);
+        qk4[1] = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tK, (int)bh, H) + pos * tK.sr + 8 * c);
     }
     const float lse = c == 0 ? LSE[row] : 0.f;
     const uint32_t ow[4] = {o4.x, o4.y, o4.z, o4.w}, gw[4] = {g4.x, g4.y, g4.z, g4.w};
@@ -771,9 +784,20 @@ bool allow_lds(F* fn, size_t bytes) {
 
 constexpr int kStagesDkdv = 2, kStagesDq = 2, kWavesDkdv = 8;
 
+// The eight tensors of one backward call (Q, K: un-rotated inputs).
+struct AttnIO {
+    TDesc Q, K, V, O, dO, dQ, dK, dV;
+};
+
+inline TDesc bhsd(const void* p, int H, int S, int D) {
+    return TDesc{p, (int64_t)H * S * D, (int64_t)S * D, (int64_t)D};
+}
+inline TDesc bshd(const void* p, int S, int D, int64_t ld) {
+    return TDesc{p, (int64_t)S * ld, (int64_t)D, ld};
+}
+
 template <int D>
-int launch_mfma_bwd(const AttnWs& w, const void* Q, const void* K, const void* V, const void* O,
-                    const void* dO, const float* LSE, void* dQ, void* dK, void* dV, int BH, int S,
+int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, int BH, int H, int S,
                     float scale, int causal, int rope_mode, float theta, hipStream_t s) {
     using C1 = DkdvCfg<D, kStagesDkdv, kWavesDkdv>;
     using C2 = DqCfg<D, kStagesDq>;
@@ -793,17 +817,17 @@ int launch_mfma_bwd(const AttnWs& w, const void* Q, const void* K, const void* V
         rope_table<<<grid_for((int64_t)S * (D / 2), 256, 4096), 256, 0, s>>>(w.cs, S, D, theta);
     const int64_t threads = rows * (D / 8);
     attn_prep<D><<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(
-        (const bf16_t*)Q, (const bf16_t*)K, (const bf16_t*)dO, (const bf16_t*)O, LSE,
-        (bf16_t*)w.Qr, (bf16_t*)w.Kr, w.Lsc, w.Di, w.cs, rows, S, Spad, rope_mode);
-    const bf16_t* Qp = (const bf16_t*)(rope_mode != GN_ROPE_NONE ? w.Qr : Q);
-    const bf16_t* Kp = (const bf16_t*)(rope_mode != GN_ROPE_NONE ? w.Kr : K);
+        io.Q, io.K, io.dO, io.O, LSE, (bf16_t*)w.Qr, (bf16_t*)w.Kr, w.Lsc, w.Di, w.cs, rows, H, S,
+        Spad, rope_mode);
+    // rotated copies when RoPE is on, else the inputs in their own layout
+    const TDesc tQ = rope_mode != GN_ROPE_NONE ? bhsd(w.Qr, H, S, D) : io.Q;
+    const TDesc tK = rope_mode != GN_ROPE_NONE ? bhsd(w.Kr, H, S, D) : io.K;
     const int nb = (S + 127) / 128;
-    hipLaunchKernelGGL((attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>), dim3(BH, nb), dim3(64 * kWavesDkdv), C1::LDS, s, Qp,
-                       Kp, (const bf16_t*)V, (const bf16_t*)dO, w.Lsc, w.Di, w.cs, (bf16_t*)dK,
-                       (bf16_t*)dV, S, Spad, scale, causal, rope_mode);
-    hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, Qp, Kp,
-                       (const bf16_t*)V, (const bf16_t*)dO, w.Lsc, w.Di, w.cs, (bf16_t*)dQ, S,
-                       Spad, scale, causal, rope_mode);
+    hipLaunchKernelGGL((attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>), dim3(BH, nb),
+                       dim3(64 * kWavesDkdv), C1::LDS, s, tQ, tK, io.V, io.dO, w.Lsc, w.Di, w.cs,
+                       io.dK, io.dV, H, S, Spad, scale, causal, rope_mode);
+    hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, tQ, tK,
+                       io.V, io.dO, w.Lsc, w.Di, w.cs, io.dQ, H, S, Spad, scale, causal, rope_mode);
     GN_LAUNCH_CHECK("gn_attn_bwd (mfma)");
     return GN_OK;
 }
@@ -822,11 +846,11 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
         return GN_E_WORKSPACE;
     }
     if (mfma_ok) {
+        const AttnIO io{bhsd(Q, H, S, D),  bhsd(K, H, S, D),  bhsd(V, H, S, D),  bhsd(O, H, S, D),
+                        bhsd(dO, H, S, D), bhsd(dQ, H, S, D), bhsd(dK, H, S, D), bhsd(dV, H, S, D)};
         if (D == 64)
-            return launch_mfma_bwd<64>(w, Q, K, V, O, dO, LSE, dQ, dK, dV, (int)BH, S, scale,
-                                       causal, rope_mode, theta, s);
-        return launch_mfma_bwd<128>(w, Q, K, V, O, dO, LSE, dQ, dK, dV, (int)BH, S, scale, causal,
-                                    rope_mode, theta, s);
+            return launch_mfma_bwd<64>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, theta, s);
+        return launch_mfma_bwd<128>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, theta, s);
     }
     const void* Qp = Q;
     const void* Kp = K;
@@ -892,6 +916,42 @@ extern "C" int gn_attn_bwd(const void* Q, const void* K, const void* V, const vo
                                      rope_mode, rope_theta, ws, ws_bytes, s);
     return attn_bwd_impl<float>(Q, K, V, O, dO, LSE, dQ, dK, dV, B, H, S, D, scale, causal,
                                 rope_mode, rope_theta, ws, ws_bytes, s);
+}
+
+extern "C" int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, const void* O,
+                                const void* dO, const float* LSE, void* dQ, void* dK, void* dV,
+                                int B, int H, int S, int D, int64_t ld_qkv, int64_t ld_o,
+                                int64_t ld_dqkv, float scale, int causal, int rope_mode,
+                                float rope_theta, int dtype, void* ws, size_t ws_bytes,
+                                void* stream) {
+    clear_error();
+    int rc = attn_check(Q, K, V, B, H, S, D, rope_mode, dtype);
+    if (rc) return rc;
+    if ((int64_t)B * H * S == 0) return GN_OK;
+    GN_REQUIRE(O && dO && LSE && dQ && dK && dV, "gn_attn_bwd_bshd: null pointer");
+    GN_REQUIRE(dtype == GN_BF16 && (D == 64 || D == 128),
+               "gn_attn_bwd_bshd: bf16 with D = 64 or 128 only (D=%d, dtype %d)", D, dtype);
+    GN_REQUIRE(ld_qkv >= (int64_t)H * D && ld_o >= (int64_t)H * D && ld_dqkv >= (int64_t)H * D,
+               "gn_attn_bwd_bshd: row strides must cover H*D = %d elements", H * D);
+    GN_REQUIRE(ld_qkv % 8 == 0 && ld_o % 8 == 0 && ld_dqkv % 8 == 0,
+               "gn_attn_bwd_bshd: row strides must be multiples of 8 elements");
+    const void* ptrs[8] = {Q, K, V, O, dO, dQ, dK, dV};
+    for (const void* p : ptrs)
+        GN_REQUIRE(((uintptr_t)p & 15u) == 0, "gn_attn_bwd_bshd: pointers must be 16-byte aligned");
+    AttnWs w;
+    const int64_t BH = (int64_t)B * H;
+    const size_t need = ws_layout(BH, S, D, 2, true, ws, &w);
+    if (!ws || ws_bytes < need) {
+        set_error("gn_attn_bwd_bshd: workspace %zu B < %zu B", ws_bytes, need);
+        return GN_E_WORKSPACE;
+    }
+    const AttnIO io{bshd(Q, S, D, ld_qkv),  bshd(K, S, D, ld_qkv),  bshd(V, S, D, ld_qkv),
+                    bshd(O, S, D, ld_o),    bshd(dO, S, D, ld_o),   bshd(dQ, S, D, ld_dqkv),
+                    bshd(dK, S, D, ld_dqkv), bshd(dV, S, D, ld_dqkv)};
+    hipStream_t s = as_stream(stream);
+    if (D == 64)
+        return launch_mfma_bwd<64>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, rope_theta, s);
+    return launch_mfma_bwd<128>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, rope_theta, s);
 }
 
 extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O, float* LSE,

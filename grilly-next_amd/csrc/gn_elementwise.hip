@@ -118,6 +118,29 @@ __global__ __launch_bounds__(256) void add_kernel(T* __restrict__ out, const T* 
     }
 }
 
+// ---- embedding (row gather) backward: dE[id[t]] += dX[t] --------------------------------
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ out, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        out[i] = 0.f;
+}
+
+// One wave per row t; lane l adds columns l, l + 64, ... (hardware fp32 atomics: repeated ids
+// make the order of additions, and so the last bits, vary from run to run).  Rows whose id
+// is outside [0, V) are skipped.
+template <typename T>
+__global__ __launch_bounds__(256) void embedding_bwd_kernel(const T* __restrict__ dX,
+                                                            const int32_t* __restrict__ ids,
+                                                            float* __restrict__ dE, int T_, int d,
+                                                            int V) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= T_) return;
+    const int id = ids[t];
+    if (id < 0 || id >= V) return;
+    const T* src = dX + (size_t)t * d;
+    float* dst = dE + (size_t)id * d;
+    for (int c = lane; c < d; c += 64) unsafeAtomicAdd(dst + c, io<T>::ld(src, c));
+}
+
 // ---- VSA surrogate loss backward (vsa-surrogate-loss-backward.glsl:50-88) ---------------
 // grid (ceil(D / (256*4)), Bn); each thread owns 4 consecutive dims i (one u32 word).
 __global__ __launch_bounds__(256) void surrogate_bwd_kernel(
@@ -332,6 +355,28 @@ extern "C" int gn_add_inplace(void* out, const void* a, int64_t n, int dtype, vo
         return GN_E_INVALID;
     }
     GN_LAUNCH_CHECK("gn_add_inplace");
+    return GN_OK;
+}
+
+extern "C" int gn_embedding_bwd(const void* dX, const int32_t* ids, float* dE, int T, int d,
+                                int V, int dtype, unsigned flags, void* stream) {
+    clear_error();
+    GN_REQUIRE(T >= 0 && d > 0 && V > 0, "gn_embedding_bwd: bad shape (T=%d d=%d V=%d)", T, d, V);
+    GN_REQUIRE(dE && (T == 0 || (dX && ids)), "gn_embedding_bwd: null pointer");
+    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_embedding_bwd: dtype %d", dtype);
+    hipStream_t s = as_stream(stream);
+    if (!(flags & GN_ACCUMULATE)) {
+        const int64_t n = (int64_t)V * d;
+        fill_zero_kernel<<<grid_for(n, 256, 8192), 256, 0, s>>>(dE, n);
+    }
+    if (T > 0) {
+        const unsigned g = (unsigned)((T + 3) / 4);
+        if (dtype == GN_BF16)
+            embedding_bwd_kernel<bf16_t><<<g, 256, 0, s>>>((const bf16_t*)dX, ids, dE, T, d, V);
+        else
+            embedding_bwd_kernel<float><<<g, 256, 0, s>>>((const float*)dX, ids, dE, T, d, V);
+    }
+    GN_LAUNCH_CHECK("gn_embedding_bwd");
     return GN_OK;
 }
 

@@ -163,6 +163,7 @@ void BackwardEngine::dispatch(Node* n) {
         case OpType::VSAUnpackProject: bwd_vsa_unpack_project(n); break;
         case OpType::VSASurrogateLoss: bwd_vsa_surrogate(n); break;
         case OpType::FusedGLU: bwd_fused_glu(n); break;
+        case OpType::Embedding: bwd_embedding(n); break;
         default: stats_.cpu_fallbacks++; break;  // no handler (autograd.cpp:126-128)
     }
 }
@@ -252,8 +253,40 @@ void BackwardEngine::bwd_rmsnorm(Node* n) {
     contribute(w, dW, 0, F, true);
 }
 
-// inputs Q, K, V [B, H, S, D]; outputs[0] = O; saved[0] = LSE fp32 [B*H*S]
+// layout 0: inputs Q, K, V [B, H, S, D]; outputs[0] = O; saved[0] = LSE fp32 [B*H*S].
+// layout 1: inputs[0] = fused QKV [B, S, 3*H*D]; outputs[0] = O [B, S, H*D]; the gradient
+// of the fused buffer comes back in one [B, S, 3*H*D] buffer (dQ | dK | dV per row).
 void BackwardEngine::bwd_attention(Node* n) {
+    AttentionParams pa = params_of<AttentionParams>(n);
+    if (pa.layout == 1) {
+        const TensorRef& qkv = n->inputs[0];
+        const TensorRef& o = n->outputs[0];
+        if (qkv.ndim != 3 || o.ndim != 3 || pa.heads == 0)
+            throw std::invalid_argument("FlashAttention2 (fused QKV): qkv [B,S,3HD], O [B,S,HD], heads > 0");
+        const int B = (int)qkv.shape[0], S = (int)qkv.shape[1], H = (int)pa.heads;
+        const int64_t C3 = qkv.shape[2], HD = o.shape[2];
+        if (C3 != 3 * HD || HD % H != 0)
+            throw std::invalid_argument("FlashAttention2 (fused QKV): qkv width must be 3 x O width");
+        const int D = (int)(HD / H);
+        const float scale = pa.scale != 0.f ? pa.scale : 1.0f / std::sqrt((float)D);
+        const float theta = pa.rope_theta != 0.f ? pa.rope_theta : 10000.f;
+        const uint64_t lse = n->saved_buffer_ids[0];
+        if (!lse) throw std::invalid_argument("FlashAttention2: saved LSE missing");
+        const size_t es = TensorRef::elem_size(qkv.dtype);
+        uint64_t dqkv = alloc_grad(qkv.size_bytes());
+        const size_t wsb = gn_attn_workspace_bytes(B, H, S, D);
+        uint64_t ws = alloc_grad(wsb);
+        const char* base = static_cast<const char*>(P(qkv.buffer_id));
+        char* gbase = static_cast<char*>(P(dqkv));
+        gn_call(gn_attn_bwd_bshd(base, base + HD * es, base + 2 * HD * es, P(o.buffer_id), gout(n),
+                                 (const float*)P(lse), gbase, gbase + HD * es, gbase + 2 * HD * es,
+                                 B, H, S, D, C3, HD, C3, scale, (int)pa.causal, (int)pa.rope_mode,
+                                 theta, gn_dtype(qkv.dtype, "FlashAttention2"), P(ws), wsb,
+                                 dev_.stream()), "attention backward (fused QKV)");
+        stats_.shaders_dispatched += 3;
+        n->grad_input_buffers[0] = dqkv;
+        return;
+    }
     const TensorRef& q = n->inputs[0];
     const TensorRef& k = n->inputs[1];
     const TensorRef& v = n->inputs[2];
@@ -375,6 +408,31 @@ void BackwardEngine::bwd_fused_glu(Node* n) {
     contribute(s[1], dWu, 0, (size_t)H * K, true);
     if (bg) contribute(bg, dbg, 0, H, true);
     if (bu) contribute(bu, dbu, 0, H, true);
+}
+
+// Embedding: outputs[0] = rows of the table gathered by inputs[0] (int32 ids, T of them);
+// saved[0] = the table [V x d].  dTable[id[t]] += dX[t] (fp32).  With a tied LM head the
+// table already holds that head's dW in the gradient table: the rows are added into it.
+void BackwardEngine::bwd_embedding(Node* n) {
+    const TensorRef& ids = n->inputs[0];
+    const TensorRef& x = n->outputs[0];
+    const uint64_t table = n->saved_buffer_ids[0];
+    if (!table) throw std::invalid_argument("Embedding: saved_buffer_ids[0] must hold the table");
+    if (n->params_size < 4)
+        throw std::invalid_argument("Embedding: params must hold the vocabulary size (uint32)");
+    uint32_t V = 0;
+    std::memcpy(&V, n->params, sizeof(V));
+    const int T = (int)ids.numel(), d = (int)x.last();
+    if ((size_t)T != x.rows()) throw std::invalid_argument("Embedding: one id per output row");
+    GradEntry* e = find(table);
+    const bool into = e && e->grad_id && e->owned && e->dtype == 0 &&
+                      e->grad_bytes == (size_t)V * d * 4;
+    uint64_t dE = into ? e->grad_id : alloc_grad((size_t)V * d * 4);
+    gn_call(gn_embedding_bwd(gout(n), (const int32_t*)P(ids.buffer_id), (float*)P(dE), T, d, (int)V,
+                             gn_dtype(x.dtype, "Embedding"), into ? GN_ACCUMULATE : 0u,
+                             dev_.stream()), "embedding backward");
+    stats_.shaders_dispatched += into ? 1 : 2;
+    if (!into) contribute(table, dE, 0, (size_t)V * d, true);
 }
 
 // ═════════════════════════════════════════════════════════════════════ TapeContext

@@ -67,7 +67,8 @@ enum class OpType : uint8_t {
     CubeMindSurprise,
     TemporalSurprise,
     VSAUnpackProject, VSASurrogateLoss, VSALoRAExpand, VSACosineBlendLoss,
-    FusedGLU,  // added by this build: fused gate/up projection + GLU backward
+    FusedGLU,   // added by this build: fused gate/up projection + GLU backward
+    Embedding,  // added by this build: row gather (tied embeddings); backward scatter-adds
     _Count
 };
 static_assert(static_cast<int>(OpType::VSACosineBlendLoss) == 33, "OpType numbering");
@@ -96,6 +97,9 @@ struct AttentionParams {
     uint32_t causal;    // 1 = causal mask j <= i
     uint32_t rope_mode; // 0 none, 1 interleaved, 2 half
     float rope_theta;   // 0 -> 10000
+    uint32_t layout;    // 0: inputs Q, K, V [B,H,S,D]; 1: inputs[0] = fused QKV [B,S,3*H*D],
+                        //    output O [B,S,H*D] (the layout a fused QKV projection produces)
+    uint32_t heads;     // H, for layout 1
 };
 struct CrossEntropyParams { float scale; uint32_t has_scale; };  // scale default 1 (no 1/B)
 struct FusedGLUParams { uint32_t kind; };                       // GN_GLU_* kind
@@ -173,6 +177,7 @@ private:
     void bwd_vsa_unpack_project(Node* n);
     void bwd_vsa_surrogate(Node* n);
     void bwd_fused_glu(Node* n);
+    void bwd_embedding(Node* n);
 
     Device& dev_;
     Stats stats_{};

@@ -27,8 +27,8 @@ SYMBOLS = [
     "gn_last_error", "gn_version", "gn_linear_bwd", "gn_gemm", "gn_colsum", "gn_act_bwd",
     "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
-    "gn_attn_workspace_bytes", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
-    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_add_inplace",
+    "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
+    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd", "gn_add_inplace",
 ]
 
 
@@ -64,10 +64,13 @@ _SIGS = {
     "gn_attn_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P,
                      _Z, _P], _I),
     "gn_attn_workspace_bytes": ([_I, _I, _I, _I], _Z),
+    "gn_attn_bwd_bshd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _F, _I,
+                          _I, _F, _I, _P, _Z, _P], _I),
     "gn_attn_fwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P, _Z, _P], _I),
     "gn_vsa_unpack_project_bwd": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _U, _P, _Z, _P], _I),
     "gn_vsa_workspace_bytes": ([_I, _I], _Z),
     "gn_vsa_surrogate_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F, _U, _P], _I),
+    "gn_embedding_bwd": ([_P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_add_inplace": ([_P, _P, _L, _I, _P], _I),
 }
 
@@ -112,6 +115,11 @@ def _ptr(t):
     if not t.is_contiguous():
         raise GnError("tensor must be contiguous")
     return ctypes.c_void_p(t.data_ptr())
+
+
+def _off(t, nbytes):
+    """Device address nbytes past the start of t (a column block of a row-major buffer)."""
+    return ctypes.c_void_p(_ptr(t).value + nbytes)
 
 
 def _stream():
@@ -306,6 +314,26 @@ def attn_bwd(Q, K, V, O, dO, LSE, scale=None, causal=True, rope="interleaved", t
     return dQ, dK, dV
 
 
+def attn_bwd_qkv(qkv, O, dO, LSE, heads, scale=None, causal=True, rope="none", theta=10000.0,
+                 ws=None, out=None):
+    """Backward on a fused QKV projection output qkv [B, S, 3*H*D] (Q | K | V along the last
+    axis, each [B, S, H, D]); O, dO [B, S, H*D]; LSE [B, H, S].  Returns dqkv like qkv."""
+    B, S, C3 = qkv.shape
+    D = C3 // (3 * heads)
+    HD = heads * D
+    scale = D ** -0.5 if scale is None else scale
+    dqkv = out if out is not None else torch.empty_like(qkv)
+    if ws is None:
+        ws = workspace(attn_workspace_bytes(B, heads, S, D), qkv.device)
+    e = qkv.element_size()
+    _check(lib().gn_attn_bwd_bshd(_ptr(qkv), _off(qkv, HD * e), _off(qkv, 2 * HD * e), _ptr(O),
+                                  _ptr(dO), _ptr(LSE), _ptr(dqkv), _off(dqkv, HD * e),
+                                  _off(dqkv, 2 * HD * e), B, heads, S, D, C3, O.shape[-1], C3,
+                                  scale, int(causal), ROPE[rope], theta, _dt(qkv), _ptr(ws),
+                                  ws.numel(), _stream()), "gn_attn_bwd_bshd")
+    return dqkv
+
+
 def attn_fwd(Q, K, V, scale=None, causal=True, rope="interleaved", theta=10000.0, ws=None):
     B, H, S, D = Q.shape
     scale = D ** -0.5 if scale is None else scale
@@ -343,6 +371,15 @@ def vsa_surrogate_bwd(preds, bits, results, weights, gamma=1.0, delta=1.0, lambd
                                       scale, ACCUMULATE if accumulate else 0, _stream()),
            "gn_vsa_surrogate_bwd")
     return dPreds
+
+
+def embedding_bwd(dX, ids, V, dE=None, accumulate=False):
+    """dE[ids[t]] (+)= dX[t]; dE fp32 [V, d]; ids int32 [T]."""
+    T, d = dX.shape
+    dE = torch.empty(V, d, device=dX.device) if dE is None else dE
+    _check(lib().gn_embedding_bwd(_ptr(dX), _ptr(ids), _ptr(dE), T, d, V, _dt(dX),
+                                  ACCUMULATE if accumulate else 0, _stream()), "gn_embedding_bwd")
+    return dE
 
 
 def add_inplace(out, a):

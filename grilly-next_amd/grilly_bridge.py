@@ -69,8 +69,17 @@ def layernorm_params(eps: float = 1e-5, stat_is_var: bool = False) -> bytes:
 
 
 def attention_params(scale: float = 0.0, causal: bool = True, rope: str = "interleaved",
-                     theta: float = 10000.0) -> bytes:
-    return struct.pack("<fIIf", scale, int(causal), ROPE_MODE[rope], theta)
+                     theta: float = 10000.0, fused_qkv_heads: int = 0) -> bytes:
+    """AttentionParams.  fused_qkv_heads = H > 0 selects the fused layout: inputs[0] is the
+    QKV projection output [B, S, 3*H*D] and the output O is [B, S, H*D]."""
+    layout = 1 if fused_qkv_heads else 0
+    return struct.pack("<fIIfII", scale, int(causal), ROPE_MODE[rope], theta, layout,
+                       int(fused_qkv_heads))
+
+
+def embedding_params(vocab: int) -> bytes:
+    """Embedding node: the table's row count (the table id goes in saved_buffer_ids[0])."""
+    return struct.pack("<I", int(vocab))
 
 
 def cross_entropy_params(scale: float = 1.0) -> bytes:

@@ -185,6 +185,21 @@ int gn_attn_bwd(const void* Q, const void* K, const void* V, const void* O, cons
 
 size_t gn_attn_workspace_bytes(int B, int H, int S, int D);
 
+/* Same backward on the [B, S, H, D] layout with row strides, so a fused QKV projection
+ * output [B*S, 3*H*D] feeds it (and its gradient buffer receives dQ, dK, dV) without head
+ * transposes: element (b, h, s, d) of Q is Q[(b*S + s)*ld_qkv + h*D + d], K and V likewise
+ * from their own base pointers with ld_qkv; O, dO use ld_o; dQ, dK, dV use ld_dqkv.  LSE
+ * stays [B, H, S].  The reference binds attention on [B,H,S,D] only
+ * (cpp/python/bindings.cpp:425-432); its FA2 forward runs on [B,S,H,D]
+ * (flash-attention2.glsl:9,136-143), which is the layout accepted here.
+ * bf16, D = 64 or 128; strides multiples of 8, pointers 16-byte aligned;
+ * ws: gn_attn_workspace_bytes(B, H, S, D). */
+int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, const void* O, const void* dO,
+                     const float* LSE, void* dQ, void* dK, void* dV, int B, int H, int S, int D,
+                     int64_t ld_qkv, int64_t ld_o, int64_t ld_dqkv, float scale, int causal,
+                     int rope_mode, float rope_theta, int dtype, void* ws, size_t ws_bytes,
+                     void* stream);
+
 /* Attention forward producing the saved-tensor contract of the backward (O and the fp32
  * row logsumexp; flash-attention2-rope.glsl:165-247 semantics plus the causal mask).
  * Same arguments as gn_attn_bwd; ws as sized by gn_attn_workspace_bytes (needed only
@@ -217,6 +232,16 @@ int gn_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32_
                          const float* weights, float* dPreds, int Bn, int K, int D, int words,
                          float gamma, float delta, float lambda_c, float scale, unsigned flags,
                          void* stream);
+
+/* ---- embedding ------------------------------------------------------------------------- */
+/* Backward of a row gather X[t] = E[ids[t]] (token embeddings, tied with the LM head in the
+ * decoder workload).  The reference tape has no embedding op; this entry serves the
+ * Embedding node this build adds next to its OpTypes (autograd.h:81-141).
+ *   dE[ids[t], :] (+)= dX[t, :]   dE fp32 [V x d]; dX [T x d] f32 or bf16; ids int32.
+ * Without GN_ACCUMULATE dE is cleared first.  Rows with ids outside [0, V) are skipped.
+ * Repeated ids are summed with fp32 atomics (order of additions not fixed). */
+int gn_embedding_bwd(const void* dX, const int32_t* ids, float* dE, int T, int d, int V,
+                     int dtype, unsigned flags, void* stream);
 
 /* ---- misc ------------------------------------------------------------------------------ */
 /* out[i] (+)= a[i] (f32/bf16): the fan-out accumulation the reference leaves as a TODO

@@ -321,6 +321,68 @@ def test_attention_bf16_mfma(gn, S, D, causal, rope):
     assert rel_err(host(dK), rK) < BF16_TOL
 
 
+@pytest.mark.parametrize("S,D,rope", [(200, 64, "none"), (256, 128, "interleaved"), (96, 64, "half")])
+def test_attention_fused_qkv_layout(gn, S, D, rope):
+    """[B,S,H,D] rows of a fused QKV buffer in, dQKV in the same layout out; equals the
+    [B,H,S,D] oracle after the head permutation."""
+    r = rng_(12)
+    B, H = 2, 3
+    Q, K, V = (rnd(r.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    dO = rnd((r.standard_normal((B, H, S, D)) * 0.01).astype(np.float32))
+    O, LSE = oracle.attn_fwd(Q, K, V, causal=True, rope_mode=rope)
+    O = rnd(O)
+    rQ, rK, rV = oracle.attn_bwd(Q, K, V, dO, LSE, causal=True, rope_mode=rope)
+    bshd = lambda t: np.ascontiguousarray(t.transpose(0, 2, 1, 3).reshape(B, S, H * D))
+    qkv = np.concatenate([bshd(Q), bshd(K), bshd(V)], axis=-1)
+    dqkv = gn.attn_bwd_qkv(dev(qkv, torch.bfloat16), dev(bshd(O), torch.bfloat16),
+                           dev(bshd(dO), torch.bfloat16), dev(LSE), H, causal=True, rope=rope)
+    got = host(dqkv).reshape(B, S, 3, H, D).transpose(2, 0, 3, 1, 4)  # [3, B, H, S, D]
+    assert rel_err(got[0], rQ) < BF16_TOL
+    assert rel_err(got[1], rK) < BF16_TOL
+    assert rel_err(got[2], rV) < BF16_TOL
+
+
+def test_attention_fused_qkv_rejects_bad_layouts(gn):
+    z = torch.zeros(1, 64, 3 * 2 * 64, dtype=torch.bfloat16, device="cuda")
+    o = torch.zeros(1, 64, 2 * 64, dtype=torch.bfloat16, device="cuda")
+    lse = torch.zeros(1, 2, 64, device="cuda")
+    with pytest.raises(gn.GnError):
+        gn.attn_bwd_qkv(z.float(), o.float(), o.float(), lse, 2)  # fp32: bf16 only
+    L = gn.lib()
+    ws = gn.workspace(gn.attn_workspace_bytes(1, 2, 64, 64), z.device)
+    zp, op_, lp = z.data_ptr(), o.data_ptr(), lse.data_ptr()
+    args = lambda ld, off: (zp, zp + 256, zp + 512, op_, op_, lp, zp + off, zp + 256, zp + 512,
+                            1, 2, 64, 64, ld, 128, 384, 0.125, 1, 0, 1e4, gn.BF16,
+                            ws.data_ptr(), ws.numel(), gn._stream())
+    assert L.gn_attn_bwd_bshd(*args(120, 0)) == -1  # row stride below H*D
+    assert L.gn_attn_bwd_bshd(*args(384, 8)) == -1  # dQ not 16-byte aligned
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_embedding_scatter_add(gn, dt):
+    """dE[ids[t]] += dX[t]: repeated ids sum, ids outside [0, V) are skipped, and
+    GN_ACCUMULATE adds onto an existing gradient (the tied LM head's)."""
+    r = rng_(13)
+    T_, d, V = 1000, 96, 50
+    dX = r.standard_normal((T_, d)).astype(np.float32)
+    if dt == "bf16":
+        dX = rnd(dX)
+    ids = r.integers(0, V, size=T_).astype(np.int32)
+    ids[::97] = -1
+    ids[5] = V + 3
+    want = np.zeros((V, d), np.float64)
+    ok = (ids >= 0) & (ids < V)
+    np.add.at(want, ids[ok], dX[ok].astype(np.float64))
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    tids = torch.from_numpy(ids).cuda()
+    dE = gn.embedding_bwd(dev(dX, tdt), tids, V)
+    assert rel_err(host(dE), want) < FP32_TOL
+    base = r.standard_normal((V, d)).astype(np.float32)
+    dE2 = gn.embedding_bwd(dev(dX, tdt), tids, V, dE=dev(base), accumulate=True)
+    assert rel_err(host(dE2), want + base) < FP32_TOL
+
+
 def test_attention_fwd_bf16_matches_oracle(gn):
     r = rng_(11)
     Q, K, V = (rnd(r.standard_normal((1, 2, 96, 64)).astype(np.float32)) for _ in range(3))

@@ -288,3 +288,77 @@ def test_tape_error_paths(env):
         for _ in range(10):
             small.record_op(gc.OpType.ReLU, [gb.tref(x, True)], [gb.tref(x)])
     small.end()
+
+
+def _decoder_reference(m):
+    """fp32 torch autograd of the same decoder, rounding to bf16 where the GPU run stores
+    (straight-through), so both differentiate the same bf16-stored forward."""
+    import math
+    rb = lambda t: t + (t.bfloat16().float() - t).detach()
+    leaf = lambda t: t.detach().float().clone().requires_grad_(True)
+    B, S, H, d, T = m.B, m.S, m.H, m.d, m.T
+    D = d // H
+    E = leaf(m.E)
+    params = [{k: leaf(v) for k, v in p.items()} for p in m.layers]
+    lnf_g, lnf_b = leaf(m.lnf_g), leaf(m.lnf_b)
+
+    def ln(x, g, b):
+        mu = x.mean(-1, keepdim=True)
+        var = ((x - mu) ** 2).mean(-1, keepdim=True)
+        return rb((x - mu) * torch.rsqrt(var + 1e-5) * g + b)
+
+    def gelu(u):
+        return 0.5 * u * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (u + 0.044715 * u ** 3)))
+
+    mask = torch.triu(torch.ones(S, S, dtype=torch.bool, device=E.device), 1)
+    x = rb(E[m.ids.long()])
+    for p in params:
+        n1 = ln(x, p["ln1_g"], p["ln1_b"])
+        qkv = rb(n1 @ p["Wqkv"].t() + p["bqkv"])
+        q, k, v = qkv.view(B, S, 3, H, D).permute(2, 0, 3, 1, 4)
+        sc = torch.matmul(q, k.transpose(-1, -2).contiguous()) / math.sqrt(D)
+        o = torch.matmul(torch.softmax(sc.masked_fill(mask, float("-inf")), -1), v)
+        o = rb(o.permute(0, 2, 1, 3).reshape(T, d))
+        x2 = rb(x + rb(o @ p["Wo"].t() + p["bo"]))
+        n2 = ln(x2, p["ln2_g"], p["ln2_b"])
+        gate = rb(n2 @ p["Wg"].t() + p["bg"])
+        up = rb(n2 @ p["Wu"].t() + p["bu"])
+        h = rb(gate * gelu(up))
+        x = rb(x2 + rb(h @ p["Wd"].t() + p["bd"]))
+    logits = rb(ln(x, lnf_g, lnf_b) @ E.t())
+    torch.nn.functional.cross_entropy(logits, m.tgt.long()).backward()
+    return E, params, lnf_g, lnf_b
+
+
+def test_decoder_stack_through_tape(env):
+    """BASELINE configs[4] at a small size: embedding, LN, fused QKV + causal attention on
+    the fused layout, residual adds, GEGLU, tied LM head and CE, all through the tape."""
+    gc, gb, dev = env
+    import decoder_tape
+    m = decoder_tape.Decoder(layers=2, d=128, heads=2, ff=256, vocab=300, batch=2, seq=128, seed=7)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(11)
+    for p in m.layers:  # non-trivial norm parameters and biases, so their gradients matter
+        for k in ("ln1_g", "ln2_g"):
+            p[k].copy_((1 + 0.2 * torch.randn(p[k].shape, device="cuda:0", generator=g)).bfloat16())
+        for k in ("ln1_b", "ln2_b", "bqkv", "bo", "bg", "bu", "bd"):
+            p[k].copy_((0.05 * torch.randn(p[k].shape, device="cuda:0", generator=g)).bfloat16())
+    m.forward()
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    loss = m.record(tape)
+    tape.backward(loss, 0)
+    got = {"E": grad(gb, dev, tape, m.E, gb.DTYPE_F32)}
+    for i, p in enumerate(m.layers):
+        for k in ("Wqkv", "bqkv", "Wo", "ln1_g", "ln2_b", "Wg", "Wu", "bu", "Wd"):
+            got[f"{k}{i}"] = grad(gb, dev, tape, p[k], gb.DTYPE_F32)
+    got["lnf_g"] = grad(gb, dev, tape, m.lnf_g, gb.DTYPE_F32)
+    tape.end()
+    E, params, lnf_g, _ = _decoder_reference(m)
+    want = {"E": E.grad, "lnf_g": lnf_g.grad}
+    for i, p in enumerate(params):
+        for k in ("Wqkv", "bqkv", "Wo", "ln1_g", "ln2_b", "Wg", "Wu", "bu", "Wd"):
+            want[f"{k}{i}"] = p[k].grad
+    errs = {k: rel_err(got[k], want[k].cpu().numpy()) for k in got}
+    bad = {k: v for k, v in errs.items() if not v < 2e-2}
+    assert not bad, f"relative errors above 2e-2: {bad} (all: {errs})"

@@ -2,6 +2,7 @@
 TensorRef contract of the reference (cpp/include/grilly/autograd/autograd.h:46-141), the
 arena's failure behaviour (tape_arena.h:94-108) and the parameter-block layouts."""
 import os
+import struct
 
 import pytest
 
@@ -67,8 +68,18 @@ def test_node_is_fixed_size():
 
 def test_param_blocks():
     assert len(gb.vsa_surrogate_params(4, 10240)) == 40
-    assert len(gb.attention_params()) == 16
+    # AttentionParams: scale, causal, rope_mode, rope_theta, layout, heads
+    assert len(gb.attention_params()) == 24
+    assert struct.unpack("<fIIfII", gb.attention_params(fused_qkv_heads=12))[4:] == (1, 12)
+    assert struct.unpack("<fIIfII", gb.attention_params())[4:] == (0, 0)
     assert len(gb.layernorm_params()) == 8
+    assert struct.unpack("<I", gb.embedding_params(32000)) == (32000,)
+
+
+def test_optype_numbering_extends_the_reference():
+    # the reference's values end at VSACosineBlendLoss = 33; this build appends two
+    assert int(grilly_core.OpType.FusedGLU) == 34
+    assert int(grilly_core.OpType.Embedding) == 35
 
 
 def test_device_without_gpu_fails_loudly():
