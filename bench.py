@@ -16,9 +16,11 @@ Other BASELINE configs (parity-tested, measured with --workload):
     vsa   configs[3]: VSA unpack-project dW (8192 x 10240 bits -> 768, fp32 dY) and the
           surrogate-loss backward (K = 4)
     mlp   configs[0]: MLP 784->256->10 fp32 B=64 through the tape engine (grilly_core)
+    decoder configs[4]: 12-layer decoder (d 768, GEGLU, tied embedding 32000, CE), B8 x S1024,
+          end-to-end backward through the tape engine
 Each prints one JSON line of the same shape; the default (ffn) is the headline metric.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ffn|attn|vsa|mlp]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ffn|attn|vsa|mlp|decoder]
 """
 import argparse
 import json
@@ -43,7 +45,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--cpu-tokens", type=int, default=T)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", default="ffn", choices=["ffn", "attn", "vsa", "mlp"])
+    p.add_argument("--workload", default="ffn", choices=["ffn", "attn", "vsa", "mlp", "decoder"])
     p.add_argument("--calib-copy", action="store_true",
                    help="after the timed region, launch one gn_add_inplace over 2^28 floats "
                         "(reads 2 GiB, writes 1 GiB): the reference dispatch that scales the "
@@ -281,6 +283,74 @@ def bench_mlp(args, torch, gn):
                 higher=False)
 
 
+def bench_decoder(args, torch, gn):
+    """12-layer decoder (d 768, 12 heads, GEGLU 3072, tied embedding 32000),
+    batch 8 x seq 1024, bf16; one step = tape begin / record / backward / end."""
+    import grilly_core
+    import grilly_bridge as gb
+    from decoder_tape import Decoder
+    m = Decoder()
+    m.forward()
+    device = grilly_core.Device(0)
+    gb.attach_torch_stream(device)
+    tape = gb.create_tape_context(device)
+    ms = timed(torch, lambda: m.backward_step(tape), args.steps, args.warmup)
+    tf = m.flops() / (ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        cpu = decoder_cpu_baseline(m)
+    return line("12-layer decoder backward tokens/s (end-to-end tape backward)",
+                round(m.T / (ms * 1e-3), 1), "tokens/s", args, ms, "bf16",
+                {"workload": "C5 12-layer decoder bwd: d768 H12 LN, fused QKV, causal attention, "
+                             "GEGLU 3072, tied embedding 32000 + CE; B8 x S1024, bf16",
+                 "tokens": m.T, "layers": m.L, "d_model": m.d, "heads": m.H, "ff": m.ff,
+                 "vocab": m.V, "parallelism": "none (1 GPU)"},
+                {"kernel": "whole step (GEMMs, attention, norms, CE, adds)", "bound": "mfma",
+                 "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                 "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                 "flops_per_step": m.flops()}, cpu)
+
+
+def decoder_cpu_baseline(m):
+    """Oracle (C, OpenMP, fp64 accumulation) on one layer's backward at full size, scaled
+    to 12 layers plus the LM head by FLOPs (the head timed as its share of the layer)."""
+    import oracle
+    T, d, ff, H, B, S = m.T, m.d, m.ff, m.H, m.B, m.S
+    D = d // H
+    r = np.random.default_rng(5)
+    f = lambda *s: r.standard_normal(s).astype(np.float32)
+    x, dY = f(T, d), (f(T, d) * 1e-2).astype(np.float32)
+    g1 = np.ones(d, np.float32)
+    Wqkv, Wo, Wg, Wu, Wd = (f(3 * d, d) * 0.02, f(d, d) * 0.02, f(ff, d) * 0.02, f(ff, d) * 0.02,
+                            f(d, ff) * 0.02)
+    n1, m1, r1 = oracle.layernorm_fwd(x, g1)
+    qkv = oracle.linear_fwd(n1, Wqkv)
+    q, k, v = (np.ascontiguousarray(t) for t in qkv.reshape(B, S, 3, H, D).transpose(2, 0, 3, 1, 4))
+    o, lse = oracle.attn_fwd(q, k, v, causal=True, rope_mode="none")
+    o2 = np.ascontiguousarray(o.transpose(0, 2, 1, 3).reshape(T, d))
+    n2, m2, r2 = oracle.layernorm_fwd(x, g1)
+    gate, up = oracle.linear_fwd(n2, Wg), oracle.linear_fwd(n2, Wu)
+    h = oracle.glu_fwd("geglu_up", gate, up)
+    t0 = time.perf_counter()
+    dH, _, _ = oracle.linear_bwd(dY, h, Wd)
+    dG, dU = oracle.glu_bwd("geglu_up", dH, gate, up)
+    dN2 = oracle.linear_bwd(dG, n2, Wg)[0] + oracle.linear_bwd(dU, n2, Wu)[0]
+    oracle.layernorm_bwd(dN2, x, g1, m2, r2)
+    dO2, _, _ = oracle.linear_bwd(dY, o2, Wo)
+    dO4 = np.ascontiguousarray(dO2.reshape(B, S, H, D).transpose(0, 2, 1, 3))
+    oracle.attn_bwd(q, k, v, dO4, lse, causal=True, rope_mode="none")
+    dQKV = (f(T, 3 * d) * 1e-2).astype(np.float32)  # the layout change back is not timed work
+    dN1, _, _ = oracle.linear_bwd(dQKV, n1, Wqkv)
+    oracle.layernorm_bwd(dN1, x, g1, m1, r1)
+    dt = time.perf_counter() - t0
+    layer_flops = (m.flops() - 2 * 2 * T * d * m.V) / m.L
+    step_s = dt * (m.L + 2 * 2 * T * d * m.V / layer_flops)
+    return {"value": round(T / step_s, 2), "unit": "tokens/s", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": f"one full-size layer backward (T={T}) on the oracle (C/OpenMP, fp64 "
+                      f"accumulation), {dt:.1f} s, scaled by FLOPs to {m.L} layers + LM head"}
+
+
 def make_inputs(torch, dev):
     g = torch.Generator(device=dev)
     g.manual_seed(2)
@@ -391,7 +461,8 @@ def main():
     import gn_bwd as gn
     gn.lib()
     if args.workload != "ffn":
-        fn = {"attn": bench_attn, "vsa": bench_vsa, "mlp": bench_mlp}[args.workload]
+        fn = {"attn": bench_attn, "vsa": bench_vsa, "mlp": bench_mlp,
+              "decoder": bench_decoder}[args.workload]
         print(json.dumps(fn(args, torch, gn)))
         return
     dev = torch.device("cuda:0")

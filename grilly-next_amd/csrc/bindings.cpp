@@ -38,7 +38,9 @@ PYBIND11_MODULE(grilly_core, m) {
         .def_property_readonly("name", &Device::name)
         .def_property_readonly("index", &Device::index)
         .def("use_stream", &Device::use_stream, py::arg("stream_handle"),
-             "Launch on a caller-owned HIP stream (e.g. torch.cuda.current_stream().cuda_stream); 0 = own stream")
+             "Launch on a caller-owned HIP stream (e.g. torch.cuda.current_stream().cuda_stream); "
+             "0 = the null (default) stream")
+        .def("use_own_stream", &Device::use_own_stream, "Launch on the device's own stream again")
         .def("stream_handle", [](const Device& d) { return reinterpret_cast<uint64_t>(d.stream()); })
         .def("alloc", &Device::acquire, py::arg("nbytes"))
         .def("free", &Device::release, py::arg("buffer_id"))

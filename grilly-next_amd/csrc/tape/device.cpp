@@ -33,9 +33,9 @@ Device::~Device() {
     if (own_stream_) hipStreamDestroy(own_stream_);
 }
 
-void Device::use_stream(uint64_t handle) {
-    stream_ = handle ? reinterpret_cast<hipStream_t>(handle) : own_stream_;
-}
+void Device::use_stream(uint64_t handle) { stream_ = reinterpret_cast<hipStream_t>(handle); }
+
+void Device::use_own_stream() { stream_ = own_stream_; }
 
 size_t Device::bucket(size_t bytes) {
     size_t b = 256;

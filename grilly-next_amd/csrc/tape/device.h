@@ -35,9 +35,11 @@ public:
     int index() const { return index_; }
     std::string name() const { return name_; }
     hipStream_t stream() const { return stream_; }
-    // Launch on a caller-owned stream (e.g. torch.cuda.current_stream().cuda_stream);
-    // 0 restores the device's own stream.
+    // Launch on a caller-owned stream (e.g. torch.cuda.current_stream().cuda_stream).
+    // 0 is the null (default) stream, which is what torch reports for its default stream.
     void use_stream(uint64_t handle);
+    // Back to the device's own (non-blocking) stream.
+    void use_own_stream();
 
     uint64_t acquire(size_t bytes);  // from the pool; contents undefined
     void release(uint64_t id);       // back to the pool

@@ -23,6 +23,19 @@ def env(gpu):
     return grilly_core, gb, dev
 
 
+def test_tape_runs_on_torchs_stream(env):
+    """attach_torch_stream puts the tape's launches on torch's current stream, the default
+    (null, handle 0) stream included, so they are ordered with the torch work around them."""
+    gc, gb, dev = env
+    assert dev.stream_handle() == torch.cuda.current_stream().cuda_stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        gb.attach_torch_stream(dev)
+        assert dev.stream_handle() == s.cuda_stream
+    gb.attach_torch_stream(dev)
+    assert dev.stream_handle() == torch.cuda.current_stream().cuda_stream
+
+
 def T(x, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0").to(dtype).contiguous()
 
