@@ -32,6 +32,10 @@ struct GemmDesc {
     int ldgu;
     int H;
     int glu_kind;
+    // split-K (plain fp32 epilogue only): blockIdx.y picks one of ksplit k-ranges and the
+    // partial tiles are added into C with fp32 atomics after C is cleared; with two splits
+    // the result is exactly a + b whichever lands first, so it stays deterministic
+    int ksplit;
 };
 
 // Store one accumulated element (m, n) according to the descriptor's epilogue.

@@ -209,6 +209,33 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& g, const float* st
         }
 }
 
+// Split-K epilogue (fp32 C, cleared beforehand): the strip's rows are added into C with
+// hardware fp32 atomics, one row per instruction round (lane = column: 256-byte segments).
+template <int WN>
+__device__ __forceinline__ void epilogue_atomic(const GemmDesc& g, const float* st, int mbase,
+                                                int nbase, int lane) {
+#pragma unroll 4
+    for (int rr = 0; rr < 32; ++rr) {
+        const int m = mbase + rr;
+        if (m >= g.M) break;
+        float* C = reinterpret_cast<float*>(m < g.Msplit ? g.C : g.C2) +
+                   (size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc;
+#pragma unroll
+        for (int c = lane; c < WN; c += 64)
+            if (nbase + c < g.N) unsafeAtomicAdd(C + nbase + c, st[rr * (WN + 4) + c]);
+    }
+}
+
+// C rows (and C2 rows past Msplit) cleared before a split-K launch
+__global__ __launch_bounds__(256) void clear_c(GemmDesc g) {
+    const int64_t total = (int64_t)g.M * g.N;
+    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int m = (int)(i / g.N), n = (int)(i % g.N);
+        float* C = reinterpret_cast<float*>(m < g.Msplit ? g.C : g.C2);
+        C[(size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n] = 0.f;
+    }
+}
+
 // Pipeline depth: three LDS stages when they fit and A is k-contiguous; with a k-outer A
 // (transpose reads for both operands) two stages measured faster on MI355X.
 template <bool TA, int BM, int BN>
@@ -251,10 +278,15 @@ __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int kt0 = g.Ks[0] / BK;
-    const int KT = kt0 + (g.nseg > 1 ? g.Ks[1] / BK : 0);
+    const int KTall = kt0 + (g.nseg > 1 ? g.Ks[1] / BK : 0);
+    // this block's k-tiles [kt_lo, kt_lo + KT): the whole range, or one half with split-K
+    const int half = KTall >> 1;
+    const int kt_lo = blockIdx.y ? half : 0;
+    const int KT = g.ksplit < 2 ? KTall : (blockIdx.y ? KTall - half : half);
 
     auto tile_base = [&](int buf) { return lds0 + (uint32_t)(buf * STAGE) * 2u; };
-    auto issue = [&](int t, int buf) {
+    auto issue = [&](int tl, int buf) {
+        const int t = kt_lo + tl;
         const int s = t < kt0 ? 0 : 1;
         const int k0 = (t < kt0 ? t : t - kt0) * BK;
         stage<BM, !TA>(g.A[s], g.lda[s], m0, g.M, k0, tile_base(buf));
@@ -262,7 +294,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
     };
     // DMA of tile t split over the four k-steps of the current tile's MFMAs:
     // step 0/1 carry the A halves, steps 2/3 the B halves.
-    auto issue_part = [&](int t, int buf, int step) {
+    auto issue_part = [&](int tl, int buf, int step) {
+        const int t = kt_lo + tl;
         const int s = t < kt0 ? 0 : 1;
         const int k0 = (t < kt0 ? t : t - kt0) * BK;
         const uint32_t base = tile_base(buf);
@@ -312,6 +345,12 @@ __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        if constexpr (EPI == 0 && sizeof(CT) == 4) {
+            if (g.ksplit > 1) {
+                epilogue_atomic<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+                return;
+            }
+        }
         epilogue_rows<CT, EPI, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
     };
     strip(std::integral_constant<int, 0>{});
@@ -335,26 +374,48 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
         return GN_E_HIP;
     }
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_dma<TA, TB, CT, BM, BN, EPI>), dim3(tiles), dim3(256), smem, s, g);
+    if (g.ksplit > 1)
+        clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
+    hipLaunchKernelGGL((gemm_dma<TA, TB, CT, BM, BN, EPI>), dim3(tiles, g.ksplit), dim3(256), smem,
+                       s, g);
     GN_LAUNCH_CHECK("gemm (dma)");
     return GN_OK;
 }
 
 // Tile shape: fewest "rounds" of 256 CUs, ties broken toward the larger tile.
+// Split-K (two halves of K) is considered for a plain fp32 epilogue that overwrites C when
+// the K loop is long: it fills an otherwise under-occupied grid (weight gradients of small
+// projections over many tokens).
 template <bool TA, bool TB, typename CT, int EPI>
-int launch_shape(const GemmDesc& g, hipStream_t s) {
-    auto cost = [&](int bm, int bn) {
-        const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+int launch_shape(const GemmDesc& g0, hipStream_t s) {
+    GemmDesc g = g0;
+    const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
+    const bool can_split = EPI == 0 && sizeof(CT) == 4 && !g.accumulate && KT >= 32;
+    auto cost = [&](int bm, int bn, int ks) {
+        const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * ks;
         const long rounds = (tiles + 255) / 256;
-        return rounds * (long)bm * bn;  // ~ time: rounds x per-tile work
+        return rounds * (long)bm * bn * 2 / ks;  // ~ time: rounds x per-block work
     };
-    const long c256 = cost(256, 256), c256x128 = cost(256, 128), c128x256 = cost(128, 256),
-               c128 = cost(128, 128);
-    long best = c256;
+    static constexpr int shapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+    auto tiles_of = [&](int i) {
+        return (long)((g.M + shapes[i][0] - 1) / shapes[i][0]) * ((g.N + shapes[i][1] - 1) / shapes[i][1]);
+    };
+    long best = -1;
     int pick = 0;
-    if (c256x128 < best) { best = c256x128; pick = 1; }
-    if (c128x256 < best) { best = c128x256; pick = 2; }
-    if (c128 < best) { best = c128; pick = 3; }
+    for (int i = 0; i < 4; ++i) {
+        const long c = cost(shapes[i][0], shapes[i][1], 1);
+        if (best < 0 || c < best) { best = c; pick = i; }
+    }
+    // split only a grid that leaves CUs idle, and only for a clear gain (the split pays a
+    // clear of C and atomic adds)
+    int ks_pick = 1;
+    if (can_split && tiles_of(pick) < 256) {
+        for (int i = 0; i < 4; ++i) {
+            const long c = cost(shapes[i][0], shapes[i][1], 2);
+            if (c * 5 < best * 4) { best = c; pick = i; ks_pick = 2; }
+        }
+    }
+    g.ksplit = ks_pick;
     switch (pick) {
         case 0: return launch_t<TA, TB, CT, 256, 256, EPI>(g, s);
         case 1: return launch_t<TA, TB, CT, 256, 128, EPI>(g, s);

@@ -123,6 +123,23 @@ def test_linear_bf16(gn, M, N, K):
     assert rel_err(host(db), rb) < 1e-4
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 256, 256), (4096, 768, 512), (6144, 136, 200)])
+def test_linear_split_k_weight_gradient(gn, M, N, K):
+    """Long-K weight gradients with few output tiles take the two-way split-K path (fp32
+    atomics onto a cleared dW): same values as the oracle, and bit-identical across runs."""
+    r = rng_(14)
+    dY = rnd(r.standard_normal((M, N)).astype(np.float32))
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    W = rnd(r.standard_normal((N, K)).astype(np.float32))
+    tdY, tX, tW = dev(dY, torch.bfloat16), dev(X, torch.bfloat16), dev(W, torch.bfloat16)
+    _, dW1, db = gn.linear_bwd(tdY, tX, tW)
+    _, dW2, _ = gn.linear_bwd(tdY, tX, tW)
+    _, rW, rb = oracle.linear_bwd(dY, X, W)
+    assert rel_err(host(dW1), rW) < FP32_TOL
+    assert rel_err(host(db), rb) < FP32_TOL
+    assert torch.equal(dW1, dW2)
+
+
 def test_linear_no_dx_and_accumulate(gn):
     g = golden("linear_small")
     dY, X, W = dev(g["dY"]), dev(g["X"]), dev(g["W"])
