@@ -255,6 +255,66 @@ __global__ __launch_bounds__(256) void colsum_kernel(const TI* __restrict__ in, 
     else atomicAdd(out + n, s);
 }
 
+// Deterministic two-pass column sums through a scratch array of R partial rows:
+//   pass 1 (grid: 512-column strips x R row ranges, 4 waves): lane l adds 8 consecutive
+//           columns over its wave's rows, the 4 waves combine in LDS in a fixed order;
+//   pass 2: out[n] (+)= sum_r part[r][n], r in order.
+template <typename TI>
+__global__ __launch_bounds__(256) void colsum_part(const TI* __restrict__ in, float* __restrict__ part,
+                                                   int M, int N, int ld, int rows_per) {
+    __shared__ float sh[4][512];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c0 = blockIdx.x * 512 + 8 * lane;
+    const int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (c0 < N) {
+#pragma unroll 4
+        for (int r = r0 + wave; r < r1; r += 4) {
+            const TI* p = in + (size_t)r * ld + c0;
+            if constexpr (sizeof(TI) == 2) {
+                const uint4 v = *reinterpret_cast<const uint4*>(p);
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    s[2 * e] += __uint_as_float(w[e] << 16);
+                    s[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+                }
+            } else {
+                const float4 a = reinterpret_cast<const float4*>(p)[0];
+                const float4 b = reinterpret_cast<const float4*>(p)[1];
+                s[0] += a.x; s[1] += a.y; s[2] += a.z; s[3] += a.w;
+                s[4] += b.x; s[5] += b.y; s[6] += b.z; s[7] += b.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sh[wave][8 * lane + e] = s[e];
+    __syncthreads();
+    for (int i = threadIdx.x; i < 512; i += 256) {
+        const int c = blockIdx.x * 512 + i;
+        if (c < N) part[(size_t)blockIdx.y * N + c] = ((sh[0][i] + sh[1][i]) + sh[2][i]) + sh[3][i];
+    }
+}
+
+// 64 columns x 16 row groups per block; the groups combine in LDS in a fixed order
+__global__ __launch_bounds__(1024) void colsum_finish(const float* __restrict__ part, int R, int N,
+                                                      float* __restrict__ out, int accumulate) {
+    __shared__ float sh[16][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int n = blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (n < N)
+        for (int r = w; r < R; r += 16) s += part[(size_t)r * N + n];
+    sh[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && n < N) {
+        float t = sh[0][lane];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) t += sh[i][lane];
+        out[n] = accumulate ? out[n] + t : t;
+    }
+}
+
 __global__ void zero_kernel(float* p, int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = 0.f;
@@ -368,11 +428,27 @@ int gemm_dispatch(const void* A0, const void* B0, int K0, const void* A1, const 
 }
 
 int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigned flags,
-                    hipStream_t s, int ld) {
+                    hipStream_t s, int ld, float* scratch, size_t scratch_floats) {
     if (ld <= 0) ld = N;
     GN_REQUIRE(M >= 0 && N >= 0, "gn_colsum: negative size");
     if (N == 0) return GN_OK;
     GN_REQUIRE(in && out, "gn_colsum: null pointer");
+    const size_t es = dtype == GN_F32 ? 4 : 2;
+    const bool vec = N % 8 == 0 && ld % 8 == 0 && al16(in) && (dtype == GN_F32 || dtype == GN_BF16);
+    if (scratch && vec && M > 0 && scratch_floats >= (size_t)N) {
+        const int cb = (N + 511) / 512;
+        int R = std::max(1, std::min({(M + 31) / 32, 512 / cb, (int)std::min<size_t>(scratch_floats / N, 4096)}));
+        const int rows_per = (M + R - 1) / R;
+        R = (M + rows_per - 1) / rows_per;
+        if (dtype == GN_F32)
+            colsum_part<float><<<dim3(cb, R), 256, 0, s>>>((const float*)in, scratch, M, N, ld, rows_per);
+        else
+            colsum_part<bf16_t><<<dim3(cb, R), 256, 0, s>>>((const bf16_t*)in, scratch, M, N, ld, rows_per);
+        colsum_finish<<<(N + 63) / 64, 1024, 0, s>>>(scratch, R, N, out, (flags & GN_ACCUMULATE) ? 1 : 0);
+        GN_LAUNCH_CHECK("gn_colsum (two-pass)");
+        return GN_OK;
+    }
+    (void)es;
     if (!(flags & GN_ACCUMULATE)) zero_kernel<<<(N + 255) / 256, 256, 0, s>>>(out, N);
     if (M == 0) { GN_LAUNCH_CHECK("gn_colsum"); return GN_OK; }
     // enough (column-block x row-split) work items to occupy the GPU
@@ -404,7 +480,7 @@ extern "C" int gn_gemm(const void* A0, const void* B0, int K0, const void* A1, c
 extern "C" int gn_colsum(const void* in, float* out, int M, int N, int dtype, unsigned flags,
                          void* stream) {
     clear_error();
-    return colsum_dispatch(in, out, M, N, dtype, flags, as_stream(stream), N);
+    return colsum_dispatch(in, out, M, N, dtype, flags, as_stream(stream), N, nullptr, 0);
 }
 
 // Linear backward (autograd.cpp:172-305): three stream-ordered launches, no host sync.
@@ -421,11 +497,13 @@ extern "C" int gn_linear_bwd(const void* dY, const void* X, const void* W, void*
         rc = gemm_dispatch(dY, W, N, nullptr, nullptr, 0, dX, M, K, 0, 0, dtype, dtype, flags, s);
         if (rc) return rc;
     }
+    // db first while dW (overwritten next, unless accumulating) can serve as its scratch
+    const bool scratch_ok = !(flags & GN_ACCUMULATE);
+    if (db && (rc = colsum_dispatch(dY, (float*)db, M, N, dtype, flags, s, N,
+                                    scratch_ok ? (float*)dW : nullptr, (size_t)N * K)))
+        return rc;
     // dW[N x K] = dY^T . X  (A = dY stored [M x N] = [Ks x Mout], transposed)
-    rc = gemm_dispatch(dY, X, M, nullptr, nullptr, 0, dW, N, K, 1, 0, dtype, GN_F32, flags, s);
-    if (rc) return rc;
-    if (db) return colsum_dispatch(dY, (float*)db, M, N, dtype, flags, s, N);
-    return GN_OK;
+    return gemm_dispatch(dY, X, M, nullptr, nullptr, 0, dW, N, K, 1, 0, dtype, GN_F32, flags, s);
 }
 
 namespace gn {
@@ -458,18 +536,19 @@ extern "C" int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, co
         d.M = M; d.N = K; d.C = dX; d.C2 = dX; d.Msplit = M; d.ldc = K; d.accumulate = acc;
         if ((rc = gemm_run(d, 0, 0, dtype, dtype, s))) return rc;
     }
-    {
-        GemmDesc d{};
-        d.nseg = 1;
-        d.A[0] = (const bf16_t*)g0; d.lda[0] = 2 * H; d.Ks[0] = M;
-        d.B[0] = (const bf16_t*)X; d.ldb[0] = K;
-        d.M = 2 * H; d.N = K; d.C = dWg; d.C2 = dWu; d.Msplit = H; d.ldc = K; d.accumulate = acc;
-        if ((rc = gemm_run(d, 1, 0, dtype, GN_F32, s))) return rc;
-    }
-    if (dbg && (rc = colsum_dispatch(g0, (float*)dbg, M, H, dtype, flags, s, 2 * H))) return rc;
-    if (dbu && (rc = colsum_dispatch(g0 + (size_t)H * esz, (float*)dbu, M, H, dtype, flags, s, 2 * H)))
+    // bias sums first, with dWg (overwritten next unless accumulating) as their scratch
+    float* scr = acc ? nullptr : (float*)dWg;
+    if (dbg && (rc = colsum_dispatch(g0, (float*)dbg, M, H, dtype, flags, s, 2 * H, scr, (size_t)H * K)))
         return rc;
-    return GN_OK;
+    if (dbu && (rc = colsum_dispatch(g0 + (size_t)H * esz, (float*)dbu, M, H, dtype, flags, s, 2 * H,
+                                     scr, (size_t)H * K)))
+        return rc;
+    GemmDesc d{};
+    d.nseg = 1;
+    d.A[0] = (const bf16_t*)g0; d.lda[0] = 2 * H; d.Ks[0] = M;
+    d.B[0] = (const bf16_t*)X; d.ldb[0] = K;
+    d.M = 2 * H; d.N = K; d.C = dWg; d.C2 = dWu; d.Msplit = H; d.ldc = K; d.accumulate = acc;
+    return gemm_run(d, 1, 0, dtype, GN_F32, s);
 }
 
 extern "C" int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, const void* up,
@@ -511,8 +590,8 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
         d.gu = (bf16_t*)gu; d.ldgu = 2 * H; d.H = H; d.glu_kind = kind;
         if ((rc = gemm_run(d, 0, 0, dtype, GN_BF16, s))) return rc;
     }
-    rc = gemm_dispatch(dY, A, M, nullptr, nullptr, 0, dWd, N, H, 1, 0, dtype, GN_F32, flags, s);
-    if (rc) return rc;
-    if (dbd) return colsum_dispatch(dY, (float*)dbd, M, N, dtype, flags, s, N);
-    return GN_OK;
+    if (dbd && (rc = colsum_dispatch(dY, (float*)dbd, M, N, dtype, flags, s, N,
+                                     (flags & GN_ACCUMULATE) ? nullptr : (float*)dWd, (size_t)N * H)))
+        return rc;
+    return gemm_dispatch(dY, A, M, nullptr, nullptr, 0, dWd, N, H, 1, 0, dtype, GN_F32, flags, s);
 }

@@ -181,7 +181,7 @@ inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 }  // namespace
 
 int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigned flags,
-                    hipStream_t s, int ld);
+                    hipStream_t s, int ld, float* scratch = nullptr, size_t scratch_floats = 0);
 
 }  // namespace gn
 
@@ -209,12 +209,17 @@ extern "C" int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, 
     hipStream_t s = as_stream(stream);
     const int tiles = ((O + VBM - 1) / VBM) * ((D + VBN - 1) / VBN);
     const int acc = (flags & GN_ACCUMULATE) ? 1 : 0;
+    // db first, with dW (overwritten next unless accumulating) as its scratch
+    if (db) {
+        const int rc = colsum_dispatch(dY, db, Bn, O, dtype, flags, s, O, acc ? nullptr : dW,
+                                       (size_t)O * D);
+        if (rc) return rc;
+    }
     const int vec_ok = (O % 8 == 0) && al16(dY);
     if (dtype == GN_F32)
         vsa_dw_kernel<true><<<tiles, 256, 0, s>>>(dY, Xbits, dW, Bn, O, D, words, acc, vec_ok);
     else
         vsa_dw_kernel<false><<<tiles, 256, 0, s>>>(dY, Xbits, dW, Bn, O, D, words, acc, vec_ok);
     GN_LAUNCH_CHECK("gn_vsa_unpack_project_bwd");
-    if (db) return colsum_dispatch(dY, db, Bn, O, dtype, flags, s, O);
     return GN_OK;
 }
