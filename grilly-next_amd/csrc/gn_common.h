@@ -40,17 +40,16 @@ typedef uint16_t bf16_t;  // raw bf16 bits in memory
 
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// round-to-nearest-even float -> bf16 (NaN stays NaN)
-__device__ __forceinline__ bf16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (bf16_t)(u >> 16);
-}
+// round-to-nearest-even float -> bf16 (NaN stays NaN): gfx950's v_cvt_pk_bf16_f32
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
-// pack two floats into one dword of bf16 (lo = a, hi = b)
+// pack two floats into one dword of bf16 (lo = a, hi = b), one v_cvt_pk_bf16_f32
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    bf16x2_v v;
+    v[0] = (__bf16)a;
+    v[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 template <typename T> struct io;

@@ -419,6 +419,71 @@ __global__ __launch_bounds__(256) void xent_bwd_kernel(const T* __restrict__ Z,
     }
 }
 
+// bf16 rows that fit in registers (C % 8 == 0, C <= 2048 NCH): each row is read once with
+// 16-byte loads and kept packed in VGPRs through the max, the sum of exp and the gradient
+// (cross-entropy-backward.glsl:41-84 does three passes over the row in memory).
+template <int NCH>
+__global__ __launch_bounds__(256) void xent_bwd_rows_bf16(const bf16_t* __restrict__ Z,
+                                                          const int32_t* __restrict__ tgt,
+                                                          bf16_t* __restrict__ dZ, int C,
+                                                          float scale) {
+    __shared__ float sh[4];
+    constexpr float kLog2e = 1.4426950408889634f;
+    const size_t off = (size_t)blockIdx.x * C;
+    const int nch = C >> 3;
+    uint4 v[NCH];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        const int c = threadIdx.x + 256 * j;
+        v[j] = c < nch ? *reinterpret_cast<const uint4*>(Z + off + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        if (threadIdx.x + 256 * j >= nch) continue;
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            m = fmaxf(m, fmaxf(__uint_as_float(w[e] << 16), __uint_as_float(w[e] & 0xffff0000u)));
+    }
+    const float M = block_max<4>(m, sh);
+    const float mb = M * kLog2e;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        if (threadIdx.x + 256 * j >= nch) continue;
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            s += __builtin_amdgcn_exp2f(__uint_as_float(w[e] << 16) * kLog2e - mb);
+            s += __builtin_amdgcn_exp2f(__uint_as_float(w[e] & 0xffff0000u) * kLog2e - mb);
+        }
+    }
+    const float S = block_sum<4>(s, sh);
+    const float inv = scale / fmaxf(S, 1e-30f);
+    const int t = tgt[blockIdx.x];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        const int c = threadIdx.x + 256 * j;
+        if (c >= nch) continue;
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        float g[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            g[2 * e] = __builtin_amdgcn_exp2f(__uint_as_float(w[e] << 16) * kLog2e - mb) * inv;
+            g[2 * e + 1] = __builtin_amdgcn_exp2f(__uint_as_float(w[e] & 0xffff0000u) * kLog2e - mb) * inv;
+        }
+        const int rel = t - 8 * c;
+        if (rel >= 0 && rel < 8) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (e == rel) g[e] -= scale;
+        }
+        *reinterpret_cast<uint4*>(dZ + off + 8 * c) =
+            make_uint4(pack_bf2(g[0], g[1]), pack_bf2(g[2], g[3]), pack_bf2(g[4], g[5]), pack_bf2(g[6], g[7]));
+    }
+}
+
 }  // namespace
 }  // namespace gn
 
@@ -496,8 +561,18 @@ extern "C" int gn_xent_bwd(const void* logits, const int32_t* targets, void* dLo
     hipStream_t s = as_stream(stream);
     if (dtype == GN_F32)
         xent_bwd_kernel<float><<<rows, 256, 0, s>>>((const float*)logits, targets, (float*)dLogits, C, scale);
-    else if (dtype == GN_BF16)
-        xent_bwd_kernel<bf16_t><<<rows, 256, 0, s>>>((const bf16_t*)logits, targets, (bf16_t*)dLogits, C, scale);
+    else if (dtype == GN_BF16) {
+        const bool vec = C % 8 == 0 && ((uintptr_t)logits & 15u) == 0 && ((uintptr_t)dLogits & 15u) == 0;
+        const int nch = (C / 8 + 255) / 256;  // 16-byte chunks per thread
+        if (vec && nch <= 4)
+            xent_bwd_rows_bf16<4><<<rows, 256, 0, s>>>((const bf16_t*)logits, targets, (bf16_t*)dLogits, C, scale);
+        else if (vec && nch <= 8)
+            xent_bwd_rows_bf16<8><<<rows, 256, 0, s>>>((const bf16_t*)logits, targets, (bf16_t*)dLogits, C, scale);
+        else if (vec && nch <= 16)
+            xent_bwd_rows_bf16<16><<<rows, 256, 0, s>>>((const bf16_t*)logits, targets, (bf16_t*)dLogits, C, scale);
+        else
+            xent_bwd_kernel<bf16_t><<<rows, 256, 0, s>>>((const bf16_t*)logits, targets, (bf16_t*)dLogits, C, scale);
+    }
     else {
         set_error("gn_xent_bwd: dtype %d not supported", dtype);
         return GN_E_INVALID;
