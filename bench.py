@@ -50,6 +50,9 @@ def parse():
                    help="after the timed region, launch one gn_add_inplace over 2^28 floats "
                         "(reads 2 GiB, writes 1 GiB): the reference dispatch that scales the "
                         "FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
+    p.add_argument("--ceilings", action="store_true",
+                   help="measure this box's MFMA (bf16 32x32x16 loop) and HBM (16-byte copy) "
+                        "ceilings with the library's probe kernels and print them as JSON")
     p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                         "'bench.py --calib-copy' into the HBM traffic of the dominant kernel")
@@ -114,6 +117,31 @@ def pmc_summary(fetch_dir, write_dir):
     print("\n".join(lines))
 
 
+def ceilings(torch, gn):
+    """Measured ceilings: gn_probe_mfma (no memory traffic) and gn_probe_copy (2 GiB)."""
+    import ctypes
+    lib = gn.lib()
+    lib.gn_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.gn_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    blocks, iters = 4096, 2000
+    out = torch.empty(blocks * 256, device=dev)
+    s = gn._stream()
+    mf = timed(torch, lambda: gn._check(lib.gn_probe_mfma(out.data_ptr(), blocks, iters, s),
+                                        "gn_probe_mfma"), 5, 2)
+    flops = blocks * 4.0 * iters * 8 * 32768
+    nbytes = 1 << 31
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    cp = timed(torch, lambda: gn._check(lib.gn_probe_copy(dst.data_ptr(), src.data_ptr(), nbytes, s),
+                                        "gn_probe_copy"), 10, 3)
+    return {"mfma_bf16_tflops": round(flops / (mf * 1e-3) / 1e12, 1),
+            "mfma_spec_tflops": BF16_PEAK_TFLOPS,
+            "copy_gbs": round(2.0 * nbytes / (cp * 1e-3) / 1e9, 1), "hbm_spec_gbs": HBM_PEAK_GBS,
+            "probe": f"gn_probe_mfma {blocks} blocks x {iters} x 8 MFMA per wave; "
+                     f"gn_probe_copy {nbytes >> 30} GiB read + written"}
+
+
 def traffic_from_profile():
     """HBM bytes per launch of the dominant GEMM from the committed counter summary."""
     try:
@@ -168,16 +196,16 @@ def bench_attn(args, torch, gn):
     if not args.no_cpu:
         import oracle
         r = np.random.default_rng(3)
-        Hs, Ss = H, S  # one of the four batch rows at full size (the rate is per flop)
-        q, k, v = (r.standard_normal((1, Hs, Ss, D)).astype(np.float32) for _ in range(3))
-        do = (r.standard_normal((1, Hs, Ss, D)) * 1e-2).astype(np.float32)
+        Bs, Hs, Ss = B, H, S  # the whole workload
+        q, k, v = (r.standard_normal((Bs, Hs, Ss, D)).astype(np.float32) for _ in range(3))
+        do = (r.standard_normal((Bs, Hs, Ss, D)) * 1e-2).astype(np.float32)
         o, lse = oracle.attn_fwd(q, k, v)
         t0 = time.perf_counter()
         oracle.attn_bwd(q, k, v, do, lse)
         dt = time.perf_counter() - t0
-        cpu = {"value": round(5 * 2.0 * Ss * Ss * D * 0.5 * Hs / dt / 1e12, 6), "unit": "TFLOP/s",
+        cpu = {"value": round(5 * 2.0 * Ss * Ss * D * 0.5 * Bs * Hs / dt / 1e12, 6), "unit": "TFLOP/s",
                "cores": oracle.num_threads(), "kind": "port",
-               "sample": f"1 x {Hs} heads x S={Ss} (oracle C/OpenMP fp64), {dt:.2f} s"}
+               "sample": f"{Bs} x {Hs} heads x S={Ss}, the whole workload (oracle C/OpenMP fp64), {dt:.2f} s"}
     return line("causal attention backward with RoPE (algorithmic TFLOP/s)", round(tf, 2),
                 "TFLOP/s", args, ms, "bf16",
                 {"workload": "C3 causal attention bwd + RoPE(1e4), B4 H16 S2048 D128",
@@ -216,7 +244,7 @@ def bench_vsa(args, torch, gn):
     cpu = None
     if not args.no_cpu:
         import oracle
-        Bs = 256
+        Bs = 4096  # half the rows: about 8 s of the oracle on the host
         bh = r.integers(0, 2**32, size=(Bs, words), dtype=np.uint64).astype(np.uint32)
         dy = r.standard_normal((Bs, O)).astype(np.float32)
         t0 = time.perf_counter()
@@ -460,6 +488,9 @@ def main():
     import torch
     import gn_bwd as gn
     gn.lib()
+    if args.ceilings:
+        print(json.dumps(ceilings(torch, gn)))
+        return
     if args.workload != "ffn":
         fn = {"attn": bench_attn, "vsa": bench_vsa, "mlp": bench_mlp,
               "decoder": bench_decoder}[args.workload]

@@ -1,0 +1,24 @@
+/* gn_probe.h — measurement helpers exported by libgn_bwd.so next to the backward ABI.
+ * They have no counterpart in the reference: bench.py --ceilings uses them to re-measure the
+ * MFMA and HBM ceilings on the box it runs on.  All launches go on `stream`; no allocation. */
+#ifndef GN_PROBE_H
+#define GN_PROBE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* `blocks` x 256 threads; every wave issues iters x 8 v_mfma_f32_32x32x16_bf16 on independent
+ * accumulators (32768 FLOP each) and writes one float per thread to out[blocks * 256]. */
+int gn_probe_mfma(float* out, int blocks, int iters, void* stream);
+
+/* dst[0 .. bytes) = src[0 .. bytes) with 16-byte loads and stores (bytes read + bytes written). */
+int gn_probe_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -33,6 +33,15 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_library_exports_the_probes():
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "gn_probe.h")).read(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(gn_[a-z0-9_]+)\s*\(", text)))
+    assert names == ["gn_probe_copy", "gn_probe_mfma"]
+    lib = ctypes.CDLL(LIB)
+    assert all(hasattr(lib, n) for n in names)
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
 def test_python_frontend_lists_every_symbol():
     import gn_bwd
     assert sorted(gn_bwd.SYMBOLS) == declared()
