@@ -54,13 +54,14 @@ __device__ __forceinline__ void dma16(const bf16_t* g, uint32_t lds_base) {
 // R/8 DMA instructions, R/32 per wave).
 //   KC (k-contiguous): element (r, k) at P[r*ld + k]; tile stored [r][64], chunk-swizzled
 //   else (k-outer):    element (r, k) at P[k*ld + r]; tile stored [64][R], chunk-swizzled
-template <int R, bool KC, int J0 = 0, int J1 = R / 32>
+template <int R, bool KC, int NW, int J0 = 0, int J1 = R / (8 * NW)>
 __device__ __forceinline__ void stage(const bf16_t* __restrict__ P, int ld, int r0, int rlim,
                                       int k0, uint32_t s) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    static_assert(R % (8 * NW) == 0, "whole DMA instructions per wave");
 #pragma unroll
     for (int j = J0; j < J1; ++j) {
-        const int q = wave * (R / 32) + j;  // DMA instruction index: slots [64q, 64q+64)
+        const int q = wave * (R / (8 * NW)) + j;  // DMA instruction index: slots [64q, 64q+64)
         const int slot = 64 * q + lane;
         const bf16_t* src;
         if (KC) {
@@ -107,10 +108,9 @@ __device__ __forceinline__ bf16x8_t frag(const bf16_t* s, int row0, int ks) {
 
 // One k-tile of MFMAs from LDS buffers (sa, sb); fragments of k-step ks+1 are requested
 // before the MFMAs of k-step ks are issued.
-template <bool TA, bool TB, int BM, int BN, int FM, int FN, typename HOOK>
+template <bool TA, bool TB, int BM, int BN, int WM, int WN, int FM, int FN, typename HOOK>
 __device__ __forceinline__ void compute_tile(const bf16_t* sa, const bf16_t* sb, int wm, int wn,
                                              f32x16_t (&acc)[FM][FN], HOOK&& after_step) {
-    constexpr int WM = BM / 2, WN = BN / 2;
     bf16x8_t a[2][FM], b[2][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i) a[0][i] = frag<BM, !TA>(sa, wm * WM + i * 32, 0);
@@ -243,14 +243,17 @@ constexpr int gemm_stages() {
     return (!TA && 3 * (BM + BN) * BK * 2 <= 160 * 1024) ? 3 : 2;
 }
 
-template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
+// NW = 4: waves 2 x 2; NW = 8: waves 4 (rows) x 2 (columns), two waves per SIMD.
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_dma(GemmDesc g) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     bf16_t* sbase = reinterpret_cast<bf16_t*>(smem_raw);
     constexpr int STAGES = gemm_stages<TA, BM, BN>();
     constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
     constexpr int STAGE = A_ELEMS + B_ELEMS;
-    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    constexpr int WR = NW / 2;  // wave rows
+    constexpr int WM = BM / WR, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    static_assert(FM >= 1 && FN >= 1, "wave tile of at least 32 x 32");
     // LDS byte address of the dynamic allocation (for the DMA's M0 operand)
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)sbase;
 
@@ -289,8 +292,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
         const int t = kt_lo + tl;
         const int s = t < kt0 ? 0 : 1;
         const int k0 = (t < kt0 ? t : t - kt0) * BK;
-        stage<BM, !TA>(g.A[s], g.lda[s], m0, g.M, k0, tile_base(buf));
-        stage<BN, TB>(g.B[s], g.ldb[s], n0, g.N, k0, tile_base(buf) + A_ELEMS * 2u);
+        stage<BM, !TA, NW>(g.A[s], g.lda[s], m0, g.M, k0, tile_base(buf));
+        stage<BN, TB, NW>(g.B[s], g.ldb[s], n0, g.N, k0, tile_base(buf) + A_ELEMS * 2u);
     };
     // DMA of tile t split over the four k-steps of the current tile's MFMAs:
     // step 0/1 carry the A halves, steps 2/3 the B halves.
@@ -299,17 +302,18 @@ __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
         const int s = t < kt0 ? 0 : 1;
         const int k0 = (t < kt0 ? t : t - kt0) * BK;
         const uint32_t base = tile_base(buf);
-        constexpr int JA = BM / 32, JB = BN / 32;
+        constexpr int JA = BM / (8 * NW), JB = BN / (8 * NW);
+        static_assert(JA >= 2 && JB >= 2, "each DMA half holds one instruction per wave at least");
         switch (step) {
-            case 0: stage<BM, !TA, 0, JA / 2>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
-            case 1: stage<BM, !TA, JA / 2, JA>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
-            case 2: stage<BN, TB, 0, JB / 2>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
-            default: stage<BN, TB, JB / 2, JB>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
+            case 0: stage<BM, !TA, NW, 0, JA / 2>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
+            case 1: stage<BM, !TA, NW, JA / 2, JA>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
+            case 2: stage<BN, TB, NW, 0, JB / 2>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
+            default: stage<BN, TB, NW, JB / 2, JB>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
         }
     };
 
     // vmcnt immediate: outstanding DMA instructions of one tile per wave
-    constexpr int DMA_PER_TILE = (BM + BN) / 32;
+    constexpr int DMA_PER_TILE = (BM + BN) / (8 * NW);
     static_assert(DMA_PER_TILE < 64, "vmcnt is a 6-bit field");
     // s_waitcnt vmcnt(N) expcnt(7) lgkmcnt(15): vmcnt bits [3:0] and [15:14]
     constexpr unsigned WAIT_ONE_TILE =
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma(GemmDesc g) {
         const int nxt = t + STAGES - 1;  // tile whose DMA is issued during this compute
         const int nbuf = nxt % STAGES;
         const bf16_t* sa = sbase + (t % STAGES) * STAGE;
-        compute_tile<TA, TB, BM, BN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc,
+        compute_tile<TA, TB, BM, BN, WM, WN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc,
                                              [&](auto, int ks) {
                                                  if (nxt < KT) issue_part(nxt, nbuf, ks);
                                              });
@@ -365,10 +369,17 @@ bool allow_lds(F* fn, size_t bytes) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
 }
 
+constexpr int kGemmWaves = 8;
+
 template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
 int launch_t(const GemmDesc& g, hipStream_t s) {
-    constexpr size_t smem = (size_t)gemm_stages<TA, BM, BN>() * (BM + BN) * BK * sizeof(bf16_t);
-    static const bool ok = allow_lds(gemm_dma<TA, TB, CT, BM, BN, EPI>, smem);
+    constexpr int NW = kGemmWaves;
+    // operand stages, or the epilogue's per-wave fp32 strips [32][BN/2 + 4] if larger
+    constexpr size_t stages_b = (size_t)gemm_stages<TA, BM, BN>() * (BM + BN) * BK * sizeof(bf16_t);
+    constexpr size_t strips_b = (size_t)NW * 32 * (BN / 2 + 4) * sizeof(float);
+    constexpr size_t smem = stages_b > strips_b ? stages_b : strips_b;
+    static_assert(smem <= 160 * 1024, "LDS per CU");
+    static const bool ok = allow_lds(gemm_dma<TA, TB, CT, BM, BN, EPI, NW>, smem);
     if (!ok) {
         set_error("gemm: cannot reserve %zu B of LDS", smem);
         return GN_E_HIP;
@@ -376,8 +387,8 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     if (g.ksplit > 1)
         clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
-    hipLaunchKernelGGL((gemm_dma<TA, TB, CT, BM, BN, EPI>), dim3(tiles, g.ksplit), dim3(256), smem,
-                       s, g);
+    hipLaunchKernelGGL((gemm_dma<TA, TB, CT, BM, BN, EPI, NW>), dim3(tiles, g.ksplit), dim3(64 * NW),
+                       smem, s, g);
     GN_LAUNCH_CHECK("gemm (dma)");
     return GN_OK;
 }
