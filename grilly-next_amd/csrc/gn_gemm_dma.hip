@@ -9,7 +9,7 @@
 //   * k-contiguous operand (rows of 64 k):   [row][k], 16-byte chunk c of row r stored at
 //     chunk c ^ swz(r); MFMA fragments are single ds_read_b128;
 //   * k-outer operand (rows of BM/BN columns): [k][col], chunk c of k-row k stored at
-//     c ^ 2(k & 3); fragments come from ds_read_b64_tr_b16, which transposes a 4(k) x 16
+//     c ^ fko(k); fragments come from ds_read_b64_tr_b16, which transposes a 4(k) x 16
 //     block across each 16-lane group (lane i gets column i, four consecutive k).
 // The DMA lane -> global-address map applies the inverse swizzle, so every DMA
 // instruction still reads whole 128-byte (or longer) row segments.
@@ -34,7 +34,11 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
 constexpr int BK = 64;
 
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
-__device__ __forceinline__ int fko(int k) { return 2 * (k & 3); }
+// k-outer tiles: chunk c of k-row k sits at c ^ fko(k), fko = {0, 6, 10, 12}[k & 3].  A
+// transpose read covers 4 consecutive k-rows x 64 bytes per 32 lanes; these four values
+// differ in bits 1-2 and in bits 2-3, so the read is conflict-free on a 32-bank and on a
+// 64-bank (gfx950) LDS alike (2(k & 3) left 2-way conflicts on 64 banks).
+__device__ __forceinline__ int fko(int k) { return ((k & 1) * 6) ^ (((k >> 1) & 1) * 10); }
 
 // One 16-byte DMA per lane: lane l's bytes land at LDS byte address lds_base + 16*l.
 // Issued from inline assembly: the compiler then does not order later LDS reads of the
