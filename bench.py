@@ -227,8 +227,9 @@ def bench_vsa(args, torch, gn):
     dY = torch.randn(Bn, O, device=dev, generator=g)
     dW = torch.empty(O, D, device=dev)
     db = torch.empty(O, device=dev)
-    ms = timed(torch, lambda: gn.vsa_unpack_project_bwd(dY, bits, D, dW=dW, db=db), args.steps,
-               args.warmup)
+    ws = gn.workspace(gn.vsa_workspace_bytes(Bn, O), dev)
+    ms = timed(torch, lambda: gn.vsa_unpack_project_bwd(dY, bits, D, dW=dW, db=db, ws=ws),
+               args.steps, args.warmup)
     flops = 2.0 * O * D * Bn
     tf = flops / (ms * 1e-3) / 1e12
     preds = torch.randn(Bn, K, D, device=dev, generator=g)
@@ -257,7 +258,8 @@ def bench_vsa(args, torch, gn):
                args, ms, "f32 (bf16x2 split MFMA)",
                {"workload": "C4 VSA unpack-project bwd: 8192 x 10240 bits -> 768, fp32 dY",
                 "rows": Bn, "vsa_dim": D, "out_dim": O},
-               {"kernel": "vsa_dw_kernel<true>", "bound": "mfma", "achieved": round(tf, 1),
+               {"kernel": "gn_vsa_unpack_project_bwd (dY split + vsa_dw_dma + db)", "bound": "mfma",
+                "achieved": round(tf, 1),
                 "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                 "traffic": None}, cpu)
     out["surrogate_bwd"] = {"ms": round(ms_s, 4), "GB/s": round(gbs, 1),

@@ -42,6 +42,24 @@ struct GemmDesc {
 template <typename CT, int EPI>
 __device__ __forceinline__ void gemm_store(const GemmDesc& g, int m, int n, float v);
 
+// VSA unpack-project weight gradient on the same core:
+//   C[M x N] (+)= sum_s A_s^T S,   A_s bf16 [K x M] (the split of dY into hi / lo bf16 parts,
+//   k-outer), S[k][n] = bit n of bits[k * words + n / 32] ? +1 : -1 (expanded in LDS).
+struct VsaDesc {
+    const bf16_t* A[2];
+    int nseg;       // 1 (bf16 dY) or 2 (fp32 dY as hi + lo)
+    int lda;        // = M
+    const uint32_t* bits;
+    int words;
+    int K, M, N;    // K = rows (batch), M = out_dim, N = vsa_dim
+    float* C;
+    int ldc;
+    int accumulate;
+    int ksplit;     // 2: blockIdx.y = segment, partial tiles added with fp32 atomics
+};
+bool vsa_dma_applicable(const VsaDesc& v);
+int vsa_dma_launch(const VsaDesc& v, hipStream_t s);
+
 bool gemm_dma_applicable(const GemmDesc& g);
 int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s);
 

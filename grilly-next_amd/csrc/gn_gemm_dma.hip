@@ -44,7 +44,7 @@ __device__ __forceinline__ int fko(int k) { return ((k & 1) * 6) ^ (((k >> 1) & 
 // Issued from inline assembly: the compiler then does not order later LDS reads of the
 // *other* stage behind this DMA (it cannot tell the two stages apart); the kernel waits
 // for its own DMA explicitly (s_waitcnt vmcnt(0) + barrier) before reading a stage.
-__device__ __forceinline__ void dma16(const bf16_t* g, uint32_t lds_base) {
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
     asm volatile(
         "s_mov_b32 m0, %0\n\t"
         "s_nop 0\n\t"
@@ -53,6 +53,10 @@ __device__ __forceinline__ void dma16(const bf16_t* g, uint32_t lds_base) {
         : "s"(lds_base), "v"(g)
         : "memory", "m0");
 }
+
+// s_waitcnt immediate: at most N vector-memory operations outstanding (vmcnt bits [3:0]
+// and [15:14]; expcnt and lgkmcnt left at their maxima)
+constexpr unsigned vmcnt_imm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
 
 // Stage one operand tile of R rows/cols (R = BM or BN) into LDS (R*64 bf16 = R*8 chunks,
 // R/8 DMA instructions, R/32 per wave).
@@ -367,6 +371,123 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma(GemmDesc g) {
     if constexpr (FM > 3) strip(std::integral_constant<int, 3>{});
 }
 
+// ---- VSA unpack-project dW --------------------------------------------------------------
+// Block tile BM x BN over K, 8 waves as in gemm_dma.  Per k-tile: the A tile (dY part,
+// k-outer) and the block's raw bit words (64 rows x BN/32 words) arrive by LDS DMA; each wave
+// then expands the rows it fetched into the ±1 bf16 B tile ([64][BN], k-outer swizzle), so
+// the expansion runs once per block and k-tile, never per fragment.  The B tile of tile t+1
+// is expanded at the end of iteration t (its DMA was issued one tile earlier) and becomes
+// visible at the next barrier.
+constexpr int kVsaBM = 256, kVsaBN = 128, kVsaNW = 8;
+
+__device__ __forceinline__ void vsa_expand_rows(const uint32_t* raw, bf16_t* sb, int wave, int lane) {
+    constexpr int BN = kVsaBN, WPR = BN / 32;  // words per k-row
+    // wave w expands k-rows 8w .. 8w+7 (the rows its own DMA fetched): 8 threads per row,
+    // each 16 bits -> two 16-byte chunks
+    const int r = 8 * wave + (lane >> 3), q = lane & 7;
+    const int wc = q >> 1, half = q & 1;
+    const uint32_t b16 = (raw[r * WPR + wc] >> (16 * half)) & 0xffffu;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t b8 = b16 >> (8 * h);
+        uint32_t d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)  // bit 1 -> +1.0 (0x3F80), bit 0 -> -1.0 (0xBF80)
+            d[i] = 0xBF80BF80u ^ (((b8 >> (2 * i)) & 1u) << 15) ^ (((b8 >> (2 * i + 1)) & 1u) << 31);
+        const int c = 4 * wc + 2 * half + h;  // 16-byte chunk of the k-row
+        *reinterpret_cast<uint4*>(sb + r * BN + ((c ^ fko(r)) * 8)) = make_uint4(d[0], d[1], d[2], d[3]);
+    }
+}
+
+__global__ __launch_bounds__(64 * kVsaNW, 1) void vsa_dw_dma(VsaDesc v) {
+    constexpr int BM = kVsaBM, BN = kVsaBN, NW = kVsaNW, STAGES = 3;
+    constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK, RAW_BYTES = 64 * (BN / 32) * 4;
+    constexpr int STAGE_B = (A_ELEMS + B_ELEMS) * 2 + RAW_BYTES;  // bytes per stage
+    constexpr int WM = BM / (NW / 2), WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem_raw;
+
+    const int tilesM = (v.M + BM - 1) / BM, tilesN = v.N / BN;
+    const int nblk = tilesM * tilesN;
+    int pid = blockIdx.x;
+    if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+    const int m0 = (pid % tilesM) * BM, n0 = (pid / tilesM) * BN;  // the M tiles of one n share bits
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    f32x16_t acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int ktps = v.K / BK;  // k-tiles per segment
+    const int seg_lo = v.ksplit > 1 ? (int)blockIdx.y : 0;
+    const int KT = v.ksplit > 1 ? ktps : ktps * v.nseg;
+    auto stage_base = [&](int buf) { return lds0 + (uint32_t)(buf * STAGE_B); };
+    auto issue = [&](int tl, int buf) {
+        const int seg = seg_lo + tl / ktps, k0 = (tl % ktps) * BK;
+        const uint32_t base = stage_base(buf);
+        stage<BM, false, NW>(v.A[seg], v.lda, m0, v.M, k0, base);
+        // raw bit words: wave w fetches k-rows 8w .. 8w+7, 16 bytes (BN / 32 words) each
+        if (lane < 8) {
+            const uint32_t* src = v.bits + (size_t)(k0 + 8 * wave + lane) * v.words + n0 / 32;
+            dma16(src, __builtin_amdgcn_readfirstlane(base + (A_ELEMS + B_ELEMS) * 2 + 128 * wave));
+        }
+    };
+    auto expand = [&](int buf) {
+        unsigned char* sbuf = smem_raw + buf * STAGE_B;
+        vsa_expand_rows(reinterpret_cast<const uint32_t*>(sbuf + (A_ELEMS + B_ELEMS) * 2),
+                        reinterpret_cast<bf16_t*>(sbuf) + A_ELEMS, wave, lane);
+    };
+    constexpr int DMA_PER_TILE = BM / (8 * NW) + 1;
+    constexpr unsigned WAIT_ONE_TILE = vmcnt_imm(DMA_PER_TILE);
+
+    issue(0, 0);
+    if (KT > 1) issue(1, 1);
+    // the raw bits of tile 0 come from this wave's own DMA: wait, expand
+    if (KT > 1) __builtin_amdgcn_s_waitcnt(WAIT_ONE_TILE);
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    expand(0);
+    for (int t = 0; t < KT; ++t) {
+        // tile t: A landed (checked at the end of iteration t-1, or above), B expanded
+        __syncthreads();
+        const int nxt = t + STAGES - 1;
+        const bf16_t* sa = reinterpret_cast<const bf16_t*>(smem_raw + (t % STAGES) * STAGE_B);
+        compute_tile<true, false, BM, BN, WM, WN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc,
+                                                           [&](auto, int ks) {
+                                                               if (ks == 0 && nxt < KT) issue(nxt, nxt % STAGES);
+                                                           });
+        if (t + 1 < KT) {
+            // tile t+1's DMA (issued during iteration t-1) has landed for this wave
+            if (nxt < KT) __builtin_amdgcn_s_waitcnt(WAIT_ONE_TILE);
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            expand((t + 1) % STAGES);
+        }
+    }
+
+    __syncthreads();
+    float* st = reinterpret_cast<float*>(smem_raw) + wave * 32 * (WN + 4);
+    const int rq = (lane >> 5) * 4;
+    GemmDesc g{};
+    g.M = v.M; g.N = v.N; g.C = v.C; g.C2 = v.C; g.Msplit = v.M; g.ldc = v.ldc;
+    g.accumulate = v.accumulate; g.ksplit = v.ksplit;
+    auto strip = [&](auto I_) {
+        constexpr int i = decltype(I_)::value;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        if (v.ksplit > 1) epilogue_atomic<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+        else epilogue_rows<float, 0, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+    };
+    strip(std::integral_constant<int, 0>{});
+    if constexpr (FM > 1) strip(std::integral_constant<int, 1>{});
+}
+
 template <typename F>
 bool allow_lds(F* fn, size_t bytes) {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -448,6 +569,38 @@ int launch_trans(const GemmDesc& g, int ta, int tb, hipStream_t s) {
 }
 
 }  // namespace
+
+bool vsa_dma_applicable(const VsaDesc& v) {
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (v.K % BK || v.N % kVsaBN || v.M % 8 || v.lda % 8 || v.ldc % 8 || v.words % 4) return false;
+    if (!al(v.C) || !al(v.bits) || !al(v.A[0]) || (v.nseg > 1 && !al(v.A[1]))) return false;
+    return v.K > 0 && v.M > 0 && v.N > 0;
+}
+
+int vsa_dma_launch(const VsaDesc& v0, hipStream_t s) {
+    VsaDesc v = v0;
+    constexpr int STAGE_B = (kVsaBM + kVsaBN) * BK * 2 + 64 * (kVsaBN / 32) * 4;
+    constexpr size_t strips = (size_t)kVsaNW * 32 * (kVsaBN / 2 + 4) * sizeof(float);
+    constexpr size_t smem = 3 * (size_t)STAGE_B > strips ? 3 * (size_t)STAGE_B : strips;
+    static_assert(smem <= 160 * 1024, "LDS per CU");
+    static const bool ok = allow_lds(vsa_dw_dma, smem);
+    if (!ok) {
+        set_error("vsa dW: cannot reserve %zu B of LDS", smem);
+        return GN_E_HIP;
+    }
+    // the two segments of an fp32 dY run as separate blocks onto a cleared C (exactly two
+    // atomic terms per element: deterministic) unless C must be accumulated into
+    v.ksplit = (v.nseg == 2 && !v.accumulate) ? 2 : 1;
+    if (v.ksplit > 1) {
+        GemmDesc g{};
+        g.M = v.M; g.N = v.N; g.C = v.C; g.C2 = v.C; g.Msplit = v.M; g.ldc = v.ldc;
+        clear_c<<<grid_for((int64_t)v.M * v.N, 256, 4096), 256, 0, s>>>(g);
+    }
+    const int tiles = ((v.M + kVsaBM - 1) / kVsaBM) * (v.N / kVsaBN);
+    hipLaunchKernelGGL(vsa_dw_dma, dim3(tiles, v.ksplit), dim3(64 * kVsaNW), smem, s, v);
+    GN_LAUNCH_CHECK("vsa dW (dma)");
+    return GN_OK;
+}
 
 bool gemm_dma_applicable(const GemmDesc& g) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };

@@ -10,6 +10,7 @@
 //
 // Tile 128 (o) x 128 (j) x 32 (b), 4 waves of 64 x 64 (2 x 2 v_mfma_f32_32x32x16_bf16).
 #include "gn_common.h"
+#include "gn_gemm_dma.h"
 
 namespace gn {
 namespace {
@@ -176,7 +177,29 @@ __global__ __launch_bounds__(256, 2) void vsa_dw_kernel(const void* __restrict__
         }
 }
 
+// fp32 dY -> (hi, lo) bf16 planes for the MFMA path: hi = bf16(dY), lo = bf16(dY - hi)
+// (the same two-term split vsa_dw_kernel forms in LDS); 8 elements per thread.
+__global__ __launch_bounds__(256) void vsa_split_dy(const float* __restrict__ dY, bf16_t* __restrict__ hi,
+                                                    bf16_t* __restrict__ lo, int64_t n8) {
+    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+        const float4 x = reinterpret_cast<const float4*>(dY)[2 * i];
+        const float4 y = reinterpret_cast<const float4*>(dY)[2 * i + 1];
+        const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            h[e] = pack_bf2(v[2 * e], v[2 * e + 1]);
+            const float r0 = v[2 * e] - __uint_as_float(h[e] << 16);
+            const float r1 = v[2 * e + 1] - __uint_as_float(h[e] & 0xffff0000u);
+            l[e] = pack_bf2(r0, r1);
+        }
+        reinterpret_cast<uint4*>(hi)[i] = make_uint4(h[0], h[1], h[2], h[3]);
+        reinterpret_cast<uint4*>(lo)[i] = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+}
+
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 }  // namespace
 
@@ -187,18 +210,18 @@ int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigne
 
 using namespace gn;
 
+// Workspace of the MFMA-DMA path for fp32 dY: the hi and lo bf16 planes of dY (bf16 dY
+// needs none).  Without it (or when the shape does not fit that path) the LDS-staging
+// kernel runs instead.
 extern "C" size_t gn_vsa_workspace_bytes(int Bn, int O) {
-    (void)Bn;
-    (void)O;
-    return 0;
+    if (Bn <= 0 || O <= 0) return 0;
+    return 2 * align256((size_t)Bn * O * sizeof(bf16_t));
 }
 
 extern "C" int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, float* dW,
                                          float* db, int Bn, int O, int D, int words, int dtype,
                                          unsigned flags, void* ws, size_t ws_bytes,
                                          void* stream) {
-    (void)ws;
-    (void)ws_bytes;
     clear_error();
     GN_REQUIRE(Bn >= 0 && O >= 0 && D >= 0, "gn_vsa_unpack_project_bwd: negative size");
     if (O == 0 || D == 0) return GN_OK;
@@ -214,6 +237,35 @@ extern "C" int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, 
         const int rc = colsum_dispatch(dY, db, Bn, O, dtype, flags, s, O, acc ? nullptr : dW,
                                        (size_t)O * D);
         if (rc) return rc;
+    }
+    // MFMA-DMA path: dY (or its hi / lo planes) k-outer, bits expanded in LDS per block
+    {
+        VsaDesc v{};
+        v.bits = Xbits;
+        v.words = words;
+        v.K = Bn; v.M = O; v.N = D;
+        v.C = dW; v.ldc = D; v.lda = O;
+        v.accumulate = acc;
+        const size_t plane = align256((size_t)Bn * O * sizeof(bf16_t));
+        bool have = true;
+        if (dtype == GN_F32) {
+            have = ws && ws_bytes >= 2 * plane && al16(ws) && al16(dY) && O % 8 == 0;
+            v.nseg = 2;
+            v.A[0] = static_cast<const bf16_t*>(ws);
+            v.A[1] = reinterpret_cast<const bf16_t*>(static_cast<const unsigned char*>(ws) + plane);
+        } else {
+            v.nseg = 1;
+            v.A[0] = v.A[1] = static_cast<const bf16_t*>(dY);
+        }
+        if (have && Bn > 0 && vsa_dma_applicable(v)) {
+            if (dtype == GN_F32) {
+                const int64_t n8 = (int64_t)Bn * O / 8;
+                vsa_split_dy<<<grid_for(n8, 256, 4096), 256, 0, s>>>(
+                    static_cast<const float*>(dY), const_cast<bf16_t*>(v.A[0]), const_cast<bf16_t*>(v.A[1]), n8);
+                GN_LAUNCH_CHECK("gn_vsa_unpack_project_bwd (split)");
+            }
+            return vsa_dma_launch(v, s);
+        }
     }
     const int vec_ok = (O % 8 == 0) && al16(dY);
     if (dtype == GN_F32)

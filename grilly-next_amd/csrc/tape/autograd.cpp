@@ -356,9 +356,12 @@ void BackwardEngine::bwd_vsa_unpack_project(Node* n) {
     const uint64_t W = n->saved_buffer_ids[0], b = n->num_saved > 1 ? n->saved_buffer_ids[1] : 0;
     uint64_t dW = alloc_grad((size_t)O * D * 4);
     uint64_t db = b ? alloc_grad((size_t)O * 4) : 0;
+    const int dt = gn_dtype(y.dtype, "VSAUnpackProject");
+    const size_t wsb = dt == GN_F32 ? gn_vsa_workspace_bytes(Bn, O) : 0;
+    uint64_t ws = wsb ? alloc_grad(wsb) : 0;
     gn_call(gn_vsa_unpack_project_bwd(gout(n), (const uint32_t*)P(bits.buffer_id), (float*)P(dW),
-                                      (float*)P(db), Bn, O, D, words, gn_dtype(y.dtype, "VSAUnpackProject"),
-                                      0, nullptr, 0, dev_.stream()), "VSA unpack-project backward");
+                                      (float*)P(db), Bn, O, D, words, dt, 0, P(ws), wsb, dev_.stream()),
+            "VSA unpack-project backward");
     stats_.shaders_dispatched += db ? 2 : 1;
     n->grad_input_buffers[0] = 0;  // bitpacked input: no gradient
     if (W) contribute(W, dW, 0, (size_t)O * D, true);

@@ -347,16 +347,27 @@ def attn_fwd(Q, K, V, scale=None, causal=True, rope="interleaved", theta=10000.0
     return O, LSE
 
 
-def vsa_unpack_project_bwd(dY, bits, D, need_db=True, dW=None, db=None, accumulate=False):
+def vsa_workspace_bytes(Bn, O):
+    return lib().gn_vsa_workspace_bytes(Bn, O)
+
+
+def vsa_unpack_project_bwd(dY, bits, D, need_db=True, dW=None, db=None, accumulate=False, ws=None):
+    """dW[o, j] (+)= sum_b dY[b, o] s_b(j) and db = sum_b dY[b]; fp32 dY uses a workspace of
+    vsa_workspace_bytes(Bn, O) (allocated here when not given; ws=False runs without one)."""
     Bn, O = dY.shape
     words = bits.shape[1]
     if dW is None:
         dW = torch.empty((O, D), dtype=torch.float32, device=dY.device)
     if need_db and db is None:
         db = torch.empty((O,), dtype=torch.float32, device=dY.device)
+    if ws is None and dY.dtype == torch.float32:
+        ws = workspace(vsa_workspace_bytes(Bn, O), dY.device)
+    ws = ws if ws is not None and ws is not False else None
     _check(lib().gn_vsa_unpack_project_bwd(_ptr(dY), _ptr(bits), _ptr(dW),
                                            _ptr(db) if need_db else None, Bn, O, D, words,
-                                           _dt(dY), ACCUMULATE if accumulate else 0, None, 0,
+                                           _dt(dY), ACCUMULATE if accumulate else 0,
+                                           _ptr(ws) if ws is not None else None,
+                                           ws.numel() * ws.element_size() if ws is not None else 0,
                                            _stream()), "gn_vsa_unpack_project_bwd")
     return dW, (db if need_db else None)
 

@@ -439,6 +439,52 @@ def test_vsa_project_fp32_split(gn, Bn, O, D):
     assert rel_err(host(db), rb) < FP32_TOL
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_vsa_project_mfma_path_popcount_exact(gn, dtype):
+    # shapes on the MFMA-DMA path (Bn % 64, D % 128), an O that leaves a partial 256-row
+    # tile, and bit rows padded past D/32 words: dW must equal 2 * popcount - Bn exactly
+    r = rng_(21)
+    Bn, O, D, words = 1024, 264, 1280, 44
+    bits = r.integers(0, 2**32, size=(Bn, words), dtype=np.uint64).astype(np.uint32)
+    dW, db = gn.vsa_unpack_project_bwd(dev(np.ones((Bn, O), np.float32), dtype),
+                                       gn.u32_tensor(bits, "cuda:0"), D)
+    pop = np.unpackbits(bits[:, :D // 32].view(np.uint8), axis=1, bitorder="little").sum(0).astype(np.int64)
+    np.testing.assert_array_equal(host(dW), np.tile(2 * pop - Bn, (O, 1)).astype(np.float32))
+    np.testing.assert_array_equal(host(db), np.full(O, Bn, np.float32))
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_vsa_project_mfma_path_fp32(gn, accumulate):
+    r = rng_(22)
+    Bn, O, D = 2048, 776, 2048
+    bits = r.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    dY = r.standard_normal((Bn, O)).astype(np.float32)
+    init = r.standard_normal((O, D)).astype(np.float32)
+    dW = dev(init) if accumulate else None
+    dW, db = gn.vsa_unpack_project_bwd(dev(dY), gn.u32_tensor(bits, "cuda:0"), D, dW=dW,
+                                       accumulate=accumulate)
+    rW, rb = oracle.vsa_unpack_project_bwd(dY, bits, D)
+    assert rel_err(host(dW), rW + (init if accumulate else 0)) < FP32_TOL
+    # the LDS-staging kernel (no workspace) agrees with the MFMA-DMA path
+    fW, _ = gn.vsa_unpack_project_bwd(dev(dY), gn.u32_tensor(bits, "cuda:0"), D, ws=False)
+    assert rel_err(host(fW), rW) < FP32_TOL
+    if not accumulate:
+        assert rel_err(host(dW), host(fW)) < FP32_TOL
+        # two segments onto a cleared output: the result is bitwise reproducible
+        dW2, _ = gn.vsa_unpack_project_bwd(dev(dY), gn.u32_tensor(bits, "cuda:0"), D)
+        assert torch.equal(dW, dW2)
+
+
+def test_vsa_project_mfma_path_bf16(gn):
+    r = rng_(23)
+    Bn, O, D = 1024, 512, 1024
+    bits = r.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    dY = rnd(r.standard_normal((Bn, O)).astype(np.float32))  # values exact in bf16
+    dW, db = gn.vsa_unpack_project_bwd(dev(dY, torch.bfloat16), gn.u32_tensor(bits, "cuda:0"), D)
+    rW, rb = oracle.vsa_unpack_project_bwd(dY, bits, D)
+    assert rel_err(host(dW), rW) < FP32_TOL and rel_err(host(db), rb) < FP32_TOL
+
+
 def test_vsa_surrogate_golden_and_random(gn):
     g = golden("vsa_surrogate")
     dP = gn.vsa_surrogate_bwd(dev(g["preds"]), gn.u32_tensor(g["bits"], "cuda:0"),
