@@ -43,19 +43,18 @@ template <typename CT, int EPI>
 __device__ __forceinline__ void gemm_store(const GemmDesc& g, int m, int n, float v);
 
 // VSA unpack-project weight gradient on the same core:
-//   C[M x N] (+)= sum_s A_s^T S,   A_s bf16 [K x M] (the split of dY into hi / lo bf16 parts,
-//   k-outer), S[k][n] = bit n of bits[k * words + n / 32] ? +1 : -1 (expanded in LDS).
+//   C[M x N] (+)= sum_s A_s S,   A_s bf16 [M x K] (the transposed hi / lo bf16 planes of dY,
+//   k-contiguous), S[k][n] = bit n % 32 of bits[k * words + n / 32] ? +1 : -1 (expanded in LDS).
 struct VsaDesc {
     const bf16_t* A[2];
     int nseg;       // 1 (bf16 dY) or 2 (fp32 dY as hi + lo)
-    int lda;        // = M
+    int lda;        // row pitch of A_s (>= K)
     const uint32_t* bits;
     int words;
     int K, M, N;    // K = rows (batch), M = out_dim, N = vsa_dim
     float* C;
     int ldc;
     int accumulate;
-    int ksplit;     // 2: blockIdx.y = segment, partial tiles added with fp32 atomics
 };
 bool vsa_dma_applicable(const VsaDesc& v);
 int vsa_dma_launch(const VsaDesc& v, hipStream_t s);

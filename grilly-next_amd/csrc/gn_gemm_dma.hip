@@ -372,45 +372,66 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma(GemmDesc g) {
 }
 
 // ---- VSA unpack-project dW --------------------------------------------------------------
-// Block tile BM x BN over K, 8 waves as in gemm_dma.  Per k-tile: the A tile (dY part,
-// k-outer) and the block's raw bit words (64 rows x BN/32 words) arrive by LDS DMA; each wave
-// then expands the rows it fetched into the ±1 bf16 B tile ([64][BN], k-outer swizzle), so
-// the expansion runs once per block and k-tile, never per fragment.  The B tile of tile t+1
-// is expanded at the end of iteration t (its DMA was issued one tile earlier) and becomes
-// visible at the next barrier.
-constexpr int kVsaBM = 256, kVsaBN = 128, kVsaNW = 8;
+// C[M x N] (+)= (A_hi + A_lo) S over K, one block per 128 x 256 tile, 4 waves (2 x 2) of
+// 64 x 128, one wave per SIMD.  Both dY planes (hi and lo, k-contiguous) share one +-1 B tile
+// per k-tile, so the bits are expanded once for both and no partial sums cross blocks.
+// Per k-tile (64 k):
+//   * A_hi, A_lo tiles arrive by LDS DMA two tiles ahead of use (stage = the tile's parity);
+//   * each lane loads two raw bit words of the tile after next into registers (plain global
+//     loads), and expands the words of the next tile into the B tile of the other stage while
+//     the MFMAs of the current tile run (the expansion is interleaved with them);
+//   * the barrier that closes k-step 2 publishes the next tile and frees the current stage,
+//     whose refill DMA then goes out while k-step 3 runs.
+constexpr int kVsaBM = 128, kVsaBN = 256, kVsaNW = 4;
 
-__device__ __forceinline__ void vsa_expand_rows(const uint32_t* raw, bf16_t* sb, int wave, int lane) {
-    constexpr int BN = kVsaBN, WPR = BN / 32;  // words per k-row
-    // wave w expands k-rows 8w .. 8w+7 (the rows its own DMA fetched): 8 threads per row,
-    // each 16 bits -> two 16-byte chunks
-    const int r = 8 * wave + (lane >> 3), q = lane & 7;
-    const int wc = q >> 1, half = q & 1;
-    const uint32_t b16 = (raw[r * WPR + wc] >> (16 * half)) & 0xffffu;
+struct VsaK {
+    static constexpr int BM = kVsaBM, BN = kVsaBN, NW = kVsaNW;
+    static constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    static constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
+    static constexpr int STAGE_B = (2 * A_ELEMS + B_ELEMS) * 2;  // hi, lo, B
+    static constexpr int WPR = BN / 32;                            // bit words per k-row
+    static constexpr int WPL = BK * WPR / (64 * NW);               // words expanded per lane
+    static constexpr size_t STRIPS = (size_t)NW * 32 * (WN + 4) * sizeof(float);
+    static constexpr size_t SMEM = 2 * (size_t)STAGE_B > STRIPS ? 2 * (size_t)STAGE_B : STRIPS;
+    static_assert(WPL == 2 && SMEM <= 160 * 1024, "tile shape");
+};
+
+// one 16-byte chunk (8 columns) of +-1 bf16 from byte b of the inverted bit word nw:
+// column bit 0 -> -1.0 (0xBF80), 1 -> +1.0 (0x3F80).  t2 holds the byte at bits 0-7 and
+// again at 15-22, so one shift puts bit 2e at 15 and bit 2e+1 at 31.
+__device__ __forceinline__ uint4 vsa_chunk(uint32_t nw, int b) {
+    const uint32_t t = (nw >> (8 * b)) & 0xffu;
+    const uint32_t t2 = t | (t << 15);
+    uint32_t d[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t b8 = b16 >> (8 * h);
-        uint32_t d[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)  // bit 1 -> +1.0 (0x3F80), bit 0 -> -1.0 (0xBF80)
-            d[i] = 0xBF80BF80u ^ (((b8 >> (2 * i)) & 1u) << 15) ^ (((b8 >> (2 * i + 1)) & 1u) << 31);
-        const int c = 4 * wc + 2 * half + h;  // 16-byte chunk of the k-row
-        *reinterpret_cast<uint4*>(sb + r * BN + ((c ^ fko(r)) * 8)) = make_uint4(d[0], d[1], d[2], d[3]);
+    for (int e = 0; e < 4; ++e) d[e] = ((t2 << (15 - 2 * e)) & 0x80008000u) | 0x3F803F80u;
+    return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+// Interleave: each MFMA followed by up to RD LDS reads, VA VALU, WR LDS writes, VM memory ops.
+template <int Q, int NM, int RD, int VA, int WR, int VM>
+__device__ __forceinline__ void vsa_sched() {
+    if constexpr (Q < NM) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (RD > 0) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+        if constexpr (VA > 0) __builtin_amdgcn_sched_group_barrier(0x002, VA, 0);
+        if constexpr (WR > 0) __builtin_amdgcn_sched_group_barrier(0x200, WR, 0);
+        if constexpr (VM > 0) __builtin_amdgcn_sched_group_barrier(0x010, VM, 0);
+        vsa_sched<Q + 1, NM, RD, VA, WR, VM>();
     }
 }
 
+template <bool TWO>
 __global__ __launch_bounds__(64 * kVsaNW, 1) void vsa_dw_dma(VsaDesc v) {
-    constexpr int BM = kVsaBM, BN = kVsaBN, NW = kVsaNW, STAGES = 3;
-    constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK, RAW_BYTES = 64 * (BN / 32) * 4;
-    constexpr int STAGE_B = (A_ELEMS + B_ELEMS) * 2 + RAW_BYTES;  // bytes per stage
-    constexpr int WM = BM / (NW / 2), WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    using C = VsaK;
+    constexpr int BM = C::BM, BN = C::BN, NW = C::NW, WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem_raw;
 
     const int tilesM = (v.M + BM - 1) / BM, tilesN = v.N / BN;
     const int nblk = tilesM * tilesN;
     int pid = blockIdx.x;
-    if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+    if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);  // XCD-contiguous ranges
     const int m0 = (pid % tilesM) * BM, n0 = (pid / tilesM) * BN;  // the M tiles of one n share bits
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -423,57 +444,136 @@ __global__ __launch_bounds__(64 * kVsaNW, 1) void vsa_dw_dma(VsaDesc v) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int ktps = v.K / BK;  // k-tiles per segment
-    const int seg_lo = v.ksplit > 1 ? (int)blockIdx.y : 0;
-    const int KT = v.ksplit > 1 ? ktps : ktps * v.nseg;
-    auto stage_base = [&](int buf) { return lds0 + (uint32_t)(buf * STAGE_B); };
-    auto issue = [&](int tl, int buf) {
-        const int seg = seg_lo + tl / ktps, k0 = (tl % ktps) * BK;
+    const int KT = v.K / BK;
+    const bf16_t* const Ahi = v.A[0];
+    const bf16_t* const Alo = v.A[1];
+    auto stage_base = [&](int buf) { return lds0 + (uint32_t)(buf * C::STAGE_B); };
+    auto dma_a = [&](int tl, int buf) {
         const uint32_t base = stage_base(buf);
-        stage<BM, false, NW>(v.A[seg], v.lda, m0, v.M, k0, base);
-        // raw bit words: wave w fetches k-rows 8w .. 8w+7, 16 bytes (BN / 32 words) each
-        if (lane < 8) {
-            const uint32_t* src = v.bits + (size_t)(k0 + 8 * wave + lane) * v.words + n0 / 32;
-            dma16(src, __builtin_amdgcn_readfirstlane(base + (A_ELEMS + B_ELEMS) * 2 + 128 * wave));
+        stage<BM, true, NW>(Ahi, v.lda, m0, v.M, tl * BK, base);
+        if constexpr (TWO) stage<BM, true, NW>(Alo, v.lda, m0, v.M, tl * BK, base + C::A_ELEMS * 2);
+    };
+    // raw words: lane (wave w, l), slot i -> k-row 16w + 8i + l/8, word l%8 of the tile's 8
+    const uint32_t* bits_base = v.bits + n0 / 32 + (lane & 7);
+    const int row_l = 16 * wave + (lane >> 3);
+    // raw bit words, two register sets used in turn: the set holding tile t+1's words is
+    // expanded during tile t and then reloaded with tile t+3's (never indexed dynamically)
+    uint32_t rx[2], ry[2];
+    auto load_raw = [&](int tl, uint32_t (&dst)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            dst[i] = __builtin_nontemporal_load(bits_base + (size_t)(tl * BK + row_l + 8 * i) * v.words);
+    };
+    // expand word slot i of set src into the B tile of stage buf: 4 chunks; the lanes
+    // holding words 4-7 of a row write their chunks rotated by one, so every 16-lane write
+    // cycle covers the 16 bank groups once
+    auto expand_word = [&](const uint32_t (&src)[2], int i, int buf) {
+        bf16_t* sb = reinterpret_cast<bf16_t*>(smem_raw + buf * C::STAGE_B) + 2 * C::A_ELEMS;
+        const int r = row_l + 8 * i, wc = lane & 7;
+        const uint32_t nw = ~src[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int b = (e + (wc >> 2)) & 3;
+            const int c = 4 * wc + b;
+            *reinterpret_cast<uint4*>(sb + r * BN + ((c ^ fko(r)) * 8)) = vsa_chunk(nw, b);
         }
     };
-    auto expand = [&](int buf) {
-        unsigned char* sbuf = smem_raw + buf * STAGE_B;
-        vsa_expand_rows(reinterpret_cast<const uint32_t*>(sbuf + (A_ELEMS + B_ELEMS) * 2),
-                        reinterpret_cast<bf16_t*>(sbuf) + A_ELEMS, wave, lane);
-    };
-    constexpr int DMA_PER_TILE = BM / (8 * NW) + 1;
-    constexpr unsigned WAIT_ONE_TILE = vmcnt_imm(DMA_PER_TILE);
-
-    issue(0, 0);
-    if (KT > 1) issue(1, 1);
-    // the raw bits of tile 0 come from this wave's own DMA: wait, expand
-    if (KT > 1) __builtin_amdgcn_s_waitcnt(WAIT_ONE_TILE);
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    expand(0);
-    for (int t = 0; t < KT; ++t) {
-        // tile t: A landed (checked at the end of iteration t-1, or above), B expanded
-        __syncthreads();
-        const int nxt = t + STAGES - 1;
-        const bf16_t* sa = reinterpret_cast<const bf16_t*>(smem_raw + (t % STAGES) * STAGE_B);
-        compute_tile<true, false, BM, BN, WM, WN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc,
-                                                           [&](auto, int ks) {
-                                                               if (ks == 0 && nxt < KT) issue(nxt, nxt % STAGES);
-                                                           });
-        if (t + 1 < KT) {
-            // tile t+1's DMA (issued during iteration t-1) has landed for this wave
-            if (nxt < KT) __builtin_amdgcn_s_waitcnt(WAIT_ONE_TILE);
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            expand((t + 1) % STAGES);
+    bf16x8_t fh[2][FM], fl[2][FM], fb[2][FN];
+    auto load_frags = [&](int buf, int ks, int slot) {
+        const bf16_t* sa = reinterpret_cast<const bf16_t*>(smem_raw + buf * C::STAGE_B);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fh[slot][i] = frag<BM, true>(sa, wm * WM + i * 32, ks);
+        if constexpr (TWO) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) fl[slot][i] = frag<BM, true>(sa + C::A_ELEMS, wm * WM + i * 32, ks);
         }
-    }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[slot][j] = frag<BN, false>(sa + 2 * C::A_ELEMS, wn * WN + j * 32, ks);
+    };
+    auto mfmas = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
+        if constexpr (TWO) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
+        }
+    };
+    constexpr int NM = FM * FN * (TWO ? 2 : 1);         // MFMAs per k-step
+    constexpr int NR = FM * (TWO ? 2 : 1) + 2 * FN;     // LDS reads per k-step
 
+    // prologue: tile 0 staged and expanded; tile 1's A DMA and the bits of tiles 1, 2 in
+    // flight.  Tail iterations clamp the tile they prefetch to the last one (in-bounds
+    // redundant work instead of branches that would split the interleaved schedule).
+    // (The DMA instructions are inline assembly that the compiler's wait-count bookkeeping
+    // does not see: every bit word is consumed only after an explicit full drain, so the
+    // compiler never has to place a vmcnt wait of its own.)
+    const int last = KT - 1;
+    load_raw(0, ry);
+    load_raw(min(1, last), rx);
+    dma_a(0, 0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    expand_word(ry, 0, 0);
+    expand_word(ry, 1, 0);
+    load_raw(min(2, last), ry);
+    dma_a(min(1, last), 1);
     __syncthreads();
+    load_frags(0, 0, 0);
+
+    // one k-tile; BUF = t & 1 is a compile-time constant, set holds tile t+1's bits
+    auto step = [&](auto BUF_, int t, uint32_t (&set)[2]) {
+        constexpr int buf = decltype(BUF_)::value;
+        // k-step 0: fragments of step 1, MFMAs of step 0, first word of tile t+1's bits
+        // (past the last tile the expansion rewrites the idle stage: harmless)
+        load_frags(buf, 1, 1);
+        mfmas(0);
+        expand_word(set, 0, buf ^ 1);
+        vsa_sched<0, NM, 1, 2, 1, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+        // k-step 1: second word
+        load_frags(buf, 2, 0);
+        mfmas(1);
+        expand_word(set, 1, buf ^ 1);
+        vsa_sched<0, NM, 1, 2, 1, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+        // k-step 2
+        load_frags(buf, 3, 1);
+        mfmas(0);
+        vsa_sched<0, NM, 1, 0, 0, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+        // tile t+1's A (and the bits of t+2) landed for this wave; the barrier publishes the
+        // B tile every wave expanded and retires every read of stage buf
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();
+        load_raw(min(t + 3, last), set);
+        dma_a(min(t + 2, last), buf);
+        load_frags(buf ^ 1, 0, 0);
+        mfmas(1);
+        vsa_sched<0, NM, 1, 2, 0, 1>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // pairs of tiles, so every path into the loop head has drained the set it expands next
+    int t = 0;
+    for (; t + 1 < KT; t += 2) {
+        step(std::integral_constant<int, 0>{}, t, rx);
+        step(std::integral_constant<int, 1>{}, t + 1, ry);
+    }
+    if (t < KT) step(std::integral_constant<int, 0>{}, t, rx);
+    // the clamped prefetches of the last iterations may still be landing in the stages
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+
+    // epilogue: one 32-row strip at a time
     float* st = reinterpret_cast<float*>(smem_raw) + wave * 32 * (WN + 4);
     const int rq = (lane >> 5) * 4;
     GemmDesc g{};
     g.M = v.M; g.N = v.N; g.C = v.C; g.C2 = v.C; g.Msplit = v.M; g.ldc = v.ldc;
-    g.accumulate = v.accumulate; g.ksplit = v.ksplit;
+    g.accumulate = v.accumulate;
     auto strip = [&](auto I_) {
         constexpr int i = decltype(I_)::value;
 #pragma unroll
@@ -481,8 +581,7 @@ __global__ __launch_bounds__(64 * kVsaNW, 1) void vsa_dw_dma(VsaDesc v) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
-        if (v.ksplit > 1) epilogue_atomic<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
-        else epilogue_rows<float, 0, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+        epilogue_rows<float, 0, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
     };
     strip(std::integral_constant<int, 0>{});
     if constexpr (FM > 1) strip(std::integral_constant<int, 1>{});
@@ -572,32 +671,28 @@ int launch_trans(const GemmDesc& g, int ta, int tb, hipStream_t s) {
 
 bool vsa_dma_applicable(const VsaDesc& v) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (v.K % BK || v.N % kVsaBN || v.M % 8 || v.lda % 8 || v.ldc % 8 || v.words % 4) return false;
-    if (!al(v.C) || !al(v.bits) || !al(v.A[0]) || (v.nseg > 1 && !al(v.A[1]))) return false;
+    if (v.K % BK || v.N % kVsaBN || v.lda % 8 || v.ldc % 8) return false;
+    if (!al(v.C) || !al(v.A[0]) || (v.nseg > 1 && !al(v.A[1]))) return false;
     return v.K > 0 && v.M > 0 && v.N > 0;
 }
 
-int vsa_dma_launch(const VsaDesc& v0, hipStream_t s) {
-    VsaDesc v = v0;
-    constexpr int STAGE_B = (kVsaBM + kVsaBN) * BK * 2 + 64 * (kVsaBN / 32) * 4;
-    constexpr size_t strips = (size_t)kVsaNW * 32 * (kVsaBN / 2 + 4) * sizeof(float);
-    constexpr size_t smem = 3 * (size_t)STAGE_B > strips ? 3 * (size_t)STAGE_B : strips;
-    static_assert(smem <= 160 * 1024, "LDS per CU");
-    static const bool ok = allow_lds(vsa_dw_dma, smem);
-    if (!ok) {
-        set_error("vsa dW: cannot reserve %zu B of LDS", smem);
-        return GN_E_HIP;
-    }
-    // the two segments of an fp32 dY run as separate blocks onto a cleared C (exactly two
-    // atomic terms per element: deterministic) unless C must be accumulated into
-    v.ksplit = (v.nseg == 2 && !v.accumulate) ? 2 : 1;
-    if (v.ksplit > 1) {
-        GemmDesc g{};
-        g.M = v.M; g.N = v.N; g.C = v.C; g.C2 = v.C; g.Msplit = v.M; g.ldc = v.ldc;
-        clear_c<<<grid_for((int64_t)v.M * v.N, 256, 4096), 256, 0, s>>>(g);
-    }
+int vsa_dma_launch(const VsaDesc& v, hipStream_t s) {
     const int tiles = ((v.M + kVsaBM - 1) / kVsaBM) * (v.N / kVsaBN);
-    hipLaunchKernelGGL(vsa_dw_dma, dim3(tiles, v.ksplit), dim3(64 * kVsaNW), smem, s, v);
+    if (v.nseg > 1) {
+        static const bool ok = allow_lds(vsa_dw_dma<true>, VsaK::SMEM);
+        if (!ok) {
+            set_error("vsa dW: cannot reserve %zu B of LDS", VsaK::SMEM);
+            return GN_E_HIP;
+        }
+        hipLaunchKernelGGL(vsa_dw_dma<true>, dim3(tiles), dim3(64 * kVsaNW), VsaK::SMEM, s, v);
+    } else {
+        static const bool ok = allow_lds(vsa_dw_dma<false>, VsaK::SMEM);
+        if (!ok) {
+            set_error("vsa dW: cannot reserve %zu B of LDS", VsaK::SMEM);
+            return GN_E_HIP;
+        }
+        hipLaunchKernelGGL(vsa_dw_dma<false>, dim3(tiles), dim3(64 * kVsaNW), VsaK::SMEM, s, v);
+    }
     GN_LAUNCH_CHECK("vsa dW (dma)");
     return GN_OK;
 }

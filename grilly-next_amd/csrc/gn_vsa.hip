@@ -177,24 +177,48 @@ __global__ __launch_bounds__(256, 2) void vsa_dw_kernel(const void* __restrict__
         }
 }
 
-// fp32 dY -> (hi, lo) bf16 planes for the MFMA path: hi = bf16(dY), lo = bf16(dY - hi)
-// (the same two-term split vsa_dw_kernel forms in LDS); 8 elements per thread.
-__global__ __launch_bounds__(256) void vsa_split_dy(const float* __restrict__ dY, bf16_t* __restrict__ hi,
-                                                    bf16_t* __restrict__ lo, int64_t n8) {
-    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
-        const float4 x = reinterpret_cast<const float4*>(dY)[2 * i];
-        const float4 y = reinterpret_cast<const float4*>(dY)[2 * i + 1];
-        const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+// dY [Bn x O] -> its transposed bf16 planes [O x Bn] for the MFMA path: hi = bf16(dY) and,
+// for fp32 dY, lo = bf16(dY - hi) (the same two-term split vsa_dw_kernel forms in LDS).
+// The transpose makes the batch (the contraction index) contiguous, so the dW kernel reads
+// its dY fragments with plain 16-byte LDS reads.  64 x 64 tiles through LDS; Bn % 64 == 0.
+template <typename T>
+__global__ __launch_bounds__(256) void vsa_split_dy_t(const T* __restrict__ dY, bf16_t* __restrict__ hi,
+                                                      bf16_t* __restrict__ lo, int Bn, int O) {
+    __shared__ float tile[64][65];
+    const int b0 = blockIdx.y * 64, o0 = blockIdx.x * 64, t = threadIdx.x;
+    // load: 64 rows (b) x 64 columns (o), 16 threads per row, 4 consecutive o per thread
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = (t >> 4) + 16 * i, c = (t & 15) * 4;
+        const int o = o0 + c;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        const size_t base = (size_t)(b0 + r) * O + o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (o + e < O) {
+                if constexpr (sizeof(T) == 4) v[e] = dY[base + e];
+                else v[e] = bf2f(dY[base + e]);
+            }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tile[r][c + e] = v[e];
+    }
+    __syncthreads();
+    // store: row o of the transposed planes, 8 consecutive b (one 16-byte chunk) per thread
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int orow = (t >> 3) + 32 * i, c = (t & 7) * 8;
+        const int o = o0 + orow;
+        if (o >= O) continue;
         uint32_t h[4], l[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            h[e] = pack_bf2(v[2 * e], v[2 * e + 1]);
-            const float r0 = v[2 * e] - __uint_as_float(h[e] << 16);
-            const float r1 = v[2 * e + 1] - __uint_as_float(h[e] & 0xffff0000u);
-            l[e] = pack_bf2(r0, r1);
+            const float x0 = tile[c + 2 * e][orow], x1 = tile[c + 2 * e + 1][orow];
+            h[e] = pack_bf2(x0, x1);
+            l[e] = pack_bf2(x0 - __uint_as_float(h[e] << 16), x1 - __uint_as_float(h[e] & 0xffff0000u));
         }
-        reinterpret_cast<uint4*>(hi)[i] = make_uint4(h[0], h[1], h[2], h[3]);
-        reinterpret_cast<uint4*>(lo)[i] = make_uint4(l[0], l[1], l[2], l[3]);
+        const size_t dst = (size_t)o * Bn + b0 + c;
+        *reinterpret_cast<uint4*>(hi + dst) = make_uint4(h[0], h[1], h[2], h[3]);
+        if (sizeof(T) == 4) *reinterpret_cast<uint4*>(lo + dst) = make_uint4(l[0], l[1], l[2], l[3]);
     }
 }
 
@@ -210,9 +234,9 @@ int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigne
 
 using namespace gn;
 
-// Workspace of the MFMA-DMA path for fp32 dY: the hi and lo bf16 planes of dY (bf16 dY
-// needs none).  Without it (or when the shape does not fit that path) the LDS-staging
-// kernel runs instead.
+// Workspace of the MFMA-DMA path: the transposed bf16 planes of dY (hi and lo for fp32 dY,
+// one plane for bf16).  Without it (or when the shape does not fit that path) the
+// LDS-staging kernel runs instead.
 extern "C" size_t gn_vsa_workspace_bytes(int Bn, int O) {
     if (Bn <= 0 || O <= 0) return 0;
     return 2 * align256((size_t)Bn * O * sizeof(bf16_t));
@@ -238,32 +262,29 @@ extern "C" int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, 
                                        (size_t)O * D);
         if (rc) return rc;
     }
-    // MFMA-DMA path: dY (or its hi / lo planes) k-outer, bits expanded in LDS per block
+    // MFMA-DMA path: dY as transposed bf16 planes (hi, and lo for fp32), bits expanded in
+    // LDS once per block and k-tile
     {
+        const size_t plane = align256((size_t)Bn * O * sizeof(bf16_t));
         VsaDesc v{};
         v.bits = Xbits;
         v.words = words;
         v.K = Bn; v.M = O; v.N = D;
-        v.C = dW; v.ldc = D; v.lda = O;
+        v.C = dW; v.ldc = D; v.lda = Bn;
         v.accumulate = acc;
-        const size_t plane = align256((size_t)Bn * O * sizeof(bf16_t));
-        bool have = true;
-        if (dtype == GN_F32) {
-            have = ws && ws_bytes >= 2 * plane && al16(ws) && al16(dY) && O % 8 == 0;
-            v.nseg = 2;
-            v.A[0] = static_cast<const bf16_t*>(ws);
-            v.A[1] = reinterpret_cast<const bf16_t*>(static_cast<const unsigned char*>(ws) + plane);
-        } else {
-            v.nseg = 1;
-            v.A[0] = v.A[1] = static_cast<const bf16_t*>(dY);
-        }
+        v.nseg = dtype == GN_F32 ? 2 : 1;
+        v.A[0] = static_cast<const bf16_t*>(ws);
+        v.A[1] = reinterpret_cast<const bf16_t*>(static_cast<const unsigned char*>(ws) + plane);
+        const bool have = ws && ws_bytes >= (size_t)v.nseg * plane && al16(ws);
         if (have && Bn > 0 && vsa_dma_applicable(v)) {
-            if (dtype == GN_F32) {
-                const int64_t n8 = (int64_t)Bn * O / 8;
-                vsa_split_dy<<<grid_for(n8, 256, 4096), 256, 0, s>>>(
-                    static_cast<const float*>(dY), const_cast<bf16_t*>(v.A[0]), const_cast<bf16_t*>(v.A[1]), n8);
-                GN_LAUNCH_CHECK("gn_vsa_unpack_project_bwd (split)");
-            }
+            const dim3 grid((O + 63) / 64, Bn / 64);
+            bf16_t* hi = const_cast<bf16_t*>(v.A[0]);
+            bf16_t* lo = const_cast<bf16_t*>(v.A[1]);
+            if (dtype == GN_F32)
+                vsa_split_dy_t<float><<<grid, 256, 0, s>>>(static_cast<const float*>(dY), hi, lo, Bn, O);
+            else
+                vsa_split_dy_t<bf16_t><<<grid, 256, 0, s>>>(static_cast<const bf16_t*>(dY), hi, lo, Bn, O);
+            GN_LAUNCH_CHECK("gn_vsa_unpack_project_bwd (transpose)");
             return vsa_dma_launch(v, s);
         }
     }

@@ -357,7 +357,7 @@ void BackwardEngine::bwd_vsa_unpack_project(Node* n) {
     uint64_t dW = alloc_grad((size_t)O * D * 4);
     uint64_t db = b ? alloc_grad((size_t)O * 4) : 0;
     const int dt = gn_dtype(y.dtype, "VSAUnpackProject");
-    const size_t wsb = dt == GN_F32 ? gn_vsa_workspace_bytes(Bn, O) : 0;
+    const size_t wsb = gn_vsa_workspace_bytes(Bn, O);
     uint64_t ws = wsb ? alloc_grad(wsb) : 0;
     gn_call(gn_vsa_unpack_project_bwd(gout(n), (const uint32_t*)P(bits.buffer_id), (float*)P(dW),
                                       (float*)P(db), Bn, O, D, words, dt, 0, P(ws), wsb, dev_.stream()),

@@ -352,15 +352,16 @@ def vsa_workspace_bytes(Bn, O):
 
 
 def vsa_unpack_project_bwd(dY, bits, D, need_db=True, dW=None, db=None, accumulate=False, ws=None):
-    """dW[o, j] (+)= sum_b dY[b, o] s_b(j) and db = sum_b dY[b]; fp32 dY uses a workspace of
-    vsa_workspace_bytes(Bn, O) (allocated here when not given; ws=False runs without one)."""
+    """dW[o, j] (+)= sum_b dY[b, o] s_b(j) and db = sum_b dY[b]; the MFMA path uses a
+    workspace of vsa_workspace_bytes(Bn, O) (allocated here when not given; ws=False runs
+    the LDS-staging kernel without one)."""
     Bn, O = dY.shape
     words = bits.shape[1]
     if dW is None:
         dW = torch.empty((O, D), dtype=torch.float32, device=dY.device)
     if need_db and db is None:
         db = torch.empty((O,), dtype=torch.float32, device=dY.device)
-    if ws is None and dY.dtype == torch.float32:
+    if ws is None:
         ws = workspace(vsa_workspace_bytes(Bn, O), dY.device)
     ws = ws if ws is not None and ws is not False else None
     _check(lib().gn_vsa_unpack_project_bwd(_ptr(dY), _ptr(bits), _ptr(dW),

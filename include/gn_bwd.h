@@ -215,9 +215,9 @@ int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O, float* LSE
  *   db[o]    (+)= sum_b dY[b, o]            [O] fp32 (skipped if NULL)
  * dY fp32 [Bn x O] (dtype GN_F32, fp32-accurate via a two-term bf16 split of dY) or bf16.
  * words = D/32 (D must be a multiple of 32).  ws (optional, 16-byte aligned):
- * gn_vsa_workspace_bytes(Bn, O) bytes for fp32 dY (holds its bf16 hi/lo planes); bf16 dY
- * needs none.  The MFMA path runs when D % 128 == 0, Bn % 64 == 0, O % 8 == 0 and words % 4 == 0
- * (and, for fp32 dY, the workspace is given); other shapes take an LDS-staging kernel. */
+ * gn_vsa_workspace_bytes(Bn, O) bytes (the transposed bf16 planes of dY).  The MFMA path runs
+ * when the workspace is given and D % 128 == 0, Bn % 64 == 0, words % 4 == 0;
+ * other calls take an LDS-staging kernel. */
 int gn_vsa_unpack_project_bwd(const void* dY, const uint32_t* Xbits, float* dW, float* db,
                               int Bn, int O, int D, int words, int dtype, unsigned flags,
                               void* ws, size_t ws_bytes, void* stream);

@@ -439,12 +439,13 @@ def test_vsa_project_fp32_split(gn, Bn, O, D):
     assert rel_err(host(db), rb) < FP32_TOL
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_vsa_project_mfma_path_popcount_exact(gn, dtype):
-    # shapes on the MFMA-DMA path (Bn % 64, D % 128), an O that leaves a partial 256-row
-    # tile, and bit rows padded past D/32 words: dW must equal 2 * popcount - Bn exactly
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 1280), (torch.bfloat16, 1280), (torch.float32, 1152)])
+def test_vsa_project_mfma_path_popcount_exact(gn, dtype, D):
+    # shapes on the MFMA-DMA path (Bn % 64, D % 128; D = 1152 takes the 128-column tiles),
+    # an O that leaves a partial 256-row tile, and bit rows padded past D/32 words: dW must
+    # equal 2 * popcount - Bn exactly
     r = rng_(21)
-    Bn, O, D, words = 1024, 264, 1280, 44
+    Bn, O, words = 1024, 264, D // 32 + 4
     bits = r.integers(0, 2**32, size=(Bn, words), dtype=np.uint64).astype(np.uint32)
     dW, db = gn.vsa_unpack_project_bwd(dev(np.ones((Bn, O), np.float32), dtype),
                                        gn.u32_tensor(bits, "cuda:0"), D)
@@ -456,7 +457,7 @@ def test_vsa_project_mfma_path_popcount_exact(gn, dtype):
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_vsa_project_mfma_path_fp32(gn, accumulate):
     r = rng_(22)
-    Bn, O, D = 2048, 776, 2048
+    Bn, O, D = 2048, 771, 2048  # O: a partial last row tile, not a multiple of 8
     bits = r.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
     dY = r.standard_normal((Bn, O)).astype(np.float32)
     init = r.standard_normal((O, D)).astype(np.float32)
