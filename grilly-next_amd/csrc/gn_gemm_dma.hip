@@ -16,7 +16,9 @@
 // Epilogues: plain store (bf16 or fp32, optional accumulate, optional row split into two
 // outputs) or the GLU epilogue, which turns the dA tile of the down projection straight
 // into the SwiGLU/GEGLU/ReGLU local gradients (dA never reaches HBM).
+#include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 #include "gn_common.h"
 #include "gn_math.h"
@@ -371,6 +373,188 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma(GemmDesc g) {
     if constexpr (FM > 3) strip(std::integral_constant<int, 3>{});
 }
 
+// ---- four-wave core ----------------------------------------------------------------------
+// Four waves (2 x 2, one per SIMD), wave tile (BM/2) x (BN/2), two LDS stages, and a k-tile
+// schedule in which nothing but MFMAs occupies the matrix pipe's critical path:
+//   k-steps 0-2: the fragments of the next step are requested between this step's MFMAs;
+//   then this wave's DMA of tile t+1 is drained and one barrier publishes tile t+1 and
+//   retires every read of tile t's stage; the DMA of tile t+2 refills that stage and the
+//   first fragments of tile t+1 are requested, interleaved with the MFMAs of k-step 3.
+// Tiles past the last one are clamped to it (redundant in-bounds DMA, no branch in the
+// interleaved regions); the tail drains every DMA before the epilogue reuses the LDS.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int Q, int NM, int RD, int VM>
+__device__ __forceinline__ void mfma_sched() {
+    if constexpr (Q < NM) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (RD > 0) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+        if constexpr (VM > 0) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);
+        mfma_sched<Q + 1, NM, RD, VM>();
+    }
+}
+
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm4(GemmDesc g) {
+    constexpr int NW = 4;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
+    constexpr int STAGE_B = (A_ELEMS + B_ELEMS) * 2;
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    constexpr int NM = FM * FN, NR = FM * (TA ? 2 : 1) + FN * (TB ? 1 : 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem_raw;
+
+    const int tilesM = (g.M + BM - 1) / BM, tilesN = (g.N + BN - 1) / BN;
+    const int nblk = tilesM * tilesN;
+    int pid = blockIdx.x;
+    if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);  // XCD-contiguous ranges
+    constexpr int GROUP = 8;
+    const int group_id = pid / (GROUP * tilesN);
+    const int first_m = group_id * GROUP;
+    const int gsize = min(tilesM - first_m, GROUP);
+    const int in_group = pid % (GROUP * tilesN);
+    const int m0 = (first_m + in_group % gsize) * BM;
+    const int n0 = (in_group / gsize) * BN;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    f32x16_t acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int kt0 = g.Ks[0] / BK;
+    const int KTall = kt0 + (g.nseg > 1 ? g.Ks[1] / BK : 0);
+    const int half = KTall >> 1;
+    const int kt_lo = blockIdx.y ? half : 0;
+    const int KT = g.ksplit < 2 ? KTall : (blockIdx.y ? KTall - half : half);
+    const int last = KT - 1;
+    // segment operands in registers (selected per tile without indexed argument reads)
+    const bf16_t* const A0 = g.A[0];
+    const bf16_t* const A1 = g.A[1];
+    const bf16_t* const B0 = g.B[0];
+    const bf16_t* const B1 = g.B[1];
+    const int lda0 = g.lda[0], lda1 = g.lda[1], ldb0 = g.ldb[0], ldb1 = g.ldb[1];
+
+    auto dma = [&](int tl, int buf) {
+        const int t = kt_lo + tl;
+        const bool s1 = t >= kt0;
+        const int k0 = (s1 ? t - kt0 : t) * BK;
+        const uint32_t base = lds0 + (uint32_t)(buf * STAGE_B);
+        stage<BM, !TA, NW>(s1 ? A1 : A0, s1 ? lda1 : lda0, m0, g.M, k0, base);
+        stage<BN, TB, NW>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, g.N, k0, base + A_ELEMS * 2);
+    };
+    // DMA instruction q of tile tl (A's first, then B's), for interleaving with MFMAs
+    constexpr int NDA = BM / (8 * NW), NDB = BN / (8 * NW);
+    auto dma_one = [&](auto Q_, int tl, int buf) {
+        constexpr int q = decltype(Q_)::value;
+        const int t = kt_lo + tl;
+        const bool s1 = t >= kt0;
+        const int k0 = (s1 ? t - kt0 : t) * BK;
+        const uint32_t base = lds0 + (uint32_t)(buf * STAGE_B);
+        if constexpr (q < NDA)
+            stage<BM, !TA, NW, q, q + 1>(s1 ? A1 : A0, s1 ? lda1 : lda0, m0, g.M, k0, base);
+        else
+            stage<BN, TB, NW, q - NDA, q - NDA + 1>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, g.N, k0,
+                                                   base + A_ELEMS * 2);
+    };
+    bf16x8_t fa[2][FM], fb[2][FN];
+    auto load_frags = [&](int buf, int ks, int slot) {
+        const bf16_t* sa = reinterpret_cast<const bf16_t*>(smem_raw + buf * STAGE_B);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[slot][i] = frag<BM, !TA>(sa, wm * WM + i * 32, ks);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[slot][j] = frag<BN, TB>(sa + A_ELEMS, wn * WN + j * 32, ks);
+    };
+    auto mfmas = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
+    };
+    // reads of the next step spread over this step's MFMAs (all of them when there are
+    // fewer MFMAs than reads)
+    constexpr int RPM = (NR + NM - 1) / NM;
+
+    if (KT > 0) {
+        dma(0, 0);
+        dma(min(1, last), 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(BM / (8 * NW) + BN / (8 * NW)));
+        __syncthreads();
+        load_frags(0, 0, 0);
+    }
+    auto step = [&](auto BUF_, int t) {
+        constexpr int buf = decltype(BUF_)::value;
+#pragma unroll
+        for (int ks = 0; ks < 3; ++ks) {
+            load_frags(buf, ks + 1, (ks + 1) & 1);
+            mfmas(ks & 1);
+            mfma_sched<0, NM, RPM, 0>();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();
+        // k-step 3 in units: one MFMA, then (while it occupies the pipe) one DMA
+        // instruction of tile t+2 and one fragment read of tile t+1
+        const int tn = min(t + 2, last);
+        const bf16_t* sn = reinterpret_cast<const bf16_t*>(smem_raw + (buf ^ 1) * STAGE_B);
+        constexpr int UNITS = NM > NDA + NDB ? (NM > FM + FN ? NM : FM + FN)
+                                             : (NDA + NDB > FM + FN ? NDA + NDB : FM + FN);
+        static_for<UNITS>([&](auto Q_) {
+            constexpr int q = decltype(Q_)::value;
+            if constexpr (q < NM)
+                acc[q / FN][q % FN] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    fa[1][q / FN], fb[1][q % FN], acc[q / FN][q % FN], 0, 0, 0);
+            if constexpr (q < NDA + NDB) dma_one(Q_, tn, buf);
+            if constexpr (q < FM) fa[0][q] = frag<BM, !TA>(sn, wm * WM + q * 32, 0);
+            else if constexpr (q < FM + FN) fb[0][q - FM] = frag<BN, TB>(sn + A_ELEMS, wn * WN + (q - FM) * 32, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    int t = 0;
+    for (; t + 1 < KT; t += 2) {
+        step(std::integral_constant<int, 0>{}, t);
+        step(std::integral_constant<int, 1>{}, t + 1);
+    }
+    if (t < KT) step(std::integral_constant<int, 0>{}, t);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+
+    float* st = reinterpret_cast<float*>(smem_raw) + wave * 32 * (WN + 4);
+    const int rq = (lane >> 5) * 4;
+    auto strip = [&](auto I_) {
+        constexpr int i = decltype(I_)::value;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        if constexpr (EPI == 0 && sizeof(CT) == 4) {
+            if (g.ksplit > 1) {
+                epilogue_atomic<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+                return;
+            }
+        }
+        epilogue_rows<CT, EPI, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+    };
+    strip(std::integral_constant<int, 0>{});
+    if constexpr (FM > 1) strip(std::integral_constant<int, 1>{});
+    if constexpr (FM > 2) strip(std::integral_constant<int, 2>{});
+    if constexpr (FM > 3) strip(std::integral_constant<int, 3>{});
+}
+
 // ---- VSA unpack-project dW --------------------------------------------------------------
 // C[M x N] (+)= (A_hi + A_lo) S over K, one block per 128 x 256 tile, 4 waves (2 x 2) of
 // 64 x 128, one wave per SIMD.  Both dY planes (hi and lo, k-contiguous) share one +-1 B tile
@@ -595,8 +779,37 @@ bool allow_lds(F* fn, size_t bytes) {
 
 constexpr int kGemmWaves = 8;
 
+// core selection for A/B measurement (GN_GEMM_CORE=8 picks the eight-wave core)
+inline bool gemm_core4() {
+    static const bool four = [] {
+        const char* e = getenv("GN_GEMM_CORE");
+        return !(e && e[0] == '8');
+    }();
+    return four;
+}
+
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
+int launch_t4(const GemmDesc& g, hipStream_t s) {
+    constexpr size_t stages_b = (size_t)2 * (BM + BN) * BK * sizeof(bf16_t);
+    constexpr size_t strips_b = (size_t)4 * 32 * (BN / 2 + 4) * sizeof(float);
+    constexpr size_t smem = stages_b > strips_b ? stages_b : strips_b;
+    static_assert(smem <= 160 * 1024, "LDS per CU");
+    static const bool ok = allow_lds(gemm4<TA, TB, CT, BM, BN, EPI>, smem);
+    if (!ok) {
+        set_error("gemm: cannot reserve %zu B of LDS", smem);
+        return GN_E_HIP;
+    }
+    const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    if (g.ksplit > 1)
+        clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
+    hipLaunchKernelGGL((gemm4<TA, TB, CT, BM, BN, EPI>), dim3(tiles, g.ksplit), dim3(256), smem, s, g);
+    GN_LAUNCH_CHECK("gemm (dma, 4 waves)");
+    return GN_OK;
+}
+
 template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
 int launch_t(const GemmDesc& g, hipStream_t s) {
+    if (gemm_core4()) return launch_t4<TA, TB, CT, BM, BN, EPI>(g, s);
     constexpr int NW = kGemmWaves;
     // operand stages, or the epilogue's per-wave fp32 strips [32][BN/2 + 4] if larger
     constexpr size_t stages_b = (size_t)gemm_stages<TA, BM, BN>() * (BM + BN) * BK * sizeof(bf16_t);
