@@ -93,9 +93,9 @@ def pmc_summary(fetch_dir, write_dir):
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         tab = load(d, counter)
         calib = [v for (k, g), v in tab.items() if "add_kernel" in k]
-        # the dN GEMM: gemm_dma / gemm4 kernel, plain epilogue, no transposes, grid of 4096 x 2048 tiles
+        # the dN GEMM: gemm_core kernel, plain epilogue, no transposes, grid of 4096 x 2048 tiles
         gemm = {(k, g): v for (k, g), v in tab.items()
-                if re.search(r"gemm(?:_dma|4)<false, false, unsigned short, \d+, \d+, 0[,>]", k)}
+                if re.search(r"gemm_core<false, false, unsigned short, \d+, \d+, 0[,>]", k)}
         if not calib or not gemm:
             raise SystemExit(f"{counter}: calibration or GEMM dispatches not found in {d}")
         cvals = [x for v in calib for x in v.values()]

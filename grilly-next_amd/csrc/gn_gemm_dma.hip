@@ -4,8 +4,8 @@
 //
 // Block tile BM x BN x 64, 256 threads = 2 x 2 waves, wave tile (BM/2) x (BN/2) built from
 // v_mfma_f32_32x32x16_bf16 with fp32 accumulators.  Global -> LDS moves use the 16-byte
-// `global_load_lds` DMA (no VGPR staging), double-buffered: the DMA of k-tile t+1 runs
-// while the MFMAs of tile t execute.  Each operand stays in LDS in its global orientation:
+// `global_load_lds` DMA (no VGPR staging) into two or three LDS stages, so the DMA of the
+// next tiles runs while the MFMAs of the current one execute.  Each operand stays in LDS in its global orientation:
 //   * k-contiguous operand (rows of 64 k):   [row][k], 16-byte chunk c of row r stored at
 //     chunk c ^ swz(r); MFMA fragments are single ds_read_b128;
 //   * k-outer operand (rows of BM/BN columns): [k][col], chunk c of k-row k stored at
@@ -116,34 +116,6 @@ __device__ __forceinline__ bf16x8_t frag(const bf16_t* s, int row0, int ks) {
     }
 }
 
-// One k-tile of MFMAs from LDS buffers (sa, sb); fragments of k-step ks+1 are requested
-// before the MFMAs of k-step ks are issued.
-template <bool TA, bool TB, int BM, int BN, int WM, int WN, int FM, int FN, typename HOOK>
-__device__ __forceinline__ void compute_tile(const bf16_t* sa, const bf16_t* sb, int wm, int wn,
-                                             f32x16_t (&acc)[FM][FN], HOOK&& after_step) {
-    bf16x8_t a[2][FM], b[2][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) a[0][i] = frag<BM, !TA>(sa, wm * WM + i * 32, 0);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) b[0][j] = frag<BN, TB>(sb, wn * WN + j * 32, 0);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-        const int cur = ks & 1, nxt = cur ^ 1;
-        if (ks + 1 < BK / 16) {
-#pragma unroll
-            for (int i = 0; i < FM; ++i) a[nxt][i] = frag<BM, !TA>(sa, wm * WM + i * 32, ks + 1);
-#pragma unroll
-            for (int j = 0; j < FN; ++j) b[nxt][j] = frag<BN, TB>(sb, wn * WN + j * 32, ks + 1);
-        }
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
-        after_step(std::integral_constant<int, 0>{}, ks);
-    }
-}
-
 // GLU local gradients of 8 consecutive elements (gate/up given as 4 packed bf16 pairs).
 template <int KIND>
 __device__ __forceinline__ void glu8(const float (&v)[8], const uint32_t (&gg)[4],
@@ -219,6 +191,92 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& g, const float* st
         }
 }
 
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// GLU epilogue of the four-wave core.  A strip is 32 rows x WN columns of dO; its gate/up
+// elements are fetched into registers with a coalesced map (LPR = WN/8 lanes per row, each
+// lane 8 consecutive columns = one 16-byte load, so a row segment is one contiguous
+// 2*WN-byte run), all loads of a strip issued before any of its math, and (for WN = 64)
+// the next strip's loads issued before this strip's math so they overlap it.  Rows and
+// columns past the matrix edge load a clamped in-bounds element and are not stored.
+template <int WN>
+struct GluStrip {
+    static constexpr int LPR = WN / 8, RP = 64 / LPR, NP = 32 / RP;
+    uint4 g[NP], u[NP];
+};
+
+template <int WN>
+__device__ __forceinline__ void glu_fetch(const GemmDesc& g, int mbase, int nbase, int lane,
+                                          GluStrip<WN>& t) {
+    using S = GluStrip<WN>;
+    const int n = min(nbase + (lane % S::LPR) * 8, g.N - 8);
+#pragma unroll
+    for (int p = 0; p < S::NP; ++p) {
+        const int m = min(mbase + p * S::RP + lane / S::LPR, g.M - 1);
+        const size_t gi = (size_t)m * g.ldg + n;
+        t.g[p] = *reinterpret_cast<const uint4*>(g.gate + gi);
+        t.u[p] = *reinterpret_cast<const uint4*>(g.up + gi);
+    }
+}
+
+template <int KIND, int WN>
+__device__ __forceinline__ void glu_store(const GemmDesc& g, const float* st, int mbase, int nbase,
+                                          int lane, const GluStrip<WN>& t) {
+    using S = GluStrip<WN>;
+    const int c = (lane % S::LPR) * 8;
+    const int n = nbase + c;
+#pragma unroll
+    for (int p = 0; p < S::NP; ++p) {
+        const int rr = p * S::RP + lane / S::LPR;
+        const int m = mbase + rr;
+        const float4 lo = *reinterpret_cast<const float4*>(st + rr * (WN + 4) + c);
+        const float4 hi = *reinterpret_cast<const float4*>(st + rr * (WN + 4) + c + 4);
+        const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        if (m >= g.M || n >= g.N) continue;
+        const uint32_t gg[4] = {t.g[p].x, t.g[p].y, t.g[p].z, t.g[p].w};
+        const uint32_t uu[4] = {t.u[p].x, t.u[p].y, t.u[p].z, t.u[p].w};
+        float dg[8], du[8];
+        glu8<KIND>(v, gg, uu, dg, du);
+        bf16_t* o = g.gu + (size_t)m * g.ldgu + n;
+        *reinterpret_cast<uint4*>(o) = make_uint4(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]),
+                                                  pack_bf2(dg[4], dg[5]), pack_bf2(dg[6], dg[7]));
+        *reinterpret_cast<uint4*>(o + g.H) = make_uint4(pack_bf2(du[0], du[1]), pack_bf2(du[2], du[3]),
+                                                        pack_bf2(du[4], du[5]), pack_bf2(du[6], du[7]));
+    }
+}
+
+// Whole GLU epilogue of one wave's (32 FM) x WN accumulator block, strip by strip through
+// the wave's private LDS strip `st` (fp32, pitch WN + 4).
+template <int KIND, int FM, int FN, int WN>
+__device__ __forceinline__ void glu_epilogue(const GemmDesc& g, const f32x16_t (&acc)[FM][FN], float* st,
+                                             int mbase, int nbase, int lane) {
+    constexpr bool AHEAD = WN <= 64;  // registers for two strips of gate/up
+    GluStrip<WN> t[AHEAD ? 2 : 1];
+    const int rq = (lane >> 5) * 4;
+    glu_fetch<WN>(g, mbase, nbase, lane, t[0]);
+    static_for<FM>([&](auto I_) {
+        constexpr int i = decltype(I_)::value;
+        constexpr int cur = AHEAD ? (i & 1) : 0;
+        if constexpr (!AHEAD) {
+            if constexpr (i > 0) glu_fetch<WN>(g, mbase + i * 32, nbase, lane, t[0]);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        if constexpr (AHEAD && i + 1 < FM) glu_fetch<WN>(g, mbase + (i + 1) * 32, nbase, lane, t[cur ^ 1]);
+        glu_store<KIND, WN>(g, st, mbase + i * 32, nbase, lane, t[cur]);
+    });
+}
+
 // Split-K epilogue (fp32 C, cleared beforehand): the strip's rows are added into C with
 // hardware fp32 atomics, one row per instruction round (lane = column: 256-byte segments).
 template <int WN>
@@ -246,169 +304,39 @@ __global__ __launch_bounds__(256) void clear_c(GemmDesc g) {
     }
 }
 
-// Pipeline depth: three LDS stages when they fit and A is k-contiguous; with a k-outer A
-// (transpose reads for both operands) two stages measured faster on MI355X.
-template <bool TA, int BM, int BN>
-constexpr int gemm_stages() {
-    return (!TA && 3 * (BM + BN) * BK * 2 <= 160 * 1024) ? 3 : 2;
+// ---- GEMM core -------------------------------------------------------------------------
+// Four waves (2 x 2, one per SIMD), wave tile (BM/2) x (BN/2), two or three LDS stages.  Every
+// MFMA operand is read from LDS two k-steps before its MFMAs run, into one of four register
+// sets (set = k-step within the tile, so every index is a compile-time constant).  Per tile t
+// (stage S = t & 1):
+//   k-step 0: MFMAs of set 0; reads of (t, 2) from S into set 2, spread over the MFMAs;
+//   k-step 1: MFMAs of set 1; reads of (t, 3) from S into set 3, all issued in the first
+//             half so they have landed by the end of the step;
+//             then vmcnt(0) (this wave's DMA of tile t+1) + lgkmcnt(0) + one barrier:
+//             tile t+1 is visible to every wave and stage S has no reader left;
+//   k-step 2: MFMAs of set 2; DMA of tile t+2 into S and reads of (t+1, 0) from S^1;
+//   k-step 3: MFMAs of set 3; reads of (t+1, 1) from S^1 into set 1.
+// Each MFMA's operands were requested at least one full k-step earlier, so the wave never
+// waits on an LDS read that was issued a couple of MFMAs before.
+template <int NM, int NR, bool FRONT>
+__host__ __device__ constexpr int reads_before(int q) {
+    // number of fragment reads issued after MFMAs 0..q-1 (spread evenly over NM, or over the
+    // first half of them when FRONT)
+    return FRONT ? (q >= (NM + 1) / 2 ? NR : (NR * q + (NM + 1) / 2 - 1) / ((NM + 1) / 2))
+                 : (NR * q + NM - 1) / NM;
 }
 
-// NW = 4: waves 2 x 2; NW = 8: waves 4 (rows) x 2 (columns), two waves per SIMD.
-template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int NW>
-__global__ __launch_bounds__(64 * NW, 1) void gemm_dma(GemmDesc g) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    bf16_t* sbase = reinterpret_cast<bf16_t*>(smem_raw);
-    constexpr int STAGES = gemm_stages<TA, BM, BN>();
-    constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
-    constexpr int STAGE = A_ELEMS + B_ELEMS;
-    constexpr int WR = NW / 2;  // wave rows
-    constexpr int WM = BM / WR, WN = BN / 2, FM = WM / 32, FN = WN / 32;
-    static_assert(FM >= 1 && FN >= 1, "wave tile of at least 32 x 32");
-    // LDS byte address of the dynamic allocation (for the DMA's M0 operand)
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)sbase;
-
-    const int tilesM = (g.M + BM - 1) / BM, tilesN = (g.N + BN - 1) / BN;
-    const int nblk = tilesM * tilesN;
-    int pid = blockIdx.x;
-    if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);  // XCD-contiguous ranges
-    constexpr int GROUP = 8;
-    const int group_id = pid / (GROUP * tilesN);
-    const int first_m = group_id * GROUP;
-    const int gsize = min(tilesM - first_m, GROUP);
-    const int in_group = pid % (GROUP * tilesN);
-    const int m0 = (first_m + in_group % gsize) * BM;
-    const int n0 = (in_group / gsize) * BN;
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-
-    f32x16_t acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const int kt0 = g.Ks[0] / BK;
-    const int KTall = kt0 + (g.nseg > 1 ? g.Ks[1] / BK : 0);
-    // this block's k-tiles [kt_lo, kt_lo + KT): the whole range, or one half with split-K
-    const int half = KTall >> 1;
-    const int kt_lo = blockIdx.y ? half : 0;
-    const int KT = g.ksplit < 2 ? KTall : (blockIdx.y ? KTall - half : half);
-
-    auto tile_base = [&](int buf) { return lds0 + (uint32_t)(buf * STAGE) * 2u; };
-    auto issue = [&](int tl, int buf) {
-        const int t = kt_lo + tl;
-        const int s = t < kt0 ? 0 : 1;
-        const int k0 = (t < kt0 ? t : t - kt0) * BK;
-        stage<BM, !TA, NW>(g.A[s], g.lda[s], m0, g.M, k0, tile_base(buf));
-        stage<BN, TB, NW>(g.B[s], g.ldb[s], n0, g.N, k0, tile_base(buf) + A_ELEMS * 2u);
-    };
-    // DMA of tile t split over the four k-steps of the current tile's MFMAs:
-    // step 0/1 carry the A halves, steps 2/3 the B halves.
-    auto issue_part = [&](int tl, int buf, int step) {
-        const int t = kt_lo + tl;
-        const int s = t < kt0 ? 0 : 1;
-        const int k0 = (t < kt0 ? t : t - kt0) * BK;
-        const uint32_t base = tile_base(buf);
-        constexpr int JA = BM / (8 * NW), JB = BN / (8 * NW);
-        static_assert(JA >= 2 && JB >= 2, "each DMA half holds one instruction per wave at least");
-        switch (step) {
-            case 0: stage<BM, !TA, NW, 0, JA / 2>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
-            case 1: stage<BM, !TA, NW, JA / 2, JA>(g.A[s], g.lda[s], m0, g.M, k0, base); break;
-            case 2: stage<BN, TB, NW, 0, JB / 2>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
-            default: stage<BN, TB, NW, JB / 2, JB>(g.B[s], g.ldb[s], n0, g.N, k0, base + A_ELEMS * 2u); break;
-        }
-    };
-
-    // vmcnt immediate: outstanding DMA instructions of one tile per wave
-    constexpr int DMA_PER_TILE = (BM + BN) / (8 * NW);
-    static_assert(DMA_PER_TILE < 64, "vmcnt is a 6-bit field");
-    // s_waitcnt vmcnt(N) expcnt(7) lgkmcnt(15): vmcnt bits [3:0] and [15:14]
-    constexpr unsigned WAIT_ONE_TILE =
-        0x0F70u | (DMA_PER_TILE & 15u) | ((unsigned)(DMA_PER_TILE >> 4) << 14);
-
-    if (KT > 0) issue(0, 0);
-    if (STAGES > 2 && KT > 1) issue(1, 1);
-    for (int t = 0; t < KT; ++t) {
-        // tile t's DMA has landed (with 3 stages, tile t+1's may still be in flight)
-        if (STAGES > 2 && t + 1 < KT) __builtin_amdgcn_s_waitcnt(WAIT_ONE_TILE);
-        else __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();  // ... for every wave; the stage about to be refilled is free
-        const int nxt = t + STAGES - 1;  // tile whose DMA is issued during this compute
-        const int nbuf = nxt % STAGES;
-        const bf16_t* sa = sbase + (t % STAGES) * STAGE;
-        compute_tile<TA, TB, BM, BN, WM, WN, FM, FN>(sa, sa + A_ELEMS, wm, wn, acc,
-                                             [&](auto, int ks) {
-                                                 if (nxt < KT) issue_part(nxt, nbuf, ks);
-                                             });
-    }
-
-    // ---- epilogue: each wave stages one 32-row strip of its tile at a time in a private
-    // LDS region (fp32, rows padded by 4), then moves 8 consecutive columns per lane with
-    // 16-byte accesses (two lanes per row).  The strip index is a compile-time constant so
-    // the accumulators are never indexed dynamically (which would put them in scratch).
-    __syncthreads();  // every wave is done with the operand stages
-    float* st = reinterpret_cast<float*>(smem_raw) + wave * 32 * (WN + 4);
-    const int rq = (lane >> 5) * 4;
-    auto strip = [&](auto I_) {
-        constexpr int i = decltype(I_)::value;
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
-        if constexpr (EPI == 0 && sizeof(CT) == 4) {
-            if (g.ksplit > 1) {
-                epilogue_atomic<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
-                return;
-            }
-        }
-        epilogue_rows<CT, EPI, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
-    };
-    strip(std::integral_constant<int, 0>{});
-    if constexpr (FM > 1) strip(std::integral_constant<int, 1>{});
-    if constexpr (FM > 2) strip(std::integral_constant<int, 2>{});
-    if constexpr (FM > 3) strip(std::integral_constant<int, 3>{});
-}
-
-// ---- four-wave core ----------------------------------------------------------------------
-// Four waves (2 x 2, one per SIMD), wave tile (BM/2) x (BN/2), two LDS stages, and a k-tile
-// schedule in which nothing but MFMAs occupies the matrix pipe's critical path:
-//   k-steps 0-2: the fragments of the next step are requested between this step's MFMAs;
-//   then this wave's DMA of tile t+1 is drained and one barrier publishes tile t+1 and
-//   retires every read of tile t's stage; the DMA of tile t+2 refills that stage and the
-//   first fragments of tile t+1 are requested, interleaved with the MFMAs of k-step 3.
-// Tiles past the last one are clamped to it (redundant in-bounds DMA, no branch in the
-// interleaved regions); the tail drains every DMA before the epilogue reuses the LDS.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-template <int Q, int NM, int RD, int VM>
-__device__ __forceinline__ void mfma_sched() {
-    if constexpr (Q < NM) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if constexpr (RD > 0) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
-        if constexpr (VM > 0) __builtin_amdgcn_sched_group_barrier(0x020, VM, 0);
-        mfma_sched<Q + 1, NM, RD, VM>();
-    }
-}
-
-template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm4(GemmDesc g) {
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES>
+__global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
+    static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
     constexpr int NW = 4;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
     constexpr int STAGE_B = (A_ELEMS + B_ELEMS) * 2;
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
-    constexpr int NM = FM * FN, NR = FM * (TA ? 2 : 1) + FN * (TB ? 1 : 2);
+    constexpr int NM = FM * FN;
+    constexpr int RA = TA ? 2 : 1, RB = TB ? 1 : 2;  // LDS reads per A / B fragment
+    constexpr int NR = FM * RA + FN * RB;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem_raw;
 
     const int tilesM = (g.M + BM - 1) / BM, tilesN = (g.N + BN - 1) / BN;
@@ -440,22 +368,12 @@ __global__ __launch_bounds__(256, 1) void gemm4(GemmDesc g) {
     const int kt_lo = blockIdx.y ? half : 0;
     const int KT = g.ksplit < 2 ? KTall : (blockIdx.y ? KTall - half : half);
     const int last = KT - 1;
-    // segment operands in registers (selected per tile without indexed argument reads)
     const bf16_t* const A0 = g.A[0];
     const bf16_t* const A1 = g.A[1];
     const bf16_t* const B0 = g.B[0];
     const bf16_t* const B1 = g.B[1];
     const int lda0 = g.lda[0], lda1 = g.lda[1], ldb0 = g.ldb[0], ldb1 = g.ldb[1];
 
-    auto dma = [&](int tl, int buf) {
-        const int t = kt_lo + tl;
-        const bool s1 = t >= kt0;
-        const int k0 = (s1 ? t - kt0 : t) * BK;
-        const uint32_t base = lds0 + (uint32_t)(buf * STAGE_B);
-        stage<BM, !TA, NW>(s1 ? A1 : A0, s1 ? lda1 : lda0, m0, g.M, k0, base);
-        stage<BN, TB, NW>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, g.N, k0, base + A_ELEMS * 2);
-    };
-    // DMA instruction q of tile tl (A's first, then B's), for interleaving with MFMAs
     constexpr int NDA = BM / (8 * NW), NDB = BN / (8 * NW);
     auto dma_one = [&](auto Q_, int tl, int buf) {
         constexpr int q = decltype(Q_)::value;
@@ -469,70 +387,119 @@ __global__ __launch_bounds__(256, 1) void gemm4(GemmDesc g) {
             stage<BN, TB, NW, q - NDA, q - NDA + 1>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, g.N, k0,
                                                    base + A_ELEMS * 2);
     };
-    bf16x8_t fa[2][FM], fb[2][FN];
-    auto load_frags = [&](int buf, int ks, int slot) {
-        const bf16_t* sa = reinterpret_cast<const bf16_t*>(smem_raw + buf * STAGE_B);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) fa[slot][i] = frag<BM, !TA>(sa, wm * WM + i * 32, ks);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) fb[slot][j] = frag<BN, TB>(sa + A_ELEMS, wn * WN + j * 32, ks);
-    };
-    auto mfmas = [&](int slot) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
-    };
-    // reads of the next step spread over this step's MFMAs (all of them when there are
-    // fewer MFMAs than reads)
-    constexpr int RPM = (NR + NM - 1) / NM;
-
-    if (KT > 0) {
-        dma(0, 0);
-        dma(min(1, last), 1);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(BM / (8 * NW) + BN / (8 * NW)));
-        __syncthreads();
-        load_frags(0, 0, 0);
-    }
-    auto step = [&](auto BUF_, int t) {
-        constexpr int buf = decltype(BUF_)::value;
-#pragma unroll
-        for (int ks = 0; ks < 3; ++ks) {
-            load_frags(buf, ks + 1, (ks + 1) & 1);
-            mfmas(ks & 1);
-            mfma_sched<0, NM, RPM, 0>();
-            __builtin_amdgcn_sched_barrier(0);
+    bf16x8_t fa[4][FM], fb[4][FN];
+    // read r of a fragment set: A fragments first, then B (whole fragments per call: a
+    // transpose-read fragment is two instructions, issued together)
+    auto read_one = [&](auto SET_, auto R_, const bf16_t* sa, int ks) {
+        constexpr int set = decltype(SET_)::value, r = decltype(R_)::value;
+        if constexpr (r < FM * RA) {
+            if constexpr (r % RA == 0) fa[set][r / RA] = frag<BM, !TA>(sa, wm * WM + (r / RA) * 32, ks);
+        } else {
+            constexpr int rb = r - FM * RA;
+            if constexpr (rb % RB == 0) fb[set][rb / RB] = frag<BN, TB>(sa + A_ELEMS, wn * WN + (rb / RB) * 32, ks);
         }
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        __syncthreads();
-        // k-step 3 in units: one MFMA, then (while it occupies the pipe) one DMA
-        // instruction of tile t+2 and one fragment read of tile t+1
-        const int tn = min(t + 2, last);
-        const bf16_t* sn = reinterpret_cast<const bf16_t*>(smem_raw + (buf ^ 1) * STAGE_B);
-        constexpr int UNITS = NM > NDA + NDB ? (NM > FM + FN ? NM : FM + FN)
-                                             : (NDA + NDB > FM + FN ? NDA + NDB : FM + FN);
-        static_for<UNITS>([&](auto Q_) {
+    };
+    auto stage_ptr = [&](int buf) { return reinterpret_cast<const bf16_t*>(smem_raw + buf * STAGE_B); };
+
+    // one k-step: MFMAs of set CUR, with the reads of set RSET (k-step rks of stage rbuf) and
+    // optionally the DMA of tile dtile into dbuf interleaved
+    auto kstep = [&](auto CUR_, auto RSET_, auto FRONT_, auto DMA_, const bf16_t* rsrc, int rks,
+                     int dtile, int dbuf) {
+        constexpr int cur = decltype(CUR_)::value;
+        constexpr bool front = decltype(FRONT_)::value, with_dma = decltype(DMA_)::value;
+        constexpr int ND = NDA + NDB;
+        static_for<NM>([&](auto Q_) {
             constexpr int q = decltype(Q_)::value;
-            if constexpr (q < NM)
-                acc[q / FN][q % FN] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    fa[1][q / FN], fb[1][q % FN], acc[q / FN][q % FN], 0, 0, 0);
-            if constexpr (q < NDA + NDB) dma_one(Q_, tn, buf);
-            if constexpr (q < FM) fa[0][q] = frag<BM, !TA>(sn, wm * WM + q * 32, 0);
-            else if constexpr (q < FM + FN) fb[0][q - FM] = frag<BN, TB>(sn + A_ELEMS, wn * WN + (q - FM) * 32, 0);
+            acc[q / FN][q % FN] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                fa[cur][q / FN], fb[cur][q % FN], acc[q / FN][q % FN], 0, 0, 0);
+            constexpr int r0 = reads_before<NM, NR, front>(q), r1 = reads_before<NM, NR, front>(q + 1);
+            static_for<NR>([&](auto R_) {
+                constexpr int r = decltype(R_)::value;
+                if constexpr (r >= r0 && r < r1) read_one(RSET_, R_, rsrc, rks);
+            });
+            if constexpr (with_dma) {
+                constexpr int d0 = (ND * q + NM - 1) / NM, d1 = (ND * (q + 1) + NM - 1) / NM;
+                static_for<ND>([&](auto D_) {
+                    constexpr int d = decltype(D_)::value;
+                    if constexpr (d >= d0 && d < d1) dma_one(D_, dtile, dbuf);
+                });
+            }
             __builtin_amdgcn_sched_barrier(0);
         });
     };
-    int t = 0;
-    for (; t + 1 < KT; t += 2) {
-        step(std::integral_constant<int, 0>{}, t);
-        step(std::integral_constant<int, 1>{}, t + 1);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using BF = std::false_type;
+    using BT = std::true_type;
+
+    // STAGES = 3: the DMA of tile t+3 goes into tile t's stage once tile t's last reads are
+    // retired (after this tile's barrier), so a tile's DMA has almost two tiles to land; the
+    // barrier then waits only for tile t+1 (tile t+2's DMA may still be in flight).
+    constexpr int ND = NDA + NDB;
+    auto tile = [&](auto BUF_, int t) {
+        constexpr int buf = decltype(BUF_)::value;
+        const bf16_t* cur = stage_ptr(buf);
+        const bf16_t* nxt = stage_ptr((buf + 1) % STAGES);
+        kstep(I0{}, I2{}, BF{}, BF{}, cur, 2, 0, 0);
+        kstep(I1{}, I3{}, BT{}, BF{}, cur, 3, 0, 0);
+        if constexpr (STAGES == 3)  // vmcnt(ND) and lgkmcnt(0)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(ND) & 0xF0FFu);
+        else  // vmcnt(0) and lgkmcnt(0)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & 0xF0FFu);
+        __syncthreads();
+        kstep(I2{}, I0{}, BF{}, BT{}, nxt, 0, min(t + STAGES, last), buf);
+        kstep(I3{}, I1{}, BF{}, BF{}, nxt, 1, 0, 0);
+    };
+
+    if (KT > 0) {
+        auto dma_all = [&](int tl, int buf) {
+            static_for<ND>([&](auto D_) { dma_one(D_, tl, buf); });
+        };
+        dma_all(0, 0);
+        dma_all(min(1, last), 1);
+        if constexpr (STAGES == 3) {
+            dma_all(min(2, last), 2);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * ND));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(ND));
+        }
+        __syncthreads();
+        static_for<NR>([&](auto R_) { read_one(I0{}, R_, stage_ptr(0), 0); });
+        static_for<NR>([&](auto R_) { read_one(I1{}, R_, stage_ptr(0), 1); });
     }
-    if (t < KT) step(std::integral_constant<int, 0>{}, t);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    int t = 0;
+    if constexpr (STAGES == 3) {
+        for (; t + 2 < KT; t += 3) {
+            tile(I0{}, t);
+            tile(I1{}, t + 1);
+            tile(I2{}, t + 2);
+        }
+        if (t < KT) tile(I0{}, t);
+        if (t + 1 < KT) tile(I1{}, t + 1);
+    } else {
+        for (; t + 1 < KT; t += 2) {
+            tile(I0{}, t);
+            tile(I1{}, t + 1);
+        }
+        if (t < KT) tile(I0{}, t);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & 0xF0FFu);
     __syncthreads();
 
     float* st = reinterpret_cast<float*>(smem_raw) + wave * 32 * (WN + 4);
+    if constexpr (EPI == 1) {
+        const int mb = m0 + wm * WM, nb = n0 + wn * WN;
+        switch (g.glu_kind) {
+            case GN_GLU_SWIGLU_UP: glu_epilogue<GN_GLU_SWIGLU_UP, FM, FN, WN>(g, acc, st, mb, nb, lane); break;
+            case GN_GLU_SWIGLU_GATE: glu_epilogue<GN_GLU_SWIGLU_GATE, FM, FN, WN>(g, acc, st, mb, nb, lane); break;
+            case GN_GLU_GEGLU_UP: glu_epilogue<GN_GLU_GEGLU_UP, FM, FN, WN>(g, acc, st, mb, nb, lane); break;
+            case GN_GLU_GEGLU_GATE: glu_epilogue<GN_GLU_GEGLU_GATE, FM, FN, WN>(g, acc, st, mb, nb, lane); break;
+            default: glu_epilogue<GN_GLU_REGLU_UP, FM, FN, WN>(g, acc, st, mb, nb, lane); break;
+        }
+        return;
+    }
     const int rq = (lane >> 5) * 4;
     auto strip = [&](auto I_) {
         constexpr int i = decltype(I_)::value;
@@ -549,10 +516,7 @@ __global__ __launch_bounds__(256, 1) void gemm4(GemmDesc g) {
         }
         epilogue_rows<CT, EPI, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
     };
-    strip(std::integral_constant<int, 0>{});
-    if constexpr (FM > 1) strip(std::integral_constant<int, 1>{});
-    if constexpr (FM > 2) strip(std::integral_constant<int, 2>{});
-    if constexpr (FM > 3) strip(std::integral_constant<int, 3>{});
+    static_for<FM>(strip);
 }
 
 // ---- VSA unpack-project dW --------------------------------------------------------------
@@ -777,94 +741,90 @@ bool allow_lds(F* fn, size_t bytes) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
 }
 
-constexpr int kGemmWaves = 8;
-
-// core selection for A/B measurement (GN_GEMM_CORE=8 picks the eight-wave core)
-inline bool gemm_core4() {
-    static const bool four = [] {
-        const char* e = getenv("GN_GEMM_CORE");
-        return !(e && e[0] == '8');
-    }();
-    return four;
-}
-
-template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
-int launch_t4(const GemmDesc& g, hipStream_t s) {
-    constexpr size_t stages_b = (size_t)2 * (BM + BN) * BK * sizeof(bf16_t);
-    constexpr size_t strips_b = (size_t)4 * 32 * (BN / 2 + 4) * sizeof(float);
-    constexpr size_t smem = stages_b > strips_b ? stages_b : strips_b;
-    static_assert(smem <= 160 * 1024, "LDS per CU");
-    static const bool ok = allow_lds(gemm4<TA, TB, CT, BM, BN, EPI>, smem);
-    if (!ok) {
-        set_error("gemm: cannot reserve %zu B of LDS", smem);
-        return GN_E_HIP;
-    }
-    const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    if (g.ksplit > 1)
-        clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
-    hipLaunchKernelGGL((gemm4<TA, TB, CT, BM, BN, EPI>), dim3(tiles, g.ksplit), dim3(256), smem, s, g);
-    GN_LAUNCH_CHECK("gemm (dma, 4 waves)");
-    return GN_OK;
-}
-
 template <bool TA, bool TB, typename CT, int BM, int BN, int EPI>
 int launch_t(const GemmDesc& g, hipStream_t s) {
-    if (gemm_core4()) return launch_t4<TA, TB, CT, BM, BN, EPI>(g, s);
-    constexpr int NW = kGemmWaves;
-    // operand stages, or the epilogue's per-wave fp32 strips [32][BN/2 + 4] if larger
-    constexpr size_t stages_b = (size_t)gemm_stages<TA, BM, BN>() * (BM + BN) * BK * sizeof(bf16_t);
-    constexpr size_t strips_b = (size_t)NW * 32 * (BN / 2 + 4) * sizeof(float);
-    constexpr size_t smem = stages_b > strips_b ? stages_b : strips_b;
-    static_assert(smem <= 160 * 1024, "LDS per CU");
-    static const bool ok = allow_lds(gemm_dma<TA, TB, CT, BM, BN, EPI, NW>, smem);
-    if (!ok) {
-        set_error("gemm: cannot reserve %zu B of LDS", smem);
+    // LDS: the operand stages, or the epilogue's per-wave fp32 strips [32][BN/2 + 4] if larger
+    constexpr size_t strips_b = (size_t)4 * 32 * (BN / 2 + 4) * sizeof(float);
+    constexpr size_t stage2_b = (size_t)2 * (BM + BN) * BK * sizeof(bf16_t);
+    constexpr size_t stage3_b = (size_t)3 * (BM + BN) * BK * sizeof(bf16_t);
+    constexpr size_t smem2 = stage2_b > strips_b ? stage2_b : strips_b;
+    constexpr size_t smem3 = stage3_b > strips_b ? stage3_b : strips_b;
+    constexpr bool fits3 = smem3 <= 160 * 1024;
+    static_assert(smem2 <= 160 * 1024, "LDS per CU");
+    // three LDS stages pay off on long k loops; short ones keep the shorter prologue
+    const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
+    const bool three = fits3 && KT / g.ksplit >= 48;
+    static const bool ok2 = allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2>, smem2);
+    static const bool ok3 = fits3 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>, smem3) : false;
+    if (!(three ? ok3 : ok2)) {
+        set_error("gemm: cannot reserve %zu B of LDS", three ? smem3 : smem2);
         return GN_E_HIP;
     }
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     if (g.ksplit > 1)
         clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
-    hipLaunchKernelGGL((gemm_dma<TA, TB, CT, BM, BN, EPI, NW>), dim3(tiles, g.ksplit), dim3(64 * NW),
-                       smem, s, g);
+    if (three)
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>), dim3(tiles, g.ksplit), dim3(256),
+                           smem3, s, g);
+    else
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2>), dim3(tiles, g.ksplit), dim3(256), smem2, s, g);
     GN_LAUNCH_CHECK("gemm (dma)");
     return GN_OK;
 }
 
-// Tile shape: fewest "rounds" of 256 CUs, ties broken toward the larger tile.
-// Split-K (two halves of K) is considered for a plain fp32 epilogue that overwrites C when
-// the K loop is long: it fills an otherwise under-occupied grid (weight gradients of small
-// projections over many tokens).
+// Tile shape and split from a time model fitted to MI355X sweeps of this core over the FFN
+// and decoder GEMMs (K from 768 to 32000):
+//   block time = KT x t_k[shape] + o[shape] + epilogue, where t_k is the time of one 64-deep
+//                k-tile with every CU busy (separate fits for a k-contiguous A and for a
+//                k-outer A, i.e. weight gradients with both operands transposed in LDS) and o
+//                the fixed cost of a block (DMA prologue, pipeline fill, drain);
+//   epilogue     C tile bytes at ~40 KB/us per block (the GLU epilogue moves ~5x that);
+//   a last round that fills a fraction f of the 256 CUs costs (0.6 + 0.4 f) of a full round
+//                (the blocks of a part-filled round get more L2 / HBM bandwidth each);
+//   split-K (two halves, fp32 C only): clear + atomic adds, ~5 us + 0.7 us per MB of C.
+struct TileChoice {
+    int shape;  // index into kTileShapes
+    int ksplit;
+};
+constexpr int kTileShapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+
+inline double tile_cost(const GemmDesc& g, bool ta, size_t c_bytes, int epi, int i, int ks) {
+    static constexpr double tk_kc[4] = {1.73, 0.98, 0.98, 0.57};
+    static constexpr double tk_ta[4] = {1.60, 0.98, 0.90, 0.52};
+    static constexpr double fixed[4] = {16.5, 6.4, 13.0, 6.4};
+    const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
+    const int bm = kTileShapes[i][0], bn = kTileShapes[i][1];
+    const long blocks = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * ks;
+    const long full = blocks / 256;
+    const double f = (double)(blocks % 256) / 256.0;
+    const double rounds = (double)full + (f > 0 ? 0.6 + 0.4 * f : 0.0);
+    const double kt = (double)((KT + ks - 1) / ks);
+    const double epi_us = (double)bm * bn * (double)c_bytes * (epi ? 5.0 : 1.0) / 40000.0;
+    double t = rounds * (kt * (ta ? tk_ta[i] : tk_kc[i]) + fixed[i] + epi_us);
+    if (ks > 1) t += 5.0 + 0.7e-6 * (double)g.M * g.N * 4.0;
+    return t;
+}
+
+inline TileChoice choose_tile(const GemmDesc& g, bool ta, size_t c_bytes, int epi) {
+    const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
+    const bool can_split = epi == 0 && c_bytes == 4 && !g.accumulate && KT >= 32;
+    TileChoice best{1, 1};
+    double bt = tile_cost(g, ta, c_bytes, epi, 1, 1);
+    for (int i = 0; i < 4; ++i) {
+        for (int ks = 1; ks <= (can_split ? 2 : 1); ++ks) {
+            const double c = tile_cost(g, ta, c_bytes, epi, i, ks);
+            if (c < bt) { bt = c; best = {i, ks}; }
+        }
+    }
+    return best;
+}
+
 template <bool TA, bool TB, typename CT, int EPI>
 int launch_shape(const GemmDesc& g0, hipStream_t s) {
     GemmDesc g = g0;
-    const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
-    const bool can_split = EPI == 0 && sizeof(CT) == 4 && !g.accumulate && KT >= 32;
-    auto cost = [&](int bm, int bn, int ks) {
-        const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * ks;
-        const long rounds = (tiles + 255) / 256;
-        return rounds * (long)bm * bn * 2 / ks;  // ~ time: rounds x per-block work
-    };
-    static constexpr int shapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
-    auto tiles_of = [&](int i) {
-        return (long)((g.M + shapes[i][0] - 1) / shapes[i][0]) * ((g.N + shapes[i][1] - 1) / shapes[i][1]);
-    };
-    long best = -1;
-    int pick = 0;
-    for (int i = 0; i < 4; ++i) {
-        const long c = cost(shapes[i][0], shapes[i][1], 1);
-        if (best < 0 || c < best) { best = c; pick = i; }
-    }
-    // split only a grid that leaves CUs idle, and only for a clear gain (the split pays a
-    // clear of C and atomic adds)
-    int ks_pick = 1;
-    if (can_split && tiles_of(pick) < 256) {
-        for (int i = 0; i < 4; ++i) {
-            const long c = cost(shapes[i][0], shapes[i][1], 2);
-            if (c * 5 < best * 4) { best = c; pick = i; ks_pick = 2; }
-        }
-    }
-    g.ksplit = ks_pick;
-    switch (pick) {
+    const TileChoice tc = choose_tile(g, TA, sizeof(CT), EPI);
+    g.ksplit = tc.ksplit;
+    switch (tc.shape) {
         case 0: return launch_t<TA, TB, CT, 256, 256, EPI>(g, s);
         case 1: return launch_t<TA, TB, CT, 256, 128, EPI>(g, s);
         case 2: return launch_t<TA, TB, CT, 128, 256, EPI>(g, s);
