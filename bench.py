@@ -326,10 +326,11 @@ def bench_decoder(args, torch, gn):
     tape = gb.create_tape_context(device)
     ms = timed(torch, lambda: m.backward_step(tape), args.steps, args.warmup)
     tf = m.flops() / (ms * 1e-3) / 1e12
+    opt = decoder_optimizer_step(torch, gn, m)
     cpu = None
     if not args.no_cpu:
         cpu = decoder_cpu_baseline(m)
-    return line("12-layer decoder backward tokens/s (end-to-end tape backward)",
+    out = line("12-layer decoder backward tokens/s (end-to-end tape backward)",
                 round(m.T / (ms * 1e-3), 1), "tokens/s", args, ms, "bf16",
                 {"workload": "C5 12-layer decoder bwd: d768 H12 LN, fused QKV, causal attention, "
                              "GEGLU 3072, tied embedding 32000 + CE; B8 x S1024, bf16",
@@ -339,6 +340,30 @@ def bench_decoder(args, torch, gn):
                  "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                  "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
                  "flops_per_step": m.flops()}, cpu)
+    out["optimizer_step"] = opt
+    return out
+
+
+def decoder_optimizer_step(torch, gn, m):
+    """AdamW after the backward over every decoder weight (fp32 masters, m, v, fp32 gradients,
+    bf16 copies written back): one gn_adamw_step call, HIP-event timed, gradients kept (the
+    tape releases them at end()).  Bytes per element: read W, g, m, v (16) + write W, m, v
+    (12) + bf16 W (2) = 30."""
+    ws = [m.E] + [w for p in m.layers for w in p.values()] + [m.lnf_g, m.lnf_b]
+    n = sum(w.numel() for w in ws)
+    ent = []
+    for w in ws:
+        f = w.float().contiguous()
+        ent.append(dict(W=f, grad=torch.randn_like(f) * 1e-3, state0=torch.zeros_like(f),
+                        state1=torch.zeros_like(f), W_bf16=torch.empty_like(w)))
+    def step():
+        gn.adamw_step(ent, lr=1e-4, weight_decay=0.01, step=1, clear_grad=False)
+    ms = timed(torch, step, 10, 3)
+    byts = 30.0 * n
+    gbs = byts / (ms * 1e-3) / 1e9
+    return {"kernel": "adamw_kernel (gn_adamw_step, %d tensors)" % len(ws), "params": n,
+            "ms": round(ms, 4), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": byts}
 
 
 def decoder_cpu_baseline(m):

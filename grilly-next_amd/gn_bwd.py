@@ -28,7 +28,8 @@ SYMBOLS = [
     "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
-    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd", "gn_add_inplace",
+    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd",
+    "gn_surprise_momentum_step", "gn_adamw_step", "gn_add_inplace",
 ]
 
 
@@ -43,6 +44,16 @@ _U = ctypes.c_uint
 _F = ctypes.c_float
 _L = ctypes.c_int64
 _Z = ctypes.c_size_t
+
+
+class OptParam(ctypes.Structure):
+    """gn_opt_param (include/gn_bwd.h): one parameter tensor of an optimizer step."""
+    _fields_ = [("W", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("state0", ctypes.c_void_p),
+                ("state1", ctypes.c_void_p), ("recalled", ctypes.c_void_p),
+                ("W_bf16", ctypes.c_void_p), ("n", ctypes.c_int64)]
+
+
+_OPTP = ctypes.POINTER(OptParam)
 
 _SIGS = {
     "gn_last_error": ([], ctypes.c_char_p),
@@ -71,6 +82,8 @@ _SIGS = {
     "gn_vsa_workspace_bytes": ([_I, _I], _Z),
     "gn_vsa_surrogate_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F, _U, _P], _I),
     "gn_embedding_bwd": ([_P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
+    "gn_surprise_momentum_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _I, _P], _I),
+    "gn_adamw_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     "gn_add_inplace": ([_P, _P, _L, _I, _P], _I),
 }
 
@@ -392,6 +405,56 @@ def embedding_bwd(dX, ids, V, dE=None, accumulate=False):
     _check(lib().gn_embedding_bwd(_ptr(dX), _ptr(ids), _ptr(dE), T, d, V, _dt(dX),
                                   ACCUMULATE if accumulate else 0, _stream()), "gn_embedding_bwd")
     return dE
+
+
+def _addr(x):
+    """Device address of a tensor (its data pointer) or of a raw buffer id (int); None -> 0."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if not x.is_cuda or not x.is_contiguous():
+        raise GnError("optimizer tensors must be contiguous GPU tensors")
+    return x.data_ptr()
+
+
+def _opt_params(entries):
+    arr = (OptParam * max(1, len(entries)))()
+    for i, e in enumerate(entries):
+        W = e["W"]
+        if W.dtype != torch.float32:
+            raise GnError("optimizer weights (masters) must be float32")
+        n = W.numel()
+        for key in ("grad", "state0", "state1", "recalled"):
+            x = e.get(key)
+            if x is not None and not isinstance(x, int) and (x.numel() != n or x.dtype != torch.float32):
+                raise GnError(f"optimizer tensor {i}: {key} must be float32 with {n} elements")
+        lp = e.get("W_bf16")
+        if lp is not None and (lp.numel() != n or lp.dtype != torch.bfloat16):
+            raise GnError(f"optimizer tensor {i}: W_bf16 must be bfloat16 with {n} elements")
+        arr[i] = OptParam(_addr(W), _addr(e["grad"]), _addr(e["state0"]), _addr(e.get("state1")),
+                          _addr(e.get("recalled")), _addr(lp), n)
+    return arr
+
+
+def surprise_momentum_step(entries, eta_base=1e-3, alpha=0.9, lambda_recall=0.0,
+                           surprise_floor=0.01, weight_decay=0.0, clip_max=1.0, clear_grad=True):
+    """entries: dicts with W, grad, state0 (= s_bar), optional state1 (= delta), recalled,
+    W_bf16.  grad may be a raw device address (a tape gradient buffer id)."""
+    arr = _opt_params(entries)
+    _check(lib().gn_surprise_momentum_step(arr, len(entries), eta_base, alpha, lambda_recall,
+                                           surprise_floor, weight_decay, clip_max,
+                                           int(clear_grad), _stream()),
+           "gn_surprise_momentum_step")
+
+
+def adamw_step(entries, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, step=1,
+               clear_grad=True):
+    """entries: dicts with W, grad, state0 (= m), state1 (= v), optional W_bf16."""
+    arr = _opt_params(entries)
+    _check(lib().gn_adamw_step(arr, len(entries), lr, beta1, beta2, eps, weight_decay,
+                               beta1 ** step, beta2 ** step, int(clear_grad), _stream()),
+           "gn_adamw_step")
 
 
 def add_inplace(out, a):

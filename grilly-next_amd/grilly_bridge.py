@@ -96,3 +96,78 @@ def vsa_surrogate_params(K: int, D: int, gamma: float = 1.0, delta: float = 1.0,
     """VSASurrogateLossParams (autograd.h:172-184); defaults as in bindings.cpp:3169-3176."""
     return struct.pack("<fffIIIIfff", gamma, delta, lambda_c, K, D, winning_k, runner_up_k,
                        0.0, temperature, 0.01)
+
+
+# ---------------------------------------------------------------------------- optimizers
+class _TapeOptimizer:
+    """Optimizer step applied between TapeContext.backward and end, the order the reference's
+    vsa_training_step uses (bindings.cpp:3196-3279): each weight's gradient is looked up with
+    tape.get_grad_buffer(weight id) (0 = no gradient: the weight is skipped) and every tensor
+    is updated by one multi-tensor launch (gn_*_step).  Weights are GPU tensors whose
+    data_ptr() is the buffer id the tape recorded; a bf16 weight gets an fp32 master copy and
+    receives the rounded update in place, so the next forward sees it."""
+
+    def __init__(self, weights):
+        import torch
+        self.weights = list(weights)
+        self.masters = [w if w.dtype == torch.float32 else w.float().contiguous()
+                        for w in self.weights]
+        self.t = 0
+
+    def _entries(self, tape, state):
+        import torch
+        out = []
+        for w, mw, st in zip(self.weights, self.masters, state):
+            g = tape.get_grad_buffer(w.data_ptr())
+            if g == 0:
+                continue
+            e = dict(W=mw, grad=int(g), **st)
+            if w.dtype == torch.bfloat16:
+                e["W_bf16"] = w
+            out.append(e)
+        return out
+
+
+class SurpriseMomentumOptimizer(_TapeOptimizer):
+    """The reference's SurpriseMomentumOptimizer (bindings.cpp:3049-3138: same attribute names
+    and defaults; the recalled gradient is zero, as there).  s_bar starts at zero per weight;
+    `delta` keeps the last update per element when keep_delta."""
+
+    def __init__(self, weights, lr=1e-3, alpha=0.9, clip=1.0, keep_delta=False):
+        import torch
+        super().__init__(weights)
+        self.eta_base, self.alpha_momentum, self.clip_max = lr, alpha, clip
+        self.lambda_recall, self.surprise_floor, self.weight_decay = 0.0, 0.01, 0.0
+        self.s_bar = [torch.zeros_like(m) for m in self.masters]
+        self.delta = [torch.zeros_like(m) for m in self.masters] if keep_delta else None
+
+    def step(self, tape):
+        import gn_bwd
+        self.t += 1
+        st = [dict(state0=s, state1=(self.delta[i] if self.delta else None))
+              for i, s in enumerate(self.s_bar)]
+        entries = self._entries(tape, st)
+        gn_bwd.surprise_momentum_step(entries, self.eta_base, self.alpha_momentum,
+                                      self.lambda_recall, self.surprise_floor, self.weight_decay,
+                                      self.clip_max, clear_grad=True)
+        return len(entries)
+
+
+class AdamW(_TapeOptimizer):
+    """AdamW over the tape's gradients (adamw-update.glsl:41-61; weight_decay 0 is
+    adam-update.glsl)."""
+
+    def __init__(self, weights, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01):
+        import torch
+        super().__init__(weights)
+        self.lr, self.betas, self.eps, self.weight_decay = lr, betas, eps, weight_decay
+        self.m = [torch.zeros_like(m) for m in self.masters]
+        self.v = [torch.zeros_like(m) for m in self.masters]
+
+    def step(self, tape):
+        import gn_bwd
+        self.t += 1
+        entries = self._entries(tape, [dict(state0=m, state1=v) for m, v in zip(self.m, self.v)])
+        gn_bwd.adamw_step(entries, self.lr, self.betas[0], self.betas[1], self.eps,
+                          self.weight_decay, step=self.t, clear_grad=True)
+        return len(entries)

@@ -246,6 +246,39 @@ int gn_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32_
 int gn_embedding_bwd(const void* dX, const int32_t* ids, float* dE, int T, int d, int V,
                      int dtype, unsigned flags, void* stream);
 
+/* ---- optimizer steps (between TapeContext.backward and end) ---------------------------- */
+/* One parameter tensor of a multi-tensor optimizer step (all fp32, n elements). */
+typedef struct gn_opt_param {
+    float* W;              /* weights, updated in place */
+    float* grad;           /* gradient; zeroed afterwards when clear_grad != 0 */
+    float* state0;         /* AdamW: first moment m;  surprise-momentum: s_bar */
+    float* state1;         /* AdamW: second moment v; surprise-momentum: delta output (may be NULL) */
+    const float* recalled; /* surprise-momentum: recalled gradient (NULL reads as zero) */
+    void* W_bf16;          /* optional bf16 copy of the updated W (NULL: none) */
+    int64_t n;
+} gn_opt_param;
+
+/* Surprise-momentum update of `count` tensors: replaces the per-parameter, per-128 MB-chunk
+ * dispatches of surprise-momentum.glsl in vsa_training_step (bindings.cpp:3198-3277) with
+ * one launch per 24 tensors.  Per element (surprise-momentum.glsl:53-114):
+ *   g, r non-finite -> delta = 0, W and s_bar unchanged;  else
+ *   s = min(alpha |g - r| + (1 - alpha) s_bar (non-finite s_bar read as 0), 5);
+ *   d = clamp(eta (1 + max(s, floor)) (g + lambda r) + eta wd W, -clip, clip);
+ *   W = clamp(W - d (non-finite -> 0), -10, 10);  s_bar = s;  delta = d;
+ *   grad = 0 when clear_grad.  params is a host array (read before the call returns). */
+int gn_surprise_momentum_step(const gn_opt_param* params, int count, float eta_base,
+                              float alpha_momentum, float lambda_recall, float surprise_floor,
+                              float weight_decay, float clip_max, int clear_grad, void* stream);
+
+/* AdamW update of `count` tensors (adamw-update.glsl:41-61; adam-update.glsl is weight_decay
+ * 0).  beta1_t, beta2_t = beta^t for bias correction at step t >= 1, as the shader's push
+ * constants.  Per element: m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;
+ *   W = W (1 - lr wd) - lr (m / max(1e-12, 1-b1t)) / (sqrt(max(v / max(1e-12, 1-b2t), 0)) + eps)
+ * grad = 0 when clear_grad; W_bf16 (if given) receives the rounded new W. */
+int gn_adamw_step(const gn_opt_param* params, int count, float lr, float beta1, float beta2,
+                  float eps, float weight_decay, float beta1_t, float beta2_t, int clear_grad,
+                  void* stream);
+
 /* ---- misc ------------------------------------------------------------------------------ */
 /* out[i] (+)= a[i] (f32/bf16): the fan-out accumulation the reference leaves as a TODO
  * (autograd.cpp:78-86). */

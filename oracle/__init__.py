@@ -324,3 +324,36 @@ def vsa_results_weights(dots, temperature=1.0, rng=None):
         e = np.exp((dots[b].astype(np.float64) - dots[b].max()) / temperature)
         weights[b] = (e / e.sum()).astype(np.float32)
     return results, weights
+
+
+def surprise_momentum_step(W, grad, s_bar, recalled=None, eta_base=1e-3, alpha=0.9,
+                           lambda_recall=0.0, surprise_floor=0.01, weight_decay=0.0,
+                           clip_max=1.0, clear_grad=True):
+    """surprise-momentum.glsl:53-114 on copies; returns (W, grad, s_bar, delta) after the step."""
+    W, pW = _f(np.array(W, dtype=np.float32, copy=True))
+    g, pg = _f(np.array(grad, dtype=np.float32, copy=True))
+    s, ps = _f(np.array(s_bar, dtype=np.float32, copy=True))
+    d, pd = _out(W.shape)
+    r = pr = None
+    if recalled is not None:
+        r, pr = _f(recalled)
+    lib().or_surprise_momentum_step(pW, pg, ps, pd, pr, ctypes.c_int64(W.size),
+                                    ctypes.c_float(eta_base), ctypes.c_float(alpha),
+                                    ctypes.c_float(lambda_recall), ctypes.c_float(surprise_floor),
+                                    ctypes.c_float(weight_decay), ctypes.c_float(clip_max),
+                                    int(clear_grad))
+    return W, g, s, d
+
+
+def adamw_step(W, grad, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0,
+               step=1, clear_grad=True):
+    """adamw-update.glsl:41-61 on copies (beta^t from `step`); returns (W, grad, m, v)."""
+    W, pW = _f(np.array(W, dtype=np.float32, copy=True))
+    g, pg = _f(np.array(grad, dtype=np.float32, copy=True))
+    m, pm = _f(np.array(m, dtype=np.float32, copy=True))
+    v, pv = _f(np.array(v, dtype=np.float32, copy=True))
+    lib().or_adamw_step(pW, pg, pm, pv, ctypes.c_int64(W.size), ctypes.c_float(lr),
+                        ctypes.c_float(beta1), ctypes.c_float(beta2), ctypes.c_float(eps),
+                        ctypes.c_float(weight_decay), ctypes.c_float(beta1 ** step),
+                        ctypes.c_float(beta2 ** step), int(clear_grad))
+    return W, g, m, v

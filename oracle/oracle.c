@@ -545,3 +545,52 @@ void or_vsa_dots(const float* preds, const uint32_t* bits, float* dots, int Bn, 
             dots[(size_t)b * K + k] = (float)s;
         }
 }
+
+/* surprise-momentum.glsl:53-114.  fmin/fmax give the clamps a defined result for a NaN
+ * update (the GLSL clamp leaves it undefined); every other branch follows the shader. */
+void or_surprise_momentum_step(float* W, float* grad, float* s_bar, float* delta,
+                               const float* recalled, int64_t n, float eta_base, float alpha,
+                               float lambda_recall, float surprise_floor, float weight_decay,
+                               float clip_max, int clear_grad) {
+    for (int64_t i = 0; i < n; ++i) {
+        const double g = grad[i], r = recalled ? recalled[i] : 0.0;
+        if (!isfinite(g) || !isfinite(r)) {  /* shader :71-77 */
+            if (delta) delta[i] = 0.0f;
+            if (clear_grad) grad[i] = 0.0f;
+            continue;
+        }
+        const double g_eff = g + (double)lambda_recall * r;            /* :80 */
+        const double pe = fabs(g - r);                                    /* :83 */
+        double sp = s_bar[i];
+        if (!isfinite(sp)) sp = 0.0;                                      /* :89 */
+        double s = (double)alpha * pe + (1.0 - (double)alpha) * sp;       /* :90 */
+        s = fmin(s, 5.0);                                                 /* :92 */
+        s_bar[i] = (float)s;
+        const double lr = (double)eta_base * (1.0 + fmax(s, (double)surprise_floor)); /* :97 */
+        double d = lr * g_eff + (double)eta_base * weight_decay * (double)W[i];       /* :100-104 */
+        d = fmin(fmax(d, -(double)clip_max), (double)clip_max);          /* :107 */
+        double wn = (double)W[i] - d;                                     /* :110 */
+        if (!isfinite(wn)) wn = 0.0;                                      /* :112 */
+        W[i] = (float)fmin(fmax(wn, -10.0), 10.0);                        /* :113 */
+        if (delta) delta[i] = (float)d;
+        if (clear_grad) grad[i] = 0.0f;
+    }
+}
+
+/* adamw-update.glsl:41-61 */
+void or_adamw_step(float* W, float* grad, float* m, float* v, int64_t n, float lr, float beta1,
+                   float beta2, float eps, float weight_decay, float beta1_t, float beta2_t,
+                   int clear_grad) {
+    for (int64_t i = 0; i < n; ++i) {
+        const double g = grad[i];
+        const double m_new = (double)beta1 * m[i] + (1.0 - (double)beta1) * g;
+        const double v_new = (double)beta2 * v[i] + (1.0 - (double)beta2) * g * g;
+        m[i] = (float)m_new;
+        v[i] = (float)v_new;
+        const double m_hat = m_new / fmax(1e-12, 1.0 - (double)beta1_t);
+        const double v_hat = v_new / fmax(1e-12, 1.0 - (double)beta2_t);
+        const double decayed = (double)W[i] * (1.0 - (double)lr * weight_decay);
+        W[i] = (float)(decayed - (double)lr * m_hat / (sqrt(fmax(v_hat, 0.0)) + (double)eps));
+        if (clear_grad) grad[i] = 0.0f;
+    }
+}

@@ -86,6 +86,17 @@ void or_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32
 void or_vsa_dots(const float* preds, const uint32_t* bits, float* dots, int Bn, int K, int D,
                  int words);
 
+/* surprise-momentum.glsl:53-114, one tensor (recalled / delta may be NULL); updates W, s_bar,
+ * delta and (clear_grad) grad in place */
+void or_surprise_momentum_step(float* W, float* grad, float* s_bar, float* delta,
+                               const float* recalled, int64_t n, float eta_base, float alpha,
+                               float lambda_recall, float surprise_floor, float weight_decay,
+                               float clip_max, int clear_grad);
+/* adamw-update.glsl:41-61 (adam-update.glsl with weight_decay 0), one tensor, in place */
+void or_adamw_step(float* W, float* grad, float* m, float* v, int64_t n, float lr, float beta1,
+                   float beta2, float eps, float weight_decay, float beta1_t, float beta2_t,
+                   int clear_grad);
+
 int or_num_threads(void);
 
 #ifdef __cplusplus

@@ -19,7 +19,11 @@ Forward definitions used (reference file:line):
   vsa project   y = unpack(bits) W^T + b                        vsa-unpack-project.glsl
   vsa surrogate sum_k w_k mean_i relu(gamma - y_i z_ki) + lambda/D * relu(delta-(dw-dr(z)))
                 vsa-surrogate-loss-forward.glsl / -backward.glsl:56-88
+  optimizers    torch.optim.AdamW / torch.optim.Adam, three steps  adamw-update.glsl:41-61,
+                                                                 adam-update.glsl
+Run with a list of set names (e.g. `optim`) to write only those files.
 """
+import sys
 import os
 
 import numpy as np
@@ -259,18 +263,48 @@ def gen_vsa(rng):
          lambda_c=np.float32(lam), scale=np.float32(scale))
 
 
-def main():
+def gen_optim(rng):
+    """AdamW (decoupled decay) and Adam over three steps with fresh gradients each step;
+    torch's update is W(1 - lr wd) - lr/bc1 m / (sqrt(v)/sqrt(bc2) + eps), the shader's
+    W(1 - lr wd) - lr m_hat / (sqrt(v_hat) + eps) written differently."""
+    n = 37
+    W0 = rng.standard_normal(n).astype(np.float32)
+    grads = (rng.standard_normal((3, n)) * np.array([1.0, 1e-3, 10.0])[:, None]).astype(np.float32)
+    # hyperparameters exactly representable in float32: the shader (and the ABI) take them as
+    # fp32 push constants, so e.g. beta2 = 0.999 would differ from torch's double by 1.3e-5
+    for tag, cls, kw in (("adamw", torch.optim.AdamW, dict(lr=2.0**-7, betas=(0.875, 1 - 2.0**-10),
+                                                           eps=2.0**-26, weight_decay=0.125)),
+                         ("adam", torch.optim.Adam, dict(lr=2.0**-8, betas=(0.75, 0.984375),
+                                                         eps=2.0**-20, weight_decay=0.0))):
+        w = t(W0)
+        w.requires_grad_(True)
+        opt = cls([w], **kw)
+        Ws, ms, vs = [], [], []
+        for k in range(3):
+            w.grad = t(grads[k])
+            opt.step()
+            st = opt.state[w]
+            Ws.append(f32(w))
+            ms.append(f32(st["exp_avg"]))
+            vs.append(f32(st["exp_avg_sq"]))
+        save("optim_" + tag, W0=W0, grads=grads, W=np.stack(Ws), m=np.stack(ms), v=np.stack(vs),
+             lr=np.float32(kw["lr"]), beta1=np.float32(kw["betas"][0]),
+             beta2=np.float32(kw["betas"][1]), eps=np.float32(kw["eps"]),
+             weight_decay=np.float32(kw["weight_decay"]))
+
+
+def main(only=()):
     rng = np.random.default_rng(20261201)
-    gen_linear(rng)
-    gen_act(rng)
-    gen_glu(rng)
-    gen_layernorm(rng)
-    gen_rmsnorm(rng)
-    gen_softmax_xent(rng)
-    gen_attention(rng)
-    gen_vsa(rng)
+    sets = [("linear", gen_linear), ("act", gen_act), ("glu", gen_glu),
+            ("layernorm", gen_layernorm), ("rmsnorm", gen_rmsnorm),
+            ("softmax_xent", gen_softmax_xent), ("attention", gen_attention), ("vsa", gen_vsa)]
+    for name, fn in sets:
+        if not only or name in only:
+            fn(rng)
+    if not only or "optim" in only:
+        gen_optim(np.random.default_rng(20261202))
     print("golden vectors written to", HERE)
 
 
 if __name__ == "__main__":
-    main()
+    main(tuple(sys.argv[1:]))

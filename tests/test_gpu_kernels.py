@@ -524,3 +524,82 @@ def test_errors_are_reported(gn):
         X = torch.zeros((8, 16), device="cuda:0")
         gn.rmsnorm_bwd(X, X, torch.ones(16, device="cuda:0"), torch.ones(8, device="cuda:0"),
                        ws=torch.empty(1, dtype=torch.uint8, device="cuda:0"))
+
+
+# ---------------------------------------------------------------------------- optimizers
+def _opt_tensors(r, sizes, offset=0):
+    """fp32 tensors of the given sizes; offset > 0 makes every tensor a view that starts
+    `offset` floats into its storage (misaligned for 16-byte vectors)."""
+    def mk(a):
+        full = torch.zeros(a.size + offset, device="cuda:0")
+        full[offset:] = torch.from_numpy(a.astype(np.float32)).to("cuda:0")
+        return full[offset:]
+    return [mk(r.standard_normal(n)) for n in sizes]
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_adamw_step_multi_tensor(gn, offset):
+    """gn_adamw_step over 30 tensors (two launches of at most 24), ragged sizes (n % 4 != 0)
+    and, with offset 1, misaligned storage (scalar path); three steps against the oracle."""
+    r = rng_(40)
+    sizes = [1, 3, 4, 5, 255, 2049, 4096 + 7] + [int(x) for x in r.integers(1, 3000, 23)]
+    W = _opt_tensors(r, sizes, offset)
+    m = [torch.zeros_like(w) for w in W]
+    v = [torch.zeros_like(w) for w in W]
+    W_lp = [torch.empty(w.numel(), dtype=torch.bfloat16, device="cuda:0") for w in W]
+    hW, hm, hv = [w.cpu().numpy() for w in W], [np.zeros(n, np.float32) for n in sizes], \
+        [np.zeros(n, np.float32) for n in sizes]
+    kw = dict(lr=2e-3, beta1=0.9, beta2=0.99, eps=1e-6, weight_decay=0.05)
+    for step in range(1, 4):
+        G = _opt_tensors(r, sizes, offset)
+        hG = [g.cpu().numpy() for g in G]
+        gn.adamw_step([dict(W=w, grad=g, state0=a, state1=b, W_bf16=lp)
+                       for w, g, a, b, lp in zip(W, G, m, v, W_lp)], step=step, **kw)
+        torch.cuda.synchronize()
+        for i in range(len(sizes)):
+            hW[i], _, hm[i], hv[i] = oracle.adamw_step(hW[i], hG[i], hm[i], hv[i], step=step, **kw)
+            assert rel_err(host(W[i]), hW[i]) < 1e-5, (step, i, sizes[i])
+            assert rel_err(host(m[i]), hm[i]) < 1e-5 and rel_err(host(v[i]), hv[i]) < 1e-5
+            assert not host(G[i]).any()  # clear_grad
+            assert np.array_equal(host(W_lp[i]), host(W[i].to(torch.bfloat16)))
+
+
+def test_surprise_momentum_step_multi_tensor(gn):
+    """gn_surprise_momentum_step with non-finite gradients, recalled gradients, an Inf s_bar,
+    clipping and the weight clamp, against the oracle over two steps."""
+    r = rng_(41)
+    sizes = [7, 1000, 4097, 33]
+    W = _opt_tensors(r, sizes)
+    W[1][:5] = torch.tensor([9.99, -9.99, 0.0, 1.0, -1.0], device="cuda:0")
+    S = [torch.zeros_like(w) for w in W]
+    S[2][::97] = float("inf")
+    D = [torch.empty_like(w) for w in W]
+    R = [None, _opt_tensors(r, [1000])[0], None, _opt_tensors(r, [33])[0]]
+    hW, hS = [host(w) for w in W], [host(s) for s in S]
+    kw = dict(eta_base=0.05, alpha=0.8, lambda_recall=0.3, surprise_floor=0.01,
+              weight_decay=0.02, clip_max=0.5)
+    for step in range(2):
+        G = _opt_tensors(r, sizes)
+        for g in G:
+            g.mul_(3.0)
+        G[0][2] = float("nan")
+        G[2][100] = float("-inf")
+        hG = [host(g) for g in G]
+        gn.surprise_momentum_step([dict(W=w, grad=g, state0=s, state1=d, recalled=rc)
+                                   for w, g, s, d, rc in zip(W, G, S, D, R)], **kw)
+        torch.cuda.synchronize()
+        for i in range(len(sizes)):
+            hW[i], _, hS[i], hD = oracle.surprise_momentum_step(
+                hW[i], hG[i], hS[i], recalled=None if R[i] is None else host(R[i]), **kw)
+            assert rel_err(host(W[i]), hW[i]) < 1e-5, (step, i)
+            assert rel_err(host(S[i]), hS[i]) < 1e-5 and rel_err(host(D[i]), hD) < 1e-5
+            assert not host(G[i]).any()
+    assert np.abs(host(W[1])).max() <= 10.0
+
+
+def test_optimizer_rejects_bad_entries(gn):
+    w = torch.zeros(8, device="cuda:0")
+    with pytest.raises(gn.GnError):
+        gn.adamw_step([dict(W=w, grad=w, state0=w)])  # AdamW needs v
+    with pytest.raises(gn.GnError):
+        gn.surprise_momentum_step([dict(W=w, grad=torch.zeros(9, device="cuda:0"), state0=w)])

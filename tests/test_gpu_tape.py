@@ -375,3 +375,61 @@ def test_decoder_stack_through_tape(env):
     errs = {k: rel_err(got[k], want[k].cpu().numpy()) for k in got}
     bad = {k: v for k, v in errs.items() if not v < 2e-2}
     assert not bad, f"relative errors above 2e-2: {bad} (all: {errs})"
+
+
+def test_training_step_with_optimizers(env):
+    """BASELINE configs[0] MLP, full training step as vsa_training_step orders it
+    (bindings.cpp:3196-3279): backward, optimizer over the tape's gradients, end; then a
+    second step on the updated weights.  Weights after each step against oracle grads +
+    oracle optimizer; bf16 weights keep an fp32 master and receive the rounded update."""
+    gc, gb, dev = env
+    r = np.random.default_rng(7)
+    B = 64
+    X = r.standard_normal((B, 784)).astype(np.float32)
+    y = r.integers(0, 10, size=B).astype(np.int32)
+    W1, W2 = xavier(r, 256, 784), xavier(r, 10, 256)
+    b1, b2 = np.zeros(256, np.float32), np.zeros(10, np.float32)
+    tX, ty = T(X), T(y, torch.int32)
+    params = [T(W1), T(b1), T(W2), T(b2)]
+    for opt_kind in ["adamw", "surprise"]:
+        ws = [p.clone() for p in params]
+        hw = [p.cpu().numpy() for p in ws]
+        if opt_kind == "adamw":
+            opt = gb.AdamW(ws, lr=1e-2, weight_decay=0.01)
+            st = [[np.zeros_like(h), np.zeros_like(h)] for h in hw]
+        else:
+            opt = gb.SurpriseMomentumOptimizer(ws, lr=1e-2, alpha=0.9, clip=1.0)
+            st = [np.zeros_like(h) for h in hw]
+        for step in range(1, 3):
+            tW1, tb1, tW2, tb2 = ws
+            Z = (tX @ tW1.t() + tb1).contiguous()
+            H = torch.relu(Z).contiguous()
+            L = (H @ tW2.t() + tb2).contiguous()
+            loss = torch.zeros(1, device="cuda:0")
+            tape = gb.create_tape_context(dev)
+            tape.begin()
+            n1 = tape.record_op(gc.OpType.Linear, [gb.tref(tX)], [gb.tref(Z)])
+            tape.save_for_backward(n1, [tW1.data_ptr(), tb1.data_ptr()])
+            tape.record_op(gc.OpType.ReLU, [gb.tref(Z, True)], [gb.tref(H)])
+            n3 = tape.record_op(gc.OpType.Linear, [gb.tref(H, True)], [gb.tref(L)])
+            tape.save_for_backward(n3, [tW2.data_ptr(), tb2.data_ptr()])
+            ce = tape.record_op(gc.OpType.CrossEntropy, [gb.tref(L, True), gb.tref(ty)],
+                                [gb.tref(loss)], gb.cross_entropy_params(1.0 / B))
+            tape.backward(ce, 0)
+            assert opt.step(tape) == 4
+            tape.end()
+            torch.cuda.synchronize()
+            # oracle: gradients from the same weights, then the same update
+            hZ, hH, hL = Z.cpu().numpy(), H.cpu().numpy(), L.cpu().numpy()
+            dL = oracle.xent_bwd(hL, y, 1.0 / B)
+            _, dW2, db2 = oracle.linear_bwd(dL, hH, hw[2])
+            dZ = oracle.act_bwd("relu", oracle.linear_bwd(dL, hH, hw[2])[0], hZ)
+            _, dW1, db1 = oracle.linear_bwd(dZ, X, hw[0], need_dx=False)
+            for i, g in enumerate([dW1, db1, dW2, db2]):
+                if opt_kind == "adamw":
+                    hw[i], _, st[i][0], st[i][1] = oracle.adamw_step(
+                        hw[i], g, st[i][0], st[i][1], lr=1e-2, weight_decay=0.01, step=step)
+                else:
+                    hw[i], _, st[i], _ = oracle.surprise_momentum_step(
+                        hw[i], g, st[i], eta_base=1e-2, alpha=0.9, clip_max=1.0)
+                assert rel_err(ws[i].cpu().numpy(), hw[i]) < 1e-4, (opt_kind, step, i)

@@ -250,3 +250,56 @@ def test_vsa_surrogate_reference_kats():
     dP = oracle.vsa_surrogate_bwd(p, bits, res, w, gamma=0.1, delta=0.5, lambda_c=0.3)
     np.testing.assert_allclose(dP[0, 1], 0.3 * y / D, rtol=1e-6)
     assert np.count_nonzero(dP[0, [0, 2, 3]]) == 0
+
+
+# ---------------------------------------------------------------------------- optimizers
+def test_adamw_and_adam_golden_three_steps():
+    """torch.optim.AdamW / Adam (float64) over three steps pin adamw-update.glsl's formula
+    (and adam-update.glsl = weight_decay 0), including the bias corrections per step."""
+    for tag in ["adamw", "adam"]:
+        g = golden("optim_" + tag)
+        W, m, v = g["W0"], np.zeros_like(g["W0"]), np.zeros_like(g["W0"])
+        for k in range(3):
+            W, gr, m, v = oracle.adamw_step(W, g["grads"][k], m, v, lr=float(g["lr"]),
+                                            beta1=float(g["beta1"]), beta2=float(g["beta2"]),
+                                            eps=float(g["eps"]),
+                                            weight_decay=float(g["weight_decay"]), step=k + 1)
+            assert rel_err(W, g["W"][k]) < TOL and rel_err(m, g["m"][k]) < TOL
+            assert rel_err(v, g["v"][k]) < TOL
+            assert not gr.any()  # clear_grad zeroes the gradient
+
+
+def test_adamw_first_step_is_signed_lr():
+    # at t = 1, m_hat = g and v_hat = g^2 exactly, so the step is lr * g / (|g| + eps)
+    g = np.array([3.0, -0.5, 1e-3], np.float32)
+    W, _, _, _ = oracle.adamw_step(np.zeros(3), g, np.zeros(3), np.zeros(3), lr=0.01, eps=0.0)
+    assert np.allclose(W, -0.01 * np.sign(g), rtol=1e-6)
+
+
+def test_surprise_momentum_known_answers():
+    """Hand-computed cases of surprise-momentum.glsl:53-114 (eta 0.1, alpha 0.5, lambda 0,
+    floor 0.01, clip 1): each exercises one branch."""
+    W0 = np.array([1.0, 1.0, 1.0, 10.5, 2.0, -3.0], np.float32)
+    g = np.array([0.2, 50.0, np.nan, 0.0, np.inf, 0.1], np.float32)
+    s0 = np.array([0.4, 0.0, 0.7, 0.0, 0.2, np.inf], np.float32)
+    W, gr, s, d = oracle.surprise_momentum_step(W0, g, s0, eta_base=0.1, alpha=0.5,
+                                                weight_decay=0.1, clip_max=1.0)
+    # [0] s = 0.5*0.2 + 0.5*0.4 = 0.3; lr = 0.1*1.3 = 0.13; d = 0.026 + 0.1*0.1*1 = 0.036
+    # [1] s = min(25, 5) = 5; d = 0.6*50 + 0.01 -> clipped to 1; W = 0
+    # [2] NaN gradient: W, s_bar unchanged, delta 0
+    # [3] g = 0: s = 0 -> floor 0.01; d = 0.1*0.1*10.5 = 0.105; W = 10.395 -> clamped to 10
+    # [4] Inf gradient: skipped like NaN
+    # [5] s_bar Inf is read as 0: s = 0.05; d = 0.1*1.05*0.1 + 0.01*(-3) = -0.0195; W = -2.9805
+    assert np.allclose(W, [0.964, 0.0, 1.0, 10.0, 2.0, -2.9805], rtol=1e-6, atol=1e-7)
+    assert np.allclose(s, [0.3, 5.0, 0.7, 0.0, 0.2, 0.05], rtol=1e-6)
+    assert np.allclose(d, [0.036, 1.0, 0.0, 0.105, 0.0, -0.0195], rtol=1e-6, atol=1e-7)
+    assert not gr.any()
+
+
+def test_surprise_momentum_recall_blend():
+    # lambda and the recalled gradient enter twice: g_eff = g + lambda r, surprise |g - r|
+    W, _, s, d = oracle.surprise_momentum_step(np.zeros(1), np.array([0.3]), np.zeros(1),
+                                               recalled=np.array([0.1]), eta_base=1.0,
+                                               alpha=1.0, lambda_recall=0.5, clip_max=10.0)
+    # s = |0.3 - 0.1| = 0.2; lr = 1.2; d = 1.2 * (0.3 + 0.05) = 0.42
+    assert np.allclose(s, [0.2]) and np.allclose(d, [0.42]) and np.allclose(W, [-0.42])
