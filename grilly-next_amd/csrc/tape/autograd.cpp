@@ -164,6 +164,19 @@ void BackwardEngine::dispatch(Node* n) {
         case OpType::VSASurrogateLoss: bwd_vsa_surrogate(n); break;
         case OpType::FusedGLU: bwd_fused_glu(n); break;
         case OpType::Embedding: bwd_embedding(n); break;
+        case OpType::Sub: bwd_binary(n, GN_BIN_SUB); break;
+        case OpType::Mul: bwd_binary(n, GN_BIN_MUL); break;
+        case OpType::Div: bwd_binary(n, GN_BIN_DIV); break;
+        case OpType::Neg: bwd_binary(n, GN_BIN_NEG); break;
+        case OpType::Sum: bwd_reduce(n, GN_RED_SUM); break;
+        case OpType::Mean: bwd_reduce(n, GN_RED_MEAN); break;
+        case OpType::Transpose: bwd_transpose(n); break;
+        case OpType::MSELoss: bwd_mse(n); break;
+        case OpType::MatMul: bwd_matmul(n); break;
+        case OpType::VSALoRAExpand: bwd_vsa_lora_expand(n); break;
+        case OpType::VSACosineBlendLoss: bwd_vsa_cosine_blend(n); break;
+        case OpType::CubeMindSurprise:
+        case OpType::TemporalSurprise: bwd_surprise_passthrough(n); break;
         default: stats_.cpu_fallbacks++; break;  // no handler (autograd.cpp:126-128)
     }
 }
@@ -506,6 +519,184 @@ void TapeContext::end() {
     engine_.clear_grads();
     seq_ = 0;
     recording_ = false;
+}
+
+}  // namespace autograd
+}  // namespace grilly
+
+namespace grilly {
+namespace autograd {
+
+// Sub / Mul / Div / Neg (stubs at autograd.cpp:631-654): elementwise, no broadcasting.
+// Sub's first input borrows the upstream buffer (backward_sub :632-633 does the same).
+void BackwardEngine::bwd_binary(Node* n, int op) {
+    const TensorRef& a = n->inputs[0];
+    const bool two = op != GN_BIN_NEG;
+    if (two && n->num_inputs < 2) throw std::invalid_argument("binary op: two inputs expected");
+    const TensorRef* b = two ? &n->inputs[1] : nullptr;
+    const size_t numel = n->outputs[0].numel();
+    if (a.numel() != numel || (b && b->numel() != numel))
+        throw std::invalid_argument("binary op: broadcasting inputs are not supported");
+    if (b && b->dtype != a.dtype) throw std::invalid_argument("binary op: inputs differ in dtype");
+    const int dt = gn_dtype(a.dtype, "binary op");
+    const bool ga = a.requires_grad, gb = b && b->requires_grad;
+    if (!ga && !gb) return;
+    uint64_t dA = 0, dB = gb ? alloc_grad(b->size_bytes()) : 0;
+    if (ga) {
+        if (op == GN_BIN_SUB) {
+            dA = reinterpret_cast<uint64_t>(gout(n));
+            borrowed_ |= 1u;
+        } else {
+            dA = alloc_grad(a.size_bytes());
+        }
+    }
+    const bool kernel_da = ga && op != GN_BIN_SUB;
+    if (kernel_da || gb) {
+        gn_call(gn_binary_bwd(op, gout(n), P(a.buffer_id), b ? P(b->buffer_id) : nullptr,
+                              kernel_da ? P(dA) : nullptr, gb ? P(dB) : nullptr, (int64_t)numel, dt,
+                              0, dev_.stream()),
+                "binary op backward");
+        stats_.shaders_dispatched++;
+    }
+    n->grad_input_buffers[0] = dA;
+    if (gb) n->grad_input_buffers[1] = dB;
+}
+
+// Sum / Mean (stubs at autograd.cpp:695-707): a reduction over the trailing elements of the
+// input, outputs[0].numel() rows of input.numel() / outputs[0].numel() each (a scalar output
+// is the full reduction).
+void BackwardEngine::bwd_reduce(Node* n, int op) {
+    const TensorRef& x = n->inputs[0];
+    if (!x.requires_grad) return;
+    const size_t outer = n->outputs[0].numel(), total = x.numel();
+    if (outer == 0 || total % outer != 0)
+        throw std::invalid_argument("Sum/Mean: output size must divide the input size");
+    uint64_t dX = alloc_grad(x.size_bytes());
+    gn_call(gn_reduce_bwd(op, gout(n), P(dX), (int64_t)outer, (int64_t)(total / outer),
+                          gn_dtype(x.dtype, "Sum/Mean"), 0, dev_.stream()),
+            "Sum/Mean backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dX;
+}
+
+// Transpose of the last two dims (stub at autograd.cpp:689-693).
+void BackwardEngine::bwd_transpose(Node* n) {
+    const TensorRef& x = n->inputs[0];
+    if (!x.requires_grad) return;
+    if (x.ndim < 2) throw std::invalid_argument("Transpose: input needs two dims or more");
+    const int rows = (int)x.shape[x.ndim - 2], cols = (int)x.shape[x.ndim - 1];
+    const int64_t batch = (int64_t)(x.numel() / ((size_t)rows * cols));
+    uint64_t dX = alloc_grad(x.size_bytes());
+    gn_call(gn_transpose_bwd(gout(n), P(dX), batch, rows, cols, gn_dtype(x.dtype, "Transpose"), 0,
+                             dev_.stream()),
+            "Transpose backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dX;
+}
+
+// MSELoss (stub at autograd.cpp:663-667): inputs[0] = pred, inputs[1] = target; the upstream
+// gradient is a scalar buffer (or the loss sentinel, read as 1).
+void BackwardEngine::bwd_mse(Node* n) {
+    const TensorRef& p = n->inputs[0];
+    if (!p.requires_grad) return;
+    if (n->num_inputs < 2 || n->inputs[1].numel() != p.numel())
+        throw std::invalid_argument("MSELoss: target must match the prediction's size");
+    MSELossParams mp = params_of<MSELossParams>(n);
+    const float scale = mp.has_scale ? mp.scale : (float)(1.0 / (double)p.numel());
+    const float* dL = n->grad_output_buffer > 1 ? (const float*)P(n->grad_output_buffer) : nullptr;
+    uint64_t dP = alloc_grad(p.size_bytes());
+    gn_call(gn_mse_bwd(P(p.buffer_id), P(n->inputs[1].buffer_id), dL, P(dP), (int64_t)p.numel(),
+                       scale, gn_dtype(p.dtype, "MSELoss"), 0, dev_.stream()),
+            "MSELoss backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dP;
+}
+
+// MatMul (stub at autograd.cpp:543-549): C [M x N] = A [M x K] . B [K x N]:
+// dA = dC B^T, dB = A^T dC, each in its input's dtype.
+void BackwardEngine::bwd_matmul(Node* n) {
+    if (n->num_inputs < 2) throw std::invalid_argument("MatMul: two inputs expected");
+    const TensorRef& a = n->inputs[0];
+    const TensorRef& b = n->inputs[1];
+    const int M = (int)a.rows(), K = (int)a.last(), N = (int)b.last();
+    if ((int)b.rows() != K || a.dtype != b.dtype)
+        throw std::invalid_argument("MatMul: shapes [M x K] . [K x N] of one dtype expected");
+    const int dt = gn_dtype(a.dtype, "MatMul");
+    if (a.requires_grad) {
+        uint64_t dA = alloc_grad(a.size_bytes());
+        gn_call(gn_gemm(gout(n), P(b.buffer_id), N, nullptr, nullptr, 0, P(dA), M, K, 0, 1, dt, dt, 0,
+                        dev_.stream()),
+                "MatMul dA");
+        stats_.shaders_dispatched++;
+        n->grad_input_buffers[0] = dA;
+    }
+    if (b.requires_grad) {
+        uint64_t dB = alloc_grad(b.size_bytes());
+        gn_call(gn_gemm(P(a.buffer_id), gout(n), M, nullptr, nullptr, 0, P(dB), K, N, 1, 0, dt, dt, 0,
+                        dev_.stream()),
+                "MatMul dB");
+        stats_.shaders_dispatched++;
+        n->grad_input_buffers[1] = dB;
+    }
+}
+
+// backward_vsa_lora_expand (autograd.cpp:817-843): inputs[0] = coefficients [Bn, K*rank]
+// (or [Bn, K, rank]); saved[0] = basis B [D x rank], saved[1] = coefficients.  The
+// coefficient gradient flows to inputs[0]; the basis gradient goes to the table under the
+// basis id (for the optimizer), as the reference does.
+void BackwardEngine::bwd_vsa_lora_expand(Node* n) {
+    VSALoRAExpandParams p = params_of<VSALoRAExpandParams>(n);
+    if (n->num_saved < 2 || !n->saved_buffer_ids[0] || !n->saved_buffer_ids[1])
+        throw std::invalid_argument("VSALoRAExpand: saved basis/coefficients missing");
+    const int Bn = (int)n->inputs[0].shape[0];
+    uint64_t dC = alloc_grad((size_t)Bn * p.K * p.rank * 4);
+    uint64_t dB = alloc_grad((size_t)p.D * p.rank * 4);
+    gn_call(gn_vsa_lora_expand_bwd((const float*)gout(n), (const float*)P(n->saved_buffer_ids[0]),
+                                   (const float*)P(n->saved_buffer_ids[1]), (float*)P(dC), (float*)P(dB),
+                                   Bn, (int)p.K, (int)p.D, (int)p.rank, 1.0f, 0, dev_.stream()),
+            "VSA LoRA-expand backward");
+    stats_.shaders_dispatched += 2;
+    n->grad_input_buffers[0] = dC;
+    contribute(n->saved_buffer_ids[0], dB, 0, (size_t)p.D * p.rank, true);
+}
+
+// backward_vsa_cosine_blend_loss (autograd.cpp:845-859): inputs[0] = preds [Bn, K, D],
+// inputs[1] = true bits; saved [n-3] = router weights, [n-2] = blended, [n-1] = loss_info;
+// grad_scale 10 on a zeroed buffer.
+void BackwardEngine::bwd_vsa_cosine_blend(Node* n) {
+    VSACosineBlendLossParams p = params_of<VSACosineBlendLossParams>(n);
+    if (n->num_saved < 3) throw std::invalid_argument("VSACosineBlendLoss: weights/blended/loss_info not saved");
+    const int Bn = (int)n->inputs[0].shape[0];
+    const int words = (int)((p.D + 31) / 32);
+    uint64_t dP = alloc_grad((size_t)Bn * p.K * p.D * 4);
+    const uint64_t* s = n->saved_buffer_ids + n->num_saved - 3;
+    gn_call(gn_vsa_cosine_blend_bwd((const uint32_t*)P(n->inputs[1].buffer_id), (const float*)P(s[0]),
+                                    (const float*)P(s[1]), (const float*)P(s[2]), (float*)P(dP), Bn,
+                                    (int)p.K, (int)p.D, words, 10.0f, 0, dev_.stream()),
+            "VSA cosine-blend backward");
+    stats_.shaders_dispatched++;
+    n->grad_input_buffers[0] = dP;
+}
+
+// backward_cubemind_surprise / backward_temporal_surprise (autograd.cpp:669-685): the
+// gradient passes through unchanged and the node's params are overwritten with the
+// multiplier (1 + alpha surprise, or clamp(temporal_multiplier alpha, -1, 1)) for the caller.
+void BackwardEngine::bwd_surprise_passthrough(Node* n) {
+    if (!n->inputs[0].requires_grad) return;
+    float mult;
+    if (n->op == OpType::CubeMindSurprise) {
+        float alpha = 0.5f;
+        if (n->params_size >= sizeof(float)) std::memcpy(&alpha, n->params, sizeof(float));
+        mult = 1.0f + alpha * n->emotion[0];
+    } else {
+        TemporalSurpriseParams t = params_of<TemporalSurpriseParams>(n);
+        mult = std::min(1.0f, std::max(-1.0f, t.temporal_multiplier * t.alpha));
+    }
+    std::memcpy(n->params, &mult, sizeof(float));
+    n->params_size = sizeof(float);
+    n->grad_input_buffers[0] = reinterpret_cast<uint64_t>(gout(n));
+    borrowed_ |= 1u;
+    stats_.shaders_dispatched++;
 }
 
 }  // namespace autograd

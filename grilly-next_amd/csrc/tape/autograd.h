@@ -103,6 +103,7 @@ struct AttentionParams {
 };
 struct CrossEntropyParams { float scale; uint32_t has_scale; };  // scale default 1 (no 1/B)
 struct FusedGLUParams { uint32_t kind; };                       // GN_GLU_* kind
+struct MSELossParams { float scale; uint32_t has_scale; };      // scale default 1/n (mean)
 
 static constexpr uint32_t kMaxNodeIO = 8;
 
@@ -178,6 +179,14 @@ private:
     void bwd_vsa_surrogate(Node* n);
     void bwd_fused_glu(Node* n);
     void bwd_embedding(Node* n);
+    void bwd_binary(Node* n, int op);
+    void bwd_reduce(Node* n, int op);
+    void bwd_transpose(Node* n);
+    void bwd_mse(Node* n);
+    void bwd_matmul(Node* n);
+    void bwd_vsa_lora_expand(Node* n);
+    void bwd_vsa_cosine_blend(Node* n);
+    void bwd_surprise_passthrough(Node* n);
 
     Device& dev_;
     Stats stats_{};

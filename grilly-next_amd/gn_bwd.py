@@ -28,9 +28,12 @@ SYMBOLS = [
     "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
-    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd",
-    "gn_surprise_momentum_step", "gn_adamw_step", "gn_add_inplace",
+    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd", "gn_binary_bwd",
+    "gn_reduce_bwd", "gn_transpose_bwd", "gn_mse_bwd", "gn_vsa_lora_expand_bwd",
+    "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_add_inplace",
 ]
+BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
+RED = {"sum": 0, "mean": 1}
 
 
 class GnError(RuntimeError):
@@ -82,6 +85,12 @@ _SIGS = {
     "gn_vsa_workspace_bytes": ([_I, _I], _Z),
     "gn_vsa_surrogate_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F, _U, _P], _I),
     "gn_embedding_bwd": ([_P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
+    "gn_binary_bwd": ([_I, _P, _P, _P, _P, _P, _L, _I, _U, _P], _I),
+    "gn_reduce_bwd": ([_I, _P, _P, _L, _L, _I, _U, _P], _I),
+    "gn_transpose_bwd": ([_P, _P, _L, _I, _I, _I, _U, _P], _I),
+    "gn_mse_bwd": ([_P, _P, _P, _P, _L, _F, _I, _U, _P], _I),
+    "gn_vsa_lora_expand_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _U, _P], _I),
+    "gn_vsa_cosine_blend_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _U, _P], _I),
     "gn_surprise_momentum_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     "gn_adamw_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     "gn_add_inplace": ([_P, _P, _L, _I, _P], _I),
@@ -405,6 +414,63 @@ def embedding_bwd(dX, ids, V, dE=None, accumulate=False):
     _check(lib().gn_embedding_bwd(_ptr(dX), _ptr(ids), _ptr(dE), T, d, V, _dt(dX),
                                   ACCUMULATE if accumulate else 0, _stream()), "gn_embedding_bwd")
     return dE
+
+
+def binary_bwd(op, dY, A=None, B=None, need_da=True, need_db=True):
+    """Sub / Mul / Div / Neg backward (no broadcasting); returns (dA, dB)."""
+    dA = torch.empty_like(dY) if need_da else None
+    dB = torch.empty_like(dY) if (need_db and op != "neg") else None
+    _check(lib().gn_binary_bwd(BIN[op], _ptr(dY), _ptr(A), _ptr(B), _ptr(dA), _ptr(dB),
+                               dY.numel(), _dt(dY), 0, _stream()), "gn_binary_bwd")
+    return dA, dB
+
+
+def reduce_bwd(op, dY, shape):
+    """Sum / Mean over the trailing elements: dY has one value per output row."""
+    dX = torch.empty(shape, dtype=dY.dtype, device=dY.device)
+    outer = dY.numel()
+    _check(lib().gn_reduce_bwd(RED[op], _ptr(dY), _ptr(dX), outer, dX.numel() // max(outer, 1),
+                               _dt(dY), 0, _stream()), "gn_reduce_bwd")
+    return dX
+
+
+def transpose_bwd(dY):
+    """dY [..., cols, rows] -> dX [..., rows, cols]."""
+    *lead, cols, rows = dY.shape
+    dX = torch.empty(*lead, rows, cols, dtype=dY.dtype, device=dY.device)
+    batch = dX.numel() // max(rows * cols, 1)
+    _check(lib().gn_transpose_bwd(_ptr(dY), _ptr(dX), batch, rows, cols, _dt(dY), 0, _stream()),
+           "gn_transpose_bwd")
+    return dX
+
+
+def mse_bwd(pred, target, scale=None, dLoss=None):
+    dP = torch.empty_like(pred)
+    scale = 1.0 / pred.numel() if scale is None else scale
+    _check(lib().gn_mse_bwd(_ptr(pred), _ptr(target), _ptr(dLoss), _ptr(dP), pred.numel(), scale,
+                            _dt(pred), 0, _stream()), "gn_mse_bwd")
+    return dP
+
+
+def vsa_lora_expand_bwd(dPreds, basis, coeffs):
+    """dPreds [Bn, K, D] fp32, basis [D, rank], coeffs [Bn, K, rank] -> (dCoeffs, dBasis)."""
+    Bn, K, D = dPreds.shape
+    rank = basis.shape[1]
+    dC = torch.empty(Bn, K, rank, device=dPreds.device)
+    dB = torch.empty(D, rank, device=dPreds.device)
+    _check(lib().gn_vsa_lora_expand_bwd(_ptr(dPreds), _ptr(basis), _ptr(coeffs), _ptr(dC), _ptr(dB),
+                                        Bn, K, D, rank, 1.0, 0, _stream()), "gn_vsa_lora_expand_bwd")
+    return dC, dB
+
+
+def vsa_cosine_blend_bwd(bits, weights, blended, loss_info, K, grad_scale=10.0):
+    """bits [Bn, words] (int32 view of u32), weights [Bn, K], blended [Bn, D], loss_info [Bn, 3]."""
+    Bn, D = blended.shape
+    dP = torch.empty(Bn, K, D, device=blended.device)
+    _check(lib().gn_vsa_cosine_blend_bwd(_ptr(bits), _ptr(weights), _ptr(blended), _ptr(loss_info),
+                                         _ptr(dP), Bn, K, D, bits.shape[1], grad_scale, 0, _stream()),
+           "gn_vsa_cosine_blend_bwd")
+    return dP
 
 
 def _addr(x):

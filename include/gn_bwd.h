@@ -246,6 +246,54 @@ int gn_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32_
 int gn_embedding_bwd(const void* dX, const int32_t* ids, float* dE, int T, int d, int V,
                      int dtype, unsigned flags, void* stream);
 
+/* ---- the remaining tape ops ------------------------------------------------------------ */
+/* The reference leaves these handlers as stubs that set a sentinel gradient id
+ * (autograd.cpp:543-711); the formulas here are the textbook ones. */
+#define GN_BIN_SUB 0 /* y = a - b: da = dy, db = -dy          (backward_sub :631-638) */
+#define GN_BIN_MUL 1 /* y = a * b: da = dy b, db = dy a       (backward_mul :640-646) */
+#define GN_BIN_DIV 2 /* y = a / b: da = dy / b, db = -dy a/b^2 (backward_div :648-654) */
+#define GN_BIN_NEG 3 /* y = -a:    da = -dy */
+/* Elementwise binary backward over n elements (no broadcasting); dA / dB nullable. */
+int gn_binary_bwd(int op, const void* dY, const void* A, const void* B, void* dA, void* dB,
+                  int64_t n, int dtype, unsigned flags, void* stream);
+
+#define GN_RED_SUM 0  /* backward_sum  :695-700 */
+#define GN_RED_MEAN 1 /* backward_mean :702-707 */
+/* Backward of a reduction over the trailing `inner` elements of each of `outer` rows:
+ * dX[o, i] (+)= dY[o] (x 1/inner for the mean). */
+int gn_reduce_bwd(int op, const void* dY, void* dX, int64_t outer, int64_t inner, int dtype,
+                  unsigned flags, void* stream);
+
+/* Backward of a transpose of the last two dims (backward_transpose :689-693):
+ * Y [batch, cols, rows] = X^T per batch, dX[b, r, c] (+)= dY[b, c, r]. */
+int gn_transpose_bwd(const void* dY, void* dX, int64_t batch, int rows, int cols, int dtype,
+                     unsigned flags, void* stream);
+
+/* MSE loss backward (backward_mse :663-667): loss = scale * sum (pred - target)^2, so
+ * dPred (+)= 2 scale (pred - target) g, g = dLoss[0] (dLoss NULL: g = 1). */
+int gn_mse_bwd(const void* pred, const void* target, const float* dLoss, void* dPred, int64_t n,
+               float scale, int dtype, unsigned flags, void* stream);
+
+/* VSA LoRA-expand backward (backward_vsa_lora_expand autograd.cpp:817-843,
+ * vsa-lora-expand-backward.glsl:38-63): forward preds[b,k,:] = B coeffs[b,k,:] with B [D x rank];
+ *   dCoeffs [Bn*K x rank] = scale dPreds B,   dBasis [D x rank] (+)= scale dPreds^T coeffs.
+ * All fp32; scale must be 1, the value the reference handler passes (autograd.cpp:834).
+ * GN_ACCUMULATE adds into dBasis (the shader's grad_B +=) and dCoeffs. */
+int gn_vsa_lora_expand_bwd(const float* dPreds, const float* basis, const float* coeffs,
+                           float* dCoeffs, float* dBasis, int Bn, int K, int D, int rank,
+                           float scale, unsigned flags, void* stream);
+
+/* VSA cosine-blend loss backward (backward_vsa_cosine_blend_loss autograd.cpp:845-859,
+ * vsa-cosine-blend-backward.glsl:37-70): with b = blended[b,:], y = +-1 from true_bits,
+ * loss_info[b] = {loss, dot(b, y), |b|^2}:
+ *   gb_i = -(y_i / (|b| sqrt(D)) - cos b_i / max(|b|^2, 1e-8)),  |b| = sqrt(max(|b|^2, 1e-8))
+ *   dPreds[b,k,i] (+)= clamp(gb_i weights[b,k] grad_scale, -1, 1)
+ * (the reference handler uses grad_scale 10 on a zeroed buffer). */
+int gn_vsa_cosine_blend_bwd(const uint32_t* true_bits, const float* weights,
+                            const float* blended, const float* loss_info, float* dPreds, int Bn,
+                            int K, int D, int words, float grad_scale, unsigned flags,
+                            void* stream);
+
 /* ---- optimizer steps (between TapeContext.backward and end) ---------------------------- */
 /* One parameter tensor of a multi-tensor optimizer step (all fp32, n elements). */
 typedef struct gn_opt_param {

@@ -357,3 +357,67 @@ def adamw_step(W, grad, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_
                         ctypes.c_float(weight_decay), ctypes.c_float(beta1 ** step),
                         ctypes.c_float(beta2 ** step), int(clear_grad))
     return W, g, m, v
+
+
+BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
+
+
+def binary_bwd(op, dY, A=None, B=None):
+    """Sub / Mul / Div / Neg backward; returns (dA, dB) (dB None for neg)."""
+    dY, pY = _f(dY)
+    A, pA = _f(A if A is not None else np.zeros_like(dY))
+    B, pB = _f(B if B is not None else np.ones_like(dY))
+    dA, pdA = _out(dY.shape)
+    dB, pdB = _out(dY.shape)
+    lib().or_binary_bwd(BIN[op], pY, pA, pB, pdA, pdB, ctypes.c_int64(dY.size))
+    return dA, (None if op == "neg" else dB)
+
+
+def reduce_bwd(op, dY, shape):
+    dY, pY = _f(dY)
+    dX, pX = _out(shape)
+    lib().or_reduce_bwd({"sum": 0, "mean": 1}[op], pY, pX, ctypes.c_int64(dY.size),
+                        ctypes.c_int64(dX.size // max(dY.size, 1)))
+    return dX
+
+
+def transpose_bwd(dY):
+    dY, pY = _f(dY)
+    *lead, cols, rows = dY.shape
+    dX, pX = _out((*lead, rows, cols))
+    lib().or_transpose_bwd(pY, pX, ctypes.c_int64(dX.size // max(rows * cols, 1)), rows, cols)
+    return dX
+
+
+def mse_bwd(P, T, scale=None, g=1.0):
+    P, pP = _f(P)
+    T, pT = _f(T)
+    dP, pd = _out(P.shape)
+    scale = 1.0 / P.size if scale is None else scale
+    lib().or_mse_bwd(pP, pT, ctypes.c_float(g), pd, ctypes.c_int64(P.size), ctypes.c_float(scale))
+    return dP
+
+
+def lora_expand_bwd(dP, basis, coeffs, scale=1.0):
+    """dP [Bn, K, D], basis [D, rank], coeffs [Bn, K, rank] -> (dCoeffs, dBasis)."""
+    dP, pdP = _f(dP)
+    basis, pB = _f(basis)
+    coeffs, pC = _f(coeffs)
+    Bn, K, D = dP.shape
+    rank = basis.shape[1]
+    dC, pdC = _out((Bn, K, rank))
+    dB, pdB = _out((D, rank))
+    lib().or_lora_expand_bwd(pdP, pB, pC, pdC, pdB, Bn * K, D, rank, ctypes.c_float(scale))
+    return dC, dB
+
+
+def cosine_blend_bwd(bits, weights, blended, info, K, grad_scale=10.0):
+    bits, pb = _u(bits)
+    weights, pw = _f(weights)
+    blended, pbl = _f(blended)
+    info, pi = _f(info)
+    Bn, D = blended.shape
+    dP, pd = _out((Bn, K, D))
+    lib().or_cosine_blend_bwd(pb, pw, pbl, pi, pd, Bn, K, D, bits.shape[1],
+                              ctypes.c_float(grad_scale))
+    return dP

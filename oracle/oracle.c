@@ -594,3 +594,69 @@ void or_adamw_step(float* W, float* grad, float* m, float* v, int64_t n, float l
         if (clear_grad) grad[i] = 0.0f;
     }
 }
+
+void or_binary_bwd(int op, const float* dY, const float* A, const float* B, float* dA, float* dB,
+                   int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const double g = dY[i];
+        double da = 0.0, db = 0.0;
+        if (op == 0) { da = g; db = -g; }                         /* a - b */
+        else if (op == 1) { da = g * B[i]; db = g * A[i]; }       /* a * b */
+        else if (op == 2) { da = g / B[i]; db = -g * A[i] / ((double)B[i] * B[i]); } /* a / b */
+        else { da = -g; }                                         /* -a */
+        if (dA) dA[i] = (float)da;
+        if (dB) dB[i] = (float)db;
+    }
+}
+
+void or_reduce_bwd(int op, const float* dY, float* dX, int64_t outer, int64_t inner) {
+    for (int64_t o = 0; o < outer; ++o)
+        for (int64_t i = 0; i < inner; ++i)
+            dX[o * inner + i] = (float)(op == 1 ? (double)dY[o] / (double)inner : (double)dY[o]);
+}
+
+void or_transpose_bwd(const float* dY, float* dX, int64_t batch, int rows, int cols) {
+    for (int64_t b = 0; b < batch; ++b)
+        for (int r = 0; r < rows; ++r)
+            for (int c = 0; c < cols; ++c)
+                dX[(b * rows + r) * cols + c] = dY[(b * cols + c) * rows + r];
+}
+
+void or_mse_bwd(const float* P, const float* T, float g, float* dP, int64_t n, float scale) {
+    for (int64_t i = 0; i < n; ++i) dP[i] = (float)(2.0 * scale * g * ((double)P[i] - T[i]));
+}
+
+void or_lora_expand_bwd(const float* dP, const float* basis, const float* coeffs, float* dC,
+                        float* dB, int BK, int D, int rank, float scale) {
+    for (int row = 0; row < BK; ++row)
+        for (int r = 0; r < rank; ++r) {
+            double s = 0.0;
+            for (int i = 0; i < D; ++i) s += (double)basis[(size_t)i * rank + r] * dP[(size_t)row * D + i];
+            dC[(size_t)row * rank + r] = (float)(s * scale);
+        }
+    for (int i = 0; i < D; ++i)
+        for (int r = 0; r < rank; ++r) {
+            double s = 0.0;
+            for (int row = 0; row < BK; ++row)
+                s += (double)dP[(size_t)row * D + i] * coeffs[(size_t)row * rank + r];
+            dB[(size_t)i * rank + r] = (float)(s * scale);
+        }
+}
+
+void or_cosine_blend_bwd(const uint32_t* bits, const float* weights, const float* blended,
+                         const float* info, float* dP, int Bn, int K, int D, int words,
+                         float grad_scale) {
+    for (int b = 0; b < Bn; ++b) {
+        const double dot = info[(size_t)b * 3 + 1], nsq = info[(size_t)b * 3 + 2];
+        const double nb = sqrt(fmax(nsq, 1e-8)), sd = sqrt((double)D);
+        const double cosine = dot / (nb * sd);
+        for (int i = 0; i < D; ++i) {
+            const double y = ((bits[(size_t)b * words + (i >> 5)] >> (i & 31)) & 1u) ? 1.0 : -1.0;
+            const double gb = -(y / (nb * sd) - cosine * blended[(size_t)b * D + i] / fmax(nsq, 1e-8));
+            for (int k = 0; k < K; ++k) {
+                const double g = gb * weights[(size_t)b * K + k] * grad_scale;
+                dP[((size_t)b * K + k) * D + i] = (float)fmin(fmax(g, -1.0), 1.0);
+            }
+        }
+    }
+}

@@ -86,6 +86,23 @@ void or_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32
 void or_vsa_dots(const float* preds, const uint32_t* bits, float* dots, int Bn, int K, int D,
                  int words);
 
+/* Sub / Mul / Div / Neg backward (op as GN_BIN_*; stubs at autograd.cpp:631-654) */
+void or_binary_bwd(int op, const float* dY, const float* A, const float* B, float* dA, float* dB,
+                   int64_t n);
+/* Sum / Mean backward over the trailing `inner` elements (stubs at autograd.cpp:695-707) */
+void or_reduce_bwd(int op, const float* dY, float* dX, int64_t outer, int64_t inner);
+/* Transpose backward of the last two dims: dX[b, r, c] = dY[b, c, r] (autograd.cpp:689-693) */
+void or_transpose_bwd(const float* dY, float* dX, int64_t batch, int rows, int cols);
+/* MSE backward: dP = 2 scale (P - T) g (autograd.cpp:663-667) */
+void or_mse_bwd(const float* P, const float* T, float g, float* dP, int64_t n, float scale);
+/* vsa-lora-expand-backward.glsl:38-63 with grad_scale: dC = s dP B, dB = s dP^T C */
+void or_lora_expand_bwd(const float* dP, const float* basis, const float* coeffs, float* dC,
+                        float* dB, int BK, int D, int rank, float scale);
+/* vsa-cosine-blend-backward.glsl:37-70 (dPreds overwritten) */
+void or_cosine_blend_bwd(const uint32_t* bits, const float* weights, const float* blended,
+                         const float* info, float* dP, int Bn, int K, int D, int words,
+                         float grad_scale);
+
 /* surprise-momentum.glsl:53-114, one tensor (recalled / delta may be NULL); updates W, s_bar,
  * delta and (clear_grad) grad in place */
 void or_surprise_momentum_step(float* W, float* grad, float* s_bar, float* delta,

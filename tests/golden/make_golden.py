@@ -21,6 +21,11 @@ Forward definitions used (reference file:line):
                 vsa-surrogate-loss-forward.glsl / -backward.glsl:56-88
   optimizers    torch.optim.AdamW / torch.optim.Adam, three steps  adamw-update.glsl:41-61,
                                                                  adam-update.glsl
+  tape ops      a-b, a*b, a/b, -a, sum/mean over trailing dims, transpose, mean((p-t)^2),
+                A @ B (autograd.cpp:543-711 stubs); LoRA expand preds = coeffs B^T
+                (vsa-lora-expand-forward.glsl); cosine blend loss = -cos(sum_k w_k preds_k, y)
+                (vsa-cosine-blend-forward.glsl; the backward's x10 scale and +-1 clamp are applied
+                to the autograd gradient)
 Run with a list of set names (e.g. `optim`) to write only those files.
 """
 import sys
@@ -293,6 +298,68 @@ def gen_optim(rng):
              weight_decay=np.float32(kw["weight_decay"]))
 
 
+def gen_tapeops(rng):
+    n = (5, 7)
+    a = rng.standard_normal(n).astype(np.float32)
+    b = (rng.standard_normal(n) + np.sign(rng.standard_normal(n)) * 1.5).astype(np.float32)
+    dy = rng.standard_normal(n).astype(np.float32)
+    out = dict(a=a, b=b, dy=dy)
+    for name, fn in (("sub", lambda x, y: x - y), ("mul", lambda x, y: x * y),
+                     ("div", lambda x, y: x / y), ("neg", lambda x, y: -x)):
+        x, y = t(a, True), t(b, True)
+        r = fn(x, y)
+        r.backward(t(dy))
+        out["d" + name + "_a"] = f32(x.grad)
+        out["d" + name + "_b"] = f32(y.grad) if y.grad is not None else np.zeros(n, np.float32)
+    X = rng.standard_normal((3, 4, 6)).astype(np.float32)
+    for name, fn in (("sum", lambda x: x.sum(-1)), ("mean", lambda x: x.mean(-1)),
+                     ("sumall", lambda x: x.sum().reshape(1)), ("meanall", lambda x: x.mean().reshape(1))):
+        x = t(X, True)
+        r = fn(x)
+        g = rng.standard_normal(tuple(r.shape)).astype(np.float32)
+        r.backward(t(g))
+        out[name + "_dy"], out[name + "_dx"] = g, f32(x.grad)
+    x = t(X, True)
+    r = x.transpose(-1, -2)
+    g = rng.standard_normal(tuple(r.shape)).astype(np.float32)
+    r.backward(t(g))
+    out["X"], out["tr_dy"], out["tr_dx"] = X, g, f32(x.grad)
+    p, tg = rng.standard_normal(11).astype(np.float32), rng.standard_normal(11).astype(np.float32)
+    x = t(p, True)
+    ((x - t(tg)) ** 2).mean().backward()
+    out["mse_p"], out["mse_t"], out["mse_dp"] = p, tg, f32(x.grad)
+    A, B = rng.standard_normal((6, 9)).astype(np.float32), rng.standard_normal((9, 4)).astype(np.float32)
+    G = rng.standard_normal((6, 4)).astype(np.float32)
+    x, y = t(A, True), t(B, True)
+    (x @ y).backward(t(G))
+    out.update(mm_a=A, mm_b=B, mm_dc=G, mm_da=f32(x.grad), mm_db=f32(y.grad))
+    save("tapeops", **out)
+    # LoRA expand: preds[b,k,i] = sum_r B[i,r] c[b,k,r]
+    Bn, K, D, rank = 3, 2, 40, 5
+    basis = rng.standard_normal((D, rank)).astype(np.float32)
+    coeffs = rng.standard_normal((Bn, K, rank)).astype(np.float32)
+    dP = rng.standard_normal((Bn, K, D)).astype(np.float32)
+    cb, cc = t(basis, True), t(coeffs, True)
+    torch.einsum("ir,bkr->bki", cb, cc).backward(t(dP))
+    save("lora_expand", basis=basis, coeffs=coeffs, dP=dP, dcoeffs=f32(cc.grad), dbasis=f32(cb.grad))
+    # cosine blend: blended = sum_k w_k preds_k, loss = -cos(blended, y) per row
+    Bn, K, D = 3, 4, 96
+    words = D // 32
+    bits = rng.integers(0, 2**32, size=(Bn, words), dtype=np.uint64).astype(np.uint32)
+    y = np.where((bits[:, np.arange(D) >> 5] >> (np.arange(D) & 31)) & 1, 1.0, -1.0)
+    preds = (rng.standard_normal((Bn, K, D)) * 0.05).astype(np.float32)
+    w = rng.dirichlet(np.ones(K), size=Bn).astype(np.float32)
+    pr = t(preds, True)
+    blended = (t(w)[:, :, None] * pr).sum(1)
+    cos = (blended * t(y)).sum(1) / (blended.norm(dim=1) * np.sqrt(D))
+    (-cos).sum().backward()
+    bl = f32(blended)
+    info = np.stack([1.0 - f32(cos), (bl * y).sum(1), (bl * bl).sum(1)], 1).astype(np.float32)
+    save("cosine_blend", bits=bits, preds=preds, weights=w, blended=bl, info=info,
+         dpreds=np.clip(10.0 * f32(pr.grad), -1.0, 1.0).astype(np.float32),
+         dpreds_raw=f32(pr.grad))
+
+
 def main(only=()):
     rng = np.random.default_rng(20261201)
     sets = [("linear", gen_linear), ("act", gen_act), ("glu", gen_glu),
@@ -303,6 +370,8 @@ def main(only=()):
             fn(rng)
     if not only or "optim" in only:
         gen_optim(np.random.default_rng(20261202))
+    if not only or "tapeops" in only:
+        gen_tapeops(np.random.default_rng(20261203))
     print("golden vectors written to", HERE)
 
 

@@ -603,3 +603,66 @@ def test_optimizer_rejects_bad_entries(gn):
         gn.adamw_step([dict(W=w, grad=w, state0=w)])  # AdamW needs v
     with pytest.raises(gn.GnError):
         gn.surprise_momentum_step([dict(W=w, grad=torch.zeros(9, device="cuda:0"), state0=w)])
+
+
+# ---------------------------------------------------------------------------- tape ops
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_binary_reduce_transpose_mse(gn, dt):
+    r = rng_(50)
+    n = 4099  # ragged
+    a = rnd(r.standard_normal(n).astype(np.float32))
+    b = rnd((r.standard_normal(n) + 2.0 * np.sign(r.standard_normal(n))).astype(np.float32))
+    dy = rnd(r.standard_normal(n).astype(np.float32))
+    tol = 1e-6 if dt == torch.float32 else BF16_TOL
+    for op in ["sub", "mul", "div", "neg"]:
+        dA, dB = gn.binary_bwd(op, dev(dy, dt), dev(a, dt), dev(b, dt))
+        rA, rB = oracle.binary_bwd(op, dy, a, b)
+        assert rel_err(host(dA), rA) < tol, op
+        if rB is not None:
+            assert rel_err(host(dB), rB) < tol, op
+    X = r.standard_normal((7, 33, 130)).astype(np.float32)
+    for op in ["sum", "mean"]:
+        g = rnd(r.standard_normal((7, 33)).astype(np.float32))
+        assert rel_err(host(gn.reduce_bwd(op, dev(g, dt), X.shape)), oracle.reduce_bwd(op, g, X.shape)) < tol
+        g1 = rnd(r.standard_normal(1).astype(np.float32))
+        assert rel_err(host(gn.reduce_bwd(op, dev(g1, dt), X.shape)), oracle.reduce_bwd(op, g1, X.shape)) < tol
+    for shape in [(7, 130, 33), (1, 64, 64), (3, 1, 65), (2, 200, 1)]:
+        dY = rnd(r.standard_normal(shape).astype(np.float32))
+        assert np.array_equal(host(gn.transpose_bwd(dev(dY, dt))), oracle.transpose_bwd(dY))
+    p, tg = rnd(r.standard_normal(n).astype(np.float32)), rnd(r.standard_normal(n).astype(np.float32))
+    assert rel_err(host(gn.mse_bwd(dev(p, dt), dev(tg, dt))), oracle.mse_bwd(p, tg)) < tol
+    assert rel_err(host(gn.mse_bwd(dev(p, dt), dev(tg, dt), scale=0.5,
+                                   dLoss=torch.full((1,), 3.0, device="cuda:0"))),
+                   oracle.mse_bwd(p, tg, scale=0.5, g=3.0)) < tol
+
+
+@pytest.mark.parametrize("Bn,K,D,rank", [(3, 2, 40, 5), (64, 4, 1024, 16)])
+def test_vsa_lora_expand(gn, Bn, K, D, rank):
+    r = rng_(51)
+    if Bn == 3:
+        gld = golden("lora_expand")
+        basis, coeffs, dP = gld["basis"], gld["coeffs"], gld["dP"]
+    else:
+        basis = r.standard_normal((D, rank)).astype(np.float32)
+        coeffs = r.standard_normal((Bn, K, rank)).astype(np.float32)
+        dP = r.standard_normal((Bn, K, D)).astype(np.float32)
+    dC, dB = gn.vsa_lora_expand_bwd(dev(dP), dev(basis), dev(coeffs))
+    rC, rB = oracle.lora_expand_bwd(dP, basis, coeffs)
+    assert rel_err(host(dC), rC) < 1e-4 and rel_err(host(dB), rB) < 1e-4
+
+
+def test_vsa_cosine_blend(gn):
+    g = golden("cosine_blend")
+    dP = gn.vsa_cosine_blend_bwd(gn.u32_tensor(g["bits"], "cuda:0"), dev(g["weights"]),
+                                 dev(g["blended"]), dev(g["info"]), K=4)
+    assert rel_err(host(dP), g["dpreds"]) < 1e-5
+    r = rng_(52)
+    Bn, K, D = 16, 4, 10240
+    bits = r.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    preds = (r.standard_normal((Bn, K, D)) * 0.05).astype(np.float32)
+    w = r.dirichlet(np.ones(K), size=Bn).astype(np.float32)
+    bl = (w[:, :, None] * preds).sum(1).astype(np.float32)
+    y = oracle.unpack_bits(bits, D)
+    info = np.stack([np.zeros(Bn), (bl * y).sum(1), (bl * bl).sum(1)], 1).astype(np.float32)
+    dP = gn.vsa_cosine_blend_bwd(gn.u32_tensor(bits, "cuda:0"), dev(w), dev(bl), dev(info), K=K)
+    assert rel_err(host(dP), oracle.cosine_blend_bwd(bits, w, bl, info, K)) < 1e-5

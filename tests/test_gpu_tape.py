@@ -433,3 +433,48 @@ def test_training_step_with_optimizers(env):
                     hw[i], _, st[i], _ = oracle.surprise_momentum_step(
                         hw[i], g, st[i], eta_base=1e-2, alpha=0.9, clip_max=1.0)
                 assert rel_err(ws[i].cpu().numpy(), hw[i]) < 1e-4, (opt_kind, step, i)
+
+
+def test_remaining_ops_through_tape(env):
+    """Sub, Mul, Div, Neg, Transpose, MatMul, Sum/Mean and MSELoss recorded on the tape (the
+    reference's stubs, autograd.cpp:543-711) against torch float64 autograd of the same graph:
+        d = (x - y) * z / w;  e = -d^T;  f = e @ M;  s = mean(f, -1);  L = mse(s, target)."""
+    gc, gb, dev = env
+    r = np.random.default_rng(9)
+    shp = (6, 10)
+    x, y, z = (r.standard_normal(shp).astype(np.float32) for _ in range(3))
+    w = (r.standard_normal(shp) + 2.0).astype(np.float32)
+    Mm = r.standard_normal((6, 5)).astype(np.float32)
+    tgt = r.standard_normal(10).astype(np.float32)
+    tx, ty, tz, tw, tM, tt = T(x), T(y), T(z), T(w), T(Mm), T(tgt)
+    d1 = (tx - ty).contiguous()
+    d2 = (d1 * tz).contiguous()
+    d = (d2 / tw).contiguous()
+    e0 = d.t().contiguous()
+    e = (-e0).contiguous()
+    f = (e @ tM).contiguous()
+    s = f.mean(-1).contiguous()
+    loss = torch.zeros(1, device="cuda:0")
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    op = gc.OpType
+    tape.record_op(op.Sub, [gb.tref(tx, True), gb.tref(ty, True)], [gb.tref(d1)])
+    tape.record_op(op.Mul, [gb.tref(d1, True), gb.tref(tz, True)], [gb.tref(d2)])
+    tape.record_op(op.Div, [gb.tref(d2, True), gb.tref(tw, True)], [gb.tref(d)])
+    tape.record_op(op.Transpose, [gb.tref(d, True)], [gb.tref(e0)])
+    tape.record_op(op.Neg, [gb.tref(e0, True)], [gb.tref(e)])
+    tape.record_op(op.MatMul, [gb.tref(e, True), gb.tref(tM, True)], [gb.tref(f)])
+    tape.record_op(op.Mean, [gb.tref(f, True)], [gb.tref(s)])
+    ln = tape.record_op(op.MSELoss, [gb.tref(s, True), gb.tref(tt)], [gb.tref(loss)])
+    tape.backward(ln, 0)
+    st = tape.last_backward_stats()
+    assert st["cpu_fallbacks"] == 0 and st["nodes_with_grad"] == 8
+
+    X = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (x, y, z, w, Mm)]
+    dd = (X[0] - X[1]) * X[2] / X[3]
+    ff = (-dd.t()) @ X[4]
+    lref = ((ff.mean(-1) - torch.tensor(tgt, dtype=torch.float64)) ** 2).mean()
+    lref.backward()
+    for t_, ref in zip([tx, ty, tz, tw, tM], X):
+        assert rel_err(grad(gb, dev, tape, t_), ref.grad.numpy()) < 1e-5
+    tape.end()

@@ -303,3 +303,40 @@ def test_surprise_momentum_recall_blend():
                                                alpha=1.0, lambda_recall=0.5, clip_max=10.0)
     # s = |0.3 - 0.1| = 0.2; lr = 1.2; d = 1.2 * (0.3 + 0.05) = 0.42
     assert np.allclose(s, [0.2]) and np.allclose(d, [0.42]) and np.allclose(W, [-0.42])
+
+
+# ---------------------------------------------------------------------------- tape ops
+def test_tape_ops_golden():
+    g = golden("tapeops")
+    for op in ["sub", "mul", "div", "neg"]:
+        dA, dB = oracle.binary_bwd(op, g["dy"], g["a"], g["b"])
+        assert rel_err(dA, g["d" + op + "_a"]) < TOL, op
+        if dB is not None:
+            assert rel_err(dB, g["d" + op + "_b"]) < TOL, op
+    X = g["X"]
+    for name, op in [("sum", "sum"), ("mean", "mean"), ("sumall", "sum"), ("meanall", "mean")]:
+        assert rel_err(oracle.reduce_bwd(op, g[name + "_dy"], X.shape), g[name + "_dx"]) < TOL, name
+    assert np.array_equal(oracle.transpose_bwd(g["tr_dy"]), g["tr_dx"])
+    assert rel_err(oracle.mse_bwd(g["mse_p"], g["mse_t"]), g["mse_dp"]) < TOL
+    # MatMul C = A B is Linear with W = B^T: dA = dC B^T, dB = (dC^T A)^T
+    dA, dW, _ = oracle.linear_bwd(g["mm_dc"], g["mm_a"], np.ascontiguousarray(g["mm_b"].T),
+                                  need_db=False)
+    assert rel_err(dA, g["mm_da"]) < TOL and rel_err(dW.T, g["mm_db"]) < TOL
+
+
+def test_lora_expand_golden():
+    g = golden("lora_expand")
+    dC, dB = oracle.lora_expand_bwd(g["dP"], g["basis"], g["coeffs"])
+    assert rel_err(dC, g["dcoeffs"]) < TOL and rel_err(dB, g["dbasis"]) < TOL
+
+
+def test_cosine_blend_golden_with_clamp():
+    """torch's gradient of -cos(sum_k w_k preds_k, y), times the handler's 10, clamped to +-1
+    (a quarter of the entries sit in the clamp)."""
+    g = golden("cosine_blend")
+    dP = oracle.cosine_blend_bwd(g["bits"], g["weights"], g["blended"], g["info"], K=4)
+    assert rel_err(dP, g["dpreds"]) < TOL
+    assert 0.1 < np.mean(np.abs(dP) == 1.0) < 0.5
+    # without the scale/clamp (grad_scale 1, all |g| < 1) the gradient is torch's exactly
+    assert rel_err(oracle.cosine_blend_bwd(g["bits"], g["weights"], g["blended"], g["info"], K=4,
+                                           grad_scale=1.0), g["dpreds_raw"]) < TOL
