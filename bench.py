@@ -206,13 +206,26 @@ def bench_attn(args, torch, gn):
         cpu = {"value": round(5 * 2.0 * Ss * Ss * D * 0.5 * Bs * Hs / dt / 1e12, 6), "unit": "TFLOP/s",
                "cores": oracle.num_threads(), "kind": "port",
                "sample": f"{Bs} x {Hs} heads x S={Ss}, the whole workload (oracle C/OpenMP fp64), {dt:.2f} s"}
-    return line("causal attention backward with RoPE (algorithmic TFLOP/s)", round(tf, 2),
-                "TFLOP/s", args, ms, "bf16",
-                {"workload": "C3 causal attention bwd + RoPE(1e4), B4 H16 S2048 D128",
-                 "batch": B, "heads": H, "seq_len": S, "head_dim": D},
-                {"kernel": "gn_attn_bwd (pre-pass + dK/dV + dQ kernels)", "bound": "mfma",
-                 "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                 "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None}, cpu)
+    out = line("causal attention backward with RoPE (algorithmic TFLOP/s)", round(tf, 2),
+               "TFLOP/s", args, ms, "bf16",
+               {"workload": "C3 causal attention bwd + RoPE(1e4), B4 H16 S2048 D128",
+                "batch": B, "heads": H, "seq_len": S, "head_dim": D},
+               {"kernel": "gn_attn_bwd (pre-pass + dK/dV + dQ kernels)", "bound": "mfma",
+                "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None}, cpu)
+    # the forward that produces the saved O and LSE (RoPE rotation + attn_fwd_mfma)
+    fo = (torch.empty_like(Q), torch.empty(B, H, S, device=dev))
+    def fwd():
+        gn._check(gn.lib().gn_attn_fwd(gn._ptr(Q), gn._ptr(K), gn._ptr(V), gn._ptr(fo[0]),
+                                       gn._ptr(fo[1]), B, H, S, D, D ** -0.5, 1, gn.ROPE["interleaved"],
+                                       1e4, gn.BF16, gn._ptr(ws), ws.numel(), gn._stream()),
+                  "gn_attn_fwd")
+    ms_f = timed(torch, fwd, args.steps, args.warmup)
+    ff = 2 * 2.0 * S * S * D * 0.5 * B * H  # causal: QK^T and PV over half the scores
+    out["forward"] = {"kernel": "gn_attn_fwd (RoPE rotation + attn_fwd_mfma)", "ms": round(ms_f, 4),
+                      "TFLOP/s": round(ff / (ms_f * 1e-3) / 1e12, 1),
+                      "frac": round(ff / (ms_f * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    return out
 
 
 def bench_vsa(args, torch, gn):

@@ -509,6 +509,146 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(
     store_rows<D>(st, head_base<bf16_t>(tdQ, bh, H), tdQ.sr, qw0, S, scale, rope_mode, cs);
 }
 
+// Forward producing the backward's saved tensors: O and the fp32 row logsumexp (natural
+// log, S scaled), flash-attention2-rope.glsl:165-247 semantics with the causal mask.  One
+// block per (b*h, 128 queries), four waves x 32 queries; K and V tiles of 64 keys arrive by
+// LDS DMA (two stages).  Per key tile and wave:
+//   S^T = K Q^T      (A = K rows from LDS, B = Q fragments kept in VGPRs): lane = query, so
+//                    the running max m and sum l are per-lane scalars (plus one exchange
+//                    with lane ^ 32, which holds the other 16 keys of each 32-key half);
+//   P^T = exp2(S^T scale log2e - m)  (m in the same base-2 units), O^T = alpha O^T;
+//   O^T += V^T P^T   (A = V columns by transpose reads, whose key order is the
+//                    accumulator's row order, B = P^T converted in registers).
+// The epilogue scales by 1/l, transposes each wave's 32 x D block through LDS and writes
+// bf16 rows; LSE = (m + log2 l) ln 2.
+template <int D, int STAGES>
+__global__ __launch_bounds__(256) void attn_fwd_mfma(TDesc tQ, TDesc tK, TDesc tV, TDesc tO,
+                                                     float* __restrict__ LSE, int H, int S,
+                                                     float scale, int causal) {
+    using C = DqCfg<D, STAGES>;
+    extern __shared__ __align__(1024) unsigned char smem[];
+    constexpr int NT = D / 32, KS = D / 16;
+    const int nqb = (S + 127) / 128;
+    const int bh = blockIdx.x, i0 = (nqb - 1 - (int)blockIdx.y) * 128;  // longest rows first
+    const bf16_t* Qr = head_base<const bf16_t>(tQ, bh, H);
+    const bf16_t* Kr = head_base<const bf16_t>(tK, bh, H);
+    const bf16_t* V = head_base<const bf16_t>(tV, bh, H);
+    const int lane = threadIdx.x & 63, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int qw0 = i0 + wave * 32, q = qw0 + (lane & 31), qc = min(q, S - 1);
+    const float c2 = scale * 1.4426950408889634f;
+
+    bf16x8_t qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = ld_frag16(Qr + qc * tQ.sr + 8 * h + 16 * ks);
+    f32x16_t aO[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) zero16(aO[t]);
+    float m = -INFINITY, l = 0.f;
+
+    const uint32_t lds0 = lds_addr(smem);
+    const int kend = causal ? min(S, i0 + 128) : S;
+    const int T = (kend + 63) / 64;
+    auto issue = [&](int it) {
+        const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
+        dma_tile<D>(Kr, tK.sr, it * 64, S, sb);
+        dma_tile<D>(V, tV.sr, it * 64, S, sb + C::TB);
+    };
+
+    issue(0);
+    if (STAGES > 2 && T > 1) issue(1);
+    for (int it = 0; it < T; ++it) {
+        if (STAGES > 2 && it + 1 < T) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::DMA_PER_TILE));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();
+        if (it + STAGES - 1 < T) issue(it + STAGES - 1);
+        const int k0 = it * 64;
+        const unsigned char* sb = smem + (it % STAGES) * C::STAGE;
+        const bf16_t* sK = reinterpret_cast<const bf16_t*>(sb);
+        const bf16_t* sV = reinterpret_cast<const bf16_t*>(sb + C::TB);
+        if (qw0 >= S || (causal && k0 > qw0 + 31)) continue;  // every key masked for the wave
+        const bool full = qw0 + 31 < S && k0 + 63 < S && (!causal || k0 + 63 <= qw0);
+
+        f32x16_t sc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            zero16(sc[i]);
+            bf16x8_t fa[2];
+            fa[0] = frag_rows<D>(sK, 32 * i, 0);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                if (ks + 1 < KS) fa[(ks + 1) & 1] = frag_rows<D>(sK, 32 * i, ks + 1);
+                sc[i] = mfma32(fa[ks & 1], qf[ks], sc[i]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // scores in base-2 units; masked entries are -inf (P = 0)
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float v = sc[i][r] * c2;
+                if (!full) {
+                    const int kk = k0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const bool ok = q < S && kk < S && (!causal || kk <= q);
+                    v = ok ? v : -INFINITY;
+                }
+                sc[i][r] = v;
+                mt = fmaxf(mt, v);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float ms = mn == -INFINITY ? 0.f : mn;  // a row with no visible key yet stays empty
+        const float alpha = __builtin_amdgcn_exp2f(m - ms);
+        float ps = 0.f;
+        bf16x8_t pb[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            float pv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                pv[e] = __builtin_amdgcn_exp2f(sc[p >> 1][8 * (p & 1) + e] - ms);
+                ps += pv[e];
+            }
+            pb[p] = to_bf16x8(pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]);
+        }
+        ps += __shfl_xor(ps, 32);
+        l = l * alpha + ps;
+        m = mn;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) aO[t][r] *= alpha;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            bf16x8_t fv[2];
+            fv[0] = frag_cols<D>(sV, 0, 32 * t);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                if (p + 1 < 4) fv[(p + 1) & 1] = frag_cols<D>(sV, 16 * (p + 1), 32 * t);
+                aO[t] = mfma32(fv[p & 1], pb[p], aO[t]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+
+    __syncthreads();
+    float* st = reinterpret_cast<float*>(smem) + wave * 32 * (D + 4);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    // O^T accumulators: lane = query (column), rows = d; transpose into the wave's strip
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            st[(lane & 31) * (D + 4) + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3)] = aO[t][r] * inv;
+    __syncthreads();
+    store_rows<D>(st, head_base<bf16_t>(tO, bh, H), tO.sr, qw0, S, 1.0f, GN_ROPE_NONE, nullptr);
+    if (h == 0 && q < S)
+        LSE[(size_t)bh * S + q] = (m + __log2f(l)) * 0.6931471805599453f;
+}
+
 // cos/sin table [S][D/2] of the RoPE angles (pair i at position p)
 __global__ __launch_bounds__(256) void rope_table(float2* __restrict__ cs, int S, int D,
                                                   float theta) {
@@ -985,6 +1125,30 @@ extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O,
         }
         Qp = w.Qr;
         Kp = w.Kr;
+    }
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    const bool mfma = dtype == GN_BF16 && (D == 64 || D == 128) && al16(Qp) && al16(Kp) && al16(V) &&
+                      al16(O);
+    if (mfma) {
+        const int BH = B * H;
+        const TDesc tQ = bhsd(Qp, H, S, D), tK = bhsd(Kp, H, S, D), tV = bhsd(V, H, S, D),
+                    tO = bhsd(O, H, S, D);
+        const dim3 grid(BH, (S + 127) / 128);
+        if (D == 64) {
+            using C = DqCfg<64, kStagesDq>;
+            static const bool ok = allow_lds(attn_fwd_mfma<64, kStagesDq>, C::LDS);
+            GN_REQUIRE(ok, "gn_attn_fwd: cannot reserve %d B of LDS", C::LDS);
+            hipLaunchKernelGGL((attn_fwd_mfma<64, kStagesDq>), grid, dim3(256), C::LDS, s, tQ, tK, tV, tO,
+                               LSE, H, S, scale, causal);
+        } else {
+            using C = DqCfg<128, kStagesDq>;
+            static const bool ok = allow_lds(attn_fwd_mfma<128, kStagesDq>, C::LDS);
+            GN_REQUIRE(ok, "gn_attn_fwd: cannot reserve %d B of LDS", C::LDS);
+            hipLaunchKernelGGL((attn_fwd_mfma<128, kStagesDq>), grid, dim3(256), C::LDS, s, tQ, tK, tV, tO,
+                               LSE, H, S, scale, causal);
+        }
+        GN_LAUNCH_CHECK("gn_attn_fwd (mfma)");
+        return GN_OK;
     }
     const unsigned gr = (unsigned)((rows + 3) / 4);
     if (dtype == GN_BF16)

@@ -400,12 +400,36 @@ def test_embedding_scatter_add(gn, dt):
     assert rel_err(host(dE2), want + base) < FP32_TOL
 
 
-def test_attention_fwd_bf16_matches_oracle(gn):
+@pytest.mark.parametrize("B,H,S,D,causal,rope", [(1, 2, 96, 64, True, "interleaved"),
+                                                 (2, 3, 200, 128, True, "none"),
+                                                 (1, 2, 130, 128, False, "half"),
+                                                 (1, 1, 64, 64, False, "none"),
+                                                 (1, 2, 257, 64, True, "none")])
+def test_attention_fwd_bf16_matches_oracle(gn, B, H, S, D, causal, rope):
+    """MFMA forward (D 64/128; ragged S, both masks, all RoPE modes) against the oracle: O to
+    the bf16 tolerance, the natural-log row LSE to 1e-3, and the LSE consistent with O's
+    own normalisation (the backward recomputes P from it)."""
     r = rng_(11)
-    Q, K, V = (rnd(r.standard_normal((1, 2, 96, 64)).astype(np.float32)) for _ in range(3))
-    O, LSE = gn.attn_fwd(dev(Q, torch.bfloat16), dev(K, torch.bfloat16), dev(V, torch.bfloat16))
-    rO, rL = oracle.attn_fwd(Q, K, V)
+    Q, K, V = (rnd(r.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    O, LSE = gn.attn_fwd(dev(Q, torch.bfloat16), dev(K, torch.bfloat16), dev(V, torch.bfloat16),
+                         causal=causal, rope=rope)
+    rO, rL = oracle.attn_fwd(Q, K, V, causal=causal, rope_mode=rope)
     assert rel_err(host(O), rO) < BF16_TOL and rel_err(host(LSE), rL) < 1e-3
+
+
+def test_attention_fwd_then_bwd_round_trip(gn):
+    """The backward run on the MFMA forward's own O and LSE matches the oracle backward."""
+    r = rng_(12)
+    B, H, S, D = 1, 2, 192, 128
+    Q, K, V = (rnd(r.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    dO = rnd((r.standard_normal((B, H, S, D)) * 0.01).astype(np.float32))
+    bf = torch.bfloat16
+    O, LSE = gn.attn_fwd(dev(Q, bf), dev(K, bf), dev(V, bf))
+    dQ, dK, dV = gn.attn_bwd(dev(Q, bf), dev(K, bf), dev(V, bf), O, dev(dO, bf), LSE)
+    _, rL = oracle.attn_fwd(Q, K, V)
+    rQ, rK, rV = oracle.attn_bwd(Q, K, V, dO, rL)
+    assert rel_err(host(dQ), rQ) < BF16_TOL and rel_err(host(dK), rK) < BF16_TOL
+    assert rel_err(host(dV), rV) < BF16_TOL
 
 
 # ---------------------------------------------------------------------------- VSA
