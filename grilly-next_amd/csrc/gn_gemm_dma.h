@@ -36,6 +36,11 @@ struct GemmDesc {
     // partial tiles are added into C with fp32 atomics after C is cleared; with two splits
     // the result is exactly a + b whichever lands first, so it stays deterministic
     int ksplit;
+    // row sums of op(A) (the bias gradient of a weight-gradient GEMM, db = sum_rows dY when
+    // A = dY^T): rows < Msplit -> bias[m], rows >= Msplit -> bias2[m - Msplit], fp32, added
+    // to the existing values when accumulate; nullptr: none (plain fp32 epilogue only)
+    float* bias;
+    float* bias2;
 };
 
 // Store one accumulated element (m, n) according to the descriptor's epilogue.

@@ -301,6 +301,7 @@ __global__ __launch_bounds__(256) void clear_c(GemmDesc g) {
         const int m = (int)(i / g.N), n = (int)(i % g.N);
         float* C = reinterpret_cast<float*>(m < g.Msplit ? g.C : g.C2);
         C[(size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n] = 0.f;
+        if (g.bias && n == 0) (m < g.Msplit ? g.bias[m] : g.bias2[m - g.Msplit]) = 0.f;
     }
 }
 
@@ -326,7 +327,7 @@ __host__ __device__ constexpr int reads_before(int q) {
                  : (NR * q + NM - 1) / NM;
 }
 
-template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES>
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES, bool BIAS = false>
 __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
     static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
     constexpr int NW = 4;
@@ -388,6 +389,14 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
                                                    base + A_ELEMS * 2);
     };
     bf16x8_t fa[4][FM], fb[4][FN];
+    // BIAS: per-lane partial row sums of op(A): fragment i holds row (lane % 32) of rows
+    // wm WM + 32 i, eight k values per lane, summed with v_dot2 against ones into four
+    // independent accumulators per fragment (one per value pair), so no dot2 waits on another
+    float bsum[BIAS ? FM : 1][4];
+#pragma unroll
+    for (int i = 0; i < (BIAS ? FM : 1); ++i)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) bsum[i][d] = 0.f;
     // read r of a fragment set: A fragments first, then B (whole fragments per call: a
     // transpose-read fragment is two instructions, issued together)
     auto read_one = [&](auto SET_, auto R_, const bf16_t* sa, int ks) {
@@ -412,6 +421,21 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
             constexpr int q = decltype(Q_)::value;
             acc[q / FN][q % FN] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 fa[cur][q / FN], fb[cur][q % FN], acc[q / FN][q % FN], 0, 0, 0);
+            if constexpr (BIAS) {
+                // the 4 dot2 of fragment q / FN spread over its FN MFMAs.  v_dot2c_f32_bf16
+                // costs MFMA-pipe time here: the bias variant measured ~25 % slower on the
+                // decoder's weight gradients, still a net win over two extra launches
+                constexpr int i = q / FN, d0 = (q % FN) * 4 / FN, d1 = (q % FN + 1) * 4 / FN;
+                typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+                const bf16x2_v one = {(__bf16)1.0f, (__bf16)1.0f};
+                static_for<4>([&](auto D_) {
+                    constexpr int d = decltype(D_)::value;
+                    if constexpr (d >= d0 && d < d1)
+                        bsum[i][d] = __builtin_amdgcn_fdot2_f32_bf16(
+                            __builtin_shufflevector(fa[cur][i], fa[cur][i], 2 * d, 2 * d + 1), one,
+                            bsum[i][d], false);
+                });
+            }
             constexpr int r0 = reads_before<NM, NR, front>(q), r1 = reads_before<NM, NR, front>(q + 1);
             static_for<NR>([&](auto R_) {
                 constexpr int r = decltype(R_)::value;
@@ -488,6 +512,21 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & 0xF0FFu);
     __syncthreads();
 
+    if constexpr (BIAS) {
+        // lanes l and l ^ 32 hold the two k-halves of one row; the blocks of the first column
+        // tile write (or, split over K, add onto the cleared vector: two terms, deterministic)
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const float p = (bsum[i][0] + bsum[i][1]) + (bsum[i][2] + bsum[i][3]);
+            const float v = p + __shfl_xor(p, 32);
+            const int m = m0 + wm * WM + i * 32 + lane;
+            if (n0 == 0 && wn == 0 && lane < 32 && m < g.M) {
+                float* dst = m < g.Msplit ? g.bias + m : g.bias2 + (m - g.Msplit);
+                if (g.ksplit > 1) unsafeAtomicAdd(dst, v);
+                else *dst = g.accumulate ? *dst + v : v;
+            }
+        }
+    }
     float* st = reinterpret_cast<float*>(smem_raw) + wave * 32 * (WN + 4);
     if constexpr (EPI == 1) {
         const int mb = m0 + wm * WM, nb = n0 + wn * WN;
@@ -754,20 +793,31 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
     // three LDS stages pay off on long k loops; short ones keep the shorter prologue
     const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
     const bool three = fits3 && KT / g.ksplit >= 48;
+    // the bias-summing variant exists for weight gradients only (fp32 C, plain epilogue)
+    constexpr bool CAN_BIAS = EPI == 0 && sizeof(CT) == 4;
+    const bool bias = CAN_BIAS && g.bias;
     static const bool ok2 = allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2>, smem2);
     static const bool ok3 = fits3 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>, smem3) : false;
-    if (!(three ? ok3 : ok2)) {
+    static const bool okb2 = CAN_BIAS ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS>, smem2) : false;
+    static const bool okb3 = CAN_BIAS && fits3
+                                 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, CAN_BIAS>, smem3)
+                                 : false;
+    if (!(three ? (bias ? okb3 : ok3) : (bias ? okb2 : ok2))) {
         set_error("gemm: cannot reserve %zu B of LDS", three ? smem3 : smem2);
         return GN_E_HIP;
     }
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     if (g.ksplit > 1)
         clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
-    if (three)
-        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>), dim3(tiles, g.ksplit), dim3(256),
-                           smem3, s, g);
+    const dim3 grid(tiles, g.ksplit);
+    if (bias && three)
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, CAN_BIAS>), grid, dim3(256), smem3, s, g);
+    else if (bias)
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS>), grid, dim3(256), smem2, s, g);
+    else if (three)
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>), grid, dim3(256), smem3, s, g);
     else
-        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2>), dim3(tiles, g.ksplit), dim3(256), smem2, s, g);
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2>), grid, dim3(256), smem2, s, g);
     GN_LAUNCH_CHECK("gemm (dma)");
     return GN_OK;
 }
