@@ -661,6 +661,68 @@ __global__ __launch_bounds__(256) void rope_table(float2* __restrict__ cs, int S
     }
 }
 
+// Rotate chunk c (8 elements) of one row of Q and of K (qk4[0], qk4[1], bf16) at sequence
+// position pos with the cos/sin table, into Qout / Kout.  Lanes c of one row are D/8
+// consecutive lanes (the half mode pairs chunk c with chunk c ^ D/16 across lanes).
+template <int D>
+__device__ __forceinline__ void rotate_qk_chunk(const uint4 (&qk4)[2], int c, int pos,
+                                                const float2* __restrict__ cs, int mode,
+                                                bf16_t* __restrict__ Qout, bf16_t* __restrict__ Kout) {
+    constexpr int LPR = D / 8;
+    const float2* t = cs + (size_t)pos * (D / 2);
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        const uint4 v4 = qk4[which];
+        const uint32_t vw[4] = {v4.x, v4.y, v4.z, v4.w};
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = __uint_as_float(vw[e] << 16);
+            x[2 * e + 1] = __uint_as_float(vw[e] & 0xffff0000u);
+        }
+        if (mode == GN_ROPE_INTERLEAVED) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float2 r = t[4 * c + e];
+                const float x0 = x[2 * e], x1 = x[2 * e + 1];
+                x[2 * e] = x0 * r.x - x1 * r.y;
+                x[2 * e + 1] = x0 * r.y + x1 * r.x;
+            }
+        } else {  // GN_ROPE_HALF: element e pairs with the same element of chunk c ^ LPR/2
+            const bool lo = c < LPR / 2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float xp = __shfl_xor(x[e], LPR / 2);
+                const float2 r = t[8 * (c % (LPR / 2)) + e];
+                x[e] = lo ? x[e] * r.x - xp * r.y : xp * r.y + x[e] * r.x;
+            }
+        }
+        *reinterpret_cast<bf16x8_t*>(which ? Kout : Qout) =
+            to_bf16x8(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
+    }
+}
+
+// Forward pre-pass (RoPE on): rotated bf16 copies of Q and K from the cos/sin table, D/8
+// lanes per row, both tensors in one launch.
+template <int D>
+__global__ __launch_bounds__(256) void rope_qk_prep(TDesc tQ, TDesc tK, bf16_t* __restrict__ Qr,
+                                                    bf16_t* __restrict__ Kr,
+                                                    const float2* __restrict__ cs, int64_t rows,
+                                                    int H, int S, int mode) {
+    constexpr int LPR = D / 8;
+    const unsigned gid = blockIdx.x * 256u + threadIdx.x;  // rows * LPR < 2^31 (host check)
+    const unsigned row = gid / LPR;
+    const int c = (int)(gid % LPR);
+    if (row >= (unsigned)rows) return;  // LPR divides 256: whole row groups leave together
+    const int pos = (int)(row % (unsigned)S);
+    const unsigned bh = row / (unsigned)S;
+    const uint4 qk4[2] = {
+        *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tQ, (int)bh, H) + pos * tQ.sr + 8 * c),
+        *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tK, (int)bh, H) + pos * tK.sr + 8 * c)};
+    const size_t off = (size_t)row * D + 8 * c;
+    rotate_qk_chunk<D>(qk4, c, pos, cs, mode, Qr + off, Kr + off);
+}
+
 // Pre-pass of the MFMA path, D/8 lanes per row: rotated Q and K (bf16), D_i = rowsum(dO*O)
 // and L log2(e), both into [B*H][Spad] arrays whose padding the kernels never unmask.
 template <int D>
@@ -701,37 +763,7 @@ __global__ __launch_bounds__(256) void attn_prep(
             for (int p = S; p < Spad; ++p) Di[(size_t)bh * Spad + p] = Lsc[(size_t)bh * Spad + p] = 0.f;
     }
     if (mode == GN_ROPE_NONE) return;
-    const float2* t = cs + (size_t)pos * (D / 2);
-#pragma unroll
-    for (int which = 0; which < 2; ++which) {
-        const uint4 v4 = qk4[which];
-        const uint32_t vw[4] = {v4.x, v4.y, v4.z, v4.w};
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            x[2 * e] = __uint_as_float(vw[e] << 16);
-            x[2 * e + 1] = __uint_as_float(vw[e] & 0xffff0000u);
-        }
-        if (mode == GN_ROPE_INTERLEAVED) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float2 r = t[4 * c + e];
-                const float x0 = x[2 * e], x1 = x[2 * e + 1];
-                x[2 * e] = x0 * r.x - x1 * r.y;
-                x[2 * e + 1] = x0 * r.y + x1 * r.x;
-            }
-        } else {  // GN_ROPE_HALF: element e pairs with the same element of chunk c ^ LPR/2
-            const bool lo = c < LPR / 2;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float xp = __shfl_xor(x[e], LPR / 2);
-                const float2 r = t[8 * (c % (LPR / 2)) + e];
-                x[e] = lo ? x[e] * r.x - xp * r.y : xp * r.y + x[e] * r.x;
-            }
-        }
-        *reinterpret_cast<bf16x8_t*>((which ? Kr : Qr) + off) =
-            to_bf16x8(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
-    }
+    rotate_qk_chunk<D>(qk4, c, pos, cs, mode, Qr + off, Kr + off);
 }
 
 // ---- SIMT path: one wave per query row (dQ, forward) or key row (dK, dV) ----------------
@@ -1104,17 +1136,36 @@ extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O,
     if (rows == 0) return GN_OK;
     GN_REQUIRE(O && LSE, "gn_attn_fwd: null pointer");
     hipStream_t s = as_stream(stream);
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    const bool mfma = dtype == GN_BF16 && (D == 64 || D == 128) && al16(Q) && al16(K) && al16(V) &&
+                      al16(O) &&
+                      (rope_mode == GN_ROPE_NONE || (al16(ws) && rows * (D / 8) < ((int64_t)1 << 31)));
     const size_t esz = dtype == GN_BF16 ? 2 : 4;
     AttnWs w;
-    ws_layout((int64_t)B * H, S, D, esz, false, ws, &w);
-    const size_t need = 2 * align_up((size_t)rows * D * esz);  // the forward uses Qr, Kr only
+    // MFMA path: rotated bf16 Q, K and the cos/sin table (the backward's layout); SIMT path:
+    // rotated Q, K only
+    const size_t need = mfma ? ws_layout((int64_t)B * H, S, D, 2, true, ws, &w)
+                             : (ws_layout((int64_t)B * H, S, D, esz, false, ws, &w),
+                                2 * align_up((size_t)rows * D * esz));
     if (rope_mode != GN_ROPE_NONE && (!ws || ws_bytes < need)) {
         set_error("gn_attn_fwd: workspace %zu B < %zu B", ws_bytes, need);
         return GN_E_WORKSPACE;
     }
     const void* Qp = Q;
     const void* Kp = K;
-    if (rope_mode != GN_ROPE_NONE) {
+    if (rope_mode != GN_ROPE_NONE && mfma) {
+        // one table pass (S * D/2 angles) and one rotation pass over Q and K together
+        rope_table<<<grid_for((int64_t)S * (D / 2), 256, 4096), 256, 0, s>>>(w.cs, S, D, rope_theta);
+        const unsigned g = (unsigned)((rows * (D / 8) + 255) / 256);
+        if (D == 64)
+            rope_qk_prep<64><<<g, 256, 0, s>>>(bhsd(Q, H, S, D), bhsd(K, H, S, D), (bf16_t*)w.Qr,
+                                               (bf16_t*)w.Kr, w.cs, rows, H, S, rope_mode);
+        else
+            rope_qk_prep<128><<<g, 256, 0, s>>>(bhsd(Q, H, S, D), bhsd(K, H, S, D), (bf16_t*)w.Qr,
+                                                (bf16_t*)w.Kr, w.cs, rows, H, S, rope_mode);
+        Qp = w.Qr;
+        Kp = w.Kr;
+    } else if (rope_mode != GN_ROPE_NONE) {
         const unsigned g = grid_for(rows * (D / 2), 256, 16384);
         if (dtype == GN_BF16) {
             rope_rotate<bf16_t><<<g, 256, 0, s>>>((const bf16_t*)Q, (bf16_t*)w.Qr, rows, S, D, rope_mode, rope_theta, 0);
@@ -1126,9 +1177,6 @@ extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O,
         Qp = w.Qr;
         Kp = w.Kr;
     }
-    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    const bool mfma = dtype == GN_BF16 && (D == 64 || D == 128) && al16(Qp) && al16(Kp) && al16(V) &&
-                      al16(O);
     if (mfma) {
         const int BH = B * H;
         const TDesc tQ = bhsd(Qp, H, S, D), tK = bhsd(Kp, H, S, D), tV = bhsd(V, H, S, D),
