@@ -340,6 +340,9 @@ def bench_decoder(args, torch, gn):
     ms = timed(torch, lambda: m.backward_step(tape), args.steps, args.warmup)
     tf = m.flops() / (ms * 1e-3) / 1e12
     opt = decoder_optimizer_step(torch, gn, m)
+    # the forward that produces the saved tensors (norm/linear/GLU/attention forward kernels)
+    fwd_ms = timed(torch, m.forward, 5, 1)
+    fwd_tf = m.fwd_flops() / (fwd_ms * 1e-3) / 1e12
     cpu = None
     if not args.no_cpu:
         cpu = decoder_cpu_baseline(m)
@@ -354,6 +357,10 @@ def bench_decoder(args, torch, gn):
                  "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
                  "flops_per_step": m.flops()}, cpu)
     out["optimizer_step"] = opt
+    out["forward"] = {"kernel": "Decoder.forward (gn_layernorm_fwd, gn_linear_fwd, "
+                                "gn_glu_linear_fwd, gn_attn_fwd; torch gather and adds)",
+                      "ms": round(fwd_ms, 4), "TFLOP/s": round(fwd_tf, 1),
+                      "frac": round(fwd_tf / BF16_PEAK_TFLOPS, 4), "flops": m.fwd_flops()}
     return out
 
 

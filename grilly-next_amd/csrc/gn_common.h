@@ -108,6 +108,34 @@ __device__ __forceinline__ float block_max(float v, float* sh) {
     return t;
 }
 
+// Eight consecutive elements as float through one or two 16-byte accesses (16-byte aligned).
+template <typename T> struct chunk8;
+template <> struct chunk8<float> {
+    static __device__ __forceinline__ void ld(const float* p, float (&v)[8]) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    static __device__ __forceinline__ void st(float* p, const float (&v)[8]) {
+        reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+};
+template <> struct chunk8<bf16_t> {
+    static __device__ __forceinline__ void ld(const bf16_t* p, float (&v)[8]) {
+        const uint4 x = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+    static __device__ __forceinline__ void st(bf16_t* p, const float (&v)[8]) {
+        *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]),
+                                                  pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7]));
+    }
+};
+
 inline unsigned grid_for(int64_t n, int per_block, unsigned cap = 65535u * 16u) {
     int64_t g = (n + per_block - 1) / per_block;
     if (g < 1) g = 1;

@@ -378,6 +378,10 @@ int gemm_run(const GemmDesc& d, int transA, int transB, int dtype, int c_dtype, 
         set_error("gemm: fused row sums need the LDS-DMA core (bf16 operands, fp32 C)");
         return GN_E_INVALID;
     }
+    if (d.cbias && !(dtype == GN_BF16 && d.epi == 0 && gemm_dma_applicable(d))) {
+        set_error("gemm: the fused column bias needs the LDS-DMA core (bf16 operands)");
+        return GN_E_INVALID;
+    }
     if (dtype == GN_BF16) {
         if (gemm_dma_applicable(d)) return gemm_dma_launch(d, transA, transB, c_dtype, s);
         if (mfma_applicable(d)) {

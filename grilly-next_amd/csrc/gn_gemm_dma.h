@@ -41,6 +41,9 @@ struct GemmDesc {
     // to the existing values when accumulate; nullptr: none (plain fp32 epilogue only)
     float* bias;
     float* bias2;
+    // column bias of the plain epilogue (a forward Linear's b): C[m][n] = acc + cbias[n],
+    // bf16, LDS-DMA core only, no split-K; nullptr: none
+    const bf16_t* cbias;
 };
 
 // Store one accumulated element (m, n) according to the descriptor's epilogue.

@@ -144,6 +144,15 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& g, const float* st
             float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             if (m >= g.M || n >= g.N) continue;
             if constexpr (EPI == 0) {
+                if (g.cbias) {
+                    const uint4 bw = *reinterpret_cast<const uint4*>(g.cbias + n);
+                    const uint32_t w[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] += __uint_as_float(w[e] << 16);
+                        v[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+                    }
+                }
                 CT* C = reinterpret_cast<CT*>(m < g.Msplit ? g.C : g.C2);
                 const size_t idx = (size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n;
                 if constexpr (sizeof(CT) == 4) {
@@ -857,7 +866,7 @@ inline double tile_cost(const GemmDesc& g, bool ta, size_t c_bytes, int epi, int
 
 inline TileChoice choose_tile(const GemmDesc& g, bool ta, size_t c_bytes, int epi) {
     const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
-    const bool can_split = epi == 0 && c_bytes == 4 && !g.accumulate && KT >= 32;
+    const bool can_split = epi == 0 && c_bytes == 4 && !g.accumulate && !g.cbias && KT >= 32;
     TileChoice best{1, 1};
     double bt = tile_cost(g, ta, c_bytes, epi, 1, 1);
     for (int i = 0; i < 4; ++i) {
@@ -923,7 +932,7 @@ int vsa_dma_launch(const VsaDesc& v, hipStream_t s) {
 bool gemm_dma_applicable(const GemmDesc& g) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     if (g.M % 8 || g.N % 8 || g.M < 8 || g.N < 8) return false;
-    if (g.epi == 0 && (!al(g.C) || !al(g.C2) || g.ldc % 8)) return false;
+    if (g.epi == 0 && (!al(g.C) || !al(g.C2) || g.ldc % 8 || (g.cbias && !al(g.cbias)))) return false;
     if (g.epi == 1 && (!al(g.gate) || !al(g.up) || !al(g.gu) || g.ldg % 8 || g.ldgu % 8 || g.H % 8))
         return false;
     for (int s = 0; s < g.nseg; ++s) {

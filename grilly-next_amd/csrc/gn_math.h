@@ -63,5 +63,14 @@ __device__ __forceinline__ void glu_grad(float d, float g, float u, float& dg, f
     }
 }
 
+// ---- GLU forward value (fused-swiglu.glsl:78, fused-geglu.glsl:81, fused-reglu.glsl:73) ------
+template <int KIND>
+__device__ __forceinline__ float glu_val(float g, float u) {
+    if constexpr (KIND == GN_GLU_SWIGLU_UP) return g * silu_f(u);
+    else if constexpr (KIND == GN_GLU_SWIGLU_GATE) return silu_f(g) * u;
+    else if constexpr (KIND == GN_GLU_GEGLU_UP) return g * gelu_tanh_f(u);
+    else if constexpr (KIND == GN_GLU_GEGLU_GATE) return gelu_tanh_f(g) * u;
+    else return g * (u > 0.0f ? u : 0.0f);  // REGLU_UP
+}
 
 }  // namespace gn

@@ -6,33 +6,19 @@ gate = n2 Wg^T + bg, up = n2 Wu^T + bu;  x3 = x2 + h Wd^T + bd.
 Embedding x0 = E[ids], final LN, tied LM head logits = LN(x_L) E^T, cross-entropy over the
 vocabulary (scale 1/T).  bf16 storage, fp32 statistics and weight gradients.
 
-`Decoder.forward()` runs the forward on the GPU (untimed: torch for the projections and
-the norms, gn_attn_fwd for attention so O and the fp32 row logsumexp match the backward's
-saved-tensor contract) and keeps every tensor the backward needs.  `Decoder.record(tape)`
+`Decoder.forward()` runs the forward on the GPU through this library's forward kernels
+(untimed: gn_layernorm_fwd saving mean/rstd, gn_linear_fwd, gn_glu_linear_fwd saving the
+gate/up caches, gn_attn_fwd saving the fp32 row logsumexp; torch only for the embedding
+gather and the residual adds) and keeps every tensor the backward needs.  `Decoder.record(tape)`
 records the nodes the reference's tape would hold for this model (Linear, LayerNorm,
 FlashAttention2, Add, CrossEntropy; autograd.h:81-141) plus this build's FusedGLU and
 Embedding nodes, with the saved-slot conventions of each handler.
 """
-import math
-
 import torch
-import torch.nn.functional as F
 
 import grilly_bridge as gb
 import grilly_core
 import gn_bwd as gn
-
-
-def _layernorm(x, g, b, eps=1e-5):
-    xf = x.float()
-    mean = xf.mean(-1)
-    rstd = torch.rsqrt(xf.var(-1, unbiased=False) + eps)
-    n = ((xf - mean[:, None]) * rstd[:, None] * g.float() + b.float()).to(x.dtype)
-    return n.contiguous(), mean.contiguous(), rstd.contiguous()
-
-
-def _gelu_tanh(u):
-    return 0.5 * u * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (u + 0.044715 * u ** 3)))
 
 
 class Decoder:
@@ -74,23 +60,22 @@ class Decoder:
         acts = []
         for p in self.layers:
             a = {"x": x}
-            a["n1"], a["m1"], a["r1"] = _layernorm(x, p["ln1_g"], p["ln1_b"])
-            a["qkv"] = F.linear(a["n1"], p["Wqkv"], p["bqkv"]).contiguous()
+            a["n1"], a["m1"], a["r1"] = gn.layernorm_fwd(x, p["ln1_g"], p["ln1_b"])
+            a["qkv"] = gn.linear_fwd(a["n1"], p["Wqkv"], p["bqkv"])
             q, k, v = (t.contiguous() for t in a["qkv"].view(B, S, 3, H, D).permute(2, 0, 3, 1, 4))
             O, a["lse"] = gn.attn_fwd(q, k, v, causal=True, rope="none", ws=ws)
             a["o"] = O.permute(0, 2, 1, 3).reshape(T, d).contiguous()
-            a["ao"] = F.linear(a["o"], p["Wo"], p["bo"]).contiguous()
+            a["ao"] = gn.linear_fwd(a["o"], p["Wo"], p["bo"])
             a["x2"] = (x + a["ao"]).contiguous()
-            a["n2"], a["m2"], a["r2"] = _layernorm(a["x2"], p["ln2_g"], p["ln2_b"])
-            a["gate"] = F.linear(a["n2"], p["Wg"], p["bg"]).contiguous()
-            a["up"] = F.linear(a["n2"], p["Wu"], p["bu"]).contiguous()
-            a["h"] = (a["gate"].float() * _gelu_tanh(a["up"].float())).to(x.dtype).contiguous()
-            a["f"] = F.linear(a["h"], p["Wd"], p["bd"]).contiguous()
+            a["n2"], a["m2"], a["r2"] = gn.layernorm_fwd(a["x2"], p["ln2_g"], p["ln2_b"])
+            a["gate"], a["up"], a["h"] = gn.glu_linear_fwd("geglu_up", a["n2"], p["Wg"], p["Wu"],
+                                                           p["bg"], p["bu"])
+            a["f"] = gn.linear_fwd(a["h"], p["Wd"], p["bd"])
             a["x3"] = (a["x2"] + a["f"]).contiguous()
             acts.append(a)
             x = a["x3"]
-        self.nf, self.mf, self.rf = _layernorm(x, self.lnf_g, self.lnf_b)
-        self.logits = F.linear(self.nf, self.E).contiguous()
+        self.nf, self.mf, self.rf = gn.layernorm_fwd(x, self.lnf_g, self.lnf_b)
+        self.logits = gn.linear_fwd(self.nf, self.E)
         self.acts = acts
         torch.cuda.synchronize()
 
@@ -146,3 +131,11 @@ class Decoder:
         per_layer = (2 * 2 * T * d * 3 * d + 2 * 2 * T * d * d + 2 * 2 * T * d * ff * 2
                      + 2 * 2 * T * ff * d + 5 * 2.0 * S * S * (d // H) * 0.5 * self.B * H)
         return self.L * per_layer + 2 * 2 * T * d * V
+
+    def fwd_flops(self):
+        """Forward GEMM + attention FLOPs: every projection once, causal attention as 2
+        products over half the score matrix, the LM head."""
+        T, d, ff, V, S, H = self.T, self.d, self.ff, self.V, self.S, self.H
+        per_layer = (2 * T * d * 3 * d + 2 * T * d * d + 2 * T * d * ff * 2 + 2 * T * ff * d
+                     + 2 * 2.0 * S * S * (d // H) * 0.5 * self.B * H)
+        return self.L * per_layer + 2 * T * d * V

@@ -30,7 +30,8 @@ SYMBOLS = [
     "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd", "gn_binary_bwd",
     "gn_reduce_bwd", "gn_transpose_bwd", "gn_mse_bwd", "gn_vsa_lora_expand_bwd",
-    "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_add_inplace",
+    "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_layernorm_fwd",
+    "gn_rmsnorm_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace",
 ]
 BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
 RED = {"sum": 0, "mean": 1}
@@ -93,6 +94,11 @@ _SIGS = {
     "gn_vsa_cosine_blend_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _U, _P], _I),
     "gn_surprise_momentum_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     "gn_adamw_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _F, _I, _P], _I),
+    "gn_layernorm_fwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P], _I),
+    "gn_rmsnorm_fwd": ([_P, _P, _P, _P, _I, _I, _F, _I, _P], _I),
+    "gn_glu_fwd": ([_I, _P, _P, _P, _L, _I, _P], _I),
+    "gn_linear_fwd": ([_P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "gn_glu_linear_fwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
     "gn_add_inplace": ([_P, _P, _L, _I, _P], _I),
 }
 
@@ -521,6 +527,59 @@ def adamw_step(entries, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=
     _check(lib().gn_adamw_step(arr, len(entries), lr, beta1, beta2, eps, weight_decay,
                                beta1 ** step, beta2 ** step, int(clear_grad), _stream()),
            "gn_adamw_step")
+
+
+# ---- forward kernels (the saved tensors the backward consumes) ------------------------------
+def layernorm_fwd(X, gamma=None, beta=None, eps=1e-5, save_var=False):
+    """Y, mean, rstd (fp32 [rows]; the variance instead of rstd when save_var)."""
+    rows, F = X.shape
+    Y = torch.empty_like(X)
+    mean = torch.empty((rows,), dtype=torch.float32, device=X.device)
+    rstd = torch.empty((rows,), dtype=torch.float32, device=X.device)
+    _check(lib().gn_layernorm_fwd(_ptr(X), _ptr(gamma), _ptr(beta), _ptr(Y), _ptr(mean),
+                                  _ptr(rstd), rows, F, eps, _dt(X),
+                                  LN_STAT_VAR if save_var else 0, _stream()), "gn_layernorm_fwd")
+    return Y, mean, rstd
+
+
+def rmsnorm_fwd(X, w=None, eps=1e-6):
+    """Y, rstd (fp32 [rows])."""
+    rows, F = X.shape
+    Y = torch.empty_like(X)
+    rstd = torch.empty((rows,), dtype=torch.float32, device=X.device)
+    _check(lib().gn_rmsnorm_fwd(_ptr(X), _ptr(w), _ptr(Y), _ptr(rstd), rows, F, eps, _dt(X),
+                                _stream()), "gn_rmsnorm_fwd")
+    return Y, rstd
+
+
+def glu_fwd(kind, gate, up, out=None):
+    out = torch.empty_like(gate) if out is None else out
+    _check(lib().gn_glu_fwd(GLU[kind], _ptr(gate), _ptr(up), _ptr(out), gate.numel(), _dt(gate),
+                            _stream()), "gn_glu_fwd")
+    return out
+
+
+def linear_fwd(X, W, b=None, out=None):
+    """Y = X W^T + b in X's dtype."""
+    M, K = X.shape
+    N = W.shape[0]
+    Y = torch.empty((M, N), dtype=X.dtype, device=X.device) if out is None else out
+    _check(lib().gn_linear_fwd(_ptr(X), _ptr(W), _ptr(b), _ptr(Y), M, N, K, _dt(X), _stream()),
+           "gn_linear_fwd")
+    return Y
+
+
+def glu_linear_fwd(kind, X, Wg, Wu, bg=None, bu=None):
+    """gate, up (the backward's caches) and out = glu(gate, up)."""
+    M, K = X.shape
+    H = Wg.shape[0]
+    gate = torch.empty((M, H), dtype=X.dtype, device=X.device)
+    up = torch.empty_like(gate)
+    out = torch.empty_like(gate)
+    _check(lib().gn_glu_linear_fwd(GLU[kind], _ptr(X), _ptr(Wg), _ptr(Wu), _ptr(bg), _ptr(bu),
+                                   _ptr(gate), _ptr(up), _ptr(out), M, H, K, _dt(X), _stream()),
+           "gn_glu_linear_fwd")
+    return gate, up, out
 
 
 def add_inplace(out, a):

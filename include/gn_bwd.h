@@ -327,6 +327,38 @@ int gn_adamw_step(const gn_opt_param* params, int count, float lr, float beta1, 
                   float eps, float weight_decay, float beta1_t, float beta2_t, int clear_grad,
                   void* stream);
 
+/* ---- forward kernels producing the saved tensors the backward consumes ----------------- */
+/* LayerNorm forward (fnn-layernorm.glsl:44-102): Y = (X - mean)/sqrt(var + eps) * gamma + beta
+ * with the biased variance; mean, rstd fp32 [rows] (the `rstd` array gets the variance, as
+ * the reference's var_vals buffer, with GN_LN_STAT_VAR).  gamma/beta NULL: 1/0; mean/rstd
+ * NULL: not saved.  Feeds gn_layernorm_bwd with the same flags. */
+int gn_layernorm_fwd(const void* X, const void* gamma, const void* beta, void* Y, float* mean,
+                     float* rstd, int rows, int F, float eps, int dtype, unsigned flags,
+                     void* stream);
+
+/* RMSNorm forward (rms-norm.glsl:34-70): Y = w * X * rsqrt(mean(X^2) + eps); rstd fp32 [rows]
+ * (the reference saves mean(X^2); the backward here takes rstd).  w NULL: 1. */
+int gn_rmsnorm_fwd(const void* X, const void* w, void* Y, float* rstd, int rows, int F, float eps,
+                   int dtype, void* stream);
+
+/* GLU product out = glu_kind(gate, up) over n elements (fused-swiglu.glsl:78,
+ * fused-geglu.glsl:81, fused-reglu.glsl:73; kinds GN_GLU_*). */
+int gn_glu_fwd(int kind, const void* gate, const void* up, void* out, int64_t n, int dtype,
+               void* stream);
+
+/* Linear forward (fnn-linear.glsl:33-55): Y [M x N] = X [M x K] W^T + b, W [N x K], b [N] or NULL,
+ * all in dtype (fp32 accumulation; bf16 rounds Y once). */
+int gn_linear_fwd(const void* X, const void* W, const void* b, void* Y, int M, int N, int K,
+                  int dtype, void* stream);
+
+/* Fused GLU projection forward (fused-swiglu.glsl:48-79 and its GEGLU/ReGLU twins):
+ * gate = X Wg^T + bg, up = X Wu^T + bu (both kept: the backward's gate/up caches,
+ * fused-swiglu-backward.glsl:26-34), out = glu_kind(gate, up).  X [M x K], Wg/Wu [H x K],
+ * bg/bu [H] or NULL; gate, up, out [M x H]. */
+int gn_glu_linear_fwd(int kind, const void* X, const void* Wg, const void* Wu, const void* bg,
+                      const void* bu, void* gate, void* up, void* out, int M, int H, int K,
+                      int dtype, void* stream);
+
 /* ---- misc ------------------------------------------------------------------------------ */
 /* out[i] (+)= a[i] (f32/bf16): the fan-out accumulation the reference leaves as a TODO
  * (autograd.cpp:78-86). */

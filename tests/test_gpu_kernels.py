@@ -690,3 +690,124 @@ def test_vsa_cosine_blend(gn):
     info = np.stack([np.zeros(Bn), (bl * y).sum(1), (bl * bl).sum(1)], 1).astype(np.float32)
     dP = gn.vsa_cosine_blend_bwd(gn.u32_tensor(bits, "cuda:0"), dev(w), dev(bl), dev(info), K=K)
     assert rel_err(host(dP), oracle.cosine_blend_bwd(bits, w, bl, info, K)) < 1e-5
+
+
+# ---------------------------------------------------------------------------- forward kernels
+def test_norm_fwd_golden_fp32(gn):
+    g = golden("layernorm")
+    Y, mean, rstd = gn.layernorm_fwd(dev(g["X"]), dev(g["gamma"]), dev(g["beta"]), eps=float(g["eps"]))
+    assert rel_err(host(Y), g["Y"]) < FP32_TOL
+    assert rel_err(host(mean), g["mean"]) < FP32_TOL and rel_err(host(rstd), g["rstd"]) < FP32_TOL
+    _, _, var = gn.layernorm_fwd(dev(g["X"]), dev(g["gamma"]), dev(g["beta"]), eps=float(g["eps"]),
+                                 save_var=True)
+    assert rel_err(host(var), g["var"]) < FP32_TOL
+    g = golden("rmsnorm")
+    Y, rstd = gn.rmsnorm_fwd(dev(g["X"]), dev(g["w"]), eps=float(g["eps"]))
+    assert rel_err(host(Y), g["Y"]) < FP32_TOL and rel_err(host(rstd), g["rstd"]) < FP32_TOL
+
+
+# F: 768 / 520 / 1536 / 2048 take the register path (1-4 chunks per lane, 520 a ragged
+# last chunk column), 100 and 4096 the generic one
+@pytest.mark.parametrize("rows,F,dt", [(8192, 768, "bf16"), (1000, 2048, "f32"), (256, 1536, "bf16"),
+                                       (64, 520, "bf16"), (77, 4096, "bf16"), (33, 100, "f32")])
+def test_layernorm_fwd_shapes(gn, rows, F, dt):
+    r = rng_(31)
+    X = (r.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32)
+    gamma = (1 + 0.3 * r.standard_normal(F)).astype(np.float32)
+    beta = (0.1 * r.standard_normal(F)).astype(np.float32)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    if dt == "bf16":
+        X, gamma, beta = rnd(X), rnd(gamma), rnd(beta)
+    Y, mean, rstd = gn.layernorm_fwd(dev(X, tdt), dev(gamma, tdt), dev(beta, tdt))
+    rY, rm, rr = oracle.layernorm_fwd(X, gamma, beta)
+    assert rel_err(host(Y), rY) < (BF16_TOL if dt == "bf16" else FP32_TOL)
+    assert rel_err(host(mean), rm) < FP32_TOL and rel_err(host(rstd), rr) < FP32_TOL
+    # no affine parameters: gamma = 1, beta = 0
+    Y0, _, _ = gn.layernorm_fwd(dev(X, tdt))
+    rY0, _, _ = oracle.layernorm_fwd(X, np.ones(F, np.float32), np.zeros(F, np.float32))
+    assert rel_err(host(Y0), rY0) < (BF16_TOL if dt == "bf16" else FP32_TOL)
+
+
+@pytest.mark.parametrize("rows,F,dt", [(4096, 2048, "bf16"), (300, 768, "f32"), (17, 50, "bf16")])
+def test_rmsnorm_fwd_shapes(gn, rows, F, dt):
+    r = rng_(32)
+    X = r.standard_normal((rows, F)).astype(np.float32)
+    w = (1 + 0.2 * r.standard_normal(F)).astype(np.float32)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    if dt == "bf16":
+        X, w = rnd(X), rnd(w)
+    Y, rstd = gn.rmsnorm_fwd(dev(X, tdt), dev(w, tdt))
+    rY, rr = oracle.rmsnorm_fwd(X, w)
+    assert rel_err(host(Y), rY) < (BF16_TOL if dt == "bf16" else FP32_TOL)
+    assert rel_err(host(rstd), rr) < FP32_TOL
+
+
+def test_norm_fwd_feeds_backward(gn):
+    # the saved statistics of the forward drive the backward exactly as the oracle's do
+    r = rng_(33)
+    rows, F = 512, 768
+    X = rnd((r.standard_normal((rows, F)) + 0.5).astype(np.float32))
+    gamma = rnd((1 + 0.3 * r.standard_normal(F)).astype(np.float32))
+    dY = rnd(r.standard_normal((rows, F)).astype(np.float32))
+    tX, tg, tdY = dev(X, torch.bfloat16), dev(gamma, torch.bfloat16), dev(dY, torch.bfloat16)
+    _, mean, var = gn.layernorm_fwd(tX, tg, save_var=True)
+    dX, dG, _ = gn.layernorm_bwd(tdY, tX, tg, mean, var, stat_is_var=True)
+    _, rm, rr = oracle.layernorm_fwd(X, gamma)
+    rX, rG, _ = oracle.layernorm_bwd(dY, X, gamma, rm, rr)
+    assert rel_err(host(dX), rX) < BF16_TOL and rel_err(host(dG), rG) < 1e-3
+
+
+@pytest.mark.parametrize("kind", ["swiglu_up", "swiglu_gate", "geglu_up", "geglu_gate", "reglu_up"])
+def test_glu_fwd(gn, kind):
+    g = golden("glu")
+    out = gn.glu_fwd(kind, dev(g["gate"]), dev(g["up"]))
+    assert rel_err(host(out), oracle.glu_fwd(kind, g["gate"], g["up"])) < FP32_TOL
+    r = rng_(34)
+    n = 8192 * 3 + 5  # a ragged tail after the 8-element vectors
+    gate = rnd(r.standard_normal(n + 1).astype(np.float32))
+    up = rnd(r.standard_normal(n + 1).astype(np.float32))
+    tg, tu = dev(gate, torch.bfloat16), dev(up, torch.bfloat16)
+    ref = oracle.glu_fwd(kind, gate[:n], up[:n])
+    assert rel_err(host(gn.glu_fwd(kind, tg[:n], tu[:n])), ref) < BF16_TOL
+    # views one element in (2-byte aligned) take the scalar path
+    ref1 = oracle.glu_fwd(kind, gate[1:], up[1:])
+    assert rel_err(host(gn.glu_fwd(kind, tg[1:], tu[1:])), ref1) < BF16_TOL
+
+
+# (M, N, K): multiples of 64 in K take the LDS-DMA core with the bias in its epilogue;
+# K = 40 the register-staged core after a bias fill; K = 0 leaves Y = b
+@pytest.mark.parametrize("M,N,K", [(512, 384, 768), (200, 136, 128), (100, 72, 40), (16, 24, 0)])
+def test_linear_fwd_bf16(gn, M, N, K):
+    r = rng_(35)
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    W = rnd((r.standard_normal((N, K)) * 0.05).astype(np.float32))
+    b = rnd(r.standard_normal(N).astype(np.float32))
+    tX, tW, tb = dev(X, torch.bfloat16), dev(W, torch.bfloat16), dev(b, torch.bfloat16)
+    Y = gn.linear_fwd(tX, tW, tb)
+    assert Y.dtype == torch.bfloat16
+    assert rel_err(host(Y), oracle.linear_fwd(X, W, b) if K else np.tile(b, (M, 1))) < 8e-3
+    if K:
+        assert rel_err(host(gn.linear_fwd(tX, tW)), oracle.linear_fwd(X, W)) < 8e-3
+
+
+def test_linear_fwd_fp32_golden(gn):
+    for tag in ["small", "c1l2"]:
+        g = golden(f"linear_{tag}")
+        Y = gn.linear_fwd(dev(g["X"]), dev(g["W"]), dev(g["b"]))
+        assert rel_err(host(Y), oracle.linear_fwd(g["X"], g["W"], g["b"])) < FP32_TOL
+
+
+@pytest.mark.parametrize("kind", ["geglu_up", "swiglu_up", "reglu_up"])
+def test_glu_linear_fwd(gn, kind):
+    r = rng_(36)
+    M, H, K = 512, 1024, 768
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    Wg, Wu = (rnd((r.standard_normal((H, K)) * 0.05).astype(np.float32)) for _ in range(2))
+    bg, bu = (rnd((0.1 * r.standard_normal(H)).astype(np.float32)) for _ in range(2))
+    gate, up, out = gn.glu_linear_fwd(kind, dev(X, torch.bfloat16), dev(Wg, torch.bfloat16),
+                                      dev(Wu, torch.bfloat16), dev(bg, torch.bfloat16),
+                                      dev(bu, torch.bfloat16))
+    assert rel_err(host(gate), oracle.linear_fwd(X, Wg, bg)) < 8e-3
+    assert rel_err(host(up), oracle.linear_fwd(X, Wu, bu)) < 8e-3
+    # out is formed from the saved (bf16) gate and up, which the backward then reads
+    assert rel_err(host(out), oracle.glu_fwd(kind, host(gate), host(up))) < 8e-3

@@ -41,6 +41,16 @@ def test_linear_transpose_identity():
     np.testing.assert_array_equal(db, [0, 1, 0])
 
 
+def test_linear_fwd_matches_numpy_matmul():
+    # fnn-linear.glsl:33-55: Y = X W^T + b, against numpy's fp64 matmul (a transposed W or a
+    # dropped bias fails; W is not square, so X W would not even have Y's shape)
+    for tag in ["small", "c1l2"]:
+        g = golden(f"linear_{tag}")
+        X, W, b = (g[k].astype(np.float64) for k in ("X", "W", "b"))
+        assert rel_err(oracle.linear_fwd(g["X"], g["W"], g["b"]), X @ W.T + b) < TOL
+        assert rel_err(oracle.linear_fwd(g["X"], g["W"]), X @ W.T) < TOL
+
+
 @pytest.mark.parametrize("kind", ["relu", "gelu_tanh", "gelu_erf", "silu", "tanh", "sigmoid"])
 def test_act_golden(kind):
     g = golden("act")
@@ -62,6 +72,20 @@ def test_glu_golden(kind):
     dG, dU = oracle.glu_bwd(kind, g["dO"], g["gate"], g["up"])
     assert rel_err(dG, g["dGate_" + kind]) < TOL
     assert rel_err(dU, g["dUp_" + kind]) < TOL
+
+
+@pytest.mark.parametrize("kind", ["swiglu_up", "swiglu_gate", "geglu_up", "geglu_gate", "reglu_up"])
+def test_glu_fwd_against_torch_activations(kind):
+    # fused-swiglu.glsl:78, fused-geglu.glsl:81, fused-reglu.glsl:73, against torch's own
+    # float64 SiLU / tanh-GELU / ReLU (library routines, not a retyped formula)
+    torch = pytest.importorskip("torch")
+    F = torch.nn.functional
+    g = golden("glu")
+    tg, tu = torch.from_numpy(g["gate"]).double(), torch.from_numpy(g["up"]).double()
+    ref = {"swiglu_up": tg * F.silu(tu), "swiglu_gate": F.silu(tg) * tu,
+           "geglu_up": tg * F.gelu(tu, approximate="tanh"),
+           "geglu_gate": F.gelu(tg, approximate="tanh") * tu, "reglu_up": tg * F.relu(tu)}[kind]
+    assert rel_err(oracle.glu_fwd(kind, g["gate"], g["up"]), ref.numpy()) < TOL
 
 
 def test_glu_orientation_differs():
