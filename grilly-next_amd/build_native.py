@@ -1,7 +1,8 @@
 """Builds the native libraries of this package, in-tree, for gfx950.
 
   libgn_bwd.so          HIP kernels + the C ABI declared in include/gn_bwd.h
-  grilly_core*.so       pybind11 module: tape engine (TensorRef, OpType, Node, TapeArena,
+  _grilly_core*.so      pybind11 module, imported through grilly_core.py: tape engine (TensorRef,
+                        OpType, Node, TapeArena,
                         BackwardEngine, TapeContext) calling libgn_bwd through the C ABI
 
 Usage: python grilly-next_amd/build_native.py   (also called by __graft_entry__.build()).
@@ -23,7 +24,7 @@ ARCH = os.environ.get("GN_OFFLOAD_ARCH", "gfx950")
 KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip", "gn_gemm_dma.hip",
                   "gn_vsa.hip", "gn_attn.hip", "gn_optim.hip", "gn_tapeops.hip", "gn_fwd.hip",
                   "gn_probe.hip"]
-TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "bindings.cpp"]
+TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "tape/checkpoint.cpp", "bindings.cpp"]
 
 # -packed-fp32-ops off: packed fp32 VALU forms are kept out of the generated code.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INCLUDE, "-I", CSRC,
@@ -73,7 +74,12 @@ def build_tape(jobs=8):
     cmds = [["g++", *flags, "-c", os.path.join(CSRC, s), "-o", _obj(s)] for s in TAPE_SOURCES]
     with ThreadPoolExecutor(jobs) as ex:
         list(ex.map(_run, cmds))
-    out = os.path.join(HERE, "grilly_core" + ext)
+    # the extension is _grilly_core; grilly_core.py loads it after torch (see there).  A
+    # grilly_core*.so left by an older build would shadow grilly_core.py: remove it.
+    for f in os.listdir(HERE):
+        if f.startswith("grilly_core.") and f.endswith(".so"):
+            os.remove(os.path.join(HERE, f))
+    out = os.path.join(HERE, "_grilly_core" + ext)
     _run(["g++", "-shared", "-o", out + ".tmp", *[_obj(s) for s in TAPE_SOURCES],
           "-L", HERE, "-lgn_bwd", "-Wl,-rpath,$ORIGIN", "-L/opt/rocm/lib", "-lamdhip64",
           "-Wl,-rpath,/opt/rocm/lib"])

@@ -1,4 +1,5 @@
-// bindings.cpp — pybind11 module `grilly_core`: the reference's autograd API surface
+// bindings.cpp — pybind11 module `_grilly_core` (imported as grilly_core through
+// grilly_core.py): the reference's autograd API surface
 // (cpp/python/bindings.cpp:2688-2880) on the MI355X tape engine, plus a Device with
 // explicit buffer upload/download (the reference gives Python no way to create a buffer
 // id for its own data, bindings.cpp:2725).
@@ -7,6 +8,7 @@
 #include <pybind11/stl.h>
 
 #include "autograd.h"
+#include "checkpoint.h"
 #include "device.h"
 #include "gn_bwd.h"
 
@@ -28,7 +30,7 @@ py::dict stats_dict(const BackwardEngine::Stats& s) {
 
 }  // namespace
 
-PYBIND11_MODULE(grilly_core, m) {
+PYBIND11_MODULE(_grilly_core, m) {
     m.doc() = "grilly-next tape autograd on MI355X (HIP kernels through libgn_bwd's C ABI)";
     m.attr("__backend__") = "hip-gfx950";
     m.def("kernel_library_version", []() { return std::string(gn_version()); });
@@ -196,6 +198,95 @@ PYBIND11_MODULE(grilly_core, m) {
         .def("save", [](const TapeArena& a) { return a.save().offset; })
         .def("restore", [](TapeArena& a, size_t off) { a.restore({off, nullptr}); });
     m.attr("NODE_BYTES") = sizeof(Node);
+
+    // ---- GRLY v3 hypernetwork checkpoint (bindings.cpp:2965-3039) + optimizer section ----
+    // dims = (d_model, vsa_dim, K, router_hidden); opt = None or dict(kind, n_states, step,
+    // hyper).  The grilly_bridge functions save/load_hypernetwork_weights wrap these.
+    using FArr = py::array_t<float, py::array::c_style | py::array::forcecast>;
+    auto to_dims = [](const std::array<uint32_t, 4>& a) {
+        ckpt::HyperDims d;
+        d.d_model = a[0]; d.vsa_dim = a[1]; d.K = a[2]; d.router_hidden = a[3];
+        return d;
+    };
+    auto to_opt = [](const py::dict& o) {
+        ckpt::OptHeader h;
+        h.kind = o["kind"].cast<uint32_t>();
+        h.n_states = o["n_states"].cast<uint32_t>();
+        h.step = o["step"].cast<uint64_t>();
+        h.hyper = o["hyper"].cast<std::vector<float>>();
+        return h;
+    };
+    auto from_opt = [](const ckpt::OptHeader& h) {
+        py::dict o;
+        o["kind"] = h.kind; o["n_states"] = h.n_states; o["step"] = h.step; o["hyper"] = h.hyper;
+        return o;
+    };
+    auto to_dev = [](const std::vector<std::tuple<uint64_t, uint64_t, int>>& v) {
+        std::vector<ckpt::DevTensor> out;
+        for (const auto& t : v) out.push_back({std::get<0>(t), std::get<1>(t), std::get<2>(t)});
+        return out;
+    };
+    m.def("hypernetwork_sizes", [to_dims](const std::array<uint32_t, 4>& dims) {
+        return ckpt::hyper_sizes(to_dims(dims));
+    }, py::arg("dims"));
+    m.def("_grly_write", [to_dims, to_opt](const std::string& path, const std::array<uint32_t, 4>& dims,
+                                          const std::vector<FArr>& w, py::object opt,
+                                          const std::vector<FArr>& states) {
+        std::vector<const float*> pw, ps;
+        for (const auto& a : w) pw.push_back(a.data());
+        for (const auto& a : states) ps.push_back(a.data());
+        const auto sizes = ckpt::hyper_sizes(to_dims(dims));
+        for (size_t i = 0; i < w.size() && i < sizes.size(); ++i)
+            if ((uint64_t)w[i].size() != sizes[i]) throw std::invalid_argument("_grly_write: tensor size");
+        ckpt::OptHeader h;
+        if (!opt.is_none()) h = to_opt(opt.cast<py::dict>());
+        for (size_t i = 0; i < states.size(); ++i)
+            if (h.n_states == 0 || (uint64_t)states[i].size() != sizes[i / h.n_states])
+                throw std::invalid_argument("_grly_write: state tensor size");
+        ckpt::write_hyper(path, to_dims(dims), pw, opt.is_none() ? nullptr : &h, ps);
+    }, py::arg("path"), py::arg("dims"), py::arg("weights"), py::arg("opt"), py::arg("states"));
+    m.def("_grly_read", [to_dims, from_opt](const std::string& path, const std::array<uint32_t, 4>& dims,
+                                           int opt_states) {
+        const auto d = to_dims(dims);
+        const auto sizes = ckpt::hyper_sizes(d);
+        std::vector<FArr> w, st;
+        std::vector<float*> pw, ps;
+        for (uint64_t n : sizes) w.emplace_back((py::ssize_t)n);
+        for (auto& a : w) pw.push_back(a.mutable_data());
+        ckpt::OptHeader h;
+        if (opt_states >= 0)
+            for (size_t i = 0; i < sizes.size() * (size_t)opt_states; ++i) st.emplace_back((py::ssize_t)sizes[i / opt_states]);
+        for (auto& a : st) ps.push_back(a.mutable_data());
+        ckpt::read_hyper(path, d, pw, opt_states >= 0 ? &h : nullptr, ps, (uint32_t)std::max(opt_states, 0));
+        return py::make_tuple(w, opt_states >= 0 ? py::object(from_opt(h)) : py::none(), st);
+    }, py::arg("path"), py::arg("dims"), py::arg("opt_states") = -1);
+    m.def("_grly_probe", [from_opt](const std::string& path) {
+        ckpt::HyperDims d;
+        ckpt::OptHeader h;
+        const bool has = ckpt::probe_hyper(path, &d, &h);
+        return py::make_tuple(std::array<uint32_t, 4>{d.d_model, d.vsa_dim, d.K, d.router_hidden},
+                              has ? py::object(from_opt(h)) : py::none());
+    }, py::arg("path"));
+    m.def("_grly_save_device", [to_dims, to_opt, to_dev](const std::string& path, const std::array<uint32_t, 4>& dims,
+                                                       const std::vector<std::tuple<uint64_t, uint64_t, int>>& w,
+                                                       py::object opt,
+                                                       const std::vector<std::tuple<uint64_t, uint64_t, int>>& states) {
+        ckpt::OptHeader h;
+        if (!opt.is_none()) h = to_opt(opt.cast<py::dict>());
+        py::gil_scoped_release nogil;
+        ckpt::save_hyper_device(path, to_dims(dims), to_dev(w), opt.is_none() ? nullptr : &h, to_dev(states));
+    }, py::arg("path"), py::arg("dims"), py::arg("weights"), py::arg("opt"), py::arg("states"));
+    m.def("_grly_load_device", [to_dims, to_dev, from_opt](const std::string& path, const std::array<uint32_t, 4>& dims,
+                                                         const std::vector<std::tuple<uint64_t, uint64_t, int>>& w,
+                                                         bool with_opt,
+                                                         const std::vector<std::tuple<uint64_t, uint64_t, int>>& states) {
+        ckpt::OptHeader h;
+        {
+            py::gil_scoped_release nogil;
+            ckpt::load_hyper_device(path, to_dims(dims), to_dev(w), with_opt ? &h : nullptr, to_dev(states));
+        }
+        return with_opt ? py::object(from_opt(h)) : py::none();
+    }, py::arg("path"), py::arg("dims"), py::arg("weights"), py::arg("with_opt"), py::arg("states"));
 
     py::register_exception_translator([](std::exception_ptr p) {
         try {

@@ -522,10 +522,13 @@ def surprise_momentum_step(entries, eta_base=1e-3, alpha=0.9, lambda_recall=0.0,
 
 def adamw_step(entries, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, step=1,
                clear_grad=True):
-    """entries: dicts with W, grad, state0 (= m), state1 (= v), optional W_bf16."""
+    """entries: dicts with W, grad, state0 (= m), state1 (= v), optional W_bf16.  The bias
+    corrections beta^step are taken from the fp32 betas the kernel receives, so the step
+    depends only on fp32 hyper-parameters (a resumed checkpoint continues bit for bit)."""
     arr = _opt_params(entries)
+    b1, b2 = ctypes.c_float(beta1).value, ctypes.c_float(beta2).value
     _check(lib().gn_adamw_step(arr, len(entries), lr, beta1, beta2, eps, weight_decay,
-                               beta1 ** step, beta2 ** step, int(clear_grad), _stream()),
+                               b1 ** step, b2 ** step, int(clear_grad), _stream()),
            "gn_adamw_step")
 
 

@@ -171,3 +171,124 @@ class AdamW(_TapeOptimizer):
         gn_bwd.adamw_step(entries, self.lr, self.betas[0], self.betas[1], self.eps,
                           self.weight_decay, step=self.t, clear_grad=True)
         return len(entries)
+
+
+# ---- GRLY v3 hypernetwork checkpoint (bindings.cpp:2965-3039) -----------------------------
+class HypernetworkWeights:
+    """The ten weight tensors of the reference's VSAHypernetwork in checkpoint order
+    (bindings.cpp:2973-2984), with the model's dimension accessors
+    (vsa_hypernetwork.h:39-43).  Tensors are GPU tensors (fp32 or bf16) holding exactly
+    grilly_core.hypernetwork_sizes(...) elements each; any shape with that many elements."""
+
+    NAMES = ("W_proj", "b_proj", "W1", "b1", "W2", "b2", "W_r1", "b_r1", "W_r2", "b_r2")
+
+    def __init__(self, d_model, vsa_dim, K, router_hidden=32, tensors=None, device="cuda:0",
+                 dtype=None):
+        import torch
+        self._dims = (int(d_model), int(vsa_dim), int(K), int(router_hidden))
+        sizes = grilly_core.hypernetwork_sizes(self._dims)
+        if tensors is None:
+            tensors = [torch.zeros(n, device=device, dtype=dtype or torch.float32) for n in sizes]
+        tensors = list(tensors)
+        if len(tensors) != 10 or any(t.numel() != n for t, n in zip(tensors, sizes)):
+            raise ValueError(f"HypernetworkWeights: ten tensors of sizes {sizes} expected")
+        self.tensors = tensors
+
+    def d_model(self):
+        return self._dims[0]
+
+    def vsa_dim(self):
+        return self._dims[1]
+
+    def K(self):
+        return self._dims[2]
+
+    def router_hidden(self):
+        return self._dims[3]
+
+    def num_weight_bufs(self):
+        return 10
+
+    def weight_buffers(self):
+        return self.tensors
+
+    def dims(self):
+        return self._dims
+
+
+_OPT_KIND = {"SurpriseMomentumOptimizer": 0, "AdamW": 1}
+
+
+def _dev_list(ts):
+    for t in ts:
+        if not (t.is_cuda and t.is_contiguous()):
+            raise ValueError("checkpoint tensors must be contiguous GPU tensors")
+    return [(t.data_ptr(), t.numel(), dtype_code(t)) for t in ts]
+
+
+def _opt_parts(model, optimizer):
+    """(kind, hyper list, state tensors parameter-major, n_states) of an optimizer built over
+    model.weight_buffers() in the same order."""
+    ws = model.weight_buffers()
+    if len(optimizer.weights) != len(ws) or any(a.data_ptr() != b.data_ptr()
+                                                for a, b in zip(optimizer.weights, ws)):
+        raise ValueError("the optimizer must be built over model.weight_buffers(), in order")
+    kind = _OPT_KIND[type(optimizer).__name__]
+    if kind == 0:
+        per = [[s] + ([optimizer.delta[i]] if optimizer.delta else [])
+               for i, s in enumerate(optimizer.s_bar)]
+        hyper = [optimizer.eta_base, optimizer.alpha_momentum, optimizer.lambda_recall,
+                 optimizer.surprise_floor, optimizer.weight_decay, optimizer.clip_max]
+    else:
+        per = [[m, v] for m, v in zip(optimizer.m, optimizer.v)]
+        hyper = [optimizer.lr, optimizer.betas[0], optimizer.betas[1], optimizer.eps,
+                 optimizer.weight_decay]
+    return kind, hyper, [t for p in per for t in p], len(per[0])
+
+
+def save_hypernetwork_weights(model, path, optimizer=None):
+    """The reference's save_hypernetwork_weights(model, path) (bindings.cpp:2965-3003): GRLY v3
+    header and the ten tensors as fp32.  With an optimizer (SurpriseMomentumOptimizer or AdamW
+    over model.weight_buffers()), its fp32 master weights are written in place of the bf16
+    copies and its state follows in an optimizer section the reference's loader skips."""
+    if optimizer is None:
+        grilly_core._grly_save_device(str(path), model.dims(), _dev_list(model.weight_buffers()),
+                                      None, [])
+        return
+    kind, hyper, states, n = _opt_parts(model, optimizer)
+    opt = dict(kind=kind, n_states=n, step=int(optimizer.t), hyper=[float(h) for h in hyper])
+    grilly_core._grly_save_device(str(path), model.dims(), _dev_list(optimizer.masters), opt,
+                                  _dev_list(states))
+
+
+def load_hypernetwork_weights(model, path, optimizer=None):
+    """The reference's load_hypernetwork_weights(model, path) (bindings.cpp:3005-3039): checks
+    the magic and dimensions (and, unlike the reference, every tensor's count, so a wrong file
+    cannot overrun a buffer).  With an optimizer, the file must hold a section of the same
+    kind; masters, state, step and hyper-parameters are restored and bf16 weights receive the
+    rounded masters."""
+    if optimizer is None:
+        grilly_core._grly_load_device(str(path), model.dims(), _dev_list(model.weight_buffers()),
+                                      False, [])
+        return
+    kind, _, states, _ = _opt_parts(model, optimizer)
+    _, info = grilly_core._grly_probe(str(path))
+    if info is None or info["kind"] != kind:
+        raise ValueError(f"{path}: no {type(optimizer).__name__} state in this checkpoint")
+    if kind == 0 and info["n_states"] == 2 and not optimizer.delta:
+        import torch
+        optimizer.delta = [torch.zeros_like(m) for m in optimizer.masters]
+        kind, _, states, _ = _opt_parts(model, optimizer)
+    opt = grilly_core._grly_load_device(str(path), model.dims(), _dev_list(optimizer.masters),
+                                        True, _dev_list(states))
+    for w, mw in zip(optimizer.weights, optimizer.masters):
+        if w.data_ptr() != mw.data_ptr():
+            w.copy_(mw)
+    optimizer.t = int(opt["step"])
+    h = opt["hyper"]
+    if kind == 0:
+        (optimizer.eta_base, optimizer.alpha_momentum, optimizer.lambda_recall,
+         optimizer.surprise_floor, optimizer.weight_decay, optimizer.clip_max) = h
+    else:
+        optimizer.lr, b1, b2, optimizer.eps, optimizer.weight_decay = h
+        optimizer.betas = (b1, b2)

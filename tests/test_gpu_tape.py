@@ -478,3 +478,92 @@ def test_remaining_ops_through_tape(env):
     for t_, ref in zip([tx, ty, tz, tw, tM], X):
         assert rel_err(grad(gb, dev, tape, t_), ref.grad.numpy()) < 1e-5
     tape.end()
+
+
+# ---------------------------------------------------------------- GRLY v3 checkpoint
+HYPER_DIMS = (64, 256, 4, 32)  # d_model, vsa_dim, K, router_hidden
+
+
+def test_hypernetwork_checkpoint_device_round_trip(env, tmp_path):
+    """save/load_hypernetwork_weights (bindings.cpp:2965-3039) from and into device tensors:
+    the file holds the exact fp32 values (bf16 widened), and an fp32 file loaded into bf16
+    tensors rounds to nearest-even like torch's conversion, ties and infinities included."""
+    gc, gb, dev = env
+    sizes = gc.hypernetwork_sizes(HYPER_DIMS)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(3)
+    for dt in (torch.float32, torch.bfloat16):
+        src = gb.HypernetworkWeights(*HYPER_DIMS, tensors=[
+            torch.randn(n, device="cuda:0", generator=g).to(dt) for n in sizes])
+        p = tmp_path / f"w_{str(dt)[6:]}.grly"
+        gb.save_hypernetwork_weights(src, p)
+        host, _, _ = gc._grly_read(str(p), HYPER_DIMS)
+        for a, t in zip(host, src.weight_buffers()):
+            np.testing.assert_array_equal(a, t.float().cpu().numpy())
+        dst = gb.HypernetworkWeights(*HYPER_DIMS, dtype=dt)
+        gb.load_hypernetwork_weights(dst, p)
+        for a, b in zip(dst.weight_buffers(), src.weight_buffers()):
+            assert torch.equal(a, b)
+    w32 = [torch.randn(n, device="cuda:0", generator=g) for n in sizes]
+    ties = torch.tensor([1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -8), 2 ** -130, float("inf"),
+                         -float("inf"), 3.0e38, 1e-45], device="cuda:0")
+    w32[3][:ties.numel()] = ties
+    src = gb.HypernetworkWeights(*HYPER_DIMS, tensors=w32)
+    p = tmp_path / "w32.grly"
+    gb.save_hypernetwork_weights(src, p)
+    dst = gb.HypernetworkWeights(*HYPER_DIMS, dtype=torch.bfloat16)
+    gb.load_hypernetwork_weights(dst, p)
+    for a, b in zip(dst.weight_buffers(), w32):
+        assert torch.equal(a, b.bfloat16())
+    with pytest.raises(RuntimeError, match="Model dimension mismatch"):
+        gb.load_hypernetwork_weights(gb.HypernetworkWeights(64, 256, 2, 32), p)
+
+
+class _GradTape:
+    """Stands in for a TapeContext after backward: weight id -> gradient buffer id."""
+
+    def __init__(self, weights, grads):
+        self.g = {w.data_ptr(): gr for w, gr in zip(weights, grads)}
+
+    def get_grad_buffer(self, wid):
+        return self.g[wid].data_ptr()
+
+
+@pytest.mark.parametrize("opt_kind", ["adamw", "surprise"])
+def test_hypernetwork_checkpoint_resumes_training(env, tmp_path, opt_kind):
+    """Checkpoint after one optimizer step, reload into a fresh model and optimizer, take the
+    next step on both: weights (bf16 copies and fp32 masters) and state agree bit for bit."""
+    gc, gb, dev = env
+    sizes = gc.hypernetwork_sizes(HYPER_DIMS)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(9)
+    A = gb.HypernetworkWeights(*HYPER_DIMS, tensors=[
+        (0.1 * torch.randn(n, device="cuda:0", generator=g)).bfloat16() for n in sizes])
+    G1, G2 = ([1e-2 * torch.randn(n, device="cuda:0", generator=g) for n in sizes] for _ in range(2))
+
+    def make(model, lr):
+        if opt_kind == "adamw":
+            return gb.AdamW(model.weight_buffers(), lr=lr, weight_decay=0.01)
+        return gb.SurpriseMomentumOptimizer(model.weight_buffers(), lr=lr, alpha=0.9, clip=1.0)
+
+    def state(o):
+        return (o.m + o.v) if opt_kind == "adamw" else o.s_bar
+
+    oa = make(A, 1e-2)
+    oa.step(_GradTape(A.weight_buffers(), [x.clone() for x in G1]))
+    p = tmp_path / "ckpt.grly"
+    gb.save_hypernetwork_weights(A, p, optimizer=oa)
+    oa.step(_GradTape(A.weight_buffers(), [x.clone() for x in G2]))
+    B = gb.HypernetworkWeights(*HYPER_DIMS, dtype=torch.bfloat16)
+    ob = make(B, 5e-4)  # hyper-parameters and step come from the file
+    gb.load_hypernetwork_weights(B, p, optimizer=ob)
+    assert ob.t == 1
+    ob.step(_GradTape(B.weight_buffers(), [x.clone() for x in G2]))
+    for a, b in zip(A.weight_buffers() + oa.masters + state(oa),
+                    B.weight_buffers() + ob.masters + state(ob)):
+        assert torch.equal(a, b)
+    # a checkpoint without an optimizer section cannot restore one
+    q = tmp_path / "plain.grly"
+    gb.save_hypernetwork_weights(A, q)
+    with pytest.raises(ValueError, match="no"):
+        gb.load_hypernetwork_weights(B, q, optimizer=ob)

@@ -8,8 +8,8 @@ import pytest
 
 from conftest import PKG
 
-if not any(f.startswith("grilly_core") and f.endswith(".so") for f in os.listdir(PKG)):
-    pytest.skip("grilly_core not built", allow_module_level=True)
+if not any(f.startswith("_grilly_core") and f.endswith(".so") for f in os.listdir(PKG)):
+    pytest.skip("_grilly_core (grilly_core's extension) not built", allow_module_level=True)
 
 import grilly_core  # noqa: E402
 import grilly_bridge as gb  # noqa: E402
