@@ -399,8 +399,8 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
     };
     bf16x8_t fa[4][FM], fb[4][FN];
     // BIAS: per-lane partial row sums of op(A): fragment i holds row (lane % 32) of rows
-    // wm WM + 32 i, eight k values per lane, summed with v_dot2 against ones into four
-    // independent accumulators per fragment (one per value pair), so no dot2 waits on another
+    // wm WM + 32 i, eight k values per lane, summed into four independent accumulators per
+    // fragment (one per value pair), so no add waits on another
     float bsum[BIAS ? FM : 1][4];
 #pragma unroll
     for (int i = 0; i < (BIAS ? FM : 1); ++i)
@@ -431,19 +431,31 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
             acc[q / FN][q % FN] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 fa[cur][q / FN], fb[cur][q % FN], acc[q / FN][q % FN], 0, 0, 0);
             if constexpr (BIAS) {
-                // the 4 dot2 of fragment q / FN spread over its FN MFMAs.  v_dot2c_f32_bf16
-                // costs MFMA-pipe time here: the bias variant measured ~25 % slower on the
-                // decoder's weight gradients, still a net win over two extra launches
+                // the 4 value pairs of fragment q / FN spread over its FN MFMAs.  With FN >= 4
+                // (one pair per MFMA) each pair is widened to fp32 with a shift and a mask
+                // (exact) and added on the VALU: 4 VALU ops per MFMA, 128x256 tiles ~10 %
+                // faster than v_dot2.  With FN = 2 that would be 8 VALU ops per MFMA, which
+                // measured ~10 % slower than one v_dot2c_f32_bf16 against ones per pair
                 constexpr int i = q / FN, d0 = (q % FN) * 4 / FN, d1 = (q % FN + 1) * 4 / FN;
-                typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
-                const bf16x2_v one = {(__bf16)1.0f, (__bf16)1.0f};
-                static_for<4>([&](auto D_) {
-                    constexpr int d = decltype(D_)::value;
-                    if constexpr (d >= d0 && d < d1)
-                        bsum[i][d] = __builtin_amdgcn_fdot2_f32_bf16(
-                            __builtin_shufflevector(fa[cur][i], fa[cur][i], 2 * d, 2 * d + 1), one,
-                            bsum[i][d], false);
-                });
+                if constexpr (FN >= 4) {
+                    typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
+                    const u32x4_v w = __builtin_bit_cast(u32x4_v, fa[cur][i]);
+                    static_for<4>([&](auto D_) {
+                        constexpr int d = decltype(D_)::value;
+                        if constexpr (d >= d0 && d < d1)
+                            bsum[i][d] += __uint_as_float(w[d] << 16) + __uint_as_float(w[d] & 0xffff0000u);
+                    });
+                } else {
+                    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+                    const bf16x2_v one = {(__bf16)1.0f, (__bf16)1.0f};
+                    static_for<4>([&](auto D_) {
+                        constexpr int d = decltype(D_)::value;
+                        if constexpr (d >= d0 && d < d1)
+                            bsum[i][d] = __builtin_amdgcn_fdot2_f32_bf16(
+                                __builtin_shufflevector(fa[cur][i], fa[cur][i], 2 * d, 2 * d + 1), one,
+                                bsum[i][d], false);
+                    });
+                }
             }
             constexpr int r0 = reads_before<NM, NR, front>(q), r1 = reads_before<NM, NR, front>(q + 1);
             static_for<NR>([&](auto R_) {

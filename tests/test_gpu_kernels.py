@@ -140,6 +140,24 @@ def test_linear_split_k_weight_gradient(gn, M, N, K):
     assert torch.equal(dW1, dW2)
 
 
+def test_linear_wide_tile_bias_sums(gn):
+    """The decoder's gate/up weight-gradient shape (8192 rows, 6144 x 768) takes the 128 x 256
+    tile, whose fused bias sums run on the VALU (narrower tiles use v_dot2): dW against an fp32
+    BLAS product of the same bf16 values, db against float64 column sums, and bit-identical
+    across runs."""
+    r = rng_(15)
+    M, N, K = 8192, 6144, 768
+    dY = rnd((r.standard_normal((M, N)) * 0.01).astype(np.float32))
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    W = rnd((r.standard_normal((N, K)) * 0.02).astype(np.float32))
+    tdY, tX, tW = dev(dY, torch.bfloat16), dev(X, torch.bfloat16), dev(W, torch.bfloat16)
+    _, dW1, db1 = gn.linear_bwd(tdY, tX, tW, need_dx=False)
+    _, dW2, db2 = gn.linear_bwd(tdY, tX, tW, need_dx=False)
+    assert rel_err(host(dW1), dY.T @ X) < 1e-4
+    assert rel_err(host(db1), dY.astype(np.float64).sum(axis=0)) < 1e-5
+    assert torch.equal(dW1, dW2) and torch.equal(db1, db2)
+
+
 def test_linear_no_dx_and_accumulate(gn):
     g = golden("linear_small")
     dY, X, W = dev(g["dY"]), dev(g["X"]), dev(g["W"])
