@@ -377,6 +377,61 @@ def test_decoder_stack_through_tape(env):
     assert not bad, f"relative errors above 2e-2: {bad} (all: {errs})"
 
 
+def test_decoder_full_size_through_tape(env):
+    """BASELINE configs[4] at its full size (12 layers, d 768, 12 heads, GEGLU 3072, tied
+    embedding 32000, B 8 x S 1024): every weight gradient of the first, a middle and the last
+    layer, the embedding and the final norm, against fp32 torch autograd of the same
+    bf16-stored forward (normwise relative error <= 2e-2).
+
+    The second LayerNorm's gain gradient dgamma = sum_rows dy * xhat cancels heavily (its
+    largest entry is ~5 % of sum_rows |dy * xhat| at this size), so the ~1 % that the bf16
+    gradients between the 12 layers leave in its upstream dy (correlated with xhat through the
+    residual stream) becomes ~3 % in dgamma.  For it the test pins the kernel exactly instead
+    (dgamma against the oracle's LayerNorm backward fed the GPU's own upstream dy, <= 1e-4) and
+    bounds the end-to-end error by 5e-2."""
+    gc, gb, dev = env
+    import decoder_tape
+    m = decoder_tape.Decoder(seed=9)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(13)
+    for p in m.layers:
+        for k in ("ln1_g", "ln2_g"):
+            p[k].copy_((1 + 0.2 * torch.randn(p[k].shape, device="cuda:0", generator=g)).bfloat16())
+        for k in ("ln1_b", "ln2_b", "bqkv", "bo", "bg", "bu", "bd"):
+            p[k].copy_((0.05 * torch.randn(p[k].shape, device="cuda:0", generator=g)).bfloat16())
+    m.forward()
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    loss = m.record(tape)
+    tape.backward(loss, 0)
+    keys = ("Wqkv", "bqkv", "Wo", "bo", "ln1_g", "ln1_b", "ln2_g", "Wg", "Wu", "bg", "Wd", "bd")
+    layers = (0, m.L // 2, m.L - 1)
+    got = {"E": grad(gb, dev, tape, m.E, gb.DTYPE_F32),
+           "lnf_g": grad(gb, dev, tape, m.lnf_g, gb.DTYPE_F32)}
+    dn2 = {}
+    for i in layers:
+        for k in keys:
+            got[f"{k}{i}"] = grad(gb, dev, tape, m.layers[i][k], gb.DTYPE_F32)
+        dn2[i] = grad(gb, dev, tape, m.acts[i]["n2"])  # the LayerNorm's upstream dy (bf16)
+    tape.end()
+    for i in layers:  # the LayerNorm backward kernel on its own input: fp32-exact
+        a, p = m.acts[i], m.layers[i]
+        _, rg, _ = oracle.layernorm_bwd(dn2[i], a["x2"].float().cpu().numpy(),
+                                        p["ln2_g"].float().cpu().numpy(),
+                                        a["m2"].float().cpu().numpy(), a["r2"].float().cpu().numpy())
+        assert rel_err(got[f"ln2_g{i}"], rg) < 1e-4, i
+    E, params, lnf_g, _ = _decoder_reference(m)
+    want = {"E": E.grad, "lnf_g": lnf_g.grad}
+    for i in layers:
+        for k in keys:
+            want[f"{k}{i}"] = params[i][k].grad
+    errs = {k: rel_err(got[k], want[k].cpu().numpy()) for k in got}
+    del E, params, lnf_g, want
+    torch.cuda.empty_cache()
+    bad = {k: v for k, v in errs.items() if not v < (5e-2 if k.startswith("ln2_g") else 2e-2)}
+    assert not bad, f"relative errors above the bound: {bad} (all: {errs})"
+
+
 def test_training_step_with_optimizers(env):
     """BASELINE configs[0] MLP, full training step as vsa_training_step orders it
     (bindings.cpp:3196-3279): backward, optimizer over the tape's gradients, end; then a
