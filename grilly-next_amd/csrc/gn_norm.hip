@@ -179,10 +179,14 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
 // out[f] (+)= sum_g part[g][f] over G partial rows.  Block: 16 waves x 64 columns (one per
 // lane, 256-byte rows); wave w sums rows w, w + 16, ...; the waves' sums are added in a
 // fixed order.
+// blockIdx.y picks the partial plane: plane 0 (part) -> out0, plane 1 (part + G F) -> out1,
+// so the gain and bias sums of a LayerNorm finish in one launch.
 __global__ __launch_bounds__(1024) void colsum_partials(const float* __restrict__ part, int G,
-                                                        int F, float* __restrict__ out,
-                                                        int accumulate) {
+                                                        int F, float* __restrict__ out0,
+                                                        float* __restrict__ out1, int accumulate) {
     __shared__ float sh[16][64];
+    float* __restrict__ out = blockIdx.y ? out1 : out0;
+    part += (size_t)blockIdx.y * G * F;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int f = blockIdx.x * 64 + lane;
     float s = 0.f;
@@ -320,8 +324,12 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
 #undef GN_NORM_LAUNCH
         GN_LAUNCH_CHECK("norm backward rows");
         const unsigned gf = (F + 63) / 64;
-        if (dA) colsum_partials<<<gf, 1024, 0, s>>>(part, G, F, dA, acc);
-        if (MODE == 0 && dB) colsum_partials<<<gf, 1024, 0, s>>>(part + (size_t)G * F, G, F, dB, acc);
+        if (dA && MODE == 0 && dB)
+            colsum_partials<<<dim3(gf, 2), 1024, 0, s>>>(part, G, F, dA, dB, acc);
+        else if (dA)
+            colsum_partials<<<gf, 1024, 0, s>>>(part, G, F, dA, nullptr, acc);
+        else if (MODE == 0 && dB)
+            colsum_partials<<<gf, 1024, 0, s>>>(part + (size_t)G * F, G, F, dB, nullptr, acc);
         GN_LAUNCH_CHECK("norm backward finish");
         return GN_OK;
     }

@@ -93,6 +93,18 @@ void BackwardEngine::contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t 
     // fan-out: the second consumer's gradient is added (autograd.cpp:78-86 drops it)
     if (e->dtype != dtype || e->grad_bytes != bytes)
         throw std::runtime_error("BackwardEngine: fan-out gradients disagree in dtype or size");
+    if (!e->owned && owned) {
+        // the recorded gradient is borrowed (another node's buffer) but the new one is this
+        // contribution's own: add the borrowed one into it and keep it (one kernel, no copy;
+        // a single fp add is commutative, so the sum is the same either way round)
+        gn_call(gn_add_inplace(P(g), P(e->grad_id), (int64_t)numel, gn_dtype(dtype, "fan-out"),
+                               dev_.stream()), "fan-out add");
+        e->grad_id = g;
+        e->owned = true;
+        stats_.fanout_accumulations++;
+        stats_.shaders_dispatched++;
+        return;
+    }
     if (!e->owned) {
         uint64_t fresh = alloc_grad(bytes);
         hip_check(hipMemcpyAsync(P(fresh), P(e->grad_id), bytes, hipMemcpyDeviceToDevice,
