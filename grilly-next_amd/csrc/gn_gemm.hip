@@ -415,8 +415,13 @@ int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigne
 // overwrites) unless accumulating.
 int weight_grad(const void* dY, int ldy, const void* X, int ldx, int M, int N, int Kin, void* dW,
                 void* dW2, int Msplit, float* db, float* db2, int dtype, unsigned flags,
-                hipStream_t s) {
+                hipStream_t s, void* ws = nullptr, size_t ws_bytes = 0) {
     GemmDesc d{};
+    // split-K partial planes need 16-byte aligned storage; a misaligned workspace is unused
+    if (ws && (reinterpret_cast<uintptr_t>(ws) & 15u) == 0) {
+        d.part = (float*)ws;
+        d.part_cap = ws_bytes;
+    }
     d.nseg = 1;
     d.A[0] = (const bf16_t*)dY; d.lda[0] = ldy; d.Ks[0] = M;
     d.B[0] = (const bf16_t*)X; d.ldb[0] = ldx;
@@ -458,6 +463,22 @@ int weight_grad(const void* dY, int ldy, const void* X, int ldx, int M, int N, i
             return rc;
     }
     return gemm_run(d, 1, 0, dtype, GN_F32, s);
+}
+
+// Workspace bytes for the split-K partials of weight_grad's GEMM (dW [N x Kin] over M rows,
+// bias sums included), as the launch would choose them with an unbounded workspace.
+size_t weight_grad_ws_bytes(int M, int N, int Kin, int dtype) {
+    if (dtype != GN_BF16 || M <= 0 || N <= 0 || Kin <= 0) return 0;
+    GemmDesc d{};
+    const bf16_t* al = reinterpret_cast<const bf16_t*>((uintptr_t)256);  // aligned stand-in
+    float* alf = reinterpret_cast<float*>((uintptr_t)256);
+    d.nseg = 1;
+    d.A[0] = al; d.lda[0] = N; d.Ks[0] = M;
+    d.B[0] = al; d.ldb[0] = Kin;
+    d.M = N; d.N = Kin; d.C = alf; d.C2 = alf; d.Msplit = N; d.ldc = Kin;
+    d.bias = alf; d.bias2 = alf;
+    if (!gemm_dma_applicable(d)) return 0;
+    return gemm_dma_part_bytes(d, 1, GN_F32);
 }
 
 // Plain-argument form used by the C entry points.
@@ -551,6 +572,18 @@ extern "C" int gn_colsum(const void* in, float* out, int M, int N, int dtype, un
 extern "C" int gn_linear_bwd(const void* dY, const void* X, const void* W, void* dX, void* dW,
                              void* db, int M, int N, int K, int dtype, unsigned flags,
                              void* stream) {
+    return gn_linear_bwd_ws(dY, X, W, dX, dW, db, M, N, K, dtype, flags, nullptr, 0, stream);
+}
+
+extern "C" size_t gn_linear_workspace_bytes(int M, int N, int K, int dtype) {
+    return weight_grad_ws_bytes(M, N, K, dtype);
+}
+
+// Same, with a workspace for the weight gradient's split-K partials (may be NULL / short:
+// the split is then limited to what fits).
+extern "C" int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, void* dX, void* dW,
+                                void* db, int M, int N, int K, int dtype, unsigned flags,
+                                void* ws, size_t ws_bytes, void* stream) {
     clear_error();
     GN_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gn_linear_bwd: negative size");
     GN_REQUIRE(dY && X && W && dW, "gn_linear_bwd: null pointer (dY, X, W, dW are required)");
@@ -562,7 +595,8 @@ extern "C" int gn_linear_bwd(const void* dY, const void* X, const void* W, void*
         if (rc) return rc;
     }
     // dW[N x K] = dY^T . X  (A = dY stored [M x N] = [Ks x Mout], transposed), db fused
-    return weight_grad(dY, N, X, K, M, N, K, dW, dW, N, (float*)db, nullptr, dtype, flags, s);
+    return weight_grad(dY, N, X, K, M, N, K, dW, dW, N, (float*)db, nullptr, dtype, flags, s, ws,
+                       ws_bytes);
 }
 
 namespace gn {
@@ -573,10 +607,23 @@ int glu_bwd_to_gu(int kind, const void* dO, const void* gate, const void* up, vo
 // Projection part of the fused GLU backward, from the local gradients gu = [dGate | dUp]
 // ([M x 2H], row pitch 2H): dX = dGate Wg + dUp Wu (one GEMM over K = 2H), dWg and dWu from
 // one GEMM over the 2H rows of gu^T X (rows < H -> dWg, rows >= H -> dWu), bias sums.
+static int glu_proj_impl(const void* gu, const void* X, const void* Wg, const void* Wu,
+                         void* dX, void* dWg, void* dWu, void* dbg, void* dbu, int M, int K,
+                         int H, int dtype, unsigned flags, void* ws, size_t ws_bytes,
+                         void* stream);
+
 extern "C" int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, const void* Wu,
                                void* dX, void* dWg, void* dWu, void* dbg, void* dbu, int M, int K,
                                int H, int dtype, unsigned flags, void* stream) {
     clear_error();
+    return glu_proj_impl(gu, X, Wg, Wu, dX, dWg, dWu, dbg, dbu, M, K, H, dtype, flags, nullptr, 0,
+                         stream);
+}
+
+static int glu_proj_impl(const void* gu, const void* X, const void* Wg, const void* Wu,
+                         void* dX, void* dWg, void* dWu, void* dbg, void* dbu, int M, int K,
+                         int H, int dtype, unsigned flags, void* ws, size_t ws_bytes,
+                         void* stream) {
     GN_REQUIRE(M >= 0 && K >= 0 && H >= 0, "gn_glu_proj_bwd: negative size");
     GN_REQUIRE(gu && X && Wg && Wu && dWg && dWu, "gn_glu_proj_bwd: null pointer");
     GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_glu_proj_bwd: dtype %d", dtype);
@@ -604,16 +651,30 @@ extern "C" int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, co
         if (dbu && (rc = colsum_dispatch(g0 + (size_t)H * esz, (float*)dbu, M, H, dtype, flags, s, 2 * H,
                                          scr, (size_t)H * K)))
             return rc;
-        return weight_grad(g0, 2 * H, X, K, M, 2 * H, K, dWg, dWu, H, nullptr, nullptr, dtype, flags, s);
+        return weight_grad(g0, 2 * H, X, K, M, 2 * H, K, dWg, dWu, H, nullptr, nullptr, dtype, flags, s,
+                           ws, ws_bytes);
     }
     return weight_grad(g0, 2 * H, X, K, M, 2 * H, K, dWg, dWu, H, (float*)dbg, (float*)dbu, dtype,
-                       flags, s);
+                       flags, s, ws, ws_bytes);
 }
 
 extern "C" int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, const void* up,
                                  const void* X, const void* Wg, const void* Wu, void* dX,
                                  void* dWg, void* dWu, void* dbg, void* dbu, void* gu_ws, int M,
                                  int K, int H, int dtype, unsigned flags, void* stream) {
+    return gn_glu_linear_bwd_ws(kind, dO, gate, up, X, Wg, Wu, dX, dWg, dWu, dbg, dbu, gu_ws, M, K,
+                                H, dtype, flags, nullptr, 0, stream);
+}
+
+extern "C" size_t gn_glu_workspace_bytes(int M, int K, int H, int dtype) {
+    return weight_grad_ws_bytes(M, 2 * H, K, dtype);
+}
+
+extern "C" int gn_glu_linear_bwd_ws(int kind, const void* dO, const void* gate, const void* up,
+                                    const void* X, const void* Wg, const void* Wu, void* dX,
+                                    void* dWg, void* dWu, void* dbg, void* dbu, void* gu_ws,
+                                    int M, int K, int H, int dtype, unsigned flags, void* ws,
+                                    size_t ws_bytes, void* stream) {
     clear_error();
     GN_REQUIRE(M >= 0 && K >= 0 && H >= 0, "gn_glu_linear_bwd: negative size");
     GN_REQUIRE(dO && gate && up && X && Wg && Wu && dWg && dWu && gu_ws,
@@ -621,7 +682,8 @@ extern "C" int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, con
     GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_glu_linear_bwd: dtype %d", dtype);
     int rc = glu_bwd_to_gu(kind, dO, gate, up, gu_ws, M, H, dtype, as_stream(stream));
     if (rc) return rc;
-    return gn_glu_proj_bwd(gu_ws, X, Wg, Wu, dX, dWg, dWu, dbg, dbu, M, K, H, dtype, flags, stream);
+    return glu_proj_impl(gu_ws, X, Wg, Wu, dX, dWg, dWu, dbg, dbu, M, K, H, dtype, flags, ws,
+                         ws_bytes, stream);
 }
 
 // Down projection backward with the GLU local gradient fused into the dA epilogue:

@@ -44,6 +44,13 @@ struct GemmDesc {
     // column bias of the plain epilogue (a forward Linear's b): C[m][n] = acc + cbias[n],
     // bf16, LDS-DMA core only, no split-K; nullptr: none
     const bf16_t* cbias;
+    // split-K through a workspace (plain fp32 epilogue, ksplit >= 3): split y stores its
+    // partial tile at part + y*M*N (row-major, pitch N) and, with a bias, its row sums at
+    // part + ksplit*M*N + y*M; split_reduce then adds the splits in index order into C and
+    // the bias, so the result does not depend on which block finishes first.  part_cap: bytes
+    // available at part (0: no workspace; splits of two then add into C with atomics)
+    float* part;
+    size_t part_cap;
 };
 
 // Store one accumulated element (m, n) according to the descriptor's epilogue.
@@ -68,6 +75,9 @@ bool vsa_dma_applicable(const VsaDesc& v);
 int vsa_dma_launch(const VsaDesc& v, hipStream_t s);
 
 bool gemm_dma_applicable(const GemmDesc& g);
+// Workspace bytes the launch of g would use for its split-K partials if part_cap were
+// unbounded (0: none).
+size_t gemm_dma_part_bytes(const GemmDesc& g, int transA, int c_dtype);
 int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s);
 
 template <typename CT, int EPI>

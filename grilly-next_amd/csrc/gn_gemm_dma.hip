@@ -314,6 +314,61 @@ __global__ __launch_bounds__(256) void clear_c(GemmDesc g) {
     }
 }
 
+// Split-K through a workspace: the strip's rows go to this split's partial tile (plain
+// 16-byte stores, the layout of epilogue_rows; N % 8 == 0 on this core).
+template <int WN>
+__device__ __forceinline__ void epilogue_part(const GemmDesc& g, const float* st, int mbase,
+                                              int nbase, int lane) {
+    const int rr = lane >> 1;
+    const int m = mbase + rr;
+    if (m >= g.M) return;
+    float* P = g.part + (size_t)blockIdx.y * g.M * g.N + (size_t)m * g.N;
+#pragma unroll
+    for (int q = 0; q < WN / 16; ++q) {
+        const int c = (lane & 1) * (WN / 2) + q * 8;
+        const int n = nbase + c;
+        if (n >= g.N) continue;
+        const float4 lo = *reinterpret_cast<const float4*>(st + rr * (WN + 4) + c);
+        const float4 hi = *reinterpret_cast<const float4*>(st + rr * (WN + 4) + c + 4);
+        float4* p = reinterpret_cast<float4*>(P + n);
+        p[0] = lo;
+        p[1] = hi;
+    }
+}
+
+// C (+)= the sum over y = 0 .. ksplit-1 of the partial tiles, added in index order (one
+// thread per 4 columns of a row), rows below Msplit to C, the rest to C2; then the bias.
+__global__ __launch_bounds__(256) void split_reduce(GemmDesc g) {
+    const int n4 = g.N / 4;
+    const int64_t total = (int64_t)g.M * n4;
+    const size_t plane = (size_t)g.M * g.N;
+    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int m = (int)(i / n4), n = (int)(i % n4) * 4;
+        const float* src = g.part + (size_t)m * g.N + n;
+        float4 v = *reinterpret_cast<const float4*>(src);
+        for (int y = 1; y < g.ksplit; ++y) {
+            const float4 w = *reinterpret_cast<const float4*>(src + y * plane);
+            v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+        }
+        float4* c4 = reinterpret_cast<float4*>(reinterpret_cast<float*>(m < g.Msplit ? g.C : g.C2) +
+                                               (size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n);
+        if (g.accumulate) {
+            const float4 o = *c4;
+            v.x = o.x + v.x; v.y = o.y + v.y; v.z = o.z + v.z; v.w = o.w + v.w;
+        }
+        *c4 = v;
+    }
+    if (g.bias) {
+        const float* bp = g.part + (size_t)g.ksplit * plane;
+        for (int64_t m = blockIdx.x * (int64_t)256 + threadIdx.x; m < g.M; m += (int64_t)gridDim.x * 256) {
+            float v = bp[m];
+            for (int y = 1; y < g.ksplit; ++y) v += bp[(size_t)y * g.M + m];
+            float* dst = m < g.Msplit ? g.bias + m : g.bias2 + (m - g.Msplit);
+            *dst = g.accumulate ? *dst + v : v;
+        }
+    }
+}
+
 // ---- GEMM core -------------------------------------------------------------------------
 // Four waves (2 x 2, one per SIMD), wave tile (BM/2) x (BN/2), two or three LDS stages.  Every
 // MFMA operand is read from LDS two k-steps before its MFMAs run, into one of four register
@@ -374,9 +429,10 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
 
     const int kt0 = g.Ks[0] / BK;
     const int KTall = kt0 + (g.nseg > 1 ? g.Ks[1] / BK : 0);
-    const int half = KTall >> 1;
-    const int kt_lo = blockIdx.y ? half : 0;
-    const int KT = g.ksplit < 2 ? KTall : (blockIdx.y ? KTall - half : half);
+    // split y takes the k-tiles [y KTall / ksplit, (y + 1) KTall / ksplit)
+    const int nsplit = g.ksplit < 1 ? 1 : g.ksplit;
+    const int kt_lo = (int)(((int64_t)blockIdx.y * KTall) / nsplit);
+    const int KT = (int)(((int64_t)(blockIdx.y + 1) * KTall) / nsplit) - kt_lo;
     const int last = KT - 1;
     const bf16_t* const A0 = g.A[0];
     const bf16_t* const A1 = g.A[1];
@@ -543,7 +599,8 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
             const int m = m0 + wm * WM + i * 32 + lane;
             if (n0 == 0 && wn == 0 && lane < 32 && m < g.M) {
                 float* dst = m < g.Msplit ? g.bias + m : g.bias2 + (m - g.Msplit);
-                if (g.ksplit > 1) unsafeAtomicAdd(dst, v);
+                if (g.ksplit > 2) g.part[(size_t)g.ksplit * g.M * g.N + (size_t)blockIdx.y * g.M + m] = v;
+                else if (g.ksplit > 1) unsafeAtomicAdd(dst, v);
                 else *dst = g.accumulate ? *dst + v : v;
             }
         }
@@ -569,6 +626,10 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
             for (int r = 0; r < 16; ++r)
                 st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
         if constexpr (EPI == 0 && sizeof(CT) == 4) {
+            if (g.ksplit > 2) {
+                epilogue_part<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
+                return;
+            }
             if (g.ksplit > 1) {
                 epilogue_atomic<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
                 return;
@@ -828,7 +889,7 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
         return GN_E_HIP;
     }
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    if (g.ksplit > 1)
+    if (g.ksplit == 2)
         clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
     const dim3 grid(tiles, g.ksplit);
     if (bias && three)
@@ -839,6 +900,8 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
         hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>), grid, dim3(256), smem3, s, g);
     else
         hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2>), grid, dim3(256), smem2, s, g);
+    if (g.ksplit > 2)
+        split_reduce<<<grid_for((int64_t)g.M * (g.N / 4), 256, 4096), 256, 0, s>>>(g);
     GN_LAUNCH_CHECK("gemm (dma)");
     return GN_OK;
 }
@@ -852,14 +915,17 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
 //   epilogue     C tile bytes at ~40 KB/us per block (the GLU epilogue moves ~5x that);
 //   a last round that fills a fraction f of the 256 CUs costs (0.6 + 0.4 f) of a full round
 //                (the blocks of a part-filled round get more L2 / HBM bandwidth each);
-//   split-K (two halves, fp32 C only): clear + atomic adds, ~5 us + 0.7 us per MB of C.
+//   split-K (two halves, fp32 C only): clear + atomic adds, ~5 us + 0.7 us per MB of C;
+//   split-K over 3..8 ranges (fp32 C, workspace given): partial tiles stored, then one
+//   reduce pass reading every plane and writing C, ~4 us + bytes at 4 TB/s.
 struct TileChoice {
     int shape;  // index into kTileShapes
     int ksplit;
 };
 constexpr int kTileShapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
 
-inline double tile_cost(const GemmDesc& g, bool ta, size_t c_bytes, int epi, int i, int ks) {
+inline double tile_cost(const GemmDesc& g, bool ta, size_t c_bytes, int epi, int i, int ks,
+                        bool filled = false) {
     static constexpr double tk_kc[4] = {1.73, 0.98, 0.98, 0.57};
     static constexpr double tk_ta[4] = {1.60, 0.98, 0.90, 0.52};
     static constexpr double fixed[4] = {16.5, 6.4, 13.0, 6.4};
@@ -868,12 +934,21 @@ inline double tile_cost(const GemmDesc& g, bool ta, size_t c_bytes, int epi, int
     const long blocks = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * ks;
     const long full = blocks / 256;
     const double f = (double)(blocks % 256) / 256.0;
-    const double rounds = (double)full + (f > 0 ? 0.6 + 0.4 * f : 0.0);
+    // filled: a grid under one round costs a whole block time (the blocks are compute-bound),
+    // and the bias variant's k-tiles ~25 % more (measured on the decoder's weight gradients)
+    const double rounds = filled && full == 0 ? 1.0 : (double)full + (f > 0 ? 0.6 + 0.4 * f : 0.0);
     const double kt = (double)((KT + ks - 1) / ks);
     const double epi_us = (double)bm * bn * (double)c_bytes * (epi ? 5.0 : 1.0) / 40000.0;
-    double t = rounds * (kt * (ta ? tk_ta[i] : tk_kc[i]) + fixed[i] + epi_us);
-    if (ks > 1) t += 5.0 + 0.7e-6 * (double)g.M * g.N * 4.0;
+    const double tk = (ta ? tk_ta[i] : tk_kc[i]) * (filled && g.bias ? 1.25 : 1.0);
+    double t = rounds * (kt * tk + fixed[i] + epi_us);
+    if (ks == 2) t += 5.0 + 0.7e-6 * (double)g.M * g.N * 4.0;
+    if (ks > 2) t += 4.0 + (double)(ks + 1 + (g.accumulate ? 1 : 0)) * g.M * g.N * 4.0 / 4.0e6;
     return t;
+}
+
+// workspace bytes of a split over ks ranges into partial planes (ks >= 3)
+inline size_t part_bytes(const GemmDesc& g, int ks) {
+    return (size_t)ks * g.M * g.N * sizeof(float) + (g.bias ? (size_t)ks * g.M * sizeof(float) : 0);
 }
 
 inline TileChoice choose_tile(const GemmDesc& g, bool ta, size_t c_bytes, int epi) {
@@ -885,6 +960,24 @@ inline TileChoice choose_tile(const GemmDesc& g, bool ta, size_t c_bytes, int ep
         for (int ks = 1; ks <= (can_split ? 2 : 1); ++ks) {
             const double c = tile_cost(g, ta, c_bytes, epi, i, ks);
             if (c < bt) { bt = c; best = {i, ks}; }
+        }
+    }
+    // Partial planes (fp32 C, workspace given; the reduce adds onto C, so accumulation is
+    // allowed; each range >= 8 k-tiles) for a choice that leaves the GPU under one round:
+    // candidates and that choice compared with the filled-round costs.  Measured on MI355X
+    // (dW + db, 8192 rows): 768 x 768 50 -> 33 us (6 ranges), 768 x 3072 86 -> 72 us and
+    // 6144 x 768 127 -> 113 us (3 ranges); 2304 x 768 stays with two halves.
+    const bool can_part = epi == 0 && c_bytes == 4 && !g.cbias && g.part_cap > 0 && KT >= 48;
+    const long tiles = (long)((g.M + kTileShapes[best.shape][0] - 1) / kTileShapes[best.shape][0]) *
+                       ((g.N + kTileShapes[best.shape][1] - 1) / kTileShapes[best.shape][1]);
+    if (can_part && tiles * best.ksplit < 256) {
+        double bf = tile_cost(g, ta, c_bytes, epi, best.shape, best.ksplit, true);
+        for (int i = 0; i < 4; ++i) {
+            for (int ks : {3, 4, 6, 8}) {
+                if (KT / ks < 8 || part_bytes(g, ks) > g.part_cap) continue;
+                const double c = tile_cost(g, ta, c_bytes, epi, i, ks, true);
+                if (c < bf) { bf = c; best = {i, ks}; }
+            }
         }
     }
     return best;
@@ -951,6 +1044,14 @@ bool gemm_dma_applicable(const GemmDesc& g) {
         if (g.Ks[s] % BK || !al(g.A[s]) || !al(g.B[s]) || g.lda[s] % 8 || g.ldb[s] % 8) return false;
     }
     return true;
+}
+
+size_t gemm_dma_part_bytes(const GemmDesc& g0, int transA, int c_dtype) {
+    if (g0.epi != 0 || c_dtype != GN_F32) return 0;
+    GemmDesc g = g0;
+    g.part_cap = ~(size_t)0;
+    const TileChoice tc = choose_tile(g, transA != 0, sizeof(float), 0);
+    return tc.ksplit > 2 ? part_bytes(g, tc.ksplit) : 0;
 }
 
 int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s) {

@@ -81,6 +81,15 @@ uint64_t BackwardEngine::alloc_grad(size_t bytes) {
     return id;
 }
 
+uint64_t BackwardEngine::split_ws(size_t bytes) {
+    if (bytes == 0) return 0;
+    if (bytes > ws_bytes_) {
+        ws_id_ = alloc_grad(bytes);
+        ws_bytes_ = bytes;
+    }
+    return ws_id_;
+}
+
 void BackwardEngine::contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t numel, bool owned) {
     if (id == 0 || g == 0) return;
     GradEntry* e = find_or_insert(id);
@@ -127,6 +136,8 @@ const void* BackwardEngine::gout(Node* n) const {
 
 void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_output_buffer) {
     stats_ = {};
+    ws_id_ = 0;
+    ws_bytes_ = 0;
     if (!loss_node) throw std::invalid_argument("backward: loss node is None");
     // autograd.cpp:30-31: 0 means "the loss computes its own gradient" (sentinel 1)
     loss_node->grad_output_buffer = grad_output_buffer ? grad_output_buffer : 1ULL;
@@ -205,8 +216,10 @@ void BackwardEngine::bwd_linear(Node* n) {
     uint64_t dX = x.requires_grad ? alloc_grad(x.size_bytes()) : 0;
     uint64_t dW = alloc_grad((size_t)N * K * 4);
     uint64_t db = b ? alloc_grad((size_t)N * 4) : 0;
-    gn_call(gn_linear_bwd(gout(n), P(x.buffer_id), P(W), P(dX), P(dW), P(db), M, N, K, dt, 0,
-                          dev_.stream()), "Linear backward");
+    const size_t wsb = gn_linear_workspace_bytes(M, N, K, dt);
+    const uint64_t ws = split_ws(wsb);
+    gn_call(gn_linear_bwd_ws(gout(n), P(x.buffer_id), P(W), P(dX), P(dW), P(db), M, N, K, dt, 0,
+                             P(ws), wsb, dev_.stream()), "Linear backward");
     stats_.shaders_dispatched += db ? 3 : 2;
     n->grad_input_buffers[0] = dX;
     contribute(W, dW, 0, (size_t)N * K, true);
@@ -427,9 +440,12 @@ void BackwardEngine::bwd_fused_glu(Node* n) {
     uint64_t dWg = alloc_grad((size_t)H * K * 4), dWu = alloc_grad((size_t)H * K * 4);
     uint64_t dbg = bg ? alloc_grad((size_t)H * 4) : 0, dbu = bu ? alloc_grad((size_t)H * 4) : 0;
     uint64_t gu = alloc_grad((size_t)2 * M * H * es);
-    gn_call(gn_glu_linear_bwd((int)params_of<FusedGLUParams>(n).kind, gout(n), P(s[2]), P(s[3]),
-                              P(x.buffer_id), P(s[0]), P(s[1]), P(dX), P(dWg), P(dWu), P(dbg), P(dbu),
-                              P(gu), M, K, H, dt, 0, dev_.stream()), "FusedGLU backward");
+    const size_t wsb = gn_glu_workspace_bytes(M, K, H, dt);
+    const uint64_t ws = split_ws(wsb);
+    gn_call(gn_glu_linear_bwd_ws((int)params_of<FusedGLUParams>(n).kind, gout(n), P(s[2]), P(s[3]),
+                                 P(x.buffer_id), P(s[0]), P(s[1]), P(dX), P(dWg), P(dWu), P(dbg),
+                                 P(dbu), P(gu), M, K, H, dt, 0, P(ws), wsb, dev_.stream()),
+            "FusedGLU backward");
     stats_.shaders_dispatched += 4;
     n->grad_input_buffers[0] = dX;
     contribute(s[0], dWg, 0, (size_t)H * K, true);

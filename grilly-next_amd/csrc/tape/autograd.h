@@ -164,6 +164,9 @@ private:
     GradEntry* find(uint64_t id) const;
     GradEntry* find_or_insert(uint64_t id);
     uint64_t alloc_grad(size_t bytes);
+    // split-K scratch shared by the handlers of one backward pass (every launch is ordered
+    // on the engine's stream, so each node may reuse it); grown on demand, 0 bytes -> 0
+    uint64_t split_ws(size_t bytes);
     const void* gout(Node* n) const;
 
     void bwd_linear(Node* n);
@@ -191,6 +194,8 @@ private:
     Device& dev_;
     Stats stats_{};
     uint32_t borrowed_ = 0;  // inputs whose gradient is the upstream buffer itself
+    uint64_t ws_id_ = 0;     // split-K scratch of the current pass (owned by backward_bufs_)
+    size_t ws_bytes_ = 0;
     std::vector<uint64_t> backward_bufs_;
     mutable std::vector<GradEntry> table_;
     uint32_t count_ = 0;

@@ -24,8 +24,9 @@ ROPE = {"none": 0, "interleaved": 1, "half": 2}
 
 # exported symbols, in the order include/gn_bwd.h declares them
 SYMBOLS = [
-    "gn_last_error", "gn_version", "gn_linear_bwd", "gn_gemm", "gn_colsum", "gn_act_bwd",
-    "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
+    "gn_last_error", "gn_version", "gn_linear_bwd", "gn_linear_bwd_ws", "gn_linear_workspace_bytes",
+    "gn_gemm", "gn_colsum", "gn_act_bwd", "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_linear_bwd_ws",
+    "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd", "gn_binary_bwd",
@@ -63,12 +64,17 @@ _SIGS = {
     "gn_last_error": ([], ctypes.c_char_p),
     "gn_version": ([], ctypes.c_char_p),
     "gn_linear_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
+    "gn_linear_bwd_ws": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P, _Z, _P], _I),
+    "gn_linear_workspace_bytes": ([_I, _I, _I, _I], _Z),
     "gn_gemm": ([_P, _P, _I, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _U, _P], _I),
     "gn_colsum": ([_P, _P, _I, _I, _I, _U, _P], _I),
     "gn_act_bwd": ([_I, _P, _P, _P, _L, _I, _U, _P], _I),
     "gn_glu_bwd": ([_I, _P, _P, _P, _P, _P, _L, _I, _P], _I),
     "gn_glu_linear_bwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                            _U, _P], _I),
+    "gn_glu_linear_bwd_ws": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                              _U, _P, _Z, _P], _I),
+    "gn_glu_workspace_bytes": ([_I, _I, _I, _I], _Z),
     "gn_glu_proj_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_ffn_down_glu_bwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_layernorm_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P, _Z, _P], _I),
@@ -166,8 +172,18 @@ def workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-def linear_bwd(dY, X, W, need_dx=True, need_db=True, dX=None, dW=None, db=None, accumulate=False):
-    """(dX, dW, db) for y = X W^T + b.  bf16 inputs give bf16 dX and fp32 dW, db."""
+def linear_workspace_bytes(M, N, K, dtype):
+    return int(lib().gn_linear_workspace_bytes(M, N, K, dtype))
+
+
+def glu_workspace_bytes(M, K, H, dtype):
+    return int(lib().gn_glu_workspace_bytes(M, K, H, dtype))
+
+
+def linear_bwd(dY, X, W, need_dx=True, need_db=True, dX=None, dW=None, db=None, accumulate=False,
+               ws=None):
+    """(dX, dW, db) for y = X W^T + b.  bf16 inputs give bf16 dX and fp32 dW, db.  ws: the
+    split-K workspace (allocated here when None and the shape uses one; False: none)."""
     M, N = dY.shape
     K = X.shape[1]
     dt = _dt(dY)
@@ -177,9 +193,14 @@ def linear_bwd(dY, X, W, need_dx=True, need_db=True, dX=None, dW=None, db=None, 
         dW = torch.empty((N, K), dtype=torch.float32, device=dY.device)
     if need_db and db is None:
         db = torch.empty((N,), dtype=torch.float32, device=dY.device)
-    _check(lib().gn_linear_bwd(_ptr(dY), _ptr(X), _ptr(W), _ptr(dX) if need_dx else None,
-                               _ptr(dW), _ptr(db) if need_db else None, M, N, K, dt,
-                               ACCUMULATE if accumulate else 0, _stream()), "gn_linear_bwd")
+    if ws is None:
+        nb = linear_workspace_bytes(M, N, K, dt)
+        ws = workspace(nb, dY.device) if nb else False
+    wsp, wsb = (None, 0) if ws is False else (_ptr(ws), ws.numel() * ws.element_size())
+    _check(lib().gn_linear_bwd_ws(_ptr(dY), _ptr(X), _ptr(W), _ptr(dX) if need_dx else None,
+                                  _ptr(dW), _ptr(db) if need_db else None, M, N, K, dt,
+                                  ACCUMULATE if accumulate else 0, wsp, wsb, _stream()),
+           "gn_linear_bwd_ws")
     return (dX if need_dx else None), dW, (db if need_db else None)
 
 
@@ -226,8 +247,9 @@ def glu_bwd(kind, dO, gate, up, dGate=None, dUp=None):
     return dGate, dUp
 
 
-def glu_linear_bwd(kind, dO, gate, up, X, Wg, Wu, need_dx=True, need_db=False, gu_ws=None):
-    """Fused GLU-projection backward: (dX, dWg, dWu, dbg, dbu)."""
+def glu_linear_bwd(kind, dO, gate, up, X, Wg, Wu, need_dx=True, need_db=False, gu_ws=None,
+                   ws=None):
+    """Fused GLU-projection backward: (dX, dWg, dWu, dbg, dbu); ws as in linear_bwd."""
     M, H = dO.shape
     K = X.shape[1]
     dev = dO.device
@@ -238,10 +260,14 @@ def glu_linear_bwd(kind, dO, gate, up, X, Wg, Wu, need_dx=True, need_db=False, g
     dbu = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
     if gu_ws is None:
         gu_ws = torch.empty((M, 2 * H), dtype=dO.dtype, device=dev)
-    _check(lib().gn_glu_linear_bwd(GLU[kind], _ptr(dO), _ptr(gate), _ptr(up), _ptr(X), _ptr(Wg),
-                                   _ptr(Wu), _ptr(dX), _ptr(dWg), _ptr(dWu), _ptr(dbg),
-                                   _ptr(dbu), _ptr(gu_ws), M, K, H, _dt(dO), 0, _stream()),
-           "gn_glu_linear_bwd")
+    if ws is None:
+        nb = glu_workspace_bytes(M, K, H, _dt(dO))
+        ws = workspace(nb, dev) if nb else False
+    wsp, wsb = (None, 0) if ws is False else (_ptr(ws), ws.numel() * ws.element_size())
+    _check(lib().gn_glu_linear_bwd_ws(GLU[kind], _ptr(dO), _ptr(gate), _ptr(up), _ptr(X), _ptr(Wg),
+                                      _ptr(Wu), _ptr(dX), _ptr(dWg), _ptr(dWu), _ptr(dbg),
+                                      _ptr(dbu), _ptr(gu_ws), M, K, H, _dt(dO), 0, wsp, wsb,
+                                      _stream()), "gn_glu_linear_bwd_ws")
     return dX, dWg, dWu, dbg, dbu
 
 

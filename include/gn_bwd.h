@@ -87,6 +87,18 @@ const char* gn_version(void);
 int gn_linear_bwd(const void* dY, const void* X, const void* W, void* dX, void* dW, void* db,
                   int M, int N, int K, int dtype, unsigned flags, void* stream);
 
+/* gn_linear_bwd with a workspace for the weight gradient's split-K partials (same
+ * reference interface: BackwardEngine::backward_linear, autograd.cpp:172-305).  With
+ * gn_linear_workspace_bytes(M, N, K, dtype) bytes (16-byte aligned) a weight gradient whose
+ * few output tiles would leave most CUs idle is split over 3..8 ranges of the M rows; each
+ * range stores its partial tile and one reduce pass adds them in a fixed order, so the result
+ * does not depend on scheduling.  ws may be NULL or shorter (the split then stays within it);
+ * 0 bytes means the shape does not use one. */
+int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, void* dX, void* dW, void* db,
+                     int M, int N, int K, int dtype, unsigned flags, void* ws, size_t ws_bytes,
+                     void* stream);
+size_t gn_linear_workspace_bytes(int M, int N, int K, int dtype);
+
 /* Plain GEMM entry used by the linear handler and exported for tests/benchmarks:
  *   C[M x N] (+)= sum_s op(A_s) op(B_s), with up to two K-segments s (the second may be NULL).
  *   transA = 0: A_s is [M x Ks] row-major;  transA = 1: A_s is stored [Ks x M] (i.e. A_s^T).
@@ -125,6 +137,14 @@ int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, const void* up
                       const void* X, const void* Wg, const void* Wu, void* dX, void* dWg,
                       void* dWu, void* dbg, void* dbu, void* gu_ws, int M, int K, int H,
                       int dtype, unsigned flags, void* stream);
+
+/* gn_glu_linear_bwd with a workspace for the dWg / dWu GEMM's split-K partials, sized by
+ * gn_glu_workspace_bytes(M, K, H, dtype); semantics as gn_linear_bwd_ws. */
+int gn_glu_linear_bwd_ws(int kind, const void* dO, const void* gate, const void* up,
+                         const void* X, const void* Wg, const void* Wu, void* dX, void* dWg,
+                         void* dWu, void* dbg, void* dbu, void* gu_ws, int M, int K, int H,
+                         int dtype, unsigned flags, void* ws, size_t ws_bytes, void* stream);
+size_t gn_glu_workspace_bytes(int M, int K, int H, int dtype);
 
 /* The projection half of gn_glu_linear_bwd, starting from gu = [dGate | dUp] ([M x 2H])
  * already computed (e.g. by gn_ffn_down_glu_bwd). Same outputs as gn_glu_linear_bwd. */

@@ -140,6 +140,31 @@ def test_linear_split_k_weight_gradient(gn, M, N, K):
     assert torch.equal(dW1, dW2)
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 768, 768), (8192, 768, 3072), (8192, 2304, 768)])
+def test_linear_split_k_workspace(gn, M, N, K):
+    """The decoder's under-filled weight gradients (O-proj, FFN down, QKV shapes) with the
+    split-K workspace: partial planes reduced in a fixed order.  Against the oracle, bit-
+    identical reruns, accumulation (which may take another split: two-way atomics need a
+    cleared C), and without a workspace."""
+    r = rng_(16)
+    dY = rnd((r.standard_normal((M, N)) * 0.01).astype(np.float32))
+    X = rnd(r.standard_normal((M, K)).astype(np.float32))
+    W = rnd((r.standard_normal((N, K)) * 0.02).astype(np.float32))
+    if (M, N, K) == (8192, 768, 768):
+        assert gn.linear_workspace_bytes(M, N, K, 4) > 0  # this shape takes the split
+    tdY, tX, tW = dev(dY, torch.bfloat16), dev(X, torch.bfloat16), dev(W, torch.bfloat16)
+    _, dW1, db1 = gn.linear_bwd(tdY, tX, tW, need_dx=False)
+    _, dW2, db2 = gn.linear_bwd(tdY, tX, tW, need_dx=False)
+    _, rW, rb = oracle.linear_bwd(dY, X, W, need_dx=False)
+    assert rel_err(host(dW1), rW) < FP32_TOL and rel_err(host(db1), rb) < FP32_TOL
+    assert torch.equal(dW1, dW2) and torch.equal(db1, db2)
+    dWa, dba = dW1.clone(), db1.clone()
+    gn.linear_bwd(tdY, tX, tW, need_dx=False, dW=dWa, db=dba, accumulate=True)
+    assert rel_err(host(dWa), 2 * rW) < FP32_TOL and rel_err(host(dba), 2 * rb) < FP32_TOL
+    _, dW0, db0 = gn.linear_bwd(tdY, tX, tW, need_dx=False, ws=False)  # no workspace
+    assert rel_err(host(dW0), rW) < FP32_TOL and rel_err(host(db0), rb) < FP32_TOL
+
+
 def test_linear_wide_tile_bias_sums(gn):
     """The decoder's gate/up weight-gradient shape (8192 rows, 6144 x 768) takes the 128 x 256
     tile, whose fused bias sums run on the VALU (narrower tiles use v_dot2): dW against an fp32
