@@ -316,14 +316,42 @@ def bench_mlp(args, torch, gn):
         tape.end()
     ms = timed(torch, step, args.steps, args.warmup)
     flops = 2.0 * Bsz * (784 * 256 + 256 * 10 + 256 * 10)
+    cpu = None
+    if not args.no_cpu:
+        h = lambda a: a.cpu().numpy()
+        cpu = mlp_cpu_baseline(h(X), h(y), h(W1), h(W2), h(Z), h(Hh), h(L))
     return line("MLP tape backward step time (784-256-10, B=64, fp32)", round(ms * 1e3, 2), "us",
                 args, ms, "f32",
                 {"workload": "C1 MLP 784->256->10 fp32 B=64: CE, 2x linear, ReLU bwd via the tape",
                  "batch": Bsz},
                 {"kernel": "whole step (launch-bound)", "bound": "latency",
                  "achieved": round(flops / (ms * 1e-3) / 1e12, 4), "peak": 157.3, "unit": "TFLOP/s",
-                 "frac": round(flops / (ms * 1e-3) / 1e12 / 157.3, 6), "traffic": None}, None,
+                 "frac": round(flops / (ms * 1e-3) / 1e12 / 157.3, 6), "traffic": None}, cpu,
                 higher=False)
+
+
+def mlp_cpu_baseline(X, y, W1, W2, Z, H, L):
+    """The same C1 backward (CE with scale 1, Linear 2 with dX, ReLU, Linear 1 without dX) on
+    the oracle (C, OpenMP), timed on this host: median of 200 steps after 20 warm-up steps."""
+    import oracle
+
+    def step():
+        dL = oracle.xent_bwd(L, y, 1.0)
+        dH, _, _ = oracle.linear_bwd(dL, H, W2)
+        dZ = oracle.act_bwd("relu", dH, Z)
+        oracle.linear_bwd(dZ, X, W1, need_dx=False)
+
+    for _ in range(20):
+        step()
+    ts = []
+    for _ in range(200):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    us = float(np.median(ts)) * 1e6
+    return {"value": round(us, 2), "unit": "us", "cores": oracle.num_threads(), "kind": "port",
+            "sample": "the whole B=64 step (oracle C/OpenMP, fp64 accumulation), median of 200 "
+                      "after 20 warm-up steps"}
 
 
 def bench_decoder(args, torch, gn):
