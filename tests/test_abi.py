@@ -53,6 +53,17 @@ def test_python_frontend_lists_every_symbol():
     assert lib.gn_norm_workspace_bytes(100, 64) == 2 * 13 * 64 * 4
     assert lib.gn_attn_workspace_bytes(4, 16, 2048, 128) > 0
     assert lib.gn_attn_workspace_bytes(0, 16, 2048, 128) == 0
+    # split-K partial planes: ks fp32 planes of dW [N x K] plus ks bias rows, ks in 3..8,
+    # only for bf16 weight gradients that leave the GPU under one round of tiles
+    BF16, F32 = 4, 0
+    plane = 768 * 768 * 4 + 768 * 4
+    o_proj = lib.gn_linear_workspace_bytes(8192, 768, 768, BF16)
+    assert o_proj in [ks * plane for ks in (3, 4, 6, 8)]
+    assert lib.gn_linear_workspace_bytes(8192, 768, 768, F32) == 0
+    assert lib.gn_linear_workspace_bytes(64, 256, 784, BF16) == 0  # short reduction: no split
+    assert lib.gn_linear_workspace_bytes(8192, 32000, 768, BF16) == 0  # LM head: many tiles
+    glu = lib.gn_glu_workspace_bytes(8192, 768, 3072, BF16)
+    assert glu in [ks * (6144 * 768 * 4 + 6144 * 4) for ks in (3, 4, 6, 8)]
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
