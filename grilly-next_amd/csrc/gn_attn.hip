@@ -1010,7 +1010,12 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
                   float scale, int causal, int rope_mode, float theta, void* ws, size_t ws_bytes,
                   hipStream_t s) {
     const int64_t BH = (int64_t)B * H, rows = BH * S, BHSD = rows * D;
-    const bool mfma_ok = sizeof(T) == 2 && (D == 64 || D == 128);
+    // the MFMA kernels move 16-byte chunks (LDS DMA, vector stores) from and to every tensor
+    // and the workspace: an offset view takes the SIMT kernels instead
+    const void* ptrs[9] = {Q, K, V, O, dO, dQ, dK, dV, ws};
+    bool al16 = true;
+    for (const void* p : ptrs) al16 = al16 && ((reinterpret_cast<uintptr_t>(p) & 15u) == 0);
+    const bool mfma_ok = sizeof(T) == 2 && (D == 64 || D == 128) && al16;
     AttnWs w;
     const size_t need = ws_layout(BH, S, D, sizeof(T), mfma_ok, ws, &w);
     if (!ws || ws_bytes < need) {

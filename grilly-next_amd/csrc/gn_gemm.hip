@@ -465,20 +465,29 @@ int weight_grad(const void* dY, int ldy, const void* X, int ldx, int M, int N, i
     return gemm_run(d, 1, 0, dtype, GN_F32, s);
 }
 
-// Workspace bytes for the split-K partials of weight_grad's GEMM (dW [N x Kin] over M rows,
-// bias sums included), as the launch would choose them with an unbounded workspace.
+// Workspace bytes for the split-K partials of weight_grad's GEMM (dW [N x Kin] over M rows),
+// as the launch would choose them with an unbounded workspace: the largest over the four
+// launches a caller can make (with or without a bias, overwrite or GN_ACCUMULATE; an
+// accumulating launch cannot take the two-way atomic split and may want planes instead).
 size_t weight_grad_ws_bytes(int M, int N, int Kin, int dtype) {
     if (dtype != GN_BF16 || M <= 0 || N <= 0 || Kin <= 0) return 0;
-    GemmDesc d{};
     const bf16_t* al = reinterpret_cast<const bf16_t*>((uintptr_t)256);  // aligned stand-in
     float* alf = reinterpret_cast<float*>((uintptr_t)256);
-    d.nseg = 1;
-    d.A[0] = al; d.lda[0] = N; d.Ks[0] = M;
-    d.B[0] = al; d.ldb[0] = Kin;
-    d.M = N; d.N = Kin; d.C = alf; d.C2 = alf; d.Msplit = N; d.ldc = Kin;
-    d.bias = alf; d.bias2 = alf;
-    if (!gemm_dma_applicable(d)) return 0;
-    return gemm_dma_part_bytes(d, 1, GN_F32);
+    size_t best = 0;
+    for (int has_bias = 0; has_bias < 2; ++has_bias)
+        for (int acc = 0; acc < 2; ++acc) {
+            GemmDesc d{};
+            d.nseg = 1;
+            d.A[0] = al; d.lda[0] = N; d.Ks[0] = M;
+            d.B[0] = al; d.ldb[0] = Kin;
+            d.M = N; d.N = Kin; d.C = alf; d.C2 = alf; d.Msplit = N; d.ldc = Kin;
+            d.bias = has_bias ? alf : nullptr;
+            d.bias2 = has_bias ? alf : nullptr;
+            d.accumulate = acc;
+            if (!gemm_dma_applicable(d)) continue;
+            best = std::max(best, gemm_dma_part_bytes(d, 1, GN_F32));
+        }
+    return best;
 }
 
 // Plain-argument form used by the C entry points.

@@ -98,8 +98,9 @@ void BackwardEngine::contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t 
         *e = GradEntry{id, g, bytes, dtype, owned};
         return;
     }
-    if (e->grad_id == g) return;  // same buffer recorded twice
-    // fan-out: the second consumer's gradient is added (autograd.cpp:78-86 drops it)
+    // fan-out: the second consumer's gradient is added (autograd.cpp:78-86 drops it).  The
+    // same buffer arriving twice is two contributions too (Add(x, x), x + Reshape(x): both
+    // borrow the upstream buffer), so it is summed like any other pair.
     if (e->dtype != dtype || e->grad_bytes != bytes)
         throw std::runtime_error("BackwardEngine: fan-out gradients disagree in dtype or size");
     if (!e->owned && owned) {
@@ -125,6 +126,24 @@ void BackwardEngine::contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t 
                            dev_.stream()), "fan-out add");
     stats_.fanout_accumulations++;
     stats_.shaders_dispatched++;
+}
+
+// A node whose output lives in one of its input buffers (an in-place op or a view such as
+// Reshape onto the same buffer) shares that buffer id between the two versions of the tensor.
+bool BackwardEngine::writes_in_place(const Node* n, uint64_t id) {
+    for (uint32_t o = 0; o < n->num_outputs && o < kMaxNodeIO; ++o)
+        if (n->outputs[o].buffer_id == id) return true;
+    return false;
+}
+
+// The gradient of the input version of an in-place tensor: the table entry under its id held
+// the gradient of the output version (already summed over that version's consumers, which
+// come later on the tape and were visited first); from here on the entry is the earlier
+// version's gradient, which the earlier consumers visited next add onto.
+void BackwardEngine::replace(uint64_t id, uint64_t g, uint32_t dtype, size_t numel, bool owned) {
+    if (id == 0 || g == 0) return;
+    GradEntry* e = find_or_insert(id);
+    *e = GradEntry{id, g, numel * TensorRef::elem_size(dtype), dtype, owned};
 }
 
 const void* BackwardEngine::gout(Node* n) const {
@@ -160,8 +179,11 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
         for (uint32_t i = 0; i < cur->num_inputs && i < kMaxNodeIO; ++i) {
             const TensorRef& in = cur->inputs[i];
             if (!in.requires_grad || cur->grad_input_buffers[i] == 0) continue;
-            contribute(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(),
-                       !((borrowed_ >> i) & 1u));
+            const bool own = !((borrowed_ >> i) & 1u);
+            if (writes_in_place(cur, in.buffer_id))
+                replace(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(), own);
+            else
+                contribute(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(), own);
         }
     }
 }

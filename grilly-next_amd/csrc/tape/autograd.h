@@ -161,6 +161,9 @@ private:
     void dispatch(Node* n);
     // record gradient `g` (dtype, numel) for tensor `id`, summing on fan-out
     void contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t numel, bool owned);
+    // record `g` as the gradient of the input version of an in-place tensor (overwrites)
+    void replace(uint64_t id, uint64_t g, uint32_t dtype, size_t numel, bool owned);
+    static bool writes_in_place(const Node* n, uint64_t id);
     GradEntry* find(uint64_t id) const;
     GradEntry* find_or_insert(uint64_t id);
     uint64_t alloc_grad(size_t bytes);

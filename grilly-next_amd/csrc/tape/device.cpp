@@ -57,7 +57,9 @@ uint64_t Device::acquire(size_t bytes) {
         void* p = nullptr;
         hipError_t e = hipMalloc(&p, b);
         if (e != hipSuccess) {
-            // give cached blocks back and retry once
+            // clear the failed call's sticky error so the next launch check does not report
+            // it, then give cached blocks back and retry once
+            (void)hipGetLastError();
             for (auto& kv : free_) hipFree(reinterpret_cast<void*>(kv.second));
             free_.clear();
             stats_.bytes_cached = 0;

@@ -93,7 +93,8 @@ int gn_linear_bwd(const void* dY, const void* X, const void* W, void* dX, void* 
  * few output tiles would leave most CUs idle is split over 3..8 ranges of the M rows; each
  * range stores its partial tile and one reduce pass adds them in a fixed order, so the result
  * does not depend on scheduling.  ws may be NULL or shorter (the split then stays within it);
- * 0 bytes means the shape does not use one. */
+ * the query returns the largest size over the four launches of a shape (with or without db,
+ * overwrite or GN_ACCUMULATE), and 0 bytes means none of them uses one. */
 int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, void* dX, void* dW, void* db,
                      int M, int N, int K, int dtype, unsigned flags, void* ws, size_t ws_bytes,
                      void* stream);

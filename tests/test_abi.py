@@ -77,3 +77,29 @@ def test_invalid_arguments_rejected_without_gpu():
     assert lib.gn_vsa_unpack_project_bwd(None, None, None, None, 8, 8, 100, 4, 0, 0, None, 0, None) == -1
     assert lib.gn_attn_bwd(None, None, None, None, None, None, None, None, None, 1, 1, 8, 300,
                            1.0, 1, 1, 1e4, 4, None, 0, None) == -1
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_workspace_query_covers_accumulating_launches():
+    # QKV weight gradient (2304 x 768 over 8192 rows): the overwriting launch splits in two
+    # atomic halves (no workspace), an accumulating one cannot and takes partial planes; the
+    # query must size for the latter
+    import gn_bwd
+    lib = gn_bwd.lib()
+    plane = 2304 * 768 * 4 + 2304 * 4
+    assert lib.gn_linear_workspace_bytes(8192, 2304, 768, 4) in [ks * plane for ks in (3, 4, 6, 8)]
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_misaligned_attention_views_rejected_without_gpu():
+    # the [B,S,H,D] entry takes only 16-byte aligned tensors (its kernels move 16-byte
+    # chunks); the check runs before any HIP call, so it is safe without a device
+    import gn_bwd
+    lib = gn_bwd.lib()
+    base = 1 << 20
+    p = lambda off=0: ctypes.c_void_p(base + off)
+    args = lambda dq_off: (p(0), p(256), p(512), p(4096), p(8192), p(12288), p(dq_off), p(256),
+                           p(512), 1, 2, 64, 64, 384, 128, 384, 0.125, 1, 0, 1e4, 4, p(1 << 16),
+                           1 << 24, None)
+    assert lib.gn_attn_bwd_bshd(*args(2)) == -1
+    assert "16-byte aligned" in gn_bwd.last_error()

@@ -403,6 +403,32 @@ def test_attention_bf16_mfma(gn, S, D, causal, rope):
     assert rel_err(host(dK), rK) < BF16_TOL
 
 
+def test_attention_bf16_offset_views(gn):
+    """Views that start one bf16 element into their storage are not 16-byte aligned: the MFMA
+    kernels (16-byte LDS DMA and stores) must not see them; the SIMT path gives the answer."""
+    r = rng_(13)
+    B, H, S, D = 1, 2, 96, 64
+    Q, K, V = (rnd(r.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    dO = rnd((r.standard_normal((B, H, S, D)) * 0.01).astype(np.float32))
+    O, LSE = oracle.attn_fwd(Q, K, V, causal=True, rope_mode="interleaved")
+    O = rnd(O)
+    rQ, rK, rV = oracle.attn_bwd(Q, K, V, dO, LSE, causal=True, rope_mode="interleaved")
+
+    def off(x):
+        flat = torch.zeros(x.size + 1, dtype=torch.bfloat16, device="cuda")
+        v = flat[1:].view(B, H, S, D)
+        v.copy_(dev(x, torch.bfloat16))
+        return v
+
+    outs = tuple(off(np.zeros_like(Q)) for _ in range(3))
+    dQ, dK, dV = gn.attn_bwd(off(Q), off(K), off(V), off(O), off(dO), dev(LSE), causal=True,
+                             rope="interleaved", out=outs)
+    assert all(t.data_ptr() % 16 == 2 for t in (dQ, dK, dV))
+    assert rel_err(host(dV), rV) < BF16_TOL
+    assert rel_err(host(dQ), rQ) < BF16_TOL
+    assert rel_err(host(dK), rK) < BF16_TOL
+
+
 @pytest.mark.parametrize("S,D,rope", [(200, 64, "none"), (256, 128, "interleaved"), (96, 64, "half")])
 def test_attention_fused_qkv_layout(gn, S, D, rope):
     """[B,S,H,D] rows of a fused QKV buffer in, dQKV in the same layout out; equals the

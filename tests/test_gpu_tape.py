@@ -175,6 +175,54 @@ def test_fanout_is_accumulated(env):
     tape.end()
 
 
+def test_same_buffer_contributions_are_summed(env):
+    """Add(x, x) and x + Reshape(x): each input borrows the one upstream buffer, so the same
+    buffer reaches x twice; both arrivals count (dx = 2 g), checked against float64."""
+    gc, gb, dev = env
+    r = np.random.default_rng(31)
+    x = T(r.standard_normal((8, 16)))
+    W = T(r.standard_normal((16, 16)) * 0.1)
+    z = (x + x).contiguous()
+    u = (z @ W.t()).contiguous()
+    dU = T(r.standard_normal((8, 16)))
+    tape = gb.create_tape_context(dev)
+    tape.begin()
+    tape.record_op(gc.OpType.Add, [gb.tref(x, True), gb.tref(x, True)], [gb.tref(z)])
+    n = tape.record_op(gc.OpType.Linear, [gb.tref(z, True)], [gb.tref(u)])
+    tape.save_for_backward(n, [W.data_ptr(), 0])
+    tape.backward(n, dU.data_ptr())
+    g = dU.double().cpu().numpy() @ W.double().cpu().numpy()
+    assert rel_err(grad(gb, dev, tape, x), 2 * g) < 1e-6
+    tape.end()
+
+    # x + Reshape(x), the view in its own buffer: x gets g (through Add) + g (through Reshape)
+    v = x.clone().reshape(16, 8).contiguous()  # separate buffer, same elements
+    z2 = (x + v.reshape(8, 16)).contiguous()
+    u2 = (z2 @ W.t()).contiguous()
+    tape.begin()
+    tape.record_op(gc.OpType.Reshape, [gb.tref(x, True)], [gb.tref(v, True)])
+    vr = gb.make_tensor_ref(v.data_ptr(), (8, 16), gb.DTYPE_F32, True)
+    tape.record_op(gc.OpType.Add, [gb.tref(x, True), vr], [gb.tref(z2)])
+    n = tape.record_op(gc.OpType.Linear, [gb.tref(z2, True)], [gb.tref(u2)])
+    tape.save_for_backward(n, [W.data_ptr(), 0])
+    tape.backward(n, dU.data_ptr())
+    assert rel_err(grad(gb, dev, tape, x), 2 * g) < 1e-6
+    tape.end()
+
+    # an in-place view (Reshape onto x's own buffer) is one tensor, not a fan-out: dx = g + g
+    # only through the Add, the view adds nothing of its own
+    tape.begin()
+    xr = gb.make_tensor_ref(x.data_ptr(), (16, 8), gb.DTYPE_F32, True)
+    tape.record_op(gc.OpType.Reshape, [gb.tref(x, True)], [xr])
+    xv = gb.make_tensor_ref(x.data_ptr(), (8, 16), gb.DTYPE_F32, True)
+    tape.record_op(gc.OpType.Add, [xv, xv], [gb.tref(z)])
+    n = tape.record_op(gc.OpType.Linear, [gb.tref(z, True)], [gb.tref(u)])
+    tape.save_for_backward(n, [W.data_ptr(), 0])
+    tape.backward(n, dU.data_ptr())
+    assert rel_err(grad(gb, dev, tape, x), 2 * g) < 1e-6
+    tape.end()
+
+
 def test_attention_and_layernorm_nodes(env):
     gc, gb, dev = env
     r = np.random.default_rng(4)
