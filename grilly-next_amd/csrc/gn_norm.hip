@@ -7,6 +7,8 @@
 // workspace, and summed by a small deterministic finish kernel (no atomics).
 #include "gn_common.h"
 
+#include <mutex>
+
 namespace gn {
 namespace {
 
@@ -466,6 +468,42 @@ __global__ __launch_bounds__(256) void xent_bwd_rows_bf16(const bf16_t* __restri
 }
 
 }  // namespace
+
+// ---- scratch of gn_layernorm_bwd_noalloc --------------------------------------------------
+// The row kernel's partial parameter-gradient rows: 2 planes x at most kNormGrid blocks x
+// F <= 2048 floats (wider or unaligned rows take the generic kernels, which need none) =
+// 4 MiB per device, held until the process ends.  Every call on one device shares it.
+constexpr size_t kNoAllocScratchBytes = (size_t)2 * kNormGrid * 2048 * sizeof(float);
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device (each
+// GPU holds its own copy of the array at its own address; the array's name in host code is
+// not a device address).
+void* scratch_on_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("gn_layernorm_bwd_noalloc: no current HIP device (or index >= %d)", kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("gn_layernorm_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                      dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
 }  // namespace gn
 
 using namespace gn;
@@ -494,6 +532,31 @@ extern "C" int gn_layernorm_bwd(const void* dY, const void* X, const void* gamma
                                    acc, ws, ws_bytes, as_stream(stream));
     set_error("gn_layernorm_bwd: dtype %d not supported", dtype);
     return GN_E_INVALID;
+}
+
+extern "C" int gn_layernorm_bwd_noalloc(const void* dY, const void* X, const void* gamma,
+                                        const float* mean, const float* rstd, void* dX,
+                                        float* dGamma, float* dBeta, int rows, int F, float eps,
+                                        int dtype, unsigned flags, void* stream) {
+    clear_error();
+    GN_REQUIRE(rows >= 0 && F > 0, "gn_layernorm_bwd_noalloc: bad shape rows=%d F=%d", rows, F);
+    if (rows == 0) return GN_OK;
+    GN_REQUIRE(dY && X && gamma && mean && rstd && dX, "gn_layernorm_bwd_noalloc: null pointer");
+    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_layernorm_bwd_noalloc: dtype %d not supported",
+               dtype);
+    void* ws = scratch_on_current_device();
+    if (!ws) return GN_E_HIP;
+    const bool acc = flags & GN_ACCUMULATE;
+    const int sv = (flags & GN_LN_STAT_VAR) ? 1 : 0;
+    const int rc = dtype == GN_F32
+        ? norm_bwd<0, float>(dY, X, gamma, mean, rstd, dX, dGamma, dBeta, rows, F, eps, sv, acc,
+                             ws, kNoAllocScratchBytes, as_stream(stream))
+        : norm_bwd<0, bf16_t>(dY, X, gamma, mean, rstd, dX, dGamma, dBeta, rows, F, eps, sv, acc,
+                              ws, kNoAllocScratchBytes, as_stream(stream));
+    if (rc == GN_E_WORKSPACE)
+        set_error("gn_layernorm_bwd_noalloc: rows=%d F=%d need more than the %zu B static scratch",
+                  rows, F, kNoAllocScratchBytes);
+    return rc;
 }
 
 extern "C" int gn_rmsnorm_bwd(const void* dY, const void* X, const void* w, const float* rstd,

@@ -26,7 +26,8 @@ ROPE = {"none": 0, "interleaved": 1, "half": 2}
 SYMBOLS = [
     "gn_last_error", "gn_version", "gn_linear_bwd", "gn_linear_bwd_ws", "gn_linear_workspace_bytes",
     "gn_gemm", "gn_colsum", "gn_act_bwd", "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_linear_bwd_ws",
-    "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd", "gn_rmsnorm_bwd",
+    "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd",
+    "gn_layernorm_bwd_noalloc", "gn_rmsnorm_bwd",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd", "gn_binary_bwd",
@@ -78,6 +79,7 @@ _SIGS = {
     "gn_glu_proj_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_ffn_down_glu_bwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_layernorm_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P, _Z, _P], _I),
+    "gn_layernorm_bwd_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P], _I),
     "gn_rmsnorm_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _U, _P, _Z, _P], _I),
     "gn_norm_workspace_bytes": ([_I, _I], _Z),
     "gn_softmax_bwd": ([_P, _P, _P, _I, _I, _I, _P], _I),

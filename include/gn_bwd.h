@@ -172,6 +172,17 @@ int gn_layernorm_bwd(const void* dY, const void* X, const void* gamma, const flo
                      int F, float eps, int dtype, unsigned flags, void* ws, size_t ws_bytes,
                      void* stream);
 
+/* gn_layernorm_bwd without a workspace argument, for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It has no
+ * counterpart in the reference.  The partial parameter-gradient rows go to a static device
+ * array of the library (4 MiB per GPU, held until the process ends; every row shape fits:
+ * F <= 2048 uses at most 2 x 256 x F floats, wider rows need none).  The call allocates
+ * nothing and computes exactly what gn_layernorm_bwd computes.  All calls on one GPU share
+ * that array: calls that overlap on one GPU (e.g. on two streams at once) race. */
+int gn_layernorm_bwd_noalloc(const void* dY, const void* X, const void* gamma, const float* mean,
+                             const float* rstd, void* dX, float* dGamma, float* dBeta, int rows,
+                             int F, float eps, int dtype, unsigned flags, void* stream);
+
 /* RMSNorm backward (no handler in the reference, autograd.cpp:126-128; forward
  * rms-norm.glsl:34-70): y = x * r * w with r = rsqrt(mean(x^2)+eps) given as rstd [rows].
  *   dx = r*w*dy - x * r^3 * mean_j(w_j dy_j x_j);  dw = sum_rows dy * x * r. */
