@@ -23,8 +23,9 @@ ARCH = os.environ.get("GN_OFFLOAD_ARCH", "gfx950")
 
 KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip", "gn_gemm_dma.hip",
                   "gn_vsa.hip", "gn_attn.hip", "gn_optim.hip", "gn_tapeops.hip", "gn_fwd.hip",
-                  "gn_probe.hip"]
-TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "tape/checkpoint.cpp", "bindings.cpp"]
+                  "gn_probe.hip", "gn_skinny.hip", "gn_vsa_fwd.hip"]
+TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "tape/checkpoint.cpp", "tape/hypernet.cpp",
+                "bindings.cpp"]
 
 # -packed-fp32-ops off: packed fp32 VALU forms are kept out of the generated code.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INCLUDE, "-I", CSRC,

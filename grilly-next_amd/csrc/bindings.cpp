@@ -11,6 +11,7 @@
 #include "checkpoint.h"
 #include "device.h"
 #include "gn_bwd.h"
+#include "hypernet.h"
 
 namespace py = pybind11;
 using namespace grilly;
@@ -287,6 +288,190 @@ PYBIND11_MODULE(_grilly_core, m) {
         }
         return with_opt ? py::object(from_opt(h)) : py::none();
     }, py::arg("path"), py::arg("dims"), py::arg("weights"), py::arg("with_opt"), py::arg("states"));
+
+    // ---- VSA hypernetwork, its optimizer and the training step (bindings.cpp:2883-3286) ----
+    using models::SurpriseMomentumOptimizer;
+    using models::VSAHypernetwork;
+    using U32Arr = py::array_t<uint32_t, py::array::c_style | py::array::forcecast>;
+    // rows x words of a bitpacked array: [words] is one row, [rows, words] a batch
+    auto rows_words = [](const U32Arr& a) {
+        if (a.ndim() == 1) return std::make_pair<uint32_t, uint32_t>(1, (uint32_t)a.shape(0));
+        if (a.ndim() == 2) return std::make_pair((uint32_t)a.shape(0), (uint32_t)a.shape(1));
+        throw py::value_error("bitpacked state: a uint32 array [words] or [rows, words] expected");
+    };
+    py::class_<VSAHypernetwork>(m, "VSAHypernetwork")
+        .def(py::init<Device&, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>(), py::arg("device"),
+             py::arg("d_model") = 768, py::arg("vsa_dim") = 10240, py::arg("K") = 16,
+             py::arg("router_hidden") = 32, py::arg("seed") = 42, py::keep_alive<1, 2>())
+        .def("forward", &VSAHypernetwork::forward, py::arg("tape"), py::arg("vsa_state"))
+        .def("parameter_buffer_ids", &VSAHypernetwork::parameter_buffer_ids)
+        .def("parameter_sizes", &VSAHypernetwork::parameter_sizes)
+        .def("last_output_buffer_id", [](const VSAHypernetwork& h) { return h.last_output().buffer_id; })
+        .def("h_t_buffer_id", [](const VSAHypernetwork& h) { return h.h_t().buffer_id; })
+        .def_property_readonly("d_model", &VSAHypernetwork::d_model)
+        .def_property_readonly("vsa_dim", &VSAHypernetwork::vsa_dim)
+        .def_property_readonly("K", &VSAHypernetwork::K)
+        .def_property_readonly("router_hidden", &VSAHypernetwork::router_hidden)
+        .def("num_weight_bufs", &VSAHypernetwork::num_weight_bufs)
+        .def_readwrite("gumbel_seed", &VSAHypernetwork::gumbel_seed,
+                       "seed of the surrogate loss's Gumbel noise (default: the model seed)")
+        .def_readwrite("gumbel_counter", &VSAHypernetwork::gumbel_counter,
+                       "draw index of the next loss forward; advances once per training step")
+        .def("forward_inference",
+             [rows_words](VSAHypernetwork& self, Device& dev, TapeContext& tape, const U32Arr& state) {
+                 const auto rw = rows_words(state);
+                 if (rw.first != 1) throw py::value_error("forward_inference: one state [words] expected");
+                 py::array_t<float> out({(py::ssize_t)self.K(), (py::ssize_t)self.vsa_dim()});
+                 {
+                     py::gil_scoped_release nogil;
+                     tape.begin();
+                     try {
+                         TensorRef s = models::upload_bitpacked(tape, state.data(), 1, rw.second);
+                         TensorRef p = self.forward(tape, s);
+                         dev.download(p.buffer_id, out.mutable_data(), (size_t)self.K() * self.vsa_dim() * 4);
+                     } catch (...) {
+                         tape.end();
+                         throw;
+                     }
+                     tape.end();
+                 }
+                 return out;
+             },
+             py::arg("device"), py::arg("tape"), py::arg("vsa_state"),
+             "Inference forward: upload the bitpacked state, run the network, return the K x vsa_dim "
+             "float32 predictions");
+
+    py::class_<SurpriseMomentumOptimizer>(m, "SurpriseMomentumOptimizer")
+        .def(py::init<Device&, const VSAHypernetwork&, float, float, float>(), py::arg("device"),
+             py::arg("model"), py::arg("lr") = 0.001f, py::arg("alpha") = 0.9f, py::arg("clip") = 1.0f,
+             py::keep_alive<1, 2>(), py::keep_alive<1, 3>())
+        .def_readwrite("eta_base", &SurpriseMomentumOptimizer::eta_base)
+        .def_readwrite("alpha_momentum", &SurpriseMomentumOptimizer::alpha_momentum)
+        .def_readwrite("lambda_recall", &SurpriseMomentumOptimizer::lambda_recall)
+        .def_readwrite("surprise_floor", &SurpriseMomentumOptimizer::surprise_floor)
+        .def_readwrite("weight_decay", &SurpriseMomentumOptimizer::weight_decay)
+        .def_readwrite("clip_max", &SurpriseMomentumOptimizer::clip_max)
+        .def_readwrite("steps", &SurpriseMomentumOptimizer::steps)
+        .def("apply", &SurpriseMomentumOptimizer::apply, py::arg("tape"),
+             "Update every parameter whose gradient the tape holds (between backward and end)")
+        .def("s_bar_buffer_ids", &SurpriseMomentumOptimizer::s_bar_buffer_ids);
+
+    m.def("upload_bitpacked",
+          [rows_words](TapeContext& tape, const U32Arr& a) {
+              const auto rw = rows_words(a);
+              return models::upload_bitpacked(tape, a.data(), rw.first, rw.second);
+          },
+          py::arg("tape"), py::arg("data"), "Step-scoped u32 buffer holding the bitpacked rows");
+    m.def("record_surrogate_loss", &models::record_surrogate_loss, py::arg("tape"), py::arg("predicted"),
+          py::arg("true_delta"), py::return_value_policy::reference);
+    m.def("vsa_loss_forward",
+          [](TapeContext& tape, Node* node, uint64_t seed, uint64_t counter, bool noise) {
+              py::gil_scoped_release nogil;
+              return models::vsa_loss_forward(tape, node, seed, counter, noise);
+          },
+          py::arg("tape"), py::arg("loss_node"), py::arg("seed"), py::arg("counter"), py::arg("noise") = true);
+    m.def("vsa_training_step",
+          [rows_words](Device& dev, TapeContext& tape, VSAHypernetwork& model, const U32Arr& state,
+                       const U32Arr& delta, py::object optimizer) {
+              const auto rw = rows_words(state), rd = rows_words(delta);
+              if (rw != rd) throw py::value_error("vsa_training_step: state and true_delta shapes differ");
+              if (&dev != &model.device())
+                  throw py::value_error("vsa_training_step: the model lives on another Device");
+              SurpriseMomentumOptimizer* opt =
+                  optimizer.is_none() ? nullptr : &optimizer.cast<SurpriseMomentumOptimizer&>();
+              py::gil_scoped_release nogil;
+              return models::vsa_training_step(tape, model, state.data(), delta.data(), rw.first,
+                                               rw.second, opt);
+          },
+          py::arg("device"), py::arg("tape"), py::arg("model"), py::arg("vsa_state"),
+          py::arg("true_delta"), py::arg("optimizer") = py::none(),
+          "Run one VSA training step: forward + loss + backward + optimizer. Returns the loss.");
+
+    // GRLY v3 checkpoint of a VSAHypernetwork (bindings.cpp:2965-3039); with a
+    // SurpriseMomentumOptimizer its s_bar follows in this build's optimizer section
+    auto model_dims = [](const VSAHypernetwork& h) {
+        ckpt::HyperDims d;
+        d.d_model = h.d_model(); d.vsa_dim = h.vsa_dim(); d.K = h.K(); d.router_hidden = h.router_hidden();
+        return d;
+    };
+    auto dev_tensors = [](const std::vector<uint64_t>& ids, const std::vector<uint64_t>& sizes) {
+        std::vector<ckpt::DevTensor> v;
+        for (size_t i = 0; i < ids.size(); ++i) v.push_back({ids[i], sizes[i], 0});
+        return v;
+    };
+    auto opt_header = [](const SurpriseMomentumOptimizer& o) {
+        ckpt::OptHeader h;
+        h.kind = 0;
+        h.n_states = 1;
+        h.step = o.steps;
+        h.hyper = {o.eta_base, o.alpha_momentum, o.lambda_recall, o.surprise_floor, o.weight_decay, o.clip_max};
+        return h;
+    };
+    m.def("save_hypernetwork_weights",
+          [model_dims, dev_tensors, opt_header](VSAHypernetwork& model, const std::string& path,
+                                                py::object optimizer) {
+              const auto sizes = model.parameter_sizes();
+              const auto w = dev_tensors(model.parameter_buffer_ids(), sizes);
+              if (optimizer.is_none()) {
+                  py::gil_scoped_release nogil;
+                  ckpt::save_hyper_device(path, model_dims(model), w, nullptr, {});
+                  return;
+              }
+              auto& o = optimizer.cast<SurpriseMomentumOptimizer&>();
+              const ckpt::OptHeader h = opt_header(o);
+              const auto st = dev_tensors(o.s_bar_buffer_ids(), sizes);
+              py::gil_scoped_release nogil;
+              ckpt::save_hyper_device(path, model_dims(model), w, &h, st);
+          },
+          py::arg("model"), py::arg("path"), py::arg("optimizer") = py::none(),
+          "Save VSAHypernetwork weights (GRLY v3); with an optimizer, also its state");
+    m.def("load_hypernetwork_weights",
+          [model_dims, dev_tensors](VSAHypernetwork& model, const std::string& path, py::object optimizer) {
+              const auto sizes = model.parameter_sizes();
+              const auto w = dev_tensors(model.parameter_buffer_ids(), sizes);
+              if (optimizer.is_none()) {
+                  py::gil_scoped_release nogil;
+                  ckpt::load_hyper_device(path, model_dims(model), w, nullptr, {});
+                  return;
+              }
+              auto& o = optimizer.cast<SurpriseMomentumOptimizer&>();
+              ckpt::HyperDims pd;
+              ckpt::OptHeader info;
+              if (!ckpt::probe_hyper(path, &pd, &info) || info.kind != 0 || info.n_states < 1 ||
+                  info.n_states > 2)
+                  throw py::value_error(path + ": no SurpriseMomentumOptimizer state in this checkpoint");
+              // a second state per parameter (the update `delta`) is read and dropped
+              std::vector<ckpt::DevTensor> st;
+              std::vector<uint64_t> scratch;
+              Device& dev = model.device();
+              const auto sb = o.s_bar_buffer_ids();
+              for (size_t i = 0; i < sizes.size(); ++i) {
+                  st.push_back({sb[i], sizes[i], 0});
+                  if (info.n_states == 2) {
+                      scratch.push_back(dev.acquire(sizes[i] * 4));
+                      st.push_back({scratch.back(), sizes[i], 0});
+                  }
+              }
+              ckpt::OptHeader h;
+              {
+                  py::gil_scoped_release nogil;
+                  try {
+                      ckpt::load_hyper_device(path, model_dims(model), w, &h, st);
+                  } catch (...) {
+                      for (uint64_t id : scratch) dev.release(id);
+                      throw;
+                  }
+                  dev.synchronize();
+              }
+              for (uint64_t id : scratch) dev.release(id);
+              o.steps = h.step;
+              if (h.hyper.size() >= 6) {
+                  o.eta_base = h.hyper[0]; o.alpha_momentum = h.hyper[1]; o.lambda_recall = h.hyper[2];
+                  o.surprise_floor = h.hyper[3]; o.weight_decay = h.hyper[4]; o.clip_max = h.hyper[5];
+              }
+          },
+          py::arg("model"), py::arg("path"), py::arg("optimizer") = py::none(),
+          "Load VSAHypernetwork weights (checks magic, dimensions and every tensor's count)");
 
     py::register_exception_translator([](std::exception_ptr p) {
         try {

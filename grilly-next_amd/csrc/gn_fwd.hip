@@ -194,6 +194,41 @@ int glu_fwd(int kind, const void* gate, const void* up, void* out, int64_t n, in
                : launch_glu_fwd<float, false>(kind, gate, up, out, n, s);
 }
 
+// Y = act(X) elementwise (activation-{relu,gelu,silu,tanh,sigmoid}.glsl forward values).
+template <int KIND>
+__device__ __forceinline__ float act_val(float x) {
+    if constexpr (KIND == GN_ACT_RELU) return x > 0.f ? x : 0.f;
+    else if constexpr (KIND == GN_ACT_GELU_TANH) return gelu_tanh_f(x);
+    else if constexpr (KIND == GN_ACT_GELU_ERF) return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+    else if constexpr (KIND == GN_ACT_SILU) return silu_f(x);
+    else if constexpr (KIND == GN_ACT_TANH) return tanhf_(x);
+    else return sigmoidf_(x);
+}
+
+template <int KIND, typename T>
+__global__ __launch_bounds__(256) void act_fwd_kernel(const T* __restrict__ X, T* __restrict__ Y,
+                                                      int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        io<T>::st(Y, i, act_val<KIND>(io<T>::ld(X, i)));
+}
+
+template <typename T>
+int act_fwd(int kind, const void* X, void* Y, int64_t n, hipStream_t s) {
+    const unsigned g = grid_for(n, 256, 16384);
+    const T* x = (const T*)X;
+    T* y = (T*)Y;
+    switch (kind) {
+        case GN_ACT_RELU: act_fwd_kernel<GN_ACT_RELU, T><<<g, 256, 0, s>>>(x, y, n); break;
+        case GN_ACT_GELU_TANH: act_fwd_kernel<GN_ACT_GELU_TANH, T><<<g, 256, 0, s>>>(x, y, n); break;
+        case GN_ACT_GELU_ERF: act_fwd_kernel<GN_ACT_GELU_ERF, T><<<g, 256, 0, s>>>(x, y, n); break;
+        case GN_ACT_SILU: act_fwd_kernel<GN_ACT_SILU, T><<<g, 256, 0, s>>>(x, y, n); break;
+        case GN_ACT_TANH: act_fwd_kernel<GN_ACT_TANH, T><<<g, 256, 0, s>>>(x, y, n); break;
+        default: act_fwd_kernel<GN_ACT_SIGMOID, T><<<g, 256, 0, s>>>(x, y, n); break;
+    }
+    GN_LAUNCH_CHECK("gn_act_fwd");
+    return GN_OK;
+}
+
 // Y[m][n] = b[n] (or 0): the starting value of a GEMM that then accumulates X W^T.
 template <typename T>
 __global__ __launch_bounds__(256) void fill_rows(const T* __restrict__ b, T* __restrict__ Y,
@@ -208,6 +243,9 @@ __global__ __launch_bounds__(256) void fill_rows(const T* __restrict__ b, T* __r
 // accumulate.
 int linear_fwd(const void* X, const void* W, const void* b, void* Y, int M, int N, int K,
                int dtype, hipStream_t s) {
+    if (dtype == GN_F32 && skinny_fwd_applicable(X, W, Y, M, K))
+        return skinny_linear_fwd((const float*)X, (const float*)W, (const float*)b, (float*)Y, M, N,
+                                 K, s);
     GemmDesc d{};
     d.nseg = 1;
     d.A[0] = (const bf16_t*)X; d.lda[0] = K; d.Ks[0] = K;
@@ -301,4 +339,15 @@ extern "C" int gn_glu_linear_fwd(int kind, const void* X, const void* Wg, const 
     if (rc == GN_OK) rc = linear_fwd(X, Wu, bu, up, M, H, K, dtype, s);
     if (rc == GN_OK) rc = glu_fwd(kind, gate, up, out, (int64_t)M * H, dtype, s);
     return rc;
+}
+
+extern "C" int gn_act_fwd(int kind, const void* X, void* Y, int64_t n, int dtype, void* stream) {
+    clear_error();
+    GN_REQUIRE(n >= 0, "gn_act_fwd: negative size");
+    GN_REQUIRE(kind >= GN_ACT_RELU && kind <= GN_ACT_SIGMOID, "gn_act_fwd: kind %d", kind);
+    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_act_fwd: dtype %d (f32, bf16)", dtype);
+    if (n == 0) return GN_OK;
+    GN_REQUIRE(X && Y, "gn_act_fwd: null pointer");
+    if (dtype == GN_BF16) return act_fwd<bf16_t>(kind, X, Y, n, as_stream(stream));
+    return act_fwd<float>(kind, X, Y, n, as_stream(stream));
 }

@@ -585,6 +585,7 @@ extern "C" int gn_linear_bwd(const void* dY, const void* X, const void* W, void*
 }
 
 extern "C" size_t gn_linear_workspace_bytes(int M, int N, int K, int dtype) {
+    if (dtype == GN_F32) return skinny_bwd_ws_bytes(M, N, K);
     return weight_grad_ws_bytes(M, N, K, dtype);
 }
 
@@ -598,6 +599,10 @@ extern "C" int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, vo
     GN_REQUIRE(dY && X && W && dW, "gn_linear_bwd: null pointer (dY, X, W, dW are required)");
     GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_linear_bwd: dtype %d", dtype);
     hipStream_t s = as_stream(stream);
+    if (dtype == GN_F32 && M > 0 && N > 0 && skinny_bwd_applicable(dY, X, W, dX, dW, M, K))
+        return skinny_linear_bwd((const float*)dY, (const float*)X, (const float*)W, (float*)dX,
+                                 (float*)dW, (float*)db, M, N, K, flags & GN_ACCUMULATE, ws,
+                                 ws_bytes, s);
     int rc;
     if (dX) {  // dX[M x K] = dY[M x N] . W[N x K]
         rc = gemm_dispatch(dY, W, N, nullptr, nullptr, 0, dX, M, K, 0, 0, dtype, dtype, flags, s);

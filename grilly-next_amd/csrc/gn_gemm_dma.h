@@ -146,6 +146,17 @@ __device__ __forceinline__ void gemm_store_tile(const GemmDesc& g, int m0, int n
     }
 }
 
+// fp32 Linear on a handful of rows (M <= 8; gn_skinny.hip): HBM-bound passes over W.
+bool skinny_fwd_applicable(const void* X, const void* W, const void* Y, int M, int K);
+bool skinny_bwd_applicable(const void* dY, const void* X, const void* W, const void* dX,
+                           const void* dW, int M, int K);
+size_t skinny_bwd_ws_bytes(int M, int N, int K);
+int skinny_linear_fwd(const float* X, const float* W, const float* b, float* Y, int M, int N,
+                      int K, hipStream_t s);
+int skinny_linear_bwd(const float* dY, const float* X, const float* W, float* dX, float* dW,
+                      float* db, int M, int N, int K, bool accumulate, void* ws, size_t ws_bytes,
+                      hipStream_t s);
+
 // Run C (+)= sum_s op(A_s) op(B_s) described by `d`: the LDS-DMA kernel when the shape
 // allows it, else the register-staged MFMA kernel, else the SIMT kernel.
 int gemm_run(const GemmDesc& d, int transA, int transB, int dtype, int c_dtype, hipStream_t s);

@@ -17,7 +17,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libgn_bwd.so")
 
 F32, F16, U32, I32, BF16 = 0, 1, 2, 3, 4
-ACCUMULATE, LN_STAT_VAR = 1, 2
+ACCUMULATE, LN_STAT_VAR, NO_GUMBEL = 1, 2, 4
 ACT = {"relu": 0, "gelu_tanh": 1, "gelu_erf": 2, "silu": 3, "tanh": 4, "sigmoid": 5}
 GLU = {"swiglu_up": 0, "swiglu_gate": 1, "geglu_up": 2, "geglu_gate": 3, "reglu_up": 4}
 ROPE = {"none": 0, "interleaved": 1, "half": 2}
@@ -30,10 +30,11 @@ SYMBOLS = [
     "gn_layernorm_bwd_noalloc", "gn_rmsnorm_bwd",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
-    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_embedding_bwd", "gn_binary_bwd",
+    "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_vsa_unpack_project_fwd",
+    "gn_vsa_fwd_workspace_bytes", "gn_vsa_surrogate_fwd", "gn_embedding_bwd", "gn_binary_bwd",
     "gn_reduce_bwd", "gn_transpose_bwd", "gn_mse_bwd", "gn_vsa_lora_expand_bwd",
     "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_layernorm_fwd",
-    "gn_rmsnorm_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace",
+    "gn_rmsnorm_fwd", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace",
 ]
 BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
 RED = {"sum": 0, "mean": 1}
@@ -93,6 +94,11 @@ _SIGS = {
     "gn_vsa_unpack_project_bwd": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _U, _P, _Z, _P], _I),
     "gn_vsa_workspace_bytes": ([_I, _I], _Z),
     "gn_vsa_surrogate_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F, _U, _P], _I),
+    "gn_vsa_unpack_project_fwd": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _Z, _P], _I),
+    "gn_vsa_fwd_workspace_bytes": ([_I, _I, _I], _Z),
+    "gn_vsa_surrogate_fwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F,
+                              ctypes.c_uint64, ctypes.c_uint64, _U, _P], _I),
+    "gn_act_fwd": ([_I, _P, _P, _L, _I, _P], _I),
     "gn_embedding_bwd": ([_P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_binary_bwd": ([_I, _P, _P, _P, _P, _P, _L, _I, _U, _P], _I),
     "gn_reduce_bwd": ([_I, _P, _P, _L, _L, _I, _U, _P], _I),
@@ -239,6 +245,12 @@ def act_bwd(kind, dY, X, dX=None, accumulate=False):
     _check(lib().gn_act_bwd(ACT[kind], _ptr(dY), _ptr(X), _ptr(dX), dY.numel(), _dt(dY),
                             ACCUMULATE if accumulate else 0, _stream()), "gn_act_bwd")
     return dX
+
+
+def act_fwd(kind, X, out=None):
+    Y = torch.empty_like(X) if out is None else out
+    _check(lib().gn_act_fwd(ACT[kind], _ptr(X), _ptr(Y), X.numel(), _dt(X), _stream()), "gn_act_fwd")
+    return Y
 
 
 def glu_bwd(kind, dO, gate, up, dGate=None, dUp=None):
@@ -439,6 +451,43 @@ def vsa_surrogate_bwd(preds, bits, results, weights, gamma=1.0, delta=1.0, lambd
                                       scale, ACCUMULATE if accumulate else 0, _stream()),
            "gn_vsa_surrogate_bwd")
     return dPreds
+
+
+def vsa_fwd_workspace_bytes(Bn, O, D):
+    return int(lib().gn_vsa_fwd_workspace_bytes(Bn, O, D))
+
+
+def vsa_unpack_project_fwd(bits, W, bias=None, ws=None):
+    """Y [Bn, O] = unpack(bits) W^T + bias (fp32).  ws: the MFMA path's operand workspace
+    (allocated here when None and the batch uses one; False: the streaming kernel only)."""
+    Bn, words = bits.shape
+    O, D = W.shape
+    Y = torch.empty((Bn, O), dtype=torch.float32, device=W.device)
+    if ws is None:
+        nb = vsa_fwd_workspace_bytes(Bn, O, D)
+        ws = workspace(nb, W.device) if nb else False
+    wsp, wsb = (None, 0) if ws is False else (_ptr(ws), ws.numel())
+    _check(lib().gn_vsa_unpack_project_fwd(_ptr(bits), _ptr(W), _ptr(bias), _ptr(Y), Bn, O, D,
+                                           words, wsp, wsb, _stream()), "gn_vsa_unpack_project_fwd")
+    return Y
+
+
+def vsa_surrogate_fwd(preds, bits, gamma=1.0, delta=1.0, lambda_c=0.3, temperature=1.0, seed=0,
+                      counter=0, noise=True):
+    """(dots [Bn,K], results u32 [Bn,4] as int32 storage, weights [Bn,K], loss [Bn])."""
+    Bn, K, D = preds.shape
+    words = bits.shape[1]
+    dev = preds.device
+    dots = torch.empty((Bn, K), dtype=torch.float32, device=dev)
+    results = torch.empty((Bn, 4), dtype=torch.int32, device=dev)
+    weights = torch.empty((Bn, K), dtype=torch.float32, device=dev)
+    loss = torch.empty((Bn,), dtype=torch.float32, device=dev)
+    _check(lib().gn_vsa_surrogate_fwd(_ptr(preds), _ptr(bits), _ptr(dots), _ptr(results),
+                                      _ptr(weights), _ptr(loss), Bn, K, D, words, gamma, delta,
+                                      lambda_c, temperature, seed, counter,
+                                      0 if noise else NO_GUMBEL, _stream()),
+           "gn_vsa_surrogate_fwd")
+    return dots, results, weights, loss
 
 
 def embedding_bwd(dX, ids, V, dE=None, accumulate=False):

@@ -49,6 +49,7 @@ extern "C" {
 /* ---- flags ------------------------------------------------------------------------ */
 #define GN_ACCUMULATE 1u  /* add into existing gradients (fan-out) instead of overwriting */
 #define GN_LN_STAT_VAR 2u /* layernorm: `rstd` argument holds the biased variance */
+#define GN_NO_GUMBEL 4u   /* surrogate forward: top-2 of the plain dot products (no noise) */
 
 /* ---- activation kinds (gn_act_bwd) ------------------------------------------------- */
 #define GN_ACT_RELU 0      /* dx = dy*[x>0]            activation-relu-backward.glsl:33-37 */
@@ -268,6 +269,39 @@ int gn_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32_
                          float gamma, float delta, float lambda_c, float scale, unsigned flags,
                          void* stream);
 
+/* VSA unpack-project forward (vsa-unpack-project.glsl:40-74; dispatch_vsa_unpack_project_forward,
+ * vsa_loss_node.cpp:476-514): Y[b, o] = sum_j s_b(j) W[o, j] + bias[o], s_b(j) as in the
+ * backward above.  Xbits [Bn x words] u32, W fp32 [O x D] (16-byte aligned), bias fp32 [O] or
+ * NULL, Y fp32 [Bn x O]; D a multiple of 32, words = D/32.  Up to 8 rows per pass stream W
+ * once (HBM-bound); with more rows and gn_vsa_fwd_workspace_bytes(Bn, O, D) bytes of ws
+ * (16-byte aligned; Bn, O multiples of 8, D of 64) the contraction runs on the matrix cores
+ * (+-1 exact in bf16, W as two bf16 terms: fp32 accuracy); otherwise one streaming pass per 8
+ * rows. */
+int gn_vsa_unpack_project_fwd(const uint32_t* Xbits, const float* W, const float* bias, float* Y,
+                              int Bn, int O, int D, int words, void* ws, size_t ws_bytes,
+                              void* stream);
+size_t gn_vsa_fwd_workspace_bytes(int Bn, int O, int D);
+
+/* VSA surrogate-loss forward (vsa-surrogate-loss-forward.glsl passes 0 and 1 and the top-2 /
+ * softmax of dispatch_vsa_loss_forward, vsa_loss_node.cpp:36-180), per row b of preds fp32
+ * [Bn x K x D] against the bipolar target bits [Bn x words]:
+ *   dots[b, k] = sum_i preds[b, k, i] y_i                                   fp32 [Bn x K]
+ *   win, run   = top-2 of dots[b, k] + temperature * g(seed, counter, b, k) (strict >, lower
+ *                index kept on ties), g a standard Gumbel sample from a counter-based generator
+ *                (splitmix64 of seed + ((counter * Bn + b) * K + k + 1) * 0x9E3779B97F4A7C15;
+ *                u = (top 23 bits + 1/2) / 2^23; g = -log(-log u)); GN_NO_GUMBEL: g = 0
+ *   results[b] = {win, run, f32bits(dots[b, win]), f32bits(dots[b, run])}  u32 [Bn x 4]
+ *   weights[b] = softmax(dots[b, :] / temperature)                          fp32 [Bn x K]
+ *   loss[b]    = mean_i max(gamma - y_i preds[b, win, i], 0)
+ *                + lambda_c * max(0, delta - (dots[b, win] - dots[b, run]))  fp32 [Bn]
+ * results and weights are the saved slots gn_vsa_surrogate_bwd reads.  K <= 64; D multiple
+ * of 32; preds 16-byte aligned.  The reference draws the noise from an unseeded host RNG
+ * (vsa_loss_node.cpp:9-14); here it is reproducible from (seed, counter). */
+int gn_vsa_surrogate_fwd(const float* preds, const uint32_t* bits, float* dots, uint32_t* results,
+                         float* weights, float* loss, int Bn, int K, int D, int words, float gamma,
+                         float delta, float lambda_c, float temperature, uint64_t seed,
+                         uint64_t counter, unsigned flags, void* stream);
+
 /* ---- embedding ------------------------------------------------------------------------- */
 /* Backward of a row gather X[t] = E[ids[t]] (token embeddings, tied with the LM head in the
  * decoder workload).  The reference tape has no embedding op; this entry serves the
@@ -372,6 +406,11 @@ int gn_layernorm_fwd(const void* X, const void* gamma, const void* beta, void* Y
  * (the reference saves mean(X^2); the backward here takes rstd).  w NULL: 1. */
 int gn_rmsnorm_fwd(const void* X, const void* w, void* Y, float* rstd, int rows, int F, float eps,
                    int dtype, void* stream);
+
+/* Activation forward Y = act(X) over n elements (activation-{relu,gelu,silu}.glsl forward
+ * values; the GN_ACT_* kinds: tanh-form GELU by default, erf form, SiLU, tanh, sigmoid).  The
+ * backward of GN_ACT_TANH / GN_ACT_SIGMOID then takes this Y, the others take X. */
+int gn_act_fwd(int kind, const void* X, void* Y, int64_t n, int dtype, void* stream);
 
 /* GLU product out = glu_kind(gate, up) over n elements (fused-swiglu.glsl:78,
  * fused-geglu.glsl:81, fused-reglu.glsl:73; kinds GN_GLU_*). */

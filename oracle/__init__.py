@@ -32,6 +32,8 @@ def lib():
         if not os.path.exists(_LIB_PATH):
             build()
         _lib = ctypes.CDLL(_LIB_PATH)
+        _lib.or_mix64.restype = ctypes.c_uint64
+        _lib.or_gumbel.restype = ctypes.c_float
     return _lib
 
 
@@ -292,6 +294,62 @@ def vsa_dots(preds, bits):
     dots, pd = _out((Bn, K))
     lib().or_vsa_dots(pp, pb, pd, Bn, K, D, words)
     return dots
+
+
+def vsa_unpack_project_fwd(bits, W, bias=None):
+    """Y [Bn x O] = unpack(bits) W^T + bias (vsa-unpack-project.glsl:40-74), fp64 sums."""
+    Bn, words = bits.shape
+    O, D = W.shape
+    bits, pb = _u(bits)
+    W, pw = _f(W)
+    pbias = None
+    if bias is not None:
+        bias, pbias = _f(bias)
+    Y, py = _out((Bn, O))
+    lib().or_vsa_unpack_project_fwd(pb, pw, pbias, py, Bn, O, D, words)
+    return Y
+
+
+def mix64(seed, idx):
+    return int(lib().or_mix64(ctypes.c_uint64(seed), ctypes.c_uint64(idx)))
+
+
+def gumbel(seed, idx):
+    return float(lib().or_gumbel(ctypes.c_uint64(seed), ctypes.c_uint64(idx)))
+
+
+def vsa_select(dots, temperature=1.0, seed=0, counter=0, noise=True):
+    """Top-2 + softmax weights of the surrogate forward from given fp32 dots [Bn x K] with
+    this build's seeded Gumbel noise (see or_vsa_select).  Returns (results, weights)."""
+    Bn, K = dots.shape
+    dots, pd = _f(dots)
+    results = np.zeros((Bn, 4), dtype=np.uint32)
+    weights, pw = _out((Bn, K))
+    lib().or_vsa_select(pd, results.ctypes.data_as(ctypes.c_void_p), pw, Bn, K,
+                        ctypes.c_float(temperature), ctypes.c_uint64(seed),
+                        ctypes.c_uint64(counter), int(noise))
+    return results, weights
+
+
+def vsa_surrogate_loss(preds, bits, results, gamma=1.0, delta=1.0, lambda_c=0.3):
+    Bn, K, D = preds.shape
+    words = bits.shape[1]
+    preds, pp = _f(preds)
+    bits, pb = _u(bits)
+    results, pr = _u(results)
+    loss, pl = _out((Bn,))
+    lib().or_vsa_surrogate_loss(pp, pb, pr, pl, Bn, K, D, words, ctypes.c_float(gamma),
+                                ctypes.c_float(delta), ctypes.c_float(lambda_c))
+    return loss
+
+
+def vsa_surrogate_fwd(preds, bits, gamma=1.0, delta=1.0, lambda_c=0.3, temperature=1.0, seed=0,
+                      counter=0, noise=True):
+    """The whole surrogate forward: (dots, results, weights, loss per row)."""
+    dots = vsa_dots(preds, bits)
+    results, weights = vsa_select(dots, temperature, seed, counter, noise)
+    loss = vsa_surrogate_loss(preds, bits, results, gamma, delta, lambda_c)
+    return dots, results, weights, loss
 
 
 def vsa_results_weights(dots, temperature=1.0, rng=None):

@@ -73,7 +73,7 @@ void or_linear_bwd(const float* dY, const float* X, const float* W, float* dX, f
 
 void or_linear_fwd(const float* X, const float* W, const float* b, float* Y, int M, int N,
                    int K) {
-#pragma omp parallel for schedule(static)
+#pragma omp parallel for collapse(2) schedule(static)
     for (int m = 0; m < M; ++m)
         for (int n = 0; n < N; ++n) {
             double s = b ? (double)b[n] : 0.0;
@@ -544,6 +544,92 @@ void or_vsa_dots(const float* preds, const uint32_t* bits, float* dots, int Bn, 
             }
             dots[(size_t)b * K + k] = (float)s;
         }
+}
+
+/* vsa-unpack-project.glsl:40-74: Y[b, o] = sum_j s_b(j) W[o, j] + bias[o] (fp64 sums). */
+void or_vsa_unpack_project_fwd(const uint32_t* bits, const float* W, const float* bias, float* Y,
+                               int Bn, int O, int D, int words) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < Bn; ++b)
+        for (int o = 0; o < O; ++o) {
+            const uint32_t* w = bits + (size_t)b * words;
+            const float* Wr = W + (size_t)o * D;
+            double s = bias ? (double)bias[o] : 0.0;
+            for (int j = 0; j < D; ++j) s += ((w[j >> 5] >> (j & 31)) & 1u) ? Wr[j] : -(double)Wr[j];
+            Y[(size_t)b * O + o] = (float)s;
+        }
+}
+
+/* The counter-based Gumbel source this build uses in place of the reference's unseeded
+ * std::mt19937 (vsa_loss_node.cpp:9-14): splitmix64 (Steele, Lea & Flood 2014) of the Weyl
+ * value seed + (idx + 1) * 0x9E3779B97F4A7C15, u = (top 23 bits + 1/2) / 2^23 (exact in fp32),
+ * g = -log(-log u) in fp32. */
+uint64_t or_mix64(uint64_t seed, uint64_t idx) {
+    uint64_t x = seed + (idx + 1) * 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+float or_gumbel(uint64_t seed, uint64_t idx) {
+    const float u = ((float)(uint32_t)(or_mix64(seed, idx) >> 41) + 0.5f) * 0x1p-23f;
+    return -logf(-logf(u));
+}
+
+/* dispatch_vsa_loss_forward (vsa_loss_node.cpp:101-148): the top-2 of dots + T g (strict >,
+ * earlier index kept on ties, both starting at index 0) and softmax(dots / T) weights, from
+ * given fp32 dots [Bn x K]; noise = 0: no Gumbel term. */
+void or_vsa_select(const float* dots, uint32_t* results, float* weights, int Bn, int K,
+                   float temperature, uint64_t seed, uint64_t counter, int noise) {
+    for (int b = 0; b < Bn; ++b) {
+        const float* d = dots + (size_t)b * K;
+        float max1 = -1e30f, max2 = -1e30f;
+        int k1 = 0, k2 = 0;
+        for (int k = 0; k < K; ++k) {
+            const float g = noise ? or_gumbel(seed, ((uint64_t)counter * Bn + b) * K + k) : 0.0f;
+            const float adj = d[k] + g * temperature;
+            if (adj > max1) {
+                max2 = max1; k2 = k1;
+                max1 = adj; k1 = k;
+            } else if (adj > max2) {
+                max2 = adj; k2 = k;
+            }
+        }
+        double mx = d[0], se = 0.0;
+        for (int k = 1; k < K; ++k) mx = d[k] > mx ? d[k] : mx;
+        for (int k = 0; k < K; ++k) se += exp((d[k] - mx) / temperature);
+        for (int k = 0; k < K; ++k) weights[(size_t)b * K + k] = (float)(exp((d[k] - mx) / temperature) / se);
+        uint32_t bw, br;
+        memcpy(&bw, &d[k1], 4);
+        memcpy(&br, &d[k2], 4);
+        results[(size_t)b * 4 + 0] = (uint32_t)k1;
+        results[(size_t)b * 4 + 1] = (uint32_t)k2;
+        results[(size_t)b * 4 + 2] = bw;
+        results[(size_t)b * 4 + 3] = br;
+    }
+}
+
+/* vsa-surrogate-loss-forward.glsl pass 1: loss[b] = mean_i max(gamma - y_i z[b, win, i], 0)
+ * + lambda max(0, delta - (dot_win - dot_run)), with win and the dots from results[b]. */
+void or_vsa_surrogate_loss(const float* preds, const uint32_t* bits, const uint32_t* results,
+                           float* loss, int Bn, int K, int D, int words, float gamma,
+                           float delta, float lambda_c) {
+    for (int b = 0; b < Bn; ++b) {
+        const int win = (int)results[(size_t)b * 4];
+        const float* z = preds + ((size_t)b * K + win) * D;
+        const uint32_t* w = bits + (size_t)b * words;
+        double h = 0.0;
+        for (int i = 0; i < D; ++i) {
+            const double y = ((w[i >> 5] >> (i & 31)) & 1u) ? 1.0 : -1.0;
+            const double m = gamma - y * z[i];
+            h += m > 0.0 ? m : 0.0;
+        }
+        float dw, dr;
+        memcpy(&dw, &results[(size_t)b * 4 + 2], 4);
+        memcpy(&dr, &results[(size_t)b * 4 + 3], 4);
+        const double c = delta - ((double)dw - dr);
+        loss[b] = (float)(h / D + lambda_c * (c > 0.0 ? c : 0.0));
+    }
 }
 
 /* surprise-momentum.glsl:53-114.  fmin/fmax give the clamps a defined result for a NaN

@@ -86,6 +86,21 @@ void or_vsa_surrogate_bwd(const float* preds, const uint32_t* bits, const uint32
 void or_vsa_dots(const float* preds, const uint32_t* bits, float* dots, int Bn, int K, int D,
                  int words);
 
+/* vsa-unpack-project.glsl:40-74 (forward): Y[b, o] = sum_j s_b(j) W[o, j] + bias[o] */
+void or_vsa_unpack_project_fwd(const uint32_t* bits, const float* W, const float* bias, float* Y,
+                               int Bn, int O, int D, int words);
+/* counter-based Gumbel noise of the surrogate forward (splitmix64; replaces the reference's
+ * unseeded std::mt19937, vsa_loss_node.cpp:9-14) */
+uint64_t or_mix64(uint64_t seed, uint64_t idx);
+float or_gumbel(uint64_t seed, uint64_t idx);
+/* vsa_loss_node.cpp:101-148: top-2 of dots + T g and softmax(dots / T) from given dots */
+void or_vsa_select(const float* dots, uint32_t* results, float* weights, int Bn, int K,
+                   float temperature, uint64_t seed, uint64_t counter, int noise);
+/* vsa-surrogate-loss-forward.glsl pass 1 (hinge on the winner + contrastive margin) */
+void or_vsa_surrogate_loss(const float* preds, const uint32_t* bits, const uint32_t* results,
+                           float* loss, int Bn, int K, int D, int words, float gamma,
+                           float delta, float lambda_c);
+
 /* Sub / Mul / Div / Neg backward (op as GN_BIN_*; stubs at autograd.cpp:631-654) */
 void or_binary_bwd(int op, const float* dY, const float* A, const float* B, float* dA, float* dB,
                    int64_t n);

@@ -276,6 +276,127 @@ def test_vsa_surrogate_reference_kats():
     assert np.count_nonzero(dP[0, [0, 2, 3]]) == 0
 
 
+@pytest.mark.parametrize("kind", ["relu", "gelu_tanh", "gelu_erf", "silu", "tanh", "sigmoid"])
+def test_act_fwd_golden(kind):
+    # forward values against torch float64 (tests/golden/make_golden.py: Y_* arrays)
+    g = golden("act")
+    assert rel_err(oracle.act_fwd(kind, g["X"]), g["Y_" + kind]) < TOL
+
+
+def test_vsa_dots_brute_force():
+    # vsa-surrogate-loss-forward.glsl pass 0 against an explicit unpack + fp64 dot per (b, k)
+    rng = np.random.default_rng(21)
+    Bn, K, D = 3, 5, 96
+    bits = rng.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    preds = rng.standard_normal((Bn, K, D)).astype(np.float32)
+    y = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little").astype(np.float64) * 2 - 1
+    ref = np.array([[float(np.dot(preds[b, k].astype(np.float64), y[b])) for k in range(K)]
+                    for b in range(Bn)])
+    assert rel_err(oracle.vsa_dots(preds, bits), ref) < TOL
+    # all-ones target: the dot is the plain row sum; all-zeros: minus it
+    ones = np.full((Bn, D // 32), 0xFFFFFFFF, np.uint32)
+    np.testing.assert_allclose(oracle.vsa_dots(preds, ones), preds.sum(-1), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(oracle.vsa_dots(preds, np.zeros_like(ones)), -preds.sum(-1),
+                               rtol=1e-5, atol=1e-5)
+
+
+def test_splitmix64_known_answers():
+    # splitmix64 from state 0 (Steele, Lea & Flood 2014): the published first outputs
+    assert [oracle.mix64(0, i) for i in range(3)] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4,
+                                                      0x06C45D188009454F]
+
+
+def test_gumbel_moments():
+    # standard Gumbel: mean = Euler-Mascheroni gamma, variance = pi^2 / 6 (a sign slip in
+    # -log(-log u) moves the mean to -gamma; a dropped log gives an exponential, mean 1)
+    g = np.array([oracle.gumbel(11, i) for i in range(60000)])
+    se = np.sqrt(np.pi ** 2 / 6 / g.size)
+    assert abs(g.mean() - 0.5772156649) < 5 * se
+    assert abs(g.var() - np.pi ** 2 / 6) < 0.05
+    # quantiles of exp(-exp(-g)) are uniform
+    u = np.exp(-np.exp(-g))
+    assert abs(np.mean(u < 0.25) - 0.25) < 0.01 and abs(np.mean(u < 0.75) - 0.75) < 0.01
+
+
+def test_vsa_select_known_answers():
+    # noise-free top-2 (vsa_loss_node.cpp:102-119): strict >, the earlier index wins ties,
+    # both start at index 0; softmax weights sum to 1 and follow the dots' order
+    dots = np.array([[3.0, 1.0, 2.0, -1.0], [1.0, 1.0, 0.0, 0.5], [0.0, 5.0, 5.0, 4.0]], np.float32)
+    res, w = oracle.vsa_select(dots, noise=False)
+    assert res[:, :2].tolist() == [[0, 2], [0, 1], [1, 2]]
+    np.testing.assert_array_equal(res[:, 2].view(np.float32), [3.0, 1.0, 5.0])
+    np.testing.assert_array_equal(res[:, 3].view(np.float32), [2.0, 1.0, 5.0])
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+    e = np.exp(dots[0] - 3.0)
+    np.testing.assert_allclose(w[0], e / e.sum(), rtol=1e-6)
+    # temperature 2 halves the logits
+    _, w2 = oracle.vsa_select(dots, temperature=2.0, noise=False)
+    e = np.exp((dots[0] - 3.0) / 2)
+    np.testing.assert_allclose(w2[0], e / e.sum(), rtol=1e-6)
+    # one branch: winner and runner-up are both 0 (no contrastive term)
+    res1, w1 = oracle.vsa_select(dots[:, :1], noise=False)
+    assert res1[:, :2].tolist() == [[0, 0]] * 3 and np.all(w1 == 1.0)
+
+
+def test_vsa_select_noise_order():
+    # with noise, the winner is the argmax of dots + T g where g is drawn at index
+    # (counter * Bn + b) * K + k; the recorded dots stay the unperturbed ones
+    rng = np.random.default_rng(22)
+    Bn, K, T, seed, ctr = 4, 6, 0.7, 1234, 3
+    dots = rng.standard_normal((Bn, K)).astype(np.float32)
+    res, _ = oracle.vsa_select(dots, temperature=T, seed=seed, counter=ctr)
+    for b in range(Bn):
+        adj = [np.float32(dots[b, k]) + np.float32(oracle.gumbel(seed, (ctr * Bn + b) * K + k))
+               * np.float32(T) for k in range(K)]
+        order = np.argsort(-np.array(adj, np.float64), kind="stable")
+        assert res[b, 0] == order[0] and res[b, 1] == order[1]
+        assert res[b, 2].view(np.float32) == dots[b, order[0]]
+
+
+def test_vsa_surrogate_loss_reference_kats():
+    # tests/test_vsa_hypernetwork.py:151-202 as losses: perfect prediction -> hinge 0;
+    # adversarial -> gamma + 1; contrastive 100 vs 99.8 at margin 0.5 -> 0.3 (times lambda)
+    D, K = 256, 2
+    rng = np.random.default_rng(23)
+    bits = rng.integers(0, 2**32, size=(1, D // 32), dtype=np.uint64).astype(np.uint32)
+    y = oracle.unpack_bits(bits, D)[0]
+    res = np.zeros((1, 4), np.uint32)
+    res[0, 1] = 1
+    res[0, 2], res[0, 3] = np.float32(100.0).view(np.uint32), np.float32(99.0).view(np.uint32)
+    perfect = np.stack([2 * y, 2 * y])[None]
+    assert oracle.vsa_surrogate_loss(perfect, bits, res, gamma=0.1, delta=0.5)[0] == 0.0
+    adv = np.stack([-y, -y])[None]
+    np.testing.assert_allclose(oracle.vsa_surrogate_loss(adv, bits, res, gamma=0.1, delta=0.5),
+                               1.1, rtol=1e-6)
+    res[0, 3] = np.float32(99.8).view(np.uint32)
+    np.testing.assert_allclose(oracle.vsa_surrogate_loss(perfect, bits, res, gamma=0.1, delta=0.5,
+                                                         lambda_c=0.3), 0.3 * 0.3, rtol=1e-4)
+    # the loss reads the winner's row only: another row's predictions do not matter
+    mixed = np.stack([2 * y, -y])[None]
+    res[0, 3] = np.float32(99.0).view(np.uint32)
+    assert oracle.vsa_surrogate_loss(mixed, bits, res, gamma=0.1, delta=0.5)[0] == 0.0
+
+
+def test_vsa_unpack_project_fwd():
+    rng = np.random.default_rng(24)
+    Bn, O, D = 3, 7, 128
+    bits = rng.integers(0, 2**32, size=(Bn, D // 32), dtype=np.uint64).astype(np.uint32)
+    W = rng.standard_normal((O, D)).astype(np.float32)
+    b = rng.standard_normal(O).astype(np.float32)
+    S = oracle.unpack_bits(bits, D).astype(np.float64)
+    assert rel_err(oracle.vsa_unpack_project_fwd(bits, W, b), S @ W.T.astype(np.float64) + b) < TOL
+    # all bits set: each output is its weight row's sum plus the bias
+    ones = np.full((1, D // 32), 0xFFFFFFFF, np.uint32)
+    np.testing.assert_allclose(oracle.vsa_unpack_project_fwd(ones, W, b)[0], W.sum(1) + b,
+                               rtol=1e-5, atol=1e-5)
+    # forward and backward are adjoint: <Y - b, dY> = <W, dW> for dW from the backward
+    dY = rng.standard_normal((Bn, O)).astype(np.float32)
+    dW, _ = oracle.vsa_unpack_project_bwd(dY, bits, D)
+    Y0 = oracle.vsa_unpack_project_fwd(bits, W)
+    np.testing.assert_allclose(np.sum(Y0.astype(np.float64) * dY), np.sum(W.astype(np.float64) * dW),
+                               rtol=1e-5)
+
+
 # ---------------------------------------------------------------------------- optimizers
 def test_adamw_and_adam_golden_three_steps():
     """torch.optim.AdamW / Adam (float64) over three steps pin adamw-update.glsl's formula
