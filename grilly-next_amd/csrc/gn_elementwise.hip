@@ -18,6 +18,10 @@ template <> struct vec<float, 4> {
         *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
     }
 };
+template <> struct vec<float, 8> {
+    static __device__ __forceinline__ void ld(const float* p, float (&v)[8]) { chunk8<float>::ld(p, v); }
+    static __device__ __forceinline__ void st(float* p, const float (&v)[8]) { chunk8<float>::st(p, v); }
+};
 template <> struct vec<bf16_t, 8> {
     static __device__ __forceinline__ void ld(const bf16_t* p, float (&v)[8]) {
         uint4 x = *reinterpret_cast<const uint4*>(p);
@@ -115,6 +119,18 @@ __global__ __launch_bounds__(256) void add_kernel(T* __restrict__ out, const T* 
 #pragma unroll
         for (int j = 0; j < V; ++j) x[j] += y[j];
         vec<T, V>::st(out + i * V, x);
+    }
+}
+
+// out = a in another storage type (fp32 <-> bf16, round to nearest-even into bf16)
+template <typename TI, typename TO, int V>
+__global__ __launch_bounds__(256) void convert_kernel(TO* __restrict__ out, const TI* __restrict__ a,
+                                                      int64_t nvec) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float x[V];
+        vec<TI, V>::ld(a + i * V, x);
+        vec<TO, V>::st(out + i * V, x);
     }
 }
 
@@ -355,6 +371,32 @@ extern "C" int gn_add_inplace(void* out, const void* a, int64_t n, int dtype, vo
         return GN_E_INVALID;
     }
     GN_LAUNCH_CHECK("gn_add_inplace");
+    return GN_OK;
+}
+
+extern "C" int gn_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
+                          void* stream) {
+    clear_error();
+    GN_REQUIRE(n >= 0, "gn_convert: negative n");
+    if (n == 0) return GN_OK;
+    GN_REQUIRE(src && dst, "gn_convert: null pointer");
+    hipStream_t s = as_stream(stream);
+    const bool v8 = aligned16(src) && aligned16(dst) && n % 8 == 0;
+    if (src_dtype == GN_F32 && dst_dtype == GN_BF16) {
+        if (v8)
+            convert_kernel<float, bf16_t, 8><<<grid_for(n / 8, 256, 8192), 256, 0, s>>>((bf16_t*)dst, (const float*)src, n / 8);
+        else
+            convert_kernel<float, bf16_t, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>((bf16_t*)dst, (const float*)src, n);
+    } else if (src_dtype == GN_BF16 && dst_dtype == GN_F32) {
+        if (v8)
+            convert_kernel<bf16_t, float, 8><<<grid_for(n / 8, 256, 8192), 256, 0, s>>>((float*)dst, (const bf16_t*)src, n / 8);
+        else
+            convert_kernel<bf16_t, float, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>((float*)dst, (const bf16_t*)src, n);
+    } else {
+        set_error("gn_convert: dtype %d -> %d not supported (f32 <-> bf16)", src_dtype, dst_dtype);
+        return GN_E_INVALID;
+    }
+    GN_LAUNCH_CHECK("gn_convert");
     return GN_OK;
 }
 

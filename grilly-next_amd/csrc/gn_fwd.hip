@@ -17,10 +17,11 @@ constexpr int kFwdWaves = 4;  // rows per 256-thread block on the register path
 // MODE 0 = LayerNorm (fnn-layernorm.glsl:44-102: mean, biased variance, (x-mean)/sqrt(var+eps)
 // * gamma + beta), MODE 1 = RMSNorm (rms-norm.glsl:34-70: x * rsqrt(mean(x^2)+eps) * w).
 // Row statistics: mean[r] (LayerNorm), stat[r] = rstd, or the variance when save_var.
-template <int MODE, typename T, int NC>
+// TX: x (a residual stream may be fp32); TY: gamma, beta and y.
+template <int MODE, typename TX, typename TY, int NC>
 __global__ __launch_bounds__(64 * kFwdWaves) void norm_fwd_rows(
-    const T* __restrict__ X, const T* __restrict__ gamma, const T* __restrict__ beta,
-    T* __restrict__ Y, float* __restrict__ mean, float* __restrict__ stat, int rows, int F,
+    const TX* __restrict__ X, const TY* __restrict__ gamma, const TY* __restrict__ beta,
+    TY* __restrict__ Y, float* __restrict__ mean, float* __restrict__ stat, int rows, int F,
     float eps, int save_var) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * kFwdWaves + (threadIdx.x >> 6);
@@ -31,7 +32,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void norm_fwd_rows(
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const int c = lane + 64 * j;
-        if (c < nchunks) chunk8<T>::ld(X + off + 8 * c, x[j]);
+        if (c < nchunks) chunk8<TX>::ld(X + off + 8 * c, x[j]);
         else
 #pragma unroll
             for (int e = 0; e < 8; ++e) x[j][e] = 0.f;
@@ -67,26 +68,26 @@ __global__ __launch_bounds__(64 * kFwdWaves) void norm_fwd_rows(
         const int c = lane + 64 * j;
         if (c >= nchunks) continue;
         float g[8], b[8], y[8];
-        if (gamma) chunk8<T>::ld(gamma + 8 * c, g);
+        if (gamma) chunk8<TY>::ld(gamma + 8 * c, g);
         else
 #pragma unroll
             for (int e = 0; e < 8; ++e) g[e] = 1.f;
-        if (MODE == 0 && beta) chunk8<T>::ld(beta + 8 * c, b);
+        if (MODE == 0 && beta) chunk8<TY>::ld(beta + 8 * c, b);
         else
 #pragma unroll
             for (int e = 0; e < 8; ++e) b[e] = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             y[e] = MODE == 0 ? (x[j][e] - mu) * rs * g[e] + b[e] : g[e] * x[j][e] * rs;
-        chunk8<T>::st(Y + off + 8 * c, y);
+        chunk8<TY>::st(Y + off + 8 * c, y);
     }
 }
 
 // Any F / alignment: one 256-thread block per row, two passes over the row in global memory.
-template <int MODE, typename T>
+template <int MODE, typename TX, typename TY>
 __global__ __launch_bounds__(256) void norm_fwd_generic(
-    const T* __restrict__ X, const T* __restrict__ gamma, const T* __restrict__ beta,
-    T* __restrict__ Y, float* __restrict__ mean, float* __restrict__ stat, int F, float eps,
+    const TX* __restrict__ X, const TY* __restrict__ gamma, const TY* __restrict__ beta,
+    TY* __restrict__ Y, float* __restrict__ mean, float* __restrict__ stat, int F, float eps,
     int save_var) {
     __shared__ float sh[4];
     const int r = blockIdx.x;
@@ -95,12 +96,12 @@ __global__ __launch_bounds__(256) void norm_fwd_generic(
     float mu = 0.f;
     if (MODE == 0) {
         float s = 0.f;
-        for (int f = threadIdx.x; f < F; f += 256) s += io<T>::ld(X, off + f);
+        for (int f = threadIdx.x; f < F; f += 256) s += io<TX>::ld(X, off + f);
         mu = block_sum<4>(s, sh) * invF;
     }
     float q = 0.f;
     for (int f = threadIdx.x; f < F; f += 256) {
-        const float d = io<T>::ld(X, off + f) - mu;
+        const float d = io<TX>::ld(X, off + f) - mu;
         q += d * d;
     }
     const float var = block_sum<4>(q, sh) * invF;
@@ -110,38 +111,54 @@ __global__ __launch_bounds__(256) void norm_fwd_generic(
         if (stat) stat[r] = (MODE == 0 && save_var) ? var : rs;
     }
     for (int f = threadIdx.x; f < F; f += 256) {
-        const float x = io<T>::ld(X, off + f);
-        const float g = gamma ? io<T>::ld(gamma, f) : 1.f;
-        const float b = (MODE == 0 && beta) ? io<T>::ld(beta, f) : 0.f;
-        io<T>::st(Y, off + f, MODE == 0 ? (x - mu) * rs * g + b : g * x * rs);
+        const float x = io<TX>::ld(X, off + f);
+        const float g = gamma ? io<TY>::ld(gamma, f) : 1.f;
+        const float b = (MODE == 0 && beta) ? io<TY>::ld(beta, f) : 0.f;
+        io<TY>::st(Y, off + f, MODE == 0 ? (x - mu) * rs * g + b : g * x * rs);
     }
 }
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int MODE, typename T>
+template <int MODE, typename TX, typename TY>
 int norm_fwd(const void* X, const void* gamma, const void* beta, void* Y, float* mean,
              float* stat, int rows, int F, float eps, int save_var, hipStream_t s) {
     const bool vec_ok = F % 8 == 0 && F <= 2048 && al16(X) && al16(Y) && (!gamma || al16(gamma)) &&
                         (!beta || al16(beta));
-    const T* x = (const T*)X;
-    const T* g = (const T*)gamma;
-    const T* b = (const T*)beta;
-    T* y = (T*)Y;
+    const TX* x = (const TX*)X;
+    const TY* g = (const TY*)gamma;
+    const TY* b = (const TY*)beta;
+    TY* y = (TY*)Y;
     if (vec_ok) {
         const unsigned grid = (unsigned)((rows + kFwdWaves - 1) / kFwdWaves);
         const int nc = (F / 8 + 63) / 64;
         switch (nc) {
-            case 1: norm_fwd_rows<MODE, T, 1><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
-            case 2: norm_fwd_rows<MODE, T, 2><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
-            case 3: norm_fwd_rows<MODE, T, 3><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
-            default: norm_fwd_rows<MODE, T, 4><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
+            case 1: norm_fwd_rows<MODE, TX, TY, 1><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
+            case 2: norm_fwd_rows<MODE, TX, TY, 2><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
+            case 3: norm_fwd_rows<MODE, TX, TY, 3><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
+            default: norm_fwd_rows<MODE, TX, TY, 4><<<grid, 64 * kFwdWaves, 0, s>>>(x, g, b, y, mean, stat, rows, F, eps, save_var); break;
         }
     } else {
-        norm_fwd_generic<MODE, T><<<rows, 256, 0, s>>>(x, g, b, y, mean, stat, F, eps, save_var);
+        norm_fwd_generic<MODE, TX, TY><<<rows, 256, 0, s>>>(x, g, b, y, mean, stat, F, eps, save_var);
     }
     GN_LAUNCH_CHECK(MODE == 0 ? "gn_layernorm_fwd" : "gn_rmsnorm_fwd");
     return GN_OK;
+}
+
+// (x, y) dtype pairs: both fp32, both bf16, or fp32 x under a bf16 y
+template <int MODE>
+int norm_fwd_dispatch(int x_dtype, int y_dtype, const void* X, const void* gamma, const void* beta,
+                      void* Y, float* mean, float* stat, int rows, int F, float eps, int save_var,
+                      hipStream_t s) {
+    if (x_dtype == GN_F32 && y_dtype == GN_F32)
+        return norm_fwd<MODE, float, float>(X, gamma, beta, Y, mean, stat, rows, F, eps, save_var, s);
+    if (x_dtype == GN_BF16 && y_dtype == GN_BF16)
+        return norm_fwd<MODE, bf16_t, bf16_t>(X, gamma, beta, Y, mean, stat, rows, F, eps, save_var, s);
+    if (x_dtype == GN_F32 && y_dtype == GN_BF16)
+        return norm_fwd<MODE, float, bf16_t>(X, gamma, beta, Y, mean, stat, rows, F, eps, save_var, s);
+    set_error("%s: x dtype %d with y dtype %d not supported (f32/f32, bf16/bf16, f32/bf16)",
+              MODE == 0 ? "gn_layernorm_fwd" : "gn_rmsnorm_fwd", x_dtype, y_dtype);
+    return GN_E_INVALID;
 }
 
 // out = glu(gate, up) elementwise; 8 elements per step through 16-byte accesses when VEC.
@@ -277,31 +294,37 @@ using namespace gn;
 extern "C" int gn_layernorm_fwd(const void* X, const void* gamma, const void* beta, void* Y,
                                 float* mean, float* rstd, int rows, int F, float eps, int dtype,
                                 unsigned flags, void* stream) {
+    return gn_layernorm_fwd_ex(X, dtype, gamma, beta, Y, dtype, mean, rstd, rows, F, eps, flags,
+                               stream);
+}
+
+extern "C" int gn_layernorm_fwd_ex(const void* X, int x_dtype, const void* gamma, const void* beta,
+                                   void* Y, int y_dtype, float* mean, float* rstd, int rows, int F,
+                                   float eps, unsigned flags, void* stream) {
     clear_error();
     GN_REQUIRE(rows >= 0 && F >= 0, "gn_layernorm_fwd: negative size");
     if (rows == 0) return GN_OK;
     GN_REQUIRE(F > 0, "gn_layernorm_fwd: F = 0 with %d rows", rows);
     GN_REQUIRE(X && Y, "gn_layernorm_fwd: null pointer");
-    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_layernorm_fwd: dtype %d (f32, bf16)", dtype);
     const int save_var = (flags & GN_LN_STAT_VAR) ? 1 : 0;
-    hipStream_t s = as_stream(stream);
-    if (dtype == GN_BF16)
-        return norm_fwd<0, bf16_t>(X, gamma, beta, Y, mean, rstd, rows, F, eps, save_var, s);
-    return norm_fwd<0, float>(X, gamma, beta, Y, mean, rstd, rows, F, eps, save_var, s);
+    return norm_fwd_dispatch<0>(x_dtype, y_dtype, X, gamma, beta, Y, mean, rstd, rows, F, eps,
+                                save_var, as_stream(stream));
 }
 
 extern "C" int gn_rmsnorm_fwd(const void* X, const void* w, void* Y, float* rstd, int rows, int F,
                               float eps, int dtype, void* stream) {
+    return gn_rmsnorm_fwd_ex(X, dtype, w, Y, dtype, rstd, rows, F, eps, stream);
+}
+
+extern "C" int gn_rmsnorm_fwd_ex(const void* X, int x_dtype, const void* w, void* Y, int y_dtype,
+                                 float* rstd, int rows, int F, float eps, void* stream) {
     clear_error();
     GN_REQUIRE(rows >= 0 && F >= 0, "gn_rmsnorm_fwd: negative size");
     if (rows == 0) return GN_OK;
     GN_REQUIRE(F > 0, "gn_rmsnorm_fwd: F = 0 with %d rows", rows);
     GN_REQUIRE(X && Y, "gn_rmsnorm_fwd: null pointer");
-    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_rmsnorm_fwd: dtype %d (f32, bf16)", dtype);
-    hipStream_t s = as_stream(stream);
-    if (dtype == GN_BF16)
-        return norm_fwd<1, bf16_t>(X, w, nullptr, Y, nullptr, rstd, rows, F, eps, 0, s);
-    return norm_fwd<1, float>(X, w, nullptr, Y, nullptr, rstd, rows, F, eps, 0, s);
+    return norm_fwd_dispatch<1>(x_dtype, y_dtype, X, w, nullptr, Y, nullptr, rstd, rows, F, eps, 0,
+                                as_stream(stream));
 }
 
 extern "C" int gn_glu_fwd(int kind, const void* gate, const void* up, void* out, int64_t n,

@@ -45,11 +45,14 @@ template <> struct raw8<bf16_t> {
 // adds into its own row, so the order of additions is fixed); at the end the block sums
 // its waves' rows and writes one partial row to the workspace.
 // MODE 0 = LayerNorm (dgamma, dbeta partials), 1 = RMSNorm (dw partials).
-template <int MODE, typename T, int NC>
+// TX: x, dX and the addend (a residual stream kept in fp32); TY: dy and gamma.  `add`
+// (nullable, may alias dX) is added to the row's input gradient: the residual branch's
+// gradient of a pre-norm block, so the fan-out sum costs no pass of its own.
+template <int MODE, typename TX, typename TY, int NC>
 __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
-    const T* __restrict__ dY, const T* __restrict__ X, const T* __restrict__ gamma,
-    const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dX,
-    float* __restrict__ part, int rows, int F, float eps, int stat_is_var, int accumulate) {
+    const TY* __restrict__ dY, const TX* __restrict__ X, const TY* __restrict__ gamma,
+    const float* __restrict__ mean, const float* __restrict__ rstd, TX* dX, const TX* add,
+    float* __restrict__ part, int rows, int F, float eps, int stat_is_var) {
     constexpr int NP = MODE == 0 ? 2 : 1;
     extern __shared__ float red[];  // [kNormWaves][NP][F]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -58,14 +61,14 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
     float* my = red + (size_t)wave * NP * F;
     for (int f = 4 * lane; f < NP * F; f += 256) *reinterpret_cast<float4*>(my + f) = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    raw8<T> gm[NC];
+    raw8<TY> gm[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const int c = lane + 64 * j;
         if (c < nchunks) gm[j].load(gamma + 8 * c);
         else gm[j].zero();
     }
-    auto load_row = [&](int r, raw8<T> (&x)[NC], raw8<T> (&dy)[NC]) {
+    auto load_row = [&](int r, raw8<TX> (&x)[NC], raw8<TY> (&dy)[NC]) {
         const size_t off = (size_t)r * F;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
@@ -87,7 +90,8 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
     };
     const int stride = gridDim.x * kNormWaves;
     int r = blockIdx.x * kNormWaves + wave;
-    raw8<T> x[NC], dy[NC];
+    raw8<TX> x[NC];
+    raw8<TY> dy[NC];
     float mu = 0.f, rs = 0.f;
     if (r < rows) {
         load_stats(r, mu, rs);
@@ -95,7 +99,8 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
     }
     while (r < rows) {
         const int rn = r + stride;
-        raw8<T> xn[NC], dyn[NC];
+        raw8<TX> xn[NC];
+        raw8<TY> dyn[NC];
         float mun = 0.f, rsn = 0.f;
         if (rn < rows) {
             load_stats(rn, mun, rsn);
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
             const int c = lane + 64 * j;
             if (c >= nchunks) continue;
             float o[8], pa[8], pb[8];
-            if (accumulate) chunk8<T>::ld(dX + off + 8 * c, o);
+            if (add) chunk8<TX>::ld(add + off + 8 * c, o);
             float4* qa = reinterpret_cast<float4*>(my + 8 * c);
             float4* qb = reinterpret_cast<float4*>(my + F + 8 * c);
             const float4 a0 = qa[0], a1 = qa[1];
@@ -146,9 +151,9 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
                     v = rs * gm[j][e] * dy[j][e] - x[j][e] * rs * rs * rs * s1 * invF;
                     pa[e] += dy[j][e] * x[j][e] * rs;
                 }
-                o[e] = accumulate ? o[e] + v : v;
+                o[e] = add ? o[e] + v : v;
             }
-            chunk8<T>::st(dX + off + 8 * c, o);
+            chunk8<TX>::st(dX + off + 8 * c, o);
             qa[0] = make_float4(pa[0], pa[1], pa[2], pa[3]);
             qa[1] = make_float4(pa[4], pa[5], pa[6], pa[7]);
             if (MODE == 0) {
@@ -207,11 +212,11 @@ __global__ __launch_bounds__(1024) void colsum_partials(const float* __restrict_
 }
 
 // Generic fallback (any F): one block per row, two passes over global memory.
-template <int MODE, typename T>
+template <int MODE, typename TX, typename TY>
 __global__ __launch_bounds__(256) void norm_bwd_generic_dx(
-    const T* __restrict__ dY, const T* __restrict__ X, const T* __restrict__ gamma,
-    const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dX, int F,
-    float eps, int stat_is_var, int accumulate) {
+    const TY* __restrict__ dY, const TX* __restrict__ X, const TY* __restrict__ gamma,
+    const float* __restrict__ mean, const float* __restrict__ rstd, TX* dX, const TX* add, int F,
+    float eps, int stat_is_var) {
     __shared__ float sh[4];
     const int r = blockIdx.x;
     const size_t off = (size_t)r * F;
@@ -224,7 +229,7 @@ __global__ __launch_bounds__(256) void norm_bwd_generic_dx(
     }
     float s1 = 0.f, s2 = 0.f;
     for (int f = threadIdx.x; f < F; f += 256) {
-        float x = io<T>::ld(X, off + f), dy = io<T>::ld(dY, off + f), g = io<T>::ld(gamma, f);
+        float x = io<TX>::ld(X, off + f), dy = io<TY>::ld(dY, off + f), g = io<TY>::ld(gamma, f);
         if (MODE == 0) {
             float xh = (x - mu) * rs;
             s1 += dy * g;
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(256) void norm_bwd_generic_dx(
     if (MODE == 0) s2 = block_sum<4>(s2, sh);
     const float invF = 1.0f / (float)F;
     for (int f = threadIdx.x; f < F; f += 256) {
-        float x = io<T>::ld(X, off + f), dy = io<T>::ld(dY, off + f), g = io<T>::ld(gamma, f);
+        float x = io<TX>::ld(X, off + f), dy = io<TY>::ld(dY, off + f), g = io<TY>::ld(gamma, f);
         float v;
         if (MODE == 0) {
             float xh = (x - mu) * rs;
@@ -245,22 +250,22 @@ __global__ __launch_bounds__(256) void norm_bwd_generic_dx(
         } else {
             v = rs * g * dy - x * rs * rs * rs * s1 * invF;
         }
-        if (accumulate) v += io<T>::ld(dX, off + f);
-        io<T>::st(dX, off + f, v);
+        if (add) v += io<TX>::ld(add, off + f);
+        io<TX>::st(dX, off + f, v);
     }
 }
 
 // Generic parameter gradients: column sums over all rows (thread per feature).
-template <int MODE, typename T>
+template <int MODE, typename TX, typename TY>
 __global__ __launch_bounds__(256) void norm_bwd_generic_param(
-    const T* __restrict__ dY, const T* __restrict__ X, const float* __restrict__ mean,
+    const TY* __restrict__ dY, const TX* __restrict__ X, const float* __restrict__ mean,
     const float* __restrict__ rstd, float* __restrict__ dA, float* __restrict__ dB, int rows,
     int F, float eps, int stat_is_var, int accumulate) {
     const int f = blockIdx.x * 256 + threadIdx.x;
     if (f >= F) return;
     float sa = 0.f, sb = 0.f;
     for (int r = 0; r < rows; ++r) {
-        float x = io<T>::ld(X, (size_t)r * F + f), dy = io<T>::ld(dY, (size_t)r * F + f);
+        float x = io<TX>::ld(X, (size_t)r * F + f), dy = io<TY>::ld(dY, (size_t)r * F + f);
         if (MODE == 0) {
             float rs = stat_is_var ? rsqrtf(rstd[r] + eps) : rstd[r];
             sa += dy * (x - mean[r]) * rs;
@@ -281,14 +286,17 @@ bool allow_lds(F* fn, size_t bytes) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
 }
 
-template <int MODE, typename T>
+// add: the input-gradient addend (nullable; dX itself for an in-place accumulation).
+// acc: the parameter gradients add onto dA / dB.
+template <int MODE, typename TX, typename TY>
 int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean,
-             const float* rstd, void* dX, float* dA, float* dB, int rows, int F, float eps,
-             int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s) {
+             const float* rstd, void* dX, const void* add, float* dA, float* dB, int rows, int F,
+             float eps, int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s) {
     // rows wider than 2048 would not fit in registers: they use the generic path
     const bool vec_ok = (F % 8 == 0) && F <= 2048 && aligned16(dY) && aligned16(X) &&
-                        aligned16(dX) && aligned16(gamma);
+                        aligned16(dX) && aligned16(gamma) && (!add || aligned16(add));
     const bool need_param = dA || dB;
+    const TX* ad = (const TX*)add;
     if (vec_ok) {
         // every wave gets two rows or more where the row count allows it
         const int G = std::max(1, std::min(kNormGrid, (rows + 2 * kNormWaves - 1) / (2 * kNormWaves)));
@@ -299,27 +307,27 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
         }
         float* part = need_param ? (float*)ws : nullptr;
         const int nc = (F / 8 + 63) / 64;
-        // part == nullptr is never dereferenced: without param grads the partial write is
-        // redirected to a dummy path below by using the generic dx kernel instead.
+        // without parameter gradients there are no partial rows to write: the generic dx
+        // kernel does the input gradient alone
         if (!need_param) {
-            norm_bwd_generic_dx<MODE, T><<<rows, 256, 0, s>>>(
-                (const T*)dY, (const T*)X, (const T*)gamma, mean, rstd, (T*)dX, F, eps, stat_var, acc);
+            norm_bwd_generic_dx<MODE, TX, TY><<<rows, 256, 0, s>>>(
+                (const TY*)dY, (const TX*)X, (const TY*)gamma, mean, rstd, (TX*)dX, ad, F, eps, stat_var);
             GN_LAUNCH_CHECK("norm backward (dx only)");
             return GN_OK;
         }
         const size_t lds = (size_t)kNormWaves * (MODE == 0 ? 2 : 1) * F * sizeof(float);
         if (lds > 64 * 1024) {
-            static const bool ok = allow_lds(norm_bwd_rows<MODE, T, 4>, 160 * 1024) &&
-                                   allow_lds(norm_bwd_rows<MODE, T, 2>, 160 * 1024);
+            static const bool ok = allow_lds(norm_bwd_rows<MODE, TX, TY, 4>, 160 * 1024) &&
+                                   allow_lds(norm_bwd_rows<MODE, TX, TY, 2>, 160 * 1024);
             if (!ok) {
                 set_error("norm backward: cannot reserve %zu B of LDS", lds);
                 return GN_E_HIP;
             }
         }
 #define GN_NORM_LAUNCH(NCV)                                                                    \
-    norm_bwd_rows<MODE, T, NCV><<<G, 64 * kNormWaves, lds, s>>>(                               \
-        (const T*)dY, (const T*)X, (const T*)gamma, mean, rstd, (T*)dX, part, rows, F, eps,   \
-        stat_var, acc)
+    norm_bwd_rows<MODE, TX, TY, NCV><<<G, 64 * kNormWaves, lds, s>>>(                          \
+        (const TY*)dY, (const TX*)X, (const TY*)gamma, mean, rstd, (TX*)dX, ad, part, rows, F, \
+        eps, stat_var)
         if (nc <= 1) GN_NORM_LAUNCH(1);
         else if (nc <= 2) GN_NORM_LAUNCH(2);
         else GN_NORM_LAUNCH(4);
@@ -336,16 +344,37 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
         return GN_OK;
     }
     if (dX) {
-        norm_bwd_generic_dx<MODE, T><<<rows, 256, 0, s>>>(
-            (const T*)dY, (const T*)X, (const T*)gamma, mean, rstd, (T*)dX, F, eps, stat_var, acc);
+        norm_bwd_generic_dx<MODE, TX, TY><<<rows, 256, 0, s>>>(
+            (const TY*)dY, (const TX*)X, (const TY*)gamma, mean, rstd, (TX*)dX, ad, F, eps, stat_var);
         GN_LAUNCH_CHECK("norm backward generic dx");
     }
     if (need_param) {
-        norm_bwd_generic_param<MODE, T><<<(F + 255) / 256, 256, 0, s>>>(
-            (const T*)dY, (const T*)X, mean, rstd, dA, dB, rows, F, eps, stat_var, acc);
+        norm_bwd_generic_param<MODE, TX, TY><<<(F + 255) / 256, 256, 0, s>>>(
+            (const TY*)dY, (const TX*)X, mean, rstd, dA, dB, rows, F, eps, stat_var, acc);
         GN_LAUNCH_CHECK("norm backward generic params");
     }
     return GN_OK;
+}
+
+// (TX, TY) pairs the library takes: both fp32, both bf16, or fp32 x / dX with bf16 dy / gamma
+// (a residual stream carried in fp32 under a bf16 block).
+template <int MODE>
+int norm_bwd_dispatch(const char* who, int dy_dtype, int x_dtype, const void* dY, const void* X,
+                      const void* gamma, const float* mean, const float* rstd, void* dX,
+                      const void* add, float* dA, float* dB, int rows, int F, float eps,
+                      int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s) {
+    if (x_dtype == GN_F32 && dy_dtype == GN_F32)
+        return norm_bwd<MODE, float, float>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F, eps,
+                                            stat_var, acc, ws, ws_bytes, s);
+    if (x_dtype == GN_BF16 && dy_dtype == GN_BF16)
+        return norm_bwd<MODE, bf16_t, bf16_t>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F,
+                                              eps, stat_var, acc, ws, ws_bytes, s);
+    if (x_dtype == GN_F32 && dy_dtype == GN_BF16)
+        return norm_bwd<MODE, float, bf16_t>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F,
+                                             eps, stat_var, acc, ws, ws_bytes, s);
+    set_error("%s: x dtype %d with dy dtype %d not supported (f32/f32, bf16/bf16, f32/bf16)", who,
+              x_dtype, dy_dtype);
+    return GN_E_INVALID;
 }
 
 // ---- softmax backward: one block per row (activation-softmax-backward.glsl:36-48) ----
@@ -524,14 +553,25 @@ extern "C" int gn_layernorm_bwd(const void* dY, const void* X, const void* gamma
     GN_REQUIRE(dY && X && gamma && mean && rstd && dX, "gn_layernorm_bwd: null pointer");
     const bool acc = flags & GN_ACCUMULATE;
     const int sv = (flags & GN_LN_STAT_VAR) ? 1 : 0;
-    if (dtype == GN_F32)
-        return norm_bwd<0, float>(dY, X, gamma, mean, rstd, dX, dGamma, dBeta, rows, F, eps, sv,
-                                  acc, ws, ws_bytes, as_stream(stream));
-    if (dtype == GN_BF16)
-        return norm_bwd<0, bf16_t>(dY, X, gamma, mean, rstd, dX, dGamma, dBeta, rows, F, eps, sv,
-                                   acc, ws, ws_bytes, as_stream(stream));
-    set_error("gn_layernorm_bwd: dtype %d not supported", dtype);
-    return GN_E_INVALID;
+    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_layernorm_bwd: dtype %d not supported", dtype);
+    return norm_bwd_dispatch<0>("gn_layernorm_bwd", dtype, dtype, dY, X, gamma, mean, rstd, dX,
+                                acc ? dX : nullptr, dGamma, dBeta, rows, F, eps, sv, acc, ws,
+                                ws_bytes, as_stream(stream));
+}
+
+extern "C" int gn_layernorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype,
+                                   const void* gamma, const float* mean, const float* rstd,
+                                   const void* dX_add, void* dX, float* dGamma, float* dBeta,
+                                   int rows, int F, float eps, unsigned flags, void* ws,
+                                   size_t ws_bytes, void* stream) {
+    clear_error();
+    GN_REQUIRE(rows >= 0 && F > 0, "gn_layernorm_bwd_ex: bad shape rows=%d F=%d", rows, F);
+    if (rows == 0) return GN_OK;
+    GN_REQUIRE(dY && X && gamma && mean && rstd && dX, "gn_layernorm_bwd_ex: null pointer");
+    return norm_bwd_dispatch<0>("gn_layernorm_bwd_ex", dy_dtype, x_dtype, dY, X, gamma, mean, rstd,
+                                dX, dX_add, dGamma, dBeta, rows, F, eps,
+                                (flags & GN_LN_STAT_VAR) ? 1 : 0, flags & GN_ACCUMULATE, ws,
+                                ws_bytes, as_stream(stream));
 }
 
 extern "C" int gn_layernorm_bwd_noalloc(const void* dY, const void* X, const void* gamma,
@@ -548,11 +588,9 @@ extern "C" int gn_layernorm_bwd_noalloc(const void* dY, const void* X, const voi
     if (!ws) return GN_E_HIP;
     const bool acc = flags & GN_ACCUMULATE;
     const int sv = (flags & GN_LN_STAT_VAR) ? 1 : 0;
-    const int rc = dtype == GN_F32
-        ? norm_bwd<0, float>(dY, X, gamma, mean, rstd, dX, dGamma, dBeta, rows, F, eps, sv, acc,
-                             ws, kNoAllocScratchBytes, as_stream(stream))
-        : norm_bwd<0, bf16_t>(dY, X, gamma, mean, rstd, dX, dGamma, dBeta, rows, F, eps, sv, acc,
-                              ws, kNoAllocScratchBytes, as_stream(stream));
+    const int rc = norm_bwd_dispatch<0>("gn_layernorm_bwd_noalloc", dtype, dtype, dY, X, gamma, mean,
+                                        rstd, dX, acc ? dX : nullptr, dGamma, dBeta, rows, F, eps,
+                                        sv, acc, ws, kNoAllocScratchBytes, as_stream(stream));
     if (rc == GN_E_WORKSPACE)
         set_error("gn_layernorm_bwd_noalloc: rows=%d F=%d need more than the %zu B static scratch",
                   rows, F, kNoAllocScratchBytes);
@@ -566,15 +604,24 @@ extern "C" int gn_rmsnorm_bwd(const void* dY, const void* X, const void* w, cons
     GN_REQUIRE(rows >= 0 && F > 0, "gn_rmsnorm_bwd: bad shape rows=%d F=%d", rows, F);
     if (rows == 0) return GN_OK;
     GN_REQUIRE(dY && X && w && rstd && dX, "gn_rmsnorm_bwd: null pointer");
+    GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_rmsnorm_bwd: dtype %d not supported", dtype);
     const bool acc = flags & GN_ACCUMULATE;
-    if (dtype == GN_F32)
-        return norm_bwd<1, float>(dY, X, w, nullptr, rstd, dX, dW, nullptr, rows, F, 0.f, 0, acc,
-                                  ws, ws_bytes, as_stream(stream));
-    if (dtype == GN_BF16)
-        return norm_bwd<1, bf16_t>(dY, X, w, nullptr, rstd, dX, dW, nullptr, rows, F, 0.f, 0, acc,
-                                   ws, ws_bytes, as_stream(stream));
-    set_error("gn_rmsnorm_bwd: dtype %d not supported", dtype);
-    return GN_E_INVALID;
+    return norm_bwd_dispatch<1>("gn_rmsnorm_bwd", dtype, dtype, dY, X, w, nullptr, rstd, dX,
+                                acc ? dX : nullptr, dW, nullptr, rows, F, 0.f, 0, acc, ws, ws_bytes,
+                                as_stream(stream));
+}
+
+extern "C" int gn_rmsnorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype,
+                                 const void* w, const float* rstd, const void* dX_add, void* dX,
+                                 float* dW, int rows, int F, unsigned flags, void* ws,
+                                 size_t ws_bytes, void* stream) {
+    clear_error();
+    GN_REQUIRE(rows >= 0 && F > 0, "gn_rmsnorm_bwd_ex: bad shape rows=%d F=%d", rows, F);
+    if (rows == 0) return GN_OK;
+    GN_REQUIRE(dY && X && w && rstd && dX, "gn_rmsnorm_bwd_ex: null pointer");
+    return norm_bwd_dispatch<1>("gn_rmsnorm_bwd_ex", dy_dtype, x_dtype, dY, X, w, nullptr, rstd, dX,
+                                dX_add, dW, nullptr, rows, F, 0.f, 0, flags & GN_ACCUMULATE, ws,
+                                ws_bytes, as_stream(stream));
 }
 
 extern "C" int gn_softmax_bwd(const void* dY, const void* Y, void* dX, int rows, int C,

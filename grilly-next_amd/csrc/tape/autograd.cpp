@@ -175,10 +175,12 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
         stats_.nodes_with_grad++;
         std::memset(cur->grad_input_buffers, 0, sizeof(cur->grad_input_buffers));
         borrowed_ = 0;
+        handled_ = 0;
         dispatch(cur);
         for (uint32_t i = 0; i < cur->num_inputs && i < kMaxNodeIO; ++i) {
             const TensorRef& in = cur->inputs[i];
-            if (!in.requires_grad || cur->grad_input_buffers[i] == 0) continue;
+            if (!in.requires_grad || cur->grad_input_buffers[i] == 0 || ((handled_ >> i) & 1u))
+                continue;
             const bool own = !((borrowed_ >> i) & 1u);
             if (writes_in_place(cur, in.buffer_id))
                 replace(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(), own);
@@ -271,7 +273,31 @@ void BackwardEngine::bwd_softmax(Node* n) {
     n->grad_input_buffers[0] = dX;
 }
 
-// saved: [0] gamma, [1] beta (or 0), [2] mean, [3] rstd (or var with stat_is_var)
+// Output buffer of a norm's input gradient.  When the input already holds a gradient of the
+// same dtype and size (the residual branch of a pre-norm block, recorded later on the tape and
+// so visited first), the norm kernel adds it in its own pass (its dX_add): into that buffer
+// when the engine owns it, else into a fresh buffer that replaces it.  The table is then up
+// to date and the input is marked handled.  *add receives the addend (nullptr: none).
+uint64_t BackwardEngine::norm_dx(Node* n, const void** add) {
+    const TensorRef& x = n->inputs[0];
+    *add = nullptr;
+    GradEntry* e = (x.requires_grad && !writes_in_place(n, x.buffer_id)) ? find(x.buffer_id) : nullptr;
+    if (e && e->grad_id && e->dtype == x.dtype && e->grad_bytes == x.size_bytes()) {
+        *add = P(e->grad_id);
+        if (!e->owned) {
+            e->grad_id = alloc_grad(x.size_bytes());
+            e->owned = true;
+        }
+        handled_ |= 1u;
+        stats_.fanout_accumulations++;
+        return e->grad_id;
+    }
+    return alloc_grad(x.size_bytes());
+}
+
+// saved: [0] gamma, [1] beta (or 0), [2] mean, [3] rstd (or var with stat_is_var).  x and its
+// gradient may be fp32 under a bf16 output (a residual stream kept in fp32): dy and gamma take
+// the output's dtype.
 void BackwardEngine::bwd_layernorm(Node* n) {
     const TensorRef& x = n->inputs[0];
     const int rows = (int)x.rows(), F = (int)x.last();
@@ -280,34 +306,40 @@ void BackwardEngine::bwd_layernorm(Node* n) {
     const uint64_t gamma = n->saved_buffer_ids[0], beta = n->saved_buffer_ids[1];
     const uint64_t mean = n->saved_buffer_ids[2], rstd = n->saved_buffer_ids[3];
     if (!gamma || !mean || !rstd) throw std::invalid_argument("LayerNorm: saved gamma/mean/rstd missing");
-    uint64_t dX = alloc_grad(x.size_bytes());
+    const int xdt = gn_dtype(x.dtype, "LayerNorm");
+    const int ydt = n->num_outputs ? gn_dtype(n->outputs[0].dtype, "LayerNorm output") : xdt;
+    const void* add = nullptr;
+    uint64_t dX = norm_dx(n, &add);
     uint64_t dG = alloc_grad((size_t)F * 4);
     uint64_t dB = beta ? alloc_grad((size_t)F * 4) : 0;
     const size_t wsb = gn_norm_workspace_bytes(rows, F);
     uint64_t ws = alloc_grad(wsb);
-    gn_call(gn_layernorm_bwd(gout(n), P(x.buffer_id), P(gamma), (const float*)P(mean),
-                             (const float*)P(rstd), P(dX), (float*)P(dG), (float*)P(dB), rows, F,
-                             p.eps, gn_dtype(x.dtype, "LayerNorm"), p.stat_is_var ? GN_LN_STAT_VAR : 0,
-                             P(ws), wsb, dev_.stream()), "LayerNorm backward");
+    gn_call(gn_layernorm_bwd_ex(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
+                                (const float*)P(rstd), add, P(dX), (float*)P(dG), (float*)P(dB), rows,
+                                F, p.eps, p.stat_is_var ? GN_LN_STAT_VAR : 0, P(ws), wsb, dev_.stream()),
+            "LayerNorm backward");
     stats_.shaders_dispatched += 2;
     if (x.requires_grad) n->grad_input_buffers[0] = dX;
     contribute(gamma, dG, 0, F, true);
     if (beta) contribute(beta, dB, 0, F, true);
 }
 
-// saved: [0] w, [1] rstd (fp32 per row)
+// saved: [0] w, [1] rstd (fp32 per row); dtypes as LayerNorm
 void BackwardEngine::bwd_rmsnorm(Node* n) {
     const TensorRef& x = n->inputs[0];
     const int rows = (int)x.rows(), F = (int)x.last();
     const uint64_t w = n->saved_buffer_ids[0], rstd = n->saved_buffer_ids[1];
     if (!w || !rstd) throw std::invalid_argument("RMSNorm: saved w/rstd missing");
-    uint64_t dX = alloc_grad(x.size_bytes());
+    const int xdt = gn_dtype(x.dtype, "RMSNorm");
+    const int ydt = n->num_outputs ? gn_dtype(n->outputs[0].dtype, "RMSNorm output") : xdt;
+    const void* add = nullptr;
+    uint64_t dX = norm_dx(n, &add);
     uint64_t dW = alloc_grad((size_t)F * 4);
     const size_t wsb = gn_norm_workspace_bytes(rows, F);
     uint64_t ws = alloc_grad(wsb);
-    gn_call(gn_rmsnorm_bwd(gout(n), P(x.buffer_id), P(w), (const float*)P(rstd), P(dX),
-                           (float*)P(dW), rows, F, gn_dtype(x.dtype, "RMSNorm"), 0, P(ws), wsb,
-                           dev_.stream()), "RMSNorm backward");
+    gn_call(gn_rmsnorm_bwd_ex(gout(n), ydt, P(x.buffer_id), xdt, P(w), (const float*)P(rstd), add,
+                              P(dX), (float*)P(dW), rows, F, 0, P(ws), wsb, dev_.stream()),
+            "RMSNorm backward");
     stats_.shaders_dispatched += 2;
     if (x.requires_grad) n->grad_input_buffers[0] = dX;
     contribute(w, dW, 0, F, true);
@@ -387,13 +419,26 @@ void BackwardEngine::bwd_cross_entropy(Node* n) {
     n->grad_input_buffers[0] = dZ;
 }
 
-// Add: both inputs receive the upstream gradient itself (borrowed, copied on fan-out).
+// Add: both inputs receive the upstream gradient itself (borrowed, copied on fan-out).  An
+// input stored in another dtype than the sum (a bf16 branch added into an fp32 residual
+// stream) receives the upstream gradient converted once to its own dtype.
 void BackwardEngine::bwd_add_sub(Node* n, bool /*sub*/) {
     const uint64_t g = reinterpret_cast<uint64_t>(gout(n));
+    const TensorRef& out = n->outputs[0];
     for (uint32_t i = 0; i < n->num_inputs && i < 2; ++i) {
-        if (!n->inputs[i].requires_grad) continue;
-        if (n->inputs[i].numel() != n->outputs[0].numel())
+        const TensorRef& in = n->inputs[i];
+        if (!in.requires_grad) continue;
+        if (in.numel() != out.numel())
             throw std::invalid_argument("Add: broadcasting inputs are not supported");
+        if (in.dtype != out.dtype) {
+            const uint64_t c = alloc_grad(in.size_bytes());
+            gn_call(gn_convert(P(g), gn_dtype(out.dtype, "Add output"), P(c), gn_dtype(in.dtype, "Add input"),
+                               (int64_t)in.numel(), dev_.stream()),
+                    "Add backward (dtype conversion)");
+            stats_.shaders_dispatched++;
+            n->grad_input_buffers[i] = c;
+            continue;
+        }
         n->grad_input_buffers[i] = g;
         borrowed_ |= 1u << i;
     }

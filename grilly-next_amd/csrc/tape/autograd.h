@@ -171,6 +171,8 @@ private:
     // on the engine's stream, so each node may reuse it); grown on demand, 0 bytes -> 0
     uint64_t split_ws(size_t bytes);
     const void* gout(Node* n) const;
+    // output buffer of a norm's input gradient, summed with the input's existing gradient
+    uint64_t norm_dx(Node* n, const void** add);
 
     void bwd_linear(Node* n);
     void bwd_act(Node* n, int kind, bool uses_output);
@@ -197,6 +199,7 @@ private:
     Device& dev_;
     Stats stats_{};
     uint32_t borrowed_ = 0;  // inputs whose gradient is the upstream buffer itself
+    uint32_t handled_ = 0;   // inputs whose gradient the handler already summed into the table
     uint64_t ws_id_ = 0;     // split-K scratch of the current pass (owned by backward_bufs_)
     size_t ws_bytes_ = 0;
     std::vector<uint64_t> backward_bufs_;

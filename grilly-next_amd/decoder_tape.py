@@ -4,7 +4,11 @@ Per layer (pre-LN):  n1 = LN(x);  qkv = n1 Wqkv^T + bqkv;  o = causal attention 
 fused qkv rows;  x2 = x + o Wo^T + bo;  n2 = LN(x2);  h = gate * GELU_tanh(up) with
 gate = n2 Wg^T + bg, up = n2 Wu^T + bu;  x3 = x2 + h Wd^T + bd.
 Embedding x0 = E[ids], final LN, tied LM head logits = LN(x_L) E^T, cross-entropy over the
-vocabulary (scale 1/T).  bf16 storage, fp32 statistics and weight gradients.
+vocabulary (scale 1/T).  bf16 weights and block activations, fp32 statistics and weight
+gradients; the residual stream x (and so its gradient) is fp32: the norms read it in fp32 and
+write bf16, each bf16 branch output is added into it in fp32.  Carried in bf16, the residual
+gradient's rounding over the 12 layers reaches the LayerNorm gains' gradient (a sum that
+cancels heavily) at a few percent; in fp32 it stays within the bf16 tolerance.
 
 `Decoder.forward()` runs the forward on the GPU through this library's forward kernels
 (untimed: gn_layernorm_fwd saving mean/rstd, gn_linear_fwd, gn_glu_linear_fwd saving the
@@ -55,26 +59,27 @@ class Decoder:
         B, S, H, d, T = self.B, self.S, self.H, self.d, self.T
         D = d // H
         ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D), self.dev)
-        x = self.E[self.ids.long()].contiguous()
+        bf = torch.bfloat16
+        x = self.E[self.ids.long()].float().contiguous()  # fp32 residual stream
         self.x0 = x
         acts = []
         for p in self.layers:
             a = {"x": x}
-            a["n1"], a["m1"], a["r1"] = gn.layernorm_fwd(x, p["ln1_g"], p["ln1_b"])
+            a["n1"], a["m1"], a["r1"] = gn.layernorm_fwd(x, p["ln1_g"], p["ln1_b"], out_dtype=bf)
             a["qkv"] = gn.linear_fwd(a["n1"], p["Wqkv"], p["bqkv"])
             q, k, v = (t.contiguous() for t in a["qkv"].view(B, S, 3, H, D).permute(2, 0, 3, 1, 4))
             O, a["lse"] = gn.attn_fwd(q, k, v, causal=True, rope="none", ws=ws)
             a["o"] = O.permute(0, 2, 1, 3).reshape(T, d).contiguous()
             a["ao"] = gn.linear_fwd(a["o"], p["Wo"], p["bo"])
-            a["x2"] = (x + a["ao"]).contiguous()
-            a["n2"], a["m2"], a["r2"] = gn.layernorm_fwd(a["x2"], p["ln2_g"], p["ln2_b"])
+            a["x2"] = (x + a["ao"].float()).contiguous()
+            a["n2"], a["m2"], a["r2"] = gn.layernorm_fwd(a["x2"], p["ln2_g"], p["ln2_b"], out_dtype=bf)
             a["gate"], a["up"], a["h"] = gn.glu_linear_fwd("geglu_up", a["n2"], p["Wg"], p["Wu"],
                                                            p["bg"], p["bu"])
             a["f"] = gn.linear_fwd(a["h"], p["Wd"], p["bd"])
-            a["x3"] = (a["x2"] + a["f"]).contiguous()
+            a["x3"] = (a["x2"] + a["f"].float()).contiguous()
             acts.append(a)
             x = a["x3"]
-        self.nf, self.mf, self.rf = gn.layernorm_fwd(x, self.lnf_g, self.lnf_b)
+        self.nf, self.mf, self.rf = gn.layernorm_fwd(x, self.lnf_g, self.lnf_b, out_dtype=bf)
         self.logits = gn.linear_fwd(self.nf, self.E)
         self.acts = acts
         torch.cuda.synchronize()

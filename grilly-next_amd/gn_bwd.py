@@ -27,14 +27,14 @@ SYMBOLS = [
     "gn_last_error", "gn_version", "gn_linear_bwd", "gn_linear_bwd_ws", "gn_linear_workspace_bytes",
     "gn_gemm", "gn_colsum", "gn_act_bwd", "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_linear_bwd_ws",
     "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd",
-    "gn_layernorm_bwd_noalloc", "gn_rmsnorm_bwd",
+    "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
     "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_vsa_unpack_project_fwd",
     "gn_vsa_fwd_workspace_bytes", "gn_vsa_surrogate_fwd", "gn_embedding_bwd", "gn_binary_bwd",
     "gn_reduce_bwd", "gn_transpose_bwd", "gn_mse_bwd", "gn_vsa_lora_expand_bwd",
     "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_layernorm_fwd",
-    "gn_rmsnorm_fwd", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace",
+    "gn_rmsnorm_fwd", "gn_layernorm_fwd_ex", "gn_rmsnorm_fwd_ex", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace", "gn_convert",
 ]
 BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
 RED = {"sum": 0, "mean": 1}
@@ -82,6 +82,12 @@ _SIGS = {
     "gn_layernorm_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P, _Z, _P], _I),
     "gn_layernorm_bwd_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P], _I),
     "gn_rmsnorm_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _U, _P, _Z, _P], _I),
+    "gn_layernorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _U, _P, _Z,
+                             _P], _I),
+    "gn_rmsnorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _U, _P, _Z, _P], _I),
+    "gn_layernorm_fwd_ex": ([_P, _I, _P, _P, _P, _I, _P, _P, _I, _I, _F, _U, _P], _I),
+    "gn_rmsnorm_fwd_ex": ([_P, _I, _P, _P, _I, _P, _I, _I, _F, _P], _I),
+    "gn_convert": ([_P, _I, _P, _I, _L, _P], _I),
     "gn_norm_workspace_bytes": ([_I, _I], _Z),
     "gn_softmax_bwd": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "gn_xent_bwd": ([_P, _P, _P, _I, _I, _F, _I, _P], _I),
@@ -320,31 +326,53 @@ def norm_workspace_bytes(rows, F):
 
 
 def layernorm_bwd(dY, X, gamma, mean, rstd, eps=1e-5, stat_is_var=False, ws=None,
-                  need_param=True):
+                  need_param=True, dX_add=None, out=None):
+    """(dX, dGamma, dBeta).  dY / gamma may be bf16 under an fp32 X (the _ex entry); dX has
+    X's dtype; dX_add (X's dtype, may be `out`) is added to dX in the same pass."""
     rows, F = X.shape
-    dX = torch.empty_like(X)
+    dX = torch.empty_like(X) if out is None else out
     dG = torch.empty((F,), dtype=torch.float32, device=X.device) if need_param else None
     dB = torch.empty((F,), dtype=torch.float32, device=X.device) if need_param else None
     if ws is None:
         ws = workspace(norm_workspace_bytes(rows, F), X.device)
-    _check(lib().gn_layernorm_bwd(_ptr(dY), _ptr(X), _ptr(gamma), _ptr(mean), _ptr(rstd),
-                                  _ptr(dX), _ptr(dG), _ptr(dB), rows, F, eps, _dt(X),
-                                  LN_STAT_VAR if stat_is_var else 0, _ptr(ws), ws.numel(),
-                                  _stream()), "gn_layernorm_bwd")
+    flags = LN_STAT_VAR if stat_is_var else 0
+    if dX_add is None and dY.dtype == X.dtype:
+        _check(lib().gn_layernorm_bwd(_ptr(dY), _ptr(X), _ptr(gamma), _ptr(mean), _ptr(rstd),
+                                      _ptr(dX), _ptr(dG), _ptr(dB), rows, F, eps, _dt(X), flags,
+                                      _ptr(ws), ws.numel(), _stream()), "gn_layernorm_bwd")
+    else:
+        _check(lib().gn_layernorm_bwd_ex(_ptr(dY), _dt(dY), _ptr(X), _dt(X), _ptr(gamma), _ptr(mean),
+                                         _ptr(rstd), _ptr(dX_add), _ptr(dX), _ptr(dG), _ptr(dB),
+                                         rows, F, eps, flags, _ptr(ws), ws.numel(), _stream()),
+               "gn_layernorm_bwd_ex")
     return dX, dG, dB
 
 
-def rmsnorm_bwd(dY, X, w, rstd, ws=None, need_param=True, dX=None, dW=None):
+def rmsnorm_bwd(dY, X, w, rstd, ws=None, need_param=True, dX=None, dW=None, dX_add=None):
     rows, F = X.shape
     dX = torch.empty_like(X) if dX is None else dX
     if need_param and dW is None:
         dW = torch.empty((F,), dtype=torch.float32, device=X.device)
     if ws is None:
         ws = workspace(norm_workspace_bytes(rows, F), X.device)
-    _check(lib().gn_rmsnorm_bwd(_ptr(dY), _ptr(X), _ptr(w), _ptr(rstd), _ptr(dX),
-                                _ptr(dW) if need_param else None, rows, F, _dt(X), 0, _ptr(ws),
-                                ws.numel(), _stream()), "gn_rmsnorm_bwd")
+    if dX_add is None and dY.dtype == X.dtype:
+        _check(lib().gn_rmsnorm_bwd(_ptr(dY), _ptr(X), _ptr(w), _ptr(rstd), _ptr(dX),
+                                    _ptr(dW) if need_param else None, rows, F, _dt(X), 0, _ptr(ws),
+                                    ws.numel(), _stream()), "gn_rmsnorm_bwd")
+    else:
+        _check(lib().gn_rmsnorm_bwd_ex(_ptr(dY), _dt(dY), _ptr(X), _dt(X), _ptr(w), _ptr(rstd),
+                                       _ptr(dX_add), _ptr(dX), _ptr(dW) if need_param else None,
+                                       rows, F, 0, _ptr(ws), ws.numel(), _stream()),
+               "gn_rmsnorm_bwd_ex")
     return dX, (dW if need_param else None)
+
+
+def convert(src, dtype):
+    """src in another storage dtype (f32 <-> bf16, nearest-even)."""
+    out = torch.empty(src.shape, dtype=dtype, device=src.device)
+    _check(lib().gn_convert(_ptr(src), _dt(src), _ptr(out), _dt(out), src.numel(), _stream()),
+           "gn_convert")
+    return out
 
 
 def softmax_bwd(dY, Y):
@@ -610,25 +638,27 @@ def adamw_step(entries, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=
 
 
 # ---- forward kernels (the saved tensors the backward consumes) ------------------------------
-def layernorm_fwd(X, gamma=None, beta=None, eps=1e-5, save_var=False):
-    """Y, mean, rstd (fp32 [rows]; the variance instead of rstd when save_var)."""
+def layernorm_fwd(X, gamma=None, beta=None, eps=1e-5, save_var=False, out_dtype=None):
+    """Y, mean, rstd (fp32 [rows]; the variance instead of rstd when save_var).  out_dtype:
+    Y's dtype (default X's; bf16 under an fp32 X normalises a residual stream into a bf16
+    block, gamma / beta then bf16)."""
     rows, F = X.shape
-    Y = torch.empty_like(X)
+    Y = torch.empty(X.shape, dtype=out_dtype or X.dtype, device=X.device)
     mean = torch.empty((rows,), dtype=torch.float32, device=X.device)
     rstd = torch.empty((rows,), dtype=torch.float32, device=X.device)
-    _check(lib().gn_layernorm_fwd(_ptr(X), _ptr(gamma), _ptr(beta), _ptr(Y), _ptr(mean),
-                                  _ptr(rstd), rows, F, eps, _dt(X),
-                                  LN_STAT_VAR if save_var else 0, _stream()), "gn_layernorm_fwd")
+    _check(lib().gn_layernorm_fwd_ex(_ptr(X), _dt(X), _ptr(gamma), _ptr(beta), _ptr(Y), _dt(Y),
+                                     _ptr(mean), _ptr(rstd), rows, F, eps,
+                                     LN_STAT_VAR if save_var else 0, _stream()), "gn_layernorm_fwd")
     return Y, mean, rstd
 
 
-def rmsnorm_fwd(X, w=None, eps=1e-6):
+def rmsnorm_fwd(X, w=None, eps=1e-6, out_dtype=None):
     """Y, rstd (fp32 [rows])."""
     rows, F = X.shape
-    Y = torch.empty_like(X)
+    Y = torch.empty(X.shape, dtype=out_dtype or X.dtype, device=X.device)
     rstd = torch.empty((rows,), dtype=torch.float32, device=X.device)
-    _check(lib().gn_rmsnorm_fwd(_ptr(X), _ptr(w), _ptr(Y), _ptr(rstd), rows, F, eps, _dt(X),
-                                _stream()), "gn_rmsnorm_fwd")
+    _check(lib().gn_rmsnorm_fwd_ex(_ptr(X), _dt(X), _ptr(w), _ptr(Y), _dt(Y), _ptr(rstd), rows, F,
+                                   eps, _stream()), "gn_rmsnorm_fwd")
     return Y, rstd
 
 

@@ -193,6 +193,23 @@ int gn_rmsnorm_bwd(const void* dY, const void* X, const void* w, const float* rs
 
 size_t gn_norm_workspace_bytes(int rows, int F);
 
+/* Mixed-precision forms of the two norm backwards (same reference formulas as above) for a
+ * residual stream kept in fp32 under a bf16 block: x, dX and dX_add in x_dtype; dY and
+ * gamma / w in dy_dtype; pairs (f32, f32), (bf16, bf16) and (x f32, dy bf16).
+ *   dX = norm_grad + dX_add    (dX_add nullable; it may alias dX for an in-place sum)
+ * so a pre-norm block's two input gradients (the residual branch and the norm) are summed in
+ * the norm's own pass: the fan-out the reference drops (autograd.cpp:78-86) costs no extra
+ * read or write.  GN_ACCUMULATE here applies to the parameter gradients only; GN_LN_STAT_VAR
+ * as above.  ws: gn_norm_workspace_bytes(rows, F). */
+int gn_layernorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype,
+                        const void* gamma, const float* mean, const float* rstd,
+                        const void* dX_add, void* dX, float* dGamma, float* dBeta, int rows,
+                        int F, float eps, unsigned flags, void* ws, size_t ws_bytes,
+                        void* stream);
+int gn_rmsnorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype, const void* w,
+                      const float* rstd, const void* dX_add, void* dX, float* dW, int rows,
+                      int F, unsigned flags, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- softmax / cross-entropy --------------------------------------------------------- */
 /* activation-softmax-backward.glsl:27-49: dX = Y * (dY - sum_c dY*Y), per row of C. */
 int gn_softmax_bwd(const void* dY, const void* Y, void* dX, int rows, int C, int dtype,
@@ -407,6 +424,14 @@ int gn_layernorm_fwd(const void* X, const void* gamma, const void* beta, void* Y
 int gn_rmsnorm_fwd(const void* X, const void* w, void* Y, float* rstd, int rows, int F, float eps,
                    int dtype, void* stream);
 
+/* The two norm forwards with X in x_dtype and gamma / beta / w and Y in y_dtype (pairs as the
+ * _ex backwards: a residual stream kept in fp32 normalised into a bf16 block). */
+int gn_layernorm_fwd_ex(const void* X, int x_dtype, const void* gamma, const void* beta, void* Y,
+                        int y_dtype, float* mean, float* rstd, int rows, int F, float eps,
+                        unsigned flags, void* stream);
+int gn_rmsnorm_fwd_ex(const void* X, int x_dtype, const void* w, void* Y, int y_dtype, float* rstd,
+                      int rows, int F, float eps, void* stream);
+
 /* Activation forward Y = act(X) over n elements (activation-{relu,gelu,silu}.glsl forward
  * values; the GN_ACT_* kinds: tanh-form GELU by default, erf form, SiLU, tanh, sigmoid).  The
  * backward of GN_ACT_TANH / GN_ACT_SIGMOID then takes this Y, the others take X. */
@@ -434,6 +459,11 @@ int gn_glu_linear_fwd(int kind, const void* X, const void* Wg, const void* Wu, c
 /* out[i] (+)= a[i] (f32/bf16): the fan-out accumulation the reference leaves as a TODO
  * (autograd.cpp:78-86). */
 int gn_add_inplace(void* out, const void* a, int64_t n, int dtype, void* stream);
+
+/* dst = src in another storage type (f32 -> bf16 rounds to nearest-even; bf16 -> f32 exact):
+ * the gradient of a bf16 tensor added into an fp32 stream (an Add node whose inputs differ in
+ * dtype) is the fp32 upstream gradient rounded once. */
+int gn_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

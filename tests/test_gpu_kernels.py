@@ -351,6 +351,67 @@ def test_rmsnorm_bf16(gn, rows, F):
     assert rel_err(host(dW), rW) < 1e-3
 
 
+@pytest.mark.parametrize("rows,F", [(8192, 768), (300, 2048), (77, 3000)])
+@pytest.mark.parametrize("kind", ["layernorm", "rmsnorm"])
+def test_norm_bwd_fp32_stream_with_addend(gn, rows, F, kind):
+    """x, dX and the addend in fp32 under bf16 dy / gamma (the _ex entries), and the addend
+    summed in the same pass: dX = norm_grad(dy) + add, in place (add = dX) too."""
+    r = rng_(71)
+    X = (r.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32)
+    g = rnd((1 + 0.3 * r.standard_normal(F)).astype(np.float32))
+    dY = rnd((r.standard_normal((rows, F)) * 0.1).astype(np.float32))
+    add = r.standard_normal((rows, F)).astype(np.float32)
+    if kind == "layernorm":
+        _, mean, rstd = oracle.layernorm_fwd(X, g)
+        rX, rG, rB = oracle.layernorm_bwd(dY, X, g, mean, rstd)
+        dX, dG, dB = gn.layernorm_bwd(dev(dY, torch.bfloat16), dev(X), dev(g, torch.bfloat16),
+                                      dev(mean), dev(rstd), dX_add=dev(add))
+        assert rel_err(host(dB), rB) < FP32_TOL
+    else:
+        _, rstd = oracle.rmsnorm_fwd(X, g)
+        rX, rG = oracle.rmsnorm_bwd(dY, X, g, rstd)
+        dX, dG = gn.rmsnorm_bwd(dev(dY, torch.bfloat16), dev(X), dev(g, torch.bfloat16), dev(rstd),
+                                dX_add=dev(add))
+    assert dX.dtype == torch.float32
+    assert rel_err(host(dX), rX + add) < FP32_TOL
+    assert rel_err(host(dG), rG) < FP32_TOL
+    # in place: the addend is the output buffer itself
+    buf = dev(add)
+    if kind == "layernorm":
+        gn.layernorm_bwd(dev(dY, torch.bfloat16), dev(X), dev(g, torch.bfloat16), dev(mean),
+                         dev(rstd), dX_add=buf, out=buf)
+    else:
+        gn.rmsnorm_bwd(dev(dY, torch.bfloat16), dev(X), dev(g, torch.bfloat16), dev(rstd),
+                       dX=buf, dX_add=buf)
+    assert rel_err(host(buf), rX + add) < FP32_TOL
+
+
+@pytest.mark.parametrize("rows,F", [(4096, 768), (50, 3000)])
+def test_norm_fwd_fp32_stream_to_bf16(gn, rows, F):
+    r = rng_(72)
+    X = (r.standard_normal((rows, F)) * 3 - 1).astype(np.float32)
+    g = rnd((1 + 0.2 * r.standard_normal(F)).astype(np.float32))
+    b = rnd((0.1 * r.standard_normal(F)).astype(np.float32))
+    Y, mean, rstd = gn.layernorm_fwd(dev(X), dev(g, torch.bfloat16), dev(b, torch.bfloat16),
+                                     out_dtype=torch.bfloat16)
+    rY, rm, rr = oracle.layernorm_fwd(X, g, b)
+    assert Y.dtype == torch.bfloat16 and rel_err(host(Y), rY) < 1e-2
+    assert rel_err(host(mean), rm) < 1e-5 and rel_err(host(rstd), rr) < 1e-5
+    Yr, rs = gn.rmsnorm_fwd(dev(X), dev(g, torch.bfloat16), out_dtype=torch.bfloat16)
+    rYr, rrs = oracle.rmsnorm_fwd(X, g)
+    assert rel_err(host(Yr), rYr) < 1e-2 and rel_err(host(rs), rrs) < 1e-5
+
+
+def test_convert_f32_bf16(gn):
+    r = rng_(73)
+    for n in (1 << 20, 1001):
+        x = torch.from_numpy((r.standard_normal(n) * 100).astype(np.float32)).cuda()
+        x[:4] = torch.tensor([1 + 2 ** -8, 1 + 3 * 2 ** -8, float("inf"), -0.0])  # ties, inf, -0
+        b = gn.convert(x, torch.bfloat16)
+        assert torch.equal(b, x.bfloat16())  # round to nearest-even, as torch
+        assert torch.equal(gn.convert(b, torch.float32), b.float())  # widening is exact
+
+
 # ---------------------------------------------------------------------------- softmax / CE
 def test_softmax_and_xent_golden(gn):
     g = golden("softmax")

@@ -353,7 +353,8 @@ def test_tape_error_paths(env):
 
 def _decoder_reference(m):
     """fp32 torch autograd of the same decoder, rounding to bf16 where the GPU run stores
-    (straight-through), so both differentiate the same bf16-stored forward."""
+    (straight-through), so both differentiate the same bf16-stored forward; the residual
+    stream is fp32 on both sides."""
     import math
     rb = lambda t: t + (t.bfloat16().float() - t).detach()
     leaf = lambda t: t.detach().float().clone().requires_grad_(True)
@@ -372,7 +373,7 @@ def _decoder_reference(m):
         return 0.5 * u * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (u + 0.044715 * u ** 3)))
 
     mask = torch.triu(torch.ones(S, S, dtype=torch.bool, device=E.device), 1)
-    x = rb(E[m.ids.long()])
+    x = E[m.ids.long()]  # bf16 values, carried in fp32
     for p in params:
         n1 = ln(x, p["ln1_g"], p["ln1_b"])
         qkv = rb(n1 @ p["Wqkv"].t() + p["bqkv"])
@@ -380,12 +381,12 @@ def _decoder_reference(m):
         sc = torch.matmul(q, k.transpose(-1, -2).contiguous()) / math.sqrt(D)
         o = torch.matmul(torch.softmax(sc.masked_fill(mask, float("-inf")), -1), v)
         o = rb(o.permute(0, 2, 1, 3).reshape(T, d))
-        x2 = rb(x + rb(o @ p["Wo"].t() + p["bo"]))
+        x2 = x + rb(o @ p["Wo"].t() + p["bo"])
         n2 = ln(x2, p["ln2_g"], p["ln2_b"])
         gate = rb(n2 @ p["Wg"].t() + p["bg"])
         up = rb(n2 @ p["Wu"].t() + p["bu"])
         h = rb(gate * gelu(up))
-        x = rb(x2 + rb(h @ p["Wd"].t() + p["bd"]))
+        x = x2 + rb(h @ p["Wd"].t() + p["bd"])
     logits = rb(ln(x, lnf_g, lnf_b) @ E.t())
     torch.nn.functional.cross_entropy(logits, m.tgt.long()).backward()
     return E, params, lnf_g, lnf_b
@@ -429,14 +430,13 @@ def test_decoder_full_size_through_tape(env):
     """BASELINE configs[4] at its full size (12 layers, d 768, 12 heads, GEGLU 3072, tied
     embedding 32000, B 8 x S 1024): every weight gradient of the first, a middle and the last
     layer, the embedding and the final norm, against fp32 torch autograd of the same
-    bf16-stored forward (normwise relative error <= 2e-2).
+    bf16-stored forward (normwise relative error <= 2e-2 for every tensor).
 
     The second LayerNorm's gain gradient dgamma = sum_rows dy * xhat cancels heavily (its
-    largest entry is ~5 % of sum_rows |dy * xhat| at this size), so the ~1 % that the bf16
-    gradients between the 12 layers leave in its upstream dy (correlated with xhat through the
-    residual stream) becomes ~3 % in dgamma.  For it the test pins the kernel exactly instead
-    (dgamma against the oracle's LayerNorm backward fed the GPU's own upstream dy, <= 1e-4) and
-    bounds the end-to-end error by 5e-2."""
+    largest entry is ~5 % of sum_rows |dy * xhat| at this size); with the residual stream and
+    its gradient in fp32 the error that reaches it stays within the bf16 bound.  The kernel
+    itself is also pinned on its own input: dgamma against the oracle's LayerNorm backward fed
+    the GPU's own upstream dy (<= 1e-4)."""
     gc, gb, dev = env
     import decoder_tape
     m = decoder_tape.Decoder(seed=9)
@@ -476,7 +476,7 @@ def test_decoder_full_size_through_tape(env):
     errs = {k: rel_err(got[k], want[k].cpu().numpy()) for k in got}
     del E, params, lnf_g, want
     torch.cuda.empty_cache()
-    bad = {k: v for k, v in errs.items() if not v < (5e-2 if k.startswith("ln2_g") else 2e-2)}
+    bad = {k: v for k, v in errs.items() if not v < 2e-2}
     assert not bad, f"relative errors above the bound: {bad} (all: {errs})"
 
 
