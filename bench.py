@@ -18,9 +18,11 @@ Other BASELINE configs (parity-tested, measured with --workload):
     mlp   configs[0]: MLP 784->256->10 fp32 B=64 through the tape engine (grilly_core)
     decoder configs[4]: 12-layer decoder (d 768, GEGLU, tied embedding 32000, CE), B8 x S1024,
           end-to-end backward through the tape engine
+    hyper the reference's VSA hypernetwork training step (grilly_core.vsa_training_step) at
+          its defaults (K 16, 1.0 GB output layer), batch 1
 Each prints one JSON line of the same shape; the default (ffn) is the headline metric.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ffn|attn|vsa|mlp|decoder]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ffn|attn|vsa|mlp|decoder|hyper]
 """
 import argparse
 import json
@@ -45,7 +47,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--cpu-tokens", type=int, default=T)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", default="ffn", choices=["ffn", "attn", "vsa", "mlp", "decoder"])
+    p.add_argument("--workload", default="ffn", choices=["ffn", "attn", "vsa", "mlp", "decoder", "hyper"])
     p.add_argument("--calib-copy", action="store_true",
                    help="after the timed region, launch one gn_add_inplace over 2^28 floats "
                         "(reads 2 GiB, writes 1 GiB): the reference dispatch that scales the "
@@ -56,10 +58,19 @@ def parse():
     p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                         "'bench.py --calib-copy' into the HBM traffic of the dominant kernel")
+    p.add_argument("--pmc-sq", metavar="DIR",
+                   help="summarise a rocprofv3 --pmc run of SQ_INSTS_VALU SQ_INSTS_MFMA "
+                        "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE per kernel (VALU instructions "
+                        "per MFMA, MFMA busy share of the SIMD cycles)")
+    p.add_argument("--pmc-kernel", default=DOMINANT_KERNEL_RE,
+                   help="regex of the kernel name --pmc-summary reports (default: the FFN "
+                        "headline's dominant kernel, the [dWg;dWu] weight-gradient GEMM)")
     return p.parse_args()
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_dn_gemm_hbm_traffic.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_dominant_gemm_hbm_traffic.txt")
+# the [dWg;dWu] GEMM: transposed A (gu^T), fp32 C, 256 x 128 tiles, three LDS stages
+DOMINANT_KERNEL_RE = r"gemm_core<true, false, float, 256, 128, 0, 3[,>]"
 CALIB_FLOATS = 1 << 28
 
 
@@ -71,9 +82,9 @@ def calib_copy(torch, gn):
     torch.cuda.synchronize()
 
 
-def pmc_summary(fetch_dir, write_dir):
-    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the dominant GEMM and of the calibration
-    add (known bytes) -> scaled HBM bytes per launch of the dominant GEMM."""
+def pmc_summary(fetch_dir, write_dir, kernel_re):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the dominant kernel (kernel_re) and of the
+    calibration add (known bytes) -> scaled HBM bytes per launch of the dominant kernel."""
     import csv
     import glob
     import re
@@ -93,9 +104,7 @@ def pmc_summary(fetch_dir, write_dir):
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         tab = load(d, counter)
         calib = [v for (k, g), v in tab.items() if "add_kernel" in k]
-        # the dN GEMM: gemm_core kernel, plain epilogue, no transposes, grid of 4096 x 2048 tiles
-        gemm = {(k, g): v for (k, g), v in tab.items()
-                if re.search(r"gemm_core<false, false, unsigned short, \d+, \d+, 0[,>]", k)}
+        gemm = {(k, g): v for (k, g), v in tab.items() if re.search(kernel_re, k)}
         if not calib or not gemm:
             raise SystemExit(f"{counter}: calibration or GEMM dispatches not found in {d}")
         cvals = [x for v in calib for x in v.values()]
@@ -110,19 +119,51 @@ def pmc_summary(fetch_dir, write_dir):
         b = gkib * 1024.0 * factor
         total += b
         lines.append(f"{counter}: calibration add {ckib:.0f} KiB/dispatch (expected "
-                     f"{known[counter] / 1024:.0f} KiB) -> factor {factor:.4f}; dominant GEMM "
+                     f"{known[counter] / 1024:.0f} KiB) -> factor {factor:.4f}; dominant kernel "
                      f"{gkib:.0f} KiB/dispatch over {n} dispatches -> {b / 1e6:.1f} MB")
     lines.append(f"kernel: {res['FETCH_SIZE'][3][:120]} grid {res['FETCH_SIZE'][4]}")
     lines.append(f"traffic_bytes_per_launch: {total:.0f}")
     print("\n".join(lines))
 
 
+def pmc_sq_summary(d, xcds=8, cus=256, simds=4):
+    """Per gn:: kernel, per dispatch means of the four counters and two ratios:
+    VALU / MFMA instructions, and MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x
+    CUs x SIMDs per CU): the share of SIMD cycles the matrix cores are busy while the kernel
+    runs.  On gfx950 SQ_VALU_MFMA_BUSY_CYCLES reads 32 cycles per v_mfma_f32_32x32x16_bf16 (its
+    issue cost at the dense peak) and GRBM_GUI_ACTIVE is summed over the 8 XCDs."""
+    import csv
+    import glob
+    tab = {}
+    for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            k = r["Kernel_Name"]
+            if "gn::" not in k:
+                continue
+            ent = tab.setdefault(k, {}).setdefault(r["Dispatch_Id"], {})
+            ent[r["Counter_Name"]] = ent.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    rows = []
+    for k, disp in tab.items():
+        n = len(disp)
+        mean = lambda c: sum(v.get(c, 0.0) for v in disp.values()) / n
+        valu, mfma = mean("SQ_INSTS_VALU"), mean("SQ_INSTS_MFMA")
+        busy, gui = mean("SQ_VALU_MFMA_BUSY_CYCLES"), mean("GRBM_GUI_ACTIVE")
+        rows.append((k, n, valu, mfma, valu / mfma if mfma else float("nan"),
+                     busy / (gui / xcds * cus * simds) if gui else float("nan")))
+    rows.sort(key=lambda r: -r[3])
+    print("# dispatches  VALU_insts  MFMA_insts  VALU/MFMA  MFMA_busy  kernel")
+    for k, n, valu, mfma, ratio, busy in rows:
+        print(f"{n:6d} {valu:14.4g} {mfma:12.4g} {ratio:9.2f} {100 * busy:9.1f}%  {k[:110]}")
+
+
 def ceilings(torch, gn):
-    """Measured ceilings: gn_probe_mfma (no memory traffic) and gn_probe_copy (2 GiB)."""
+    """Measured ceilings: gn_probe_mfma (no memory traffic) and gn_probe_copy (2 GiB, every
+    access mode; the best copy and the read-only stream are reported)."""
     import ctypes
     lib = gn.lib()
     lib.gn_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    lib.gn_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.gn_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                  ctypes.c_void_p]
     dev = torch.device("cuda:0")
     blocks, iters = 4096, 2000
     out = torch.empty(blocks * 256, device=dev)
@@ -133,13 +174,18 @@ def ceilings(torch, gn):
     nbytes = 1 << 31
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
-    cp = timed(torch, lambda: gn._check(lib.gn_probe_copy(dst.data_ptr(), src.data_ptr(), nbytes, s),
-                                        "gn_probe_copy"), 10, 3)
+    modes = {}
+    for mode, name in ((0, "copy_nt_x4"), (1, "copy_x4"), (2, "copy_x8"), (3, "read_nt_x8")):
+        ms = timed(torch, lambda: gn._check(lib.gn_probe_copy(dst.data_ptr(), src.data_ptr(), nbytes,
+                                                              mode, s), "gn_probe_copy"), 10, 3)
+        moved = (2.0 if mode < 3 else 1.0) * nbytes
+        modes[name] = round(moved / (ms * 1e-3) / 1e9, 1)
+    best_copy = max(v for k, v in modes.items() if k.startswith("copy"))
     return {"mfma_bf16_tflops": round(flops / (mf * 1e-3) / 1e12, 1),
-            "mfma_spec_tflops": BF16_PEAK_TFLOPS,
-            "copy_gbs": round(2.0 * nbytes / (cp * 1e-3) / 1e9, 1), "hbm_spec_gbs": HBM_PEAK_GBS,
+            "mfma_spec_tflops": BF16_PEAK_TFLOPS, "copy_gbs": best_copy,
+            "read_gbs": modes["read_nt_x8"], "copy_modes_gbs": modes, "hbm_spec_gbs": HBM_PEAK_GBS,
             "probe": f"gn_probe_mfma {blocks} blocks x {iters} x 8 MFMA per wave; "
-                     f"gn_probe_copy {nbytes >> 30} GiB read + written"}
+                     f"gn_probe_copy {nbytes >> 30} GiB per mode (copies: read + written)"}
 
 
 def traffic_from_profile():
@@ -194,18 +240,22 @@ def bench_attn(args, torch, gn):
     tf = flops / (ms * 1e-3) / 1e12
     cpu = None
     if not args.no_cpu:
-        import oracle
+        from oracle import cpu_ref
         r = np.random.default_rng(3)
-        Bs, Hs, Ss = B, H, S  # the whole workload
-        q, k, v = (r.standard_normal((Bs, Hs, Ss, D)).astype(np.float32) for _ in range(3))
-        do = (r.standard_normal((Bs, Hs, Ss, D)) * 1e-2).astype(np.float32)
-        o, lse = oracle.attn_fwd(q, k, v)
-        t0 = time.perf_counter()
-        oracle.attn_bwd(q, k, v, do, lse)
-        dt = time.perf_counter() - t0
-        cpu = {"value": round(5 * 2.0 * Ss * Ss * D * 0.5 * Bs * Hs / dt / 1e12, 6), "unit": "TFLOP/s",
-               "cores": oracle.num_threads(), "kind": "port",
-               "sample": f"{Bs} x {Hs} heads x S={Ss}, the whole workload (oracle C/OpenMP fp64), {dt:.2f} s"}
+        Hs = 8  # 8 of the 64 (b, h) heads: P is S x S fp32 per head
+        q, k, v = (r.standard_normal((Hs, S, D)).astype(np.float32) for _ in range(3))
+        do = (r.standard_normal((Hs, S, D)) * 1e-2).astype(np.float32)
+        nt = cpu_ref.threads()
+        with cpu_ref.limit_threads(nt):
+            cpu_ref.attention_step(q[:1], k[:1], v[:1], do[:1], D ** -0.5)
+            t0 = time.perf_counter()
+            cpu_ref.attention_step(q, k, v, do, D ** -0.5)
+            dt = time.perf_counter() - t0
+        cpu = {"value": round(5 * 2.0 * S * S * D * 0.5 * Hs / dt / 1e12, 5), "unit": "TFLOP/s",
+               "cores": nt, "kind": "port",
+               "sample": f"{Hs} of {B * H} heads at S={S}, numpy fp32 with P materialised (the "
+                         f"reference's CPU path, autograd_core.py:617-654; no RoPE there), "
+                         f"{dt:.2f} s; algorithmic causal FLOPs", "cpu_model": cpu_ref.cpu_model()}
     out = line("causal attention backward with RoPE (algorithmic TFLOP/s)", round(tf, 2),
                "TFLOP/s", args, ms, "bf16",
                {"workload": "C3 causal attention bwd + RoPE(1e4), B4 H16 S2048 D128",
@@ -257,16 +307,20 @@ def bench_vsa(args, torch, gn):
     gbs = bytes_s / (ms_s * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu:
-        import oracle
-        Bs = 4096  # half the rows: about 8 s of the oracle on the host
+        from oracle import cpu_ref
+        Bs = 2048  # a quarter of the rows
         bh = r.integers(0, 2**32, size=(Bs, words), dtype=np.uint64).astype(np.uint32)
         dy = r.standard_normal((Bs, O)).astype(np.float32)
-        t0 = time.perf_counter()
-        oracle.vsa_unpack_project_bwd(dy, bh, D)
-        dt = time.perf_counter() - t0
-        cpu = {"value": round(2.0 * O * D * Bs / dt / 1e12, 6), "unit": "TFLOP/s",
-               "cores": oracle.num_threads(), "kind": "port",
-               "sample": f"{Bs} of {Bn} rows of the dW contraction (oracle C/OpenMP fp64), {dt:.2f} s"}
+        nt = cpu_ref.threads()
+        with cpu_ref.limit_threads(nt):
+            t0 = time.perf_counter()
+            cpu_ref.vsa_unpack_project_backward(dy, bh, D)
+            dt = time.perf_counter() - t0
+        cpu = {"value": round(2.0 * O * D * Bs / dt / 1e12, 5), "unit": "TFLOP/s", "cores": nt,
+               "kind": "port",
+               "sample": f"{Bs} of {Bn} rows: unpack to +-1 and dY^T S in numpy fp32 (the shader's "
+                         f"formula in the reference's numpy style), {dt:.2f} s",
+               "cpu_model": cpu_ref.cpu_model()}
     out = line("VSA unpack-project dW backward (algorithmic TFLOP/s)", round(tf, 2), "TFLOP/s",
                args, ms, "f32 (bf16x2 split MFMA)",
                {"workload": "C4 VSA unpack-project bwd: 8192 x 10240 bits -> 768, fp32 dY",
@@ -331,27 +385,23 @@ def bench_mlp(args, torch, gn):
 
 
 def mlp_cpu_baseline(X, y, W1, W2, Z, H, L):
-    """The same C1 backward (CE with scale 1, Linear 2 with dX, ReLU, Linear 1 without dX) on
-    the oracle (C, OpenMP), timed on this host: median of 200 steps after 20 warm-up steps."""
-    import oracle
-
-    def step():
-        dL = oracle.xent_bwd(L, y, 1.0)
-        dH, _, _ = oracle.linear_bwd(dL, H, W2)
-        dZ = oracle.act_bwd("relu", dH, Z)
-        oracle.linear_bwd(dZ, X, W1, need_dx=False)
-
-    for _ in range(20):
-        step()
-    ts = []
-    for _ in range(200):
-        t0 = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t0)
+    """The same C1 backward (CE with scale 1, Linear 2 with dX, ReLU, Linear 1 without dX) in
+    numpy fp32 (oracle/cpu_ref.py), timed on this host: median of 200 after 20 warm-up steps."""
+    from oracle import cpu_ref
+    nt = cpu_ref.threads()
+    with cpu_ref.limit_threads(nt):
+        for _ in range(20):
+            cpu_ref.mlp_step(X, y, W1, W2, Z, H, L)
+        ts = []
+        for _ in range(200):
+            t0 = time.perf_counter()
+            cpu_ref.mlp_step(X, y, W1, W2, Z, H, L)
+            ts.append(time.perf_counter() - t0)
     us = float(np.median(ts)) * 1e6
-    return {"value": round(us, 2), "unit": "us", "cores": oracle.num_threads(), "kind": "port",
-            "sample": "the whole B=64 step (oracle C/OpenMP, fp64 accumulation), median of 200 "
-                      "after 20 warm-up steps"}
+    return {"value": round(us, 2), "unit": "us", "cores": nt, "kind": "port",
+            "sample": "the whole B=64 step in numpy fp32 (the reference's CPU path, "
+                      "autograd_core.py:486-554), median of 200 after 20 warm-up steps",
+            "cpu_model": cpu_ref.cpu_model()}
 
 
 def bench_decoder(args, torch, gn):
@@ -415,8 +465,9 @@ def decoder_optimizer_step(torch, gn, m):
 
 
 def decoder_cpu_baseline(m):
-    """Oracle (C, OpenMP, fp64 accumulation) on one layer's backward at full size, scaled
-    to 12 layers plus the LM head by FLOPs (the head timed as its share of the layer)."""
+    """One full-size layer's backward in numpy fp32 (oracle/cpu_ref.py: the reference's CPU
+    formulas, attention with P materialised), scaled by FLOPs to 12 layers plus the LM head."""
+    from oracle import cpu_ref
     import oracle
     T, d, ff, H, B, S = m.T, m.d, m.ff, m.H, m.B, m.S
     D = d // H
@@ -427,31 +478,119 @@ def decoder_cpu_baseline(m):
     Wqkv, Wo, Wg, Wu, Wd = (f(3 * d, d) * 0.02, f(d, d) * 0.02, f(ff, d) * 0.02, f(ff, d) * 0.02,
                             f(d, ff) * 0.02)
     n1, m1, r1 = oracle.layernorm_fwd(x, g1)
+    v1 = (1.0 / r1.astype(np.float64) ** 2 - 1e-5).astype(np.float32)[:, None]
     qkv = oracle.linear_fwd(n1, Wqkv)
     q, k, v = (np.ascontiguousarray(t) for t in qkv.reshape(B, S, 3, H, D).transpose(2, 0, 3, 1, 4))
-    o, lse = oracle.attn_fwd(q, k, v, causal=True, rope_mode="none")
-    o2 = np.ascontiguousarray(o.transpose(0, 2, 1, 3).reshape(T, d))
-    n2, m2, r2 = oracle.layernorm_fwd(x, g1)
-    gate, up = oracle.linear_fwd(n2, Wg), oracle.linear_fwd(n2, Wu)
+    q, k, v = (t.reshape(B * H, S, D) for t in (q, k, v))
+    gate, up = oracle.linear_fwd(n1, Wg), oracle.linear_fwd(n1, Wu)
     h = oracle.glu_fwd("geglu_up", gate, up)
-    t0 = time.perf_counter()
-    dH, _, _ = oracle.linear_bwd(dY, h, Wd)
-    dG, dU = oracle.glu_bwd("geglu_up", dH, gate, up)
-    dN2 = oracle.linear_bwd(dG, n2, Wg)[0] + oracle.linear_bwd(dU, n2, Wu)[0]
-    oracle.layernorm_bwd(dN2, x, g1, m2, r2)
-    dO2, _, _ = oracle.linear_bwd(dY, o2, Wo)
-    dO4 = np.ascontiguousarray(dO2.reshape(B, S, H, D).transpose(0, 2, 1, 3))
-    oracle.attn_bwd(q, k, v, dO4, lse, causal=True, rope_mode="none")
-    dQKV = (f(T, 3 * d) * 1e-2).astype(np.float32)  # the layout change back is not timed work
-    dN1, _, _ = oracle.linear_bwd(dQKV, n1, Wqkv)
-    oracle.layernorm_bwd(dN1, x, g1, m1, r1)
-    dt = time.perf_counter() - t0
+    o2 = (f(T, d) * 0.1).astype(np.float32)
+    nt = cpu_ref.threads()
+    with cpu_ref.limit_threads(nt):
+        t0 = time.perf_counter()
+        dH, _, _ = cpu_ref.linear_backward(dY, h, Wd)
+        t = np.tanh(np.float32(np.sqrt(2 / np.pi)) * (up + np.float32(0.044715) * up ** 3))
+        gl = 0.5 * up * (1 + t)
+        dG = dH * gl
+        dU = cpu_ref.gelu_tanh_backward(dH * gate, up)
+        dN2 = cpu_ref.linear_backward(dG, n1, Wg)[0] + cpu_ref.linear_backward(dU, n1, Wu)[0]
+        cpu_ref.layernorm_backward(dN2, x, g1, m1[:, None], v1)
+        dO2, _, _ = cpu_ref.linear_backward(dY, o2, Wo)
+        dO4 = np.ascontiguousarray(dO2.reshape(B, S, H, D).transpose(0, 2, 1, 3)).reshape(B * H, S, D)
+        cpu_ref.attention_step(q, k, v, dO4, D ** -0.5)
+        dQKV = (f(T, 3 * d) * 1e-2).astype(np.float32)  # the layout change back is not timed work
+        dN1, _, _ = cpu_ref.linear_backward(dQKV, n1, Wqkv)
+        cpu_ref.layernorm_backward(dN1, x, g1, m1[:, None], v1)
+        dt = time.perf_counter() - t0
     layer_flops = (m.flops() - 2 * 2 * T * d * m.V) / m.L
     step_s = dt * (m.L + 2 * 2 * T * d * m.V / layer_flops)
-    return {"value": round(T / step_s, 2), "unit": "tokens/s", "cores": oracle.num_threads(),
-            "kind": "port",
-            "sample": f"one full-size layer backward (T={T}) on the oracle (C/OpenMP, fp64 "
-                      f"accumulation), {dt:.1f} s, scaled by FLOPs to {m.L} layers + LM head"}
+    return {"value": round(T / step_s, 2), "unit": "tokens/s", "cores": nt, "kind": "port",
+            "sample": f"one full-size layer backward (T={T}) in numpy fp32 (the reference's CPU "
+                      f"path, autograd_core.py:486-654, attention with P materialised), {dt:.1f} s, "
+                      f"scaled by FLOPs to {m.L} layers + LM head", "cpu_model": cpu_ref.cpu_model()}
+
+
+def bench_hyper(args, torch, gn):
+    """The reference's VSA hypernetwork training step (vsa_training_step, bindings.cpp:
+    3140-3286) at its defaults: d_model 768, vsa_dim 10240, K 16, router 32 (W2 = 16 x 10240 x
+    1536 fp32 = 1.0 GB), one bitpacked state per step.  One step = upload, forward, loss forward
+    (one 64-byte readback, as the reference), backward, surprise-momentum update, end."""
+    import grilly_core as gc
+    import grilly_bridge as gb
+    dev = gc.Device(0)
+    gb.attach_torch_stream(dev)
+    d, v, K = 768, 10240, 16
+    model = gc.VSAHypernetwork(dev)
+    opt = gc.SurpriseMomentumOptimizer(dev, model)
+    tape = gc.TapeContext(dev)
+    rng = np.random.RandomState(42)
+    state = rng.randint(0, 2 ** 32, size=v // 32, dtype=np.uint32)
+    delta = rng.randint(0, 2 ** 32, size=v // 32, dtype=np.uint32)
+    ms = timed(torch, lambda: gc.vsa_training_step(dev, tape, model, state, delta, opt),
+               args.steps, args.warmup)
+    # the same step composed call by call with HIP events between the phases
+    sizes = model.parameter_sizes()
+    n_upd = sum(sizes[:6])
+    phases = [("forward: unpack-project, Linear 768->1536, GELU, Linear 1536->163840 (skinny fp32)",
+               4.0 * (sizes[0] + sizes[2] + sizes[4]) + 4.0 * (d + 2 * 1536 + K * v)),
+              ("backward: surrogate, Linear 2 (dX, dW2, db2), GELU, Linear 1, unpack-project",
+               4.0 * (2 * sizes[4] + 2 * K * v + 2 * sizes[2] + sizes[0])),
+              ("surprise-momentum update of the six parameters with gradients (read W, g, s_bar; "
+               "write W, s_bar)", 20.0 * n_upd)]
+    mk = lambda: torch.cuda.Event(enable_timing=True)
+    acc = [0.0, 0.0, 0.0]
+    reps = max(3, args.steps // 2)
+    for it in range(reps + 1):
+        ev = [mk() for _ in range(5)]
+        tape.begin()
+        s = gc.upload_bitpacked(tape, state)
+        ev[0].record()
+        pred = model.forward(tape, s)
+        ev[1].record()
+        dl = gc.upload_bitpacked(tape, delta)
+        node = gc.record_surrogate_loss(tape, pred, dl)
+        gc.vsa_loss_forward(tape, node, model.gumbel_seed, model.gumbel_counter)
+        ev[2].record()
+        tape.backward(node, 0)
+        ev[3].record()
+        opt.apply(tape)
+        ev[4].record()
+        torch.cuda.synchronize()
+        tape.end()
+        if it:
+            for j, (a, b) in enumerate(((0, 1), (2, 3), (3, 4))):
+                acc[j] += ev[a].elapsed_time(ev[b]) / reps
+    kernels = []
+    for (name, byts), t in zip(phases, acc):
+        gbs = byts / (t * 1e-3) / 1e9
+        kernels.append({"call": name, "bound": "hbm", "ms": round(t, 4), "achieved": round(gbs, 1),
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "work": byts})
+    dom = max(kernels, key=lambda k: k["ms"])
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_ref
+        W = [gb.download(dev, i, (n,)) for i, n in zip(model.parameter_buffer_ids(), sizes)]
+        sb = [np.zeros_like(w) for w in W]
+        nt = cpu_ref.threads()
+        with cpu_ref.limit_threads(nt):
+            t0 = time.perf_counter()
+            cpu_ref.hypernet_step(W, state[None], delta[None], d, v, K, sb)
+            dt = time.perf_counter() - t0
+        cpu = {"value": round(1.0 / dt, 3), "unit": "steps/s", "cores": nt, "kind": "port",
+               "sample": f"one full step in numpy fp32 (oracle/cpu_ref.py hypernet_step: the "
+                         f"reference's CPU formulas), {dt:.2f} s", "cpu_model": cpu_ref.cpu_model()}
+    out = line("VSA hypernetwork training steps/s (vsa_training_step at the reference defaults)",
+               round(1e3 / ms, 2), "steps/s", args, ms, "f32",
+               {"workload": "H22 vsa_training_step: d_model 768, vsa_dim 10240, K 16, router 32, "
+                            "batch 1 (W2 1.0 GB fp32), surprise-momentum optimizer",
+                "params": int(sum(sizes)), "parallelism": "none (1 GPU)"},
+               {"kernel": dom["call"], "bound": "hbm", "achieved": dom["achieved"],
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"], "launch_ms": dom["ms"],
+                "traffic": None,
+                "timing": "HIP events around the phase inside the composed step, mean"}, cpu)
+    out["kernels"] = kernels
+    out["step_bytes"] = sum(p[1] for p in phases)
+    return out
 
 
 def make_inputs(torch, dev):
@@ -475,7 +614,9 @@ def make_inputs(torch, dev):
 
 
 class Step:
-    """The timed backward step; all buffers preallocated (no allocation inside)."""
+    """The timed backward step; all buffers preallocated (no allocation inside).  Each GEMM of
+    the block is its own C-ABI call (the fused entry points take NULL for the half they skip),
+    so HIP events between the calls time every kernel inside the timed steps."""
 
     def __init__(self, gn, torch, d):
         self.gn, self.d = gn, d
@@ -490,47 +631,56 @@ class Step:
         self.dw = torch.empty(DM, device=dev, dtype=f32)
         self.ws = gn.workspace(gn.norm_workspace_bytes(T, DM), dev)
 
-    def __call__(self):
+    # (call, kernels, bound, algorithmic work per call: FLOP or bytes)
+    CALLS = [
+        ("down-projection GEMM with the SwiGLU backward in its epilogue: gu = glu'(dY Wd), "
+         "4096x5632x2048", "gemm_core (epi 1)", "mfma", 2.0 * T * HID * DM),
+        ("dWd = dY^T A, 2048x5632x4096", "gemm_core (fp32 C)", "mfma", 2.0 * DM * HID * T),
+        ("dN = [dG|dU] [Wg;Wu], 4096x2048x11264", "gemm_core (bf16 C)", "mfma", 2.0 * T * DM * 2 * HID),
+        ("[dWg;dWu] = [dG|dU]^T N, 11264x2048x4096", "gemm_core (fp32 C)", "mfma", 2.0 * 2 * HID * DM * T),
+        ("RMSNorm backward 4096x2048 (rows + parameter partials)", "norm_bwd_rows + colsum_partials",
+         "hbm", 3.0 * T * DM * 2 + 4.0 * T),
+    ]
+
+    def __call__(self, ev=None):
         gn, d, P, s = self.gn, self.d, self.gn._ptr, self.gn._stream()
         L = gn.lib()
+        rec = (lambda i: ev[i].record()) if ev else (lambda i: None)
+        rec(0)
         gn._check(L.gn_ffn_down_glu_bwd(gn.GLU["swiglu_up"], P(d["dY"]), P(d["a"]), P(d["Wd"]),
-                                        P(d["gate"]), P(d["up"]), P(self.gu), P(self.dWd), None,
+                                        P(d["gate"]), P(d["up"]), P(self.gu), None, None,
                                         T, DM, HID, gn.BF16, 0, s), "ffn_down_glu_bwd")
+        rec(1)
+        gn._check(L.gn_linear_bwd(P(d["dY"]), P(d["a"]), P(d["Wd"]), None, P(self.dWd), None, T, DM,
+                                  HID, gn.BF16, 0, s), "linear_bwd (dWd)")
+        rec(2)
         gn._check(L.gn_glu_proj_bwd(P(self.gu), P(d["n"]), P(d["Wg"]), P(d["Wu"]), P(self.dN),
+                                    None, None, None, None, T, DM, HID, gn.BF16, 0, s), "glu_proj_bwd (dN)")
+        rec(3)
+        gn._check(L.gn_glu_proj_bwd(P(self.gu), P(d["n"]), P(d["Wg"]), P(d["Wu"]), None,
                                     P(self.dWg), P(self.dWu), None, None, T, DM, HID, gn.BF16, 0,
-                                    s), "glu_proj_bwd")
+                                    s), "glu_proj_bwd (dWg, dWu)")
+        rec(4)
         gn._check(L.gn_rmsnorm_bwd(P(self.dN), P(d["x"]), P(d["w"]), P(d["rstd"]), P(self.dx),
                                    P(self.dw), T, DM, gn.BF16, 0, P(self.ws), self.ws.numel(), s),
                   "rmsnorm_bwd")
+        rec(5)
 
 
-def time_dominant(gn, torch, st, reps=20):
-    """HIP-event timing of the dominant GEMM launch: dN = dG Wg + dU Wu (K = 2*5632)."""
-    d = st.d
-    dG = st.gu[:, :HID].contiguous()
-    dU = st.gu[:, HID:].contiguous()
-    P, L = gn._ptr, gn.lib()
-    stream = torch.cuda.current_stream()
-
-    def launch():
-        gn._check(L.gn_gemm(P(dG), P(d["Wg"]), HID, P(dU), P(d["Wu"]), HID, P(st.dN), T, DM, 0, 0,
-                            gn.BF16, gn.BF16, 0, gn._stream()), "gemm")
-    for _ in range(3):
-        launch()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        launch()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    flops = 2.0 * T * DM * (2 * HID)
-    return ms, flops
+def kernel_breakdown(calls, evs):
+    """Per-call mean ms over the timed steps from the events recorded between the calls."""
+    out = []
+    for i, (name, kern, bound, work) in enumerate(calls):
+        ms = sum(e[i].elapsed_time(e[i + 1]) for e in evs) / len(evs)
+        rate = work / (ms * 1e-3) / (1e12 if bound == "mfma" else 1e9)
+        peak = BF16_PEAK_TFLOPS if bound == "mfma" else HBM_PEAK_GBS
+        out.append({"call": name, "kernels": kern, "bound": bound, "ms": round(ms, 4),
+                    "achieved": round(rate, 1), "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                    "frac": round(rate / peak, 4), "work": work})
+    return out
 
 
-def cpu_baseline(tokens):
-    """Oracle (C, OpenMP, fp64 accumulation) on `tokens` rows of the same workload."""
-    import oracle
+def ffn_inputs_host(tokens):
     r = np.random.default_rng(2)
     x = r.standard_normal((tokens, DM)).astype(np.float32)
     w = np.ones(DM, np.float32)
@@ -538,6 +688,38 @@ def cpu_baseline(tokens):
     Wu = (r.standard_normal((HID, DM)) * 0.02).astype(np.float32)
     Wd = (r.standard_normal((DM, HID)) * 0.02).astype(np.float32)
     dY = (r.standard_normal((tokens, DM)) * 1e-2).astype(np.float32)
+    return x, w, Wg, Wu, Wd, dY
+
+
+def cpu_baseline(tokens):
+    """The reference's CPU path (numpy fp32 restatement of autograd_core.py:486-654 with the
+    SwiGLU / RMSNorm formulas, oracle/cpu_ref.py) on the whole FFN-block backward: median of 5
+    after one warm-up, BLAS threads = the host's CPU share."""
+    from oracle import cpu_ref
+    import oracle
+    x, w, Wg, Wu, Wd, dY = ffn_inputs_host(tokens)
+    n, rstd = oracle.rmsnorm_fwd(x, w)
+    gate, up = oracle.linear_fwd(n, Wg), oracle.linear_fwd(n, Wu)
+    a = oracle.glu_fwd("swiglu_up", gate, up)
+    nt = cpu_ref.threads()
+    with cpu_ref.limit_threads(nt):
+        cpu_ref.ffn_block_step(x, w, rstd, n, gate, up, a, Wg, Wu, Wd, dY)
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            cpu_ref.ffn_block_step(x, w, rstd, n, gate, up, a, Wg, Wu, Wd, dY)
+            ts.append(time.perf_counter() - t0)
+    dt = float(np.median(ts))
+    return {"value": round(tokens / dt, 1), "unit": "tokens/s", "cores": nt, "kind": "port",
+            "sample": f"the whole {tokens}-token FFN-block backward in numpy fp32 (the reference's "
+                      f"CPU path, autograd_core.py:486-654 restated in oracle/cpu_ref.py), median "
+                      f"of 5: {dt:.3f} s", "cpu_model": cpu_ref.cpu_model()}
+
+
+def oracle_timing(tokens):
+    """The C oracle (fp64 accumulation, OpenMP) on `tokens` rows: the checker, timed apart."""
+    import oracle
+    x, w, Wg, Wu, Wd, dY = ffn_inputs_host(tokens)
     n, rstd = oracle.rmsnorm_fwd(x, w)
     gate, up = oracle.linear_fwd(n, Wg), oracle.linear_fwd(n, Wu)
     a = oracle.glu_fwd("swiglu_up", gate, up)
@@ -548,13 +730,17 @@ def cpu_baseline(tokens):
     dN2, _, _ = oracle.linear_bwd(dU, n, Wu, need_db=False)
     oracle.rmsnorm_bwd(dN1 + dN2, x, w, rstd)
     dt = time.perf_counter() - t0
-    return tokens / dt, oracle.num_threads(), dt
+    return {"value": round(tokens / dt, 2), "unit": "tokens/s", "threads": oracle.num_threads(),
+            "sample": f"{tokens} tokens on the C oracle (fp64 accumulation), {dt:.2f} s"}
 
 
 def main():
     args = parse()
     if args.pmc_summary:
-        pmc_summary(*args.pmc_summary)
+        pmc_summary(*args.pmc_summary, args.pmc_kernel)
+        return
+    if args.pmc_sq:
+        pmc_sq_summary(args.pmc_sq)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the backward "
@@ -568,7 +754,7 @@ def main():
         return
     if args.workload != "ffn":
         fn = {"attn": bench_attn, "vsa": bench_vsa, "mlp": bench_mlp,
-              "decoder": bench_decoder}[args.workload]
+              "decoder": bench_decoder, "hyper": bench_hyper}[args.workload]
         print(json.dumps(fn(args, torch, gn)))
         return
     dev = torch.device("cuda:0")
@@ -578,26 +764,27 @@ def main():
         st()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    mk = lambda: torch.cuda.Event(enable_timing=True)
+    evs = [[mk() for _ in range(len(Step.CALLS) + 1)] for _ in range(args.steps)]
+    e0, e1 = mk(), mk()
     t0 = time.perf_counter()
     e0.record(stream)
-    for _ in range(args.steps):
-        st()
+    for i in range(args.steps):
+        st(evs[i])
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
-    dom_ms, dom_flops = time_dominant(gn, torch, st)
+    kernels = kernel_breakdown(Step.CALLS, evs)
     if args.calib_copy:
         calib_copy(torch, gn)
-    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    dom = max(kernels, key=lambda k: k["ms"])
     flops_step = 6 * 2.0 * T * DM * HID
     cpu = None
+    extra = {}
     if not args.no_cpu:
-        v, cores, dt = cpu_baseline(args.cpu_tokens)
-        cpu = {"value": round(v, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-               "sample": f"{args.cpu_tokens} of {T} tokens of the same FFN-block backward "
-                         f"(oracle C/OpenMP, fp64 accumulation), {dt:.2f} s"}
+        cpu = cpu_baseline(args.cpu_tokens)
+        extra["cpu_oracle"] = oracle_timing(args.cpu_tokens)
     out = {
         "metric": "layer backward tokens/s (FFN block: RMSNorm + SwiGLU)",
         "value": round(T / (ms * 1e-3), 1),
@@ -615,14 +802,16 @@ def main():
                                "T=4096 (4x1024), bf16 / fp32 accumulate",
                    "tokens": T, "d_model": DM, "hidden": HID, "parallelism": "none (1 GPU)"},
         "step_tflops": round(flops_step / (ms * 1e-3) / 1e12, 2),
-        "roofline": {"kernel": "gemm_bf16_mfma (dN = dG Wg + dU Wu, 4096x2048x11264)",
-                     "bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "launch_ms": round(dom_ms, 4), "traffic": traffic_from_profile(),
-                     "algorithmic_bytes": 2 * (2 * T * HID + 2 * HID * DM) + 2 * T * DM},
+        "roofline": {"kernel": dom["call"], "bound": dom["bound"], "achieved": dom["achieved"],
+                     "peak": BF16_PEAK_TFLOPS if dom["bound"] == "mfma" else HBM_PEAK_GBS,
+                     "unit": dom["unit"], "frac": dom["frac"], "launch_ms": dom["ms"],
+                     "traffic": traffic_from_profile(),
+                     "timing": "HIP events around the call inside every timed step, mean"},
+        "kernels": kernels,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }
+    out.update(extra)
     print(json.dumps(out))
 
 

@@ -639,7 +639,9 @@ static int glu_proj_impl(const void* gu, const void* X, const void* Wg, const vo
                          int H, int dtype, unsigned flags, void* ws, size_t ws_bytes,
                          void* stream) {
     GN_REQUIRE(M >= 0 && K >= 0 && H >= 0, "gn_glu_proj_bwd: negative size");
-    GN_REQUIRE(gu && X && Wg && Wu && dWg && dWu, "gn_glu_proj_bwd: null pointer");
+    GN_REQUIRE(gu && X && Wg && Wu, "gn_glu_proj_bwd: null pointer");
+    GN_REQUIRE((dWg == nullptr) == (dWu == nullptr) && (dWg || (!dbg && !dbu)),
+               "gn_glu_proj_bwd: dWg and dWu go together (both NULL: frozen weights, no biases)");
     GN_REQUIRE(dtype == GN_F32 || dtype == GN_BF16, "gn_glu_proj_bwd: dtype %d", dtype);
     hipStream_t s = as_stream(stream);
     const size_t esz = dtype == GN_F32 ? 4 : 2;
@@ -656,6 +658,7 @@ static int glu_proj_impl(const void* gu, const void* X, const void* Wg, const vo
         d.M = M; d.N = K; d.C = dX; d.C2 = dX; d.Msplit = M; d.ldc = K; d.accumulate = acc;
         if ((rc = gemm_run(d, 0, 0, dtype, dtype, s))) return rc;
     }
+    if (!dWg) return GN_OK;  // frozen projection weights: the input gradient only
     // dWg / dWu from one GEMM over the 2H rows of gu^T X, with the bias sums fused
     if ((dbg == nullptr) != (dbu == nullptr)) {
         // one bias only: sum it separately, the GEMM carries none
@@ -709,7 +712,8 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
                                    void* stream) {
     clear_error();
     GN_REQUIRE(M >= 0 && N >= 0 && H >= 0, "gn_ffn_down_glu_bwd: negative size");
-    GN_REQUIRE(dY && A && Wd && gate && up && gu && dWd, "gn_ffn_down_glu_bwd: null pointer");
+    GN_REQUIRE(dY && A && Wd && gate && up && gu, "gn_ffn_down_glu_bwd: null pointer");
+    GN_REQUIRE(dWd || !dbd, "gn_ffn_down_glu_bwd: dbd without dWd");
     GN_REQUIRE(dtype == GN_BF16, "gn_ffn_down_glu_bwd: bf16 only (fp32: gn_linear_bwd + gn_glu_linear_bwd)");
     GN_REQUIRE(kind >= GN_GLU_SWIGLU_UP && kind <= GN_GLU_REGLU_UP, "gn_ffn_down_glu_bwd: kind %d", kind);
     if (M == 0 || H == 0) return GN_OK;
@@ -725,5 +729,6 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
         d.gu = (bf16_t*)gu; d.ldgu = 2 * H; d.H = H; d.glu_kind = kind;
         if ((rc = gemm_run(d, 0, 0, dtype, GN_BF16, s))) return rc;
     }
+    if (!dWd) return GN_OK;  // frozen down projection: the local gradients only
     return weight_grad(dY, N, A, H, M, N, H, dWd, dWd, N, (float*)dbd, nullptr, dtype, flags, s);
 }

@@ -31,24 +31,45 @@ __global__ __launch_bounds__(256) void probe_mfma(float* __restrict__ out, int i
     out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
-// Four independent 16-byte loads in flight per thread before their stores.
-__global__ __launch_bounds__(256) void probe_copy(uint4* __restrict__ dst, const uint4* __restrict__ src,
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming copy, grid-stride over 16-byte vectors, NV vectors loaded per thread before any
+// of them is stored.  NT: non-temporal (streaming) loads and stores, else plain ones.
+template <int NV, bool NT>
+__global__ __launch_bounds__(256) void probe_copy(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
                                                   int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * 256;
     int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x;
-    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
-    u32x4* d4 = reinterpret_cast<u32x4*>(dst);
-    for (; i + 3 * stride < n; i += 4 * stride) {  // streaming (non-temporal) accesses
-        const u32x4 a = __builtin_nontemporal_load(s4 + i), b = __builtin_nontemporal_load(s4 + i + stride);
-        const u32x4 c = __builtin_nontemporal_load(s4 + i + 2 * stride);
-        const u32x4 d = __builtin_nontemporal_load(s4 + i + 3 * stride);
-        __builtin_nontemporal_store(a, d4 + i);
-        __builtin_nontemporal_store(b, d4 + i + stride);
-        __builtin_nontemporal_store(c, d4 + i + 2 * stride);
-        __builtin_nontemporal_store(d, d4 + i + 3 * stride);
+    for (; i + (NV - 1) * stride < n; i += NV * stride) {
+        u32x4 v[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            v[k] = NT ? __builtin_nontemporal_load(src + i + k * stride) : src[i + k * stride];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            if (NT) __builtin_nontemporal_store(v[k], dst + i + k * stride);
+            else dst[i + k * stride] = v[k];
+        }
     }
     for (; i < n; i += stride) dst[i] = src[i];
+}
+
+// Read-only stream: 8 vectors in flight per thread, one xor-folded word per thread written
+// so the loads cannot be dropped (4 bytes per thread of writes: negligible traffic).
+__global__ __launch_bounds__(256) void probe_read(unsigned* __restrict__ out, const u32x4* __restrict__ src,
+                                                  int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (; i + 7 * stride < n; i += 8 * stride) {
+        u32x4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = __builtin_nontemporal_load(src + i + k * stride);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc ^= v[k];
+    }
+    for (; i < n; i += stride) acc ^= src[i];
+    out[blockIdx.x * 256 + threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
 }
 
 }  // namespace
@@ -64,13 +85,27 @@ extern "C" int gn_probe_mfma(float* out, int blocks, int iters, void* stream) {
     return GN_OK;
 }
 
-extern "C" int gn_probe_copy(void* dst, const void* src, size_t bytes, void* stream) {
+extern "C" int gn_probe_copy(void* dst, const void* src, size_t bytes, int mode, void* stream) {
     clear_error();
     GN_REQUIRE(dst && src && bytes % 16 == 0, "gn_probe_copy: 16-byte multiples only");
     GN_REQUIRE(((uintptr_t)dst & 15u) == 0 && ((uintptr_t)src & 15u) == 0,
                "gn_probe_copy: 16-byte aligned pointers only");
+    GN_REQUIRE(mode >= 0 && mode <= 3, "gn_probe_copy: mode %d (0..3)", mode);
     const int64_t n = (int64_t)(bytes / 16);
-    probe_copy<<<grid_for(n, 256, 4096), 256, 0, as_stream(stream)>>>((uint4*)dst, (const uint4*)src, n);
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = grid_for(n, 256, 4096);
+    u32x4* d = (u32x4*)dst;
+    const u32x4* sv = (const u32x4*)src;
+    switch (mode) {
+        case 0: probe_copy<4, true><<<grid, 256, 0, s>>>(d, sv, n); break;
+        case 1: probe_copy<4, false><<<grid, 256, 0, s>>>(d, sv, n); break;
+        case 2: probe_copy<8, false><<<grid, 256, 0, s>>>(d, sv, n); break;
+        default:
+            GN_REQUIRE(bytes >= (size_t)grid * 256 * 4, "gn_probe_copy: read mode needs dst >= %u B",
+                       grid * 256 * 4);
+            probe_read<<<grid, 256, 0, s>>>((unsigned*)dst, sv, n);
+            break;
+    }
     GN_LAUNCH_CHECK("gn_probe_copy");
     return GN_OK;
 }

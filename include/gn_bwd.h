@@ -149,7 +149,9 @@ int gn_glu_linear_bwd_ws(int kind, const void* dO, const void* gate, const void*
 size_t gn_glu_workspace_bytes(int M, int K, int H, int dtype);
 
 /* The projection half of gn_glu_linear_bwd, starting from gu = [dGate | dUp] ([M x 2H])
- * already computed (e.g. by gn_ffn_down_glu_bwd). Same outputs as gn_glu_linear_bwd. */
+ * already computed (e.g. by gn_ffn_down_glu_bwd). Same outputs as gn_glu_linear_bwd; dX may be
+ * NULL (input needs no gradient) and dWg = dWu = NULL skips the weight gradients (frozen
+ * projections; dbg, dbu must then be NULL too), so the two GEMMs can also run as two calls. */
 int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, const void* Wu, void* dX,
                     void* dWg, void* dWu, void* dbg, void* dbu, int M, int K, int H, int dtype,
                     unsigned flags, void* stream);
@@ -158,7 +160,9 @@ int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, const void* W
  * fusion of backward_linear and the fused-*-backward.glsl local gradients):
  *   dA = dY Wd is never stored; gu = [dGate | dUp] of glu(gate, up) at dO = dA ([M x 2H])
  *   dWd = dY^T A [N x H] fp32;  dbd = column sums of dY [N] (skipped when NULL)
- * dY [M x N], A = glu(gate, up) [M x H], Wd [N x H], gate/up [M x H]. bf16 only. */
+ * dY [M x N], A = glu(gate, up) [M x H], Wd [N x H], gate/up [M x H]. bf16 only.  dWd = NULL
+ * (with dbd = NULL) skips the weight gradient: a frozen projection, or the two GEMMs as two
+ * calls (the weight gradient is then gn_linear_bwd with dX = NULL on the same operands). */
 int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, const void* Wd,
                         const void* gate, const void* up, void* gu, void* dWd, void* dbd, int M,
                         int N, int H, int dtype, unsigned flags, void* stream);

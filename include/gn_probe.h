@@ -14,8 +14,11 @@ extern "C" {
  * accumulators (32768 FLOP each) and writes one float per thread to out[blocks * 256]. */
 int gn_probe_mfma(float* out, int blocks, int iters, void* stream);
 
-/* dst[0 .. bytes) = src[0 .. bytes) with 16-byte loads and stores (bytes read + bytes written). */
-int gn_probe_copy(void* dst, const void* src, size_t bytes, void* stream);
+/* dst[0 .. bytes) = src[0 .. bytes) with 16-byte loads and stores (bytes read + bytes written),
+ * grid-stride: mode 0 four vectors in flight per thread, non-temporal; 1 four, plain; 2 eight,
+ * plain.  Mode 3 only reads src (eight vectors in flight, non-temporal) and writes one word
+ * per thread to dst (bytes read + 4 per thread written). */
+int gn_probe_copy(void* dst, const void* src, size_t bytes, int mode, void* stream);
 
 #ifdef __cplusplus
 }
