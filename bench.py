@@ -357,31 +357,55 @@ def bench_mlp(args, torch, gn):
     gb.attach_torch_stream(device)
     tape = gb.create_tape_context(device)
 
-    def step():
-        tape.begin()
+    def record():
         n1 = tape.record_op(grilly_core.OpType.Linear, [gb.tref(X)], [gb.tref(Z)])
         tape.save_for_backward(n1, [W1.data_ptr(), b1.data_ptr()])
         tape.record_op(grilly_core.OpType.ReLU, [gb.tref(Z, True)], [gb.tref(Hh)])
         n3 = tape.record_op(grilly_core.OpType.Linear, [gb.tref(Hh, True)], [gb.tref(L)])
         tape.save_for_backward(n3, [W2.data_ptr(), b2.data_ptr()])
-        ce = tape.record_op(grilly_core.OpType.CrossEntropy, [gb.tref(L, True), gb.tref(y)],
-                            [gb.tref(loss)], gb.cross_entropy_params(1.0))
-        tape.backward(ce, 0)
+        return tape.record_op(grilly_core.OpType.CrossEntropy, [gb.tref(L, True), gb.tref(y)],
+                              [gb.tref(loss)], gb.cross_entropy_params(1.0))
+
+    def step():
+        tape.begin()
+        tape.backward(record(), 0)
         tape.end()
     ms = timed(torch, step, args.steps, args.warmup)
+    graph = graph_replay(torch, grilly_core, device, tape, record, args, ms)
     flops = 2.0 * Bsz * (784 * 256 + 256 * 10 + 256 * 10)
     cpu = None
     if not args.no_cpu:
         h = lambda a: a.cpu().numpy()
         cpu = mlp_cpu_baseline(h(X), h(y), h(W1), h(W2), h(Z), h(Hh), h(L))
-    return line("MLP tape backward step time (784-256-10, B=64, fp32)", round(ms * 1e3, 2), "us",
-                args, ms, "f32",
-                {"workload": "C1 MLP 784->256->10 fp32 B=64: CE, 2x linear, ReLU bwd via the tape",
-                 "batch": Bsz},
-                {"kernel": "whole step (launch-bound)", "bound": "latency",
-                 "achieved": round(flops / (ms * 1e-3) / 1e12, 4), "peak": 157.3, "unit": "TFLOP/s",
-                 "frac": round(flops / (ms * 1e-3) / 1e12 / 157.3, 6), "traffic": None}, cpu,
-                higher=False)
+    out = line("MLP tape backward step time (784-256-10, B=64, fp32)", round(ms * 1e3, 2), "us",
+               args, ms, "f32",
+               {"workload": "C1 MLP 784->256->10 fp32 B=64: CE, 2x linear, ReLU bwd via the tape",
+                "batch": Bsz},
+               {"kernel": "whole step (launch-bound)", "bound": "latency",
+                "achieved": round(flops / (ms * 1e-3) / 1e12, 4), "peak": 157.3, "unit": "TFLOP/s",
+                "frac": round(flops / (ms * 1e-3) / 1e12 / 157.3, 6), "traffic": None}, cpu,
+               higher=False)
+    out["with_graph"] = graph
+    return out
+
+
+def graph_replay(torch, grilly_core, device, tape, record, args, eager_ms):
+    """The same backward captured once into a HIP graph (grilly_core.OpGraph, the replacement
+    of the reference's OpGraph) and replayed: one hipGraphLaunch per step in place of the tape
+    walk (begin / record / backward / end) and its per-kernel launches.  Same kernels, same
+    buffers, same work per step."""
+    g = grilly_core.OpGraph()
+    tape.begin()
+    g.capture_backward(tape, record(), 0)
+    tape.end()
+    g.optimize(device)
+    ms = timed(torch, lambda: g.execute(device), args.steps, args.warmup)
+    counts = g.node_counts()
+    g.clear()
+    return {"ms_per_step": round(ms, 4), "eager_ms_per_step": round(eager_ms, 4),
+            "speedup": round(eager_ms / ms, 3), "kernel_nodes": counts["kernel"],
+            "memset_nodes": counts["memset"], "memcpy_nodes": counts["memcpy"],
+            "how": "grilly_core.OpGraph.capture_backward once, then execute() per step"}
 
 
 def mlp_cpu_baseline(X, y, W1, W2, Z, H, L):
@@ -416,6 +440,7 @@ def bench_decoder(args, torch, gn):
     gb.attach_torch_stream(device)
     tape = gb.create_tape_context(device)
     ms = timed(torch, lambda: m.backward_step(tape), args.steps, args.warmup)
+    graph = graph_replay(torch, grilly_core, device, tape, lambda: m.record(tape), args, ms)
     tf = m.flops() / (ms * 1e-3) / 1e12
     opt = decoder_optimizer_step(torch, gn, m)
     # the forward that produces the saved tensors (norm/linear/GLU/attention forward kernels)
@@ -435,6 +460,7 @@ def bench_decoder(args, torch, gn):
                  "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
                  "flops_per_step": m.flops()}, cpu)
     out["optimizer_step"] = opt
+    out["with_graph"] = graph
     out["forward"] = {"kernel": "Decoder.forward (gn_layernorm_fwd, gn_linear_fwd, "
                                 "gn_glu_linear_fwd, gn_attn_fwd; torch gather and adds)",
                       "ms": round(fwd_ms, 4), "TFLOP/s": round(fwd_tf, 1),

@@ -25,7 +25,7 @@ KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm
                   "gn_vsa.hip", "gn_attn.hip", "gn_optim.hip", "gn_tapeops.hip", "gn_fwd.hip",
                   "gn_probe.hip", "gn_skinny.hip", "gn_vsa_fwd.hip"]
 TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "tape/checkpoint.cpp", "tape/hypernet.cpp",
-                "bindings.cpp"]
+                "tape/op_graph.cpp", "bindings.cpp"]
 
 # -packed-fp32-ops off: packed fp32 VALU forms are kept out of the generated code.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INCLUDE, "-I", CSRC,
@@ -64,14 +64,15 @@ def build_kernels(jobs=8):
     return out
 
 
-def build_tape(jobs=8):
+def build_tape(jobs=8, extra=()):
+    """extra: flags added to every compile and to the link (e.g. sanitizers)."""
     import pybind11
     os.makedirs(BUILD, exist_ok=True)
     py_inc = sysconfig.get_paths()["include"]
     ext = sysconfig.get_config_var("EXT_SUFFIX")
     flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I", INCLUDE, "-I", CSRC,
              "-I", os.path.join(CSRC, "tape"), "-I", pybind11.get_include(), "-I", py_inc,
-             "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-fvisibility=hidden"]
+             "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-fvisibility=hidden", *extra]
     cmds = [["g++", *flags, "-c", os.path.join(CSRC, s), "-o", _obj(s)] for s in TAPE_SOURCES]
     with ThreadPoolExecutor(jobs) as ex:
         list(ex.map(_run, cmds))
@@ -81,7 +82,7 @@ def build_tape(jobs=8):
         if f.startswith("grilly_core.") and f.endswith(".so"):
             os.remove(os.path.join(HERE, f))
     out = os.path.join(HERE, "_grilly_core" + ext)
-    _run(["g++", "-shared", "-o", out + ".tmp", *[_obj(s) for s in TAPE_SOURCES],
+    _run(["g++", "-shared", *extra, "-o", out + ".tmp", *[_obj(s) for s in TAPE_SOURCES],
           "-L", HERE, "-lgn_bwd", "-Wl,-rpath,$ORIGIN", "-L/opt/rocm/lib", "-lamdhip64",
           "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(out + ".tmp", out)

@@ -12,6 +12,7 @@
 #include "device.h"
 #include "gn_bwd.h"
 #include "hypernet.h"
+#include "op_graph.h"
 
 namespace py = pybind11;
 using namespace grilly;
@@ -186,6 +187,48 @@ PYBIND11_MODULE(_grilly_core, m) {
         .def("get_saved_buffer",
              [](const Node& n, uint32_t i) -> uint64_t { return i < kMaxNodeIO ? n.saved_buffer_ids[i] : 0; },
              py::arg("index"));
+
+    // OpGraph (bindings.cpp:212-235 of the reference): recorded launches replayed as one
+    // HIP graph.  The reference records with addOp from C++; here launches are recorded by
+    // capturing them (begin_capture/end_capture, or capture_backward for a tape's backward).
+    py::class_<OpGraph>(m, "OpGraph")
+        .def(py::init<>())
+        .def("size", &OpGraph::size, "Number of kernel launches recorded in the graph")
+        .def("clear", &OpGraph::clear,
+             "Drop the recorded launches; the buffers pinned by the captures go back to the pool")
+        .def("optimize",
+             [](OpGraph& g, Device& dev) {
+                 FusionStats st = g.optimize(dev);
+                 py::dict d;
+                 d["ops_fused"] = st.opsFused;
+                 d["barriers_eliminated"] = st.barriersEliminated;
+                 d["original_ops"] = st.originalOps;
+                 d["optimized_ops"] = st.optimizedOps;
+                 return d;
+             },
+             py::arg("device"), "Instantiate the executable graph; returns the reference's statistics")
+        .def("execute", &OpGraph::execute, py::arg("device"),
+             "Replay every recorded launch with one hipGraphLaunch on the device's current stream")
+        .def("begin_capture", &OpGraph::begin_capture, py::arg("device"), py::keep_alive<1, 2>(),
+             "Record the launches issued on `device` until end_capture()")
+        .def("end_capture", &OpGraph::end_capture)
+        .def("capture_backward",
+             [](OpGraph& g, TapeContext& t, Node* loss, uint64_t grad) { g.capture_backward(t, loss, grad); },
+             py::arg("tape"), py::arg("loss_node"), py::arg("grad_output_buffer") = 0,
+             py::keep_alive<1, 2>(),
+             "Record the tape's backward pass (nothing runs until execute) and keep its gradient table")
+        .def("get_grad_buffer", &OpGraph::get_grad_buffer, py::arg("input_buffer_id"))
+        .def("is_capturing", &OpGraph::capturing)
+        .def("replays", &OpGraph::replays)
+        .def("node_counts", [](const OpGraph& g) {
+            OpGraph::NodeCounts c = g.node_counts();
+            py::dict d;
+            d["kernel"] = c.kernel;
+            d["memcpy"] = c.memcpy;
+            d["memset"] = c.memset;
+            d["other"] = c.other;
+            return d;
+        });
 
     // Host-only view of the bump allocator, for tests of its failure behaviour.
     py::class_<TapeArena>(m, "_TapeArena")

@@ -143,4 +143,9 @@ inline unsigned grid_for(int64_t n, int per_block, unsigned cap = 65535u * 16u) 
     return (unsigned)g;
 }
 
+// Zero `bytes` bytes at p with a fill kernel (gn_elementwise.hip).  The library clears memory
+// this way, never with hipMemsetAsync, so that every entry point records only kernel nodes
+// when a caller captures it into a HIP graph.
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+
 }  // namespace gn

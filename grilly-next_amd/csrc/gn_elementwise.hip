@@ -134,6 +134,20 @@ __global__ __launch_bounds__(256) void convert_kernel(TO* __restrict__ out, cons
     }
 }
 
+// ---- clear and copy of n items of W (uint4, uint32, uint16 or uint8) ----------------------
+template <typename W>
+__global__ __launch_bounds__(256) void zero_items_kernel(W* __restrict__ out, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        out[i] = W{};
+}
+
+template <typename W>
+__global__ __launch_bounds__(256) void copy_items_kernel(W* __restrict__ out, const W* __restrict__ a,
+                                                         int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        out[i] = a[i];
+}
+
 // ---- embedding (row gather) backward: dE[id[t]] += dX[t] --------------------------------
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ out, int64_t n) {
     for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
@@ -318,6 +332,22 @@ int glu_bwd_to_gu(int kind, const void* dO, const void* gate, const void* up, vo
     return GN_E_INVALID;
 }
 
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    if ((a & 15u) == 0 && bytes % 16 == 0) {
+        const int64_t n = (int64_t)(bytes / 16);
+        zero_items_kernel<uint4><<<grid_for(n, 256, 8192), 256, 0, s>>>((uint4*)p, n);
+    } else if ((a & 3u) == 0 && bytes % 4 == 0) {
+        const int64_t n = (int64_t)(bytes / 4);
+        zero_items_kernel<uint32_t><<<grid_for(n, 256, 8192), 256, 0, s>>>((uint32_t*)p, n);
+    } else {
+        const int64_t n = (int64_t)bytes;
+        zero_items_kernel<uint8_t><<<grid_for(n, 256, 8192), 256, 0, s>>>((uint8_t*)p, n);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace gn
 
 using namespace gn;
@@ -374,6 +404,18 @@ extern "C" int gn_add_inplace(void* out, const void* a, int64_t n, int dtype, vo
     return GN_OK;
 }
 
+extern "C" int gn_zero(void* dst, int64_t bytes, void* stream) {
+    clear_error();
+    GN_REQUIRE(bytes >= 0, "gn_zero: negative size");
+    if (bytes == 0) return GN_OK;
+    GN_REQUIRE(dst, "gn_zero: null pointer");
+    if (launch_zero(dst, (size_t)bytes, as_stream(stream)) != hipSuccess) {
+        set_error("gn_zero: launch failed");
+        return GN_E_HIP;
+    }
+    return GN_OK;
+}
+
 extern "C" int gn_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
                           void* stream) {
     clear_error();
@@ -392,8 +434,18 @@ extern "C" int gn_convert(const void* src, int src_dtype, void* dst, int dst_dty
             convert_kernel<bf16_t, float, 8><<<grid_for(n / 8, 256, 8192), 256, 0, s>>>((float*)dst, (const bf16_t*)src, n / 8);
         else
             convert_kernel<bf16_t, float, 1><<<grid_for(n, 256, 8192), 256, 0, s>>>((float*)dst, (const bf16_t*)src, n);
+    } else if (src_dtype == dst_dtype && (src_dtype == GN_F32 || src_dtype == GN_BF16)) {
+        // same storage type: a word copy (bit-exact, NaN payloads included)
+        const size_t bytes = (size_t)n * (src_dtype == GN_F32 ? 4 : 2);
+        const uintptr_t a = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst);
+        if ((a & 15u) == 0 && bytes % 16 == 0)
+            copy_items_kernel<uint4><<<grid_for(bytes / 16, 256, 8192), 256, 0, s>>>((uint4*)dst, (const uint4*)src, bytes / 16);
+        else if ((a & 3u) == 0 && bytes % 4 == 0)
+            copy_items_kernel<uint32_t><<<grid_for(bytes / 4, 256, 8192), 256, 0, s>>>((uint32_t*)dst, (const uint32_t*)src, bytes / 4);
+        else
+            copy_items_kernel<uint16_t><<<grid_for(bytes / 2, 256, 8192), 256, 0, s>>>((uint16_t*)dst, (const uint16_t*)src, bytes / 2);
     } else {
-        set_error("gn_convert: dtype %d -> %d not supported (f32 <-> bf16)", src_dtype, dst_dtype);
+        set_error("gn_convert: dtype %d -> %d not supported (f32, bf16)", src_dtype, dst_dtype);
         return GN_E_INVALID;
     }
     GN_LAUNCH_CHECK("gn_convert");

@@ -430,11 +430,11 @@ int weight_grad(const void* dY, int ldy, const void* X, int ldx, int M, int N, i
     if (M == 0 || N == 0 || Kin == 0) {
         if (M == 0 && !d.accumulate && N > 0 && Kin > 0) {
             // no rows: the gradients are zero
-            hipError_t e = hipMemsetAsync(dW, 0, (size_t)std::min(N, Msplit) * Kin * 4, s);
-            if (e == hipSuccess && N > Msplit) e = hipMemsetAsync(dW2, 0, (size_t)(N - Msplit) * Kin * 4, s);
-            if (e == hipSuccess && db) e = hipMemsetAsync(db, 0, (size_t)std::min(N, Msplit) * 4, s);
-            if (e == hipSuccess && db2 && N > Msplit) e = hipMemsetAsync(db2, 0, (size_t)(N - Msplit) * 4, s);
-            if (e != hipSuccess) { set_error("weight gradient: memset failed"); return GN_E_HIP; }
+            hipError_t e = launch_zero(dW, (size_t)std::min(N, Msplit) * Kin * 4, s);
+            if (e == hipSuccess && N > Msplit) e = launch_zero(dW2, (size_t)(N - Msplit) * Kin * 4, s);
+            if (e == hipSuccess && db) e = launch_zero(db, (size_t)std::min(N, Msplit) * 4, s);
+            if (e == hipSuccess && db2 && N > Msplit) e = launch_zero(db2, (size_t)(N - Msplit) * 4, s);
+            if (e != hipSuccess) { set_error("weight gradient: clear failed"); return GN_E_HIP; }
         }
         return GN_OK;
     }
@@ -503,8 +503,8 @@ int gemm_dispatch(const void* A0, const void* B0, int K0, const void* A1, const 
     const bool seg1 = A1 && B1 && K1 > 0;
     if (K0 + (seg1 ? K1 : 0) == 0) {
         if (acc) return GN_OK;
-        hipError_t e = hipMemsetAsync(C, 0, (size_t)M * N * (c_dtype == GN_F32 ? 4 : 2), s);
-        if (e != hipSuccess) { set_error("gn_gemm: memset failed"); return GN_E_HIP; }
+        hipError_t e = launch_zero(C, (size_t)M * N * (c_dtype == GN_F32 ? 4 : 2), s);
+        if (e != hipSuccess) { set_error("gn_gemm: clear failed"); return GN_E_HIP; }
         return GN_OK;
     }
     GN_REQUIRE(A0 && B0, "gn_gemm: null operand");

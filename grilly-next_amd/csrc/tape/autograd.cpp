@@ -117,8 +117,10 @@ void BackwardEngine::contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t 
     }
     if (!e->owned) {
         uint64_t fresh = alloc_grad(bytes);
-        hip_check(hipMemcpyAsync(P(fresh), P(e->grad_id), bytes, hipMemcpyDeviceToDevice,
-                                 dev_.stream()), "fan-out copy");
+        gn_call(gn_convert(P(e->grad_id), gn_dtype(dtype, "fan-out"), P(fresh),
+                           gn_dtype(dtype, "fan-out"), (int64_t)numel, dev_.stream()),
+                "fan-out copy");
+        stats_.shaders_dispatched++;
         e->grad_id = fresh;
         e->owned = true;
     }
@@ -603,6 +605,13 @@ void TapeContext::save_for_backward(Node* node, const uint64_t* ids, uint32_t co
 void TapeContext::backward(Node* loss_node, uint64_t grad_output_buffer) {
     recording_ = false;
     engine_.backward(arena_, loss_node, grad_output_buffer);
+}
+
+std::vector<std::pair<uint64_t, uint64_t>> TapeContext::grads() const {
+    std::vector<std::pair<uint64_t, uint64_t>> out;
+    for (const auto& e : engine_.table_)
+        if (e.buffer_id && e.grad_id) out.emplace_back(e.buffer_id, e.grad_id);
+    return out;
 }
 
 void TapeContext::end() {

@@ -22,6 +22,7 @@
 #include <cstdint>
 #include <cstring>
 #include <stdexcept>
+#include <utility>
 #include <vector>
 
 #include "device.h"
@@ -218,6 +219,8 @@ public:
     void save_for_backward(Node* node, const uint64_t* ids, uint32_t count);
     void backward(Node* loss_node, uint64_t grad_output_buffer);
     uint64_t get_grad_buffer(uint64_t id) const { return engine_.get_grad_buffer(id); }
+    // every (tensor id, gradient buffer id) pair of the last backward pass
+    std::vector<std::pair<uint64_t, uint64_t>> grads() const;
     void end();
     uint64_t acquire_temp(size_t bytes);
 

@@ -1,6 +1,8 @@
 // device.cpp — HIP device, stream and caching buffer pool (see device.h).
 #include "device.h"
 
+#include "gn_bwd.h"
+
 #include <cstring>
 
 namespace grilly {
@@ -70,11 +72,41 @@ uint64_t Device::acquire(size_t bytes) {
     }
     live_[id] = b;
     stats_.bytes_live += b;
+    if (pin_sink_) {
+        pin_sink_->push_back(id);
+        pinned_[id] = false;
+    }
     return id;
 }
 
 void Device::release(uint64_t id) {
     std::lock_guard<std::mutex> g(mu_);
+    auto p = pinned_.find(id);
+    if (p != pinned_.end()) {
+        if (p->second) throw std::runtime_error("Device.release: buffer released twice");
+        p->second = true;  // back to the pool at unpin()
+        return;
+    }
+    release_locked(id);
+}
+
+void Device::pin_acquisitions(std::vector<uint64_t>* sink) {
+    std::lock_guard<std::mutex> g(mu_);
+    pin_sink_ = sink;
+}
+
+void Device::unpin(const std::vector<uint64_t>& ids) {
+    std::lock_guard<std::mutex> g(mu_);
+    for (uint64_t id : ids) {
+        auto p = pinned_.find(id);
+        if (p == pinned_.end()) continue;
+        const bool released = p->second;
+        pinned_.erase(p);
+        if (released) release_locked(id);
+    }
+}
+
+void Device::release_locked(uint64_t id) {
     auto it = live_.find(id);
     if (it == live_.end()) throw std::runtime_error("Device.release: unknown buffer id");
     free_.emplace(it->second, id);
@@ -102,7 +134,9 @@ void Device::download(uint64_t id, void* host, size_t bytes, size_t offset) {
 }
 
 void Device::zero(uint64_t id, size_t bytes) {
-    hip_check(hipMemsetAsync(reinterpret_cast<void*>(id), 0, bytes, stream_), "zero");
+    // a fill kernel, not hipMemsetAsync: the stream may be under HIP graph capture
+    if (gn_zero(reinterpret_cast<void*>(id), (int64_t)bytes, stream_) != GN_OK)
+        throw std::runtime_error(std::string("Device.zero: ") + gn_last_error());
 }
 
 void Device::synchronize() { hip_check(hipStreamSynchronize(stream_), "synchronize"); }

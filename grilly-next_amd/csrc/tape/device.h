@@ -50,6 +50,13 @@ public:
     void zero(uint64_t id, size_t bytes);  // fill kernel, stream-ordered
     void synchronize();
 
+    // HIP graph capture (OpGraph): while a sink is set, every buffer acquire() hands out is
+    // appended to it and pinned.  release() of a pinned buffer is deferred until unpin(), so
+    // memory a captured graph reads or writes is not handed out again while the graph can
+    // still be replayed.
+    void pin_acquisitions(std::vector<uint64_t>* sink);  // nullptr: stop pinning
+    void unpin(const std::vector<uint64_t>& ids);
+
     struct Stats {
         size_t bytes_live = 0, bytes_cached = 0;
         uint64_t allocs = 0, reuses = 0;
@@ -66,6 +73,9 @@ private:
     mutable std::mutex mu_;
     std::unordered_map<uint64_t, size_t> live_;            // id -> bucket bytes
     std::multimap<size_t, uint64_t> free_;                 // bucket bytes -> id
+    std::vector<uint64_t>* pin_sink_ = nullptr;
+    std::unordered_map<uint64_t, bool> pinned_;            // id -> released by its owner
+    void release_locked(uint64_t id);
     Stats stats_;
 };
 

@@ -34,7 +34,7 @@ SYMBOLS = [
     "gn_vsa_fwd_workspace_bytes", "gn_vsa_surrogate_fwd", "gn_embedding_bwd", "gn_binary_bwd",
     "gn_reduce_bwd", "gn_transpose_bwd", "gn_mse_bwd", "gn_vsa_lora_expand_bwd",
     "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_layernorm_fwd",
-    "gn_rmsnorm_fwd", "gn_layernorm_fwd_ex", "gn_rmsnorm_fwd_ex", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace", "gn_convert",
+    "gn_rmsnorm_fwd", "gn_layernorm_fwd_ex", "gn_rmsnorm_fwd_ex", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace", "gn_convert", "gn_zero",
 ]
 BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
 RED = {"sum": 0, "mean": 1}
@@ -88,6 +88,7 @@ _SIGS = {
     "gn_layernorm_fwd_ex": ([_P, _I, _P, _P, _P, _I, _P, _P, _I, _I, _F, _U, _P], _I),
     "gn_rmsnorm_fwd_ex": ([_P, _I, _P, _P, _I, _P, _I, _I, _F, _P], _I),
     "gn_convert": ([_P, _I, _P, _I, _L, _P], _I),
+    "gn_zero": ([_P, _L, _P], _I),
     "gn_norm_workspace_bytes": ([_I, _I], _Z),
     "gn_softmax_bwd": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "gn_xent_bwd": ([_P, _P, _P, _I, _I, _F, _I, _P], _I),
@@ -367,8 +368,16 @@ def rmsnorm_bwd(dY, X, w, rstd, ws=None, need_param=True, dX=None, dW=None, dX_a
     return dX, (dW if need_param else None)
 
 
+def zero(t):
+    """t[...] = 0 through the library's fill kernel (what it clears with instead of
+    hipMemsetAsync); t must be contiguous."""
+    assert t.is_contiguous()
+    _check(lib().gn_zero(_ptr(t), t.numel() * t.element_size(), _stream()), "gn_zero")
+    return t
+
+
 def convert(src, dtype):
-    """src in another storage dtype (f32 <-> bf16, nearest-even)."""
+    """src in another storage dtype (f32 <-> bf16, nearest-even; the same dtype copies)."""
     out = torch.empty(src.shape, dtype=dtype, device=src.device)
     _check(lib().gn_convert(_ptr(src), _dt(src), _ptr(out), _dt(out), src.numel(), _stream()),
            "gn_convert")

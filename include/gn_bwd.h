@@ -466,8 +466,17 @@ int gn_add_inplace(void* out, const void* a, int64_t n, int dtype, void* stream)
 
 /* dst = src in another storage type (f32 -> bf16 rounds to nearest-even; bf16 -> f32 exact):
  * the gradient of a bf16 tensor added into an fp32 stream (an Add node whose inputs differ in
- * dtype) is the fp32 upstream gradient rounded once. */
+ * dtype) is the fp32 upstream gradient rounded once.  src_dtype == dst_dtype is a bit-exact
+ * copy (the tape's fan-out copy of a borrowed gradient). */
 int gn_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
+
+/* dst[0, bytes) = 0 with a fill kernel.  No entry point of this library calls hipMemsetAsync,
+ * hipMalloc or a synchronising HIP call, so any sequence of them (the tape's backward among
+ * them) can be captured into a HIP graph and replayed: the graph holds kernel nodes only.
+ * Replaces the host memset of a mapped gradient buffer the reference does before each
+ * accumulating dispatch (cpp/src/autograd.cpp:223-226, 507, 721), which a device-resident
+ * buffer cannot take. */
+int gn_zero(void* dst, int64_t bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -421,6 +421,25 @@ def test_softmax_and_xent_golden(gn):
     assert rel_err(host(dL), g["dLogits"]) < FP32_TOL
 
 
+@pytest.mark.parametrize("C", [1024, 2048, 4096])
+def test_softmax_bwd_bf16_attention_widths(gn, C):
+    """Softmax backward on bf16 probability rows as wide as an attention score row (S = 1024 to
+    4096 keys; causal rows carry exact zeros past the diagonal), against the oracle on the same
+    bf16-rounded inputs (normwise 2e-2)."""
+    r = rng_(C)
+    rows = 256
+    s = (r.standard_normal((rows, C)) * 3).astype(np.float32)
+    s[np.triu_indices(rows, 1)[0], np.triu_indices(rows, 1)[1]] = -np.inf  # causal prefix rows
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    Y = dev(p, torch.bfloat16)
+    dY = dev(r.standard_normal((rows, C)).astype(np.float32), torch.bfloat16)
+    got = host(gn.softmax_bwd(dY, Y))
+    want = oracle.softmax_bwd(host(dY), host(Y))
+    assert rel_err(got, want) < BF16_TOL
+    assert np.all(got[np.triu_indices(rows, 1)] == 0)  # masked keys get no gradient
+
+
 def test_xent_vocab_bf16(gn):
     r = rng_(9)
     rows, C = 64, 32000

@@ -91,3 +91,39 @@ def test_device_without_gpu_fails_loudly():
         pass
     with pytest.raises(RuntimeError, match="no HIP device"):
         grilly_core.Device()
+
+
+def test_opgraph_api_matches_reference_names():
+    """grilly_core.OpGraph carries the reference's Python surface (bindings.cpp:212-235:
+    OpGraph(), size, clear, optimize(device) -> dict, execute(device)); an empty graph needs
+    no GPU to build, size or clear."""
+    g = grilly_core.OpGraph()
+    for name in ("size", "clear", "optimize", "execute", "begin_capture", "end_capture",
+                 "capture_backward", "get_grad_buffer", "node_counts", "replays"):
+        assert callable(getattr(g, name)), name
+    assert g.size() == 0 and not g.is_capturing() and g.replays() == 0
+    assert g.get_grad_buffer(0x1000) == 0
+    assert g.node_counts() == {"kernel": 0, "memcpy": 0, "memset": 0, "other": 0}
+    g.clear()
+    with pytest.raises(RuntimeError, match="no capture is open"):
+        g.end_capture()
+
+
+def test_library_code_is_capturable():
+    """No kernel-library source and no tape source on the backward path clears, copies,
+    allocates or synchronises through the HIP runtime: a HIP graph captured from them holds
+    kernel nodes only (the runtime's memset nodes are avoided on purpose).  The device pool
+    (device.cpp) allocates outside any capture, or relaxed-mode inside one."""
+    import glob
+    import re
+    csrc = os.path.join(PKG, "csrc")
+    banned = re.compile(r"\b(hipMemsetAsync|hipMemset|hipMemcpy|hipMemcpyAsync|hipMalloc|hipFree|"
+                        r"hipStreamSynchronize|hipDeviceSynchronize)\s*\(")
+    files = glob.glob(os.path.join(csrc, "*.hip")) + [os.path.join(csrc, "tape", "autograd.cpp")]
+    hits = []
+    for f in files:
+        for i, line in enumerate(open(f), 1):
+            code = line.split("//", 1)[0]
+            if banned.search(code):
+                hits.append(f"{os.path.relpath(f, PKG)}:{i}: {line.strip()}")
+    assert not hits, hits
