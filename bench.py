@@ -20,9 +20,12 @@ Other BASELINE configs (parity-tested, measured with --workload):
           end-to-end backward through the tape engine
     hyper the reference's VSA hypernetwork training step (grilly_core.vsa_training_step) at
           its defaults (K 16, 1.0 GB output layer), batch 1
+    linear32 fp32 Linear backward at the hypernetwork's output layer, batch 64
+          (1536 -> 163840), on the six-product bf16 MFMA path (fp32-grade)
 Each prints one JSON line of the same shape; the default (ffn) is the headline metric.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ffn|attn|vsa|mlp|decoder|hyper]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--workload ffn|attn|vsa|mlp|decoder|hyper|linear32]
 """
 import argparse
 import json
@@ -38,6 +41,7 @@ sys.path.insert(0, os.path.join(ROOT, "grilly-next_amd"))
 T, DM, HID = 4096, 2048, 5632
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA (v_mfma_f32_32x32x2_f32)
 
 
 def parse():
@@ -47,7 +51,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--cpu-tokens", type=int, default=T)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", default="ffn", choices=["ffn", "attn", "vsa", "mlp", "decoder", "hyper"])
+    p.add_argument("--workload", default="ffn",
+                   choices=["ffn", "attn", "vsa", "mlp", "decoder", "hyper", "linear32"])
     p.add_argument("--calib-copy", action="store_true",
                    help="after the timed region, launch one gn_add_inplace over 2^28 floats "
                         "(reads 2 GiB, writes 1 GiB): the reference dispatch that scales the "
@@ -536,6 +541,43 @@ def decoder_cpu_baseline(m):
                       f"scaled by FLOPs to {m.L} layers + LM head", "cpu_model": cpu_ref.cpu_model()}
 
 
+def bench_linear32(args, torch, gn):
+    """fp32 Linear backward at the hypernetwork's output layer with batch 64: 1536 -> 163840
+    (K 16 x vsa 10240), W 1.0 GB.  One step = gn_linear_bwd_ws: dX = dY W (split-K over
+    163840), dW = dY^T X (1.0 GB written), db, on the six-product bf16 MFMA path."""
+    M, N, K = 64, 163840, 1536
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    dY = torch.randn(M, N, device=dev, generator=g)
+    X = torch.randn(M, K, device=dev, generator=g)
+    W = torch.randn(N, K, device=dev, generator=g) * 0.02
+    dX = torch.empty(M, K, device=dev)
+    dW = torch.empty(N, K, device=dev)
+    db = torch.empty(N, device=dev)
+    ws = gn.workspace(gn.linear_workspace_bytes(M, N, K, 0), dev)
+    ms = timed(torch, lambda: gn.linear_bwd(dY, X, W, dX=dX, dW=dW, db=db, ws=ws),
+               args.steps, args.warmup)
+    byts = 4.0 * (2 * N * K + M * N + 2 * M * K + N)  # W, dW, dY, X, dX, db once each
+    gbs = byts / (ms * 1e-3) / 1e9
+    flops = 4.0 * M * N * K
+    tf = flops / (ms * 1e-3) / 1e12
+    out = line("fp32 Linear backward, hypernetwork output layer at batch 64 (GB/s)",
+               round(gbs, 1), "GB/s", args, ms, "f32 (bf16x6 split on MFMA)",
+               {"workload": "Linear bwd fp32 64 x 1536 -> 163840 (K 16 x vsa 10240): dX, dW, db",
+                "M": M, "N": N, "K": K},
+               {"kernel": "gn_linear_bwd_ws (dX split-K GEMM + plane sum, dW GEMM, db)",
+                "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes": byts}, None)
+    out["fp32_work"] = {"flops": flops, "TFLOP/s": round(tf, 1),
+                        "vs_fp32_mfma_peak": round(tf / FP32_PEAK_TFLOPS, 3),
+                        "fp32_mfma_floor_ms": round(flops / FP32_PEAK_TFLOPS / 1e9, 4),
+                        "hbm_floor_ms": round(byts / HBM_PEAK_GBS / 1e6, 4),
+                        "note": "a kernel on v_mfma_f32_32x32x2_f32 cannot finish under "
+                                "fp32_mfma_floor_ms; the split moves the floor to HBM"}
+    return out
+
+
 def bench_hyper(args, torch, gn):
     """The reference's VSA hypernetwork training step (vsa_training_step, bindings.cpp:
     3140-3286) at its defaults: d_model 768, vsa_dim 10240, K 16, router 32 (W2 = 16 x 10240 x
@@ -780,7 +822,7 @@ def main():
         return
     if args.workload != "ffn":
         fn = {"attn": bench_attn, "vsa": bench_vsa, "mlp": bench_mlp,
-              "decoder": bench_decoder, "hyper": bench_hyper}[args.workload]
+              "decoder": bench_decoder, "hyper": bench_hyper, "linear32": bench_linear32}[args.workload]
         print(json.dumps(fn(args, torch, gn)))
         return
     dev = torch.device("cuda:0")

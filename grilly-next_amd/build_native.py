@@ -23,7 +23,7 @@ ARCH = os.environ.get("GN_OFFLOAD_ARCH", "gfx950")
 
 KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip", "gn_gemm_dma.hip",
                   "gn_vsa.hip", "gn_attn.hip", "gn_optim.hip", "gn_tapeops.hip", "gn_fwd.hip",
-                  "gn_probe.hip", "gn_skinny.hip", "gn_vsa_fwd.hip"]
+                  "gn_probe.hip", "gn_skinny.hip", "gn_vsa_fwd.hip", "gn_gemm_f32.hip"]
 TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "tape/checkpoint.cpp", "tape/hypernet.cpp",
                 "tape/op_graph.cpp", "bindings.cpp"]
 

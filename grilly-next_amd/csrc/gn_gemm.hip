@@ -398,6 +398,7 @@ int gemm_run(const GemmDesc& d, int transA, int transB, int dtype, int c_dtype, 
             set_error("gemm: the GLU epilogue needs bf16 operands");
             return GN_E_INVALID;
         }
+        if (gemm_f32_applicable(d)) return gemm_f32_launch(d, transA, transB, s);
         return launch_simt<float, float, 0>(d, transA, transB, s);
     }
     set_error("gn_gemm: dtype %d not supported (f32, bf16)", dtype);
@@ -491,9 +492,11 @@ size_t weight_grad_ws_bytes(int M, int N, int Kin, int dtype) {
 }
 
 // Plain-argument form used by the C entry points.
+// ws: split-K partial planes of the fp32 path (may be NULL / short: the split is then
+// limited to what fits).
 int gemm_dispatch(const void* A0, const void* B0, int K0, const void* A1, const void* B1, int K1,
                   void* C, int M, int N, int transA, int transB, int dtype, int c_dtype,
-                  unsigned flags, hipStream_t s) {
+                  unsigned flags, hipStream_t s, void* ws = nullptr, size_t ws_bytes = 0) {
     GN_REQUIRE(M >= 0 && N >= 0 && K0 >= 0 && K1 >= 0, "gn_gemm: negative size");
     if (M == 0 || N == 0) return GN_OK;
     GN_REQUIRE(C, "gn_gemm: null C");
@@ -518,7 +521,33 @@ int gemm_dispatch(const void* A0, const void* B0, int K0, const void* A1, const 
     }
     d.M = M; d.N = N; d.C = C; d.C2 = C; d.Msplit = M; d.ldc = N;
     d.accumulate = acc ? 1 : 0;
+    if (ws && al16(ws)) {
+        d.part = (float*)ws;
+        d.part_cap = ws_bytes;
+    }
     return gemm_run(d, transA, transB, dtype, c_dtype, s);
+}
+
+// Split-K workspace bytes of the fp32 Linear backward's two GEMMs (dX = dY W over N,
+// dW = dY^T X over M rows) on the six-product bf16 MFMA path: the larger of the two (they run
+// one after the other on the stream and share it).
+static size_t linear_f32_ws_bytes(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const bf16_t* al = reinterpret_cast<const bf16_t*>((uintptr_t)256);  // aligned stand-in
+    float* alf = reinterpret_cast<float*>((uintptr_t)256);
+    GemmDesc x{};
+    x.nseg = 1;
+    x.A[0] = al; x.lda[0] = N; x.Ks[0] = N;
+    x.B[0] = al; x.ldb[0] = K;
+    x.M = M; x.N = K; x.C = alf; x.C2 = alf; x.Msplit = M; x.ldc = K;
+    GemmDesc w = x;
+    w.A[0] = al; w.lda[0] = N; w.Ks[0] = M;
+    w.B[0] = al; w.ldb[0] = K;
+    w.M = N; w.N = K; w.Msplit = N; w.ldc = K;
+    size_t b = 0;
+    if (gemm_f32_applicable(x)) b = std::max(b, gemm_f32_part_bytes(x));
+    if (gemm_f32_applicable(w)) b = std::max(b, gemm_f32_part_bytes(w));
+    return b;
 }
 
 int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigned flags,
@@ -585,7 +614,7 @@ extern "C" int gn_linear_bwd(const void* dY, const void* X, const void* W, void*
 }
 
 extern "C" size_t gn_linear_workspace_bytes(int M, int N, int K, int dtype) {
-    if (dtype == GN_F32) return skinny_bwd_ws_bytes(M, N, K);
+    if (dtype == GN_F32) return std::max(skinny_bwd_ws_bytes(M, N, K), linear_f32_ws_bytes(M, N, K));
     return weight_grad_ws_bytes(M, N, K, dtype);
 }
 
@@ -605,7 +634,8 @@ extern "C" int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, vo
                                  ws_bytes, s);
     int rc;
     if (dX) {  // dX[M x K] = dY[M x N] . W[N x K]
-        rc = gemm_dispatch(dY, W, N, nullptr, nullptr, 0, dX, M, K, 0, 0, dtype, dtype, flags, s);
+        rc = gemm_dispatch(dY, W, N, nullptr, nullptr, 0, dX, M, K, 0, 0, dtype, dtype, flags, s,
+                           dtype == GN_F32 ? ws : nullptr, ws_bytes);
         if (rc) return rc;
     }
     // dW[N x K] = dY^T . X  (A = dY stored [M x N] = [Ks x Mout], transposed), db fused

@@ -79,6 +79,15 @@ bool gemm_dma_applicable(const GemmDesc& g);
 // unbounded (0: none).
 size_t gemm_dma_part_bytes(const GemmDesc& g, int transA, int c_dtype);
 int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s);
+// C (+)= sum over y < g.ksplit of the planes at g.part (index order); N % 4 == 0, C and ldc
+// 16-byte aligned.
+void launch_split_reduce(const GemmDesc& g, hipStream_t s);
+
+// fp32 operands on the bf16 MFMA pipe through a six-product three-piece split (gn_gemm_f32.hip)
+bool gemm_f32_applicable(const GemmDesc& g);
+// workspace bytes the launch would use for split-K partial planes (0: none)
+size_t gemm_f32_part_bytes(const GemmDesc& g);
+int gemm_f32_launch(const GemmDesc& g, int transA, int transB, hipStream_t s);
 
 template <typename CT, int EPI>
 __device__ __forceinline__ void gemm_store(const GemmDesc& g, int m, int n, float v) {

@@ -1054,6 +1054,10 @@ size_t gemm_dma_part_bytes(const GemmDesc& g0, int transA, int c_dtype) {
     return tc.ksplit > 2 ? part_bytes(g, tc.ksplit) : 0;
 }
 
+void launch_split_reduce(const GemmDesc& g, hipStream_t s) {
+    split_reduce<<<grid_for((int64_t)g.M * (g.N / 4), 256, 4096), 256, 0, s>>>(g);
+}
+
 int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s) {
     if (g.epi == 1) return launch_trans<bf16_t, 1>(g, transA, transB, s);
     if (c_dtype == GN_F32) return launch_trans<float, 0>(g, transA, transB, s);

@@ -10,7 +10,7 @@ namespace gn {
 
 int gemm_dispatch(const void* A0, const void* B0, int K0, const void* A1, const void* B1, int K1,
                   void* C, int M, int N, int transA, int transB, int dtype, int c_dtype,
-                  unsigned flags, hipStream_t s);
+                  unsigned flags, hipStream_t s, void* ws, size_t ws_bytes);
 
 namespace {
 
@@ -230,11 +230,11 @@ extern "C" int gn_vsa_lora_expand_bwd(const float* dPreds, const float* basis, c
     int rc;
     // dCoeffs [Bn*K x rank] = dPreds [Bn*K x D] . basis [D x rank]
     if (dCoeffs && (rc = gemm_dispatch(dPreds, basis, D, nullptr, nullptr, 0, dCoeffs, rowsBK, rank,
-                                       0, 0, GN_F32, GN_F32, flags, s)))
+                                       0, 0, GN_F32, GN_F32, flags, s, nullptr, 0)))
         return rc;
     // dBasis [D x rank] (+)= dPreds^T . coeffs  (A stored [Bn*K x D] = transposed)
     if (dBasis && (rc = gemm_dispatch(dPreds, coeffs, rowsBK, nullptr, nullptr, 0, dBasis, D, rank,
-                                      1, 0, GN_F32, GN_F32, flags, s)))
+                                      1, 0, GN_F32, GN_F32, flags, s, nullptr, 0)))
         return rc;
     return GN_OK;
 }

@@ -59,7 +59,14 @@ def test_python_frontend_lists_every_symbol():
     plane = 768 * 768 * 4 + 768 * 4
     o_proj = lib.gn_linear_workspace_bytes(8192, 768, 768, BF16)
     assert o_proj in [ks * plane for ks in (3, 4, 6, 8)]
-    assert lib.gn_linear_workspace_bytes(8192, 768, 768, F32) == 0
+    # fp32 (six-product bf16 MFMA path): K-split planes of the GEMM that has fewer tiles than
+    # the grid has blocks, here dW [768 x 768] over 8192 rows (dX [8192 x 768] has enough)
+    f32 = lib.gn_linear_workspace_bytes(8192, 768, 768, F32)
+    assert f32 in [ks * 768 * 768 * 4 for ks in range(2, 129)]
+    assert lib.gn_linear_workspace_bytes(64, 256, 784, F32) == 0  # short reductions: no split
+    # the hypernetwork's output layer at batch 64: dX [64 x 1536] over K = 163840
+    hyp = lib.gn_linear_workspace_bytes(64, 163840, 1536, F32)
+    assert hyp in [ks * 64 * 1536 * 4 for ks in range(2, 129)]
     assert lib.gn_linear_workspace_bytes(64, 256, 784, BF16) == 0  # short reduction: no split
     assert lib.gn_linear_workspace_bytes(8192, 32000, 768, BF16) == 0  # LM head: many tiles
     glu = lib.gn_glu_workspace_bytes(8192, 768, 3072, BF16)

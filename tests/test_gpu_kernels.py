@@ -98,6 +98,85 @@ def test_gemm_unaligned_falls_back(gn):
     assert rel_err(host(C), A.astype(np.float64) @ B) < 1e-5
 
 
+# ---------------------------------------------------------------------------- fp32 on MFMA
+# fp32 operands run on the bf16 matrix cores through a three-piece split and six products
+# (fp32-grade).  Against float64: normwise <= 1e-4 (the fp32 bar), and, element by element,
+# within a few fp32 ulps of the summed magnitudes (what an FMA chain guarantees), which a
+# two-piece split (~2^-16 per product) would miss.  A bf16-only product would be off by
+# ~2e-3 on these inputs.
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("shape", [(136, 200, 72), (256, 128, 640), (132, 68, 1000), (8, 8, 8),
+                                   (10, 13, 7)])
+def test_gemm_fp32_layouts(gn, ta, tb, shape):
+    M, N, K = shape
+    r = rng_(31)
+    A = (r.standard_normal((K, M) if ta else (M, K)) * 3).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    C = gn.gemm(dev(A), dev(B), bool(ta), bool(tb))
+    assert rel_err(host(C), ref) < FP32_TOL
+    mag = np.abs(A.T if ta else A).astype(np.float64) @ np.abs(B.T if tb else B)
+    bound = 2.0 ** (-20 if K <= 128 else -18)  # fp32 accumulation over K terms, elementwise
+    assert np.all(np.abs(host(C) - ref) <= bound * mag + 1e-30)
+    bf16_only = (rnd(A).T if ta else rnd(A)).astype(np.float64) @ (rnd(B).T if tb else rnd(B))
+    if K >= 64:  # the bound separates the split from a bf16-only product
+        assert rel_err(bf16_only, ref) > 10 * FP32_TOL
+
+
+def test_gemm_fp32_two_segments_and_accumulate(gn):
+    r = rng_(32)
+    M, N, K0, K1 = 200, 136, 96, 260
+    A0, A1 = (r.standard_normal((M, k)).astype(np.float32) for k in (K0, K1))
+    B0, B1 = (r.standard_normal((k, N)).astype(np.float32) for k in (K0, K1))
+    ref = A0.astype(np.float64) @ B0 + A1.astype(np.float64) @ B1
+    C = gn.gemm(dev(A0), dev(B0), A1=dev(A1), B1=dev(B1))
+    assert rel_err(host(C), ref) < FP32_TOL
+    gn.gemm(dev(A0), dev(B0), C=C, accumulate=True)
+    assert rel_err(host(C), ref + A0.astype(np.float64) @ B0) < FP32_TOL
+
+
+def test_linear_fp32_c1_first_layer(gn):
+    """BASELINE configs[0]'s first Linear (784 -> 256, batch 64, fp32): dW1 [256 x 784] over 64
+    rows and db1 on the MFMA path, dX on it too, against the oracle."""
+    r = rng_(33)
+    X = r.standard_normal((64, 784)).astype(np.float32)
+    W = (r.standard_normal((256, 784)) * 0.05).astype(np.float32)
+    dY = r.standard_normal((64, 256)).astype(np.float32)
+    dX, dW, db = gn.linear_bwd(dev(dY), dev(X), dev(W))
+    rdX, rdW, rdb = oracle.linear_bwd(dY, X, W)
+    assert rel_err(host(dX), rdX) < FP32_TOL
+    assert rel_err(host(dW), rdW) < FP32_TOL
+    assert rel_err(host(db), rdb) < FP32_TOL
+
+
+def test_linear_fp32_hypernetwork_shape(gn):
+    """The hypernetwork's output Linear at batch 64 (1536 -> 163840 = K 16 x vsa 10240, fp32,
+    W 1.0 GB): dX = dY W runs split-K (K = 163840) through the workspace, dW = dY^T X writes
+    the 1 GB gradient.  Checked on samples against float64 (96 columns of dX, 512 rows of dW,
+    all of db; normwise <= 1e-4) and bit-identical on a rerun (the planes are reduced in
+    index order)."""
+    M, N, K = 64, 163840, 1536
+    assert gn.linear_workspace_bytes(M, N, K, 0) > 0  # the dX GEMM splits K
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(34)
+    dY = torch.randn(M, N, device="cuda:0", generator=g)
+    X = torch.randn(M, K, device="cuda:0", generator=g)
+    W = torch.randn(N, K, device="cuda:0", generator=g) * 0.02
+    dX, dW, db = gn.linear_bwd(dY, X, W)
+    dX2, _, _ = gn.linear_bwd(dY, X, W, dW=torch.empty_like(dW))
+    assert torch.equal(dX, dX2)
+    r = rng_(35)
+    cols = np.sort(r.choice(K, 96, replace=False))
+    rows = np.sort(r.choice(N, 512, replace=False))
+    hdY = dY.cpu().numpy().astype(np.float64)
+    hX = X.cpu().numpy().astype(np.float64)
+    ref_dx = hdY @ W[:, torch.from_numpy(cols).cuda()].cpu().numpy().astype(np.float64)
+    assert rel_err(host(dX)[:, cols], ref_dx) < FP32_TOL
+    ref_dw = hdY[:, rows].T @ hX
+    assert rel_err(host(dW[torch.from_numpy(rows).cuda()]), ref_dw) < FP32_TOL
+    assert rel_err(host(db), hdY.sum(axis=0)) < FP32_TOL
+
+
 # ---------------------------------------------------------------------------- linear
 def test_linear_fp32_golden(gn):
     for tag in ["small", "c1l2"]:
