@@ -24,11 +24,10 @@
 // global loads to LDS as contiguous runs and a wave's writes do not collide in the banks.  Software pipeline with two LDS
 // stages, two register sets and one barrier per stage: while the MFMAs read stage t, the
 // registers holding k-tile t+1 are split into the other stage and take the loads of k-tile
-// t+3, so each load has two stages of MFMAs to arrive.  The grid is persistent (two blocks per
-// CU): a block runs a stream of work items (tile, k-range) through that pipeline, so the
-// next item's loads are in flight while the current one stores its tile.  Long-K shapes with
-// few tiles split K into fp32 partial planes that split_reduce adds in index order
-// (deterministic).
+// t+3, so each load has two stages of MFMAs to arrive.  Long-K shapes with few tiles split K
+// over blockIdx.y into fp32 partial planes that split_reduce adds in index order
+// (deterministic).  (A persistent grid streaming (tile, k-range) items through the pipeline
+// was measured slower: 445 against 350 us on the 1 GB weight gradient below.)
 #include <algorithm>
 
 #include "gn_common.h"
@@ -168,15 +167,6 @@ struct Cfg {
     static constexpr int WN = TN / 64;  // waves along N (4 waves of 64 x 64)
 };
 
-// Work item j of the persistent grid: output tile j % tiles over the k-tiles of split
-// j / tiles.  Blocks take items blockIdx.x, + gridDim.x, ...; the k-tiles of a block's items
-// form one stream through the load / split / MFMA pipeline, so the loads of an item's first
-// k-tiles are in flight while the previous item finishes and stores its tile.
-struct Item {
-    int j, t, te;  // item, current k-tile, end of the item's k-tiles
-    int m0, n0;
-};
-
 template <int TM, int TN, bool TA, bool TB>
 __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
     using C = Cfg<TM, TN, TA, TB>;
@@ -185,34 +175,17 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     bf16_t* smem = reinterpret_cast<bf16_t*>(smem_raw);  // [2][A planes | B planes]
 
+    // tile coordinates: XCD-contiguous ranges (blocks are dispatched round-robin over the
+    // 8 XCDs), then 8-tall groups
     const int tilesM = (g.M + TM - 1) / TM, tilesN = (g.N + TN - 1) / TN;
     const int tiles = tilesM * tilesN;
-    const int kt0 = (g.Ks[0] + TK - 1) / TK;
-    const int KT = kt0 + (g.nseg > 1 ? (g.Ks[1] + TK - 1) / TK : 0);
-    const int splits = g.ksplit > 1 ? g.ksplit : 1;
-    const int per = (KT + splits - 1) / splits;
-    const int items = tiles * splits;
-
-    // item -> tile coordinates: XCD-contiguous tile ranges (consecutive items run on
-    // consecutive blocks, dispatched round-robin over the 8 XCDs), then 8-tall groups
-    auto setup = [&](Item& it, int j) {
-        it.j = j;
-        int pid = j % tiles;
-        if ((tiles & 7) == 0) pid = (pid & 7) * (tiles >> 3) + (pid >> 3);
-        const int group_id = pid / (8 * tilesN);
-        const int first_m = group_id * 8;
-        const int gsize = min(tilesM - first_m, 8);
-        const int in_group = pid % (8 * tilesN);
-        it.m0 = (first_m + in_group % gsize) * TM;
-        it.n0 = (in_group / gsize) * TN;
-        it.t = (j / tiles) * per;
-        it.te = min(KT, it.t + per);
-    };
-    // next k-tile of the stream; past the block's last item it stays on the last k-tile
-    auto advance = [&](Item& it) {
-        if (it.t + 1 < it.te) ++it.t;
-        else if (it.j + (int)gridDim.x < items) setup(it, it.j + gridDim.x);
-    };
+    int pid = blockIdx.x;
+    if ((tiles & 7) == 0) pid = (pid & 7) * (tiles >> 3) + (pid >> 3);
+    const int group_id = pid / (8 * tilesN);
+    const int first_m = group_id * 8;
+    const int gsize = min(tilesM - first_m, 8);
+    const int in_group = pid % (8 * tilesN);
+    const int m0 = (first_m + in_group % gsize) * TM, n0 = (in_group / gsize) * TN;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / C::WN, wn = wave % C::WN;
@@ -224,20 +197,27 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) zero16(acc[i][j]);
 
-    // two register sets in flight: when the MFMAs run k-tile u of the stream, set X holds
-    // k-tile u+1 and the other set k-tile u+2 (loads issued two iterations before use)
+    // this block's k-tiles (split blockIdx.y) over the concatenated segments
+    const int kt0 = (g.Ks[0] + TK - 1) / TK;
+    const int KT = kt0 + (g.nseg > 1 ? (g.Ks[1] + TK - 1) / TK : 0);
+    const int splits = g.ksplit > 1 ? g.ksplit : 1;
+    const int per = (KT + splits - 1) / splits;
+    const int tb = blockIdx.y * per, te = min(KT, tb + per);
+
+    // two register sets in flight: when the MFMAs run k-tile t, set X holds k-tile t+1 and
+    // the other set k-tile t+2 (loads issued two iterations before they are needed)
     struct Regs {
         float4 a[LA::NV], b[LB::NV];
         uint32_t oka, okb;
     };
     Regs r0s, r1s;
-    auto gload = [&](const Item& it, Regs& R) {
-        const int sg = it.t < kt0 ? 0 : 1;
-        const int k0 = (it.t < kt0 ? it.t : it.t - kt0) * TK;
+    auto gload = [&](int t, Regs& R) {
+        const int sg = t < kt0 ? 0 : 1;
+        const int k0 = (t < kt0 ? t : t - kt0) * TK;
         // A: TA = 0 -> A[m * lda + k] (k contiguous); TA = 1 -> A[k * lda + m]
-        LA::load(reinterpret_cast<const float*>(g.A[sg]), g.lda[sg], it.m0, g.M, k0, g.Ks[sg], R.a, R.oka);
+        LA::load(reinterpret_cast<const float*>(g.A[sg]), g.lda[sg], m0, g.M, k0, g.Ks[sg], R.a, R.oka);
         // B: TB = 1 -> B[n * ldb + k] (k contiguous); TB = 0 -> B[k * ldb + n]
-        LB::load(reinterpret_cast<const float*>(g.B[sg]), g.ldb[sg], it.n0, g.N, k0, g.Ks[sg], R.b, R.okb);
+        LB::load(reinterpret_cast<const float*>(g.B[sg]), g.ldb[sg], n0, g.N, k0, g.Ks[sg], R.b, R.okb);
     };
     auto sstore = [&](int buf, const Regs& R) {
         bf16_t* st = smem + buf * C::STAGE;
@@ -245,46 +225,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
         LB::store(st + 3 * LA::PLANE, R.b, R.okb);
     };
 
-    // epilogue of an item: accumulator element r of lane l is (row 8(r/4) + 4(l/32) + r%4,
-    // col l%32); split items go to their partial plane; the accumulators restart at zero
-    auto finish = [&](const Item& it) {
-        if (splits > 1) {
-            float* P = g.part + (size_t)(it.j / tiles) * g.M * g.N;
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int n = it.n0 + rb0 + j * 32 + (lane & 31);
-                    if (n >= g.N) continue;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int m = it.m0 + ra0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (m < g.M) P[(size_t)m * g.N + n] = acc[i][j][r];
-                    }
-                }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    gemm_store_tile<float, 0>(g, it.m0 + ra0 + i * 32, it.n0 + rb0 + j * 32, acc[i][j]);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) zero16(acc[i][j]);
-    };
-
-    Item cc, cp;  // the k-tile the MFMAs run, the k-tile the next loads fetch
-    int u = 0;    // position in the stream (selects the LDS stage)
-
-    // one pipeline step on register set R (holding stream k-tile u+1); false once the block's
-    // last item is done
-    auto step = [&](Regs& R) -> bool {
-        // stage u&1 holds k-tile u (split last step); every wave has finished reading the
-        // other stage, which the split below overwrites
+    auto iter = [&](int t, Regs& R) {
+        // stage (t - tb) & 1 holds k-tile t (split last iteration); every wave has finished
+        // reading the other stage, which the split below overwrites
         __syncthreads();
-        const bf16_t* As = smem + (u & 1) * C::STAGE;
+        const bf16_t* As = smem + ((t - tb) & 1) * C::STAGE;
         const bf16_t* Bs = As + 3 * LA::PLANE;
         bf16x8_t a[3][2], b[3][2];
 #pragma unroll
@@ -294,11 +239,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
             b[p][0] = LB::frag(Bs, p, rb0);
             b[p][1] = LB::frag(Bs, p, rb0 + 32);
         }
-        // the next k-tile's split goes into the other stage while the MFMAs below run; the
-        // registers then take the loads of k-tile u+3
-        sstore((u & 1) ^ 1, R);
-        gload(cp, R);
-        advance(cp);
+        // The next k-tile's split goes into the other stage while the MFMAs below run; its
+        // registers then take the loads of k-tile t+3 (clamped into this split's range: past
+        // its end the last tile is loaded again and its split lands in a stage nothing reads).
+        sstore(((t - tb) & 1) ^ 1, R);
+        gload(min(t + 3, te - 1), R);
         // smallest terms first: (2,0) (1,1) (0,2) (1,0) (0,1) (0,0)
         constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
@@ -317,36 +262,46 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
             __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
         }
-        ++u;
-        if (cc.t + 1 < cc.te) {
-            ++cc.t;
-            return true;
-        }
-        finish(cc);
-        if (cc.j + (int)gridDim.x >= items) return false;
-        setup(cc, cc.j + gridDim.x);
-        return true;
     };
 
-    if ((int)blockIdx.x >= items) return;
-    setup(cc, blockIdx.x);
-    cp = cc;
-    gload(cp, r0s);
-    sstore(0, r0s);
-    advance(cp);
-    gload(cp, r0s);
-    advance(cp);
-    gload(cp, r1s);
-    advance(cp);
-    while (step(r0s) && step(r1s)) {
+    if (tb < te) {
+        gload(tb, r0s);
+        sstore(0, r0s);
+        gload(min(tb + 1, te - 1), r0s);
+        gload(min(tb + 2, te - 1), r1s);
+        for (int t = tb; t < te; t += 2) {
+            iter(t, r0s);
+            if (t + 1 < te) iter(t + 1, r1s);
+        }
+    }
+
+    // epilogue: accumulator element r of lane l is (row 8(r/4) + 4(l/32) + r%4, col l%32);
+    // a split's partial tile goes to its plane
+    if (splits > 1) {
+        float* P = g.part + (size_t)blockIdx.y * g.M * g.N;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + rb0 + j * 32 + (lane & 31);
+                if (n >= g.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + ra0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (m < g.M) P[(size_t)m * g.N + n] = acc[i][j][r];
+                }
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                gemm_store_tile<float, 0>(g, m0 + ra0 + i * 32, n0 + rb0 + j * 32, acc[i][j]);
     }
 }
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// persistent grid (measured on MI355X at the hypernetwork's output layer, dW 163840 x 1536
-// over 64 rows: 445 us persistent, 477 us with one block per item)
-constexpr bool PERSIST = true;
 
 inline int k_tiles(const GemmDesc& g) {
     return (g.Ks[0] + TK - 1) / TK + (g.nseg > 1 ? (g.Ks[1] + TK - 1) / TK : 0);
@@ -356,7 +311,7 @@ inline int k_tiles(const GemmDesc& g) {
 // else 128 x 128 (also measured for wide outputs: 256-column tiles were no faster)
 inline bool wide(const GemmDesc& g) { return g.M <= 64; }
 
-// Blocks the persistent grid runs: two per CU (the kernel's VGPRs allow two waves per SIMD).
+// Blocks that run at once: two per CU (the kernel's VGPRs allow two waves per SIMD).
 int resident_blocks() {
     static const int n = [] {
         int dev = 0, cus = 0;
@@ -369,8 +324,8 @@ int resident_blocks() {
     return n;
 }
 
-// Splits of K for shapes with fewer tiles than the persistent grid has blocks: as many ranges
-// as fill the grid once (items = tiles x splits <= blocks, no half-empty second round), each
+// Splits of K for shapes with fewer tiles than the GPU runs blocks at once: as many ranges as
+// fill it once (tiles x splits <= blocks, no half-empty second round), each
 // at least 16 k-tiles (256 k), the partial planes within cap.  Returns the number of
 // non-empty ranges (1: no split).
 int choose_split(const GemmDesc& g, size_t cap) {
@@ -397,9 +352,9 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
         set_error("gn_gemm (fp32): cannot reserve %zu B of LDS", smem);
         return GN_E_HIP;
     }
-    const long items = (long)((g.M + TM - 1) / TM) * ((g.N + TN - 1) / TN) * (g.ksplit > 1 ? g.ksplit : 1);
-    const int grid = (int)std::min<long>(items, PERSIST ? resident_blocks() : INT32_MAX);
-    hipLaunchKernelGGL((gemm_f32x6<TM, TN, TA, TB>), dim3(grid), dim3(256), smem, s, g);
+    const int tiles = ((g.M + TM - 1) / TM) * ((g.N + TN - 1) / TN);
+    hipLaunchKernelGGL((gemm_f32x6<TM, TN, TA, TB>), dim3(tiles, g.ksplit > 1 ? g.ksplit : 1),
+                       dim3(256), smem, s, g);
     if (g.ksplit > 1) launch_split_reduce(g, s);
     GN_LAUNCH_CHECK("gn_gemm (fp32 bf16x6)");
     return GN_OK;
