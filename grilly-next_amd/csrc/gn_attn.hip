@@ -124,6 +124,41 @@ __device__ __forceinline__ void dma_tile(const bf16_t* __restrict__ g, int64_t s
     }
 }
 
+// Lane byte offsets of dma_tile's instructions relative to the tile's first row (the
+// wave's D/(8 NW) instructions; the row stride sr is below 2^24 elements, checked by the
+// entry points).  A tile whose 64 rows all lie before S then moves with a scalar base only.
+template <int D, int NW = 4>
+struct TileOffsets {
+    static constexpr int CPR = D / 8, RPI = 64 / CPR, PER_WAVE = CPR / NW;
+    uint32_t v[PER_WAVE];
+    __device__ __forceinline__ void init(int64_t sr, int wave) {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            const int r = (wave * PER_WAVE + j) * RPI + lane / CPR;
+            const int c = (lane % CPR) ^ tswz<D>(r);
+            v[j] = (uint32_t)(r * (int)sr + c * 8) * 2u;
+        }
+    }
+};
+
+// dma_tile with precomputed lane offsets (wave: the wave-uniform wave index); the last tile
+// of a sequence that is not a multiple of 64 long takes the clamping path
+template <int D, int NW = 4>
+__device__ __forceinline__ void dma_tile_o(const bf16_t* __restrict__ g, int64_t sr, int row0,
+                                           int S, uint32_t lds, int wave,
+                                           const TileOffsets<D, NW>& o) {
+    using O = TileOffsets<D, NW>;
+    if (row0 + 64 <= S) {
+        const bf16_t* base = g + (int64_t)row0 * sr;
+#pragma unroll
+        for (int j = 0; j < O::PER_WAVE; ++j)
+            dma16s(base, o.v[j], lds + (uint32_t)((wave * O::PER_WAVE + j) * 1024));
+    } else {
+        dma_tile<D, NW>(g, sr, row0, S, lds);
+    }
+}
+
 // Fragment whose 32 rows are tile rows m0 .. m0+31 and whose k runs along d:
 // lane l -> row m0 + l%32, d = 16 ks + 8(l/32) .. +7.
 template <int D>
@@ -254,11 +289,14 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     const uint32_t lds0 = lds_addr(smem);
     const int t0 = causal ? j0 / 64 : 0;
     const int T = (S + 63) / 64 - t0;
+    TileOffsets<D, NW> oQ, oG;
+    oQ.init(tQ.sr, wave);
+    oG.init(tG.sr, wave);
     auto issue = [&](int it) {
         const int q0 = (t0 + it) * 64;
         const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
-        dma_tile<D, NW>(Qr, tQ.sr, q0, S, sb);
-        dma_tile<D, NW>(dO, tG.sr, q0, S, sb + C::TB);
+        dma_tile_o<D, NW>(Qr, tQ.sr, q0, S, sb, wave, oQ);
+        dma_tile_o<D, NW>(dO, tG.sr, q0, S, sb + C::TB, wave, oG);
         // 64 L values then 64 D_i values: one DMA instruction per wave
         constexpr int LANES = 32 / NW;  // 16-byte pieces per wave (32 pieces in all)
         if (lane < LANES) {
@@ -433,10 +471,13 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(
     const uint32_t lds0 = lds_addr(smem);
     const int kend = causal ? min(S, i0 + 128) : S;
     const int T = (kend + 63) / 64;
+    TileOffsets<D> oK, oV;
+    oK.init(tK.sr, wave);
+    oV.init(tV.sr, wave);
     auto issue = [&](int it) {
         const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
-        dma_tile<D>(Kr, tK.sr, it * 64, S, sb);
-        dma_tile<D>(V, tV.sr, it * 64, S, sb + C::TB);
+        dma_tile_o<D>(Kr, tK.sr, it * 64, S, sb, wave, oK);
+        dma_tile_o<D>(V, tV.sr, it * 64, S, sb + C::TB, wave, oV);
     };
 
     issue(0);
@@ -549,10 +590,13 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma(TDesc tQ, TDesc tK, TDesc t
     const uint32_t lds0 = lds_addr(smem);
     const int kend = causal ? min(S, i0 + 128) : S;
     const int T = (kend + 63) / 64;
+    TileOffsets<D> oK, oV;
+    oK.init(tK.sr, wave);
+    oV.init(tV.sr, wave);
     auto issue = [&](int it) {
         const uint32_t sb = lds0 + (it % STAGES) * C::STAGE;
-        dma_tile<D>(Kr, tK.sr, it * 64, S, sb);
-        dma_tile<D>(V, tV.sr, it * 64, S, sb + C::TB);
+        dma_tile_o<D>(Kr, tK.sr, it * 64, S, sb, wave, oK);
+        dma_tile_o<D>(V, tV.sr, it * 64, S, sb + C::TB, wave, oV);
     };
 
     issue(0);
@@ -1112,6 +1156,8 @@ extern "C" int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, con
                "gn_attn_bwd_bshd: row strides must cover H*D = %d elements", H * D);
     GN_REQUIRE(ld_qkv % 8 == 0 && ld_o % 8 == 0 && ld_dqkv % 8 == 0,
                "gn_attn_bwd_bshd: row strides must be multiples of 8 elements");
+    GN_REQUIRE(ld_qkv < (1 << 24) && ld_o < (1 << 24) && ld_dqkv < (1 << 24),
+               "gn_attn_bwd_bshd: row strides must be below 2^24 elements");
     const void* ptrs[8] = {Q, K, V, O, dO, dQ, dK, dV};
     for (const void* p : ptrs)
         GN_REQUIRE(((uintptr_t)p & 15u) == 0, "gn_attn_bwd_bshd: pointers must be 16-byte aligned");

@@ -21,17 +21,12 @@
 #include <utility>
 
 #include "gn_common.h"
-#include "gn_math.h"
 #include "gn_gemm_dma.h"
+#include "gn_math.h"
+#include "gn_mfma.h"
 
 namespace gn {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
 
 constexpr int BK = 64;
 
@@ -41,24 +36,6 @@ __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
 // differ in bits 1-2 and in bits 2-3, so the read is conflict-free on a 32-bank and on a
 // 64-bank (gfx950) LDS alike (2(k & 3) left 2-way conflicts on 64 banks).
 __device__ __forceinline__ int fko(int k) { return ((k & 1) * 6) ^ (((k >> 1) & 1) * 10); }
-
-// One 16-byte DMA per lane: lane l's bytes land at LDS byte address lds_base + 16*l.
-// Issued from inline assembly: the compiler then does not order later LDS reads of the
-// *other* stage behind this DMA (it cannot tell the two stages apart); the kernel waits
-// for its own DMA explicitly (s_waitcnt vmcnt(0) + barrier) before reading a stage.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off"
-        :
-        : "s"(lds_base), "v"(g)
-        : "memory", "m0");
-}
-
-// s_waitcnt immediate: at most N vector-memory operations outstanding (vmcnt bits [3:0]
-// and [15:14]; expcnt and lgkmcnt left at their maxima)
-constexpr unsigned vmcnt_imm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }
 
 // Stage one operand tile of R rows/cols (R = BM or BN) into LDS (R*64 bf16 = R*8 chunks,
 // R/8 DMA instructions, R/32 per wave).
@@ -90,6 +67,32 @@ __device__ __forceinline__ void stage(const bf16_t* __restrict__ P, int ld, int 
     }
 }
 
+// Lane byte offsets of the wave's DMA instructions of stage<R, KC, NW> (same element map),
+// relative to the tile base stage_base<KC>(P, ld, r0, k0); independent of k0.
+template <int R, bool KC, int NW, int NJ = R / (8 * NW)>
+__device__ __forceinline__ void stage_offsets(int ld, int r0, int rlim, int wave, uint32_t (&vo)[NJ]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int slot = 64 * (wave * NJ + j) + lane;
+        if (KC) {
+            const int r = slot >> 3, c = (slot & 7) ^ swz(r);
+            const int rr = min(r0 + r, rlim - 1) - r0;  // rows past the edge re-read a valid row
+            vo[j] = (uint32_t)(rr * ld + c * 8) * 2u;
+        } else {
+            constexpr int CPR = R / 8;
+            const int k = slot / CPR, c = (slot % CPR) ^ fko(k);
+            const int col = min(r0 + c * 8, rlim - 8) - r0;
+            vo[j] = (uint32_t)(k * ld + col) * 2u;
+        }
+    }
+}
+
+template <bool KC>
+__device__ __forceinline__ const bf16_t* stage_base(const bf16_t* P, int ld, int r0, int k0) {
+    return KC ? P + (size_t)r0 * ld + k0 : P + (size_t)k0 * ld + r0;
+}
+
 // A-type fragment (32 rows x 16 k) for v_mfma_f32_32x32x16_bf16: lane l -> row l%32,
 // k = 8(l/32) .. +7 within k-step ks.
 template <int R, bool KC>
@@ -110,7 +113,6 @@ __device__ __forceinline__ bf16x8_t frag(const bf16_t* s, int row0, int ks) {
         const bf16_t* p1 = p0 + 4 * R;  // k + 4 (same swizzle: fko(k+4) == fko(k))
         s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
         s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
-        typedef short s16x8_t __attribute__((ext_vector_type(8)));
         s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         return __builtin_bit_cast(bf16x8_t, v);
     }
@@ -416,7 +418,8 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
     const int m0 = (first_m + in_group % gsize) * BM;
     const int n0 = (in_group / gsize) * BN;
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;
 
     f32x16_t acc[FM][FN];
@@ -441,17 +444,44 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
     const int lda0 = g.lda[0], lda1 = g.lda[1], ldb0 = g.ldb[0], ldb1 = g.ldb[1];
 
     constexpr int NDA = BM / (8 * NW), NDB = BN / (8 * NW);
+    // Lane offsets of the wave's DMA instructions for segment `oseg` (they depend on the
+    // segment's leading dimensions only; recomputed once if the two segments differ).  The
+    // 256 x 256 bias variant has no 16 VGPRs to spare for them (its accumulators fill the
+    // AGPRs): it computes each DMA address as it issues it.
+    constexpr bool PRE = !(BM == 256 && BN == 256 && BIAS);
+    uint32_t voa[PRE ? NDA : 1], vob[PRE ? NDB : 1];
+    int oseg = 0;
+    auto set_offsets = [&](int seg) {
+        if constexpr (PRE) {
+            stage_offsets<BM, !TA, NW>(seg ? lda1 : lda0, m0, g.M, wave, voa);
+            stage_offsets<BN, TB, NW>(seg ? ldb1 : ldb0, n0, g.N, wave, vob);
+        }
+        oseg = seg;
+    };
+    const bool reoffset = PRE && g.nseg > 1 && (lda0 != lda1 || ldb0 != ldb1);
+    auto offsets_for = [&](int tl) {  // before the DMAs of tile tl (tiles are issued in order)
+        if (reoffset && oseg == 0 && kt_lo + tl >= kt0) set_offsets(1);
+    };
     auto dma_one = [&](auto Q_, int tl, int buf) {
         constexpr int q = decltype(Q_)::value;
         const int t = kt_lo + tl;
         const bool s1 = t >= kt0;
         const int k0 = (s1 ? t - kt0 : t) * BK;
         const uint32_t base = lds0 + (uint32_t)(buf * STAGE_B);
-        if constexpr (q < NDA)
-            stage<BM, !TA, NW, q, q + 1>(s1 ? A1 : A0, s1 ? lda1 : lda0, m0, g.M, k0, base);
-        else
-            stage<BN, TB, NW, q - NDA, q - NDA + 1>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, g.N, k0,
-                                                   base + A_ELEMS * 2);
+        if constexpr (!PRE) {
+            if constexpr (q < NDA)
+                stage<BM, !TA, NW, q, q + 1>(s1 ? A1 : A0, s1 ? lda1 : lda0, m0, g.M, k0, base);
+            else
+                stage<BN, TB, NW, q - NDA, q - NDA + 1>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, g.N, k0,
+                                                       base + A_ELEMS * 2);
+        } else if constexpr (q < NDA) {
+            const bf16_t* src = stage_base<!TA>(s1 ? A1 : A0, s1 ? lda1 : lda0, m0, k0);
+            dma16s(src, voa[q], base + 1024u * (uint32_t)(wave * NDA + q));
+        } else {
+            constexpr int qb = q - NDA;
+            const bf16_t* src = stage_base<TB>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, k0);
+            dma16s(src, vob[qb], base + A_ELEMS * 2 + 1024u * (uint32_t)(wave * NDB + qb));
+        }
     };
     bf16x8_t fa[4][FM], fb[4][FN];
     // BIAS: per-lane partial row sums of op(A): fragment i holds row (lane % 32) of rows
@@ -550,6 +580,7 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
         else  // vmcnt(0) and lgkmcnt(0)
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & 0xF0FFu);
         __syncthreads();
+        offsets_for(min(t + STAGES, last));
         kstep(I2{}, I0{}, BF{}, BT{}, nxt, 0, min(t + STAGES, last), buf);
         kstep(I3{}, I1{}, BF{}, BF{}, nxt, 1, 0, 0);
     };
@@ -558,9 +589,12 @@ __global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
         auto dma_all = [&](int tl, int buf) {
             static_for<ND>([&](auto D_) { dma_one(D_, tl, buf); });
         };
+        set_offsets(kt_lo >= kt0 ? 1 : 0);
         dma_all(0, 0);
+        offsets_for(min(1, last));
         dma_all(min(1, last), 1);
         if constexpr (STAGES == 3) {
+            offsets_for(min(2, last));
             dma_all(min(2, last), 2);
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * ND));
         } else {

@@ -67,6 +67,21 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
         : "memory", "m0");
 }
 
+// The same DMA from a wave-uniform base (SGPRs) plus a per-lane 32-bit byte offset.  A
+// tile's base moves with k on the scalar unit while the lane offsets (row and swizzled
+// chunk within the tile) are computed once per kernel, so a tile's DMA costs no vector
+// instructions; 64-bit per-lane address arithmetic per tile takes ~8 VALU instructions
+// per DMA, most of them multi-pass, and stretches the MFMA step that issues them.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2"
+        :
+        : "s"(lds_base), "v"(voff), "s"(sbase)
+        : "memory", "m0");
+}
+
 // s_waitcnt immediate that waits until at most N vector-memory operations are
 // outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima)
 constexpr unsigned vmcnt_imm(unsigned n) { return 0x0F70u | (n & 15u) | ((n >> 4) << 14); }

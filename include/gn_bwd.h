@@ -246,8 +246,8 @@ size_t gn_attn_workspace_bytes(int B, int H, int S, int D);
  * stays [B, H, S].  The reference binds attention on [B,H,S,D] only
  * (cpp/python/bindings.cpp:425-432); its FA2 forward runs on [B,S,H,D]
  * (flash-attention2.glsl:9,136-143), which is the layout accepted here.
- * bf16, D = 64 or 128; strides multiples of 8, pointers 16-byte aligned;
- * ws: gn_attn_workspace_bytes(B, H, S, D). */
+ * bf16, D = 64 or 128; strides multiples of 8 and below 2^24 elements, pointers 16-byte
+ * aligned; ws: gn_attn_workspace_bytes(B, H, S, D). */
 int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, const void* O, const void* dO,
                      const float* LSE, void* dQ, void* dK, void* dV, int B, int H, int S, int D,
                      int64_t ld_qkv, int64_t ld_o, int64_t ld_dqkv, float scale, int causal,

@@ -110,3 +110,18 @@ def test_misaligned_attention_views_rejected_without_gpu():
                            1 << 24, None)
     assert lib.gn_attn_bwd_bshd(*args(2)) == -1
     assert "16-byte aligned" in gn_bwd.last_error()
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_attention_row_strides_bounded_without_gpu():
+    # the DMA lane offsets of the attention kernels are 32-bit: a [B,S,H,D] row stride of
+    # 2^24 elements or more is refused before any HIP call
+    import gn_bwd
+    lib = gn_bwd.lib()
+    base = 1 << 20
+    p = lambda off=0: ctypes.c_void_p(base + off)
+    big = 1 << 24
+    args = (p(0), p(256), p(512), p(4096), p(8192), p(12288), p(16384), p(256), p(512), 1, 2,
+            64, 64, big, 128, 384, 0.125, 1, 0, 1e4, 4, p(1 << 16), 1 << 24, None)
+    assert lib.gn_attn_bwd_bshd(*args) == -1
+    assert "below 2^24" in gn_bwd.last_error()
