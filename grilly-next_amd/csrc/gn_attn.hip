@@ -335,22 +335,27 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
 #pragma unroll
         for (int hh = 0; hh < HALVES; ++hh) {
             const int i = half0 + hh;
-            // S, dP: the fragments of k-step ks+1 are requested before the MFMAs of ks; the
+            // S, dP: all four fragments of k-step ks+1 (Q, dO, K, V rows) are requested before
+            // the MFMAs of ks, so no MFMA waits on a read issued right before it; the
             // scheduling fences keep the compiler from hoisting every LDS read up front
             f32x16_t s, dp;
             zero16(s);
             zero16(dp);
-            bf16x8_t fa[2][2];
+            bf16x8_t fa[2][2], kv[2][2];
             fa[0][0] = frag_rows<D>(sQ, 32 * i, 0);
             fa[0][1] = frag_rows<D>(sG, 32 * i, 0);
+            kv[0][0] = frag_rows<D>(sKb, 32 * kg, 0);
+            kv[0][1] = frag_rows<D>(sVb, 32 * kg, 0);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if (ks + 1 < KS) {
                     fa[(ks + 1) & 1][0] = frag_rows<D>(sQ, 32 * i, ks + 1);
                     fa[(ks + 1) & 1][1] = frag_rows<D>(sG, 32 * i, ks + 1);
+                    kv[(ks + 1) & 1][0] = frag_rows<D>(sKb, 32 * kg, ks + 1);
+                    kv[(ks + 1) & 1][1] = frag_rows<D>(sVb, 32 * kg, ks + 1);
                 }
-                s = mfma32(fa[ks & 1][0], frag_rows<D>(sKb, 32 * kg, ks), s);
-                dp = mfma32(fa[ks & 1][1], frag_rows<D>(sVb, 32 * kg, ks), dp);
+                s = mfma32(fa[ks & 1][0], kv[ks & 1][0], s);
+                dp = mfma32(fa[ks & 1][1], kv[ks & 1][1], dp);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // the first transpose fragments of the dV / dK step are in flight during the exp work
