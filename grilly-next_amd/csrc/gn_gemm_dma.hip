@@ -988,6 +988,14 @@ inline size_t part_bytes(const GemmDesc& g, int ks) {
 inline TileChoice choose_tile(const GemmDesc& g, bool ta, size_t c_bytes, int epi) {
     const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
     const bool can_split = epi == 0 && c_bytes == 4 && !g.accumulate && !g.cbias && KT >= 32;
+    // GLU epilogue over a long k loop: 128 x 128 tiles.  Their two-stage variant holds two
+    // blocks per CU (64 KB of LDS, 197 registers), so one block's epilogue (gate/up loads,
+    // glu', 16-byte stores) overlaps the other's main loop, which the time model does not
+    // describe.  Measured on MI355X, down projection 4096 x 5632 x 2048 with dWd: 225-228 us
+    // against 230-236 us for the 256 x 128 / 128 x 256 / 256 x 256 shapes (interleaved runs,
+    // one process).  Short k loops (the decoder's 8192 x 3072 x 768) keep the model's choice:
+    // there the doubled block count's fixed costs weigh more.
+    if (epi == 1 && KT >= 24) return {3, 1};
     TileChoice best{1, 1};
     double bt = tile_cost(g, ta, c_bytes, epi, 1, 1);
     for (int i = 0; i < 4; ++i) {
