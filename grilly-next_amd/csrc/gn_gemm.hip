@@ -242,6 +242,79 @@ __global__ __launch_bounds__(256) void gemm_simt(GemmDesc g) {
         }
 }
 
+// ---- small products: one thread per output, the whole k loop in registers ---------------
+// For products whose tiles would leave the GPU nearly idle (an MLP layer of a few hundred
+// units over a batch of 64, the 10-wide output layer): every load of the k loop is issued
+// without a barrier or an LDS round trip, so the kernel costs about one memory latency.
+// Sequential k order per output (deterministic); fp32 FMA, so fp32 operands get full fp32
+// precision.
+constexpr int kSmallMaxK = 128;
+constexpr int64_t kSmallMaxMac = (int64_t)1 << 24;
+
+template <typename TI, typename CT, bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_small(GemmDesc g) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)g.M * g.N) return;
+    const int m = (int)(idx / g.N), n = (int)(idx % g.N);
+    float acc = 0.f;
+    for (int s = 0; s < g.nseg; ++s) {
+        const TI* A = reinterpret_cast<const TI*>(g.A[s]);
+        const TI* B = reinterpret_cast<const TI*>(g.B[s]);
+        const int Ks = g.Ks[s], lda = g.lda[s], ldb = g.ldb[s];
+#pragma unroll 16
+        for (int k = 0; k < Ks; ++k) {
+            const float a = TA ? io<TI>::ld(A, (size_t)k * lda + m) : io<TI>::ld(A, (size_t)m * lda + k);
+            const float b = TB ? io<TI>::ld(B, (size_t)n * ldb + k) : io<TI>::ld(B, (size_t)k * ldb + n);
+            acc = fmaf(a, b, acc);
+        }
+    }
+    gemm_store<CT, 0>(g, m, n, acc);
+}
+
+inline bool small_applicable(const GemmDesc& d) {
+    const int64_t K = (int64_t)d.Ks[0] + (d.nseg > 1 ? d.Ks[1] : 0);
+    return d.epi == 0 && !d.bias && !d.cbias && d.ksplit <= 1 && K <= kSmallMaxK &&
+           (int64_t)d.M * d.N * K <= kSmallMaxMac;
+}
+
+template <typename TI, typename CT>
+int launch_small(const GemmDesc& g, int ta, int tb, hipStream_t s) {
+    const unsigned grid = (unsigned)(((int64_t)g.M * g.N + 255) / 256);
+    if (!ta && !tb) gemm_small<TI, CT, false, false><<<grid, 256, 0, s>>>(g);
+    else if (!ta && tb) gemm_small<TI, CT, false, true><<<grid, 256, 0, s>>>(g);
+    else if (ta && !tb) gemm_small<TI, CT, true, false><<<grid, 256, 0, s>>>(g);
+    else gemm_small<TI, CT, true, true><<<grid, 256, 0, s>>>(g);
+    GN_LAUNCH_CHECK("gemm (small)");
+    return GN_OK;
+}
+
+// ---- column sums over few rows: one pass, deterministic ---------------------------------
+// Block: 16 waves x 64 columns (lane = column); wave w adds rows w, w + 16, ... (all of its
+// loads issued together), the waves' sums are added in a fixed order.  No clear, no second
+// launch.
+constexpr int kColsumSmallRows = 1024;
+
+template <typename TI>
+__global__ __launch_bounds__(1024) void colsum_small(const TI* __restrict__ in, float* __restrict__ out,
+                                                     int M, int N, int ld, int accumulate) {
+    __shared__ float sh[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (n < N) {
+#pragma unroll 8
+        for (int r = wave; r < M; r += 16) s += io<TI>::ld(in, (size_t)r * ld + n);
+    }
+    sh[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && n < N) {
+        float t = sh[0][lane];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) t += sh[w][lane];
+        out[n] = accumulate ? out[n] + t : t;
+    }
+}
+
 // ---- column sums (db): thread per column, rows split over grid.y with fp32 atomics ------
 template <typename TI>
 __global__ __launch_bounds__(256) void colsum_kernel(const TI* __restrict__ in, float* out,
@@ -398,6 +471,7 @@ int gemm_run(const GemmDesc& d, int transA, int transB, int dtype, int c_dtype, 
             set_error("gemm: the GLU epilogue needs bf16 operands");
             return GN_E_INVALID;
         }
+        if (small_applicable(d)) return launch_small<float, float>(d, transA, transB, s);
         if (gemm_f32_applicable(d)) return gemm_f32_launch(d, transA, transB, s);
         return launch_simt<float, float, 0>(d, transA, transB, s);
     }
@@ -557,6 +631,14 @@ int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigne
     if (N == 0) return GN_OK;
     GN_REQUIRE(in && out, "gn_colsum: null pointer");
     const size_t es = dtype == GN_F32 ? 4 : 2;
+    if (M > 0 && M <= kColsumSmallRows && (dtype == GN_F32 || dtype == GN_BF16)) {
+        const unsigned g = (unsigned)((N + 63) / 64);
+        const int acc = (flags & GN_ACCUMULATE) ? 1 : 0;
+        if (dtype == GN_F32) colsum_small<float><<<g, 1024, 0, s>>>((const float*)in, out, M, N, ld, acc);
+        else colsum_small<bf16_t><<<g, 1024, 0, s>>>((const bf16_t*)in, out, M, N, ld, acc);
+        GN_LAUNCH_CHECK("gn_colsum (few rows)");
+        return GN_OK;
+    }
     const bool vec = N % 8 == 0 && ld % 8 == 0 && al16(in) && (dtype == GN_F32 || dtype == GN_BF16);
     if (scratch && vec && M > 0 && scratch_floats >= (size_t)N) {
         const int cb = (N + 511) / 512;
