@@ -736,7 +736,8 @@ __global__ __launch_bounds__(64 * kVsaNW, 1) void vsa_dw_dma(VsaDesc v) {
     int pid = blockIdx.x;
     if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);  // XCD-contiguous ranges
     const int m0 = (pid % tilesM) * BM, n0 = (pid / tilesM) * BN;  // the M tiles of one n share bits
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;
 
     f32x16_t acc[FM][FN];
@@ -750,11 +751,20 @@ __global__ __launch_bounds__(64 * kVsaNW, 1) void vsa_dw_dma(VsaDesc v) {
     const int KT = v.K / BK;
     const bf16_t* const Ahi = v.A[0];
     const bf16_t* const Alo = v.A[1];
-    auto stage_base = [&](int buf) { return lds0 + (uint32_t)(buf * C::STAGE_B); };
+    // lane offsets of the wave's A DMAs (the hi and lo planes share lda, hence the offsets)
+    constexpr int NJ = BM / (8 * NW);
+    uint32_t voa[NJ];
+    stage_offsets<BM, true, NW>(v.lda, m0, v.M, wave, voa);
     auto dma_a = [&](int tl, int buf) {
-        const uint32_t base = stage_base(buf);
-        stage<BM, true, NW>(Ahi, v.lda, m0, v.M, tl * BK, base);
-        if constexpr (TWO) stage<BM, true, NW>(Alo, v.lda, m0, v.M, tl * BK, base + C::A_ELEMS * 2);
+        const uint32_t base = lds0 + (uint32_t)(buf * C::STAGE_B) + 1024u * (uint32_t)(wave * NJ);
+        const bf16_t* hi = stage_base<true>(Ahi, v.lda, m0, tl * BK);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) dma16s(hi, voa[j], base + 1024u * j);
+        if constexpr (TWO) {
+            const bf16_t* lo = stage_base<true>(Alo, v.lda, m0, tl * BK);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) dma16s(lo, voa[j], base + C::A_ELEMS * 2 + 1024u * j);
+        }
     };
     // raw words: lane (wave w, l), slot i -> k-row 16w + 8i + l/8, word l%8 of the tile's 8
     const uint32_t* bits_base = v.bits + n0 / 32 + (lane & 7);
