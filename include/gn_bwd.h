@@ -111,7 +111,9 @@ int gn_gemm(const void* A0, const void* B0, int K0, const void* A1, const void* 
             void* C, int M, int N, int transA, int transB, int dtype, int c_dtype,
             unsigned flags, void* stream);
 
-/* Column sums: out[N] (+)= sum_rows in[M x N] (fp32 out; in is f32 or bf16). */
+/* Column sums: out[N] (+)= sum_rows in[M x N] (fp32 out; in is f32 or bf16).  Up to 1024 rows
+ * in one pass with a fixed summation order (bit-identical reruns); more rows are split over
+ * row blocks added with fp32 atomics. */
 int gn_colsum(const void* in, float* out, int M, int N, int dtype, unsigned flags, void* stream);
 
 /* ---- activations ------------------------------------------------------------------ */

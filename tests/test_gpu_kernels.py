@@ -106,7 +106,7 @@ def test_gemm_unaligned_falls_back(gn):
 # ~2e-3 on these inputs.
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("shape", [(136, 200, 72), (256, 128, 640), (132, 68, 1000), (8, 8, 8),
-                                   (10, 13, 7)])
+                                   (10, 13, 7), (1024, 1024, 64)])
 def test_gemm_fp32_layouts(gn, ta, tb, shape):
     M, N, K = shape
     r = rng_(31)
@@ -133,6 +133,51 @@ def test_gemm_fp32_two_segments_and_accumulate(gn):
     assert rel_err(host(C), ref) < FP32_TOL
     gn.gemm(dev(A0), dev(B0), C=C, accumulate=True)
     assert rel_err(host(C), ref + A0.astype(np.float64) @ B0) < FP32_TOL
+
+
+# Small fp32 products (k <= 128 and M*N*k <= 2^24) take a one-thread-per-output kernel with a
+# sequential fp32 k loop; the shapes straddle both limits, so each pair runs on the two paths.
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+@pytest.mark.parametrize("shape", [(40, 52, 128), (40, 52, 129), (2048, 64, 128), (2048, 65, 128),
+                                   (10, 256, 64), (64, 256, 10), (1, 1, 1)])
+def test_gemm_fp32_small_path_edges(gn, ta, tb, shape):
+    M, N, K = shape
+    r = rng_(34)
+    A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    a = (A.T if ta else A).astype(np.float64)
+    b = (B.T if tb else B).astype(np.float64)
+    ref = a @ b
+    C0 = r.standard_normal((M, N)).astype(np.float32)
+    C = gn.gemm(dev(A), dev(B), bool(ta), bool(tb))
+    mag = np.abs(a) @ np.abs(b)
+    bound = 2.0 ** (-20 if K <= 128 else -18) * max(1, K // 64)
+    assert np.all(np.abs(host(C) - ref) <= bound * mag + 1e-30)
+    Cacc = dev(C0)
+    gn.gemm(dev(A), dev(B), bool(ta), bool(tb), C=Cacc, accumulate=True)
+    assert np.all(np.abs(host(Cacc) - (ref + C0)) <= bound * (mag + np.abs(C0)) + 1e-30)
+
+
+@pytest.mark.parametrize("M", [1, 7, 64, 1024, 1025])
+@pytest.mark.parametrize("N", [10, 300])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_colsum_few_and_many_rows(gn, M, N, dtype):
+    """Column sums: up to 1024 rows in one deterministic pass (reruns bit-identical), more
+    over row blocks; both against fp64 sums of the same (rounded) values, overwrite and
+    accumulate."""
+    r = rng_(35)
+    x = r.standard_normal((M, N)).astype(np.float32)
+    xd = dev(x, dtype)
+    ref = host(xd).astype(np.float64).sum(axis=0)
+    out = gn.colsum(xd)
+    tol = 1e-6 * np.abs(host(xd)).astype(np.float64).sum(axis=0) + 1e-30
+    assert np.all(np.abs(host(out) - ref) <= tol)
+    if M <= 1024:
+        assert torch.equal(out, gn.colsum(xd))
+    base = dev(r.standard_normal(N).astype(np.float32))
+    acc = base.clone()
+    gn.colsum(xd, out=acc, accumulate=True)
+    assert np.all(np.abs(host(acc) - (ref + host(base))) <= tol + 1e-6 * np.abs(host(base)))
 
 
 def test_linear_fp32_c1_first_layer(gn):
