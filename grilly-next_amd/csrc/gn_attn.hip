@@ -710,15 +710,40 @@ __global__ __launch_bounds__(256) void rope_table(float2* __restrict__ cs, int S
     }
 }
 
-// Rotate chunk c (8 elements) of one row of Q and of K (qk4[0], qk4[1], bf16) at sequence
-// position pos with the cos/sin table, into Qout / Kout.  Lanes c of one row are D/8
+// The cos/sin entries chunk c of a row at position pos needs: 4 pairs (interleaved mode,
+// pairs 4c .. 4c+3) or 8 (half mode, pairs 8 (c mod D/16) .. +7), as 16-byte loads, issued
+// with the row's own loads so a lane waits on one memory round trip.
+template <int D>
+struct RopeTab {
+    float4 w[4];  // pair e: (w[e / 2].x, .y) for even e, (.z, .w) for odd e
+    __device__ __forceinline__ float2 operator[](int e) const {
+        const float4 v = w[e >> 1];
+        return (e & 1) ? make_float2(v.z, v.w) : make_float2(v.x, v.y);
+    }
+};
+template <int D>
+__device__ __forceinline__ void load_rope_tab(const float2* __restrict__ cs, int pos, int c, int mode,
+                                              RopeTab<D>& tab) {
+    constexpr int LPR = D / 8;
+    const float4* t = reinterpret_cast<const float4*>(cs + (size_t)pos * (D / 2));
+    const bool inter = mode == GN_ROPE_INTERLEAVED;  // uniform: a kernel argument
+    const int base = inter ? 2 * c : 4 * (c % (LPR / 2));
+    // four unconditional loads from in-row addresses (the interleaved mode re-reads its second
+    // vector for the unused pairs 4..7), so no load hides behind a branch or a pointer select
+    tab.w[0] = t[base];
+    tab.w[1] = t[base + 1];
+    tab.w[2] = t[inter ? base + 1 : base + 2];
+    tab.w[3] = t[inter ? base + 1 : base + 3];
+}
+
+// Rotate chunk c (8 elements) of one row of Q and of K (qk4[0], qk4[1], bf16) with the
+// chunk's cos/sin entries (load_rope_tab), into Qout / Kout.  Lanes c of one row are D/8
 // consecutive lanes (the half mode pairs chunk c with chunk c ^ D/16 across lanes).
 template <int D>
-__device__ __forceinline__ void rotate_qk_chunk(const uint4 (&qk4)[2], int c, int pos,
-                                                const float2* __restrict__ cs, int mode,
-                                                bf16_t* __restrict__ Qout, bf16_t* __restrict__ Kout) {
+__device__ __forceinline__ void rotate_qk_chunk(const uint4 (&qk4)[2], int c, const RopeTab<D>& tab,
+                                                int mode, bf16_t* __restrict__ Qout,
+                                                bf16_t* __restrict__ Kout) {
     constexpr int LPR = D / 8;
-    const float2* t = cs + (size_t)pos * (D / 2);
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
         const uint4 v4 = qk4[which];
@@ -732,7 +757,7 @@ __device__ __forceinline__ void rotate_qk_chunk(const uint4 (&qk4)[2], int c, in
         if (mode == GN_ROPE_INTERLEAVED) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float2 r = t[4 * c + e];
+                const float2 r = tab[e];
                 const float x0 = x[2 * e], x1 = x[2 * e + 1];
                 x[2 * e] = x0 * r.x - x1 * r.y;
                 x[2 * e + 1] = x0 * r.y + x1 * r.x;
@@ -742,7 +767,7 @@ __device__ __forceinline__ void rotate_qk_chunk(const uint4 (&qk4)[2], int c, in
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float xp = __shfl_xor(x[e], LPR / 2);
-                const float2 r = t[8 * (c % (LPR / 2)) + e];
+                const float2 r = tab[e];
                 x[e] = lo ? x[e] * r.x - xp * r.y : xp * r.y + x[e] * r.x;
             }
         }
@@ -768,8 +793,10 @@ __global__ __launch_bounds__(256) void rope_qk_prep(TDesc tQ, TDesc tK, bf16_t* 
     const uint4 qk4[2] = {
         *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tQ, (int)bh, H) + pos * tQ.sr + 8 * c),
         *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tK, (int)bh, H) + pos * tK.sr + 8 * c)};
+    RopeTab<D> tab;
+    load_rope_tab<D>(cs, pos, c, mode, tab);
     const size_t off = (size_t)row * D + 8 * c;
-    rotate_qk_chunk<D>(qk4, c, pos, cs, mode, Qr + off, Kr + off);
+    rotate_qk_chunk<D>(qk4, c, tab, mode, Qr + off, Kr + off);
 }
 
 // Pre-pass of the MFMA path, D/8 lanes per row: rotated Q and K (bf16), D_i = rowsum(dO*O)
@@ -791,11 +818,13 @@ __global__ __launch_bounds__(256) void attn_prep(
     const uint4 o4 = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tO, (int)bh, H) + pos * tO.sr + 8 * c);
     const uint4 g4 = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tG, (int)bh, H) + pos * tG.sr + 8 * c);
     uint4 qk4[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    RopeTab<D> tab;
     if (mode != GN_ROPE_NONE) {
         qk4[0] = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tQ, (int)bh, H) + pos * tQ.sr + 8 * c);
         qk4[1] = *reinterpret_cast<const uint4*>(head_base<const bf16_t>(tK, (int)bh, H) + pos * tK.sr + 8 * c);
+        load_rope_tab<D>(cs, pos, c, mode, tab);
     }
-    const float lse = c == 0 ? LSE[row] : 0.f;
+    const float lse = LSE[row];  // every lane of the row (one address)
     const uint32_t ow[4] = {o4.x, o4.y, o4.z, o4.w}, gw[4] = {g4.x, g4.y, g4.z, g4.w};
     float dot = 0.f;
 #pragma unroll
@@ -805,14 +834,15 @@ __global__ __launch_bounds__(256) void attn_prep(
     }
 #pragma unroll
     for (int m = LPR / 2; m >= 1; m >>= 1) dot += __shfl_xor(dot, m);
-    if (c == 0) {
-        Di[(size_t)bh * Spad + pos] = dot;
-        Lsc[(size_t)bh * Spad + pos] = lse * 1.4426950408889634f;
-        if (pos == S - 1)  // finite padding: masked entries compute exp2(-inf - 0) * (dP - 0)
-            for (int p = S; p < Spad; ++p) Di[(size_t)bh * Spad + p] = Lsc[(size_t)bh * Spad + p] = 0.f;
-    }
+    // every lane of the row holds the full dot (butterfly) and stores the row's two values
+    // (same address and value across the row's lanes): no branch, so the LSE load stays with
+    // the others instead of being sunk behind their wait
+    Di[(size_t)bh * Spad + pos] = dot;
+    Lsc[(size_t)bh * Spad + pos] = lse * 1.4426950408889634f;
+    if (c == 0 && pos == S - 1)  // finite padding: masked entries compute exp2(-inf - 0) * (dP - 0)
+        for (int p = S; p < Spad; ++p) Di[(size_t)bh * Spad + p] = Lsc[(size_t)bh * Spad + p] = 0.f;
     if (mode == GN_ROPE_NONE) return;
-    rotate_qk_chunk<D>(qk4, c, pos, cs, mode, Qr + off, Kr + off);
+    rotate_qk_chunk<D>(qk4, c, tab, mode, Qr + off, Kr + off);
 }
 
 // ---- SIMT path: one wave per query row (dQ, forward) or key row (dK, dV) ----------------
