@@ -340,17 +340,32 @@ __device__ __forceinline__ void epilogue_part(const GemmDesc& g, const float* st
 
 // C (+)= the sum over y = 0 .. ksplit-1 of the partial tiles, added in index order (one
 // thread per 4 columns of a row), rows below Msplit to C, the rest to C2; then the bias.
+// The planes' loads go out together, up to eight per memory round trip (ksplit is uniform,
+// so the guards are uniform branches with no wait between the loads), and are then added in
+// index order.
 __global__ __launch_bounds__(256) void split_reduce(GemmDesc g) {
     const int n4 = g.N / 4;
     const int64_t total = (int64_t)g.M * n4;
     const size_t plane = (size_t)g.M * g.N;
+    const int ks = g.ksplit;
     for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
         const int m = (int)(i / n4), n = (int)(i % n4) * 4;
         const float* src = g.part + (size_t)m * g.N + n;
-        float4 v = *reinterpret_cast<const float4*>(src);
-        for (int y = 1; y < g.ksplit; ++y) {
-            const float4 w = *reinterpret_cast<const float4*>(src + y * plane);
-            v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int y0 = 0; y0 < ks; y0 += 8) {
+            float4 w[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (y0 + j < ks) w[j] = *reinterpret_cast<const float4*>(src + (size_t)(y0 + j) * plane);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (y0 + j >= ks) break;
+                if (y0 + j == 0) {
+                    v = w[0];
+                } else {
+                    v.x += w[j].x; v.y += w[j].y; v.z += w[j].z; v.w += w[j].w;
+                }
+            }
         }
         float4* c4 = reinterpret_cast<float4*>(reinterpret_cast<float*>(m < g.Msplit ? g.C : g.C2) +
                                                (size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n);
@@ -363,8 +378,18 @@ __global__ __launch_bounds__(256) void split_reduce(GemmDesc g) {
     if (g.bias) {
         const float* bp = g.part + (size_t)g.ksplit * plane;
         for (int64_t m = blockIdx.x * (int64_t)256 + threadIdx.x; m < g.M; m += (int64_t)gridDim.x * 256) {
-            float v = bp[m];
-            for (int y = 1; y < g.ksplit; ++y) v += bp[(size_t)y * g.M + m];
+            float v = 0.f;
+            for (int y0 = 0; y0 < ks; y0 += 8) {
+                float w[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (y0 + j < ks) w[j] = bp[(size_t)(y0 + j) * g.M + m];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (y0 + j >= ks) break;
+                    v = y0 + j == 0 ? w[0] : v + w[j];
+                }
+            }
             float* dst = m < g.Msplit ? g.bias + m : g.bias2 + (m - g.Msplit);
             *dst = g.accumulate ? *dst + v : v;
         }
