@@ -288,6 +288,69 @@ int launch_small(const GemmDesc& g, int ta, int tb, hipStream_t s) {
     return GN_OK;
 }
 
+// ---- small fp32 Linear backward in one launch -------------------------------------------
+// dX = dY W, dW = dY^T X and db = column sums of dY for an fp32 Linear whose two products
+// gemm_small takes (an MLP layer over a batch of <= 128 rows): block ranges pick the output.
+// A dX or dW element runs gemm_small's sequential k loop, and a db column follows
+// colsum_small's order (16 interleaved row subsets summed from zero, then added in subset
+// order), so the results are bit-identical to the three launches this replaces.
+struct SmallLinearBwd {
+    const float* dY;  // [M x N]
+    const float* X;   // [M x K]
+    const float* W;   // [N x K]
+    float *dX, *dW, *db;
+    int M, N, K, accumulate;
+    int bx, bw;  // blocks of the dX range, of the dW range (db follows)
+};
+
+__global__ __launch_bounds__(256) void linear_bwd_small(SmallLinearBwd p) {
+    const int b = blockIdx.x;
+    if (b < p.bx) {  // dX[m][k] = sum_n dY[m][n] W[n][k]
+        const int64_t idx = (int64_t)b * 256 + threadIdx.x;
+        if (idx >= (int64_t)p.M * p.K) return;
+        const int m = (int)(idx / p.K), k = (int)(idx % p.K);
+        float a = 0.f;
+#pragma unroll 16
+        for (int n = 0; n < p.N; ++n) a = fmaf(p.dY[(size_t)m * p.N + n], p.W[(size_t)n * p.K + k], a);
+        p.dX[idx] = p.accumulate ? a + p.dX[idx] : a;
+        return;
+    }
+    if (b < p.bx + p.bw) {  // dW[n][k] = sum_m dY[m][n] X[m][k]
+        const int64_t idx = (int64_t)(b - p.bx) * 256 + threadIdx.x;
+        if (idx >= (int64_t)p.N * p.K) return;
+        const int n = (int)(idx / p.K), k = (int)(idx % p.K);
+        float a = 0.f;
+#pragma unroll 16
+        for (int m = 0; m < p.M; ++m) a = fmaf(p.dY[(size_t)m * p.N + n], p.X[(size_t)m * p.K + k], a);
+        p.dW[idx] = p.accumulate ? a + p.dW[idx] : a;
+        return;
+    }
+    // db[n] = sum_m dY[m][n]: 16 columns per block, thread (j, c) sums rows j, j + 16, ...
+    // of column c (its <= 8 loads issued together), then thread j = 0 adds the 16 subsets in
+    // order
+    __shared__ float sh[16][17];
+    const int c = threadIdx.x & 15, j = threadIdx.x >> 4;
+    const int n = (b - p.bx - p.bw) * 16 + c;
+    float v[kSmallMaxK / 16];
+#pragma unroll
+    for (int i = 0; i < kSmallMaxK / 16; ++i) {
+        const int r = j + 16 * i;
+        v[i] = (n < p.N && r < p.M) ? p.dY[(size_t)r * p.N + n] : 0.f;
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSmallMaxK / 16; ++i)
+        if (j + 16 * i < p.M) s += v[i];
+    sh[j][c] = s;
+    __syncthreads();
+    if (j == 0 && n < p.N) {
+        float t = sh[0][c];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) t += sh[w][c];
+        p.db[n] = p.accumulate ? p.db[n] + t : t;
+    }
+}
+
 // ---- column sums over few rows: one pass, deterministic ---------------------------------
 // Block: 16 waves x 64 columns (lane = column); wave w adds rows w, w + 16, ... (all of its
 // loads issued together), the waves' sums are added in a fixed order.  No clear, no second
@@ -670,6 +733,27 @@ int colsum_dispatch(const void* in, float* out, int M, int N, int dtype, unsigne
     return GN_OK;
 }
 
+// An fp32 Linear backward whose products gemm_small takes (batch <= kSmallMaxK rows, dX's
+// k loop over the N outputs <= kSmallMaxK, each product <= kSmallMaxMac multiply-adds) runs
+// as one launch of linear_bwd_small: same results as the dX GEMM, the db column sums and
+// the dW GEMM launched one after another, a third of the launches.
+bool small_linear_applicable(int M, int N, int K, bool with_dx) {
+    if (M < 1 || N < 1 || K < 1 || M > kSmallMaxK) return false;
+    if ((int64_t)N * K * M > kSmallMaxMac) return false;
+    return !with_dx || (N <= kSmallMaxK && (int64_t)M * K * N <= kSmallMaxMac);
+}
+
+int small_linear_launch(const float* dY, const float* X, const float* W, float* dX, float* dW,
+                        float* db, int M, int N, int K, bool acc, hipStream_t s) {
+    SmallLinearBwd p{dY, X, W, dX, dW, db, M, N, K, acc ? 1 : 0, 0, 0};
+    p.bx = dX ? (int)(((int64_t)M * K + 255) / 256) : 0;
+    p.bw = (int)(((int64_t)N * K + 255) / 256);
+    const int bb = db ? (N + 15) / 16 : 0;
+    linear_bwd_small<<<p.bx + p.bw + bb, 256, 0, s>>>(p);
+    GN_LAUNCH_CHECK("linear backward (small, one launch)");
+    return GN_OK;
+}
+
 }  // namespace gn
 
 using namespace gn;
@@ -714,6 +798,9 @@ extern "C" int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, vo
         return skinny_linear_bwd((const float*)dY, (const float*)X, (const float*)W, (float*)dX,
                                  (float*)dW, (float*)db, M, N, K, flags & GN_ACCUMULATE, ws,
                                  ws_bytes, s);
+    if (dtype == GN_F32 && small_linear_applicable(M, N, K, dX != nullptr))
+        return small_linear_launch((const float*)dY, (const float*)X, (const float*)W, (float*)dX,
+                                   (float*)dW, (float*)db, M, N, K, flags & GN_ACCUMULATE, s);
     int rc;
     if (dX) {  // dX[M x K] = dY[M x N] . W[N x K]
         rc = gemm_dispatch(dY, W, N, nullptr, nullptr, 0, dX, M, K, 0, 0, dtype, dtype, flags, s,

@@ -158,6 +158,42 @@ def test_gemm_fp32_small_path_edges(gn, ta, tb, shape):
     assert np.all(np.abs(host(Cacc) - (ref + C0)) <= bound * (mag + np.abs(C0)) + 1e-30)
 
 
+@pytest.mark.parametrize("shape", [(64, 10, 256), (64, 256, 784), (128, 128, 100), (7, 33, 9),
+                                   (128, 129, 3), (129, 10, 20)])
+@pytest.mark.parametrize("with_dx", [True, False])
+def test_linear_fp32_one_launch_matches_separate(gn, shape, with_dx):
+    """An fp32 Linear backward small enough for one launch (batch <= 128, dX's k loop over
+    the N outputs <= 128) against the launches it replaces (dX and dW as plain GEMMs, db as
+    column sums): bit-identical, overwrite and accumulate.  (128, 129, 3) with dX and
+    (129, 10, 20) are past the bounds and run the separate launches inside the entry too.
+    Rows above 8 or K % 4 != 0, so the skinny path (batch <= 8) is not the one taken."""
+    M, N, K = shape
+    r = rng_(36)
+    dY = dev(r.standard_normal((M, N)).astype(np.float32))
+    X = dev(r.standard_normal((M, K)).astype(np.float32))
+    W = dev(r.standard_normal((N, K)).astype(np.float32))
+    dX, dW, db = gn.linear_bwd(dY, X, W, need_dx=with_dx, ws=False)
+    assert torch.equal(dW, gn.gemm(dY, X, transA=True))
+    assert torch.equal(db, gn.colsum(dY))
+    if with_dx:
+        assert torch.equal(dX, gn.gemm(dY, W))
+    base = [dev(r.standard_normal(s).astype(np.float32)) for s in ((M, K), (N, K), (N,))]
+    aX, aW, ab = [b.clone() for b in base]
+    gn.linear_bwd(dY, X, W, need_dx=with_dx, dX=aX if with_dx else None, dW=aW, db=ab,
+                  accumulate=True, ws=False)
+    eX, eW, eb = [b.clone() for b in base]
+    gn.gemm(dY, X, transA=True, C=eW, accumulate=True)
+    gn.colsum(dY, out=eb, accumulate=True)
+    assert torch.equal(aW, eW) and torch.equal(ab, eb)
+    if with_dx:
+        gn.gemm(dY, W, C=eX, accumulate=True)
+        assert torch.equal(aX, eX)
+    # and against fp64
+    y, x, w = (host(t).astype(np.float64) for t in (dY, X, W))
+    mag = np.abs(y).T @ np.abs(x)
+    assert np.all(np.abs(host(dW) - y.T @ x) <= 2.0 ** -20 * mag + 1e-30)
+
+
 @pytest.mark.parametrize("M", [1, 7, 64, 1024, 1025])
 @pytest.mark.parametrize("N", [10, 300])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
