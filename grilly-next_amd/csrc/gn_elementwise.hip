@@ -173,11 +173,13 @@ __global__ __launch_bounds__(256) void embedding_bwd_kernel(const T* __restrict_
 
 // ---- VSA surrogate loss backward (vsa-surrogate-loss-backward.glsl:50-88) ---------------
 // grid (ceil(D / (256*4)), Bn); each thread owns 4 consecutive dims i (one u32 word).
+// VEC4: 16-byte accesses (D % 4 == 0, aligned rows); ACC: add onto dP.
+template <bool VEC4, bool ACC>
 __global__ __launch_bounds__(256) void surrogate_bwd_kernel(
     const float* __restrict__ preds, const uint32_t* __restrict__ bits,
     const uint32_t* __restrict__ results, const float* __restrict__ weights,
     float* __restrict__ dP, int K, int D, int words, float gamma, float delta, float lambda_c,
-    float scale, int accumulate, int vec4) {
+    float scale) {
     const int b = blockIdx.y;
     const int i0 = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (i0 >= D) return;
@@ -193,38 +195,50 @@ __global__ __launch_bounds__(256) void surrogate_bwd_kernel(
         uint32_t w = (i < D) ? bits[(size_t)b * words + (i >> 5)] : 0u;
         y[j] = ((w >> (i & 31)) & 1u) ? 1.0f : -1.0f;
     }
-    for (int k = 0; k < K; ++k) {
-        const size_t base = ((size_t)b * K + k) * D + i0;
-        const float wk = weights[(size_t)b * K + k] * scale;
-        const float cterm = (contrast && (uint32_t)k == run) ? lambda_c * scale * invD : 0.0f;
-        float z[4], g[4];
-        if (vec4) {
-            float4 t = *reinterpret_cast<const float4*>(preds + base);
-            z[0] = t.x; z[1] = t.y; z[2] = t.z; z[3] = t.w;
-            if (accumulate) {
-                float4 a = *reinterpret_cast<const float4*>(dP + base);
-                g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
+    // branches in groups of four: every load of a group goes out before its math, so a thread
+    // waits on one memory round trip per four branches instead of one per branch
+    for (int k0 = 0; k0 < K; k0 += 4) {
+        float z[4][4], g[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (k0 + u >= K) break;
+            const size_t base = ((size_t)b * K + k0 + u) * D + i0;
+            if constexpr (VEC4) {
+                const float4 t = *reinterpret_cast<const float4*>(preds + base);
+                z[u][0] = t.x; z[u][1] = t.y; z[u][2] = t.z; z[u][3] = t.w;
+                if constexpr (ACC) {
+                    const float4 a = *reinterpret_cast<const float4*>(dP + base);
+                    g[u][0] = a.x; g[u][1] = a.y; g[u][2] = a.z; g[u][3] = a.w;
+                } else {
+                    g[u][0] = g[u][1] = g[u][2] = g[u][3] = 0.0f;
+                }
             } else {
-                g[0] = g[1] = g[2] = g[3] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    z[u][j] = (i0 + j < D) ? preds[base + j] : 0.0f;
+                    g[u][j] = (ACC && i0 + j < D) ? dP[base + j] : 0.0f;
+                }
             }
-        } else {
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int k = k0 + u;
+            if (k >= K) break;
+            const size_t base = ((size_t)b * K + k) * D + i0;
+            const float wk = weights[(size_t)b * K + k] * scale;
+            const float cterm = (contrast && (uint32_t)k == run) ? lambda_c * scale * invD : 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                z[j] = (i0 + j < D) ? preds[base + j] : 0.0f;
-                g[j] = (accumulate && i0 + j < D) ? dP[base + j] : 0.0f;
+                if (gamma - y[j] * z[u][j] > 0.0f) g[u][j] += (-y[j] * invD) * wk;
+                g[u][j] += y[j] * cterm;
             }
-        }
+            if constexpr (VEC4) {
+                *reinterpret_cast<float4*>(dP + base) = make_float4(g[u][0], g[u][1], g[u][2], g[u][3]);
+            } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (gamma - y[j] * z[j] > 0.0f) g[j] += (-y[j] * invD) * wk;
-            g[j] += y[j] * cterm;
-        }
-        if (vec4) {
-            *reinterpret_cast<float4*>(dP + base) = make_float4(g[0], g[1], g[2], g[3]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (i0 + j < D) dP[base + j] = g[j];
+                for (int j = 0; j < 4; ++j)
+                    if (i0 + j < D) dP[base + j] = g[u][j];
+            }
         }
     }
 }
@@ -491,9 +505,18 @@ extern "C" int gn_vsa_surrogate_bwd(const float* preds, const uint32_t* bits,
     GN_REQUIRE(Bn <= 65535, "gn_vsa_surrogate_bwd: Bn %d exceeds grid.y limit 65535", Bn);
     const int vec4 = (D % 4 == 0) && aligned16(preds) && aligned16(dPreds);
     dim3 grid((D + 1023) / 1024, Bn);
-    surrogate_bwd_kernel<<<grid, 256, 0, as_stream(stream)>>>(
-        preds, bits, results, weights, dPreds, K, D, words, gamma, delta, lambda_c, scale,
-        (flags & GN_ACCUMULATE) ? 1 : 0, vec4);
+    const bool acc = flags & GN_ACCUMULATE;
+#define GN_SUR_LAUNCH(V, A)                                                                    \
+    surrogate_bwd_kernel<V, A><<<grid, 256, 0, as_stream(stream)>>>(                           \
+        preds, bits, results, weights, dPreds, K, D, words, gamma, delta, lambda_c, scale)
+    if (vec4) {
+        if (acc) GN_SUR_LAUNCH(true, true);
+        else GN_SUR_LAUNCH(true, false);
+    } else {
+        if (acc) GN_SUR_LAUNCH(false, true);
+        else GN_SUR_LAUNCH(false, false);
+    }
+#undef GN_SUR_LAUNCH
     GN_LAUNCH_CHECK("gn_vsa_surrogate_bwd");
     return GN_OK;
 }
