@@ -160,26 +160,61 @@ __device__ __forceinline__ float gumbel(uint64_t seed, uint64_t idx) {
     return -logf(-logf(u));
 }
 
-__global__ __launch_bounds__(256) void surrogate_fwd_rows(
+// one block per row, 16 waves: a row's K x D predictions are read once, up to 16 branches'
+// loads in flight per thread, so a single row (batch 1) is not held to one wave's round trips
+constexpr int kSurThreads = 1024, kSurWaves = kSurThreads / 64;
+
+__global__ __launch_bounds__(kSurThreads) void surrogate_fwd_rows(
     const float* __restrict__ preds, const uint32_t* __restrict__ bits, float* __restrict__ dots,
     uint32_t* __restrict__ results, float* __restrict__ weights, float* __restrict__ loss,
     int Bn, int K, int D, int words, float gamma, float delta, float lambda_c, float temperature,
     uint64_t seed, uint64_t counter, int noise) {
-    __shared__ float sh[4];
-    __shared__ float sd[kSurrogateMaxK];
+    __shared__ float sh[kSurWaves];
+    __shared__ float sd[kSurrogateMaxK], sadj[kSurrogateMaxK];
     __shared__ int swin;
     __shared__ float sdw, sdr;
     const int b = blockIdx.x, t = threadIdx.x;
     const uint32_t* yb = bits + (size_t)b * words;
     const int nc = D >> 2;  // D % 32 == 0
-    for (int k = 0; k < K; ++k) {
-        const float* p = preds + ((size_t)b * K + k) * D;
-        float s = 0.f;
-        for (int c = t; c < nc; c += 256)
-            s += signed_sum4(ld_nt4(p + 4 * c), yb[c >> 3] >> (4 * (c & 7)));
-        s = block_sum<4>(s, sh);
-        if (t == 0) sd[k] = s;
+    // the branches' dot products in groups of KG: a thread's loads for all branches of a group
+    // go out together (one memory round trip per chunk of D, not one per branch), each branch
+    // then reduced as block_sum does (wave sum, the wave sums added in order from zero)
+    constexpr int KG = 16;
+    __shared__ float shk[KG][kSurWaves];
+    const int wv = t >> 6, ln = t & 63;
+    for (int k0 = 0; k0 < K; k0 += KG) {
+        float s[KG];
+#pragma unroll
+        for (int j = 0; j < KG; ++j) s[j] = 0.f;
+        for (int c = t; c < nc; c += kSurThreads) {
+            const uint32_t nib = yb[c >> 3] >> (4 * (c & 7));
+            float4 w[KG];
+#pragma unroll
+            for (int j = 0; j < KG; ++j)
+                if (k0 + j < K) w[j] = ld_nt4(preds + ((size_t)b * K + k0 + j) * D + 4 * c);
+#pragma unroll
+            for (int j = 0; j < KG; ++j)
+                if (k0 + j < K) s[j] += signed_sum4(w[j], nib);
+        }
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            if (k0 + j >= K) break;
+            const float v = wave_sum(s[j]);
+            if (ln == 0) shk[j][wv] = v;
+        }
+        __syncthreads();
+        if (t < KG && k0 + t < K) {
+            float tt = 0.f;
+#pragma unroll
+            for (int i = 0; i < kSurWaves; ++i) tt += shk[t][i];
+            sd[k0 + t] = tt;
+        }
+        __syncthreads();
     }
+    // the perturbed scores, one branch per thread
+    if (t < K)
+        sadj[t] = sd[t] + (noise ? gumbel(seed, ((uint64_t)counter * Bn + b) * K + t) : 0.f) *
+                              temperature;
     __syncthreads();
     if (t == 0) {
         // top-2 over the perturbed scores, as the reference's host loop (vsa_loss_node.cpp:
@@ -187,8 +222,7 @@ __global__ __launch_bounds__(256) void surrogate_fwd_rows(
         float max1 = -1e30f, max2 = -1e30f;
         int k1 = 0, k2 = 0;
         for (int k = 0; k < K; ++k) {
-            const float g = noise ? gumbel(seed, ((uint64_t)counter * Bn + b) * K + k) : 0.f;
-            const float adj = sd[k] + g * temperature;
+            const float adj = sadj[k];
             if (adj > max1) {
                 max2 = max1; k2 = k1;
                 max1 = adj; k1 = k;
@@ -215,14 +249,14 @@ __global__ __launch_bounds__(256) void surrogate_fwd_rows(
     __syncthreads();
     const float* pw = preds + ((size_t)b * K + swin) * D;
     float h = 0.f;
-    for (int c = t; c < nc; c += 256) {
+    for (int c = t; c < nc; c += kSurThreads) {
         const float4 z = *reinterpret_cast<const float4*>(pw + 4 * c);
         const uint32_t nib = yb[c >> 3] >> (4 * (c & 7));
         // y z = +-z: the hinge term gamma - y z, one per element
         h += fmaxf(gamma - sgn(z.x, nib), 0.f) + fmaxf(gamma - sgn(z.y, nib >> 1), 0.f) +
              fmaxf(gamma - sgn(z.z, nib >> 2), 0.f) + fmaxf(gamma - sgn(z.w, nib >> 3), 0.f);
     }
-    h = block_sum<4>(h, sh);
+    h = block_sum<kSurWaves>(h, sh);
     if (t == 0) loss[b] = h / (float)D + lambda_c * fmaxf(0.f, delta - (sdw - sdr));
 }
 
@@ -324,7 +358,7 @@ extern "C" int gn_vsa_surrogate_fwd(const float* preds, const uint32_t* bits, fl
     GN_REQUIRE(al16(preds), "gn_vsa_surrogate_fwd: preds must be 16-byte aligned");
     GN_REQUIRE(temperature > 0.f, "gn_vsa_surrogate_fwd: temperature must be > 0");
     hipStream_t s = as_stream(stream);
-    surrogate_fwd_rows<<<Bn, 256, 0, s>>>(preds, bits, dots, results, weights, loss, Bn, K, D, words,
+    surrogate_fwd_rows<<<Bn, kSurThreads, 0, s>>>(preds, bits, dots, results, weights, loss, Bn, K, D, words,
                                           gamma, delta, lambda_c, temperature, seed, counter,
                                           (flags & GN_NO_GUMBEL) ? 0 : 1);
     GN_LAUNCH_CHECK("gn_vsa_surrogate_fwd");

@@ -78,7 +78,8 @@ def test_vsa_unpack_project_fwd_integer_identity(env):
         np.testing.assert_array_equal(Y.cpu().numpy(), (S @ Wi.T).astype(np.float32))
 
 
-@pytest.mark.parametrize("Bn,K,D", [(1, 16, 10240), (5, 4, 1024), (64, 3, 256)])
+@pytest.mark.parametrize("Bn,K,D", [(1, 16, 10240), (5, 4, 1024), (64, 3, 256), (3, 33, 512),
+                                    (2, 64, 1024)])
 @pytest.mark.parametrize("noise", [True, False])
 def test_vsa_surrogate_fwd(env, Bn, K, D, noise):
     gc, gb, gn, dev = env
