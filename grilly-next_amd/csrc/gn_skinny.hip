@@ -85,9 +85,11 @@ __global__ __launch_bounds__(256) void linear_fwd_skinny(const float* __restrict
 }
 
 // ---- backward: block = 64 * WV threads owning float4 chunks c = t + 64 WV q (q < Q) -----
-// Rows [r0, r1) of W; four rows per step, their W chunks loaded before use.
-template <int MT, int Q>
-__global__ __launch_bounds__(256) void linear_bwd_skinny(
+// Rows [r0, r1) of W, R rows per step, their W chunks loaded before use; with PIPE the next
+// step's rows are requested before this step's dW stores, so a wave keeps a step of loads in
+// flight behind its stores (one row: R = 8, up to 16 waves, one chunk per thread).
+template <int MT, int Q, int R, bool PIPE>
+__global__ __launch_bounds__(MT == 1 ? 1024 : 256) void linear_bwd_skinny(
     const float* __restrict__ dY, const float* __restrict__ X, const float* __restrict__ W,
     float* __restrict__ dW, float* __restrict__ db, float* __restrict__ part,
     float* __restrict__ dX_atomic, int M, int N, int K, int rows_per_block, int acc_dw,
@@ -105,11 +107,11 @@ __global__ __launch_bounds__(256) void linear_bwd_skinny(
                                          : make_float4(0.f, 0.f, 0.f, 0.f);
             ax[m][q] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    for (int n0 = r0; n0 < r1; n0 += 4) {
-        float4 w[4][Q];
-        float g[4][MT];
+    float4 w[R][Q];
+    float g[R][MT];
+    auto load_rows = [&](int n0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < R; ++i) {
             const int n = n0 + i;
 #pragma unroll
             for (int m = 0; m < MT; ++m) g[i][m] = (n < r1 && m < M) ? dY[(size_t)m * N + n] : 0.f;
@@ -120,8 +122,22 @@ __global__ __launch_bounds__(256) void linear_bwd_skinny(
                                                         : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
+    };
+    if (PIPE) load_rows(r0);
+    for (int n0 = r0; n0 < r1; n0 += R) {
+        float4 wc[R][Q];
+        float gc[R][MT];
+        if (!PIPE) load_rows(n0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < R; ++i) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) gc[i][m] = g[i][m];
+#pragma unroll
+            for (int q = 0; q < Q; ++q) wc[i][q] = w[i][q];
+        }
+        if (PIPE && n0 + R < r1) load_rows(n0 + R);
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
             const int n = n0 + i;
             if (n >= r1) break;
 #pragma unroll
@@ -131,14 +147,14 @@ __global__ __launch_bounds__(256) void linear_bwd_skinny(
                 float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
-                    o.x += g[i][m] * xr[m][q].x;
-                    o.y += g[i][m] * xr[m][q].y;
-                    o.z += g[i][m] * xr[m][q].z;
-                    o.w += g[i][m] * xr[m][q].w;
-                    ax[m][q].x += g[i][m] * w[i][q].x;
-                    ax[m][q].y += g[i][m] * w[i][q].y;
-                    ax[m][q].z += g[i][m] * w[i][q].z;
-                    ax[m][q].w += g[i][m] * w[i][q].w;
+                    o.x += gc[i][m] * xr[m][q].x;
+                    o.y += gc[i][m] * xr[m][q].y;
+                    o.z += gc[i][m] * xr[m][q].z;
+                    o.w += gc[i][m] * xr[m][q].w;
+                    ax[m][q].x += gc[i][m] * wc[i][q].x;
+                    ax[m][q].y += gc[i][m] * wc[i][q].y;
+                    ax[m][q].z += gc[i][m] * wc[i][q].z;
+                    ax[m][q].w += gc[i][m] * wc[i][q].w;
                 }
                 float* dst = dW + (size_t)n * K + 4 * c;
                 if (acc_dw) {
@@ -216,10 +232,12 @@ struct BwdShape {
     int threads, Q, blocks, rows_per_block;
 };
 
-BwdShape bwd_shape(int N, int K) {
+// One row (M = 1): one float4 chunk per thread, up to 16 waves (K <= 4096).  More rows: up
+// to 4 waves, Q chunks per thread (their X chunks and dX partials stay in registers).
+BwdShape bwd_shape(int M, int N, int K) {
     BwdShape s{};
     const int nc = K / 4;
-    s.Q = std::max(1, (nc + 255) / 256);
+    s.Q = M <= 1 ? 1 : std::max(1, (nc + 255) / 256);
     const int waves = std::max(1, (nc + 64 * s.Q - 1) / (64 * s.Q));
     s.threads = 64 * waves;
     s.blocks = std::max(1, std::min(kSkinnyBlocks, (N + 15) / 16));
@@ -240,19 +258,24 @@ template <int MT, int Q>
 void launch_bwd_mq(const BwdShape& sh, const float* dY, const float* X, const float* W, float* dW,
                    float* db, float* part, float* dXa, int M, int N, int K, int acc, int want_dx,
                    hipStream_t s) {
-    linear_bwd_skinny<MT, Q><<<sh.blocks, sh.threads, 0, s>>>(dY, X, W, dW, db, part, dXa, M, N, K,
-                                                              sh.rows_per_block, acc, acc, want_dx);
+    constexpr int R = MT == 1 ? 8 : 4;
+    linear_bwd_skinny<MT, Q, R, MT == 1><<<sh.blocks, sh.threads, 0, s>>>(
+        dY, X, W, dW, db, part, dXa, M, N, K, sh.rows_per_block, acc, acc, want_dx);
 }
 
 template <int MT>
 void launch_bwd_m(const BwdShape& sh, const float* dY, const float* X, const float* W, float* dW,
                   float* db, float* part, float* dXa, int M, int N, int K, int acc, int want_dx,
                   hipStream_t s) {
-    switch (sh.Q) {
-        case 1: launch_bwd_mq<MT, 1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
-        case 2: launch_bwd_mq<MT, 2>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
-        case 3: launch_bwd_mq<MT, 3>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
-        default: launch_bwd_mq<MT, 4>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
+    if constexpr (MT == 1) {
+        launch_bwd_mq<1, 1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s);
+    } else {
+        switch (sh.Q) {
+            case 1: launch_bwd_mq<MT, 1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
+            case 2: launch_bwd_mq<MT, 2>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
+            case 3: launch_bwd_mq<MT, 3>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
+            default: launch_bwd_mq<MT, 4>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
+        }
     }
 }
 
@@ -277,7 +300,7 @@ bool skinny_bwd_applicable(const void* dY, const void* X, const void* W, const v
 // Workspace for the deterministic dX reduction: one [M x K] fp32 plane per row-range block.
 size_t skinny_bwd_ws_bytes(int M, int N, int K) {
     if (M < 1 || M > kSkinnyMaxM || N <= 0 || K <= 0 || K % 4) return 0;
-    return (size_t)bwd_shape(N, K).blocks * M * K * sizeof(float);
+    return (size_t)bwd_shape(M, N, K).blocks * M * K * sizeof(float);
 }
 
 int skinny_linear_fwd(const float* X, const float* W, const float* b, float* Y, int M, int N,
@@ -294,7 +317,7 @@ int skinny_linear_fwd(const float* X, const float* W, const float* b, float* Y, 
 int skinny_linear_bwd(const float* dY, const float* X, const float* W, float* dX, float* dW,
                       float* db, int M, int N, int K, bool accumulate, void* ws, size_t ws_bytes,
                       hipStream_t s) {
-    const BwdShape sh = bwd_shape(N, K);
+    const BwdShape sh = bwd_shape(M, N, K);
     const size_t need = (size_t)sh.blocks * M * K * sizeof(float);
     float* part = (dX && ws && ws_bytes >= need && al16(ws)) ? (float*)ws : nullptr;
     float* dXa = nullptr;

@@ -104,7 +104,7 @@ def test_vsa_surrogate_fwd(env, Bn, K, D, noise):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1536, 768), (2, 777, 1536), (5, 300, 64), (8, 640, 1024),
-                                   (1, 10, 256), (4, 4096, 2048)])
+                                   (1, 10, 256), (4, 4096, 2048), (1, 999, 4096), (1, 5003, 1540)])
 def test_linear_fp32_skinny(env, M, N, K):
     gc, gb, gn, dev = env
     rng = np.random.RandomState(M * 31 + N)
