@@ -70,15 +70,23 @@ def parse():
                    help="summarise a rocprofv3 --pmc run of SQ_INSTS_VALU SQ_INSTS_MFMA "
                         "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE per kernel (VALU instructions "
                         "per MFMA, MFMA busy share of the SIMD cycles)")
-    p.add_argument("--pmc-kernel", default=DOMINANT_KERNEL_RE,
-                   help="regex of the kernel name --pmc-summary reports (default: the FFN "
-                        "headline's dominant kernel, the [dWg;dWu] weight-gradient GEMM)")
+    p.add_argument("--pmc-call", default=DOMINANT_CALL, choices=sorted(CALL_KERNELS),
+                   help="the FFN step's call whose launches --pmc-summary adds up (default: the "
+                        "headline's dominant call, the [dWg;dWu] weight-gradient GEMM)")
     return p.parse_args()
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_dominant_gemm_hbm_traffic.txt")
-# the [dWg;dWu] GEMM: transposed A (gu^T), fp32 C, 256 x 128 tiles, three LDS stages
-DOMINANT_KERNEL_RE = r"gemm_core<true, false, float, 256, 128, 0, 3[,>]"
+# The launches of the FFN step's two largest calls as rocprof names them: (kernel pattern,
+# work-items per dispatch).  [dWg;dWu] (transposed A, fp32 C) runs its first 8192 rows as one
+# round of 256 x 256 tiles (two LDS stages) and the last 3072 rows on 256 x 128 tiles (three
+# stages); the grid size tells its 256 x 256 launch from dWd's (176 tiles).
+CALL_KERNELS = {
+    "[dWg;dWu]": [(r"gemm_core<true, false, float, 256, 256, 0, 2[,>]", 256 * 256),
+                  (r"gemm_core<true, false, float, 256, 128, 0, 3[,>]", 192 * 256)],
+    "dN": [(r"gemm_core<false, false, unsigned short, 256, 128, 0, 3[,>]", 256 * 256)],
+}
+DOMINANT_CALL = "[dWg;dWu]"
 CALIB_FLOATS = 1 << 28
 
 
@@ -90,9 +98,9 @@ def calib_copy(torch, gn):
     torch.cuda.synchronize()
 
 
-def pmc_summary(fetch_dir, write_dir, kernel_re):
-    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the dominant kernel (kernel_re) and of the
-    calibration add (known bytes) -> scaled HBM bytes per launch of the dominant kernel."""
+def pmc_summary(fetch_dir, write_dir, call):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of each launch of `call` (CALL_KERNELS) and of
+    the calibration add (known bytes) -> scaled HBM bytes per call, summed over its launches."""
     import csv
     import glob
     import re
@@ -108,29 +116,29 @@ def pmc_summary(fetch_dir, write_dir, kernel_re):
                 out[key][r["Dispatch_Id"]] += float(r["Counter_Value"])
         return out
 
-    res = {}
-    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
-        tab = load(d, counter)
-        calib = [v for (k, g), v in tab.items() if "add_kernel" in k]
-        gemm = {(k, g): v for (k, g), v in tab.items() if re.search(kernel_re, k)}
-        if not calib or not gemm:
-            raise SystemExit(f"{counter}: calibration or GEMM dispatches not found in {d}")
-        cvals = [x for v in calib for x in v.values()]
-        (gk, gg), gv = max(gemm.items(), key=lambda kv: len(kv[1]))
-        gvals = list(gv.values())
-        res[counter] = (sum(cvals) / len(cvals), sum(gvals) / len(gvals), len(gvals), gk, gg)
     known = {"FETCH_SIZE": 2.0 * CALIB_FLOATS * 4, "WRITE_SIZE": 1.0 * CALIB_FLOATS * 4}
     total = 0.0
-    lines = []
-    for counter, (ckib, gkib, n, gk, gg) in res.items():
+    lines = [f"call: {call}"]
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        tab = load(d, counter)
+        calib = [x for (k, g), v in tab.items() if "add_kernel" in k for x in v.values()]
+        if not calib:
+            raise SystemExit(f"{counter}: no calibration dispatch in {d}")
+        ckib = sum(calib) / len(calib)
         factor = known[counter] / (ckib * 1024.0)
-        b = gkib * 1024.0 * factor
-        total += b
         lines.append(f"{counter}: calibration add {ckib:.0f} KiB/dispatch (expected "
-                     f"{known[counter] / 1024:.0f} KiB) -> factor {factor:.4f}; dominant kernel "
-                     f"{gkib:.0f} KiB/dispatch over {n} dispatches -> {b / 1e6:.1f} MB")
-    lines.append(f"kernel: {res['FETCH_SIZE'][3][:120]} grid {res['FETCH_SIZE'][4]}")
-    lines.append(f"traffic_bytes_per_launch: {total:.0f}")
+                     f"{known[counter] / 1024:.0f} KiB) -> factor {factor:.4f}")
+        for pat, grid in CALL_KERNELS[call]:
+            vals = [x for (k, g), v in tab.items() if re.search(pat, k) and int(float(g)) == grid
+                    for x in v.values()]
+            if not vals:
+                raise SystemExit(f"{counter}: no dispatch of {pat} with grid {grid} in {d}")
+            kib = sum(vals) / len(vals)
+            b = kib * 1024.0 * factor
+            total += b
+            lines.append(f"  {pat.split('[')[0]}> grid {grid}: {kib:.0f} KiB/dispatch over "
+                         f"{len(vals)} dispatches -> {b / 1e6:.1f} MB")
+    lines.append(f"traffic_bytes_per_call: {total:.0f}")
     print("\n".join(lines))
 
 
@@ -196,14 +204,18 @@ def ceilings(torch, gn):
                      f"gn_probe_copy {nbytes >> 30} GiB per mode (copies: read + written)"}
 
 
-def traffic_from_profile():
-    """HBM bytes per launch of the dominant GEMM from the committed counter summary."""
+def traffic_from_profile(call):
+    """HBM bytes per call of `call` from the committed counter summary (None when the summary
+    covers another call or is missing)."""
     try:
-        for l in open(TRAFFIC_FILE):
-            if l.startswith("traffic_bytes_per_launch:"):
-                return int(float(l.split(":", 1)[1]))
+        lines = open(TRAFFIC_FILE).read().splitlines()
     except OSError:
-        pass
+        return None
+    if f"call: {call}" not in lines:
+        return None
+    for l in lines:
+        if l.startswith("traffic_bytes_per_call:"):
+            return int(float(l.split(":", 1)[1]))
     return None
 
 
@@ -706,9 +718,12 @@ class Step:
     CALLS = [
         ("down-projection GEMM with the SwiGLU backward in its epilogue: gu = glu'(dY Wd), "
          "4096x5632x2048", "gemm_core (epi 1)", "mfma", 2.0 * T * HID * DM),
-        ("dWd = dY^T A, 2048x5632x4096", "gemm_core (fp32 C)", "mfma", 2.0 * DM * HID * T),
-        ("dN = [dG|dU] [Wg;Wu], 4096x2048x11264", "gemm_core (bf16 C)", "mfma", 2.0 * T * DM * 2 * HID),
-        ("[dWg;dWu] = [dG|dU]^T N, 11264x2048x4096", "gemm_core (fp32 C)", "mfma", 2.0 * 2 * HID * DM * T),
+        ("dWd = dY^T A, 2048x5632x4096", "gemm_core 256x256 (fp32 C)", "mfma", 2.0 * DM * HID * T),
+        ("dN = [dG|dU] [Wg;Wu], 4096x2048x11264", "gemm_core 256x128 (bf16 C)", "mfma",
+         2.0 * T * DM * 2 * HID),
+        ("[dWg;dWu] = [dG|dU]^T N, 11264x2048x4096",
+         "gemm_core 256x256 on rows 0-8191, then 256x128 on rows 8192-11263 (fp32 C; two launches)",
+         "mfma", 2.0 * 2 * HID * DM * T),
         ("RMSNorm backward 4096x2048 (rows + parameter partials)", "norm_bwd_rows + colsum_partials",
          "hbm", 3.0 * T * DM * 2 + 4.0 * T),
     ]
@@ -816,7 +831,7 @@ def oracle_timing(tokens):
 def main():
     args = parse()
     if args.pmc_summary:
-        pmc_summary(*args.pmc_summary, args.pmc_kernel)
+        pmc_summary(*args.pmc_summary, args.pmc_call)
         return
     if args.pmc_sq:
         pmc_sq_summary(args.pmc_sq)
@@ -895,10 +910,11 @@ def main():
                                "T=4096 (4x1024), bf16 / fp32 accumulate",
                    "tokens": T, "d_model": DM, "hidden": HID, "parallelism": "none (1 GPU)"},
         "step_tflops": round(flops_step / (ms * 1e-3) / 1e12, 2),
-        "roofline": {"kernel": dom["call"], "bound": dom["bound"], "achieved": dom["achieved"],
+        "roofline": {"kernel": dom["call"], "launches": dom["kernels"], "bound": dom["bound"],
+                     "achieved": dom["achieved"],
                      "peak": BF16_PEAK_TFLOPS if dom["bound"] == "mfma" else HBM_PEAK_GBS,
                      "unit": dom["unit"], "frac": dom["frac"], "launch_ms": dom["ms"],
-                     "traffic": traffic_from_profile(),
+                     "traffic": traffic_from_profile(dom["call"].split(" = ")[0]),
                      "timing": "HIP events around the call inside every timed step, mean"},
         "kernels_timing": f"per-call HIP events over {nb} steps of a pass before the timed region",
         "kernels": kernels,

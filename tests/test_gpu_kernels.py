@@ -90,6 +90,44 @@ def test_gemm_two_segments_dma_path(gn):
         assert rel_err(host(C), ref) < 1e-5, (ta, tb)
 
 
+def test_gemm_row_split_whole_rounds(gn):
+    """A grid whose last round of tiles would be part-filled (11264 x 2048 x 4096 with a
+    k-outer A: the FFN's [dWg;dWu] shape) runs its first 8192 rows as one round of 256 x 256
+    tiles and the rest as a second launch: bit-identical to the same rows computed in blocks
+    small enough for one launch each, within the fp32 bar of the float64 product on rows
+    either side of 8192, and accumulate adds onto what is there.  The weight gradient of a
+    Linear of that shape splits its row sums (db) the same way."""
+    M, N, K = 11264, 2048, 4096
+    g = torch.Generator(device="cuda:0").manual_seed(46)
+    A = torch.randn(K, M, device="cuda:0", generator=g).bfloat16()
+    B = torch.randn(K, N, device="cuda:0", generator=g).bfloat16()
+    C = gn.gemm(A, B, transA=True, out_dtype=torch.float32)
+    # the blocks accumulate onto zeros, so none takes a split-K schedule (whose two halves
+    # would add in another order)
+    zeros = lambda *shape: torch.zeros(shape, device="cuda:0")
+    parts = [gn.gemm(A[:, r0:r0 + 1024].contiguous(), B, transA=True, C=zeros(1024, N),
+                     accumulate=True) for r0 in range(0, M, 1024)]
+    assert torch.equal(C, torch.cat(parts))
+    rows = np.r_[0, 255, 8191, 8192, 8193, 10000, M - 1]
+    ref = host(A[:, rows]).astype(np.float64).T @ host(B).astype(np.float64)
+    assert rel_err(host(C[rows]), ref) < 1e-5
+    C2 = C.clone()
+    gn.gemm(A, B, transA=True, out_dtype=torch.float32, C=C2, accumulate=True)
+    assert torch.equal(C2, C + C)
+    # Linear y = x W^T + b with 11264 outputs over 4096 tokens: dW = dY^T X, db = sum_t dY
+    dY = torch.randn(K, M, device="cuda:0", generator=g).bfloat16()
+    X = torch.randn(K, N, device="cuda:0", generator=g).bfloat16()
+    W = (torch.randn(M, N, device="cuda:0", generator=g) * 0.02).bfloat16()
+    _, dW, db = gn.linear_bwd(dY, X, W, need_dx=False)
+    dWp = [gn.linear_bwd(dY[:, r0:r0 + 1024].contiguous(), X, W[r0:r0 + 1024].contiguous(),
+                         need_dx=False, dW=zeros(1024, N), db=zeros(1024), accumulate=True,
+                         ws=False)[1] for r0 in range(0, M, 1024)]
+    assert torch.equal(dW, torch.cat(dWp))
+    hdY = host(dY).astype(np.float64)
+    assert rel_err(host(dW[rows]), hdY[:, rows].T @ host(X).astype(np.float64)) < 1e-5
+    assert rel_err(host(db), hdY.sum(0)) < 1e-5
+
+
 def test_gemm_unaligned_falls_back(gn):
     r = rng_(3)
     A = rnd(r.standard_normal((10, 13)).astype(np.float32))
