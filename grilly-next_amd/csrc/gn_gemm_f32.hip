@@ -265,13 +265,15 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
     };
 
     if (tb < te) {
+        // the first two k-tiles' loads go out together, so only one load latency precedes the
+        // first split (short k loops, e.g. K = 64, are all prologue)
         gload(tb, r0s);
+        gload(min(tb + 1, te - 1), r1s);
         sstore(0, r0s);
-        gload(min(tb + 1, te - 1), r0s);
-        gload(min(tb + 2, te - 1), r1s);
+        gload(min(tb + 2, te - 1), r0s);
         for (int t = tb; t < te; t += 2) {
-            iter(t, r0s);
-            if (t + 1 < te) iter(t + 1, r1s);
+            iter(t, r1s);
+            if (t + 1 < te) iter(t + 1, r0s);
         }
     }
 
@@ -289,6 +291,36 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
                 for (int r = 0; r < 16; ++r) {
                     const int m = m0 + ra0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                     if (m < g.M) P[(size_t)m * g.N + n] = acc[i][j][r];
+                }
+            }
+    } else if ((((uintptr_t)g.C | (uintptr_t)g.C2) & 15) == 0 && (g.ldc & 3) == 0) {
+        // 16-byte stores: each wave stages one 32 x 32 accumulator at a time in its own LDS
+        // strip (pitch 40 floats, so the two row groups of a staging write fall in disjoint
+        // banks) and writes it back as whole row segments, lane l taking rows l / 8 + 8 q and
+        // columns 4 (l % 8) .. +3 (N % 4 == 0, so a vector is entirely in or out)
+        __syncthreads();  // every wave is done reading the operand stages
+        float* strip = reinterpret_cast<float*>(smem_raw) + wave * (32 * 40);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    strip[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 40 + (lane & 31)] = acc[i][j][r];
+                const int n = n0 + rb0 + j * 32 + 4 * (lane & 7);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int row = (lane >> 3) + 8 * q;
+                    float4 v = *reinterpret_cast<const float4*>(strip + row * 40 + 4 * (lane & 7));
+                    const int m = m0 + ra0 + i * 32 + row;
+                    if (m >= g.M || n >= g.N) continue;
+                    float* dst = reinterpret_cast<float*>(m < g.Msplit ? g.C : g.C2) +
+                                 (size_t)(m < g.Msplit ? m : m - g.Msplit) * g.ldc + n;
+                    if (g.accumulate) {
+                        const float4 o = *reinterpret_cast<const float4*>(dst);
+                        v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+                    }
+                    *reinterpret_cast<float4*>(dst) = v;
                 }
             }
     } else {
