@@ -248,6 +248,10 @@ def test_colsum_few_and_many_rows(gn, M, N, dtype):
     assert np.all(np.abs(host(out) - ref) <= tol)
     if M <= 1024:
         assert torch.equal(out, gn.colsum(xd))
+        if N % 4 == 0:
+            # four columns per lane (N % 4 == 0, aligned rows) add exactly as one per lane
+            for j in (0, 1, N // 2, N - 1):
+                assert torch.equal(out[j:j + 1], gn.colsum(xd[:, j:j + 1].contiguous()))
     base = dev(r.standard_normal(N).astype(np.float32))
     acc = base.clone()
     gn.colsum(xd, out=acc, accumulate=True)
