@@ -204,12 +204,22 @@ __global__ __launch_bounds__(1024) void plane_sum(const float* __restrict__ part
     const int f = blockIdx.x * 64 + lane;
     float s0 = 0.f, s1 = 0.f;
     if (f < L) {
-        int g = wave;
-        for (; g + 16 < G; g += 32) {
-            s0 += part[(size_t)g * L + f];
-            s1 += part[(size_t)(g + 16) * L + f];
+        // rows g = wave + 16 i: even i into s0, odd i into s1, in order; eight rows' loads go
+        // out before their adds (one memory round trip per eight rows)
+        for (int g0 = wave; g0 < G; g0 += 128) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int g = g0 + 16 * i;
+                v[i] = g < G ? part[(size_t)g * L + f] : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (g0 + 16 * i >= G) break;
+                if (i % 2 == 0) s0 += v[i];
+                else s1 += v[i];
+            }
         }
-        if (g < G) s0 += part[(size_t)g * L + f];
     }
     sh[wave][lane] = s0 + s1;
     __syncthreads();
