@@ -19,6 +19,14 @@
 // keep the dQ reduction free of atomics and deterministic.  The epilogues stage each
 // wave's rows in LDS and apply the inverse rotation from a cos/sin table.
 // A SIMT path (any D <= 256, fp32 or bf16) serves other shapes and the fp32 dtype.
+//
+// Key-padding mask (flash-attention2.glsl:150-154, flash-attention2-rope.glsl:201-205: the
+// score of key k in batch b gets (mask[b S + k] - 1) 1e9): a pre-pass turns the mask into a
+// per-key additive bias in the kernels' base-2 units (0 for a kept key, -inf where the
+// reference's bias is below -1e4, i.e. where exp() of the biased score is 0 in fp32 for any
+// row that keeps a key) and one flag per 64-key tile, so tiles without a masked key take the
+// unmasked code.  A row whose visible keys are all masked gets O = 0, LSE = -inf and zero
+// gradients (the reference's fp32 forward averages such a row uniformly instead).
 #include <math.h>
 
 #include <type_traits>
@@ -262,8 +270,9 @@ struct DkdvCfg {
 template <int D, int STAGES, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     TDesc tQ, TDesc tK, TDesc tV, TDesc tG, const float* __restrict__ Lsc,
-    const float* __restrict__ Di, const float2* __restrict__ cs, TDesc tdK, TDesc tdV, int H,
-    int S, int Spad, float scale, int causal, int rope_mode) {
+    const float* __restrict__ Di, const float2* __restrict__ cs, const float* __restrict__ kb,
+    const int* __restrict__ kt, TDesc tdK, TDesc tdV, int H, int S, int Spad, float scale,
+    int causal, int rope_mode) {
     static_assert(NW == 4 || NW == 8, "four or eight waves");
     using C = DkdvCfg<D, STAGES, NW>;
     extern __shared__ __align__(1024) unsigned char smem[];
@@ -278,6 +287,10 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     const int kg = wave & 3, half0 = NW == 4 ? 0 : wave >> 2;
     const int kw0 = j0 + kg * 32, key = kw0 + (lane & 31);
     const float c2 = scale * 1.4426950408889634f;
+    // key-padding bias of this lane's key; the wave's 32 keys lie in one 64-key tile
+    const int bb = bh / H;
+    const bool kmask = kb && kw0 < S && kt[bb * (Spad / 64) + kw0 / 64];
+    const float kbl = kmask && key < S ? kb[(size_t)bb * Spad + key] : 0.f;
 
     // the block's K and V rows stay in LDS (after the stages) for the whole block
     const bf16_t* sKb = reinterpret_cast<const bf16_t*>(smem + STAGES * C::STAGE);
@@ -376,7 +389,12 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
                 const int ql = 32 * i + 8 * g + 4 * h;
                 const float4 L4 = *reinterpret_cast<const float4*>(sL + ql);
                 const float4 D4 = *reinterpret_cast<const float4*>(sD + ql);
-                const float Lv[4] = {L4.x, L4.y, L4.z, L4.w}, Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+                float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
+                const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+                if (kmask) {  // wave-uniform: the bias rides on the L term
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) Lv[e] -= kbl;
+                }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int r = 4 * g + e;
@@ -446,8 +464,9 @@ struct DqCfg {
 template <int D, int STAGES>
 __global__ __launch_bounds__(256) void attn_dq_mfma(
     TDesc tQ, TDesc tK, TDesc tV, TDesc tG, const float* __restrict__ Lsc,
-    const float* __restrict__ Di, const float2* __restrict__ cs, TDesc tdQ, int H, int S,
-    int Spad, float scale, int causal, int rope_mode) {
+    const float* __restrict__ Di, const float2* __restrict__ cs, const float* __restrict__ kb,
+    const int* __restrict__ kt, TDesc tdQ, int H, int S, int Spad, float scale, int causal,
+    int rope_mode) {
     using C = DqCfg<D, STAGES>;
     extern __shared__ __align__(1024) unsigned char smem[];
     constexpr int NT = D / 32, KS = D / 16;
@@ -498,6 +517,7 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(
         const bf16_t* sV = reinterpret_cast<const bf16_t*>(sb + C::TB);
         if (qw0 >= S || (causal && k0 > qw0 + 31)) continue;  // every key masked for the wave
         const bool full = qw0 + 31 < S && k0 + 63 < S && (!causal || k0 + 63 <= qw0);
+        const float* kbt = kb && kt[(bh / H) * (Spad / 64) + it] ? kb + (size_t)(bh / H) * Spad + k0 : nullptr;
 
         // masked entries get S = -inf, hence dS = 0
 #pragma unroll
@@ -529,6 +549,17 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(
                 }
             }
             float dv[16];
+            if (kbt) {  // key-padding biases of the 16 keys this lane holds (masked tiles only),
+                        // in score units (scale > 0, checked by the entry points)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(kbt + 32 * i + 8 * g + 4 * h);
+                    s[4 * g] += k4.x / c2;
+                    s[4 * g + 1] += k4.y / c2;
+                    s[4 * g + 2] += k4.z / c2;
+                    s[4 * g + 3] += k4.w / c2;
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 dv[r] = __builtin_amdgcn_exp2f(s[r] * c2 - lq) * (dp[r] - dq);
@@ -569,8 +600,10 @@ __global__ __launch_bounds__(256) void attn_dq_mfma(
 // bf16 rows; LSE = (m + log2 l) ln 2.
 template <int D, int STAGES>
 __global__ __launch_bounds__(256) void attn_fwd_mfma(TDesc tQ, TDesc tK, TDesc tV, TDesc tO,
-                                                     float* __restrict__ LSE, int H, int S,
-                                                     float scale, int causal) {
+                                                     float* __restrict__ LSE,
+                                                     const float* __restrict__ kb,
+                                                     const int* __restrict__ kt, int H, int S,
+                                                     int Spad, float scale, int causal) {
     using C = DqCfg<D, STAGES>;
     extern __shared__ __align__(1024) unsigned char smem[];
     constexpr int NT = D / 32, KS = D / 16;
@@ -617,6 +650,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma(TDesc tQ, TDesc tK, TDesc t
         const bf16_t* sV = reinterpret_cast<const bf16_t*>(sb + C::TB);
         if (qw0 >= S || (causal && k0 > qw0 + 31)) continue;  // every key masked for the wave
         const bool full = qw0 + 31 < S && k0 + 63 < S && (!causal || k0 + 63 <= qw0);
+        const float* kbt = kb && kt[(bh / H) * (Spad / 64) + it] ? kb + (size_t)(bh / H) * Spad + k0 : nullptr;
 
         f32x16_t sc[2];
 #pragma unroll
@@ -638,6 +672,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma(TDesc tQ, TDesc tK, TDesc t
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float v = sc[i][r] * c2;
+                if (kbt) v += kbt[32 * i + 8 * (r >> 2) + 4 * h + (r & 3)];
                 if (!full) {
                     const int kk = k0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
                     const bool ok = q < S && kk < S && (!causal || kk <= q);
@@ -838,11 +873,33 @@ __global__ __launch_bounds__(256) void attn_prep(
     // (same address and value across the row's lanes): no branch, so the LSE load stays with
     // the others instead of being sunk behind their wait
     Di[(size_t)bh * Spad + pos] = dot;
-    Lsc[(size_t)bh * Spad + pos] = lse * 1.4426950408889634f;
+    // a row with every visible key masked (LSE = -inf, O = 0) gets P = 0 through L = +inf
+    Lsc[(size_t)bh * Spad + pos] = lse == -INFINITY ? INFINITY : lse * 1.4426950408889634f;
     if (c == 0 && pos == S - 1)  // finite padding: masked entries compute exp2(-inf - 0) * (dP - 0)
         for (int p = S; p < Spad; ++p) Di[(size_t)bh * Spad + p] = Lsc[(size_t)bh * Spad + p] = 0.f;
     if (mode == GN_ROPE_NONE) return;
     rotate_qk_chunk<D>(qk4, c, tab, mode, Qr + off, Kr + off);
+}
+
+// Key-padding pre-pass: kb[b][k] = the reference's score bias (mask[b S + k] - 1) 1e9 in
+// base-2 units, -inf where that bias is below -1e4 (exp() of the biased score is then 0 in fp32
+// for any row that keeps a key), 0 past S; kt[b][t] = 1 when 64-key tile t holds a nonzero
+// bias.  One wave per tile.
+__global__ __launch_bounds__(256) void attn_key_bias(const float* __restrict__ mask,
+                                                     float* __restrict__ kb, int* __restrict__ kt,
+                                                     int B, int S, int Spad) {
+    const int tile = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int tiles = Spad / 64;
+    if (tile >= B * tiles) return;  // whole waves leave together
+    const int b = tile / tiles, k = (tile % tiles) * 64 + lane;
+    float v = 0.f;
+    if (k < S) {
+        const float bias = (mask[(size_t)b * S + k] - 1.0f) * 1e9f;
+        v = bias < -1e4f ? -INFINITY : bias * 1.4426950408889634f;
+    }
+    kb[(size_t)b * Spad + k] = v;
+    const unsigned long long any = __ballot(v != 0.f);
+    if (lane == 0) kt[tile] = any != 0ull;
 }
 
 // ---- SIMT path: one wave per query row (dQ, forward) or key row (dK, dV) ----------------
@@ -860,17 +917,25 @@ __device__ __forceinline__ float dot4(const float (&a)[4], const float (&b)[4]) 
     return wave_sum(a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3]);
 }
 
+// key-padding bias in natural-log units (kb holds base-2 units; -inf stays -inf)
+__device__ __forceinline__ float kbias_nat(const float* kbb, int j) {
+    return kbb ? kbb[j] * 0.6931471805599453f : 0.f;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void attn_fwd_simt(const T* __restrict__ Qr,
                                                      const T* __restrict__ Kr,
                                                      const T* __restrict__ V, T* __restrict__ O,
-                                                     float* __restrict__ LSE, int64_t BH, int S,
-                                                     int D, float scale, int causal) {
+                                                     float* __restrict__ LSE,
+                                                     const float* __restrict__ kb, int H,
+                                                     int64_t BH, int S, int Spad, int D,
+                                                     float scale, int causal) {
     const int64_t row = blockIdx.x * (int64_t)4 + (threadIdx.x >> 6);
     if (row >= BH * S) return;
     const int64_t bh = row / S;
     const int i = (int)(row % S);
     const size_t base = (size_t)bh * S * D;
+    const float* kbb = kb ? kb + (size_t)(bh / H) * Spad : nullptr;
     float q[4], o[4] = {0.f, 0.f, 0.f, 0.f};
     ld_row(Qr + base + (size_t)i * D, D, q);
     float m = -INFINITY, l = 0.f;
@@ -879,7 +944,8 @@ __global__ __launch_bounds__(256) void attn_fwd_simt(const T* __restrict__ Qr,
         float k[4], v[4];
         ld_row(Kr + base + (size_t)j * D, D, k);
         ld_row(V + base + (size_t)j * D, D, v);
-        const float s = dot4(q, k) * scale;
+        const float s = dot4(q, k) * scale + kbias_nat(kbb, j);
+        if (s == -INFINITY) continue;  // a masked key (uniform across the wave)
         const float mn = fmaxf(m, s);
         const float a = __expf(m - mn), p = __expf(s - mn);
         l = l * a + p;
@@ -888,34 +954,40 @@ __global__ __launch_bounds__(256) void attn_fwd_simt(const T* __restrict__ Qr,
         m = mn;
     }
     const int lane = threadIdx.x & 63;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;  // no visible kept key: O = 0, LSE = -inf
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int d = lane + 64 * e;
-        if (d < D) io<T>::st(O, base + (size_t)i * D + d, o[e] / l);
+        if (d < D) io<T>::st(O, base + (size_t)i * D + d, o[e] * inv);
     }
-    if (lane == 0) LSE[row] = m + __logf(l);
+    if (lane == 0) LSE[row] = l > 0.f ? m + __logf(l) : -INFINITY;
 }
+
+// LSE of a row with no visible kept key is -inf: +inf here makes its P (and dS) 0
+__device__ __forceinline__ float lse_eff(float lse) { return lse == -INFINITY ? INFINITY : lse; }
 
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dq_simt(
     const T* __restrict__ Qr, const T* __restrict__ Kr, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Di,
-    float* __restrict__ dQacc, int64_t BH, int S, int D, float scale, int causal) {
+    const float* __restrict__ kb, float* __restrict__ dQacc, int H, int64_t BH, int S,
+    int Spad, int D, float scale, int causal) {
     const int64_t row = blockIdx.x * (int64_t)4 + (threadIdx.x >> 6);
     if (row >= BH * S) return;
     const int64_t bh = row / S;
     const int i = (int)(row % S);
     const size_t base = (size_t)bh * S * D;
+    const float* kbb = kb ? kb + (size_t)(bh / H) * Spad : nullptr;
     float q[4], g[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
     ld_row(Qr + base + (size_t)i * D, D, q);
     ld_row(dO + base + (size_t)i * D, D, g);
-    const float lse = LSE[row], di = Di[row];
+    const float lse = lse_eff(LSE[row]), di = Di[row];
     const int jn = causal ? i + 1 : S;
     for (int j = 0; j < jn; ++j) {
         float k[4], v[4];
         ld_row(Kr + base + (size_t)j * D, D, k);
         ld_row(V + base + (size_t)j * D, D, v);
-        const float p = __expf(dot4(q, k) * scale - lse);
+        const float p = __expf(dot4(q, k) * scale + kbias_nat(kbb, j) - lse);
         const float ds = p * (dot4(g, v) - di);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] += ds * k[e];
@@ -932,13 +1004,14 @@ template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_simt(
     const T* __restrict__ Qr, const T* __restrict__ Kr, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Di,
-    float* __restrict__ dKacc, T* __restrict__ dV, int64_t BH, int S, int D, float scale,
-    int causal) {
+    const float* __restrict__ kb, float* __restrict__ dKacc, T* __restrict__ dV, int H,
+    int64_t BH, int S, int Spad, int D, float scale, int causal) {
     const int64_t row = blockIdx.x * (int64_t)4 + (threadIdx.x >> 6);
     if (row >= BH * S) return;
     const int64_t bh = row / S;
     const int j = (int)(row % S);
     const size_t base = (size_t)bh * S * D;
+    const float kbj = kb ? kbias_nat(kb + (size_t)(bh / H) * Spad, j) : 0.f;
     float k[4], v[4], ak[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f};
     ld_row(Kr + base + (size_t)j * D, D, k);
     ld_row(V + base + (size_t)j * D, D, v);
@@ -946,7 +1019,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_simt(
         float q[4], g[4];
         ld_row(Qr + base + (size_t)i * D, D, q);
         ld_row(dO + base + (size_t)i * D, D, g);
-        const float p = __expf(dot4(q, k) * scale - LSE[bh * S + i]);
+        const float p = __expf(dot4(q, k) * scale + kbj - lse_eff(LSE[bh * S + i]));
         const float ds = p * (dot4(g, v) - Di[bh * S + i]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -997,7 +1070,11 @@ struct AttnWs {
     float* Lsc;   // MFMA path: L log2(e), [B*H][Spad]
     float2* cs;   // MFMA path: RoPE cos/sin table [S][D/2]
     float* acc;   // SIMT path: fp32 [B*H*S*D]
+    float* kb;    // key-padding bias (base 2) [B][Spad] (sized for B*H rows)
+    int* kt;      // per 64-key tile: any key biased [B][Spad/64]
 };
+
+
 
 inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 inline int spad_of(int S) { return (S + 63) / 64 * 64; }
@@ -1023,8 +1100,23 @@ size_t ws_layout(int64_t BH, int S, int D, size_t esz, bool mfma, void* base, At
         t.Di = (float*)take(BH * S * 4);
         t.acc = (float*)take(BHSD * 4);
     }
+    t.kb = (float*)take(BH * spad_of(S) * 4);
+    t.kt = (int*)take(BH * (spad_of(S) / 64) * 4);
     if (w) *w = t;
     return off;
+}
+
+// key bias and tile flags from a [B][S] mask (nothing without one); returns the kb / kt
+// pointers the kernels take (null: no mask)
+void key_bias(const float* mask, const AttnWs& w, int B, int S, hipStream_t s, const float** kb,
+              const int** kt) {
+    *kb = nullptr;
+    *kt = nullptr;
+    if (!mask) return;
+    const int tiles = B * (spad_of(S) / 64);
+    attn_key_bias<<<(tiles + 3) / 4, 256, 0, s>>>(mask, w.kb, w.kt, B, S, spad_of(S));
+    *kb = w.kb;
+    *kt = w.kt;
 }
 
 template <typename F>
@@ -1048,8 +1140,9 @@ inline TDesc bshd(const void* p, int S, int D, int64_t ld) {
 }
 
 template <int D>
-int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, int BH, int H, int S,
-                    float scale, int causal, int rope_mode, float theta, hipStream_t s) {
+int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, const float* mask,
+                    int BH, int H, int S, float scale, int causal, int rope_mode, float theta,
+                    hipStream_t s) {
     using C1 = DkdvCfg<D, kStagesDkdv, kWavesDkdv>;
     using C2 = DqCfg<D, kStagesDq>;
     static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>, C1::LDS);
@@ -1066,6 +1159,9 @@ int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, int BH,
     }
     if (rope_mode != GN_ROPE_NONE)
         rope_table<<<grid_for((int64_t)S * (D / 2), 256, 4096), 256, 0, s>>>(w.cs, S, D, theta);
+    const float* kb;
+    const int* kt;
+    key_bias(mask, w, BH / H, S, s, &kb, &kt);
     const int64_t threads = rows * (D / 8);
     attn_prep<D><<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(
         io.Q, io.K, io.dO, io.O, LSE, (bf16_t*)w.Qr, (bf16_t*)w.Kr, w.Lsc, w.Di, w.cs, rows, H, S,
@@ -1076,18 +1172,19 @@ int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, int BH,
     const int nb = (S + 127) / 128;
     hipLaunchKernelGGL((attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>), dim3(BH, nb),
                        dim3(64 * kWavesDkdv), C1::LDS, s, tQ, tK, io.V, io.dO, w.Lsc, w.Di, w.cs,
-                       io.dK, io.dV, H, S, Spad, scale, causal, rope_mode);
+                       kb, kt, io.dK, io.dV, H, S, Spad, scale, causal, rope_mode);
     hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, tQ, tK,
-                       io.V, io.dO, w.Lsc, w.Di, w.cs, io.dQ, H, S, Spad, scale, causal, rope_mode);
+                       io.V, io.dO, w.Lsc, w.Di, w.cs, kb, kt, io.dQ, H, S, Spad, scale, causal,
+                       rope_mode);
     GN_LAUNCH_CHECK("gn_attn_bwd (mfma)");
     return GN_OK;
 }
 
 template <typename T>
 int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, const void* dO,
-                  const float* LSE, void* dQ, void* dK, void* dV, int B, int H, int S, int D,
-                  float scale, int causal, int rope_mode, float theta, void* ws, size_t ws_bytes,
-                  hipStream_t s) {
+                  const float* LSE, const float* mask, void* dQ, void* dK, void* dV, int B, int H,
+                  int S, int D, float scale, int causal, int rope_mode, float theta, void* ws,
+                  size_t ws_bytes, hipStream_t s) {
     const int64_t BH = (int64_t)B * H, rows = BH * S, BHSD = rows * D;
     // the MFMA kernels move 16-byte chunks (LDS DMA, vector stores) from and to every tensor
     // and the workspace: an offset view takes the SIMT kernels instead
@@ -1105,9 +1202,13 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
         const AttnIO io{bhsd(Q, H, S, D),  bhsd(K, H, S, D),  bhsd(V, H, S, D),  bhsd(O, H, S, D),
                         bhsd(dO, H, S, D), bhsd(dQ, H, S, D), bhsd(dK, H, S, D), bhsd(dV, H, S, D)};
         if (D == 64)
-            return launch_mfma_bwd<64>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, theta, s);
-        return launch_mfma_bwd<128>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, theta, s);
+            return launch_mfma_bwd<64>(w, io, LSE, mask, (int)BH, H, S, scale, causal, rope_mode, theta, s);
+        return launch_mfma_bwd<128>(w, io, LSE, mask, (int)BH, H, S, scale, causal, rope_mode, theta, s);
     }
+    const float* kb;
+    const int* kt;
+    key_bias(mask, w, B, S, s, &kb, &kt);
+    const int Spad = spad_of(S);
     const void* Qp = Q;
     const void* Kp = K;
     if (rope_mode != GN_ROPE_NONE) {
@@ -1121,11 +1222,11 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
     const unsigned gr = (unsigned)((rows + 3) / 4);
     const unsigned ge = grid_for(rows * (D / 2), 256, 16384);
     attn_bwd_dq_simt<T><<<gr, 256, 0, s>>>((const T*)Qp, (const T*)Kp, (const T*)V, (const T*)dO,
-                                           LSE, w.Di, w.acc, BH, S, D, scale, causal);
+                                           LSE, w.Di, kb, w.acc, H, BH, S, Spad, D, scale, causal);
     unrotate_store<T><<<ge, 256, 0, s>>>(w.acc, (T*)dQ, rows, S, D, rope_mode, theta);
     attn_bwd_dkdv_simt<T><<<gr, 256, 0, s>>>((const T*)Qp, (const T*)Kp, (const T*)V,
-                                             (const T*)dO, LSE, w.Di, w.acc, (T*)dV, BH, S, D,
-                                             scale, causal);
+                                             (const T*)dO, LSE, w.Di, kb, w.acc, (T*)dV, H, BH, S,
+                                             Spad, D, scale, causal);
     unrotate_store<T><<<ge, 256, 0, s>>>(w.acc, (T*)dK, rows, S, D, rope_mode, theta);
     GN_LAUNCH_CHECK("gn_attn_bwd (simt)");
     (void)BHSD;
@@ -1146,8 +1247,9 @@ extern "C" size_t gn_attn_workspace_bytes(int B, int H, int S, int D) {
 }
 
 static int attn_check(const void* Q, const void* K, const void* V, int B, int H, int S, int D,
-                      int rope_mode, int dtype) {
+                      int rope_mode, int dtype, float scale) {
     GN_REQUIRE(B >= 0 && H >= 0 && S >= 0 && D > 0, "attention: bad shape");
+    GN_REQUIRE(scale > 0.f && scale < INFINITY, "attention: scale %g must be positive and finite", scale);
     GN_REQUIRE(Q && K && V, "attention: null pointer");
     GN_REQUIRE(D <= 256 && D % 2 == 0, "attention: D=%d must be even and <= 256", D);
     GN_REQUIRE(rope_mode >= GN_ROPE_NONE && rope_mode <= GN_ROPE_HALF, "attention: rope_mode %d", rope_mode);
@@ -1156,32 +1258,41 @@ static int attn_check(const void* Q, const void* K, const void* V, int B, int H,
     return GN_OK;
 }
 
-extern "C" int gn_attn_bwd(const void* Q, const void* K, const void* V, const void* O,
-                           const void* dO, const float* LSE, void* dQ, void* dK, void* dV, int B,
-                           int H, int S, int D, float scale, int causal, int rope_mode,
-                           float rope_theta, int dtype, void* ws, size_t ws_bytes,
-                           void* stream) {
+extern "C" int gn_attn_bwd_mask(const void* Q, const void* K, const void* V, const void* O,
+                                const void* dO, const float* LSE, const float* key_mask, void* dQ,
+                                void* dK, void* dV, int B, int H, int S, int D, float scale,
+                                int causal, int rope_mode, float rope_theta, int dtype, void* ws,
+                                size_t ws_bytes, void* stream) {
     clear_error();
-    int rc = attn_check(Q, K, V, B, H, S, D, rope_mode, dtype);
+    int rc = attn_check(Q, K, V, B, H, S, D, rope_mode, dtype, scale);
     if (rc) return rc;
     if ((int64_t)B * H * S == 0) return GN_OK;
     GN_REQUIRE(O && dO && LSE && dQ && dK && dV, "gn_attn_bwd: null pointer");
     hipStream_t s = as_stream(stream);
     if (dtype == GN_BF16)
-        return attn_bwd_impl<bf16_t>(Q, K, V, O, dO, LSE, dQ, dK, dV, B, H, S, D, scale, causal,
-                                     rope_mode, rope_theta, ws, ws_bytes, s);
-    return attn_bwd_impl<float>(Q, K, V, O, dO, LSE, dQ, dK, dV, B, H, S, D, scale, causal,
-                                rope_mode, rope_theta, ws, ws_bytes, s);
+        return attn_bwd_impl<bf16_t>(Q, K, V, O, dO, LSE, key_mask, dQ, dK, dV, B, H, S, D, scale,
+                                     causal, rope_mode, rope_theta, ws, ws_bytes, s);
+    return attn_bwd_impl<float>(Q, K, V, O, dO, LSE, key_mask, dQ, dK, dV, B, H, S, D, scale,
+                                causal, rope_mode, rope_theta, ws, ws_bytes, s);
 }
 
-extern "C" int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, const void* O,
-                                const void* dO, const float* LSE, void* dQ, void* dK, void* dV,
-                                int B, int H, int S, int D, int64_t ld_qkv, int64_t ld_o,
-                                int64_t ld_dqkv, float scale, int causal, int rope_mode,
-                                float rope_theta, int dtype, void* ws, size_t ws_bytes,
-                                void* stream) {
+extern "C" int gn_attn_bwd(const void* Q, const void* K, const void* V, const void* O,
+                           const void* dO, const float* LSE, void* dQ, void* dK, void* dV, int B,
+                           int H, int S, int D, float scale, int causal, int rope_mode,
+                           float rope_theta, int dtype, void* ws, size_t ws_bytes,
+                           void* stream) {
+    return gn_attn_bwd_mask(Q, K, V, O, dO, LSE, nullptr, dQ, dK, dV, B, H, S, D, scale, causal,
+                            rope_mode, rope_theta, dtype, ws, ws_bytes, stream);
+}
+
+extern "C" int gn_attn_bwd_bshd_mask(const void* Q, const void* K, const void* V, const void* O,
+                                     const void* dO, const float* LSE, const float* key_mask,
+                                     void* dQ, void* dK, void* dV, int B, int H, int S, int D,
+                                     int64_t ld_qkv, int64_t ld_o, int64_t ld_dqkv, float scale,
+                                     int causal, int rope_mode, float rope_theta, int dtype,
+                                     void* ws, size_t ws_bytes, void* stream) {
     clear_error();
-    int rc = attn_check(Q, K, V, B, H, S, D, rope_mode, dtype);
+    int rc = attn_check(Q, K, V, B, H, S, D, rope_mode, dtype, scale);
     if (rc) return rc;
     if ((int64_t)B * H * S == 0) return GN_OK;
     GN_REQUIRE(O && dO && LSE && dQ && dK && dV, "gn_attn_bwd_bshd: null pointer");
@@ -1193,9 +1304,10 @@ extern "C" int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, con
                "gn_attn_bwd_bshd: row strides must be multiples of 8 elements");
     GN_REQUIRE(ld_qkv < (1 << 24) && ld_o < (1 << 24) && ld_dqkv < (1 << 24),
                "gn_attn_bwd_bshd: row strides must be below 2^24 elements");
-    const void* ptrs[8] = {Q, K, V, O, dO, dQ, dK, dV};
+    const void* ptrs[9] = {Q, K, V, O, dO, dQ, dK, dV, ws};
     for (const void* p : ptrs)
-        GN_REQUIRE(((uintptr_t)p & 15u) == 0, "gn_attn_bwd_bshd: pointers must be 16-byte aligned");
+        GN_REQUIRE(((uintptr_t)p & 15u) == 0,
+                   "gn_attn_bwd_bshd: pointers (and the workspace) must be 16-byte aligned");
     AttnWs w;
     const int64_t BH = (int64_t)B * H;
     const size_t need = ws_layout(BH, S, D, 2, true, ws, &w);
@@ -1208,15 +1320,29 @@ extern "C" int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, con
                     bshd(dK, S, D, ld_dqkv), bshd(dV, S, D, ld_dqkv)};
     hipStream_t s = as_stream(stream);
     if (D == 64)
-        return launch_mfma_bwd<64>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, rope_theta, s);
-    return launch_mfma_bwd<128>(w, io, LSE, (int)BH, H, S, scale, causal, rope_mode, rope_theta, s);
+        return launch_mfma_bwd<64>(w, io, LSE, key_mask, (int)BH, H, S, scale, causal, rope_mode,
+                                   rope_theta, s);
+    return launch_mfma_bwd<128>(w, io, LSE, key_mask, (int)BH, H, S, scale, causal, rope_mode,
+                                rope_theta, s);
 }
 
-extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O, float* LSE,
-                           int B, int H, int S, int D, float scale, int causal, int rope_mode,
-                           float rope_theta, int dtype, void* ws, size_t ws_bytes, void* stream) {
+extern "C" int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, const void* O,
+                                const void* dO, const float* LSE, void* dQ, void* dK, void* dV,
+                                int B, int H, int S, int D, int64_t ld_qkv, int64_t ld_o,
+                                int64_t ld_dqkv, float scale, int causal, int rope_mode,
+                                float rope_theta, int dtype, void* ws, size_t ws_bytes,
+                                void* stream) {
+    return gn_attn_bwd_bshd_mask(Q, K, V, O, dO, LSE, nullptr, dQ, dK, dV, B, H, S, D, ld_qkv,
+                                 ld_o, ld_dqkv, scale, causal, rope_mode, rope_theta, dtype, ws,
+                                 ws_bytes, stream);
+}
+
+extern "C" int gn_attn_fwd_mask(const void* Q, const void* K, const void* V, const float* key_mask,
+                                void* O, float* LSE, int B, int H, int S, int D, float scale,
+                                int causal, int rope_mode, float rope_theta, int dtype, void* ws,
+                                size_t ws_bytes, void* stream) {
     clear_error();
-    int rc = attn_check(Q, K, V, B, H, S, D, rope_mode, dtype);
+    int rc = attn_check(Q, K, V, B, H, S, D, rope_mode, dtype, scale);
     if (rc) return rc;
     const int64_t rows = (int64_t)B * H * S;
     if (rows == 0) return GN_OK;
@@ -1224,19 +1350,22 @@ extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O,
     hipStream_t s = as_stream(stream);
     auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     const bool mfma = dtype == GN_BF16 && (D == 64 || D == 128) && al16(Q) && al16(K) && al16(V) &&
-                      al16(O) &&
-                      (rope_mode == GN_ROPE_NONE || (al16(ws) && rows * (D / 8) < ((int64_t)1 << 31)));
+                      al16(O) && ((rope_mode == GN_ROPE_NONE && !key_mask) || al16(ws)) &&
+                      (rope_mode == GN_ROPE_NONE || rows * (D / 8) < ((int64_t)1 << 31));
     const size_t esz = dtype == GN_BF16 ? 2 : 4;
     AttnWs w;
-    // MFMA path: rotated bf16 Q, K and the cos/sin table (the backward's layout); SIMT path:
-    // rotated Q, K only
+    // MFMA path: rotated bf16 Q, K, the cos/sin table (the backward's layout) and the key
+    // bias; SIMT path: rotated Q, K and the key bias
     const size_t need = mfma ? ws_layout((int64_t)B * H, S, D, 2, true, ws, &w)
-                             : (ws_layout((int64_t)B * H, S, D, esz, false, ws, &w),
-                                2 * align_up((size_t)rows * D * esz));
-    if (rope_mode != GN_ROPE_NONE && (!ws || ws_bytes < need)) {
+                             : ws_layout((int64_t)B * H, S, D, esz, false, ws, &w);
+    if ((rope_mode != GN_ROPE_NONE || key_mask) && (!ws || ws_bytes < need)) {
         set_error("gn_attn_fwd: workspace %zu B < %zu B", ws_bytes, need);
         return GN_E_WORKSPACE;
     }
+    const float* kb;
+    const int* kt;
+    key_bias(key_mask, w, B, S, s, &kb, &kt);
+    const int Spad = spad_of(S);
     const void* Qp = Q;
     const void* Kp = K;
     if (rope_mode != GN_ROPE_NONE && mfma) {
@@ -1273,13 +1402,13 @@ extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O,
             static const bool ok = allow_lds(attn_fwd_mfma<64, kStagesDq>, C::LDS);
             GN_REQUIRE(ok, "gn_attn_fwd: cannot reserve %d B of LDS", C::LDS);
             hipLaunchKernelGGL((attn_fwd_mfma<64, kStagesDq>), grid, dim3(256), C::LDS, s, tQ, tK, tV, tO,
-                               LSE, H, S, scale, causal);
+                               LSE, kb, kt, H, S, Spad, scale, causal);
         } else {
             using C = DqCfg<128, kStagesDq>;
             static const bool ok = allow_lds(attn_fwd_mfma<128, kStagesDq>, C::LDS);
             GN_REQUIRE(ok, "gn_attn_fwd: cannot reserve %d B of LDS", C::LDS);
             hipLaunchKernelGGL((attn_fwd_mfma<128, kStagesDq>), grid, dim3(256), C::LDS, s, tQ, tK, tV, tO,
-                               LSE, H, S, scale, causal);
+                               LSE, kb, kt, H, S, Spad, scale, causal);
         }
         GN_LAUNCH_CHECK("gn_attn_fwd (mfma)");
         return GN_OK;
@@ -1287,10 +1416,19 @@ extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O,
     const unsigned gr = (unsigned)((rows + 3) / 4);
     if (dtype == GN_BF16)
         attn_fwd_simt<bf16_t><<<gr, 256, 0, s>>>((const bf16_t*)Qp, (const bf16_t*)Kp, (const bf16_t*)V,
-                                                 (bf16_t*)O, LSE, (int64_t)B * H, S, D, scale, causal);
+                                                 (bf16_t*)O, LSE, kb, H, (int64_t)B * H, S, Spad, D,
+                                                 scale, causal);
     else
         attn_fwd_simt<float><<<gr, 256, 0, s>>>((const float*)Qp, (const float*)Kp, (const float*)V,
-                                                (float*)O, LSE, (int64_t)B * H, S, D, scale, causal);
+                                                (float*)O, LSE, kb, H, (int64_t)B * H, S, Spad, D,
+                                                scale, causal);
     GN_LAUNCH_CHECK("gn_attn_fwd");
     return GN_OK;
+}
+
+extern "C" int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O, float* LSE,
+                           int B, int H, int S, int D, float scale, int causal, int rope_mode,
+                           float rope_theta, int dtype, void* ws, size_t ws_bytes, void* stream) {
+    return gn_attn_fwd_mask(Q, K, V, nullptr, O, LSE, B, H, S, D, scale, causal, rope_mode,
+                            rope_theta, dtype, ws, ws_bytes, stream);
 }

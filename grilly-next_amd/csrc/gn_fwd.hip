@@ -16,7 +16,9 @@ constexpr int kFwdWaves = 4;  // rows per 256-thread block on the register path
 
 // MODE 0 = LayerNorm (fnn-layernorm.glsl:44-102: mean, biased variance, (x-mean)/sqrt(var+eps)
 // * gamma + beta), MODE 1 = RMSNorm (rms-norm.glsl:34-70: x * rsqrt(mean(x^2)+eps) * w).
-// Row statistics: mean[r] (LayerNorm), stat[r] = rstd, or the variance when save_var.
+// Row statistics: mean[r] (LayerNorm) and stat[r] by `save_var`: 0 = rstd, 1 = the variance
+// (LayerNorm's var_vals) or mean(x^2) (RMSNorm, rms-norm.glsl:52), 2 = sqrt(mean(x^2) + eps)
+// (snn-rmsnorm.glsl:55).
 // TX: x (a residual stream may be fp32); TY: gamma, beta and y.
 template <int MODE, typename TX, typename TY, int NC>
 __global__ __launch_bounds__(64 * kFwdWaves) void norm_fwd_rows(
@@ -61,7 +63,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void norm_fwd_rows(
     const float rs = rsqrtf(var + eps);
     if (lane == 0) {
         if (MODE == 0 && mean) mean[r] = mu;
-        if (stat) stat[r] = (MODE == 0 && save_var) ? var : rs;
+        if (stat) stat[r] = save_var == 1 ? var : save_var == 2 ? sqrtf(var + eps) : rs;
     }
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256) void norm_fwd_generic(
     const float rs = rsqrtf(var + eps);
     if (threadIdx.x == 0) {
         if (MODE == 0 && mean) mean[r] = mu;
-        if (stat) stat[r] = (MODE == 0 && save_var) ? var : rs;
+        if (stat) stat[r] = save_var == 1 ? var : save_var == 2 ? sqrtf(var + eps) : rs;
     }
     for (int f = threadIdx.x; f < F; f += 256) {
         const float x = io<TX>::ld(X, off + f);
@@ -316,15 +318,23 @@ extern "C" int gn_rmsnorm_fwd(const void* X, const void* w, void* Y, float* rstd
     return gn_rmsnorm_fwd_ex(X, dtype, w, Y, dtype, rstd, rows, F, eps, stream);
 }
 
-extern "C" int gn_rmsnorm_fwd_ex(const void* X, int x_dtype, const void* w, void* Y, int y_dtype,
-                                 float* rstd, int rows, int F, float eps, void* stream) {
+extern "C" int gn_rmsnorm_fwd_stat(const void* X, int x_dtype, const void* w, void* Y, int y_dtype,
+                                   float* stat, int rows, int F, float eps, unsigned flags,
+                                   void* stream) {
     clear_error();
     GN_REQUIRE(rows >= 0 && F >= 0, "gn_rmsnorm_fwd: negative size");
     if (rows == 0) return GN_OK;
     GN_REQUIRE(F > 0, "gn_rmsnorm_fwd: F = 0 with %d rows", rows);
     GN_REQUIRE(X && Y, "gn_rmsnorm_fwd: null pointer");
-    return norm_fwd_dispatch<1>(x_dtype, y_dtype, X, w, nullptr, Y, nullptr, rstd, rows, F, eps, 0,
-                                as_stream(stream));
+    const bool meansq = flags & GN_RMS_STAT_MEANSQ, rms = flags & GN_RMS_STAT_RMS;
+    GN_REQUIRE(!(meansq && rms), "gn_rmsnorm_fwd: GN_RMS_STAT_MEANSQ and GN_RMS_STAT_RMS together");
+    return norm_fwd_dispatch<1>(x_dtype, y_dtype, X, w, nullptr, Y, nullptr, stat, rows, F, eps,
+                                meansq ? 1 : rms ? 2 : 0, as_stream(stream));
+}
+
+extern "C" int gn_rmsnorm_fwd_ex(const void* X, int x_dtype, const void* w, void* Y, int y_dtype,
+                                 float* rstd, int rows, int F, float eps, void* stream) {
+    return gn_rmsnorm_fwd_stat(X, x_dtype, w, Y, y_dtype, rstd, rows, F, eps, 0, stream);
 }
 
 extern "C" int gn_glu_fwd(int kind, const void* gate, const void* up, void* out, int64_t n,

@@ -39,6 +39,13 @@ template <> struct raw8<bf16_t> {
     }
 };
 
+// The saved per-row statistic as the row's 1/sqrt(var + eps): kind 0 = rstd itself; 1 = the
+// variance (LayerNorm, fnn-layernorm.glsl:77 var_vals) or mean(x^2) (RMSNorm, rms-norm.glsl:52),
+// plus eps; 2 = sqrt(mean(x^2) + eps) (snn-rmsnorm.glsl:55).
+__device__ __forceinline__ float stat_rstd(float s, int kind, float eps) {
+    return kind == 1 ? rsqrtf(s + eps) : kind == 2 ? 1.0f / s : s;
+}
+
 // One wave per row; lane l owns 8-element chunks c = l + 64 j (j < NC).  Each wave walks
 // rows r, r + stride, ... and requests row r + stride before it works on row r.  gamma / w
 // stays in registers.  Parameter-gradient partials live in LDS, one row per wave (each wave
@@ -52,7 +59,7 @@ template <int MODE, typename TX, typename TY, int NC>
 __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
     const TY* __restrict__ dY, const TX* __restrict__ X, const TY* __restrict__ gamma,
     const float* __restrict__ mean, const float* __restrict__ rstd, TX* dX, const TX* add,
-    float* __restrict__ part, int rows, int F, float eps, int stat_is_var) {
+    float* __restrict__ part, int rows, int F, float eps, int stat_kind) {
     constexpr int NP = MODE == 0 ? 2 : 1;
     extern __shared__ float red[];  // [kNormWaves][NP][F]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -107,7 +114,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
             load_row(rn, xn, dyn);
         }
         const size_t off = (size_t)r * F;
-        if (MODE == 0 && stat_is_var) rs = rsqrtf(rs + eps);
+        rs = stat_rstd(rs, stat_kind, eps);
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int j = 0; j < NC; ++j)
@@ -216,17 +223,12 @@ template <int MODE, typename TX, typename TY>
 __global__ __launch_bounds__(256) void norm_bwd_generic_dx(
     const TY* __restrict__ dY, const TX* __restrict__ X, const TY* __restrict__ gamma,
     const float* __restrict__ mean, const float* __restrict__ rstd, TX* dX, const TX* add, int F,
-    float eps, int stat_is_var) {
+    float eps, int stat_kind) {
     __shared__ float sh[4];
     const int r = blockIdx.x;
     const size_t off = (size_t)r * F;
-    float mu = 0.f, rs;
-    if (MODE == 0) {
-        mu = mean[r];
-        rs = stat_is_var ? rsqrtf(rstd[r] + eps) : rstd[r];
-    } else {
-        rs = rstd[r];
-    }
+    const float mu = MODE == 0 ? mean[r] : 0.f;
+    const float rs = stat_rstd(rstd[r], stat_kind, eps);
     float s1 = 0.f, s2 = 0.f;
     for (int f = threadIdx.x; f < F; f += 256) {
         float x = io<TX>::ld(X, off + f), dy = io<TY>::ld(dY, off + f), g = io<TY>::ld(gamma, f);
@@ -260,18 +262,18 @@ template <int MODE, typename TX, typename TY>
 __global__ __launch_bounds__(256) void norm_bwd_generic_param(
     const TY* __restrict__ dY, const TX* __restrict__ X, const float* __restrict__ mean,
     const float* __restrict__ rstd, float* __restrict__ dA, float* __restrict__ dB, int rows,
-    int F, float eps, int stat_is_var, int accumulate) {
+    int F, float eps, int stat_kind, int accumulate) {
     const int f = blockIdx.x * 256 + threadIdx.x;
     if (f >= F) return;
     float sa = 0.f, sb = 0.f;
     for (int r = 0; r < rows; ++r) {
         float x = io<TX>::ld(X, (size_t)r * F + f), dy = io<TY>::ld(dY, (size_t)r * F + f);
+        const float rs = stat_rstd(rstd[r], stat_kind, eps);
         if (MODE == 0) {
-            float rs = stat_is_var ? rsqrtf(rstd[r] + eps) : rstd[r];
             sa += dy * (x - mean[r]) * rs;
             sb += dy;
         } else {
-            sa += dy * x * rstd[r];
+            sa += dy * x * rs;
         }
     }
     if (dA) dA[f] = accumulate ? dA[f] + sa : sa;
@@ -611,17 +613,27 @@ extern "C" int gn_rmsnorm_bwd(const void* dY, const void* X, const void* w, cons
                                 as_stream(stream));
 }
 
+extern "C" int gn_rmsnorm_bwd_stat(const void* dY, int dy_dtype, const void* X, int x_dtype,
+                                   const void* w, const float* stat, const void* dX_add, void* dX,
+                                   float* dW, int rows, int F, float eps, unsigned flags, void* ws,
+                                   size_t ws_bytes, void* stream) {
+    clear_error();
+    GN_REQUIRE(rows >= 0 && F > 0, "gn_rmsnorm_bwd: bad shape rows=%d F=%d", rows, F);
+    if (rows == 0) return GN_OK;
+    GN_REQUIRE(dY && X && w && stat && dX, "gn_rmsnorm_bwd: null pointer");
+    const bool meansq = flags & GN_RMS_STAT_MEANSQ, rms = flags & GN_RMS_STAT_RMS;
+    GN_REQUIRE(!(meansq && rms), "gn_rmsnorm_bwd: GN_RMS_STAT_MEANSQ and GN_RMS_STAT_RMS together");
+    return norm_bwd_dispatch<1>("gn_rmsnorm_bwd", dy_dtype, x_dtype, dY, X, w, nullptr, stat, dX,
+                                dX_add, dW, nullptr, rows, F, eps, meansq ? 1 : rms ? 2 : 0,
+                                flags & GN_ACCUMULATE, ws, ws_bytes, as_stream(stream));
+}
+
 extern "C" int gn_rmsnorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype,
                                  const void* w, const float* rstd, const void* dX_add, void* dX,
                                  float* dW, int rows, int F, unsigned flags, void* ws,
                                  size_t ws_bytes, void* stream) {
-    clear_error();
-    GN_REQUIRE(rows >= 0 && F > 0, "gn_rmsnorm_bwd_ex: bad shape rows=%d F=%d", rows, F);
-    if (rows == 0) return GN_OK;
-    GN_REQUIRE(dY && X && w && rstd && dX, "gn_rmsnorm_bwd_ex: null pointer");
-    return norm_bwd_dispatch<1>("gn_rmsnorm_bwd_ex", dy_dtype, x_dtype, dY, X, w, nullptr, rstd, dX,
-                                dX_add, dW, nullptr, rows, F, 0.f, 0, flags & GN_ACCUMULATE, ws,
-                                ws_bytes, as_stream(stream));
+    return gn_rmsnorm_bwd_stat(dY, dy_dtype, X, x_dtype, w, rstd, dX_add, dX, dW, rows, F, 0.f,
+                               flags & GN_ACCUMULATE, ws, ws_bytes, stream);
 }
 
 extern "C" int gn_softmax_bwd(const void* dY, const void* Y, void* dX, int rows, int C,

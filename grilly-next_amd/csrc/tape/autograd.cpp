@@ -326,10 +326,15 @@ void BackwardEngine::bwd_layernorm(Node* n) {
     if (beta) contribute(beta, dB, 0, F, true);
 }
 
-// saved: [0] w, [1] rstd (fp32 per row); dtypes as LayerNorm
+// saved: [0] w, [1] the per-row statistic (fp32; rstd unless RMSNormParams names another
+// form); dtypes as LayerNorm
 void BackwardEngine::bwd_rmsnorm(Node* n) {
     const TensorRef& x = n->inputs[0];
     const int rows = (int)x.rows(), F = (int)x.last();
+    RMSNormParams p = params_of<RMSNormParams>(n);
+    if (p.eps == 0.f) p.eps = 1e-6f;
+    if (p.stat_kind > 2) throw std::invalid_argument("RMSNorm: stat_kind must be 0, 1 or 2");
+    const unsigned stat_flag = p.stat_kind == 1 ? GN_RMS_STAT_MEANSQ : p.stat_kind == 2 ? GN_RMS_STAT_RMS : 0u;
     const uint64_t w = n->saved_buffer_ids[0], rstd = n->saved_buffer_ids[1];
     if (!w || !rstd) throw std::invalid_argument("RMSNorm: saved w/rstd missing");
     const int xdt = gn_dtype(x.dtype, "RMSNorm");
@@ -339,8 +344,9 @@ void BackwardEngine::bwd_rmsnorm(Node* n) {
     uint64_t dW = alloc_grad((size_t)F * 4);
     const size_t wsb = gn_norm_workspace_bytes(rows, F);
     uint64_t ws = alloc_grad(wsb);
-    gn_call(gn_rmsnorm_bwd_ex(gout(n), ydt, P(x.buffer_id), xdt, P(w), (const float*)P(rstd), add,
-                              P(dX), (float*)P(dW), rows, F, 0, P(ws), wsb, dev_.stream()),
+    gn_call(gn_rmsnorm_bwd_stat(gout(n), ydt, P(x.buffer_id), xdt, P(w), (const float*)P(rstd), add,
+                                P(dX), (float*)P(dW), rows, F, p.eps, stat_flag, P(ws), wsb,
+                                dev_.stream()),
             "RMSNorm backward");
     stats_.shaders_dispatched += 2;
     if (x.requires_grad) n->grad_input_buffers[0] = dX;
@@ -350,6 +356,16 @@ void BackwardEngine::bwd_rmsnorm(Node* n) {
 // layout 0: inputs Q, K, V [B, H, S, D]; outputs[0] = O; saved[0] = LSE fp32 [B*H*S].
 // layout 1: inputs[0] = fused QKV [B, S, 3*H*D]; outputs[0] = O [B, S, H*D]; the gradient
 // of the fused buffer comes back in one [B, S, 3*H*D] buffer (dQ | dK | dV per row).
+// An optional last input (inputs[3] in layout 0, inputs[1] in layout 1) is the reference's
+// key-padding mask, fp32 [B, S] (flash-attention2.glsl:150-154); it gets no gradient.
+static const float* attention_mask(const Node* n, uint32_t slot, int B, int S) {
+    if (n->num_inputs <= slot || n->inputs[slot].buffer_id == 0) return nullptr;
+    const TensorRef& m = n->inputs[slot];
+    if (m.dtype != 0 || m.numel() != (uint64_t)B * S)
+        throw std::invalid_argument("FlashAttention2: the key mask must be fp32 [B, S]");
+    return static_cast<const float*>(P(m.buffer_id));
+}
+
 void BackwardEngine::bwd_attention(Node* n) {
     AttentionParams pa = params_of<AttentionParams>(n);
     if (pa.layout == 1) {
@@ -372,11 +388,13 @@ void BackwardEngine::bwd_attention(Node* n) {
         uint64_t ws = alloc_grad(wsb);
         const char* base = static_cast<const char*>(P(qkv.buffer_id));
         char* gbase = static_cast<char*>(P(dqkv));
-        gn_call(gn_attn_bwd_bshd(base, base + HD * es, base + 2 * HD * es, P(o.buffer_id), gout(n),
-                                 (const float*)P(lse), gbase, gbase + HD * es, gbase + 2 * HD * es,
-                                 B, H, S, D, C3, HD, C3, scale, (int)pa.causal, (int)pa.rope_mode,
-                                 theta, gn_dtype(qkv.dtype, "FlashAttention2"), P(ws), wsb,
-                                 dev_.stream()), "attention backward (fused QKV)");
+        const float* mask = attention_mask(n, 1, B, S);
+        gn_call(gn_attn_bwd_bshd_mask(base, base + HD * es, base + 2 * HD * es, P(o.buffer_id),
+                                      gout(n), (const float*)P(lse), mask, gbase, gbase + HD * es,
+                                      gbase + 2 * HD * es, B, H, S, D, C3, HD, C3, scale,
+                                      (int)pa.causal, (int)pa.rope_mode, theta,
+                                      gn_dtype(qkv.dtype, "FlashAttention2"), P(ws), wsb,
+                                      dev_.stream()), "attention backward (fused QKV)");
         stats_.shaders_dispatched += 3;
         n->grad_input_buffers[0] = dqkv;
         return;
@@ -395,10 +413,12 @@ void BackwardEngine::bwd_attention(Node* n) {
     uint64_t dQ = alloc_grad(q.size_bytes()), dK = alloc_grad(k.size_bytes()), dV = alloc_grad(v.size_bytes());
     const size_t wsb = gn_attn_workspace_bytes(B, H, S, D);
     uint64_t ws = alloc_grad(wsb);
-    gn_call(gn_attn_bwd(P(q.buffer_id), P(k.buffer_id), P(v.buffer_id), P(n->outputs[0].buffer_id),
-                        gout(n), (const float*)P(lse), P(dQ), P(dK), P(dV), B, H, S, D, scale,
-                        (int)p.causal, (int)p.rope_mode, theta, gn_dtype(q.dtype, "FlashAttention2"),
-                        P(ws), wsb, dev_.stream()), "attention backward");
+    const float* mask = attention_mask(n, 3, B, S);
+    gn_call(gn_attn_bwd_mask(P(q.buffer_id), P(k.buffer_id), P(v.buffer_id),
+                             P(n->outputs[0].buffer_id), gout(n), (const float*)P(lse), mask,
+                             P(dQ), P(dK), P(dV), B, H, S, D, scale, (int)p.causal,
+                             (int)p.rope_mode, theta, gn_dtype(q.dtype, "FlashAttention2"), P(ws),
+                             wsb, dev_.stream()), "attention backward");
     stats_.shaders_dispatched += 3;
     n->grad_input_buffers[0] = dQ;
     n->grad_input_buffers[1] = dK;

@@ -93,6 +93,10 @@ struct VSACosineBlendLossParams {
 // Parameter blocks for the handlers this build adds (all optional: zeros mean defaults).
 struct GELUParams { uint32_t erf_form; };                     // 0 = tanh form (GLSL)
 struct LayerNormParams { float eps; uint32_t stat_is_var; };  // eps default 1e-5
+// RMSNorm: the saved per-row statistic (saved slot 1) is 0 = rstd, 1 = mean(x^2) as
+// rms-norm.glsl:52 saves it, 2 = sqrt(mean(x^2) + eps) as snn-rmsnorm.glsl:55 saves it;
+// eps (default 1e-6) is used by form 1 only.
+struct RMSNormParams { float eps; uint32_t stat_kind; };
 struct AttentionParams {
     float scale;        // 0 -> 1/sqrt(D)
     uint32_t causal;    // 1 = causal mask j <= i

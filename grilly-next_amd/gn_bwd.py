@@ -17,7 +17,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libgn_bwd.so")
 
 F32, F16, U32, I32, BF16 = 0, 1, 2, 3, 4
-ACCUMULATE, LN_STAT_VAR, NO_GUMBEL = 1, 2, 4
+ACCUMULATE, LN_STAT_VAR, NO_GUMBEL, RMS_STAT_MEANSQ, RMS_STAT_RMS = 1, 2, 4, 8, 16
+RMS_STAT = {"rstd": 0, "meansq": RMS_STAT_MEANSQ, "rms": RMS_STAT_RMS}
 ACT = {"relu": 0, "gelu_tanh": 1, "gelu_erf": 2, "silu": 3, "tanh": 4, "sigmoid": 5}
 GLU = {"swiglu_up": 0, "swiglu_gate": 1, "geglu_up": 2, "geglu_gate": 3, "reglu_up": 4}
 ROPE = {"none": 0, "interleaved": 1, "half": 2}
@@ -28,13 +29,14 @@ SYMBOLS = [
     "gn_gemm", "gn_colsum", "gn_act_bwd", "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_linear_bwd_ws",
     "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd",
     "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
-    "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
-    "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_vsa_unpack_project_bwd",
+    "gn_rmsnorm_bwd_stat", "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
+    "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_attn_fwd_mask",
+    "gn_attn_bwd_mask", "gn_attn_bwd_bshd_mask", "gn_vsa_unpack_project_bwd",
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_vsa_unpack_project_fwd",
     "gn_vsa_fwd_workspace_bytes", "gn_vsa_surrogate_fwd", "gn_embedding_bwd", "gn_binary_bwd",
     "gn_reduce_bwd", "gn_transpose_bwd", "gn_mse_bwd", "gn_vsa_lora_expand_bwd",
     "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_layernorm_fwd",
-    "gn_rmsnorm_fwd", "gn_layernorm_fwd_ex", "gn_rmsnorm_fwd_ex", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace", "gn_convert", "gn_zero",
+    "gn_rmsnorm_fwd", "gn_layernorm_fwd_ex", "gn_rmsnorm_fwd_ex", "gn_rmsnorm_fwd_stat", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace", "gn_convert", "gn_zero",
 ]
 BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
 RED = {"sum": 0, "mean": 1}
@@ -85,8 +87,10 @@ _SIGS = {
     "gn_layernorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _U, _P, _Z,
                              _P], _I),
     "gn_rmsnorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _U, _P, _Z, _P], _I),
+    "gn_rmsnorm_bwd_stat": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _F, _U, _P, _Z, _P], _I),
     "gn_layernorm_fwd_ex": ([_P, _I, _P, _P, _P, _I, _P, _P, _I, _I, _F, _U, _P], _I),
     "gn_rmsnorm_fwd_ex": ([_P, _I, _P, _P, _I, _P, _I, _I, _F, _P], _I),
+    "gn_rmsnorm_fwd_stat": ([_P, _I, _P, _P, _I, _P, _I, _I, _F, _U, _P], _I),
     "gn_convert": ([_P, _I, _P, _I, _L, _P], _I),
     "gn_zero": ([_P, _L, _P], _I),
     "gn_norm_workspace_bytes": ([_I, _I], _Z),
@@ -98,6 +102,12 @@ _SIGS = {
     "gn_attn_bwd_bshd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _F, _I,
                           _I, _F, _I, _P, _Z, _P], _I),
     "gn_attn_fwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P, _Z, _P], _I),
+    "gn_attn_fwd_mask": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P, _Z,
+                          _P], _I),
+    "gn_attn_bwd_mask": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F,
+                          _I, _P, _Z, _P], _I),
+    "gn_attn_bwd_bshd_mask": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _L, _L, _L,
+                               _F, _I, _I, _F, _I, _P, _Z, _P], _I),
     "gn_vsa_unpack_project_bwd": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _U, _P, _Z, _P], _I),
     "gn_vsa_workspace_bytes": ([_I, _I], _Z),
     "gn_vsa_surrogate_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F, _U, _P], _I),
@@ -349,14 +359,23 @@ def layernorm_bwd(dY, X, gamma, mean, rstd, eps=1e-5, stat_is_var=False, ws=None
     return dX, dG, dB
 
 
-def rmsnorm_bwd(dY, X, w, rstd, ws=None, need_param=True, dX=None, dW=None, dX_add=None):
+def rmsnorm_bwd(dY, X, w, rstd, ws=None, need_param=True, dX=None, dW=None, dX_add=None,
+                stat="rstd", eps=1e-6):
+    """(dX, dW).  `rstd` holds the per-row statistic named by `stat`: "rstd", "meansq"
+    (mean(x^2), rms-norm.glsl:52; eps added) or "rms" (sqrt(mean(x^2) + eps),
+    snn-rmsnorm.glsl:55)."""
     rows, F = X.shape
     dX = torch.empty_like(X) if dX is None else dX
     if need_param and dW is None:
         dW = torch.empty((F,), dtype=torch.float32, device=X.device)
     if ws is None:
         ws = workspace(norm_workspace_bytes(rows, F), X.device)
-    if dX_add is None and dY.dtype == X.dtype:
+    if stat != "rstd":
+        _check(lib().gn_rmsnorm_bwd_stat(_ptr(dY), _dt(dY), _ptr(X), _dt(X), _ptr(w), _ptr(rstd),
+                                         _ptr(dX_add), _ptr(dX), _ptr(dW) if need_param else None,
+                                         rows, F, eps, RMS_STAT[stat], _ptr(ws), ws.numel(),
+                                         _stream()), "gn_rmsnorm_bwd_stat")
+    elif dX_add is None and dY.dtype == X.dtype:
         _check(lib().gn_rmsnorm_bwd(_ptr(dY), _ptr(X), _ptr(w), _ptr(rstd), _ptr(dX),
                                     _ptr(dW) if need_param else None, rows, F, _dt(X), 0, _ptr(ws),
                                     ws.numel(), _stream()), "gn_rmsnorm_bwd")
@@ -406,23 +425,31 @@ def attn_workspace_bytes(B, H, S, D):
 
 
 def attn_bwd(Q, K, V, O, dO, LSE, scale=None, causal=True, rope="interleaved", theta=10000.0,
-             ws=None, out=None):
+             ws=None, out=None, mask=None):
+    """(dQ, dK, dV).  mask: fp32 [B, S] key-padding mask (1 keep, 0 masked), or None."""
     B, H, S, D = Q.shape
     scale = D ** -0.5 if scale is None else scale
     dQ, dK, dV = out if out is not None else (torch.empty_like(Q), torch.empty_like(K),
                                               torch.empty_like(V))
     if ws is None:
         ws = workspace(attn_workspace_bytes(B, H, S, D), Q.device)
-    _check(lib().gn_attn_bwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(LSE), _ptr(dQ),
-                             _ptr(dK), _ptr(dV), B, H, S, D, scale, int(causal), ROPE[rope],
-                             theta, _dt(Q), _ptr(ws), ws.numel(), _stream()), "gn_attn_bwd")
+    if mask is None:
+        _check(lib().gn_attn_bwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(LSE), _ptr(dQ),
+                                 _ptr(dK), _ptr(dV), B, H, S, D, scale, int(causal), ROPE[rope],
+                                 theta, _dt(Q), _ptr(ws), ws.numel(), _stream()), "gn_attn_bwd")
+    else:
+        _check(lib().gn_attn_bwd_mask(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(LSE),
+                                      _ptr(mask), _ptr(dQ), _ptr(dK), _ptr(dV), B, H, S, D, scale,
+                                      int(causal), ROPE[rope], theta, _dt(Q), _ptr(ws), ws.numel(),
+                                      _stream()), "gn_attn_bwd_mask")
     return dQ, dK, dV
 
 
 def attn_bwd_qkv(qkv, O, dO, LSE, heads, scale=None, causal=True, rope="none", theta=10000.0,
-                 ws=None, out=None):
+                 ws=None, out=None, mask=None):
     """Backward on a fused QKV projection output qkv [B, S, 3*H*D] (Q | K | V along the last
-    axis, each [B, S, H, D]); O, dO [B, S, H*D]; LSE [B, H, S].  Returns dqkv like qkv."""
+    axis, each [B, S, H, D]); O, dO [B, S, H*D]; LSE [B, H, S]; mask: fp32 [B, S] key-padding
+    mask or None.  Returns dqkv like qkv."""
     B, S, C3 = qkv.shape
     D = C3 // (3 * heads)
     HD = heads * D
@@ -431,24 +458,27 @@ def attn_bwd_qkv(qkv, O, dO, LSE, heads, scale=None, causal=True, rope="none", t
     if ws is None:
         ws = workspace(attn_workspace_bytes(B, heads, S, D), qkv.device)
     e = qkv.element_size()
-    _check(lib().gn_attn_bwd_bshd(_ptr(qkv), _off(qkv, HD * e), _off(qkv, 2 * HD * e), _ptr(O),
-                                  _ptr(dO), _ptr(LSE), _ptr(dqkv), _off(dqkv, HD * e),
-                                  _off(dqkv, 2 * HD * e), B, heads, S, D, C3, O.shape[-1], C3,
-                                  scale, int(causal), ROPE[rope], theta, _dt(qkv), _ptr(ws),
-                                  ws.numel(), _stream()), "gn_attn_bwd_bshd")
+    _check(lib().gn_attn_bwd_bshd_mask(_ptr(qkv), _off(qkv, HD * e), _off(qkv, 2 * HD * e),
+                                       _ptr(O), _ptr(dO), _ptr(LSE), _ptr(mask), _ptr(dqkv),
+                                       _off(dqkv, HD * e), _off(dqkv, 2 * HD * e), B, heads, S, D,
+                                       C3, O.shape[-1], C3, scale, int(causal), ROPE[rope], theta,
+                                       _dt(qkv), _ptr(ws), ws.numel(), _stream()),
+           "gn_attn_bwd_bshd")
     return dqkv
 
 
-def attn_fwd(Q, K, V, scale=None, causal=True, rope="interleaved", theta=10000.0, ws=None):
+def attn_fwd(Q, K, V, scale=None, causal=True, rope="interleaved", theta=10000.0, ws=None,
+             mask=None):
+    """(O, LSE).  mask: fp32 [B, S] key-padding mask (1 keep, 0 masked), or None."""
     B, H, S, D = Q.shape
     scale = D ** -0.5 if scale is None else scale
     O = torch.empty_like(Q)
     LSE = torch.empty((B, H, S), dtype=torch.float32, device=Q.device)
     if ws is None:
         ws = workspace(attn_workspace_bytes(B, H, S, D), Q.device)
-    _check(lib().gn_attn_fwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(LSE), B, H, S, D, scale,
-                             int(causal), ROPE[rope], theta, _dt(Q), _ptr(ws), ws.numel(),
-                             _stream()), "gn_attn_fwd")
+    _check(lib().gn_attn_fwd_mask(_ptr(Q), _ptr(K), _ptr(V), _ptr(mask), _ptr(O), _ptr(LSE), B,
+                                  H, S, D, scale, int(causal), ROPE[rope], theta, _dt(Q), _ptr(ws),
+                                  ws.numel(), _stream()), "gn_attn_fwd")
     return O, LSE
 
 
@@ -661,13 +691,14 @@ def layernorm_fwd(X, gamma=None, beta=None, eps=1e-5, save_var=False, out_dtype=
     return Y, mean, rstd
 
 
-def rmsnorm_fwd(X, w=None, eps=1e-6, out_dtype=None):
-    """Y, rstd (fp32 [rows])."""
+def rmsnorm_fwd(X, w=None, eps=1e-6, out_dtype=None, stat="rstd"):
+    """Y, and the per-row statistic named by `stat` (fp32 [rows]): "rstd", "meansq" or "rms"
+    (the reference's saved forms, as rmsnorm_bwd takes them)."""
     rows, F = X.shape
     Y = torch.empty(X.shape, dtype=out_dtype or X.dtype, device=X.device)
     rstd = torch.empty((rows,), dtype=torch.float32, device=X.device)
-    _check(lib().gn_rmsnorm_fwd_ex(_ptr(X), _dt(X), _ptr(w), _ptr(Y), _dt(Y), _ptr(rstd), rows, F,
-                                   eps, _stream()), "gn_rmsnorm_fwd")
+    _check(lib().gn_rmsnorm_fwd_stat(_ptr(X), _dt(X), _ptr(w), _ptr(Y), _dt(Y), _ptr(rstd), rows,
+                                     F, eps, RMS_STAT[stat], _stream()), "gn_rmsnorm_fwd")
     return Y, rstd
 
 

@@ -68,6 +68,13 @@ def layernorm_params(eps: float = 1e-5, stat_is_var: bool = False) -> bytes:
     return struct.pack("<fI", eps, int(stat_is_var))
 
 
+def rmsnorm_params(eps: float = 1e-6, stat: str = "rstd") -> bytes:
+    """RMSNormParams: which per-row statistic saved slot 1 holds: "rstd", "meansq" (mean(x^2),
+    rms-norm.glsl:52; eps added in the backward) or "rms" (sqrt(mean(x^2) + eps),
+    snn-rmsnorm.glsl:55)."""
+    return struct.pack("<fI", eps, {"rstd": 0, "meansq": 1, "rms": 2}[stat])
+
+
 def attention_params(scale: float = 0.0, causal: bool = True, rope: str = "interleaved",
                      theta: float = 10000.0, fused_qkv_heads: int = 0) -> bytes:
     """AttentionParams.  fused_qkv_heads = H > 0 selects the fused layout: inputs[0] is the

@@ -50,6 +50,8 @@ extern "C" {
 #define GN_ACCUMULATE 1u  /* add into existing gradients (fan-out) instead of overwriting */
 #define GN_LN_STAT_VAR 2u /* layernorm: `rstd` argument holds the biased variance */
 #define GN_NO_GUMBEL 4u   /* surrogate forward: top-2 of the plain dot products (no noise) */
+#define GN_RMS_STAT_MEANSQ 8u /* rmsnorm: the statistic is mean(x^2) (rms-norm.glsl:52); eps added */
+#define GN_RMS_STAT_RMS 16u   /* rmsnorm: the statistic is sqrt(mean(x^2)+eps) (snn-rmsnorm.glsl:55) */
 
 /* ---- activation kinds (gn_act_bwd) ------------------------------------------------- */
 #define GN_ACT_RELU 0      /* dx = dy*[x>0]            activation-relu-backward.glsl:33-37 */
@@ -216,6 +218,17 @@ int gn_rmsnorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype, 
                       const float* rstd, const void* dX_add, void* dX, float* dW, int rows,
                       int F, unsigned flags, void* ws, size_t ws_bytes, void* stream);
 
+/* gn_rmsnorm_bwd_ex for a forward that saved another per-row statistic than rstd: the
+ * reference's rms-norm.glsl:52 leaves mean(x^2) in its rms_vals buffer (flag
+ * GN_RMS_STAT_MEANSQ: r = rsqrt(stat + eps)) and snn-rmsnorm.glsl:55 leaves sqrt(mean(x^2) +
+ * eps) (flag GN_RMS_STAT_RMS: r = 1/stat); with neither flag `stat` is rstd and eps is unused.
+ * Same replaced interface as gn_rmsnorm_bwd (no RMSNorm handler in the reference,
+ * autograd.cpp:126-128). */
+int gn_rmsnorm_bwd_stat(const void* dY, int dy_dtype, const void* X, int x_dtype, const void* w,
+                        const float* stat, const void* dX_add, void* dX, float* dW, int rows,
+                        int F, float eps, unsigned flags, void* ws, size_t ws_bytes,
+                        void* stream);
+
 /* ---- softmax / cross-entropy --------------------------------------------------------- */
 /* activation-softmax-backward.glsl:27-49: dX = Y * (dY - sum_c dY*Y), per row of C. */
 int gn_softmax_bwd(const void* dY, const void* Y, void* dX, int rows, int C, int dtype,
@@ -259,10 +272,32 @@ int gn_attn_bwd_bshd(const void* Q, const void* K, const void* V, const void* O,
 /* Attention forward producing the saved-tensor contract of the backward (O and the fp32
  * row logsumexp; flash-attention2-rope.glsl:165-247 semantics plus the causal mask).
  * Same arguments as gn_attn_bwd; ws as sized by gn_attn_workspace_bytes (needed only
- * when rope_mode != GN_ROPE_NONE). */
+ * when rope_mode != GN_ROPE_NONE or a key mask is given). */
 int gn_attn_fwd(const void* Q, const void* K, const void* V, void* O, float* LSE, int B,
                 int H, int S, int D, float scale, int causal, int rope_mode,
                 float rope_theta, int dtype, void* ws, size_t ws_bytes, void* stream);
+
+/* The three attention entries above with the reference's key-padding mask
+ * (flash-attention2.glsl:150-154, flash-attention2-rope.glsl:201-205, bound with its mask by
+ * flash_attention2 in cpp/python/bindings.cpp:415-450): key_mask fp32 [B, S], 1.0 = keep,
+ * 0.0 = masked; the score of key k in batch b gets (key_mask[b*S + k] - 1) * 1e9, applied as
+ * -inf where that bias is below -1e4 (so a masked key has P = dS = 0 exactly).  A row whose
+ * visible keys are all masked gets O = 0, LSE = -inf and zero gradients (the reference's fp32
+ * forward averages such a row uniformly instead).  key_mask NULL: no mask (the entries
+ * above).  ws: gn_attn_workspace_bytes(B, H, S, D), 16-byte aligned. */
+int gn_attn_fwd_mask(const void* Q, const void* K, const void* V, const float* key_mask, void* O,
+                     float* LSE, int B, int H, int S, int D, float scale, int causal,
+                     int rope_mode, float rope_theta, int dtype, void* ws, size_t ws_bytes,
+                     void* stream);
+int gn_attn_bwd_mask(const void* Q, const void* K, const void* V, const void* O, const void* dO,
+                     const float* LSE, const float* key_mask, void* dQ, void* dK, void* dV, int B,
+                     int H, int S, int D, float scale, int causal, int rope_mode,
+                     float rope_theta, int dtype, void* ws, size_t ws_bytes, void* stream);
+int gn_attn_bwd_bshd_mask(const void* Q, const void* K, const void* V, const void* O,
+                          const void* dO, const float* LSE, const float* key_mask, void* dQ,
+                          void* dK, void* dV, int B, int H, int S, int D, int64_t ld_qkv,
+                          int64_t ld_o, int64_t ld_dqkv, float scale, int causal, int rope_mode,
+                          float rope_theta, int dtype, void* ws, size_t ws_bytes, void* stream);
 
 /* ---- VSA ------------------------------------------------------------------------------ */
 /* backward_vsa_unpack_project (autograd.cpp:727-815), vsa-unpack-project-backward.glsl:42-74:
@@ -437,6 +472,11 @@ int gn_layernorm_fwd_ex(const void* X, int x_dtype, const void* gamma, const voi
                         unsigned flags, void* stream);
 int gn_rmsnorm_fwd_ex(const void* X, int x_dtype, const void* w, void* Y, int y_dtype, float* rstd,
                       int rows, int F, float eps, void* stream);
+/* gn_rmsnorm_fwd_ex saving the statistic in the reference's forms: GN_RMS_STAT_MEANSQ writes
+ * mean(x^2) (rms-norm.glsl:52), GN_RMS_STAT_RMS writes sqrt(mean(x^2) + eps)
+ * (snn-rmsnorm.glsl:55), neither writes rstd.  Feeds gn_rmsnorm_bwd_stat with the same flag. */
+int gn_rmsnorm_fwd_stat(const void* X, int x_dtype, const void* w, void* Y, int y_dtype,
+                        float* stat, int rows, int F, float eps, unsigned flags, void* stream);
 
 /* Activation forward Y = act(X) over n elements (activation-{relu,gelu,silu}.glsl forward
  * values; the GN_ACT_* kinds: tanh-form GELU by default, erf form, SiLU, tanh, sigmoid).  The

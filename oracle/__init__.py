@@ -217,21 +217,31 @@ def rope(X, mode="interleaved", theta=10000.0, inverse=False):
     return X
 
 
-def attn_fwd(Q, K, V, scale=None, causal=True, rope_mode="interleaved", theta=10000.0):
+def _mask_arg(mask, B, S):
+    """fp32 [B, S] key-padding mask (flash-attention2.glsl:150-154) as a pointer, or None."""
+    if mask is None:
+        return None, None
+    m, pm = _f(np.asarray(mask, dtype=np.float32).reshape(B, S))
+    return m, pm
+
+
+def attn_fwd(Q, K, V, scale=None, causal=True, rope_mode="interleaved", theta=10000.0,
+             mask=None):
     B, H, S, D = Q.shape
     scale = 1.0 / np.sqrt(D) if scale is None else scale
     Q, pq = _f(Q)
     K, pk = _f(K)
     V, pv = _f(V)
+    m, pm = _mask_arg(mask, B, S)
     O, po = _out((B, H, S, D))
     LSE, pl = _out((B, H, S))
     lib().or_attn_fwd(pq, pk, pv, po, pl, B, H, S, D, ctypes.c_float(scale), int(causal),
-                      ROPE[rope_mode], ctypes.c_float(theta))
+                      ROPE[rope_mode], ctypes.c_float(theta), pm)
     return O, LSE
 
 
 def attn_bwd(Q, K, V, dO, LSE, scale=None, causal=True, rope_mode="interleaved",
-             theta=10000.0):
+             theta=10000.0, mask=None):
     B, H, S, D = Q.shape
     scale = 1.0 / np.sqrt(D) if scale is None else scale
     Q, pq = _f(Q)
@@ -239,11 +249,12 @@ def attn_bwd(Q, K, V, dO, LSE, scale=None, causal=True, rope_mode="interleaved",
     V, pv = _f(V)
     dO, pdo = _f(dO)
     LSE, pl = _f(LSE)
+    m, pm = _mask_arg(mask, B, S)
     dQ, pdq = _out((B, H, S, D))
     dK, pdk = _out((B, H, S, D))
     dV, pdv = _out((B, H, S, D))
     lib().or_attn_bwd(pq, pk, pv, pdo, pl, pdq, pdk, pdv, B, H, S, D, ctypes.c_float(scale),
-                      int(causal), ROPE[rope_mode], ctypes.c_float(theta))
+                      int(causal), ROPE[rope_mode], ctypes.c_float(theta), pm)
     return dQ, dK, dV
 
 

@@ -382,13 +382,22 @@ static void rope_d(double* X, int S, int D, int mode, double theta, int inverse)
 }
 
 /* ---------------------------------------------------------------- attention ------- */
-/* Forward with the saved-tensor contract: O and LSE_i = log sum_j exp(scale q_i.k_j),
- * RoPE applied to Q and K (flash-attention2-rope.glsl:95-148), causal mask j <= i. */
+/* Key-padding bias of flash-attention2.glsl:150-154 (flash-attention2-rope.glsl:201-205):
+ * score += (mask[b*S + k] - 1) * 1e9; 0 without a mask. */
+static double key_bias(const float* mask, int b, int S, int k) {
+    return mask ? ((double)mask[(size_t)b * S + k] - 1.0) * 1e9 : 0.0;
+}
+
+/* Forward with the saved-tensor contract: O and LSE_i = log sum_j exp(scale q_i.k_j + bias_j),
+ * RoPE applied to Q and K (flash-attention2-rope.glsl:95-148), causal mask j <= i, key-padding
+ * bias from `mask` [B, S] (nullable). */
 void or_attn_fwd(const float* Q, const float* K, const float* V, float* O, float* LSE, int B,
-                 int H, int S, int D, float scale, int causal, int rope_mode, float theta) {
+                 int H, int S, int D, float scale, int causal, int rope_mode, float theta,
+                 const float* mask) {
 #pragma omp parallel for schedule(dynamic)
     for (int bh = 0; bh < B * H; ++bh) {
         size_t off = (size_t)bh * S * D;
+        const int b = bh / H;
         double* q = (double*)malloc(sizeof(double) * (size_t)S * D);
         double* k = (double*)malloc(sizeof(double) * (size_t)S * D);
         double* p = (double*)malloc(sizeof(double) * (size_t)S);
@@ -401,7 +410,7 @@ void or_attn_fwd(const float* Q, const float* K, const float* V, float* O, float
             for (int j = 0; j < jn; ++j) {
                 double s = 0.0;
                 for (int d = 0; d < D; ++d) s += q[(size_t)i * D + d] * k[(size_t)j * D + d];
-                p[j] = s * scale;
+                p[j] = s * scale + key_bias(mask, b, S, j);
                 if (p[j] > mx) mx = p[j];
             }
             double sum = 0.0;
@@ -422,10 +431,11 @@ void or_attn_fwd(const float* Q, const float* K, const float* V, float* O, float
  * RoPE: the contraction runs on rotated q, k and dQ, dK are rotated back (R^T). */
 void or_attn_bwd(const float* Q, const float* K, const float* V, const float* dO,
                  const float* LSE, float* dQ, float* dK, float* dV, int B, int H, int S, int D,
-                 float scale, int causal, int rope_mode, float theta) {
+                 float scale, int causal, int rope_mode, float theta, const float* mask) {
 #pragma omp parallel for schedule(dynamic)
     for (int bh = 0; bh < B * H; ++bh) {
         size_t off = (size_t)bh * S * D;
+        const int b = bh / H;
         size_t SD = (size_t)S * D;
         double* q = (double*)malloc(sizeof(double) * SD);
         double* k = (double*)malloc(sizeof(double) * SD);
@@ -446,7 +456,7 @@ void or_attn_bwd(const float* Q, const float* K, const float* V, const float* dO
                     s += q[(size_t)i * D + d] * k[(size_t)j * D + d];
                     t += (double)dO[off + (size_t)i * D + d] * V[off + (size_t)j * D + d];
                 }
-                p[j] = exp(s * scale - lse);
+                p[j] = exp(s * scale + key_bias(mask, b, S, j) - lse);
                 dp[j] = t;
                 rowdot += p[j] * t;
             }

@@ -68,9 +68,10 @@ void or_rope(float* X, int S, int D, int mode, float theta, int inverse);
  * P is recomputed from LSE; D_i = sum_j P_ij dP_ij as in the reference pass 2. */
 void or_attn_bwd(const float* Q, const float* K, const float* V, const float* dO,
                  const float* LSE, float* dQ, float* dK, float* dV, int B, int H, int S, int D,
-                 float scale, int causal, int rope_mode, float theta);
+                 float scale, int causal, int rope_mode, float theta, const float* mask);
 void or_attn_fwd(const float* Q, const float* K, const float* V, float* O, float* LSE, int B,
-                 int H, int S, int D, float scale, int causal, int rope_mode, float theta);
+                 int H, int S, int D, float scale, int causal, int rope_mode, float theta,
+                 const float* mask);
 
 /* vsa-unpack-project-backward.glsl:42-74 */
 void or_unpack_bits(const uint32_t* bits, float* out, int Bn, int D, int words);

@@ -16,6 +16,9 @@ Forward definitions used (reference file:line):
   softmax       softmax over the last axis                      activation-softmax.glsl
   cross-entropy sum over rows of -log softmax[target]           loss-cross-entropy.glsl
   attention     softmax(scale * R(q) R(k)^T, causal) v          flash-attention2-rope.glsl:95-148
+  masked attn   the same with (mask - 1) * 1e9 added per key     flash-attention2.glsl:150-154
+  rmsnorm stats mean(x^2) and sqrt(mean(x^2) + eps) saved          rms-norm.glsl:52,
+                                                                 snn-rmsnorm.glsl:55
   vsa project   y = unpack(bits) W^T + b                        vsa-unpack-project.glsl
   vsa surrogate sum_k w_k mean_i relu(gamma - y_i z_ki) + lambda/D * relu(delta-(dw-dr(z)))
                 vsa-surrogate-loss-forward.glsl / -backward.glsl:56-88
@@ -208,6 +211,47 @@ def gen_attention(rng):
              causal=np.int32(c["causal"]), rope=np.array(c["rope"]), theta=np.float32(theta))
 
 
+def gen_mask_stats(rng):
+    """Key-padding-masked attention (flash-attention2.glsl:150-154: score += (mask - 1) * 1e9)
+    and the RMSNorm statistic forms the reference's forwards save (rms-norm.glsl:52 mean(x^2),
+    snn-rmsnorm.glsl:55 sqrt(mean(x^2) + eps))."""
+    cases = {
+        "mask_causal_rope": dict(B=2, H=2, S=13, D=8, causal=True, rope="interleaved"),
+        "mask_full": dict(B=2, H=1, S=9, D=16, causal=False, rope="none"),
+    }
+    theta = 10000.0
+    for tag, c in cases.items():
+        B, H, S, D = c["B"], c["H"], c["S"], c["D"]
+        scale = 1.0 / np.sqrt(D)
+        Q, K, V, dO = (rng.standard_normal((B, H, S, D)).astype(np.float32) for _ in range(4))
+        mask = np.ones((B, S), np.float32)
+        mask[1, S - 4:] = 0.0  # a padded tail
+        mask[1, 2] = 0.0       # and one key inside the sequence
+        q, k, v = t(Q, True), t(K, True), t(V, True)
+        s = scale * rope_t(q, c["rope"], theta) @ rope_t(k, c["rope"], theta).transpose(-1, -2)
+        s = s + (t(mask)[:, None, None, :] - 1.0) * 1e9
+        if c["causal"]:
+            s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+        lse = torch.logsumexp(s, -1)
+        o = torch.softmax(s, -1) @ v
+        (o * t(dO)).sum().backward()
+        save(f"attn_{tag}", Q=Q, K=K, V=V, dO=dO, mask=mask, O=f32(o), LSE=f32(lse),
+             dQ=f32(q.grad), dK=f32(k.grad), dV=f32(v.grad), scale=np.float32(scale),
+             causal=np.int32(c["causal"]), rope=np.array(c["rope"]), theta=np.float32(theta))
+    rows, F, eps = 9, 48, 1e-5
+    X = rng.standard_normal((rows, F)).astype(np.float32)
+    w = (1 + 0.5 * rng.standard_normal(F)).astype(np.float32)
+    dY = rng.standard_normal((rows, F)).astype(np.float32)
+    x, ww = t(X, True), t(w, True)
+    ms = (x * x).mean(-1, keepdim=True)
+    y = ww * x * torch.rsqrt(ms + eps)
+    (y * t(dY)).sum().backward()
+    ms0 = (t(X) ** 2).mean(-1)
+    save("rmsnorm_stats", X=X, w=w, dY=dY, meansq=f32(ms0), rms=f32(torch.sqrt(ms0 + eps)),
+         rstd=f32(torch.rsqrt(ms0 + eps)), Y=f32(y), dX=f32(x.grad), dW=f32(ww.grad),
+         eps=np.float32(eps))
+
+
 def unpack_t(bits, D):
     b = torch.tensor(bits.astype(np.int64))
     j = torch.arange(D)
@@ -372,6 +416,8 @@ def main(only=()):
         gen_optim(np.random.default_rng(20261202))
     if not only or "tapeops" in only:
         gen_tapeops(np.random.default_rng(20261203))
+    if not only or "mask" in only:
+        gen_mask_stats(np.random.default_rng(20261204))
     print("golden vectors written to", HERE)
 
 

@@ -192,6 +192,50 @@ def test_attention_golden(tag):
     assert rel_err(dV, g["dV"]) < TOL
 
 
+@pytest.mark.parametrize("tag", ["mask_causal_rope", "mask_full"])
+def test_attention_key_mask_golden(tag):
+    """The key-padding bias (mask - 1) * 1e9 of flash-attention2.glsl:150-154, against torch
+    float64 autograd of the masked forward."""
+    g = golden(f"attn_{tag}")
+    kw = dict(scale=float(g["scale"]), causal=bool(g["causal"]), rope_mode=str(g["rope"]),
+              theta=float(g["theta"]), mask=g["mask"])
+    O, LSE = oracle.attn_fwd(g["Q"], g["K"], g["V"], **kw)
+    assert rel_err(O, g["O"]) < TOL and rel_err(LSE, g["LSE"]) < TOL
+    dQ, dK, dV = oracle.attn_bwd(g["Q"], g["K"], g["V"], g["dO"], g["LSE"], **kw)
+    assert rel_err(dQ, g["dQ"]) < TOL
+    assert rel_err(dK, g["dK"]) < TOL
+    assert rel_err(dV, g["dV"]) < TOL
+
+
+def test_attention_key_mask_equals_removing_keys():
+    """Without the causal mask and RoPE, masking keys is attention over the kept keys alone:
+    O, LSE and dQ equal those of the shortened key/value sequence, and the masked keys get
+    dK = dV = 0."""
+    rng = np.random.default_rng(5)
+    B, H, S, D = 1, 2, 12, 8
+    Q, K, V, dO = (rng.standard_normal((B, H, S, D)).astype(np.float32) for _ in range(4))
+    mask = np.ones((B, S), np.float32)
+    drop = [3, 7, 8]
+    mask[0, drop] = 0.0
+    keep = [j for j in range(S) if j not in drop]
+    kw = dict(causal=False, rope_mode="none")
+    O, LSE = oracle.attn_fwd(Q, K, V, mask=mask, **kw)
+    dQ, dK, dV = oracle.attn_bwd(Q, K, V, dO, LSE, mask=mask, **kw)
+    # the shortened problem: queries stay, keys/values are the kept ones (pad queries to the key
+    # count is not needed: the oracle takes equal lengths, so run it per query row block)
+    Kk, Vk = K[:, :, keep], V[:, :, keep]
+    for i in range(S):
+        q = np.ascontiguousarray(np.repeat(Q[:, :, i:i + 1], len(keep), axis=2))
+        g = np.zeros_like(q)
+        g[:, :, 0] = dO[:, :, i]
+        o, l = oracle.attn_fwd(q, Kk, Vk, **kw)
+        np.testing.assert_allclose(o[:, :, 0], O[:, :, i], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(l[:, :, 0], LSE[:, :, i], rtol=1e-6, atol=1e-6)
+        dq, _, _ = oracle.attn_bwd(q, Kk, Vk, g, l, **kw)
+        np.testing.assert_allclose(dq[:, :, 0], dQ[:, :, i], rtol=1e-4, atol=1e-6)
+    assert np.all(dK[:, :, drop] == 0.0) and np.all(dV[:, :, drop] == 0.0)
+
+
 def test_attention_single_key_closed_form():
     # S == 1: P == 1, so dV == dO and dS == P (dP - rowdot) == 0 -> dQ == dK == 0.
     rng = np.random.default_rng(3)
