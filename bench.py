@@ -16,6 +16,7 @@ reported apart (cpu_oracle).
 
 Other BASELINE configs (parity-tested, measured with --workload):
     attn  configs[2]: causal attention backward with RoPE, B4 H16 S2048 D128, bf16
+    attn32 the same shape in fp32 (the reference's dtype) on the generic matrix-core kernels
     vsa   configs[3]: VSA unpack-project dW (8192 x 10240 bits -> 768, fp32 dY) and the
           surrogate-loss backward (K = 4)
     mlp   configs[0]: MLP 784->256->10 fp32 B=64 through the tape engine (grilly_core)
@@ -28,7 +29,7 @@ Other BASELINE configs (parity-tested, measured with --workload):
 Each prints one JSON line of the same shape; the default (ffn) is the headline metric.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload ffn|attn|vsa|mlp|decoder|hyper|linear32]
+                       [--workload ffn|attn|attn32|vsa|mlp|decoder|hyper|linear32]
 """
 import argparse
 import json
@@ -55,7 +56,7 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=T)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--workload", default="ffn",
-                   choices=["ffn", "attn", "vsa", "mlp", "decoder", "hyper", "linear32"])
+                   choices=["ffn", "attn", "attn32", "vsa", "mlp", "decoder", "hyper", "linear32"])
     p.add_argument("--calib-copy", action="store_true",
                    help="after the timed region, launch one gn_add_inplace over 2^28 floats "
                         "(reads 2 GiB, writes 1 GiB): the reference dispatch that scales the "
@@ -242,6 +243,60 @@ def line(metric, value, unit, args, ms, dtype, config, roofline, cpu, higher=Tru
             "cpu_baseline": cpu}
 
 
+def attn_cpu_baseline(args, S, D, BH):
+    """The reference's CPU attention backward (numpy fp32, P materialised) on 8 heads."""
+    if args.no_cpu:
+        return None
+    from oracle import cpu_ref
+    r = np.random.default_rng(3)
+    Hs = 8  # 8 of the B*H heads: P is S x S fp32 per head
+    q, k, v = (r.standard_normal((Hs, S, D)).astype(np.float32) for _ in range(3))
+    do = (r.standard_normal((Hs, S, D)) * 1e-2).astype(np.float32)
+    nt = cpu_ref.threads()
+    with cpu_ref.limit_threads(nt):
+        cpu_ref.attention_step(q[:1], k[:1], v[:1], do[:1], D ** -0.5)
+        t0 = time.perf_counter()
+        cpu_ref.attention_step(q, k, v, do, D ** -0.5)
+        dt = time.perf_counter() - t0
+    return {"value": round(5 * 2.0 * S * S * D * 0.5 * Hs / dt / 1e12, 5), "unit": "TFLOP/s",
+            "cores": nt, "kind": "port",
+            "sample": f"{Hs} of {BH} heads at S={S}, numpy fp32 with P materialised (the "
+                      f"reference's CPU path, autograd_core.py:617-654; no RoPE there), "
+                      f"{dt:.2f} s; algorithmic causal FLOPs", "cpu_model": cpu_ref.cpu_model()}
+
+
+def bench_attn32(args, torch, gn):
+    """configs[2]'s shape with fp32 tensors (the reference's own dtype): causal attention
+    backward with RoPE, B4 H16 S2048 D128, on the generic matrix-core kernels (two-piece bf16
+    split, three products per product)."""
+    B, H, S, D = 4, 16, 2048, 128
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    Q, K, V = (torch.randn(B, H, S, D, device=dev, generator=g) for _ in range(3))
+    dO = torch.randn(B, H, S, D, device=dev, generator=g) * 1e-2
+    ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D), dev)
+    O, LSE = gn.attn_fwd(Q, K, V, causal=True, rope="interleaved", ws=ws)
+    out = (torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V))
+    ms = timed(torch, lambda: gn.attn_bwd(Q, K, V, O, dO, LSE, causal=True, rope="interleaved",
+                                          ws=ws, out=out), args.steps, args.warmup)
+    flops = 5 * 2.0 * S * S * D * 0.5 * B * H  # causal, algorithmic (5 GEMMs)
+    tf = flops / (ms * 1e-3) / 1e12
+    out = line("causal attention backward with RoPE, fp32 (algorithmic TFLOP/s)", round(tf, 2),
+               "TFLOP/s", args, ms, "f32 (bf16x2 split on MFMA, 3 products)",
+               {"workload": "C3 shape in fp32: causal attention bwd + RoPE(1e4), B4 H16 S2048 D128",
+                "batch": B, "heads": H, "seq_len": S, "head_dim": D},
+               {"kernel": "gn_attn_bwd fp32 (split pre-pass + attn_bwd_gen dK/dV and dQ + "
+                          "un-rotating conversion)", "bound": "mfma",
+                "achieved": round(tf, 1), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tf / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                "note": "peak = dense fp32 MFMA; the kernels issue 3 bf16 MFMA products per fp32 "
+                        "product and 7 products for the algorithmic 5 (the dQ pass recomputes S "
+                        f"and dP): {tf * 3 * 7 / 5:.0f} TFLOP/s of bf16 MFMA work issued"},
+               attn_cpu_baseline(args, S, D, B * H))
+    return out
+
+
 def bench_attn(args, torch, gn):
     """causal attention backward with RoPE (theta 1e4), B4 H16 S2048 D128."""
     B, H, S, D = 4, 16, 2048, 128
@@ -258,24 +313,7 @@ def bench_attn(args, torch, gn):
                                           ws=ws, out=out), args.steps, args.warmup)
     flops = 5 * 2.0 * S * S * D * 0.5 * B * H  # causal, algorithmic (5 GEMMs)
     tf = flops / (ms * 1e-3) / 1e12
-    cpu = None
-    if not args.no_cpu:
-        from oracle import cpu_ref
-        r = np.random.default_rng(3)
-        Hs = 8  # 8 of the 64 (b, h) heads: P is S x S fp32 per head
-        q, k, v = (r.standard_normal((Hs, S, D)).astype(np.float32) for _ in range(3))
-        do = (r.standard_normal((Hs, S, D)) * 1e-2).astype(np.float32)
-        nt = cpu_ref.threads()
-        with cpu_ref.limit_threads(nt):
-            cpu_ref.attention_step(q[:1], k[:1], v[:1], do[:1], D ** -0.5)
-            t0 = time.perf_counter()
-            cpu_ref.attention_step(q, k, v, do, D ** -0.5)
-            dt = time.perf_counter() - t0
-        cpu = {"value": round(5 * 2.0 * S * S * D * 0.5 * Hs / dt / 1e12, 5), "unit": "TFLOP/s",
-               "cores": nt, "kind": "port",
-               "sample": f"{Hs} of {B * H} heads at S={S}, numpy fp32 with P materialised (the "
-                         f"reference's CPU path, autograd_core.py:617-654; no RoPE there), "
-                         f"{dt:.2f} s; algorithmic causal FLOPs", "cpu_model": cpu_ref.cpu_model()}
+    cpu = attn_cpu_baseline(args, S, D, B * H)
     out = line("causal attention backward with RoPE (algorithmic TFLOP/s)", round(tf, 2),
                "TFLOP/s", args, ms, "bf16",
                {"workload": "C3 causal attention bwd + RoPE(1e4), B4 H16 S2048 D128",
@@ -847,7 +885,7 @@ def main():
         print(json.dumps(ceilings(torch, gn)))
         return
     if args.workload != "ffn":
-        fn = {"attn": bench_attn, "vsa": bench_vsa, "mlp": bench_mlp,
+        fn = {"attn": bench_attn, "attn32": bench_attn32, "vsa": bench_vsa, "mlp": bench_mlp,
               "decoder": bench_decoder, "hyper": bench_hyper, "linear32": bench_linear32}[args.workload]
         print(json.dumps(fn(args, torch, gn)))
         return

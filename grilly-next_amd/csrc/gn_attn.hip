@@ -902,6 +902,468 @@ __global__ __launch_bounds__(256) void attn_key_bias(const float* __restrict__ m
     if (lane == 0) kt[tile] = any != 0ull;
 }
 
+// ---- generic MFMA path: D a multiple of 32 up to 256, bf16 or fp32 ---------------------
+//
+// For the head dims and dtypes the tuned kernels above do not take: bf16 with D = 32, 96, 192
+// or 256, and fp32 at any of those D and at 64 and 128.  fp32 operands run on the bf16 matrix
+// cores as NP = 2 pieces x = hi + lo (hi = bf16(x), lo = bf16(x - hi), |x - hi - lo| <=
+// 2^-17 |x|); a product takes lo.hi + hi.lo + hi.hi (the dropped lo.lo is below 2^-16 of
+// |a b|), and P and dS are split the same way in registers.  One template serves both passes:
+//   ROLE 0 (dK, dV): wave rows = 32 keys, tiles = 32 queries;
+//       S = Q K^T, dP = dO V^T  (A = tile rows, B = the wave's rows),
+//       P = exp2(S scale log2e + bias - L log2e), dS = P (dP - D_i),
+//       dV += P^T dO, dK += dS^T Q  (A = P / dS from the accumulators, B = tile columns);
+//   ROLE 1 (dQ): wave rows = 32 queries, tiles = 32 keys;
+//       S^T = K Q^T, dP^T = V dO^T, then dQ += dS K.
+// The wave's own operand rows (K, V or Q, dO) stay in registers when D NP <= 256, else they are
+// re-read per tile (L2); a tile (both tensors, every piece) is staged through registers into
+// LDS (row pitch D + 8 elements), double-buffered, one barrier per tile.  The dK/dV pass
+// accumulates DC <= 128 columns per block (gridDim.z column groups for D > 128; S and dP are
+// then formed once per group).  Gradients leave as fp32 rows, dQ and dK times scale in the
+// rotated space, for the un-rotating conversion pass.
+struct GenIn {
+    const bf16_t* t[4][2];  // [Q (rotated), K (rotated), V, dO][piece], each [B*H][S][D]
+};
+
+template <int NP>
+__device__ __forceinline__ f32x16_t mma_np(const bf16x8_t (&a)[NP], const bf16x8_t (&b)[NP],
+                                           f32x16_t c) {
+    if constexpr (NP == 2) {
+        c = mfma32(a[1], b[0], c);
+        c = mfma32(a[0], b[1], c);
+    }
+    return mfma32(a[0], b[0], c);
+}
+
+// 8 accumulator values -> NP bf16 operand pieces (hi, then the rounding residual)
+template <int NP>
+__device__ __forceinline__ void split8(const float* v, bf16x8_t (&o)[NP]) {
+    o[0] = to_bf16x8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+    if constexpr (NP == 2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[NP - 1][e] = (__bf16)(v[e] - (float)o[0][e]);
+    }
+}
+
+template <int D, int NP>
+struct GenCfg {
+    static constexpr int P = D + 8;                       // LDS row pitch (elements)
+    static constexpr int TILE = 2 * NP * 32 * P * 2;      // both tensors, all pieces (bytes)
+    static constexpr int STAGE = TILE + 256;              // + 64 floats of per-row data
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int CHUNKS = 2 * NP * 32 * (D / 8);  // 16-byte pieces per tile
+    static constexpr int NCH = CHUNKS / 256;              // per thread
+    static_assert(CHUNKS % 256 == 0, "every thread stages the same number of pieces");
+    static constexpr bool RES = D * NP <= 256;            // wave rows held in registers
+};
+
+// A tile's register staging: thread tid holds 16-byte pieces j = tid + 256 u of the tile
+// (tensor-piece group tp = j / (32 D/8), row, chunk), plus one float4 of per-row data.
+template <int D, int NP>
+struct GenStage {
+    uint4 v[GenCfg<D, NP>::NCH];
+    float4 r;
+};
+struct GenSrc {
+    const bf16_t *p0, *p1, *p2, *p3;  // tile planes by group tp (NP = 1: p0, p2)
+    const float *r0, *r1;             // row data: r0 then r1 (r1 null: r0 only, 32 floats)
+    const float* any;                 // a readable float array (stands in for a null r0 / r1)
+    size_t roff, hb;                  // row-data offset of the head / batch; head offset
+};
+
+template <int D, int NP>
+__device__ __forceinline__ void gen_load(GenStage<D, NP>& st, const GenSrc& g, int t0, int S, int tid) {
+    using C = GenCfg<D, NP>;
+    constexpr int CR = D / 8;
+    // unconditional loads (a conditional one would make the staging array a memory object)
+#pragma unroll
+    for (int u = 0; u < C::NCH; ++u) {
+        const int j = tid + 256 * u;
+        const int ch = j % CR, row = (j / CR) % 32, tp = j / (CR * 32);
+        const bf16_t* p = NP == 1 ? (tp == 0 ? g.p0 : g.p2)
+                                  : (tp == 0 ? g.p0 : tp == 1 ? g.p1 : tp == 2 ? g.p2 : g.p3);
+        st.v[u] = *reinterpret_cast<const uint4*>(p + g.hb + (size_t)min(t0 + row, S - 1) * D + 8 * ch);
+    }
+    // 32 floats from r0 (threads 0-7) then 32 from r1 (threads 8-15); zeros elsewhere
+    const float* rp = tid < 8 ? g.r0 : g.r1;
+    const bool ok = tid < 16 && rp;
+    const float4 v = *reinterpret_cast<const float4*>(ok ? rp + g.roff + t0 + 4 * (tid & 7) : g.any);
+    st.r = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+template <int D, int NP>
+__device__ __forceinline__ void gen_store(const GenStage<D, NP>& st, unsigned char* sb, int tid) {
+    using C = GenCfg<D, NP>;
+    constexpr int CR = D / 8;
+#pragma unroll
+    for (int u = 0; u < C::NCH; ++u) {
+        const int j = tid + 256 * u;
+        const int ch = j % CR, row = (j / CR) % 32, tp = j / (CR * 32);
+        *reinterpret_cast<uint4*>(sb + ((tp * 32 + row) * C::P + 8 * ch) * 2) = st.v[u];
+    }
+    if (tid < 16) reinterpret_cast<float4*>(sb + C::TILE)[tid] = st.r;
+}
+
+template <int ROLE, int D, int NP, int DC>
+__global__ __launch_bounds__(256) void attn_bwd_gen(GenIn in, const float* __restrict__ L2,
+                                                    const float* __restrict__ Di,
+                                                    const float* __restrict__ kb,
+                                                    float* __restrict__ outA,
+                                                    float* __restrict__ outB, int H, int S,
+                                                    int Spad, float scale, int causal) {
+    using C = GenCfg<D, NP>;
+    constexpr int KS = D / 16, NT = DC / 32, CR = D / 8;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int bh = blockIdx.x, bb = bh / H;
+    const int lane = threadIdx.x & 63, h = lane >> 5, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int blk = ROLE == 0 ? (int)blockIdx.y : (S + 127) / 128 - 1 - (int)blockIdx.y;
+    const int w0 = blk * 128 + 32 * wave, wrow = w0 + (lane & 31);
+    const int dcol0 = blockIdx.z * DC;
+    const float c2 = scale * 1.4426950408889634f;
+    const size_t hb = (size_t)bh * S * D;
+    // tensors by role: W = the wave's rows, T = the tiles
+    constexpr int w_t0 = ROLE == 0 ? 1 : 0, w_t1 = ROLE == 0 ? 2 : 3;
+    constexpr int t_t0 = ROLE == 0 ? 0 : 1, t_t1 = ROLE == 0 ? 3 : 2;
+    // the tile planes as scalars (a per-thread index into the argument array would put it in
+    // scratch memory): tile chunk group tp = tensor * NP + piece
+    const bf16_t* tp0 = in.t[t_t0][0];
+    const bf16_t* tp1 = in.t[t_t0][NP - 1];
+    const bf16_t* tp2 = in.t[t_t1][0];
+    const bf16_t* tp3 = in.t[t_t1][NP - 1];
+
+    // the wave's operand rows: B fragments (lane -> row wrow, k = d)
+    const size_t wr = hb + (size_t)min(wrow, S - 1) * D + 8 * h;
+    auto wfrag = [&](int which, int ks, int p) {
+        return ld_frag16((which ? in.t[w_t1][p] : in.t[w_t0][p]) + wr + 16 * ks);
+    };
+    bf16x8_t wres[C::RES ? 2 : 1][C::RES ? KS : 1][NP];
+    if constexpr (C::RES) {
+#pragma unroll
+        for (int which = 0; which < 2; ++which)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int p = 0; p < NP; ++p) wres[which][ks][p] = wfrag(which, ks, p);
+    }
+    // per-lane row data of the wave's rows: key bias (ROLE 0), L log2e and D_i (ROLE 1)
+    float lb = 0.f, lL = 0.f, lD = 0.f;
+    if (ROLE == 0) {
+        lb = kb && wrow < S ? kb[(size_t)bb * Spad + wrow] : 0.f;
+    } else {
+        lL = L2[(size_t)bh * Spad + min(wrow, S - 1)];
+        lD = Di[(size_t)bh * Spad + min(wrow, S - 1)];
+    }
+
+    f32x16_t accA[ROLE == 0 ? NT : 1], accB[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        zero16(accB[t]);
+        if (ROLE == 0) zero16(accA[t]);
+    }
+
+    // tiles of 32 rows: ROLE 0 queries from the block's first key (causal) to S; ROLE 1 keys
+    // from 0 to the block's last query (causal) or S
+    const int tbeg = ROLE == 0 && causal ? blk * 128 : 0;
+    const int tend = ROLE == 1 && causal ? min(S, blk * 128 + 128) : S;
+    const int T = tbeg < tend ? (tend - tbeg + 31) / 32 : 0;
+    GenStage<D, NP> stg;
+    const GenSrc src{tp0, tp1, tp2, tp3, ROLE == 0 ? L2 : kb, ROLE == 0 ? Di : nullptr, L2,
+                     ROLE == 0 ? (size_t)bh * Spad : (size_t)bb * Spad, hb};
+    // T >= 1 (the causal ranges always hold the block's own rows).  The loads and stores run
+    // unconditionally (the last iteration re-stages its own tile into the unused buffer), so the
+    // staging registers stay registers.
+    gen_load<D, NP>(stg, src, tbeg, S, tid);
+    gen_store<D, NP>(stg, smem, tid);
+    for (int it = 0; it < T; ++it) {
+        __syncthreads();  // tile it is in LDS; the other buffer's readers are done
+        gen_load<D, NP>(stg, src, tbeg + 32 * min(it + 1, T - 1), S, tid);
+        const int t0 = tbeg + 32 * it;
+        const unsigned char* sb = smem + (it & 1) * C::STAGE;
+        const bf16_t* tT[2][NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            tT[0][p] = reinterpret_cast<const bf16_t*>(sb) + (size_t)p * 32 * C::P;
+            tT[1][p] = reinterpret_cast<const bf16_t*>(sb) + (size_t)(NP + p) * 32 * C::P;
+        }
+        const float* srow = reinterpret_cast<const float*>(sb + C::TILE);
+        // tile rows t0 .. t0+31 against the wave's rows w0 .. w0+31
+        const int q_lo = ROLE == 0 ? t0 : w0, k_lo = ROLE == 0 ? w0 : t0;
+        const bool skip = w0 >= S || (causal && k_lo > q_lo + 31);
+        if (!skip) {
+            const bool full = t0 + 31 < S && w0 + 31 < S && (!causal || k_lo + 31 <= q_lo);
+            f32x16_t s, dp;
+            zero16(s);
+            zero16(dp);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                bf16x8_t a0[NP], a1[NP], b0[NP], b1[NP];
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    a0[p] = ld_frag16(tT[0][p] + (lane & 31) * C::P + 16 * ks + 8 * h);
+                    a1[p] = ld_frag16(tT[1][p] + (lane & 31) * C::P + 16 * ks + 8 * h);
+                    if constexpr (C::RES) {
+                        b0[p] = wres[0][ks][p];
+                        b1[p] = wres[1][ks][p];
+                    } else {
+                        b0[p] = wfrag(0, ks, p);
+                        b1[p] = wfrag(1, ks, p);
+                    }
+                }
+                s = mma_np<NP>(a0, b0, s);
+                dp = mma_np<NP>(a1, b1, dp);
+            }
+            // element r: tile row t0 + 8(r/4) + 4h + r%4, wave row wrow
+            float pv[16], dv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tr = 8 * (r >> 2) + 4 * h + (r & 3);
+                float Lr, Dr, br;
+                if (ROLE == 0) { Lr = srow[tr]; Dr = srow[32 + tr]; br = lb; }
+                else { Lr = lL; Dr = lD; br = kb ? srow[tr] : 0.f; }
+                float x = s[r] * c2 + br - Lr;
+                if (!full) {
+                    const int q = ROLE == 0 ? t0 + tr : wrow, k = ROLE == 0 ? wrow : t0 + tr;
+                    x = (q < S && k < S && (!causal || k <= q)) ? x : -INFINITY;
+                }
+                pv[r] = __builtin_amdgcn_exp2f(x);
+                dv[r] = pv[r] * (dp[r] - Dr);
+            }
+            bf16x8_t pa[2][NP], da[2][NP];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                if (ROLE == 0) split8<NP>(pv + 8 * p, pa[p]);
+                split8<NP>(dv + 8 * p, da[p]);
+            }
+            // k-step p: tile rows 16p + {4h, 8 + 4h} + 0..3 in both operands
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const int n0 = dcol0 + 32 * t;
+                    bf16x8_t c0[NP], c1[NP];
+#pragma unroll
+                    for (int q = 0; q < NP; ++q) {
+                        const int lan = lane & 15;
+                        const int col = n0 + 16 * ((lane >> 4) & 1) + 4 * (lan & 3);
+                        const int r0 = 16 * p + 4 * h + (lan >> 2);
+                        c0[q] = ld_tr_pair(tT[0][q] + r0 * C::P + col, tT[0][q] + (r0 + 8) * C::P + col);
+                        if (ROLE == 0)
+                            c1[q] = ld_tr_pair(tT[1][q] + r0 * C::P + col, tT[1][q] + (r0 + 8) * C::P + col);
+                    }
+                    if (ROLE == 0) accA[t] = mma_np<NP>(pa[p], c1, accA[t]);
+                    accB[t] = mma_np<NP>(da[p], c0, accB[t]);
+                }
+        }
+        gen_store<D, NP>(stg, smem + ((it + 1) & 1) * C::STAGE, tid);
+    }
+
+    // fp32 rows out: column dcol0 + 32t + lane%32, wave rows w0 + 8(r/4) + 4h + r%4
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = w0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row < S) {
+                const size_t o = hb + (size_t)row * D + dcol0 + 32 * t + (lane & 31);
+                outB[o] = accB[t][r] * scale;
+                if (ROLE == 0) outA[o] = accA[t][r];
+            }
+        }
+}
+
+// Generic forward (same D, dtypes and operand pieces as attn_bwd_gen): one block per (b*h, 128
+// queries), four waves x 32 queries, key tiles of 32 staged into LDS.  Per tile and wave:
+//   S^T = K Q^T (A = K tile rows, B = the wave's Q rows, in registers or re-read): lane = query,
+//   so the running max m and sum l are per-lane (one exchange with lane ^ 32 per tile);
+//   P^T = exp2(S^T scale log2e + bias - m), O^T = alpha O^T + V^T P^T (A = V tile columns by
+//   transpose reads, B = P^T from the accumulator, both in the accumulator's key order).
+// O = O^T / l leaves in the input dtype, LSE = (m + log2 l) ln 2 (-inf for a row with no visible
+// kept key, whose O is 0).
+template <typename T, int D, int NP>
+__global__ __launch_bounds__(256) void attn_fwd_gen(GenIn in, const float* __restrict__ kb,
+                                                    T* __restrict__ O, float* __restrict__ LSE,
+                                                    int H, int S, int Spad, float scale, int causal) {
+    using C = GenCfg<D, NP>;
+    constexpr int KS = D / 16, NT = D / 32;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int bh = blockIdx.x, bb = bh / H;
+    const int lane = threadIdx.x & 63, h = lane >> 5, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int blk = (S + 127) / 128 - 1 - (int)blockIdx.y;  // longest rows first
+    const int w0 = blk * 128 + 32 * wave, q = w0 + (lane & 31);
+    const float c2 = scale * 1.4426950408889634f;
+    const size_t hb = (size_t)bh * S * D;
+    const size_t wr = hb + (size_t)min(q, S - 1) * D + 8 * h;
+    bf16x8_t qres[C::RES ? KS : 1][NP];
+    if constexpr (C::RES) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int p = 0; p < NP; ++p) qres[ks][p] = ld_frag16(in.t[0][p] + wr + 16 * ks);
+    }
+    f32x16_t aO[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) zero16(aO[t]);
+    float m = -INFINITY, l = 0.f;
+
+    const int tend = causal ? min(S, blk * 128 + 128) : S;
+    const int Tn = (tend + 31) / 32;
+    GenStage<D, NP> stg;
+    const GenSrc src{in.t[1][0], in.t[1][NP - 1], in.t[2][0], in.t[2][NP - 1], kb, nullptr, LSE,
+                     (size_t)bb * Spad, hb};
+    gen_load<D, NP>(stg, src, 0, S, tid);
+    gen_store<D, NP>(stg, smem, tid);
+    for (int it = 0; it < Tn; ++it) {
+        __syncthreads();
+        gen_load<D, NP>(stg, src, 32 * min(it + 1, Tn - 1), S, tid);
+        const int k0 = 32 * it;
+        const unsigned char* sb = smem + (it & 1) * C::STAGE;
+        const bf16_t* tK[NP];
+        const bf16_t* tV[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            tK[p] = reinterpret_cast<const bf16_t*>(sb) + (size_t)p * 32 * C::P;
+            tV[p] = reinterpret_cast<const bf16_t*>(sb) + (size_t)(NP + p) * 32 * C::P;
+        }
+        const float* sbias = reinterpret_cast<const float*>(sb + C::TILE);
+        if (!(w0 >= S || (causal && k0 > w0 + 31))) {
+            const bool full = k0 + 31 < S && w0 + 31 < S && (!causal || k0 + 31 <= w0);
+            f32x16_t s;
+            zero16(s);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                bf16x8_t a[NP], b[NP];
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    a[p] = ld_frag16(tK[p] + (lane & 31) * C::P + 16 * ks + 8 * h);
+                    if constexpr (C::RES) b[p] = qres[ks][p];
+                    else b[p] = ld_frag16(in.t[0][p] + wr + 16 * ks);
+                }
+                s = mma_np<NP>(a, b, s);
+            }
+            // element r: key k0 + 8(r/4) + 4h + r%4, query q (scores in base-2 units)
+            float x[16], mt = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int kr = 8 * (r >> 2) + 4 * h + (r & 3);
+                float v = s[r] * c2 + (kb ? sbias[kr] : 0.f);
+                if (!full) {
+                    const int k = k0 + kr;
+                    v = (q < S && k < S && (!causal || k <= q)) ? v : -INFINITY;
+                }
+                x[r] = v;
+                mt = fmaxf(mt, v);
+            }
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float mn = fmaxf(m, mt);
+            const float ms = mn == -INFINITY ? 0.f : mn;  // no visible key yet: the row stays empty
+            const float alpha = __builtin_amdgcn_exp2f(m - ms);
+            float ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                x[r] = __builtin_amdgcn_exp2f(x[r] - ms);
+                ps += x[r];
+            }
+            ps += __shfl_xor(ps, 32);
+            l = l * alpha + ps;
+            m = mn;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) aO[t][r] *= alpha;
+            bf16x8_t pb[2][NP];
+            split8<NP>(x, pb[0]);
+            split8<NP>(x + 8, pb[1]);
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    bf16x8_t va[NP];
+#pragma unroll
+                    for (int u = 0; u < NP; ++u) {
+                        const int lan = lane & 15;
+                        const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lan & 3);
+                        const int r0 = 16 * p + 4 * h + (lan >> 2);
+                        va[u] = ld_tr_pair(tV[u] + r0 * C::P + col, tV[u] + (r0 + 8) * C::P + col);
+                    }
+                    aO[t] = mma_np<NP>(va, pb[p], aO[t]);
+                }
+        }
+        gen_store<D, NP>(stg, smem + ((it + 1) & 1) * C::STAGE, tid);
+    }
+    // O^T accumulators: lane = query, element r of tile t: d = 32t + 8(r/4) + 4h + r%4
+    if (q < S) {
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        T* orow = O + hb + (size_t)q * D;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * t + 8 * g + 4 * h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) io<T>::st(orow, d + e, aO[t][4 * g + e] * inv);
+            }
+        if (h == 0) LSE[(size_t)bh * S + q] = l > 0.f ? (m + __log2f(l)) * 0.6931471805599453f : -INFINITY;
+    }
+}
+
+// Generic path pre-pass: NP bf16 pieces of one [B*H*S, D] tensor (rotated when `mode` is
+// set), one thread per element pair.
+template <typename T, int NP>
+__global__ __launch_bounds__(256) void gen_split(const T* __restrict__ X, bf16_t* __restrict__ y0,
+                                                 bf16_t* __restrict__ y1, int64_t rows, int S,
+                                                 int D, int mode, float theta) {
+    const int half = D / 2;
+    for (int64_t idx = blockIdx.x * (int64_t)256 + threadIdx.x; idx < rows * half;
+         idx += (int64_t)gridDim.x * 256) {
+        const int64_t row = idx / half;
+        const int i = (int)(idx % half);
+        int e0 = 2 * i, e1 = 2 * i + 1;
+        if (mode != GN_ROPE_NONE) rope_pair(mode, i, D, e0, e1);
+        float x0 = io<T>::ld(X, row * D + e0), x1 = io<T>::ld(X, row * D + e1);
+        if (mode != GN_ROPE_NONE) {
+            float c, sn;
+            rope_cs((int)(row % S), i, D, theta, c, sn);
+            const float r0 = x0 * c - x1 * sn, r1 = x0 * sn + x1 * c;
+            x0 = r0;
+            x1 = r1;
+        }
+        const bf16_t h0 = f2bf(x0), h1 = f2bf(x1);
+        y0[row * D + e0] = h0;
+        y0[row * D + e1] = h1;
+        if (NP == 2) {
+            y1[row * D + e0] = f2bf(x0 - bf2f(h0));
+            y1[row * D + e1] = f2bf(x1 - bf2f(h1));
+        }
+    }
+}
+
+// Generic path row data: D_i = rowsum(dO O) (fp32) and L log2(e) (+inf for a row with no
+// visible kept key) into [B*H][Spad], padding zero.  One wave per row.
+template <typename T>
+__global__ __launch_bounds__(256) void gen_rows(const T* __restrict__ dO, const T* __restrict__ O,
+                                                const float* __restrict__ LSE, float* __restrict__ L2,
+                                                float* __restrict__ Di, int64_t BH, int S, int Spad,
+                                                int D) {
+    const int64_t r = blockIdx.x * (int64_t)4 + (threadIdx.x >> 6);  // padded row index
+    const int lane = threadIdx.x & 63;
+    if (r >= BH * Spad) return;
+    const int64_t bh = r / Spad;
+    const int pos = (int)(r % Spad);
+    float dot = 0.f;
+    if (pos < S) {
+        const size_t off = ((size_t)bh * S + pos) * D;
+        for (int d = lane; d < D; d += 64) dot += io<T>::ld(dO, off + d) * io<T>::ld(O, off + d);
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) {
+        const float lse = pos < S ? LSE[(size_t)bh * S + pos] : 0.f;
+        Di[r] = dot;
+        L2[r] = pos >= S ? 0.f : lse == -INFINITY ? INFINITY : lse * 1.4426950408889634f;
+    }
+}
+
 // ---- SIMT path: one wave per query row (dQ, forward) or key row (dK, dV) ----------------
 // Each lane owns up to 4 d-values (D <= 256).  Q and K are the already-rotated tensors.
 template <typename T>
@@ -1066,6 +1528,10 @@ __global__ __launch_bounds__(256) void unrotate_store(const float* __restrict__ 
 struct AttnWs {
     void* Qr;
     void* Kr;
+    bf16_t* plane[4][2];  // generic path: [Q, K, V, dO][piece] bf16 [B*H][S][D]
+    float* L2;            // generic path: L log2(e) [B*H][Spad]
+    float* accB;          // generic path: fp32 dK (dQ after it) and dV rows
+    float* accA;
     float* Di;
     float* Lsc;   // MFMA path: L log2(e), [B*H][Spad]
     float2* cs;   // MFMA path: RoPE cos/sin table [S][D/2]
@@ -1081,7 +1547,9 @@ inline int spad_of(int S) { return (S + 63) / 64 * 64; }
 
 // mfma: bf16 Qr, Kr; Di, Lsc padded to Spad per (b, h); cos/sin table.
 // simt: esz-sized Qr, Kr; Di; fp32 accumulator.
-size_t ws_layout(int64_t BH, int S, int D, size_t esz, bool mfma, void* base, AttnWs* w) {
+enum WsKind { kWsSimt = 0, kWsMfma = 1, kWsGen1 = 2, kWsGen2 = 3 };  // Gen: NP = 1, 2
+
+size_t ws_layout(int64_t BH, int S, int D, size_t esz, int kind, void* base, AttnWs* w) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
         void* p = base ? (char*)base + off : nullptr;
@@ -1090,6 +1558,20 @@ size_t ws_layout(int64_t BH, int S, int D, size_t esz, bool mfma, void* base, At
     };
     const int64_t BHSD = BH * S * D;
     AttnWs t{};
+    if (kind == kWsGen1 || kind == kWsGen2) {
+        const int np = kind == kWsGen2 ? 2 : 1;
+        for (int i = 0; i < 4; ++i)
+            for (int p = 0; p < np; ++p) t.plane[i][p] = (bf16_t*)take(BHSD * 2);
+        t.L2 = (float*)take(BH * spad_of(S) * 4);
+        t.Di = (float*)take(BH * spad_of(S) * 4);
+        t.accA = (float*)take(BHSD * 4);
+        t.accB = (float*)take(BHSD * 4);
+        t.kb = (float*)take(BH * spad_of(S) * 4);
+        t.kt = (int*)take(BH * (spad_of(S) / 64) * 4);
+        if (w) *w = t;
+        return off;
+    }
+    const bool mfma = kind == kWsMfma;
     t.Qr = take(BHSD * esz);
     t.Kr = take(BHSD * esz);
     if (mfma) {
@@ -1180,6 +1662,127 @@ int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, const f
     return GN_OK;
 }
 
+// head dims of the generic MFMA path (multiples of 32 whose dK/dV column groups of <= 128
+// divide D)
+inline bool gen_dim(int D) { return D == 32 || D == 64 || D == 96 || D == 128 || D == 192 || D == 256; }
+
+template <typename F>
+bool allow_gen_lds(F* fn, size_t bytes) {
+    return bytes <= 64 * 1024 || allow_lds(fn, bytes);
+}
+
+template <typename T, int D, int NP>
+int launch_gen_bwd(const AttnWs& w, const void* Q, const void* K, const void* V, const void* O,
+                   const void* dO, const float* LSE, const float* mask, void* dQ, void* dK,
+                   void* dV, int B, int H, int S, float scale, int causal, int rope_mode,
+                   float theta, hipStream_t s) {
+    using C = GenCfg<D, NP>;
+    constexpr int DC = D > 128 ? D / 2 : D;
+    static const bool ok0 = allow_gen_lds(attn_bwd_gen<0, D, NP, DC>, C::LDS);
+    static const bool ok1 = allow_gen_lds(attn_bwd_gen<1, D, NP, D>, C::LDS);
+    if (!ok0 || !ok1) {
+        set_error("gn_attn_bwd: cannot reserve %d B of LDS (generic path)", C::LDS);
+        return GN_E_HIP;
+    }
+    const int64_t BH = (int64_t)B * H, rows = BH * S;
+    const int Spad = spad_of(S);
+    const float* kb;
+    const int* kt;
+    key_bias(mask, w, B, S, s, &kb, &kt);
+    GenIn in{};
+    const void* src[4] = {Q, K, V, dO};
+    gen_planes<T, NP>(w, src, 4, in, rows, S, D, rope_mode, theta, s);
+    gen_rows<T><<<(unsigned)((BH * Spad + 3) / 4), 256, 0, s>>>((const T*)dO, (const T*)O, LSE, w.L2,
+                                                                 w.Di, BH, S, Spad, D);
+    const unsigned nb = (unsigned)((S + 127) / 128);
+    hipLaunchKernelGGL((attn_bwd_gen<0, D, NP, DC>), dim3((unsigned)BH, nb, D / DC), dim3(256), C::LDS,
+                       s, in, w.L2, w.Di, kb, w.accA, w.accB, H, S, Spad, scale, causal);
+    const unsigned ge = grid_for(rows * (D / 2), 256, 16384);
+    unrotate_store<T><<<ge, 256, 0, s>>>(w.accB, (T*)dK, rows, S, D, rope_mode, theta);
+    unrotate_store<T><<<ge, 256, 0, s>>>(w.accA, (T*)dV, rows, S, D, GN_ROPE_NONE, theta);
+    hipLaunchKernelGGL((attn_bwd_gen<1, D, NP, D>), dim3((unsigned)BH, nb, 1), dim3(256), C::LDS, s,
+                       in, w.L2, w.Di, kb, nullptr, w.accB, H, S, Spad, scale, causal);
+    unrotate_store<T><<<ge, 256, 0, s>>>(w.accB, (T*)dQ, rows, S, D, rope_mode, theta);
+    GN_LAUNCH_CHECK("gn_attn_bwd (generic mfma)");
+    return GN_OK;
+}
+
+// operand planes of the generic path: rotated Q, K; V, dO as they are (bf16 inputs without
+// rotation are used in place).  n = 3 for the forward (Q, K, V), 4 for the backward.
+template <typename T, int NP>
+void gen_planes(const AttnWs& w, const void* const* src, int n, GenIn& in, int64_t rows, int S,
+                int D, int rope_mode, float theta, hipStream_t s) {
+    const unsigned g = grid_for(rows * (D / 2), 256, 16384);
+    for (int i = 0; i < n; ++i) {
+        const int mode = i < 2 ? rope_mode : GN_ROPE_NONE;
+        if (NP == 1 && mode == GN_ROPE_NONE) {
+            in.t[i][0] = in.t[i][1] = (const bf16_t*)src[i];
+            continue;
+        }
+        gen_split<T, NP><<<g, 256, 0, s>>>((const T*)src[i], w.plane[i][0], w.plane[i][NP - 1], rows,
+                                           S, D, mode, theta);
+        for (int p = 0; p < 2; ++p) in.t[i][p] = w.plane[i][p < NP ? p : 0];
+    }
+}
+
+template <typename T, int D, int NP>
+int launch_gen_fwd(const AttnWs& w, const void* Q, const void* K, const void* V, const float* kb,
+                   void* O, float* LSE, int B, int H, int S, float scale, int causal,
+                   int rope_mode, float theta, hipStream_t s) {
+    using C = GenCfg<D, NP>;
+    static const bool ok = allow_gen_lds(attn_fwd_gen<T, D, NP>, C::LDS);
+    if (!ok) {
+        set_error("gn_attn_fwd: cannot reserve %d B of LDS (generic path)", C::LDS);
+        return GN_E_HIP;
+    }
+    const int64_t BH = (int64_t)B * H;
+    GenIn in{};
+    const void* src[3] = {Q, K, V};
+    gen_planes<T, NP>(w, src, 3, in, BH * S, S, D, rope_mode, theta, s);
+    hipLaunchKernelGGL((attn_fwd_gen<T, D, NP>), dim3((unsigned)BH, (unsigned)((S + 127) / 128)),
+                       dim3(256), C::LDS, s, in, kb, (T*)O, LSE, H, S, spad_of(S), scale, causal);
+    GN_LAUNCH_CHECK("gn_attn_fwd (generic mfma)");
+    return GN_OK;
+}
+
+template <typename T, int NP>
+int gen_fwd_dispatch(const AttnWs& w, const void* Q, const void* K, const void* V, const float* kb,
+                     void* O, float* LSE, int B, int H, int S, int D, float scale, int causal,
+                     int rope_mode, float theta, hipStream_t s) {
+    switch (D) {
+        case 32: return launch_gen_fwd<T, 32, NP>(w, Q, K, V, kb, O, LSE, B, H, S, scale, causal, rope_mode, theta, s);
+        case 64: return launch_gen_fwd<T, 64, NP>(w, Q, K, V, kb, O, LSE, B, H, S, scale, causal, rope_mode, theta, s);
+        case 96: return launch_gen_fwd<T, 96, NP>(w, Q, K, V, kb, O, LSE, B, H, S, scale, causal, rope_mode, theta, s);
+        case 128: return launch_gen_fwd<T, 128, NP>(w, Q, K, V, kb, O, LSE, B, H, S, scale, causal, rope_mode, theta, s);
+        case 192: return launch_gen_fwd<T, 192, NP>(w, Q, K, V, kb, O, LSE, B, H, S, scale, causal, rope_mode, theta, s);
+        case 256: return launch_gen_fwd<T, 256, NP>(w, Q, K, V, kb, O, LSE, B, H, S, scale, causal, rope_mode, theta, s);
+    }
+    set_error("gn_attn_fwd: generic path has no D=%d", D);
+    return GN_E_INVALID;
+}
+
+template <typename T, int NP>
+int gen_bwd_dispatch(const AttnWs& w, const void* Q, const void* K, const void* V, const void* O,
+                     const void* dO, const float* LSE, const float* mask, void* dQ, void* dK,
+                     void* dV, int B, int H, int S, int D, float scale, int causal, int rope_mode,
+                     float theta, hipStream_t s) {
+#define GN_GEN(DV)                                                                              \
+    case DV:                                                                                    \
+        return launch_gen_bwd<T, DV, NP>(w, Q, K, V, O, dO, LSE, mask, dQ, dK, dV, B, H, S, scale, \
+                                         causal, rope_mode, theta, s);
+    switch (D) {
+        GN_GEN(32)
+        GN_GEN(96)
+        GN_GEN(192)
+        GN_GEN(256)
+        GN_GEN(64)
+        GN_GEN(128)
+    }
+#undef GN_GEN
+    set_error("gn_attn_bwd: generic path has no D=%d", D);
+    return GN_E_INVALID;
+}
+
 template <typename T>
 int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, const void* dO,
                   const float* LSE, const float* mask, void* dQ, void* dK, void* dV, int B, int H,
@@ -1192,8 +1795,24 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
     bool al16 = true;
     for (const void* p : ptrs) al16 = al16 && ((reinterpret_cast<uintptr_t>(p) & 15u) == 0);
     const bool mfma_ok = sizeof(T) == 2 && (D == 64 || D == 128) && al16;
+    // the generic matrix-core path for the other D and for fp32
+    const bool gen_ok = !mfma_ok && gen_dim(D) && al16 && BH * S * (int64_t)D < ((int64_t)1 << 31);
+    if (gen_ok) {
+        AttnWs w;
+        const int kind = sizeof(T) == 4 ? kWsGen2 : kWsGen1;
+        const size_t need = ws_layout(BH, S, D, sizeof(T), kind, ws, &w);
+        if (!ws || ws_bytes < need) {
+            set_error("gn_attn_bwd: workspace %zu B < %zu B", ws_bytes, need);
+            return GN_E_WORKSPACE;
+        }
+        if (sizeof(T) == 4)
+            return gen_bwd_dispatch<T, 2>(w, Q, K, V, O, dO, LSE, mask, dQ, dK, dV, B, H, S, D, scale,
+                                          causal, rope_mode, theta, s);
+        return gen_bwd_dispatch<T, 1>(w, Q, K, V, O, dO, LSE, mask, dQ, dK, dV, B, H, S, D, scale,
+                                      causal, rope_mode, theta, s);
+    }
     AttnWs w;
-    const size_t need = ws_layout(BH, S, D, sizeof(T), mfma_ok, ws, &w);
+    const size_t need = ws_layout(BH, S, D, sizeof(T), mfma_ok ? kWsMfma : kWsSimt, ws, &w);
     if (!ws || ws_bytes < need) {
         set_error("gn_attn_bwd: workspace %zu B < %zu B", ws_bytes, need);
         return GN_E_WORKSPACE;
@@ -1238,12 +1857,25 @@ int attn_bwd_impl(const void* Q, const void* K, const void* V, const void* O, co
 
 using namespace gn;
 
+extern "C" size_t gn_attn_workspace_bytes_dtype(int B, int H, int S, int D, int dtype) {
+    if (B <= 0 || H <= 0 || S <= 0 || D <= 0) return 0;
+    const int64_t BH = (int64_t)B * H;
+    const size_t esz = dtype == GN_BF16 ? 2 : 4;
+    // the path a call takes depends on D, the dtype and the pointers' alignment (unaligned
+    // views fall back to the SIMT kernels): the largest layout among the candidates
+    size_t need = ws_layout(BH, S, D, esz, kWsSimt, nullptr, nullptr);
+    size_t alt = 0;
+    if (dtype == GN_BF16 && (D == 64 || D == 128)) alt = ws_layout(BH, S, D, 2, kWsMfma, nullptr, nullptr);
+    else if (gen_dim(D)) alt = ws_layout(BH, S, D, esz, dtype == GN_BF16 ? kWsGen1 : kWsGen2, nullptr, nullptr);
+    return need > alt ? need : alt;
+}
+
 extern "C" size_t gn_attn_workspace_bytes(int B, int H, int S, int D) {
     if (B <= 0 || H <= 0 || S <= 0 || D <= 0) return 0;
     // the larger of the two layouts, so one query covers every dtype and path
-    const size_t simt = ws_layout((int64_t)B * H, S, D, 4, false, nullptr, nullptr);
-    const size_t mfma = ws_layout((int64_t)B * H, S, D, 2, true, nullptr, nullptr);
-    return simt > mfma ? simt : mfma;
+    return gn_attn_workspace_bytes_dtype(B, H, S, D, GN_F32) > gn_attn_workspace_bytes_dtype(B, H, S, D, GN_BF16)
+               ? gn_attn_workspace_bytes_dtype(B, H, S, D, GN_F32)
+               : gn_attn_workspace_bytes_dtype(B, H, S, D, GN_BF16);
 }
 
 static int attn_check(const void* Q, const void* K, const void* V, int B, int H, int S, int D,
@@ -1310,7 +1942,7 @@ extern "C" int gn_attn_bwd_bshd_mask(const void* Q, const void* K, const void* V
                    "gn_attn_bwd_bshd: pointers (and the workspace) must be 16-byte aligned");
     AttnWs w;
     const int64_t BH = (int64_t)B * H;
-    const size_t need = ws_layout(BH, S, D, 2, true, ws, &w);
+    const size_t need = ws_layout(BH, S, D, 2, kWsMfma, ws, &w);
     if (!ws || ws_bytes < need) {
         set_error("gn_attn_bwd_bshd: workspace %zu B < %zu B", ws_bytes, need);
         return GN_E_WORKSPACE;
@@ -1356,11 +1988,27 @@ extern "C" int gn_attn_fwd_mask(const void* Q, const void* K, const void* V, con
     AttnWs w;
     // MFMA path: rotated bf16 Q, K, the cos/sin table (the backward's layout) and the key
     // bias; SIMT path: rotated Q, K and the key bias
-    const size_t need = mfma ? ws_layout((int64_t)B * H, S, D, 2, true, ws, &w)
-                             : ws_layout((int64_t)B * H, S, D, esz, false, ws, &w);
+    const size_t need = mfma ? ws_layout((int64_t)B * H, S, D, 2, kWsMfma, ws, &w)
+                             : ws_layout((int64_t)B * H, S, D, esz, kWsSimt, ws, &w);
     if ((rope_mode != GN_ROPE_NONE || key_mask) && (!ws || ws_bytes < need)) {
         set_error("gn_attn_fwd: workspace %zu B < %zu B", ws_bytes, need);
         return GN_E_WORKSPACE;
+    }
+    // the generic matrix-core forward for the other D and fp32, when a workspace is given
+    const bool gen = !mfma && gen_dim(D) && al16(Q) && al16(K) && al16(V) && al16(O) && al16(ws) &&
+                     rows * D < ((int64_t)1 << 31) &&
+                     ws_bytes >= ws_layout((int64_t)B * H, S, D, esz, dtype == GN_BF16 ? kWsGen1 : kWsGen2,
+                                           nullptr, nullptr);
+    if (gen) {
+        ws_layout((int64_t)B * H, S, D, esz, dtype == GN_BF16 ? kWsGen1 : kWsGen2, ws, &w);
+        const float* kbg;
+        const int* ktg;
+        key_bias(key_mask, w, B, S, s, &kbg, &ktg);
+        if (dtype == GN_BF16)
+            return gen_fwd_dispatch<bf16_t, 1>(w, Q, K, V, kbg, O, LSE, B, H, S, D, scale, causal,
+                                               rope_mode, rope_theta, s);
+        return gen_fwd_dispatch<float, 2>(w, Q, K, V, kbg, O, LSE, B, H, S, D, scale, causal,
+                                          rope_mode, rope_theta, s);
     }
     const float* kb;
     const int* kt;

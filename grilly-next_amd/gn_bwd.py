@@ -30,7 +30,7 @@ SYMBOLS = [
     "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd",
     "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
     "gn_rmsnorm_bwd_stat", "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
-    "gn_attn_workspace_bytes", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_attn_fwd_mask",
+    "gn_attn_workspace_bytes", "gn_attn_workspace_bytes_dtype", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_attn_fwd_mask",
     "gn_attn_bwd_mask", "gn_attn_bwd_bshd_mask", "gn_vsa_unpack_project_bwd",
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_vsa_unpack_project_fwd",
     "gn_vsa_fwd_workspace_bytes", "gn_vsa_surrogate_fwd", "gn_embedding_bwd", "gn_binary_bwd",
@@ -99,6 +99,7 @@ _SIGS = {
     "gn_attn_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P,
                      _Z, _P], _I),
     "gn_attn_workspace_bytes": ([_I, _I, _I, _I], _Z),
+    "gn_attn_workspace_bytes_dtype": ([_I, _I, _I, _I, _I], _Z),
     "gn_attn_bwd_bshd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _F, _I,
                           _I, _F, _I, _P, _Z, _P], _I),
     "gn_attn_fwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _F, _I, _P, _Z, _P], _I),

@@ -246,13 +246,21 @@ int gn_xent_bwd(const void* logits, const int32_t* targets, void* dLogits, int r
  * Q, K, V, O, dO, dQ, dK, dV: [B, H, S, D]; LSE fp32 [B*H*S] = log sum_j exp(scale*q.k_j).
  * Q and K are the *pre-rotation* tensors; dQ, dK are gradients w.r.t. them.
  * rope_theta = base (10000); positions are 0..S-1.
- * ws: gn_attn_workspace_bytes(B, H, S, D). D must be 64 or 128 on the bf16 path. */
+ * ws: gn_attn_workspace_bytes(B, H, S, D) (or gn_attn_workspace_bytes_dtype).  D even, <= 256. */
 int gn_attn_bwd(const void* Q, const void* K, const void* V, const void* O, const void* dO,
                 const float* LSE, void* dQ, void* dK, void* dV, int B, int H, int S, int D,
                 float scale, int causal, int rope_mode, float rope_theta, int dtype,
                 void* ws, size_t ws_bytes, void* stream);
 
 size_t gn_attn_workspace_bytes(int B, int H, int S, int D);
+
+/* The attention workspace for one dtype (GN_F32 or GN_BF16): the largest layout among the
+ * paths a call of that dtype and shape can take.  gn_attn_workspace_bytes is the larger of
+ * the two.  Paths: bf16 with D = 64 or 128 runs the tuned matrix-core kernels; bf16 with
+ * D = 32, 96, 192 or 256 and fp32 with D = 32, 64, 96, 128, 192 or 256 run the generic
+ * matrix-core kernels (fp32 as a two-piece bf16 split with three products, fp32-grade);
+ * other D (even, <= 256) and views that are not 16-byte aligned run SIMT kernels. */
+size_t gn_attn_workspace_bytes_dtype(int B, int H, int S, int D, int dtype);
 
 /* Same backward on the [B, S, H, D] layout with row strides, so a fused QKV projection
  * output [B*S, 3*H*D] feeds it (and its gradient buffer receives dQ, dK, dV) without head
