@@ -275,7 +275,7 @@ def bench_attn32(args, torch, gn):
     g.manual_seed(3)
     Q, K, V = (torch.randn(B, H, S, D, device=dev, generator=g) for _ in range(3))
     dO = torch.randn(B, H, S, D, device=dev, generator=g) * 1e-2
-    ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D), dev)
+    ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D, gn.F32), dev)
     O, LSE = gn.attn_fwd(Q, K, V, causal=True, rope="interleaved", ws=ws)
     out = (torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V))
     ms = timed(torch, lambda: gn.attn_bwd(Q, K, V, O, dO, LSE, causal=True, rope="interleaved",
@@ -306,7 +306,7 @@ def bench_attn(args, torch, gn):
     bf = torch.bfloat16
     Q, K, V = (torch.randn(B, H, S, D, device=dev, generator=g).to(bf) for _ in range(3))
     dO = (torch.randn(B, H, S, D, device=dev, generator=g) * 1e-2).to(bf)
-    ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D), dev)
+    ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D, gn.BF16), dev)
     O, LSE = gn.attn_fwd(Q, K, V, causal=True, rope="interleaved", ws=ws)
     out = (torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V))
     ms = timed(torch, lambda: gn.attn_bwd(Q, K, V, O, dO, LSE, causal=True, rope="interleaved",

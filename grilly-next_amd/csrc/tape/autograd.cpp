@@ -384,7 +384,7 @@ void BackwardEngine::bwd_attention(Node* n) {
         if (!lse) throw std::invalid_argument("FlashAttention2: saved LSE missing");
         const size_t es = TensorRef::elem_size(qkv.dtype);
         uint64_t dqkv = alloc_grad(qkv.size_bytes());
-        const size_t wsb = gn_attn_workspace_bytes(B, H, S, D);
+        const size_t wsb = gn_attn_workspace_bytes_dtype(B, H, S, D, gn_dtype(qkv.dtype, "FlashAttention2"));
         uint64_t ws = alloc_grad(wsb);
         const char* base = static_cast<const char*>(P(qkv.buffer_id));
         char* gbase = static_cast<char*>(P(dqkv));
@@ -411,7 +411,7 @@ void BackwardEngine::bwd_attention(Node* n) {
     const uint64_t lse = n->saved_buffer_ids[0];
     if (!lse) throw std::invalid_argument("FlashAttention2: saved LSE missing");
     uint64_t dQ = alloc_grad(q.size_bytes()), dK = alloc_grad(k.size_bytes()), dV = alloc_grad(v.size_bytes());
-    const size_t wsb = gn_attn_workspace_bytes(B, H, S, D);
+    const size_t wsb = gn_attn_workspace_bytes_dtype(B, H, S, D, gn_dtype(q.dtype, "FlashAttention2"));
     uint64_t ws = alloc_grad(wsb);
     const float* mask = attention_mask(n, 3, B, S);
     gn_call(gn_attn_bwd_mask(P(q.buffer_id), P(k.buffer_id), P(v.buffer_id),

@@ -58,7 +58,7 @@ class Decoder:
     def forward(self):
         B, S, H, d, T = self.B, self.S, self.H, self.d, self.T
         D = d // H
-        ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D), self.dev)
+        ws = gn.workspace(gn.attn_workspace_bytes(B, H, S, D, gn.BF16), self.dev)
         bf = torch.bfloat16
         x = self.E[self.ids.long()].float().contiguous()  # fp32 residual stream
         self.x0 = x

@@ -421,8 +421,12 @@ def xent_bwd(logits, targets, scale=1.0, dLogits=None):
     return dLogits
 
 
-def attn_workspace_bytes(B, H, S, D):
-    return int(lib().gn_attn_workspace_bytes(B, H, S, D))
+def attn_workspace_bytes(B, H, S, D, dtype=None):
+    """Workspace bytes for one dtype (torch dtype or a GN_* code); None: either dtype."""
+    if dtype is None:
+        return int(lib().gn_attn_workspace_bytes(B, H, S, D))
+    code = dtype if isinstance(dtype, int) else (BF16 if dtype == torch.bfloat16 else F32)
+    return int(lib().gn_attn_workspace_bytes_dtype(B, H, S, D, code))
 
 
 def attn_bwd(Q, K, V, O, dO, LSE, scale=None, causal=True, rope="interleaved", theta=10000.0,
@@ -433,7 +437,7 @@ def attn_bwd(Q, K, V, O, dO, LSE, scale=None, causal=True, rope="interleaved", t
     dQ, dK, dV = out if out is not None else (torch.empty_like(Q), torch.empty_like(K),
                                               torch.empty_like(V))
     if ws is None:
-        ws = workspace(attn_workspace_bytes(B, H, S, D), Q.device)
+        ws = workspace(attn_workspace_bytes(B, H, S, D, Q.dtype), Q.device)
     if mask is None:
         _check(lib().gn_attn_bwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(LSE), _ptr(dQ),
                                  _ptr(dK), _ptr(dV), B, H, S, D, scale, int(causal), ROPE[rope],
@@ -457,7 +461,7 @@ def attn_bwd_qkv(qkv, O, dO, LSE, heads, scale=None, causal=True, rope="none", t
     scale = D ** -0.5 if scale is None else scale
     dqkv = out if out is not None else torch.empty_like(qkv)
     if ws is None:
-        ws = workspace(attn_workspace_bytes(B, heads, S, D), qkv.device)
+        ws = workspace(attn_workspace_bytes(B, heads, S, D, qkv.dtype), qkv.device)
     e = qkv.element_size()
     _check(lib().gn_attn_bwd_bshd_mask(_ptr(qkv), _off(qkv, HD * e), _off(qkv, 2 * HD * e),
                                        _ptr(O), _ptr(dO), _ptr(LSE), _ptr(mask), _ptr(dqkv),
@@ -476,7 +480,7 @@ def attn_fwd(Q, K, V, scale=None, causal=True, rope="interleaved", theta=10000.0
     O = torch.empty_like(Q)
     LSE = torch.empty((B, H, S), dtype=torch.float32, device=Q.device)
     if ws is None:
-        ws = workspace(attn_workspace_bytes(B, H, S, D), Q.device)
+        ws = workspace(attn_workspace_bytes(B, H, S, D, Q.dtype), Q.device)
     _check(lib().gn_attn_fwd_mask(_ptr(Q), _ptr(K), _ptr(V), _ptr(mask), _ptr(O), _ptr(LSE), B,
                                   H, S, D, scale, int(causal), ROPE[rope], theta, _dt(Q), _ptr(ws),
                                   ws.numel(), _stream()), "gn_attn_fwd")
