@@ -152,6 +152,15 @@ template <> struct chunk8<bf16_t> {
     }
 };
 
+// Orders one wave's LDS accesses across its lanes (writes of some lanes before reads of
+// others, or reads before the next overwrite) without a block barrier: wave-scope release and
+// acquire fences around a wave barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 inline unsigned grid_for(int64_t n, int per_block, unsigned cap = 65535u * 16u) {
     int64_t g = (n + per_block - 1) / per_block;
     if (g < 1) g = 1;

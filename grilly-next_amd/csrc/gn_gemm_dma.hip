@@ -278,11 +278,13 @@ __device__ __forceinline__ void glu_epilogue(const GemmDesc& g, const f32x16_t (
         if constexpr (!AHEAD) {
             if constexpr (i > 0) glu_fetch<WN>(g, mbase + i * 32, nbase, lane, t[0]);
         }
+        wave_lds_sync();  // the previous strip's reads (other lanes) before these writes
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        wave_lds_sync();  // these writes before other lanes read them
         if constexpr (AHEAD && i + 1 < FM) glu_fetch<WN>(g, mbase + (i + 1) * 32, nbase, lane, t[cur ^ 1]);
         glu_store<KIND, WN>(g, st, mbase + i * 32, nbase, lane, t[cur]);
     });
@@ -684,13 +686,17 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
         return;
     }
     const int rq = (lane >> 5) * 4;
+    // the strip is private to the wave but each lane reads rows other lanes wrote: wave-scope
+    // fences around a wave barrier order the accesses (no instructions on a wave64 CU)
     auto strip = [&](auto I_) {
         constexpr int i = decltype(I_)::value;
+        wave_lds_sync();
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        wave_lds_sync();
         if constexpr (EPI == 0 && sizeof(CT) == 4) {
             if (g.ksplit > 2) {
                 epilogue_part<WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
@@ -936,11 +942,13 @@ __global__ __launch_bounds__(64 * kVsaNW, 1) void vsa_dw_dma(VsaDesc v) {
     g.accumulate = v.accumulate;
     auto strip = [&](auto I_) {
         constexpr int i = decltype(I_)::value;
+        wave_lds_sync();
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 st[(8 * (r >> 2) + rq + (r & 3)) * (WN + 4) + j * 32 + (lane & 31)] = acc[i][j][r];
+        wave_lds_sync();
         epilogue_rows<float, 0, WN>(g, st, m0 + wm * WM + i * 32, n0 + wn * WN, lane);
     };
     strip(std::integral_constant<int, 0>{});

@@ -304,9 +304,15 @@ __global__ __launch_bounds__(256, 2) void gemm_f32x6(GemmDesc g) {
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
+                // the strip is private to the wave, but its lanes read what other lanes wrote:
+                // wave-scope release/acquire around a wave barrier order the writes before the
+                // reads (and the reads before the next tile's writes, below); no instruction
+                // is emitted for them on a wave64 CU
+                wave_lds_sync();
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     strip[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 40 + (lane & 31)] = acc[i][j][r];
+                wave_lds_sync();
                 const int n = n0 + rb0 + j * 32 + 4 * (lane & 7);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {

@@ -298,18 +298,26 @@ bool skinny_fwd_applicable(const void* X, const void* W, const void* Y, int M, i
 }
 
 // (register budget: the rows' X chunks and dX partials, MT x Q float4 each, stay <= 8 x 2)
-bool skinny_bwd_applicable(const void* dY, const void* X, const void* W, const void* dX,
-                           const void* dW, int M, int K) {
+// The shapes the skinny backward takes (rows, K and the per-lane register budget mt * q); the
+// workspace query and the dispatch share it, so no shape gets a workspace it never uses.
+static bool skinny_bwd_shape_ok(int M, int K) {
     if (!(M >= 1 && M <= kSkinnyMaxM && K > 0 && K % 4 == 0 && K <= 4 * 256 * kSkinnyMaxQ))
         return false;
     const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
     const int q = (K / 4 + 255) / 256;
-    return mt * q <= 16 && al16(X) && al16(W) && al16(dW) && (!dX || al16(dX)) && dY != nullptr;
+    return mt * q <= 16;
 }
 
-// Workspace for the deterministic dX reduction: one [M x K] fp32 plane per row-range block.
+bool skinny_bwd_applicable(const void* dY, const void* X, const void* W, const void* dX,
+                           const void* dW, int M, int K) {
+    return skinny_bwd_shape_ok(M, K) && al16(X) && al16(W) && al16(dW) && (!dX || al16(dX)) &&
+           dY != nullptr;
+}
+
+// Workspace for the deterministic dX reduction: one [M x K] fp32 plane per row-range block
+// (0 for shapes the skinny kernel does not take).
 size_t skinny_bwd_ws_bytes(int M, int N, int K) {
-    if (M < 1 || M > kSkinnyMaxM || N <= 0 || K <= 0 || K % 4) return 0;
+    if (N <= 0 || !skinny_bwd_shape_ok(M, K)) return 0;
     return (size_t)bwd_shape(M, N, K).blocks * M * K * sizeof(float);
 }
 

@@ -184,7 +184,14 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
             if (!in.requires_grad || cur->grad_input_buffers[i] == 0 || ((handled_ >> i) & 1u))
                 continue;
             const bool own = !((borrowed_ >> i) & 1u);
-            if (writes_in_place(cur, in.buffer_id))
+            // an in-place node's first input with this id replaces the entry (it becomes the
+            // input version's gradient); a later input with the same id (Add(x, x) written
+            // into x) adds onto it, as the out-of-place form does
+            bool first = true;
+            for (uint32_t j = 0; j < i && first; ++j)
+                first = !(cur->inputs[j].buffer_id == in.buffer_id && cur->inputs[j].requires_grad &&
+                          cur->grad_input_buffers[j] != 0 && !((handled_ >> j) & 1u));
+            if (first && writes_in_place(cur, in.buffer_id))
                 replace(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(), own);
             else
                 contribute(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(), own);

@@ -81,7 +81,9 @@ const char* gn_version(void);
 
 /* ---- linear ----------------------------------------------------------------------- */
 /* Replaces BackwardEngine::backward_linear / backward_linear_chunked
- * (cpp/src/autograd.cpp:172-483) and fnn-linear-backward.glsl:43-89.
+ * (cpp/src/autograd.cpp:172-483) and fnn-linear-backward.glsl:43-89.  fp32 products follow
+ * gn_gemm's fp32 rules below (matrix-core split above the small-product sizes: fp32-grade per
+ * element, NaN where an operand is inf).
  *   dX = dY W      [M x K]  (skipped when dX == NULL: input needs no grad, autograd.cpp:259)
  *   dW = dY^T X    [N x K]
  *   db = sum_rows dY [N]    (skipped when db == NULL)
@@ -108,7 +110,15 @@ size_t gn_linear_workspace_bytes(int M, int N, int K, int dtype);
  *   transA = 0: A_s is [M x Ks] row-major;  transA = 1: A_s is stored [Ks x M] (i.e. A_s^T).
  *   transB = 0: B_s is [Ks x N] row-major;  transB = 1: B_s is stored [N x Ks].
  * dtype GN_BF16: A, B bf16, fp32 accumulation, C is bf16 (c_dtype GN_BF16) or fp32 (GN_F32).
- * dtype GN_F32: all fp32. */
+ * dtype GN_F32: all fp32.  Small products (k <= 128 and M*N*k <= 2^24) are plain fp32 FMA
+ * chains.  Larger ones with M, N, K multiples of 4 and 16-byte aligned operands run on the
+ * bf16 matrix cores: each element x is split into three bf16 pieces (|x - x0 - x1 - x2| <=
+ * 2^-25 |x|) and six piece products are accumulated in fp32, so each product term is within
+ * ~2^-24 |a b| (fp32-grade: the sum carries fp32 accumulation error on top).  That path has
+ * two documented limits: an inf operand, or one above the bf16 maximum (|x| > 3.3895e38),
+ * makes every output it feeds NaN (inf - inf in the split) where fp32 FMA gives inf; and
+ * operands below the fp32 normal range (|x| < 2^-126) may lose their pieces to denormal
+ * flushing on the matrix cores (relative accuracy holds down to about 2^-100 |x|max). */
 int gn_gemm(const void* A0, const void* B0, int K0, const void* A1, const void* B1, int K1,
             void* C, int M, int N, int transA, int transB, int dtype, int c_dtype,
             unsigned flags, void* stream);

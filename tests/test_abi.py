@@ -98,6 +98,20 @@ def test_workspace_query_covers_accumulating_launches():
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
+def test_fp32_workspace_query_only_sizes_paths_the_shape_takes():
+    # M <= 8 rows but K too wide for the skinny kernel's registers (8 rows x 8192): the call
+    # takes the split-K GEMM, whose partial planes are a few MiB; the skinny kernel's planes
+    # (one M x K plane per row block, ~256 MiB here) must not be asked for
+    import gn_bwd
+    lib = gn_bwd.lib()
+    wide = lib.gn_linear_workspace_bytes(8, 163840, 8192, 0)
+    assert wide < 64 << 20
+    # a shape the skinny kernel does take (one row, the hypernetwork's output layer) keeps its
+    # deterministic dX planes
+    assert lib.gn_linear_workspace_bytes(1, 163840, 1536, 0) > 0
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
 def test_misaligned_attention_views_rejected_without_gpu():
     # the [B,S,H,D] entry takes only 16-byte aligned tensors (its kernels move 16-byte
     # chunks); the check runs before any HIP call, so it is safe without a device

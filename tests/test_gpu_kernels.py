@@ -173,6 +173,32 @@ def test_gemm_fp32_two_segments_and_accumulate(gn):
     assert rel_err(host(C), ref + A0.astype(np.float64) @ B0) < FP32_TOL
 
 
+def test_gemm_fp32_split_non_finite_and_tiny_operands(gn):
+    """The documented limits of the fp32 matrix-core split (include/gn_bwd.h, gn_gemm): an inf
+    in A makes its whole output row NaN (the split forms inf - inf) while every other row stays
+    fp32-grade; operands scaled into the low normal range (1e-30) keep the relative bound; the
+    small-product FMA path keeps IEEE inf."""
+    r = rng_(35)
+    M, N, K = 128, 128, 256  # k > 128: the split path
+    A = r.standard_normal((M, K)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    A[3, 5] = np.inf
+    C = host(gn.gemm(dev(A), dev(B)))
+    assert np.all(np.isnan(C[3]))
+    rest = np.arange(M) != 3
+    ref = A[rest].astype(np.float64) @ B
+    assert rel_err(C[rest], ref) < FP32_TOL
+    At = (r.standard_normal((M, K)) * 1e-30).astype(np.float32)
+    Ct = host(gn.gemm(dev(At), dev(B)))
+    assert rel_err(Ct, At.astype(np.float64) @ B) < FP32_TOL
+    # small-product path (k <= 128): IEEE inf, finite elsewhere
+    As = r.standard_normal((16, 64)).astype(np.float32)
+    As[2, 7] = np.inf
+    Bs = np.abs(r.standard_normal((64, 8))).astype(np.float32) + 0.5
+    Cs = host(gn.gemm(dev(As), dev(Bs)))
+    assert np.all(np.isposinf(Cs[2])) and np.all(np.isfinite(np.delete(Cs, 2, axis=0)))
+
+
 # Small fp32 products (k <= 128 and M*N*k <= 2^24) take a one-thread-per-output kernel with a
 # sequential fp32 k loop; the shapes straddle both limits, so each pair runs on the two paths.
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])

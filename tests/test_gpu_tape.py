@@ -222,6 +222,19 @@ def test_same_buffer_contributions_are_summed(env):
     assert rel_err(grad(gb, dev, tape, x), 2 * g) < 1e-6
     tape.end()
 
+    # in-place Add(x, x) written into x itself: both inputs are the input version of x, so its
+    # gradient is 2 g as in the out-of-place form (the first input replaces the entry, the
+    # second adds onto it)
+    y = x.clone().contiguous()
+    u3 = ((y + y) @ W.t()).contiguous()
+    tape.begin()
+    tape.record_op(gc.OpType.Add, [gb.tref(y, True), gb.tref(y, True)], [gb.tref(y)])
+    n = tape.record_op(gc.OpType.Linear, [gb.tref(y, True)], [gb.tref(u3)])
+    tape.save_for_backward(n, [W.data_ptr(), 0])
+    tape.backward(n, dU.data_ptr())
+    assert rel_err(grad(gb, dev, tape, y), 2 * g) < 1e-6
+    tape.end()
+
 
 def test_attention_and_layernorm_nodes(env):
     gc, gb, dev = env
