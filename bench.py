@@ -177,7 +177,9 @@ def ceilings(torch, gn):
     """Measured ceilings: gn_probe_mfma (no memory traffic) and gn_probe_copy (2 GiB, every
     access mode; the best copy and the read-only stream are reported)."""
     import ctypes
-    lib = gn.lib()
+    gn.lib()
+    # the probes live in their own library next to libgn_bwd.so (not part of the backward ABI)
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(gn.__file__)), "libgn_probe.so"))
     lib.gn_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.gn_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                   ctypes.c_void_p]
@@ -429,7 +431,10 @@ def bench_mlp(args, torch, gn):
         tape.backward(record(), 0)
         tape.end()
     ms = timed(torch, step, args.steps, args.warmup)
-    graph = graph_replay(torch, grilly_core, device, tape, record, args, ms)
+    # the graph comparison: both forms over 200 launch-bound steps
+    reps = max(args.steps, 200)
+    eager_reps = timed(torch, step, reps, reps // 10)
+    graph = graph_replay(torch, grilly_core, device, tape, record, args, eager_reps, reps)
     flops = 2.0 * Bsz * (784 * 256 + 256 * 10 + 256 * 10)
     cpu = None
     if not args.no_cpu:
@@ -447,23 +452,28 @@ def bench_mlp(args, torch, gn):
     return out
 
 
-def graph_replay(torch, grilly_core, device, tape, record, args, eager_ms):
+def graph_replay(torch, grilly_core, device, tape, record, args, eager_ms, reps=None):
     """The same backward captured once into a HIP graph (grilly_core.OpGraph, the replacement
     of the reference's OpGraph) and replayed: one hipGraphLaunch per step in place of the tape
     walk (begin / record / backward / end) and its per-kernel launches.  Same kernels, same
-    buffers, same work per step."""
+    buffers, same work per step.  reps: replays timed (a launch-bound step needs more than
+    --steps for a stable mean; the eager figure it is compared with is then re-timed over the
+    same count)."""
+    steps = reps or args.steps
+    warm = max(args.warmup, steps // 10)
     g = grilly_core.OpGraph()
     tape.begin()
     g.capture_backward(tape, record(), 0)
     tape.end()
     g.optimize(device)
-    ms = timed(torch, lambda: g.execute(device), args.steps, args.warmup)
+    ms = timed(torch, lambda: g.execute(device), steps, warm)
     counts = g.node_counts()
     g.clear()
     return {"ms_per_step": round(ms, 4), "eager_ms_per_step": round(eager_ms, 4),
             "speedup": round(eager_ms / ms, 3), "kernel_nodes": counts["kernel"],
-            "memset_nodes": counts["memset"], "memcpy_nodes": counts["memcpy"],
-            "how": "grilly_core.OpGraph.capture_backward once, then execute() per step"}
+            "memset_nodes": counts["memset"], "memcpy_nodes": counts["memcpy"], "replays": steps,
+            "how": "grilly_core.OpGraph.capture_backward once, then execute() per step, "
+                   f"mean over {steps} replays (eager step over the same count)"}
 
 
 def mlp_cpu_baseline(X, y, W1, W2, Z, H, L):

@@ -1,6 +1,7 @@
 """Builds the native libraries of this package, in-tree, for gfx950.
 
   libgn_bwd.so          HIP kernels + the C ABI declared in include/gn_bwd.h
+  libgn_probe.so        measurement kernels of include/gn_probe.h (bench.py --ceilings only)
   _grilly_core*.so      pybind11 module, imported through grilly_core.py: tape engine (TensorRef,
                         OpType, Node, TapeArena,
                         BackwardEngine, TapeContext) calling libgn_bwd through the C ABI
@@ -22,8 +23,11 @@ INCLUDE = os.path.join(ROOT, "include")
 ARCH = os.environ.get("GN_OFFLOAD_ARCH", "gfx950")
 
 KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip", "gn_gemm_dma.hip",
-                  "gn_vsa.hip", "gn_attn.hip", "gn_optim.hip", "gn_tapeops.hip", "gn_fwd.hip",
-                  "gn_probe.hip", "gn_skinny.hip", "gn_vsa_fwd.hip", "gn_gemm_f32.hip"]
+                  "gn_gemm_dma_f32a.hip", "gn_gemm_dma_f32b.hip", "gn_gemm_dma_bf16.hip",
+                  "gn_gemm_dma_glu.hip", "gn_vsa.hip", "gn_attn.hip", "gn_optim.hip", "gn_tapeops.hip",
+                  "gn_fwd.hip", "gn_skinny.hip", "gn_vsa_fwd.hip", "gn_gemm_f32.hip"]
+# measurement kernels for bench.py --ceilings, kept out of the backward library
+PROBE_SOURCES = ["gn_probe.hip"]
 TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "tape/checkpoint.cpp", "tape/hypernet.cpp",
                 "tape/op_graph.cpp", "bindings.cpp"]
 
@@ -53,15 +57,25 @@ def _obj(src):
 
 def build_kernels(jobs=8):
     os.makedirs(BUILD, exist_ok=True)
+    srcs = KERNEL_SOURCES + PROBE_SOURCES
+    # the longest compiles first, so the pool's tail is short
+    srcs.sort(key=lambda s: -os.path.getsize(os.path.join(CSRC, s)))
     cmds = [["hipcc", *HIP_FLAGS, *FILE_FLAGS.get(s, []), "-c", os.path.join(CSRC, s), "-o", _obj(s)]
-            for s in KERNEL_SOURCES]
+            for s in srcs]
     with ThreadPoolExecutor(jobs) as ex:
         list(ex.map(_run, cmds))
-    out = os.path.join(HERE, "libgn_bwd.so")
-    _run(["hipcc", "-shared", f"--offload-arch={ARCH}", "-o", out + ".tmp",
-          *[_obj(s) for s in KERNEL_SOURCES]])
-    os.replace(out + ".tmp", out)
-    return out
+    link_kernels()
+    return os.path.join(HERE, "libgn_bwd.so")
+
+
+def link_kernels():
+    """libgn_bwd.so (the C ABI of include/gn_bwd.h) and libgn_probe.so (include/gn_probe.h)."""
+    for name, srcs in (("libgn_bwd.so", KERNEL_SOURCES),
+                       ("libgn_probe.so", PROBE_SOURCES + ["gn_errors.cpp"])):
+        out = os.path.join(HERE, name)
+        _run(["hipcc", "-shared", f"--offload-arch={ARCH}", "-o", out + ".tmp",
+              *[_obj(s) for s in srcs]])
+        os.replace(out + ".tmp", out)
 
 
 def build_tape(jobs=8, extra=()):

@@ -79,6 +79,12 @@ bool gemm_dma_applicable(const GemmDesc& g);
 // unbounded (0: none).
 size_t gemm_dma_part_bytes(const GemmDesc& g, int transA, int c_dtype);
 int gemm_dma_launch(const GemmDesc& g, int transA, int transB, int c_dtype, hipStream_t s);
+// Its instantiation units (gn_gemm_dma_{f32a,f32b,bf16,glu}.hip): fp32 C with A k-contiguous /
+// k-outer, bf16 C, and the GLU epilogue (untransposed operands only).
+int gemm_dma_f32_ta0(const GemmDesc& g, int transB, hipStream_t s);
+int gemm_dma_f32_ta1(const GemmDesc& g, int transB, hipStream_t s);
+int gemm_dma_bf16(const GemmDesc& g, int transA, int transB, hipStream_t s);
+int gemm_dma_glu(const GemmDesc& g, int transA, int transB, hipStream_t s);
 // C (+)= sum over y < g.ksplit of the planes at g.part (index order); N % 4 == 0, C and ldc
 // 16-byte aligned.
 void launch_split_reduce(const GemmDesc& g, hipStream_t s);

@@ -1,6 +1,7 @@
-/* gn_probe.h — measurement helpers exported by libgn_bwd.so next to the backward ABI.
- * They have no counterpart in the reference: bench.py --ceilings uses them to re-measure the
- * MFMA and HBM ceilings on the box it runs on.  All launches go on `stream`; no allocation. */
+/* gn_probe.h — measurement helpers exported by libgn_probe.so, a library of its own built next
+ * to libgn_bwd.so (they are not part of the backward ABI).  They have no counterpart in the
+ * reference: bench.py --ceilings uses them to re-measure the MFMA and HBM ceilings on the box it
+ * runs on.  All launches go on `stream`; no allocation. */
 #ifndef GN_PROBE_H
 #define GN_PROBE_H
 

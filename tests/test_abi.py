@@ -32,13 +32,18 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
-@pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
-def test_library_exports_the_probes():
+PROBE_LIB = os.path.join(PKG, "libgn_probe.so")
+
+
+@pytest.mark.skipif(not os.path.exists(PROBE_LIB), reason="libgn_probe.so not built")
+def test_probe_library_exports_the_probes():
+    """The ceiling probes live in libgn_probe.so, not in the backward library."""
     text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "gn_probe.h")).read(), flags=re.S)
     names = sorted(set(re.findall(r"\b(gn_[a-z0-9_]+)\s*\(", text)))
     assert names == ["gn_probe_copy", "gn_probe_mfma"]
-    lib = ctypes.CDLL(LIB)
-    assert all(hasattr(lib, n) for n in names)
+    probe = ctypes.CDLL(PROBE_LIB)
+    assert all(hasattr(probe, n) for n in names)
+    assert not any(hasattr(ctypes.CDLL(LIB), n) for n in names)
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
