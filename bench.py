@@ -59,14 +59,16 @@ def parse():
                    choices=["ffn", "attn", "attn32", "vsa", "mlp", "decoder", "hyper", "linear32"])
     p.add_argument("--calib-copy", action="store_true",
                    help="after the timed region, launch one gn_add_inplace over 2^28 floats "
-                        "(reads 2 GiB, writes 1 GiB): the reference dispatch that scales the "
-                        "FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
+                        "(reads 2 GiB, writes 1 GiB): the reference dispatch that sizes the "
+                        "L2 read requests of a --pmc run and checks its write requests")
     p.add_argument("--ceilings", action="store_true",
                    help="measure this box's MFMA (bf16 32x32x16 loop) and HBM (16-byte copy) "
                         "ceilings with the library's probe kernels and print them as JSON")
-    p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                   help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
-                        "'bench.py --calib-copy' into the HBM traffic of the dominant kernel")
+    p.add_argument("--pmc-summary", nargs=2, metavar=("READ_DIR", "WRITE_DIR"),
+                   help="summarise two rocprofv3 --pmc runs of 'bench.py --calib-copy' (read "
+                        "requests: TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_32B_sum TCC_BUBBLE_sum; write "
+                        "requests: TCC_EA0_WRREQ_sum TCC_EA0_WRREQ_64B_sum) into the HBM traffic "
+                        "of the dominant kernel")
     p.add_argument("--pmc-sq", metavar="DIR",
                    help="summarise a rocprofv3 --pmc run of SQ_INSTS_VALU SQ_INSTS_MFMA "
                         "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE per kernel (VALU instructions "
@@ -99,46 +101,58 @@ def calib_copy(torch, gn):
     torch.cuda.synchronize()
 
 
-def pmc_summary(fetch_dir, write_dir, call):
-    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of each launch of `call` (CALL_KERNELS) and of
-    the calibration add (known bytes) -> scaled HBM bytes per call, summed over its launches."""
+def pmc_summary(read_dir, write_dir, call):
+    """HBM traffic per call of `call` (CALL_KERNELS) from the L2 -> memory request counters,
+    summed over every TCC instance of the 8 XCDs (two --pmc passes of the same command):
+      reads:  TCC_EA0_RDREQ_sum (all read requests), TCC_EA0_RDREQ_32B_sum, TCC_BUBBLE_sum (the
+              128-byte ones as gfx950 documents them); an ordinary request's size is calibrated
+              on the add of --calib-copy, which reads exactly 2 GiB;
+      writes: TCC_EA0_WRREQ_sum, TCC_EA0_WRREQ_64B_sum (64-byte ones, the rest 32 bytes),
+              checked against the add's 1 GiB.
+    Each launch's per-dispatch mean is summed over the call's launches."""
     import csv
     import glob
     import re
 
-    def load(d, counter):
+    def load(d):
         out = {}
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             for r in csv.DictReader(open(path)):
-                if r["Counter_Name"] != counter:
-                    continue
-                key = (r["Kernel_Name"], r["Grid_Size"])
-                out.setdefault(key, {}).setdefault(r["Dispatch_Id"], 0.0)
-                out[key][r["Dispatch_Id"]] += float(r["Counter_Value"])
+                key = (r["Kernel_Name"], int(float(r["Grid_Size"])), r["Dispatch_Id"])
+                out.setdefault(key, {}).setdefault(r["Counter_Name"], 0.0)
+                out[key][r["Counter_Name"]] += float(r["Counter_Value"])
         return out
 
-    known = {"FETCH_SIZE": 2.0 * CALIB_FLOATS * 4, "WRITE_SIZE": 1.0 * CALIB_FLOATS * 4}
+    def mean(tab, pat, grid, counters):
+        rows = [v for (k, g, _), v in tab.items() if re.search(pat, k) and (grid is None or g == grid)]
+        if not rows:
+            raise SystemExit(f"no dispatch of {pat} (grid {grid})")
+        return len(rows), {c: sum(r.get(c, 0.0) for r in rows) / len(rows) for c in counters}
+
+    rd = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum")
+    wr = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
+    R, W = load(read_dir), load(write_dir)
+    _, ca = mean(R, "add_kernel", None, rd)
+    plain = ca[rd[0]] - ca[rd[1]] - ca[rd[2]]
+    bytes_per_req = (2.0 * CALIB_FLOATS * 4 - 32 * ca[rd[1]] - 128 * ca[rd[2]]) / plain
+    rbytes = lambda c: (c[rd[0]] - c[rd[1]] - c[rd[2]]) * bytes_per_req + 32 * c[rd[1]] + 128 * c[rd[2]]
+    wbytes = lambda c: (c[wr[0]] - c[wr[1]]) * 32 + 64 * c[wr[1]]
+    _, cw = mean(W, "add_kernel", None, wr)
+    lines = [f"call: {call}",
+             f"reads: calibration add {ca[rd[0]]:.0f} requests ({ca[rd[1]]:.0f} of 32 B, {ca[rd[2]]:.0f} "
+             f"of 128 B) for 2 GiB -> {bytes_per_req:.1f} B per ordinary request",
+             f"writes: calibration add {cw[wr[0]]:.0f} requests ({cw[wr[1]]:.0f} of 64 B) -> "
+             f"{wbytes(cw) / 2**30:.4f} GiB (1 GiB written)"]
     total = 0.0
-    lines = [f"call: {call}"]
-    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
-        tab = load(d, counter)
-        calib = [x for (k, g), v in tab.items() if "add_kernel" in k for x in v.values()]
-        if not calib:
-            raise SystemExit(f"{counter}: no calibration dispatch in {d}")
-        ckib = sum(calib) / len(calib)
-        factor = known[counter] / (ckib * 1024.0)
-        lines.append(f"{counter}: calibration add {ckib:.0f} KiB/dispatch (expected "
-                     f"{known[counter] / 1024:.0f} KiB) -> factor {factor:.4f}")
-        for pat, grid in CALL_KERNELS[call]:
-            vals = [x for (k, g), v in tab.items() if re.search(pat, k) and int(float(g)) == grid
-                    for x in v.values()]
-            if not vals:
-                raise SystemExit(f"{counter}: no dispatch of {pat} with grid {grid} in {d}")
-            kib = sum(vals) / len(vals)
-            b = kib * 1024.0 * factor
-            total += b
-            lines.append(f"  {pat.split('[')[0]}> grid {grid}: {kib:.0f} KiB/dispatch over "
-                         f"{len(vals)} dispatches -> {b / 1e6:.1f} MB")
+    for pat, grid in CALL_KERNELS[call]:
+        n, c = mean(R, pat, grid, rd)
+        _, w = mean(W, pat, grid, wr)
+        rb, wb = rbytes(c), wbytes(w)
+        total += rb + wb
+        lines.append(f"  {pat.split('[')[0]}> grid {grid}: {c[rd[0]]:.0f} read requests "
+                     f"({c[rd[1]]:.0f} of 32 B, {c[rd[2]]:.0f} of 128 B) -> {rb / 1e6:.1f} MB read; "
+                     f"{w[wr[0]]:.0f} write requests ({w[wr[1]]:.0f} of 64 B) -> {wb / 1e6:.1f} MB "
+                     f"written; mean over {n} dispatches")
     lines.append(f"traffic_bytes_per_call: {total:.0f}")
     print("\n".join(lines))
 
