@@ -978,7 +978,9 @@ def main():
                      "unit": dom["unit"], "frac": dom["frac"], "launch_ms": dom["ms"],
                      "traffic": traffic_from_profile(dom["call"].split(" = ")[0]),
                      "timing": "HIP events around the call inside every timed step, mean"},
-        "kernels_timing": f"per-call HIP events over {nb} steps of a pass before the timed region",
+        "kernels_timing": f"per-call HIP events over {nb} steps of a pass before the timed region; "
+                          "an event pair at every call boundary adds ~5-10 % to each call, so the "
+                          "calls sum above ms_per_step (the timed steps carry one pair only)",
         "kernels": kernels,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
