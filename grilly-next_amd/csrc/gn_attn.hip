@@ -267,7 +267,7 @@ struct DkdvCfg {
 //   dV += P^T dO, dK += dS^T Q    (A = P / dS straight from the accumulators,
 //                                  B = dO / Q columns by transpose reads)
 // The next tiles' Q, dO, L, D_i arrive by LDS DMA while the current one is computed.
-template <int D, int STAGES, int NW>
+template <int D, int STAGES, int NW, bool KB>
 __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     TDesc tQ, TDesc tK, TDesc tV, TDesc tG, const float* __restrict__ Lsc,
     const float* __restrict__ Di, const float2* __restrict__ cs, const float* __restrict__ kb,
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     const float c2 = scale * 1.4426950408889634f;
     // key-padding bias of this lane's key; the wave's 32 keys lie in one 64-key tile
     const int bb = bh / H;
-    const bool kmask = kb && kw0 < S && kt[bb * (Spad / 64) + kw0 / 64];
+    const bool kmask = KB && kw0 < S && kt[bb * (Spad / 64) + kw0 / 64];
     const float kbl = kmask && key < S ? kb[(size_t)bb * Spad + key] : 0.f;
 
     // the block's K and V rows stay in LDS (after the stages) for the whole block
@@ -344,7 +344,8 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
 
         // 32-query halves (keeps S, dP, P, dS of one half live).  Masked entries get
         // S = -inf, hence P = dS = 0 (L and D_i are finite everywhere, padding included);
-        // only tiles on the diagonal or the sequence end evaluate the mask.
+        // only tiles on the diagonal or the sequence end evaluate the mask (an empty volatile
+        // asm keeps the compiler from speculating the mask into every tile as selects).
 #pragma unroll
         for (int hh = 0; hh < HALVES; ++hh) {
             const int i = half0 + hh;
@@ -376,6 +377,7 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
             fb[0][0] = frag_cols<D>(sG, 32 * i, 0);
             fb[0][1] = frag_cols<D>(sQ, 32 * i, 0);
             if (!full) {
+                asm volatile("" ::: "memory");
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int q = q0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -391,7 +393,7 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
                 const float4 D4 = *reinterpret_cast<const float4*>(sD + ql);
                 float Lv[4] = {L4.x, L4.y, L4.z, L4.w};
                 const float Dv[4] = {D4.x, D4.y, D4.z, D4.w};
-                if (kmask) {  // wave-uniform: the bias rides on the L term
+                if (KB && kmask) {  // wave-uniform: the bias rides on the L term
 #pragma unroll
                     for (int e = 0; e < 4; ++e) Lv[e] -= kbl;
                 }
@@ -1627,7 +1629,8 @@ int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, const f
                     hipStream_t s) {
     using C1 = DkdvCfg<D, kStagesDkdv, kWavesDkdv>;
     using C2 = DqCfg<D, kStagesDq>;
-    static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>, C1::LDS);
+    static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, false>, C1::LDS) &&
+                            allow_lds(attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, true>, C1::LDS);
     static const bool ok2 = allow_lds(attn_dq_mfma<D, kStagesDq>, C2::LDS);
     if (!ok1 || !ok2) {
         set_error("gn_attn_bwd: cannot reserve LDS (%d / %d B)", C1::LDS, C2::LDS);
@@ -1652,9 +1655,11 @@ int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, const f
     const TDesc tQ = rope_mode != GN_ROPE_NONE ? bhsd(w.Qr, H, S, D) : io.Q;
     const TDesc tK = rope_mode != GN_ROPE_NONE ? bhsd(w.Kr, H, S, D) : io.K;
     const int nb = (S + 127) / 128;
-    hipLaunchKernelGGL((attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv>), dim3(BH, nb),
-                       dim3(64 * kWavesDkdv), C1::LDS, s, tQ, tK, io.V, io.dO, w.Lsc, w.Di, w.cs,
-                       kb, kt, io.dK, io.dV, H, S, Spad, scale, causal, rope_mode);
+    auto dkdv = kb ? attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, true>
+                   : attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, false>;
+    hipLaunchKernelGGL(dkdv, dim3(BH, nb), dim3(64 * kWavesDkdv), C1::LDS, s, tQ, tK, io.V,
+                       io.dO, w.Lsc, w.Di, w.cs, kb, kt, io.dK, io.dV, H, S, Spad, scale, causal,
+                       rope_mode);
     hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, tQ, tK,
                        io.V, io.dO, w.Lsc, w.Di, w.cs, kb, kt, io.dQ, H, S, Spad, scale, causal,
                        rope_mode);
