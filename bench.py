@@ -659,7 +659,8 @@ def bench_hyper(args, torch, gn):
     """The reference's VSA hypernetwork training step (vsa_training_step, bindings.cpp:
     3140-3286) at its defaults: d_model 768, vsa_dim 10240, K 16, router 32 (W2 = 16 x 10240 x
     1536 fp32 = 1.0 GB), one bitpacked state per step.  One step = upload, forward, loss forward
-    (one 64-byte readback, as the reference), backward, surprise-momentum update, end."""
+    (one 64-byte readback, as the reference), backward (the two Linear weights stepped inside
+    it), surprise-momentum update of the other parameters, end."""
     import grilly_core as gc
     import grilly_bridge as gb
     dev = gc.Device(0)
@@ -673,15 +674,18 @@ def bench_hyper(args, torch, gn):
     delta = rng.randint(0, 2 ** 32, size=v // 32, dtype=np.uint32)
     ms = timed(torch, lambda: gc.vsa_training_step(dev, tape, model, state, delta, opt),
                args.steps, args.warmup)
-    # the same step composed call by call with HIP events between the phases
+    # the same step composed call by call with HIP events between the phases.  The two Linear
+    # weights take their surprise-momentum step inside their backward pass (read W, s_bar;
+    # write W, s_bar; dW never stored); the optimizer pass updates the other four.
     sizes = model.parameter_sizes()
-    n_upd = sum(sizes[:6])
+    n_upd = sizes[0] + sizes[1] + sizes[3] + sizes[5]
     phases = [("forward: unpack-project, Linear 768->1536, GELU, Linear 1536->163840 (skinny fp32)",
                4.0 * (sizes[0] + sizes[2] + sizes[4]) + 4.0 * (d + 2 * 1536 + K * v)),
-              ("backward: surrogate, Linear 2 (dX, dW2, db2), GELU, Linear 1, unpack-project",
-               4.0 * (2 * sizes[4] + 2 * K * v + 2 * sizes[2] + sizes[0])),
-              ("surprise-momentum update of the six parameters with gradients (read W, g, s_bar; "
-               "write W, s_bar)", 20.0 * n_upd)]
+              ("backward: surrogate, Linear 2 (dX, db2, W2 + s_bar stepped in the same pass), GELU, "
+               "Linear 1 (likewise), unpack-project",
+               16.0 * (sizes[4] + sizes[2]) + 4.0 * (2 * K * v + sizes[0])),
+              ("surprise-momentum update of the other four parameters with gradients (read W, g, "
+               "s_bar; write W, s_bar)", 20.0 * n_upd)]
     mk = lambda: torch.cuda.Event(enable_timing=True)
     acc = [0.0, 0.0, 0.0]
     reps = max(3, args.steps // 2)
@@ -696,6 +700,7 @@ def bench_hyper(args, torch, gn):
         node = gc.record_surrogate_loss(tape, pred, dl)
         gc.vsa_loss_forward(tape, node, model.gumbel_seed, model.gumbel_counter)
         ev[2].record()
+        opt.prepare(tape)
         tape.backward(node, 0)
         ev[3].record()
         opt.apply(tape)

@@ -395,6 +395,11 @@ PYBIND11_MODULE(_grilly_core, m) {
         .def_readwrite("weight_decay", &SurpriseMomentumOptimizer::weight_decay)
         .def_readwrite("clip_max", &SurpriseMomentumOptimizer::clip_max)
         .def_readwrite("steps", &SurpriseMomentumOptimizer::steps)
+        .def_readwrite("fuse_linear_updates", &SurpriseMomentumOptimizer::fuse_linear_updates,
+                       "Apply a weight's step inside its Linear backward when a few rows use it "
+                       "(same result bit for bit; False runs the separate optimizer pass)")
+        .def("prepare", &SurpriseMomentumOptimizer::prepare, py::arg("tape"),
+             "Before backward: hand the steps of Linear-only weights to the backward pass")
         .def("apply", &SurpriseMomentumOptimizer::apply, py::arg("tape"),
              "Update every parameter whose gradient the tape holds (between backward and end)")
         .def("s_bar_buffer_ids", &SurpriseMomentumOptimizer::s_bar_buffer_ids);

@@ -168,9 +168,10 @@ bool skinny_bwd_applicable(const void* dY, const void* X, const void* W, const v
 size_t skinny_bwd_ws_bytes(int M, int N, int K);
 int skinny_linear_fwd(const float* X, const float* W, const float* b, float* Y, int M, int N,
                       int K, hipStream_t s);
+struct SmHyper;
 int skinny_linear_bwd(const float* dY, const float* X, const float* W, float* dX, float* dW,
                       float* db, int M, int N, int K, bool accumulate, void* ws, size_t ws_bytes,
-                      hipStream_t s);
+                      hipStream_t s, float* s_bar = nullptr, const SmHyper* sm = nullptr);
 
 // Run C (+)= sum_s op(A_s) op(B_s) described by `d`: the LDS-DMA kernel when the shape
 // allows it, else the register-staged MFMA kernel, else the SIMT kernel.

@@ -11,6 +11,7 @@
 #include <algorithm>
 
 #include "gn_common.h"
+#include "gn_sm.h"
 
 namespace gn {
 namespace {
@@ -27,40 +28,10 @@ struct OptBatch {
     int count;
 };
 
-struct SmHyper {
-    float eta, alpha, lambda, floor_, wd, clip;
-    int clear;
-};
 struct AdamHyper {
     float lr, b1, b2, eps, wd, b1t, b2t;
     int clear;
 };
-
-__device__ __forceinline__ bool finite_(float x) { return !(isnan(x) || isinf(x)); }
-
-// surprise-momentum.glsl:53-114 for one element
-__device__ __forceinline__ void sm_elem(const SmHyper& h, float g, float r, float& s_bar, float& w,
-                                        float& d_out) {
-    if (!finite_(g) || !finite_(r)) {
-        d_out = 0.f;
-        return;  // W and s_bar unchanged
-    }
-    const float g_eff = g + h.lambda * r;
-    const float pe = fabsf(g - r);
-    float s_prev = s_bar;
-    if (!finite_(s_prev)) s_prev = 0.f;
-    float s_new = h.alpha * pe + (1.0f - h.alpha) * s_prev;
-    s_new = fminf(s_new, 5.0f);
-    s_bar = s_new;
-    const float lr = h.eta * (1.0f + fmaxf(s_new, h.floor_));
-    float d = lr * g_eff;
-    d += h.eta * h.wd * w;
-    d = fminf(fmaxf(d, -h.clip), h.clip);
-    float w_new = w - d;
-    if (!finite_(w_new)) w_new = 0.f;
-    w = fminf(fmaxf(w_new, -10.0f), 10.0f);
-    d_out = d;
-}
 
 // adamw-update.glsl:41-61 for one element
 __device__ __forceinline__ void adamw_elem(const AdamHyper& h, float g, float& m, float& v, float& w) {

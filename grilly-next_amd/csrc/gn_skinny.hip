@@ -17,6 +17,7 @@
 // does not depend on scheduling.  Without a workspace the partials are added into dX with
 // fp32 atomics (order of additions not fixed).
 #include "gn_common.h"
+#include "gn_sm.h"
 
 #include <algorithm>
 
@@ -88,12 +89,16 @@ __global__ __launch_bounds__(256) void linear_fwd_skinny(const float* __restrict
 // Rows [r0, r1) of W, R rows per step, their W chunks loaded before use; with PIPE the next
 // step's rows are requested before this step's dW stores, so a wave keeps a step of loads in
 // flight behind its stores (one row: R = 8, up to 16 waves, one chunk per thread).
-template <int MT, int Q, int R, bool PIPE>
+// SM: instead of storing dW, apply the surprise-momentum update to W with it (the chunk of
+// dW just formed, the W chunk already loaded for dX, the surprise state s_bar streamed with
+// it), writing W and s_bar in place: dW never goes to memory.  dX uses the W loaded before
+// the update.
+template <int MT, int Q, int R, bool PIPE, bool SM>
 __global__ __launch_bounds__(MT == 1 ? 1024 : 256) void linear_bwd_skinny(
-    const float* __restrict__ dY, const float* __restrict__ X, const float* __restrict__ W,
+    const float* __restrict__ dY, const float* __restrict__ X, const float* W,
     float* __restrict__ dW, float* __restrict__ db, float* __restrict__ part,
     float* __restrict__ dX_atomic, int M, int N, int K, int rows_per_block, int acc_dw,
-    int acc_db, int want_dx) {
+    int acc_db, int want_dx, float* s_bar, SmHyper h) {
     const int t = threadIdx.x, nthr = blockDim.x;
     const int nc = K >> 2;
     const int r0 = blockIdx.x * rows_per_block, r1 = min(N, r0 + rows_per_block);
@@ -107,7 +112,7 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 256) void linear_bwd_skinny(
                                          : make_float4(0.f, 0.f, 0.f, 0.f);
             ax[m][q] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    float4 w[R][Q];
+    float4 w[R][Q], sv[SM ? R : 1][SM ? Q : 1];
     float g[R][MT];
     auto load_rows = [&](int n0) {
 #pragma unroll
@@ -118,14 +123,17 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 256) void linear_bwd_skinny(
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
                 const int c = t + nthr * q;
-                w[i][q] = (want_dx && n < r1 && c < nc) ? ld_nt4(W + (size_t)n * K + 4 * c)
-                                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+                const bool in = n < r1 && c < nc;
+                w[i][q] = ((SM || want_dx) && in) ? ld_nt4(W + (size_t)n * K + 4 * c)
+                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+                if constexpr (SM)
+                    sv[i][q] = in ? ld_nt4(s_bar + (size_t)n * K + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
     };
     if (PIPE) load_rows(r0);
     for (int n0 = r0; n0 < r1; n0 += R) {
-        float4 wc[R][Q];
+        float4 wc[R][Q], sc[SM ? R : 1][SM ? Q : 1];
         float gc[R][MT];
         if (!PIPE) load_rows(n0);
 #pragma unroll
@@ -133,7 +141,10 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 256) void linear_bwd_skinny(
 #pragma unroll
             for (int m = 0; m < MT; ++m) gc[i][m] = g[i][m];
 #pragma unroll
-            for (int q = 0; q < Q; ++q) wc[i][q] = w[i][q];
+            for (int q = 0; q < Q; ++q) {
+                wc[i][q] = w[i][q];
+                if constexpr (SM) sc[i][q] = sv[i][q];
+            }
         }
         if (PIPE && n0 + R < r1) load_rows(n0 + R);
 #pragma unroll
@@ -155,6 +166,19 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 256) void linear_bwd_skinny(
                     ax[m][q].y += gc[i][m] * wc[i][q].y;
                     ax[m][q].z += gc[i][m] * wc[i][q].z;
                     ax[m][q].w += gc[i][m] * wc[i][q].w;
+                }
+                if constexpr (SM) {
+                    const float gv[4] = {o.x, o.y, o.z, o.w};
+                    float sb[4] = {sc[i][q].x, sc[i][q].y, sc[i][q].z, sc[i][q].w};
+                    float wv[4] = {wc[i][q].x, wc[i][q].y, wc[i][q].z, wc[i][q].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float d;
+                        sm_elem(h, gv[e], 0.f, sb[e], wv[e], d);
+                    }
+                    st_nt4(const_cast<float*>(W) + (size_t)n * K + 4 * c, make_float4(wv[0], wv[1], wv[2], wv[3]));
+                    st_nt4(s_bar + (size_t)n * K + 4 * c, make_float4(sb[0], sb[1], sb[2], sb[3]));
+                    continue;
                 }
                 float* dst = dW + (size_t)n * K + 4 * c;
                 if (acc_dw) {
@@ -264,27 +288,36 @@ void launch_fwd_mt(const float* X, const float* W, const float* b, float* Y, int
     linear_fwd_skinny<MT><<<grid, 256, 0, s>>>(X, W, b, Y, M, N, K);
 }
 
+// sm: the fused surprise-momentum update (s_bar, h) instead of the dW store
 template <int MT, int Q>
 void launch_bwd_mq(const BwdShape& sh, const float* dY, const float* X, const float* W, float* dW,
                    float* db, float* part, float* dXa, int M, int N, int K, int acc, int want_dx,
-                   hipStream_t s) {
+                   float* s_bar, const SmHyper* sm, hipStream_t s) {
     constexpr int R = MT == 1 ? 8 : 4;
-    linear_bwd_skinny<MT, Q, R, MT == 1><<<sh.blocks, sh.threads, 0, s>>>(
-        dY, X, W, dW, db, part, dXa, M, N, K, sh.rows_per_block, acc, acc, want_dx);
+    // the fused update streams s_bar next to W: half the rows per step keeps the prefetched
+    // chunks within the 128 registers a 1024-thread block allows (8 rows spill)
+    constexpr int RS = MT == 1 ? 4 : R;
+    if (sm)
+        linear_bwd_skinny<MT, Q, RS, MT == 1, true><<<sh.blocks, sh.threads, 0, s>>>(
+            dY, X, W, dW, db, part, dXa, M, N, K, sh.rows_per_block, 0, acc, want_dx, s_bar, *sm);
+    else
+        linear_bwd_skinny<MT, Q, R, MT == 1, false><<<sh.blocks, sh.threads, 0, s>>>(
+            dY, X, W, dW, db, part, dXa, M, N, K, sh.rows_per_block, acc, acc, want_dx, nullptr,
+            SmHyper{});
 }
 
 template <int MT>
 void launch_bwd_m(const BwdShape& sh, const float* dY, const float* X, const float* W, float* dW,
                   float* db, float* part, float* dXa, int M, int N, int K, int acc, int want_dx,
-                  hipStream_t s) {
+                  float* s_bar, const SmHyper* sm, hipStream_t s) {
     if constexpr (MT == 1) {
-        launch_bwd_mq<1, 1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s);
+        launch_bwd_mq<1, 1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s);
     } else {
         switch (sh.Q) {
-            case 1: launch_bwd_mq<MT, 1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
-            case 2: launch_bwd_mq<MT, 2>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
-            case 3: launch_bwd_mq<MT, 3>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
-            default: launch_bwd_mq<MT, 4>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s); break;
+            case 1: launch_bwd_mq<MT, 1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s); break;
+            case 2: launch_bwd_mq<MT, 2>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s); break;
+            case 3: launch_bwd_mq<MT, 3>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s); break;
+            default: launch_bwd_mq<MT, 4>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s); break;
         }
     }
 }
@@ -332,9 +365,11 @@ int skinny_linear_fwd(const float* X, const float* W, const float* b, float* Y, 
 }
 
 // dX (nullable), dW, db (nullable); ws of skinny_bwd_ws_bytes makes dX deterministic.
+// sm (nullable): apply the surprise-momentum update to W (s_bar its state) in place of the
+// dW store; dW is then not touched.
 int skinny_linear_bwd(const float* dY, const float* X, const float* W, float* dX, float* dW,
                       float* db, int M, int N, int K, bool accumulate, void* ws, size_t ws_bytes,
-                      hipStream_t s) {
+                      hipStream_t s, float* s_bar = nullptr, const SmHyper* sm = nullptr) {
     const BwdShape sh = bwd_shape(M, N, K);
     const size_t need = (size_t)sh.blocks * M * K * sizeof(float);
     float* part = (dX && ws && ws_bytes >= need && al16(ws)) ? (float*)ws : nullptr;
@@ -347,10 +382,10 @@ int skinny_linear_bwd(const float* dY, const float* X, const float* W, float* dX
         }
     }
     const int acc = accumulate ? 1 : 0, want_dx = dX ? 1 : 0;
-    if (M <= 1) launch_bwd_m<1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s);
-    else if (M <= 2) launch_bwd_m<2>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s);
-    else if (M <= 4) launch_bwd_m<4>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s);
-    else launch_bwd_m<8>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s);
+    if (M <= 1) launch_bwd_m<1>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s);
+    else if (M <= 2) launch_bwd_m<2>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s);
+    else if (M <= 4) launch_bwd_m<4>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s);
+    else launch_bwd_m<8>(sh, dY, X, W, dW, db, part, dXa, M, N, K, acc, want_dx, s_bar, sm, s);
     GN_LAUNCH_CHECK("linear backward (skinny fp32)");
     if (part) {
         const int L = M * K;
@@ -361,3 +396,26 @@ int skinny_linear_bwd(const float* dY, const float* X, const float* W, float* dX
 }
 
 }  // namespace gn
+
+// Linear backward of a few fp32 rows with the weight's surprise-momentum step fused in: the
+// backward of bwd_linear (autograd.cpp:172-305; dX, db) and the optimizer's per-element
+// update (surprise-momentum.glsl:53-114 with no recalled gradient, as vsa_training_step runs
+// it: bindings.cpp:3198-3277, 3045-3047) in one pass over W.  W and s_bar are updated in
+// place; dW is formed in registers and never stored.
+extern "C" int gn_linear_bwd_surprise_momentum(const void* dY, const void* X, void* W, float* s_bar,
+                                               void* dX, void* db, int M, int N, int K,
+                                               float eta_base, float alpha_momentum,
+                                               float lambda_recall, float surprise_floor,
+                                               float weight_decay, float clip_max, void* ws,
+                                               size_t ws_bytes, void* stream) {
+    using namespace gn;
+    clear_error();
+    GN_REQUIRE(M > 0 && N > 0 && K > 0, "gn_linear_bwd_surprise_momentum: sizes must be positive");
+    GN_REQUIRE(dY && X && W && s_bar, "gn_linear_bwd_surprise_momentum: null pointer (dY, X, W, s_bar)");
+    GN_REQUIRE(skinny_bwd_applicable(dY, X, W, dX, s_bar, M, K),
+               "gn_linear_bwd_surprise_momentum: takes M <= 8 rows, K a multiple of 4 up to 4096 "
+               "and 16-byte aligned X, W, s_bar, dX (M=%d K=%d)", M, K);
+    const SmHyper h{eta_base, alpha_momentum, lambda_recall, surprise_floor, weight_decay, clip_max, 0};
+    return skinny_linear_bwd((const float*)dY, (const float*)X, (const float*)W, (float*)dX, nullptr,
+                             (float*)db, M, N, K, false, ws, ws_bytes, as_stream(stream), s_bar, &h);
+}

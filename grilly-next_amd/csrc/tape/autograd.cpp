@@ -162,6 +162,21 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
     if (!loss_node) throw std::invalid_argument("backward: loss node is None");
     // autograd.cpp:30-31: 0 means "the loss computes its own gradient" (sentinel 1)
     loss_node->grad_output_buffer = grad_output_buffer ? grad_output_buffer : 1ULL;
+    // a fused weight update needs the weight's whole gradient from one Linear node
+    for (FusedSlot& f : fused_) {
+        int linear_uses = 0, other_uses = 0;
+        for (Node* cur = tape.tail<Node>(); cur != nullptr; cur = cur->prev_in_tape) {
+            for (uint32_t i = 0; i < cur->num_inputs && i < kMaxNodeIO; ++i)
+                other_uses += cur->inputs[i].buffer_id == f.weight;
+            for (uint32_t i = 0; i < cur->num_saved && i < kMaxNodeIO; ++i)
+                if (cur->saved_buffer_ids[i] == f.weight) {
+                    if (cur->op == OpType::Linear && i == 0) ++linear_uses;
+                    else ++other_uses;
+                }
+        }
+        f.eligible = linear_uses == 1 && other_uses == 0;
+        f.u.applied = false;
+    }
     for (Node* cur = tape.tail<Node>(); cur != nullptr; cur = cur->prev_in_tape) {
         stats_.nodes_visited++;
         if (cur->grad_output_buffer == 0) {
@@ -237,6 +252,27 @@ void BackwardEngine::dispatch(Node* n) {
     }
 }
 
+void BackwardEngine::set_fused_update(uint64_t weight, const FusedUpdate& u) {
+    if (!weight || !u.state) throw std::invalid_argument("set_fused_update: weight and state buffers required");
+    if (FusedSlot* f = fused_for(weight)) {
+        f->u = u;
+        return;
+    }
+    fused_.push_back(FusedSlot{weight, u, false});
+}
+
+BackwardEngine::FusedSlot* BackwardEngine::fused_for(uint64_t weight) {
+    for (FusedSlot& f : fused_)
+        if (f.weight == weight) return &f;
+    return nullptr;
+}
+
+bool BackwardEngine::fused_update_applied(uint64_t weight) const {
+    for (const FusedSlot& f : fused_)
+        if (f.weight == weight) return f.u.applied;
+    return false;
+}
+
 // Linear: y = x W^T + b (autograd.cpp:172-305); saved[0] = W [N x K], saved[1] = b or 0.
 void BackwardEngine::bwd_linear(Node* n) {
     const TensorRef& x = n->inputs[0];
@@ -246,6 +282,27 @@ void BackwardEngine::bwd_linear(Node* n) {
     const int dt = gn_dtype(x.dtype, "Linear");
     const uint64_t W = n->saved_buffer_ids[0], b = n->num_saved > 1 ? n->saved_buffer_ids[1] : 0;
     if (!W) throw std::invalid_argument("Linear: saved_buffer_ids[0] must hold W");
+    FusedSlot* f = fused_for(W);
+    if (f && f->eligible && dt == GN_F32 && M > 0 && N > 0) {
+        // the weight's optimizer step in this pass over W; dW is never stored
+        uint64_t dX = x.requires_grad ? alloc_grad(x.size_bytes()) : 0;
+        uint64_t db = b ? alloc_grad((size_t)N * 4) : 0;
+        const size_t wsb = gn_linear_workspace_bytes(M, N, K, dt);
+        const uint64_t ws = split_ws(wsb);
+        const FusedUpdate& u = f->u;
+        const int rc = gn_linear_bwd_surprise_momentum(
+            gout(n), P(x.buffer_id), P(W), (float*)P(u.state), P(dX), P(db), M, N, K, u.eta,
+            u.alpha, u.lambda, u.floor_, u.wd, u.clip, P(ws), wsb, dev_.stream());
+        if (rc == GN_OK) {
+            f->u.applied = true;
+            stats_.shaders_dispatched += 2;
+            n->grad_input_buffers[0] = dX;
+            if (b) contribute(b, db, 0, (size_t)N, true);
+            return;
+        }
+        if (rc != GN_E_INVALID) gn_call(rc, "Linear backward (fused surprise-momentum)");
+        // a shape the fused kernel does not take: the usual backward below
+    }
     uint64_t dX = x.requires_grad ? alloc_grad(x.size_bytes()) : 0;
     uint64_t dW = alloc_grad((size_t)N * K * 4);
     uint64_t db = b ? alloc_grad((size_t)N * 4) : 0;

@@ -151,6 +151,21 @@ public:
     };
     Stats last_stats() const { return stats_; }
 
+    // A weight whose surprise-momentum step the Linear backward applies in its own pass over
+    // W (gn_linear_bwd_surprise_momentum): the weight's gradient is then never stored and
+    // get_grad_buffer(weight) stays 0, so an optimizer that skips gradient-less weights does
+    // not apply the step twice.  Taken only when the weight is saved by exactly one Linear
+    // node of the tape (its whole gradient comes from that node) and the kernel takes the
+    // shape; otherwise the pass stores the gradient as usual.
+    struct FusedUpdate {
+        uint64_t state;  // s_bar buffer, same shape as the weight
+        float eta, alpha, lambda, floor_, wd, clip;
+        bool applied;    // set by the pass that applied it
+    };
+    void set_fused_update(uint64_t weight, const FusedUpdate& u);
+    void clear_fused_updates() { fused_.clear(); }
+    bool fused_update_applied(uint64_t weight) const;
+
     static constexpr size_t kGradTableSize = 8192;  // power of two
 
 private:
@@ -210,6 +225,13 @@ private:
     std::vector<uint64_t> backward_bufs_;
     mutable std::vector<GradEntry> table_;
     uint32_t count_ = 0;
+    struct FusedSlot {
+        uint64_t weight;
+        FusedUpdate u;
+        bool eligible;  // saved by exactly one Linear node of the current tape
+    };
+    std::vector<FusedSlot> fused_;
+    FusedSlot* fused_for(uint64_t weight);
 };
 
 class TapeContext {
@@ -223,6 +245,11 @@ public:
     void save_for_backward(Node* node, const uint64_t* ids, uint32_t count);
     void backward(Node* loss_node, uint64_t grad_output_buffer);
     uint64_t get_grad_buffer(uint64_t id) const { return engine_.get_grad_buffer(id); }
+    void set_fused_update(uint64_t weight, const BackwardEngine::FusedUpdate& u) {
+        engine_.set_fused_update(weight, u);
+    }
+    void clear_fused_updates() { engine_.clear_fused_updates(); }
+    bool fused_update_applied(uint64_t weight) const { return engine_.fused_update_applied(weight); }
     // every (tensor id, gradient buffer id) pair of the last backward pass
     std::vector<std::pair<uint64_t, uint64_t>> grads() const;
     void end();

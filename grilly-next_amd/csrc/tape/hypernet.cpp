@@ -190,9 +190,23 @@ SurpriseMomentumOptimizer::~SurpriseMomentumOptimizer() {
     }
 }
 
+void SurpriseMomentumOptimizer::prepare(TapeContext& tape) {
+    tape.clear_fused_updates();
+    if (!fuse_linear_updates) return;
+    for (size_t i = 0; i < weights_.size(); ++i)
+        tape.set_fused_update(weights_[i], autograd::BackwardEngine::FusedUpdate{
+                                               s_bar_[i], eta_base, alpha_momentum, lambda_recall,
+                                               surprise_floor, weight_decay, clip_max, false});
+}
+
 int SurpriseMomentumOptimizer::apply(TapeContext& tape) {
     std::vector<gn_opt_param> entries;
+    int fused = 0;
     for (size_t i = 0; i < weights_.size(); ++i) {
+        if (tape.fused_update_applied(weights_[i])) {  // stepped by its Linear backward
+            ++fused;
+            continue;
+        }
         const uint64_t g = tape.get_grad_buffer(weights_[i]);
         if (g == 0) continue;  // no gradient for this parameter (bindings.cpp:3228-3232)
         gn_opt_param p{};
@@ -209,8 +223,9 @@ int SurpriseMomentumOptimizer::apply(TapeContext& tape) {
                                           lambda_recall, surprise_floor, weight_decay, clip_max, 0,
                                           dev_.stream()),
                 "SurpriseMomentumOptimizer step");
+    tape.clear_fused_updates();
     ++steps;
-    return (int)entries.size();
+    return (int)entries.size() + fused;
 }
 
 // ───────────────────────────────────────────────────────────────────── loss and step
@@ -306,11 +321,13 @@ float vsa_training_step(TapeContext& tape, VSAHypernetwork& model, const uint32_
         TensorRef d = upload_bitpacked(tape, delta, rows, words);
         Node* loss_node = record_surrogate_loss(tape, predicted, d);
         const float loss = vsa_loss_forward(tape, loss_node, model.gumbel_seed, model.gumbel_counter++);
+        if (optimizer) optimizer->prepare(tape);
         tape.backward(loss_node, 0ULL);
         if (optimizer) optimizer->apply(tape);
         tape.end();
         return loss;
     } catch (...) {
+        tape.clear_fused_updates();
         tape.end();
         throw;
     }

@@ -84,9 +84,15 @@ public:
     SurpriseMomentumOptimizer(const SurpriseMomentumOptimizer&) = delete;
     SurpriseMomentumOptimizer& operator=(const SurpriseMomentumOptimizer&) = delete;
 
+    // Before the backward pass: hand each weight's step to the tape, so a weight that only a
+    // Linear node of a few rows uses is updated inside that node's backward pass over W
+    // (gn_linear_bwd_surprise_momentum, same result bit for bit) and its gradient is never
+    // stored.  A no-op when fuse_linear_updates is false.
+    void prepare(TapeContext& tape);
     // The update vsa_training_step applies between backward and end (bindings.cpp:3198-3277):
-    // every parameter whose gradient the tape holds, one launch per 24 tensors.  Returns the
-    // number of parameters updated.
+    // every parameter whose gradient the tape holds, one launch per 24 tensors (the weights
+    // prepare() handed over were updated by the backward pass).  Returns the number of
+    // parameters updated.
     int apply(TapeContext& tape);
 
     const std::vector<uint64_t>& s_bar_buffer_ids() const { return s_bar_; }
@@ -96,6 +102,7 @@ public:
     float eta_base, alpha_momentum, lambda_recall = 0.0f, surprise_floor = 0.01f,
                                      weight_decay = 0.0f, clip_max;
     uint64_t steps = 0;
+    bool fuse_linear_updates = true;
 
 private:
     Device& dev_;

@@ -35,7 +35,8 @@ SYMBOLS = [
     "gn_vsa_workspace_bytes", "gn_vsa_surrogate_bwd", "gn_vsa_unpack_project_fwd",
     "gn_vsa_fwd_workspace_bytes", "gn_vsa_surrogate_fwd", "gn_embedding_bwd", "gn_binary_bwd",
     "gn_reduce_bwd", "gn_transpose_bwd", "gn_mse_bwd", "gn_vsa_lora_expand_bwd",
-    "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_adamw_step", "gn_layernorm_fwd",
+    "gn_vsa_cosine_blend_bwd", "gn_surprise_momentum_step", "gn_linear_bwd_surprise_momentum",
+    "gn_adamw_step", "gn_layernorm_fwd",
     "gn_rmsnorm_fwd", "gn_layernorm_fwd_ex", "gn_rmsnorm_fwd_ex", "gn_rmsnorm_fwd_stat", "gn_act_fwd", "gn_glu_fwd", "gn_linear_fwd", "gn_glu_linear_fwd", "gn_add_inplace", "gn_convert", "gn_zero",
 ]
 BIN = {"sub": 0, "mul": 1, "div": 2, "neg": 3}
@@ -125,6 +126,8 @@ _SIGS = {
     "gn_vsa_lora_expand_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _U, _P], _I),
     "gn_vsa_cosine_blend_bwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _U, _P], _I),
     "gn_surprise_momentum_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _I, _P], _I),
+    "gn_linear_bwd_surprise_momentum": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _F, _F, _F,
+                                         _F, _P, _Z, _P], _I),
     "gn_adamw_step": ([_OPTP, _I, _F, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     "gn_layernorm_fwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P], _I),
     "gn_rmsnorm_fwd": ([_P, _P, _P, _P, _I, _I, _F, _I, _P], _I),
@@ -667,6 +670,27 @@ def surprise_momentum_step(entries, eta_base=1e-3, alpha=0.9, lambda_recall=0.0,
                                            surprise_floor, weight_decay, clip_max,
                                            int(clear_grad), _stream()),
            "gn_surprise_momentum_step")
+
+
+def linear_bwd_surprise_momentum(dY, X, W, s_bar, eta_base=1e-3, alpha=0.9, lambda_recall=0.0,
+                                 surprise_floor=0.01, weight_decay=0.0, clip_max=1.0,
+                                 need_dx=True, need_db=True, ws=None):
+    """fp32 Linear backward of a few rows with W's surprise-momentum step fused in: W and
+    s_bar are updated in place, dW is never formed in memory.  Returns (dX, db)."""
+    M, N = dY.shape
+    K = X.shape[1]
+    dX = torch.empty((M, K), dtype=torch.float32, device=dY.device) if need_dx else None
+    db = torch.empty((N,), dtype=torch.float32, device=dY.device) if need_db else None
+    if ws is None:
+        nb = linear_workspace_bytes(M, N, K, F32)
+        ws = workspace(nb, dY.device) if nb else False
+    wsp, wsb = (None, 0) if ws is False else (_ptr(ws), ws.numel() * ws.element_size())
+    _check(lib().gn_linear_bwd_surprise_momentum(_ptr(dY), _ptr(X), _ptr(W), _ptr(s_bar), _ptr(dX),
+                                                 _ptr(db), M, N, K, eta_base, alpha, lambda_recall,
+                                                 surprise_floor, weight_decay, clip_max, wsp, wsb,
+                                                 _stream()),
+           "gn_linear_bwd_surprise_momentum")
+    return dX, db
 
 
 def adamw_step(entries, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, step=1,

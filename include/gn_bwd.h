@@ -460,6 +460,23 @@ int gn_surprise_momentum_step(const gn_opt_param* params, int count, float eta_b
                               float alpha_momentum, float lambda_recall, float surprise_floor,
                               float weight_decay, float clip_max, int clear_grad, void* stream);
 
+/* fp32 Linear backward of M <= 8 rows with the weight's surprise-momentum step fused into the
+ * same pass over W: the backward of bwd_linear (autograd.cpp:172-305: dX = dY W, db = sum of
+ * dY's rows) and, in place of storing dW = dY^T X, the update above with that dW as g and no
+ * recalled gradient (r = 0, as vsa_training_step runs the optimizer: bindings.cpp:3045-3047,
+ * 3198-3277), applied to W and s_bar [N x K] in place.  dX is computed from W before its
+ * update; dW is never written (the pass moves 16 bytes per weight instead of the 8 of the
+ * backward plus the 20 of the optimizer).  The result equals gn_linear_bwd_ws followed by
+ * gn_surprise_momentum_step on the produced dW, bit for bit.  dX and db may be NULL.  Takes K a
+ * multiple of 4 up to 4096 and 16-byte aligned X, W, s_bar, dX; other shapes return
+ * GN_E_INVALID (run the two calls instead).  ws: gn_linear_workspace_bytes(M, N, K, GN_F32)
+ * makes dX deterministic, as for gn_linear_bwd_ws. */
+int gn_linear_bwd_surprise_momentum(const void* dY, const void* X, void* W, float* s_bar, void* dX,
+                                    void* db, int M, int N, int K, float eta_base,
+                                    float alpha_momentum, float lambda_recall, float surprise_floor,
+                                    float weight_decay, float clip_max, void* ws, size_t ws_bytes,
+                                    void* stream);
+
 /* AdamW update of `count` tensors (adamw-update.glsl:41-61; adam-update.glsl is weight_decay
  * 0).  beta1_t, beta2_t = beta^t for bias correction at step t >= 1, as the shader's push
  * constants.  Per element: m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;

@@ -272,6 +272,93 @@ def test_training_step_reference_defaults_full_size(env):
     assert m.gumbel_counter == 2 and opt.steps == 2
 
 
+# ------------------------------------------- Linear backward with the optimizer step fused in
+@pytest.mark.parametrize("M,N,K", [(1, 4099, 1536), (1, 300, 4096), (3, 1000, 768), (8, 517, 2048)])
+def test_linear_bwd_surprise_momentum_matches_two_calls(env, M, N, K):
+    """gn_linear_bwd_surprise_momentum against gn_linear_bwd_ws followed by
+    gn_surprise_momentum_step on the dW it stored: W, s_bar, dX and db bit for bit, with the
+    step's branches exercised (weight decay on, a clip that binds, the +-10 weight bound,
+    non-finite s_bar entries, and a column whose gradient is non-finite: an inf in X)."""
+    gc, gb, gn, dev = env
+    rng = np.random.RandomState(7 * M + K)
+    dY = rng.standard_normal((M, N)).astype(np.float32)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    X[0, 3] = np.inf
+    W = np.clip(rng.standard_normal((N, K)) * 3, -9.99, 9.99).astype(np.float32)
+    W[1, :8] = 9.999
+    sb = np.abs(rng.standard_normal((N, K))).astype(np.float32)
+    sb[2, :4] = np.nan
+    sb[3, 4:8] = np.inf
+    hyper = dict(eta_base=0.05, alpha=0.7, lambda_recall=0.3, surprise_floor=0.02,
+                 weight_decay=0.1, clip_max=0.05)
+    t = lambda a: torch.from_numpy(a.copy()).cuda()
+    Wa, sa = t(W), t(sb)
+    dXa, dWa, dba = gn.linear_bwd(t(dY), t(X), Wa)
+    gn.surprise_momentum_step([dict(W=Wa, grad=dWa, state0=sa)], clear_grad=False, **hyper)
+    Wb, sbb = t(W), t(sb)
+    dXb, dbb = gn.linear_bwd_surprise_momentum(t(dY), t(X), Wb, sbb, **hyper)
+    torch.cuda.synchronize()
+    for name, a, b in [("W", Wa, Wb), ("s_bar", sa, sbb), ("dX", dXa, dXb), ("db", dba, dbb)]:
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+    # the update did move W (the step is not skipped), and the clamps bound
+    assert not torch.equal(Wb, t(W))
+    assert float(Wb.abs().max()) <= 10.0
+
+
+def test_linear_bwd_surprise_momentum_refuses_other_shapes(env):
+    gc, gb, gn, dev = env
+    dY = torch.zeros((9, 64), device="cuda")  # nine rows: not a skinny shape
+    X = torch.zeros((9, 32), device="cuda")
+    W = torch.zeros((64, 32), device="cuda")
+    with pytest.raises(gn.GnError, match="M <= 8"):
+        gn.linear_bwd_surprise_momentum(dY, X, W, torch.zeros_like(W))
+
+
+@pytest.mark.parametrize("dims", [dict(d_model=64, vsa_dim=512, K=3, router_hidden=8), None])
+def test_training_step_fused_update_bit_identical(env, dims):
+    """vsa_training_step with the Linear weights stepped inside their backward passes (the
+    default) against the separate optimizer pass (fuse_linear_updates = False): losses, all
+    ten parameters and their s_bar bit for bit over three steps, at a small shape and at the
+    reference's defaults (W2 16 x 10240 x 1536 fp32 = 1.0 GB).  The fused pass stores no
+    gradient for the two Linear weights and steps exactly those."""
+    gc, gb, gn, dev = env
+    dims = dims or {}
+    a = gc.VSAHypernetwork(dev, seed=11, **dims)
+    b = gc.VSAHypernetwork(dev, seed=11, **dims)
+    oa = gc.SurpriseMomentumOptimizer(dev, a, lr=0.01)
+    ob = gc.SurpriseMomentumOptimizer(dev, b, lr=0.01)
+    assert oa.fuse_linear_updates
+    ob.fuse_linear_updates = False
+    words = a.vsa_dim // 32
+    rng = np.random.RandomState(3)
+    tape = gc.TapeContext(dev)
+    for step in range(3):
+        state = rng.randint(0, 2 ** 32, size=words, dtype=np.uint32)
+        delta = rng.randint(0, 2 ** 32, size=words, dtype=np.uint32)
+        la = gc.vsa_training_step(dev, tape, a, state, delta, oa)
+        lb = gc.vsa_training_step(dev, tape, b, state, delta, ob)
+        assert la == lb, step
+    for i, (x, y) in enumerate(zip(_download_params(gb, dev, a), _download_params(gb, dev, b))):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), i
+    sizes = a.parameter_sizes()
+    for i, (ia, ib) in enumerate(zip(oa.s_bar_buffer_ids(), ob.s_bar_buffer_ids())):
+        x, y = gb.download(dev, ia, (sizes[i],)), gb.download(dev, ib, (sizes[i],))
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), i
+    # which weights the fused pass steps: W1 and W2 (parameters 2 and 4), by their backward
+    tape.begin()
+    s = gc.upload_bitpacked(tape, state)
+    pred = a.forward(tape, s)
+    node = gc.record_surrogate_loss(tape, pred, gc.upload_bitpacked(tape, delta))
+    gc.vsa_loss_forward(tape, node, a.gumbel_seed, a.gumbel_counter)
+    oa.prepare(tape)
+    tape.backward(node, 0)
+    ids = a.parameter_buffer_ids()
+    no_grad = [i for i in range(6) if tape.get_grad_buffer(ids[i]) == 0]
+    assert no_grad == [2, 4], no_grad
+    assert oa.apply(tape) == 6
+    tape.end()
+
+
 def test_checkpoint_under_reference_names(env, tmp_path):
     """grilly_core.save/load_hypernetwork_weights(model, path) (bindings.cpp:2965-3039): the
     file is the GRLY v3 layout the Python bridge reads too; with the optimizer, a resumed step
