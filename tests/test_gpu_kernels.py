@@ -61,6 +61,27 @@ def test_gemm_bf16_layouts(gn, ta, tb, shape):
     assert rel_err(host(Cb), ref) < 8e-3
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("shape", [(8192, 768, 768), (8192, 768, 2304), (1000, 384, 192),
+                                   (520, 1536, 640)])
+def test_gemm_bf16_decoder_input_gradient_shapes(gn, ta, tb, shape):
+    """bf16-output products of the decoder's N = 768 input-gradient shapes (192 output tiles of
+    256 x 128, under one round of the 256 CUs) and two edge shapes: against fp64, and bit-equal
+    to the fp32-output product rounded to bf16 where that one is not split over K (an output
+    element's k order does not depend on the tile shape the time model picks)."""
+    M, N, K = shape
+    r = rng_(2)
+    A = rnd(r.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = rnd(r.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    Ad, Bd = dev(A, torch.bfloat16), dev(B, torch.bfloat16)
+    Cb = gn.gemm(Ad, Bd, bool(ta), bool(tb), out_dtype=torch.bfloat16)
+    assert rel_err(host(Cb), ref) < 8e-3
+    if K < 2048:
+        C = gn.gemm(Ad, Bd, bool(ta), bool(tb), out_dtype=torch.float32)
+        assert torch.equal(Cb, C.to(torch.bfloat16))
+
+
 def test_gemm_two_segments_and_accumulate(gn):
     r = rng_(2)
     M, N, K0, K1 = 64, 96, 40, 24
