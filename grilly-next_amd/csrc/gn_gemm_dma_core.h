@@ -49,7 +49,7 @@ __device__ __forceinline__ int fko(int k) { return ((k & 1) * 6) ^ (((k >> 1) & 
 template <int R, bool KC, int NW, int J0 = 0, int J1 = R / (8 * NW)>
 __device__ __forceinline__ void stage(const bf16_t* __restrict__ P, int ld, int r0, int rlim,
                                       int k0, uint32_t s) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & (NW - 1);
     static_assert(R % (8 * NW) == 0, "whole DMA instructions per wave");
 #pragma unroll
     for (int j = J0; j < J1; ++j) {
@@ -428,9 +428,17 @@ __host__ __device__ constexpr int reads_before(int q) {
 // BPAR: with BIAS, the two waves of a wave row (wn = 0, 1) hold the same A fragments; the
 // wave with wn == BPAR sums the row sums of the fragments i with i % 2 == BPAR only, so each
 // row is summed once (-1: no bias).
-template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES, bool BIAS, int BPAR>
+// PROD = 4: four more waves (one per SIMD) issue every LDS DMA of the block, so the four
+// compute waves never stall on a DMA instruction's issue (a wave that issues its share of a
+// k-tile's DMA spends ~550 cycles of each ~1800-cycle k-tile there with its matrix pipe idle,
+// measured on the dN shape).  The producers mirror the compute waves' barriers: before the
+// barrier that publishes tile t+1 they wait for its DMA, after it they issue tile t+STAGES into
+// the stage tile t just left.
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES, bool BIAS, int BPAR,
+          int PROD = 0>
 __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
     static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
+    static_assert(PROD == 0 || (PROD == 4 && !BIAS), "producer waves: 4, without bias sums");
     static_assert(!BIAS || (BPAR >= 0 && BPAR < 2 && (BM / 64) % 2 == 0), "bias rows split by fragment parity");
     constexpr int NW = 4;
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -457,6 +465,8 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;
+    const int dw = wave & 3;  // the wave's slice of a tile's DMA (producer or compute wave)
+    constexpr bool SELF_DMA = PROD == 0;  // the compute waves issue the DMA themselves
 
     f32x16_t acc[FM][FN];
 #pragma unroll
@@ -489,8 +499,8 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
     int oseg = 0;
     auto set_offsets = [&](int seg) {
         if constexpr (PRE) {
-            stage_offsets<BM, !TA, NW>(seg ? lda1 : lda0, m0, g.M, wave, voa);
-            stage_offsets<BN, TB, NW>(seg ? ldb1 : ldb0, n0, g.N, wave, vob);
+            stage_offsets<BM, !TA, NW>(seg ? lda1 : lda0, m0, g.M, dw, voa);
+            stage_offsets<BN, TB, NW>(seg ? ldb1 : ldb0, n0, g.N, dw, vob);
         }
         oseg = seg;
     };
@@ -512,11 +522,11 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
                                                        base + A_ELEMS * 2);
         } else if constexpr (q < NDA) {
             const bf16_t* src = stage_base<!TA>(s1 ? A1 : A0, s1 ? lda1 : lda0, m0, k0);
-            dma16s(src, voa[q], base + 1024u * (uint32_t)(wave * NDA + q));
+            dma16s(src, voa[q], base + 1024u * (uint32_t)(dw * NDA + q));
         } else {
             constexpr int qb = q - NDA;
             const bf16_t* src = stage_base<TB>(s1 ? B1 : B0, s1 ? ldb1 : ldb0, n0, k0);
-            dma16s(src, vob[qb], base + A_ELEMS * 2 + 1024u * (uint32_t)(wave * NDB + qb));
+            dma16s(src, vob[qb], base + A_ELEMS * 2 + 1024u * (uint32_t)(dw * NDB + qb));
         }
     };
     bf16x8_t fa[4][FM], fb[4][FN];
@@ -614,20 +624,22 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
         const bf16_t* nxt = stage_ptr((buf + 1) % STAGES);
         kstep(I0{}, I2{}, BF{}, BF{}, cur, 2, 0, 0);
         kstep(I1{}, I3{}, BT{}, BF{}, cur, 3, 0, 0);
-        if constexpr (STAGES == 3)  // vmcnt(ND) and lgkmcnt(0)
+        if constexpr (!SELF_DMA)  // lgkmcnt(0): the producers wait for the DMA
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & 0xF0FFu);
+        else if constexpr (STAGES == 3)  // vmcnt(ND) and lgkmcnt(0)
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(ND) & 0xF0FFu);
         else  // vmcnt(0) and lgkmcnt(0)
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & 0xF0FFu);
         __syncthreads();
-        offsets_for(min(t + STAGES, last));
-        kstep(I2{}, I0{}, BF{}, BT{}, nxt, 0, min(t + STAGES, last), buf);
+        if constexpr (SELF_DMA) offsets_for(min(t + STAGES, last));
+        kstep(I2{}, I0{}, BF{}, std::integral_constant<bool, SELF_DMA>{}, nxt, 0,
+              min(t + STAGES, last), buf);
         kstep(I3{}, I1{}, BF{}, BF{}, nxt, 1, 0, 0);
     };
-
-    if (KT > 0) {
-        auto dma_all = [&](int tl, int buf) {
-            static_for<ND>([&](auto D_) { dma_one(D_, tl, buf); });
-        };
+    auto dma_all = [&](int tl, int buf) {
+        static_for<ND>([&](auto D_) { dma_one(D_, tl, buf); });
+    };
+    auto prologue_dma = [&]() {  // tiles 0 .. STAGES-1, then wait for tile 0
         set_offsets(kt_lo >= kt0 ? 1 : 0);
         dma_all(0, 0);
         offsets_for(min(1, last));
@@ -639,6 +651,31 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(ND));
         }
+    };
+
+    if constexpr (PROD > 0) {
+        if (wave >= 4) {  // producer: the compute waves' barriers, each with the DMA around it
+            if (KT > 0) {
+                prologue_dma();
+                __syncthreads();
+            }
+            for (int t = 0; t < KT; ++t) {
+                // tile t+1 has landed before the barrier that publishes it (tile t+2 may still
+                // be in flight with three stages); tile t's stage is free after it
+                if constexpr (STAGES == 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(ND));
+                else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                __syncthreads();
+                offsets_for(min(t + STAGES, last));
+                dma_all(min(t + STAGES, last), t % STAGES);
+            }
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            return;
+        }
+    }
+
+    if (KT > 0) {
+        if constexpr (SELF_DMA) prologue_dma();
         __syncthreads();
         static_for<NR>([&](auto R_) { read_one(I0{}, R_, stage_ptr(0), 0); });
         static_for<NR>([&](auto R_) { read_one(I1{}, R_, stage_ptr(0), 1); });
@@ -717,9 +754,12 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
     static_for<FM>(strip);
 }
 
-template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES, bool BIAS = false>
-__global__ __launch_bounds__(256, 1) void gemm_core(GemmDesc g) {
-    if constexpr (BIAS) {
+template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES, bool BIAS = false,
+          int PROD = 0>
+__global__ __launch_bounds__(PROD ? 512 : 256, 1) void gemm_core(GemmDesc g) {
+    if constexpr (PROD > 0) {
+        gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, false, -1, PROD>(g);
+    } else if constexpr (BIAS) {
         // the fused bias sums are split between the two waves of each wave row: two copies of
         // the body, one per fragment parity (measured 5-10 % faster on the decoder's weight
         // gradients than both waves summing every fragment)
@@ -982,8 +1022,13 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
     // the bias-summing variant exists for weight gradients only (fp32 C, plain epilogue)
     constexpr bool CAN_BIAS = EPI == 0 && sizeof(CT) == 4;
     const bool bias = CAN_BIAS && g.bias;
-    static const bool ok2 = allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2>, smem2);
-    static const bool ok3 = fits3 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>, smem3) : false;
+    // without bias sums, tiles up to 256 x 128 take four producer waves (two waves per SIMD:
+    // 256 x 256's accumulators do not fit beside a second wave)
+    constexpr int PR = (EPI == 0 && BM * BN <= 256 * 128) ? 4 : 0;
+    constexpr int NT = 256 + 64 * PR;
+    static const bool ok2 = allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2, false, PR>, smem2);
+    static const bool ok3 =
+        fits3 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, false, PR>, smem3) : false;
     static const bool okb2 = CAN_BIAS ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS>, smem2) : false;
     static const bool okb3 = CAN_BIAS && fits3
                                  ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, CAN_BIAS>, smem3)
@@ -1001,9 +1046,9 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
     else if (bias)
         hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS>), grid, dim3(256), smem2, s, g);
     else if (three)
-        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2>), grid, dim3(256), smem3, s, g);
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, false, PR>), grid, dim3(NT), smem3, s, g);
     else
-        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2>), grid, dim3(256), smem2, s, g);
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2, false, PR>), grid, dim3(NT), smem2, s, g);
     if (g.ksplit > 2)
         split_reduce<<<grid_for((int64_t)g.M * (g.N / 4), 256, 4096), 256, 0, s>>>(g);
     GN_LAUNCH_CHECK("gemm (dma)");
@@ -1044,7 +1089,13 @@ inline double tile_cost(const GemmDesc& g, bool ta, size_t c_bytes, int epi, int
     const double rounds = filled && full == 0 ? 1.0 : (double)full + (f > 0 ? 0.6 + 0.4 * f : 0.0);
     const double kt = (double)((KT + ks - 1) / ks);
     const double epi_us = (double)bm * bn * (double)c_bytes * (epi ? 5.0 : 1.0) / 40000.0;
-    const double tk = (ta ? tk_ta[i] : tk_kc[i]) * (filled && g.bias ? 1.25 : 1.0);
+    // the producer-wave kernels (plain epilogue, no bias sums, tiles up to 256 x 128) run their
+    // k-tiles faster than the sweeps above measured for the self-issuing ones: scaled by the
+    // ratio a second sweep (C2 and C5 shapes, every tile forced in turn) picks the fastest or
+    // near-fastest tile with
+    static constexpr double prod_f[4] = {1.0, 0.88, 0.86, 0.95};
+    const double pf = epi == 0 && !g.bias ? prod_f[i] : 1.0;
+    const double tk = (ta ? tk_ta[i] : tk_kc[i]) * pf * (filled && g.bias ? 1.25 : 1.0);
     double t = rounds * (kt * tk + fixed[i] + epi_us);
     if (ks == 2) t += 5.0 + 0.7e-6 * (double)g.M * g.N * 4.0;
     if (ks > 2) t += 4.0 + (double)(ks + 1 + (g.accumulate ? 1 : 0)) * g.M * g.N * 4.0 / 4.0e6;
