@@ -81,13 +81,12 @@ def parse():
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_dominant_gemm_hbm_traffic.txt")
 # The launches of the FFN step's two largest calls as rocprof names them: (kernel pattern,
-# work-items per dispatch).  [dWg;dWu] (transposed A, fp32 C) runs its first 8192 rows as one
-# round of 256 x 256 tiles (two LDS stages) and the last 3072 rows on 256 x 128 tiles (three
-# stages); the grid size tells its 256 x 256 launch from dWd's (176 tiles).
+# work-items per dispatch).  [dWg;dWu] (transposed A, fp32 C) and dN run one launch each on
+# 256 x 128 tiles with three LDS stages and four producer waves (512 threads per block):
+# 704 and 256 blocks.
 CALL_KERNELS = {
-    "[dWg;dWu]": [(r"gemm_core<true, false, float, 256, 256, 0, 2[,>]", 256 * 256),
-                  (r"gemm_core<true, false, float, 256, 128, 0, 3[,>]", 192 * 256)],
-    "dN": [(r"gemm_core<false, false, unsigned short, 256, 128, 0, 3[,>]", 256 * 256)],
+    "[dWg;dWu]": [(r"gemm_core<true, false, float, 256, 128, 0, 3, false, 4>", 704 * 512)],
+    "dN": [(r"gemm_core<false, false, unsigned short, 256, 128, 0, 3, false, 4>", 256 * 512)],
 }
 DOMINANT_CALL = "[dWg;dWu]"
 CALIB_FLOATS = 1 << 28
@@ -786,11 +785,10 @@ class Step:
         ("down-projection GEMM with the SwiGLU backward in its epilogue: gu = glu'(dY Wd), "
          "4096x5632x2048", "gemm_core (epi 1)", "mfma", 2.0 * T * HID * DM),
         ("dWd = dY^T A, 2048x5632x4096", "gemm_core 256x256 (fp32 C)", "mfma", 2.0 * DM * HID * T),
-        ("dN = [dG|dU] [Wg;Wu], 4096x2048x11264", "gemm_core 256x128 (bf16 C)", "mfma",
-         2.0 * T * DM * 2 * HID),
+        ("dN = [dG|dU] [Wg;Wu], 4096x2048x11264", "gemm_core 256x128 with producer waves (bf16 C)",
+         "mfma", 2.0 * T * DM * 2 * HID),
         ("[dWg;dWu] = [dG|dU]^T N, 11264x2048x4096",
-         "gemm_core 256x256 on rows 0-8191, then 256x128 on rows 8192-11263 (fp32 C; two launches)",
-         "mfma", 2.0 * 2 * HID * DM * T),
+         "gemm_core 256x128 with producer waves (fp32 C; 704 blocks)", "mfma", 2.0 * 2 * HID * DM * T),
         ("RMSNorm backward 4096x2048 (rows + parameter partials)", "norm_bwd_rows + colsum_partials",
          "hbm", 3.0 * T * DM * 2 + 4.0 * T),
     ]
