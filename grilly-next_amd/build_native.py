@@ -25,7 +25,7 @@ ARCH = os.environ.get("GN_OFFLOAD_ARCH", "gfx950")
 KERNEL_SOURCES = ["gn_errors.cpp", "gn_elementwise.hip", "gn_norm.hip", "gn_gemm.hip", "gn_gemm_dma.hip",
                   "gn_gemm_dma_f32a.hip", "gn_gemm_dma_f32b.hip", "gn_gemm_dma_bf16.hip",
                   "gn_gemm_dma_glu.hip", "gn_vsa.hip", "gn_attn.hip", "gn_optim.hip", "gn_tapeops.hip",
-                  "gn_fwd.hip", "gn_skinny.hip", "gn_vsa_fwd.hip", "gn_gemm_f32.hip"]
+                  "gn_fwd.hip", "gn_skinny.hip", "gn_vsa_fwd.hip", "gn_gemm_f32.hip", "gn_lane.cpp"]
 # measurement kernels for bench.py --ceilings, kept out of the backward library
 PROBE_SOURCES = ["gn_probe.hip"]
 TAPE_SOURCES = ["tape/autograd.cpp", "tape/device.cpp", "tape/checkpoint.cpp", "tape/hypernet.cpp",

@@ -18,6 +18,7 @@
 
 #include "gn_common.h"
 #include "gn_gemm_dma.h"
+#include "gn_lane.h"
 
 namespace gn {
 namespace {
@@ -813,6 +814,28 @@ int small_linear_launch(const float* dY, const float* X, const float* W, float* 
     return GN_OK;
 }
 
+// Whether a call's input-gradient product runs beside its weight-gradient product (on the
+// device's side stream, gn_lane.h), both on the LDS-DMA core (bf16).  The weight gradient is
+// issued first, on the caller's stream: its grid takes the compute units it needs and the
+// input gradient's blocks fill the rest, which pays where a grid leaves part of the GPU idle
+// in its last round (the decoder's 192-tile input gradients, the FFN's 176-tile dWd).  The
+// two outputs do not alias and each product's k order is unchanged, so the results are
+// those of the two products run one after the other.
+// Measured on the C5 decoder (12 layers, eager step / graph replay, ms): no fork 9.07 / 9.07;
+// fork from 2 GFLOP per product 9.06 / 8.64; from 50 GFLOP 8.97-8.99 / 8.82.  Eagerly, each
+// fork/join costs ~40 us of host time (two event records, two cross-stream waits) and
+// cross-queue latency on the GPU that the smaller pairs do not win back; a captured graph
+// pays the host part once.  Hence: forked from kSideBySideFlop under capture, from
+// kSideBySideEagerFlop otherwise.
+constexpr double kSideBySideFlop = 2.0e9;
+constexpr double kSideBySideEagerFlop = 5.0e10;
+
+Fork side_by_side(int dtype, double flop_dx, double flop_dw) {
+    const double lo = std::min(flop_dx, flop_dw);
+    if (dtype != GN_BF16 || lo < kSideBySideFlop) return Fork::kNever;
+    return lo >= kSideBySideEagerFlop ? Fork::kAlways : Fork::kCaptured;
+}
+
 }  // namespace gn
 
 using namespace gn;
@@ -860,15 +883,16 @@ extern "C" int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, vo
     if (dtype == GN_F32 && small_linear_applicable(M, N, K, dX != nullptr))
         return small_linear_launch((const float*)dY, (const float*)X, (const float*)W, (float*)dX,
                                    (float*)dW, (float*)db, M, N, K, flags & GN_ACCUMULATE, s);
-    int rc;
-    if (dX) {  // dX[M x K] = dY[M x N] . W[N x K]
-        rc = gemm_dispatch(dY, W, N, nullptr, nullptr, 0, dX, M, K, 0, 0, dtype, dtype, flags, s,
-                           dtype == GN_F32 ? ws : nullptr, ws_bytes);
-        if (rc) return rc;
-    }
+    const double mac = (double)M * N * K;
+    SideBySide sb(s, dX ? side_by_side(dtype, 2.0 * mac, 2.0 * mac) : Fork::kNever);
     // dW[N x K] = dY^T . X  (A = dY stored [M x N] = [Ks x Mout], transposed), db fused
-    return weight_grad(dY, N, X, K, M, N, K, dW, dW, N, (float*)db, nullptr, dtype, flags, s, ws,
-                       ws_bytes);
+    int rc = weight_grad(dY, N, X, K, M, N, K, dW, dW, N, (float*)db, nullptr, dtype, flags, s, ws,
+                         ws_bytes);
+    if (rc == GN_OK && dX)  // dX[M x K] = dY[M x N] . W[N x K]
+        rc = gemm_dispatch(dY, W, N, nullptr, nullptr, 0, dX, M, K, 0, 0, dtype, dtype, flags,
+                           sb.side(), dtype == GN_F32 ? ws : nullptr, ws_bytes);
+    const int jr = sb.join();
+    return rc ? rc : jr;
 }
 
 namespace gn {
@@ -905,32 +929,39 @@ static int glu_proj_impl(const void* gu, const void* X, const void* Wg, const vo
     const size_t esz = dtype == GN_F32 ? 4 : 2;
     const char* g0 = (const char*)gu;
     const bool acc = flags & GN_ACCUMULATE;
-    int rc;
     if (M == 0 || K == 0 || H == 0) return GN_OK;
-    if (dX) {
+    const double mac = 2.0 * (double)M * K * H;
+    SideBySide sb(s, dX && dWg ? side_by_side(dtype, 2.0 * mac, 2.0 * mac) : Fork::kNever);
+    int rc = GN_OK;
+    if (dWg) {
+        // dWg / dWu from one GEMM over the 2H rows of gu^T X, with the bias sums fused
+        if ((dbg == nullptr) != (dbu == nullptr)) {
+            // one bias only: sum it separately, the GEMM carries none
+            float* scr = acc ? nullptr : (float*)dWg;
+            if (dbg)
+                rc = colsum_dispatch(g0, (float*)dbg, M, H, dtype, flags, s, 2 * H, scr, (size_t)H * K);
+            if (rc == GN_OK && dbu)
+                rc = colsum_dispatch(g0 + (size_t)H * esz, (float*)dbu, M, H, dtype, flags, s, 2 * H,
+                                     scr, (size_t)H * K);
+            if (rc == GN_OK)
+                rc = weight_grad(g0, 2 * H, X, K, M, 2 * H, K, dWg, dWu, H, nullptr, nullptr, dtype,
+                                 flags, s, ws, ws_bytes);
+        } else {
+            rc = weight_grad(g0, 2 * H, X, K, M, 2 * H, K, dWg, dWu, H, (float*)dbg, (float*)dbu,
+                             dtype, flags, s, ws, ws_bytes);
+        }
+    }
+    if (rc == GN_OK && dX) {
         GemmDesc d{};
         d.nseg = 2;
         d.A[0] = (const bf16_t*)g0; d.lda[0] = 2 * H; d.B[0] = (const bf16_t*)Wg; d.ldb[0] = K; d.Ks[0] = H;
         d.A[1] = (const bf16_t*)(g0 + (size_t)H * esz); d.lda[1] = 2 * H;
         d.B[1] = (const bf16_t*)Wu; d.ldb[1] = K; d.Ks[1] = H;
         d.M = M; d.N = K; d.C = dX; d.C2 = dX; d.Msplit = M; d.ldc = K; d.accumulate = acc;
-        if ((rc = gemm_run(d, 0, 0, dtype, dtype, s))) return rc;
+        rc = gemm_run(d, 0, 0, dtype, dtype, sb.side());
     }
-    if (!dWg) return GN_OK;  // frozen projection weights: the input gradient only
-    // dWg / dWu from one GEMM over the 2H rows of gu^T X, with the bias sums fused
-    if ((dbg == nullptr) != (dbu == nullptr)) {
-        // one bias only: sum it separately, the GEMM carries none
-        float* scr = acc ? nullptr : (float*)dWg;
-        if (dbg && (rc = colsum_dispatch(g0, (float*)dbg, M, H, dtype, flags, s, 2 * H, scr, (size_t)H * K)))
-            return rc;
-        if (dbu && (rc = colsum_dispatch(g0 + (size_t)H * esz, (float*)dbu, M, H, dtype, flags, s, 2 * H,
-                                         scr, (size_t)H * K)))
-            return rc;
-        return weight_grad(g0, 2 * H, X, K, M, 2 * H, K, dWg, dWu, H, nullptr, nullptr, dtype, flags, s,
-                           ws, ws_bytes);
-    }
-    return weight_grad(g0, 2 * H, X, K, M, 2 * H, K, dWg, dWu, H, (float*)dbg, (float*)dbu, dtype,
-                       flags, s, ws, ws_bytes);
+    const int jr = sb.join();
+    return rc ? rc : jr;
 }
 
 extern "C" int gn_glu_linear_bwd(int kind, const void* dO, const void* gate, const void* up,
@@ -976,8 +1007,12 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
     GN_REQUIRE(kind >= GN_GLU_SWIGLU_UP && kind <= GN_GLU_REGLU_UP, "gn_ffn_down_glu_bwd: kind %d", kind);
     if (M == 0 || H == 0) return GN_OK;
     hipStream_t s = as_stream(stream);
-    int rc;
-    {
+    const double mac = (double)M * N * H;
+    SideBySide sb(s, dWd ? side_by_side(dtype, 2.0 * mac, 2.0 * mac) : Fork::kNever);
+    int rc = GN_OK;
+    // frozen down projection (dWd NULL): the local gradients only
+    if (dWd) rc = weight_grad(dY, N, A, H, M, N, H, dWd, dWd, N, (float*)dbd, nullptr, dtype, flags, s);
+    if (rc == GN_OK) {
         GemmDesc d{};
         d.nseg = 1;
         d.A[0] = (const bf16_t*)dY; d.lda[0] = N; d.Ks[0] = N;
@@ -985,8 +1020,8 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
         d.M = M; d.N = H; d.Msplit = M;
         d.epi = 1; d.gate = (const bf16_t*)gate; d.up = (const bf16_t*)up; d.ldg = H;
         d.gu = (bf16_t*)gu; d.ldgu = 2 * H; d.H = H; d.glu_kind = kind;
-        if ((rc = gemm_run(d, 0, 0, dtype, GN_BF16, s))) return rc;
+        rc = gemm_run(d, 0, 0, dtype, GN_BF16, sb.side());
     }
-    if (!dWd) return GN_OK;  // frozen down projection: the local gradients only
-    return weight_grad(dY, N, A, H, M, N, H, dWd, dWd, N, (float*)dbd, nullptr, dtype, flags, s);
+    const int jr = sb.join();
+    return rc ? rc : jr;
 }

@@ -438,7 +438,7 @@ template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES, bo
           int PROD = 0>
 __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
     static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
-    static_assert(PROD == 0 || (PROD == 4 && !BIAS), "producer waves: 4, without bias sums");
+    static_assert(PROD == 0 || PROD == 4, "producer waves: 0 or 4");
     static_assert(!BIAS || (BPAR >= 0 && BPAR < 2 && (BM / 64) % 2 == 0), "bias rows split by fragment parity");
     constexpr int NW = 4;
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -454,7 +454,7 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
     const int nblk = tilesM * tilesN;
     int pid = blockIdx.x;
     if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);  // XCD-contiguous ranges
-    constexpr int GROUP = 8;
+    constexpr int GROUP = BM == 2 * BN ? 4 : 8;
     const int group_id = pid / (GROUP * tilesN);
     const int first_m = group_id * GROUP;
     const int gsize = min(tilesM - first_m, GROUP);
@@ -757,18 +757,16 @@ __device__ __forceinline__ void gemm_body(const GemmDesc& g) {
 template <bool TA, bool TB, typename CT, int BM, int BN, int EPI, int STAGES, bool BIAS = false,
           int PROD = 0>
 __global__ __launch_bounds__(PROD ? 512 : 256, 1) void gemm_core(GemmDesc g) {
-    if constexpr (PROD > 0) {
-        gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, false, -1, PROD>(g);
-    } else if constexpr (BIAS) {
+    if constexpr (BIAS) {
         // the fused bias sums are split between the two waves of each wave row: two copies of
         // the body, one per fragment parity (measured 5-10 % faster on the decoder's weight
         // gradients than both waves summing every fragment)
         if ((__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 1) == 0)
-            gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, true, 0>(g);
+            gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, true, 0, PROD>(g);
         else
-            gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, true, 1>(g);
+            gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, true, 1, PROD>(g);
     } else {
-        gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, false, -1>(g);
+        gemm_body<TA, TB, CT, BM, BN, EPI, STAGES, false, -1, PROD>(g);
     }
 }
 
@@ -1022,16 +1020,16 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
     // the bias-summing variant exists for weight gradients only (fp32 C, plain epilogue)
     constexpr bool CAN_BIAS = EPI == 0 && sizeof(CT) == 4;
     const bool bias = CAN_BIAS && g.bias;
-    // without bias sums, tiles up to 256 x 128 take four producer waves (two waves per SIMD:
+    // plain-epilogue tiles up to 256 x 128 take four producer waves (two waves per SIMD:
     // 256 x 256's accumulators do not fit beside a second wave)
     constexpr int PR = (EPI == 0 && BM * BN <= 256 * 128) ? 4 : 0;
     constexpr int NT = 256 + 64 * PR;
     static const bool ok2 = allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2, false, PR>, smem2);
     static const bool ok3 =
         fits3 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, false, PR>, smem3) : false;
-    static const bool okb2 = CAN_BIAS ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS>, smem2) : false;
+    static const bool okb2 = CAN_BIAS ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS, PR>, smem2) : false;
     static const bool okb3 = CAN_BIAS && fits3
-                                 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, CAN_BIAS>, smem3)
+                                 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, CAN_BIAS, PR>, smem3)
                                  : false;
     if (!(three ? (bias ? okb3 : ok3) : (bias ? okb2 : ok2))) {
         set_error("gemm: cannot reserve %zu B of LDS", three ? smem3 : smem2);
@@ -1042,9 +1040,9 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
         clear_c<<<grid_for((int64_t)g.M * g.N, 256, 4096), 256, 0, s>>>(g);
     const dim3 grid(tiles, g.ksplit);
     if (bias && three)
-        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, CAN_BIAS>), grid, dim3(256), smem3, s, g);
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, CAN_BIAS, PR>), grid, dim3(NT), smem3, s, g);
     else if (bias)
-        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS>), grid, dim3(256), smem2, s, g);
+        hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, 2, CAN_BIAS, PR>), grid, dim3(NT), smem2, s, g);
     else if (three)
         hipLaunchKernelGGL((gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, false, PR>), grid, dim3(NT), smem3, s, g);
     else
@@ -1089,7 +1087,7 @@ inline double tile_cost(const GemmDesc& g, bool ta, size_t c_bytes, int epi, int
     const double rounds = filled && full == 0 ? 1.0 : (double)full + (f > 0 ? 0.6 + 0.4 * f : 0.0);
     const double kt = (double)((KT + ks - 1) / ks);
     const double epi_us = (double)bm * bn * (double)c_bytes * (epi ? 5.0 : 1.0) / 40000.0;
-    // the producer-wave kernels (plain epilogue, no bias sums, tiles up to 256 x 128) run their
+    // the producer-wave kernels (plain epilogue, tiles up to 256 x 128) run their
     // k-tiles faster than the sweeps above measured for the self-issuing ones: scaled by the
     // ratio a second sweep (C2 and C5 shapes, every tile forced in turn) picks the fastest or
     // near-fastest tile with
