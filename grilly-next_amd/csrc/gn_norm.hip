@@ -75,7 +75,11 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
         if (c < nchunks) gm[j].load(gamma + 8 * c);
         else gm[j].zero();
     }
-    auto load_row = [&](int r, raw8<TX> (&x)[NC], raw8<TY> (&dy)[NC]) {
+    // the addend travels with the row too (loaded after the row's reductions it puts a second
+    // memory round trip on every row), except for fp32 rows of 4 chunks per lane, where the
+    // extra registers would spill
+    constexpr bool PRE_ADD = !(sizeof(TX) == 4 && NC == 4);
+    auto load_row = [&](int r, raw8<TX> (&x)[NC], raw8<TY> (&dy)[NC], raw8<TX> (&ad)[NC]) {
         const size_t off = (size_t)r * F;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
@@ -83,9 +87,12 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
             if (c < nchunks) {
                 x[j].load(X + off + 8 * c);
                 dy[j].load(dY + off + 8 * c);
+                if (PRE_ADD && add) ad[j].load(add + off + 8 * c);
+                else ad[j].zero();
             } else {
                 x[j].zero();
                 dy[j].zero();
+                ad[j].zero();
             }
         }
     };
@@ -97,21 +104,21 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
     };
     const int stride = gridDim.x * kNormWaves;
     int r = blockIdx.x * kNormWaves + wave;
-    raw8<TX> x[NC];
+    raw8<TX> x[NC], ad[NC];
     raw8<TY> dy[NC];
     float mu = 0.f, rs = 0.f;
     if (r < rows) {
         load_stats(r, mu, rs);
-        load_row(r, x, dy);
+        load_row(r, x, dy, ad);
     }
     while (r < rows) {
         const int rn = r + stride;
-        raw8<TX> xn[NC];
+        raw8<TX> xn[NC], adn[NC];
         raw8<TY> dyn[NC];
         float mun = 0.f, rsn = 0.f;
         if (rn < rows) {
             load_stats(rn, mun, rsn);
-            load_row(rn, xn, dyn);
+            load_row(rn, xn, dyn, adn);
         }
         const size_t off = (size_t)r * F;
         rs = stat_rstd(rs, stat_kind, eps);
@@ -135,7 +142,12 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
             const int c = lane + 64 * j;
             if (c >= nchunks) continue;
             float o[8], pa[8], pb[8];
-            if (add) chunk8<TX>::ld(add + off + 8 * c, o);
+            if (PRE_ADD) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = ad[j][e];
+            } else if (add) {
+                chunk8<TX>::ld(add + off + 8 * c, o);
+            }
             float4* qa = reinterpret_cast<float4*>(my + 8 * c);
             float4* qb = reinterpret_cast<float4*>(my + F + 8 * c);
             const float4 a0 = qa[0], a1 = qa[1];
@@ -169,7 +181,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
             }
         }
 #pragma unroll
-        for (int j = 0; j < NC; ++j) { x[j] = xn[j]; dy[j] = dyn[j]; }
+        for (int j = 0; j < NC; ++j) { x[j] = xn[j]; dy[j] = dyn[j]; ad[j] = adn[j]; }
         mu = mun;
         rs = rsn;
         r = rn;
