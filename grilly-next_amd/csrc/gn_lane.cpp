@@ -29,6 +29,12 @@ SideBySide::SideBySide(hipStream_t s, Fork when) : s_(s) {
         (void)hipGetLastError();
         return;
     }
+    // the lane belongs to the current device: a stream of another device keeps issue order
+    hipDevice_t sdev = dev;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess || sdev != dev) {
+        (void)hipGetLastError();
+        return;
+    }
     Lane& L = g_lanes[dev];
     std::unique_lock<std::mutex> lk(L.mu);
     if (L.state == 0) {
