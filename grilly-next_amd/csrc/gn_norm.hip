@@ -59,7 +59,7 @@ template <int MODE, typename TX, typename TY, int NC>
 __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
     const TY* __restrict__ dY, const TX* __restrict__ X, const TY* __restrict__ gamma,
     const float* __restrict__ mean, const float* __restrict__ rstd, TX* dX, const TX* add,
-    float* __restrict__ part, int rows, int F, float eps, int stat_kind) {
+    float* __restrict__ part, int rows, int F, float eps, int stat_kind, bf16_t* __restrict__ dX16) {
     constexpr int NP = MODE == 0 ? 2 : 1;
     extern __shared__ float red[];  // [kNormWaves][NP][F]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -173,6 +173,7 @@ __global__ __launch_bounds__(64 * kNormWaves) void norm_bwd_rows(
                 o[e] = add ? o[e] + v : v;
             }
             chunk8<TX>::st(dX + off + 8 * c, o);
+            if (dX16) chunk8<bf16_t>::st(dX16 + off + 8 * c, o);  // the same values, bf16
             qa[0] = make_float4(pa[0], pa[1], pa[2], pa[3]);
             qa[1] = make_float4(pa[4], pa[5], pa[6], pa[7]);
             if (MODE == 0) {
@@ -301,11 +302,22 @@ bool allow_lds(F* fn, size_t bytes) {
 }
 
 // add: the input-gradient addend (nullable; dX itself for an in-place accumulation).
-// acc: the parameter gradients add onto dA / dB.
+// acc: the parameter gradients add onto dA / dB.  dX16 (nullable, fp32 dX only): a bf16 copy
+// of dX, written in the row kernel's pass (a conversion pass after the other paths).
 template <int MODE, typename TX, typename TY>
 int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean,
              const float* rstd, void* dX, const void* add, float* dA, float* dB, int rows, int F,
-             float eps, int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s) {
+             float eps, int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s,
+             bf16_t* dX16 = nullptr) {
+    if (dX16 && sizeof(TX) != 4) {
+        set_error("norm backward: a bf16 copy of dX needs an fp32 dX");
+        return GN_E_INVALID;
+    }
+    // the paths without the row kernel: the copy as a conversion pass after them
+    auto copy16 = [&]() -> int {
+        if (!dX16) return GN_OK;
+        return gn_convert(dX, GN_F32, dX16, GN_BF16, (int64_t)rows * F, s);
+    };
     // rows wider than 2048 would not fit in registers: they use the generic path
     const bool vec_ok = (F % 8 == 0) && F <= 2048 && aligned16(dY) && aligned16(X) &&
                         aligned16(dX) && aligned16(gamma) && (!add || aligned16(add));
@@ -327,7 +339,7 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
             norm_bwd_generic_dx<MODE, TX, TY><<<rows, 256, 0, s>>>(
                 (const TY*)dY, (const TX*)X, (const TY*)gamma, mean, rstd, (TX*)dX, ad, F, eps, stat_var);
             GN_LAUNCH_CHECK("norm backward (dx only)");
-            return GN_OK;
+            return copy16();
         }
         const size_t lds = (size_t)kNormWaves * (MODE == 0 ? 2 : 1) * F * sizeof(float);
         if (lds > 64 * 1024) {
@@ -341,7 +353,7 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
 #define GN_NORM_LAUNCH(NCV)                                                                    \
     norm_bwd_rows<MODE, TX, TY, NCV><<<G, 64 * kNormWaves, lds, s>>>(                          \
         (const TY*)dY, (const TX*)X, (const TY*)gamma, mean, rstd, (TX*)dX, ad, part, rows, F, \
-        eps, stat_var)
+        eps, stat_var, dX16)
         if (nc <= 1) GN_NORM_LAUNCH(1);
         else if (nc <= 2) GN_NORM_LAUNCH(2);
         else GN_NORM_LAUNCH(4);
@@ -361,6 +373,7 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
         norm_bwd_generic_dx<MODE, TX, TY><<<rows, 256, 0, s>>>(
             (const TY*)dY, (const TX*)X, (const TY*)gamma, mean, rstd, (TX*)dX, ad, F, eps, stat_var);
         GN_LAUNCH_CHECK("norm backward generic dx");
+        if (int rc = copy16()) return rc;
     }
     if (need_param) {
         norm_bwd_generic_param<MODE, TX, TY><<<(F + 255) / 256, 256, 0, s>>>(
@@ -376,16 +389,17 @@ template <int MODE>
 int norm_bwd_dispatch(const char* who, int dy_dtype, int x_dtype, const void* dY, const void* X,
                       const void* gamma, const float* mean, const float* rstd, void* dX,
                       const void* add, float* dA, float* dB, int rows, int F, float eps,
-                      int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s) {
+                      int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s,
+                      bf16_t* dX16 = nullptr) {
     if (x_dtype == GN_F32 && dy_dtype == GN_F32)
         return norm_bwd<MODE, float, float>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F, eps,
-                                            stat_var, acc, ws, ws_bytes, s);
+                                            stat_var, acc, ws, ws_bytes, s, dX16);
     if (x_dtype == GN_BF16 && dy_dtype == GN_BF16)
         return norm_bwd<MODE, bf16_t, bf16_t>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F,
-                                              eps, stat_var, acc, ws, ws_bytes, s);
+                                              eps, stat_var, acc, ws, ws_bytes, s, dX16);
     if (x_dtype == GN_F32 && dy_dtype == GN_BF16)
         return norm_bwd<MODE, float, bf16_t>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F,
-                                             eps, stat_var, acc, ws, ws_bytes, s);
+                                             eps, stat_var, acc, ws, ws_bytes, s, dX16);
     set_error("%s: x dtype %d with dy dtype %d not supported (f32/f32, bf16/bf16, f32/bf16)", who,
               x_dtype, dy_dtype);
     return GN_E_INVALID;
@@ -586,6 +600,22 @@ extern "C" int gn_layernorm_bwd_ex(const void* dY, int dy_dtype, const void* X, 
                                 dX, dX_add, dGamma, dBeta, rows, F, eps,
                                 (flags & GN_LN_STAT_VAR) ? 1 : 0, flags & GN_ACCUMULATE, ws,
                                 ws_bytes, as_stream(stream));
+}
+
+extern "C" int gn_layernorm_bwd_ex16(const void* dY, int dy_dtype, const void* X, int x_dtype,
+                                     const void* gamma, const float* mean, const float* rstd,
+                                     const void* dX_add, void* dX, void* dX_bf16, float* dGamma,
+                                     float* dBeta, int rows, int F, float eps, unsigned flags,
+                                     void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    GN_REQUIRE(rows >= 0 && F > 0, "gn_layernorm_bwd_ex16: bad shape rows=%d F=%d", rows, F);
+    if (rows == 0) return GN_OK;
+    GN_REQUIRE(dY && X && gamma && mean && rstd && dX && dX_bf16, "gn_layernorm_bwd_ex16: null pointer");
+    GN_REQUIRE(x_dtype == GN_F32, "gn_layernorm_bwd_ex16: the bf16 copy is of an fp32 dX (x dtype %d)", x_dtype);
+    return norm_bwd_dispatch<0>("gn_layernorm_bwd_ex16", dy_dtype, x_dtype, dY, X, gamma, mean, rstd,
+                                dX, dX_add, dGamma, dBeta, rows, F, eps,
+                                (flags & GN_LN_STAT_VAR) ? 1 : 0, flags & GN_ACCUMULATE, ws,
+                                ws_bytes, as_stream(stream), (bf16_t*)dX_bf16);
 }
 
 extern "C" int gn_layernorm_bwd_noalloc(const void* dY, const void* X, const void* gamma,

@@ -159,6 +159,7 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
     stats_ = {};
     ws_id_ = 0;
     ws_bytes_ = 0;
+    bf16_copies_.clear();
     if (!loss_node) throw std::invalid_argument("backward: loss node is None");
     // autograd.cpp:30-31: 0 means "the loss computes its own gradient" (sentinel 1)
     loss_node->grad_output_buffer = grad_output_buffer ? grad_output_buffer : 1ULL;
@@ -361,6 +362,31 @@ uint64_t BackwardEngine::norm_dx(Node* n, const void** add) {
     return alloc_grad(x.size_bytes());
 }
 
+// A pre-norm block with its residual stream in fp32 records x = Add(x_prev, y_bf16) right
+// before Norm(x): in the reverse walk the Add is the next node, and no other consumer of x is
+// visited in between, so the norm's dX (with every earlier consumer's gradient summed in by
+// norm_dx) is x's whole gradient, and the Add would convert it to bf16 for y.  The norm then
+// writes that bf16 copy in its own pass: returns the copy's buffer (0: no copy wanted).
+uint64_t BackwardEngine::bf16_copy_for(Node* n, uint64_t dX) {
+    const TensorRef& x = n->inputs[0];
+    const Node* a = n->prev_in_tape;
+    if (!dX || !x.requires_grad || x.dtype != 0 /* f32 */ || !a || a->op != OpType::Add || a->num_outputs < 1 ||
+        a->outputs[0].buffer_id != x.buffer_id || writes_in_place(n, x.buffer_id))
+        return 0;
+    // dX is x's whole gradient only when no earlier contribution is left to add after this node
+    const GradEntry* e = find(x.buffer_id);
+    if (!(handled_ & 1u) && e && e->grad_id) return 0;
+    bool wants = false;
+    for (uint32_t i = 0; i < a->num_inputs && i < kMaxNodeIO; ++i) {
+        const TensorRef& in = a->inputs[i];
+        wants = wants || (in.requires_grad && in.dtype == 4 /* bf16 */ && in.numel() == x.numel());
+    }
+    if (!wants) return 0;
+    const uint64_t c = alloc_grad(x.numel() * 2);
+    bf16_copies_.emplace_back(dX, c);
+    return c;
+}
+
 // saved: [0] gamma, [1] beta (or 0), [2] mean, [3] rstd (or var with stat_is_var).  x and its
 // gradient may be fp32 under a bf16 output (a residual stream kept in fp32): dy and gamma take
 // the output's dtype.
@@ -380,10 +406,18 @@ void BackwardEngine::bwd_layernorm(Node* n) {
     uint64_t dB = beta ? alloc_grad((size_t)F * 4) : 0;
     const size_t wsb = gn_norm_workspace_bytes(rows, F);
     uint64_t ws = alloc_grad(wsb);
-    gn_call(gn_layernorm_bwd_ex(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
-                                (const float*)P(rstd), add, P(dX), (float*)P(dG), (float*)P(dB), rows,
-                                F, p.eps, p.stat_is_var ? GN_LN_STAT_VAR : 0, P(ws), wsb, dev_.stream()),
-            "LayerNorm backward");
+    const uint64_t dX16 = bf16_copy_for(n, dX);
+    if (dX16)
+        gn_call(gn_layernorm_bwd_ex16(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
+                                      (const float*)P(rstd), add, P(dX), P(dX16), (float*)P(dG), (float*)P(dB),
+                                      rows, F, p.eps, p.stat_is_var ? GN_LN_STAT_VAR : 0, P(ws), wsb,
+                                      dev_.stream()),
+                "LayerNorm backward");
+    else
+        gn_call(gn_layernorm_bwd_ex(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
+                                    (const float*)P(rstd), add, P(dX), (float*)P(dG), (float*)P(dB), rows,
+                                    F, p.eps, p.stat_is_var ? GN_LN_STAT_VAR : 0, P(ws), wsb, dev_.stream()),
+                "LayerNorm backward");
     stats_.shaders_dispatched += 2;
     if (x.requires_grad) n->grad_input_buffers[0] = dX;
     contribute(gamma, dG, 0, F, true);
@@ -517,11 +551,23 @@ void BackwardEngine::bwd_add_sub(Node* n, bool /*sub*/) {
         if (in.numel() != out.numel())
             throw std::invalid_argument("Add: broadcasting inputs are not supported");
         if (in.dtype != out.dtype) {
-            const uint64_t c = alloc_grad(in.size_bytes());
-            gn_call(gn_convert(P(g), gn_dtype(out.dtype, "Add output"), P(c), gn_dtype(in.dtype, "Add input"),
-                               (int64_t)in.numel(), dev_.stream()),
-                    "Add backward (dtype conversion)");
-            stats_.shaders_dispatched++;
+            // the bf16 copy the norm visited just before wrote in its pass (bf16_copy_for);
+            // taken once, so a second bf16 input gets its own buffer
+            uint64_t c = 0;
+            if (in.dtype == 4 /* bf16 */)
+                for (auto& bc : bf16_copies_)
+                    if (bc.first == g && bc.second) {
+                        c = bc.second;
+                        bc.second = 0;
+                        break;
+                    }
+            if (!c) {
+                c = alloc_grad(in.size_bytes());
+                gn_call(gn_convert(P(g), gn_dtype(out.dtype, "Add output"), P(c), gn_dtype(in.dtype, "Add input"),
+                                   (int64_t)in.numel(), dev_.stream()),
+                        "Add backward (dtype conversion)");
+                stats_.shaders_dispatched++;
+            }
             n->grad_input_buffers[i] = c;
             continue;
         }

@@ -193,6 +193,7 @@ private:
     const void* gout(Node* n) const;
     // output buffer of a norm's input gradient, summed with the input's existing gradient
     uint64_t norm_dx(Node* n, const void** add);
+    uint64_t bf16_copy_for(Node* n, uint64_t dX);
 
     void bwd_linear(Node* n);
     void bwd_act(Node* n, int kind, bool uses_output);
@@ -231,6 +232,9 @@ private:
         bool eligible;  // saved by exactly one Linear node of the current tape
     };
     std::vector<FusedSlot> fused_;
+    // (fp32 gradient buffer, its bf16 copy) pairs a norm backward wrote in its own pass for the
+    // bf16 input of the Add visited next (bwd_layernorm, bwd_add_sub)
+    std::vector<std::pair<uint64_t, uint64_t>> bf16_copies_;
     FusedSlot* fused_for(uint64_t weight);
 };
 

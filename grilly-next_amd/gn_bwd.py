@@ -28,7 +28,7 @@ SYMBOLS = [
     "gn_last_error", "gn_version", "gn_linear_bwd", "gn_linear_bwd_ws", "gn_linear_workspace_bytes",
     "gn_gemm", "gn_colsum", "gn_act_bwd", "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_linear_bwd_ws",
     "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd",
-    "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
+    "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_layernorm_bwd_ex16", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
     "gn_rmsnorm_bwd_stat", "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_workspace_bytes_dtype", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_attn_fwd_mask",
     "gn_attn_bwd_mask", "gn_attn_bwd_bshd_mask", "gn_vsa_unpack_project_bwd",
@@ -87,6 +87,8 @@ _SIGS = {
     "gn_rmsnorm_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _U, _P, _Z, _P], _I),
     "gn_layernorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _U, _P, _Z,
                              _P], _I),
+    "gn_layernorm_bwd_ex16": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _U,
+                               _P, _Z, _P], _I),
     "gn_rmsnorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _U, _P, _Z, _P], _I),
     "gn_rmsnorm_bwd_stat": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _F, _U, _P, _Z, _P], _I),
     "gn_layernorm_fwd_ex": ([_P, _I, _P, _P, _P, _I, _P, _P, _I, _I, _F, _U, _P], _I),
@@ -341,9 +343,10 @@ def norm_workspace_bytes(rows, F):
 
 
 def layernorm_bwd(dY, X, gamma, mean, rstd, eps=1e-5, stat_is_var=False, ws=None,
-                  need_param=True, dX_add=None, out=None):
+                  need_param=True, dX_add=None, out=None, dX_bf16=None):
     """(dX, dGamma, dBeta).  dY / gamma may be bf16 under an fp32 X (the _ex entry); dX has
-    X's dtype; dX_add (X's dtype, may be `out`) is added to dX in the same pass."""
+    X's dtype; dX_add (X's dtype, may be `out`) is added to dX in the same pass.  dX_bf16 (fp32
+    X): a bf16 tensor that receives dX rounded to bf16 in the same pass (the _ex16 entry)."""
     rows, F = X.shape
     dX = torch.empty_like(X) if out is None else out
     dG = torch.empty((F,), dtype=torch.float32, device=X.device) if need_param else None
@@ -351,7 +354,12 @@ def layernorm_bwd(dY, X, gamma, mean, rstd, eps=1e-5, stat_is_var=False, ws=None
     if ws is None:
         ws = workspace(norm_workspace_bytes(rows, F), X.device)
     flags = LN_STAT_VAR if stat_is_var else 0
-    if dX_add is None and dY.dtype == X.dtype:
+    if dX_bf16 is not None:
+        _check(lib().gn_layernorm_bwd_ex16(_ptr(dY), _dt(dY), _ptr(X), _dt(X), _ptr(gamma), _ptr(mean),
+                                           _ptr(rstd), _ptr(dX_add), _ptr(dX), _ptr(dX_bf16), _ptr(dG),
+                                           _ptr(dB), rows, F, eps, flags, _ptr(ws), ws.numel(),
+                                           _stream()), "gn_layernorm_bwd_ex16")
+    elif dX_add is None and dY.dtype == X.dtype:
         _check(lib().gn_layernorm_bwd(_ptr(dY), _ptr(X), _ptr(gamma), _ptr(mean), _ptr(rstd),
                                       _ptr(dX), _ptr(dG), _ptr(dB), rows, F, eps, _dt(X), flags,
                                       _ptr(ws), ws.numel(), _stream()), "gn_layernorm_bwd")

@@ -224,6 +224,16 @@ int gn_layernorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype
                         const void* dX_add, void* dX, float* dGamma, float* dBeta, int rows,
                         int F, float eps, unsigned flags, void* ws, size_t ws_bytes,
                         void* stream);
+/* gn_layernorm_bwd_ex that also writes dX rounded to bf16 into dX_bf16 in the same pass
+ * (x_dtype GN_F32): in a residual stream kept in fp32, the gradient of the Add that produced
+ * x reaches its bf16 branch as this copy, where the reference's Add backward
+ * (autograd.cpp:611-616) would hand on the fp32 gradient and a conversion pass would follow.
+ * No counterpart in the reference; bit-identical to gn_convert(dX -> bf16). */
+int gn_layernorm_bwd_ex16(const void* dY, int dy_dtype, const void* X, int x_dtype,
+                          const void* gamma, const float* mean, const float* rstd,
+                          const void* dX_add, void* dX, void* dX_bf16, float* dGamma,
+                          float* dBeta, int rows, int F, float eps, unsigned flags, void* ws,
+                          size_t ws_bytes, void* stream);
 int gn_rmsnorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype, const void* w,
                       const float* rstd, const void* dX_add, void* dX, float* dW, int rows,
                       int F, unsigned flags, void* ws, size_t ws_bytes, void* stream);

@@ -635,6 +635,30 @@ def test_norm_bwd_fp32_stream_with_addend(gn, rows, F, kind):
     assert rel_err(host(buf), rX + add) < FP32_TOL
 
 
+@pytest.mark.parametrize("rows,F,with_add", [(8192, 768, True), (300, 2048, False), (77, 3000, True),
+                                            (64, 100, True)])
+def test_layernorm_bwd_bf16_copy_of_dx(gn, rows, F, with_add):
+    """gn_layernorm_bwd_ex16: the bf16 copy written in the norm's pass equals dX rounded by
+    torch (round to nearest even), and dX, dGamma, dBeta equal the _ex entry's bit for bit
+    (F = 100: the generic path, the copy by a conversion pass)."""
+    r = rng_(73)
+    X = (r.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32)
+    g = rnd((1 + 0.3 * r.standard_normal(F)).astype(np.float32))
+    dY = rnd((r.standard_normal((rows, F)) * 0.1).astype(np.float32))
+    add = dev(r.standard_normal((rows, F)).astype(np.float32)) if with_add else None
+    _, mean, rstd = oracle.layernorm_fwd(X, g)
+    args = (dev(dY, torch.bfloat16), dev(X), dev(g, torch.bfloat16), dev(mean), dev(rstd))
+    c16 = torch.empty((rows, F), dtype=torch.bfloat16, device="cuda:0")
+    dX, dG, dB = gn.layernorm_bwd(*args, dX_add=add, dX_bf16=c16)
+    dX1, dG1, dB1 = gn.layernorm_bwd(*args, dX_add=add if with_add else torch.zeros_like(dX))
+    torch.cuda.synchronize()
+    assert torch.equal(dX, dX1) and torch.equal(dG, dG1) and torch.equal(dB, dB1)
+    assert torch.equal(c16, dX.to(torch.bfloat16))
+    rX, _, _ = oracle.layernorm_bwd(dY, X, g, mean, rstd)
+    ref = rX + (host(add) if with_add else 0.0)
+    assert rel_err(host(dX), ref) < FP32_TOL
+
+
 @pytest.mark.parametrize("rows,F", [(4096, 768), (50, 3000)])
 def test_norm_fwd_fp32_stream_to_bf16(gn, rows, F):
     r = rng_(72)
