@@ -231,6 +231,47 @@ __global__ __launch_bounds__(1024) void colsum_partials(const float* __restrict_
     }
 }
 
+// colsum_partials over a batch of deferred norm calls: blockIdx.z = item, blockIdx.y = plane,
+// blockIdx.x = 64-column group; the same sums in the same order as colsum_partials.
+struct NormFinishItem {
+    const float* part;
+    float* out0;
+    float* out1;
+    int G, F, planes, accumulate;
+};
+constexpr int kNormFinishBatch = 32;
+struct NormFinishBatch {
+    NormFinishItem it[kNormFinishBatch];
+};
+__global__ __launch_bounds__(1024) void colsum_partials_batch(NormFinishBatch b) {
+    __shared__ float sh[16][64];
+    const NormFinishItem& it = b.it[blockIdx.z];
+    if ((int)blockIdx.y >= it.planes || (int)blockIdx.x * 64 >= it.F) return;  // uniform
+    float* __restrict__ out = blockIdx.y ? it.out1 : it.out0;
+    if (!out) return;
+    const float* part = it.part + (size_t)blockIdx.y * it.G * it.F;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int f = blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (f < it.F) {
+#pragma unroll 8
+        for (int g = wave; g < it.G; g += 16) s += part[(size_t)g * it.F + f];
+    }
+    sh[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && f < it.F) {
+        float t = sh[0][lane];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) t += sh[w][lane];
+        out[f] = it.accumulate ? out[f] + t : t;
+    }
+}
+
+// partial rows the row kernel writes for `rows` (its grid)
+inline int norm_grid(int rows) {
+    return std::max(1, std::min(kNormGrid, (rows + 2 * kNormWaves - 1) / (2 * kNormWaves)));
+}
+
 // Generic fallback (any F): one block per row, two passes over global memory.
 template <int MODE, typename TX, typename TY>
 __global__ __launch_bounds__(256) void norm_bwd_generic_dx(
@@ -308,7 +349,7 @@ template <int MODE, typename TX, typename TY>
 int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean,
              const float* rstd, void* dX, const void* add, float* dA, float* dB, int rows, int F,
              float eps, int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s,
-             bf16_t* dX16 = nullptr) {
+             bf16_t* dX16 = nullptr, bool partials_only = false) {
     if (dX16 && sizeof(TX) != 4) {
         set_error("norm backward: a bf16 copy of dX needs an fp32 dX");
         return GN_E_INVALID;
@@ -323,9 +364,14 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
                         aligned16(dX) && aligned16(gamma) && (!add || aligned16(add));
     const bool need_param = dA || dB;
     const TX* ad = (const TX*)add;
+    if (partials_only && !(vec_ok && need_param)) {
+        set_error("norm backward: GN_NORM_PARTIALS needs the row kernel (F %% 8 == 0, F <= 2048, "
+                  "16-byte aligned tensors) and a parameter gradient");
+        return GN_E_INVALID;
+    }
     if (vec_ok) {
         // every wave gets two rows or more where the row count allows it
-        const int G = std::max(1, std::min(kNormGrid, (rows + 2 * kNormWaves - 1) / (2 * kNormWaves)));
+        const int G = norm_grid(rows);
         const size_t need = (size_t)(MODE == 0 ? 2 : 1) * G * F * sizeof(float);
         if (need_param && (!ws || ws_bytes < need)) {
             set_error("norm backward: workspace %zu B < %zu B", ws_bytes, need);
@@ -359,6 +405,7 @@ int norm_bwd(const void* dY, const void* X, const void* gamma, const float* mean
         else GN_NORM_LAUNCH(4);
 #undef GN_NORM_LAUNCH
         GN_LAUNCH_CHECK("norm backward rows");
+        if (partials_only) return GN_OK;  // gn_norm_finish adds the partial rows
         const unsigned gf = (F + 63) / 64;
         if (dA && MODE == 0 && dB)
             colsum_partials<<<dim3(gf, 2), 1024, 0, s>>>(part, G, F, dA, dB, acc);
@@ -390,16 +437,16 @@ int norm_bwd_dispatch(const char* who, int dy_dtype, int x_dtype, const void* dY
                       const void* gamma, const float* mean, const float* rstd, void* dX,
                       const void* add, float* dA, float* dB, int rows, int F, float eps,
                       int stat_var, bool acc, void* ws, size_t ws_bytes, hipStream_t s,
-                      bf16_t* dX16 = nullptr) {
+                      bf16_t* dX16 = nullptr, bool partials_only = false) {
     if (x_dtype == GN_F32 && dy_dtype == GN_F32)
         return norm_bwd<MODE, float, float>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F, eps,
-                                            stat_var, acc, ws, ws_bytes, s, dX16);
+                                            stat_var, acc, ws, ws_bytes, s, dX16, partials_only);
     if (x_dtype == GN_BF16 && dy_dtype == GN_BF16)
         return norm_bwd<MODE, bf16_t, bf16_t>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F,
-                                              eps, stat_var, acc, ws, ws_bytes, s, dX16);
+                                              eps, stat_var, acc, ws, ws_bytes, s, dX16, partials_only);
     if (x_dtype == GN_F32 && dy_dtype == GN_BF16)
         return norm_bwd<MODE, float, bf16_t>(dY, X, gamma, mean, rstd, dX, add, dA, dB, rows, F,
-                                             eps, stat_var, acc, ws, ws_bytes, s, dX16);
+                                             eps, stat_var, acc, ws, ws_bytes, s, dX16, partials_only);
     set_error("%s: x dtype %d with dy dtype %d not supported (f32/f32, bf16/bf16, f32/bf16)", who,
               x_dtype, dy_dtype);
     return GN_E_INVALID;
@@ -599,7 +646,28 @@ extern "C" int gn_layernorm_bwd_ex(const void* dY, int dy_dtype, const void* X, 
     return norm_bwd_dispatch<0>("gn_layernorm_bwd_ex", dy_dtype, x_dtype, dY, X, gamma, mean, rstd,
                                 dX, dX_add, dGamma, dBeta, rows, F, eps,
                                 (flags & GN_LN_STAT_VAR) ? 1 : 0, flags & GN_ACCUMULATE, ws,
-                                ws_bytes, as_stream(stream));
+                                ws_bytes, as_stream(stream), nullptr, flags & GN_NORM_PARTIALS);
+}
+
+extern "C" int gn_norm_finish(const GnNormFinish* items, int n, void* stream) {
+    clear_error();
+    GN_REQUIRE(n >= 0 && (n == 0 || items), "gn_norm_finish: %d items", n);
+    hipStream_t s = as_stream(stream);
+    for (int i0 = 0; i0 < n; i0 += kNormFinishBatch) {
+        NormFinishBatch b{};
+        const int m = std::min(kNormFinishBatch, n - i0);
+        int maxF = 0;
+        for (int i = 0; i < m; ++i) {
+            const GnNormFinish& f = items[i0 + i];
+            GN_REQUIRE(f.ws && f.rows > 0 && f.F > 0, "gn_norm_finish: item %d: bad workspace or shape", i0 + i);
+            b.it[i] = NormFinishItem{(const float*)f.ws, f.dgamma, f.layernorm ? f.dbeta : nullptr,
+                                     norm_grid(f.rows), f.F, f.layernorm ? 2 : 1, f.accumulate ? 1 : 0};
+            maxF = std::max(maxF, f.F);
+        }
+        colsum_partials_batch<<<dim3((maxF + 63) / 64, 2, m), 1024, 0, s>>>(b);
+        GN_LAUNCH_CHECK("gn_norm_finish");
+    }
+    return GN_OK;
 }
 
 extern "C" int gn_layernorm_bwd_ex16(const void* dY, int dy_dtype, const void* X, int x_dtype,
@@ -615,7 +683,7 @@ extern "C" int gn_layernorm_bwd_ex16(const void* dY, int dy_dtype, const void* X
     return norm_bwd_dispatch<0>("gn_layernorm_bwd_ex16", dy_dtype, x_dtype, dY, X, gamma, mean, rstd,
                                 dX, dX_add, dGamma, dBeta, rows, F, eps,
                                 (flags & GN_LN_STAT_VAR) ? 1 : 0, flags & GN_ACCUMULATE, ws,
-                                ws_bytes, as_stream(stream), (bf16_t*)dX_bf16);
+                                ws_bytes, as_stream(stream), (bf16_t*)dX_bf16, flags & GN_NORM_PARTIALS);
 }
 
 extern "C" int gn_layernorm_bwd_noalloc(const void* dY, const void* X, const void* gamma,
@@ -667,7 +735,8 @@ extern "C" int gn_rmsnorm_bwd_stat(const void* dY, int dy_dtype, const void* X, 
     GN_REQUIRE(!(meansq && rms), "gn_rmsnorm_bwd: GN_RMS_STAT_MEANSQ and GN_RMS_STAT_RMS together");
     return norm_bwd_dispatch<1>("gn_rmsnorm_bwd", dy_dtype, x_dtype, dY, X, w, nullptr, stat, dX,
                                 dX_add, dW, nullptr, rows, F, eps, meansq ? 1 : rms ? 2 : 0,
-                                flags & GN_ACCUMULATE, ws, ws_bytes, as_stream(stream));
+                                flags & GN_ACCUMULATE, ws, ws_bytes, as_stream(stream), nullptr,
+                                flags & GN_NORM_PARTIALS);
 }
 
 extern "C" int gn_rmsnorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype,
@@ -675,7 +744,7 @@ extern "C" int gn_rmsnorm_bwd_ex(const void* dY, int dy_dtype, const void* X, in
                                  float* dW, int rows, int F, unsigned flags, void* ws,
                                  size_t ws_bytes, void* stream) {
     return gn_rmsnorm_bwd_stat(dY, dy_dtype, X, x_dtype, w, rstd, dX_add, dX, dW, rows, F, 0.f,
-                               flags & GN_ACCUMULATE, ws, ws_bytes, stream);
+                               flags & (GN_ACCUMULATE | GN_NORM_PARTIALS), ws, ws_bytes, stream);
 }
 
 extern "C" int gn_softmax_bwd(const void* dY, const void* Y, void* dX, int rows, int C,

@@ -93,6 +93,8 @@ uint64_t BackwardEngine::split_ws(size_t bytes) {
 void BackwardEngine::contribute(uint64_t id, uint64_t g, uint32_t dtype, size_t numel, bool owned) {
     if (id == 0 || g == 0) return;
     GradEntry* e = find_or_insert(id);
+    // a fan-out add reads or writes a gradient a deferred norm finish has not written yet
+    if (e->grad_id != 0 && (norm_pending(g) || norm_pending(e->grad_id))) flush_norms();
     const size_t bytes = numel * TensorRef::elem_size(dtype);
     if (e->grad_id == 0) {
         *e = GradEntry{id, g, bytes, dtype, owned};
@@ -160,6 +162,7 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
     ws_id_ = 0;
     ws_bytes_ = 0;
     bf16_copies_.clear();
+    norm_pending_.clear();
     if (!loss_node) throw std::invalid_argument("backward: loss node is None");
     // autograd.cpp:30-31: 0 means "the loss computes its own gradient" (sentinel 1)
     loss_node->grad_output_buffer = grad_output_buffer ? grad_output_buffer : 1ULL;
@@ -213,6 +216,23 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
                 contribute(in.buffer_id, cur->grad_input_buffers[i], in.dtype, in.numel(), own);
         }
     }
+    flush_norms();
+}
+
+bool BackwardEngine::norm_pending(uint64_t buf) const {
+    if (!buf) return false;
+    for (const GnNormFinish& f : norm_pending_)
+        if (reinterpret_cast<uint64_t>(f.dgamma) == buf || reinterpret_cast<uint64_t>(f.dbeta) == buf)
+            return true;
+    return false;
+}
+
+void BackwardEngine::flush_norms() {
+    if (norm_pending_.empty()) return;
+    gn_call(gn_norm_finish(norm_pending_.data(), (int)norm_pending_.size(), dev_.stream()),
+            "norm parameter gradients (deferred finish)");
+    stats_.shaders_dispatched++;
+    norm_pending_.clear();
 }
 
 void BackwardEngine::dispatch(Node* n) {
@@ -407,17 +427,24 @@ void BackwardEngine::bwd_layernorm(Node* n) {
     const size_t wsb = gn_norm_workspace_bytes(rows, F);
     uint64_t ws = alloc_grad(wsb);
     const uint64_t dX16 = bf16_copy_for(n, dX);
-    if (dX16)
-        gn_call(gn_layernorm_bwd_ex16(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
-                                      (const float*)P(rstd), add, P(dX), P(dX16), (float*)P(dG), (float*)P(dB),
-                                      rows, F, p.eps, p.stat_is_var ? GN_LN_STAT_VAR : 0, P(ws), wsb,
-                                      dev_.stream()),
-                "LayerNorm backward");
-    else
-        gn_call(gn_layernorm_bwd_ex(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
-                                    (const float*)P(rstd), add, P(dX), (float*)P(dG), (float*)P(dB), rows,
-                                    F, p.eps, p.stat_is_var ? GN_LN_STAT_VAR : 0, P(ws), wsb, dev_.stream()),
-                "LayerNorm backward");
+    // the parameter gradients' finish is deferred to one launch for the whole pass (the call
+    // refuses shapes off the row-kernel path, which then finish here)
+    auto call = [&](unsigned fl) {
+        fl |= p.stat_is_var ? GN_LN_STAT_VAR : 0;
+        if (dX16)
+            return gn_layernorm_bwd_ex16(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
+                                         (const float*)P(rstd), add, P(dX), P(dX16), (float*)P(dG),
+                                         (float*)P(dB), rows, F, p.eps, fl, P(ws), wsb, dev_.stream());
+        return gn_layernorm_bwd_ex(gout(n), ydt, P(x.buffer_id), xdt, P(gamma), (const float*)P(mean),
+                                   (const float*)P(rstd), add, P(dX), (float*)P(dG), (float*)P(dB), rows,
+                                   F, p.eps, fl, P(ws), wsb, dev_.stream());
+    };
+    int rc = call(GN_NORM_PARTIALS);
+    if (rc == GN_OK)
+        norm_pending_.push_back(GnNormFinish{P(ws), (float*)P(dG), (float*)P(dB), rows, F, 1, 0});
+    else if (rc == GN_E_INVALID)
+        rc = call(0);
+    gn_call(rc, "LayerNorm backward");
     stats_.shaders_dispatched += 2;
     if (x.requires_grad) n->grad_input_buffers[0] = dX;
     contribute(gamma, dG, 0, F, true);
@@ -442,10 +469,17 @@ void BackwardEngine::bwd_rmsnorm(Node* n) {
     uint64_t dW = alloc_grad((size_t)F * 4);
     const size_t wsb = gn_norm_workspace_bytes(rows, F);
     uint64_t ws = alloc_grad(wsb);
-    gn_call(gn_rmsnorm_bwd_stat(gout(n), ydt, P(x.buffer_id), xdt, P(w), (const float*)P(rstd), add,
-                                P(dX), (float*)P(dW), rows, F, p.eps, stat_flag, P(ws), wsb,
-                                dev_.stream()),
-            "RMSNorm backward");
+    auto call = [&](unsigned fl) {
+        return gn_rmsnorm_bwd_stat(gout(n), ydt, P(x.buffer_id), xdt, P(w), (const float*)P(rstd), add,
+                                   P(dX), (float*)P(dW), rows, F, p.eps, stat_flag | fl, P(ws), wsb,
+                                   dev_.stream());
+    };
+    int rc = call(GN_NORM_PARTIALS);
+    if (rc == GN_OK)
+        norm_pending_.push_back(GnNormFinish{P(ws), (float*)P(dW), nullptr, rows, F, 0, 0});
+    else if (rc == GN_E_INVALID)
+        rc = call(0);
+    gn_call(rc, "RMSNorm backward");
     stats_.shaders_dispatched += 2;
     if (x.requires_grad) n->grad_input_buffers[0] = dX;
     contribute(w, dW, 0, F, true);

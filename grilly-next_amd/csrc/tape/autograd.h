@@ -26,6 +26,7 @@
 #include <vector>
 
 #include "device.h"
+#include "gn_bwd.h"
 #include "tape_arena.h"
 
 namespace grilly {
@@ -235,6 +236,11 @@ private:
     // (fp32 gradient buffer, its bf16 copy) pairs a norm backward wrote in its own pass for the
     // bf16 input of the Add visited next (bwd_layernorm, bwd_add_sub)
     std::vector<std::pair<uint64_t, uint64_t>> bf16_copies_;
+    // norm backwards whose parameter gradients are still partial rows in their workspaces,
+    // summed by one gn_norm_finish at the end of the pass (or before anything reads them)
+    std::vector<GnNormFinish> norm_pending_;
+    bool norm_pending(uint64_t buf) const;
+    void flush_norms();
     FusedSlot* fused_for(uint64_t weight);
 };
 

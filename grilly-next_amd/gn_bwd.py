@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(_HERE, "libgn_bwd.so")
 
 F32, F16, U32, I32, BF16 = 0, 1, 2, 3, 4
 ACCUMULATE, LN_STAT_VAR, NO_GUMBEL, RMS_STAT_MEANSQ, RMS_STAT_RMS = 1, 2, 4, 8, 16
+NORM_PARTIALS = 32
 RMS_STAT = {"rstd": 0, "meansq": RMS_STAT_MEANSQ, "rms": RMS_STAT_RMS}
 ACT = {"relu": 0, "gelu_tanh": 1, "gelu_erf": 2, "silu": 3, "tanh": 4, "sigmoid": 5}
 GLU = {"swiglu_up": 0, "swiglu_gate": 1, "geglu_up": 2, "geglu_gate": 3, "reglu_up": 4}
@@ -28,7 +29,7 @@ SYMBOLS = [
     "gn_last_error", "gn_version", "gn_linear_bwd", "gn_linear_bwd_ws", "gn_linear_workspace_bytes",
     "gn_gemm", "gn_colsum", "gn_act_bwd", "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_linear_bwd_ws",
     "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd",
-    "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_layernorm_bwd_ex16", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
+    "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_layernorm_bwd_ex16", "gn_norm_finish", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
     "gn_rmsnorm_bwd_stat", "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_workspace_bytes_dtype", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_attn_fwd_mask",
     "gn_attn_bwd_mask", "gn_attn_bwd_bshd_mask", "gn_vsa_unpack_project_bwd",
@@ -87,6 +88,7 @@ _SIGS = {
     "gn_rmsnorm_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _U, _P, _Z, _P], _I),
     "gn_layernorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _U, _P, _Z,
                              _P], _I),
+    "gn_norm_finish": ([_P, _I, _P], _I),
     "gn_layernorm_bwd_ex16": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _U,
                                _P, _Z, _P], _I),
     "gn_rmsnorm_bwd_ex": ([_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _U, _P, _Z, _P], _I),
@@ -369,6 +371,24 @@ def layernorm_bwd(dY, X, gamma, mean, rstd, eps=1e-5, stat_is_var=False, ws=None
                                          rows, F, eps, flags, _ptr(ws), ws.numel(), _stream()),
                "gn_layernorm_bwd_ex")
     return dX, dG, dB
+
+
+class NormFinish(ctypes.Structure):
+    """GnNormFinish (include/gn_bwd.h): one deferred norm backward's parameter gradients."""
+    _fields_ = [("ws", ctypes.c_void_p), ("dgamma", ctypes.c_void_p), ("dbeta", ctypes.c_void_p),
+                ("rows", ctypes.c_int), ("F", ctypes.c_int), ("layernorm", ctypes.c_int),
+                ("accumulate", ctypes.c_int)]
+
+
+def norm_finish(items):
+    """Sum the partial rows of deferred norm backwards (GN_NORM_PARTIALS calls) into their
+    parameter gradients, one launch for all: items = [(ws, dgamma, dbeta or None, rows, F,
+    layernorm, accumulate), ...]."""
+    arr = (NormFinish * max(1, len(items)))()
+    for i, (ws, dg, db, rows, F, ln, acc) in enumerate(items):
+        arr[i] = NormFinish(_ptr(ws), _ptr(dg), _ptr(db), rows, F, int(ln), int(acc))
+    _check(lib().gn_norm_finish(ctypes.cast(arr, ctypes.c_void_p), len(items), _stream()),
+           "gn_norm_finish")
 
 
 def rmsnorm_bwd(dY, X, w, rstd, ws=None, need_param=True, dX=None, dW=None, dX_add=None,

@@ -52,6 +52,8 @@ extern "C" {
 #define GN_NO_GUMBEL 4u   /* surrogate forward: top-2 of the plain dot products (no noise) */
 #define GN_RMS_STAT_MEANSQ 8u /* rmsnorm: the statistic is mean(x^2) (rms-norm.glsl:52); eps added */
 #define GN_RMS_STAT_RMS 16u   /* rmsnorm: the statistic is sqrt(mean(x^2)+eps) (snn-rmsnorm.glsl:55) */
+#define GN_NORM_PARTIALS 32u  /* norm backward: leave the parameter gradients as partial rows in
+                                 the workspace, for a later gn_norm_finish (see there) */
 
 /* ---- activation kinds (gn_act_bwd) ------------------------------------------------- */
 #define GN_ACT_RELU 0      /* dx = dy*[x>0]            activation-relu-backward.glsl:33-37 */
@@ -224,6 +226,25 @@ int gn_layernorm_bwd_ex(const void* dY, int dy_dtype, const void* X, int x_dtype
                         const void* dX_add, void* dX, float* dGamma, float* dBeta, int rows,
                         int F, float eps, unsigned flags, void* ws, size_t ws_bytes,
                         void* stream);
+/* Deferred parameter gradients of the norm backwards.  A gn_layernorm_bwd_ex / _ex16 /
+ * gn_rmsnorm_bwd_ex call with GN_NORM_PARTIALS writes dX as usual but leaves dGamma / dBeta
+ * (dW) as the row kernel's per-block partial rows in its workspace, which must then stay
+ * untouched until gn_norm_finish sums them (in the same fixed order, so the results are bit
+ * for bit those of the undeferred call).  It takes the row-kernel path only (F % 8 == 0,
+ * F <= 2048, 16-byte aligned tensors) and returns GN_E_INVALID otherwise, before any launch.
+ * gn_norm_finish sums any number of such calls' partials in one launch: what a tape's backward
+ * does once at its end instead of one small launch per norm.  No counterpart in the reference
+ * (its LayerNorm backward finishes the parameter gradients itself, ops/layernorm.cpp). */
+typedef struct GnNormFinish {
+    const void* ws;   /* the workspace of the deferred call */
+    float* dgamma;    /* its dGamma (LayerNorm) or dW (RMSNorm); NULL: not wanted */
+    float* dbeta;     /* its dBeta (LayerNorm only); NULL: not wanted */
+    int rows, F;      /* the deferred call's shape */
+    int layernorm;    /* 1: LayerNorm (two planes of partials), 0: RMSNorm (one) */
+    int accumulate;   /* add onto dgamma / dbeta instead of overwriting */
+} GnNormFinish;
+int gn_norm_finish(const GnNormFinish* items, int n, void* stream);
+
 /* gn_layernorm_bwd_ex that also writes dX rounded to bf16 into dX_bf16 in the same pass
  * (x_dtype GN_F32): in a residual stream kept in fp32, the gradient of the Add that produced
  * x reaches its bf16 branch as this copy, where the reference's Add backward

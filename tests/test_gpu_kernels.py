@@ -659,6 +659,56 @@ def test_layernorm_bwd_bf16_copy_of_dx(gn, rows, F, with_add):
     assert rel_err(host(dX), ref) < FP32_TOL
 
 
+def test_norm_deferred_parameter_finish(gn):
+    """GN_NORM_PARTIALS + gn_norm_finish: a LayerNorm and an RMSNorm backward whose parameter
+    gradients are summed later in one launch give the immediate calls' dX and parameter
+    gradients bit for bit (accumulating form included); a shape off the row-kernel path is
+    refused before any launch."""
+    r = rng_(74)
+    L, P, s = gn.lib(), gn._ptr, gn._stream()
+    rows, F = 8192, 768
+    X = dev((r.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32))
+    g = dev((1 + 0.3 * r.standard_normal(F)).astype(np.float32), torch.bfloat16)
+    dY = dev((r.standard_normal((rows, F)) * 0.1).astype(np.float32), torch.bfloat16)
+    _, mean, rstd = oracle.layernorm_fwd(host(X), host(g))
+    mean, rstd = dev(mean), dev(rstd)
+    dX0, dG0, dB0 = gn.layernorm_bwd(dY, X, g, mean, rstd, dX_add=torch.zeros_like(X))
+    rows2, F2 = 4096, 2048
+    X2 = dev(r.standard_normal((rows2, F2)).astype(np.float32), torch.bfloat16)
+    w2 = dev((1 + 0.2 * r.standard_normal(F2)).astype(np.float32), torch.bfloat16)
+    dY2 = dev((r.standard_normal((rows2, F2)) * 0.1).astype(np.float32), torch.bfloat16)
+    _, rs2 = oracle.rmsnorm_fwd(host(X2), host(w2))
+    rs2 = dev(rs2)
+    dX20, dW20 = gn.rmsnorm_bwd(dY2, X2, w2, rs2)
+    # deferred: both partial sets stay in their workspaces until one finish
+    ws1 = gn.workspace(gn.norm_workspace_bytes(rows, F), X.device)
+    ws2 = gn.workspace(gn.norm_workspace_bytes(rows2, F2), X.device)
+    dX, dG, dB = torch.empty_like(X), torch.full((F,), 7.0, device="cuda:0"), torch.full((F,), 7.0, device="cuda:0")
+    dX2, dW2 = torch.empty_like(X2), torch.full((F2,), 7.0, device="cuda:0")
+    gn._check(L.gn_layernorm_bwd_ex(P(dY), gn.BF16, P(X), gn.F32, P(g), P(mean), P(rstd), None, P(dX),
+                                    P(dG), P(dB), rows, F, 1e-5, gn.NORM_PARTIALS, P(ws1), ws1.numel(), s),
+              "layernorm deferred")
+    gn._check(L.gn_rmsnorm_bwd_ex(P(dY2), gn.BF16, P(X2), gn.BF16, P(w2), P(rs2), None, P(dX2), P(dW2),
+                                  rows2, F2, gn.NORM_PARTIALS, P(ws2), ws2.numel(), s), "rmsnorm deferred")
+    torch.cuda.synchronize()
+    assert torch.all(dG == 7.0) and torch.all(dW2 == 7.0)  # not written before the finish
+    gn.norm_finish([(ws1, dG, dB, rows, F, True, False), (ws2, dW2, None, rows2, F2, False, False)])
+    torch.cuda.synchronize()
+    assert torch.equal(dX, dX0) and torch.equal(dX2, dX20)
+    assert torch.equal(dG, dG0) and torch.equal(dB, dB0) and torch.equal(dW2, dW20)
+    # accumulating finish: onto the values already there
+    gn.norm_finish([(ws1, dG, dB, rows, F, True, True)])
+    torch.cuda.synchronize()
+    assert torch.equal(dG, dG0 + dG0) and torch.equal(dB, dB0 + dB0)
+    # F = 100 takes the generic path: refused
+    Xs = dev(r.standard_normal((64, 100)).astype(np.float32))
+    with pytest.raises(gn.GnError):
+        gn._check(L.gn_layernorm_bwd_ex(P(Xs), gn.F32, P(Xs), gn.F32, P(Xs[0]), P(Xs[:, 0].contiguous()),
+                                        P(Xs[:, 1].contiguous()), None, P(torch.empty_like(Xs)),
+                                        P(Xs[1]), P(Xs[2]), 64, 100, 1e-5, gn.NORM_PARTIALS, P(ws1),
+                                        ws1.numel(), s), "layernorm deferred (generic)")
+
+
 @pytest.mark.parametrize("rows,F", [(4096, 768), (50, 3000)])
 def test_norm_fwd_fp32_stream_to_bf16(gn, rows, F):
     r = rng_(72)
