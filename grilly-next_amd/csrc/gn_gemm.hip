@@ -827,12 +827,23 @@ int small_linear_launch(const float* dY, const float* X, const float* W, float* 
 // cross-queue latency on the GPU that the smaller pairs do not win back; a captured graph
 // pays the host part once.  Hence: forked from kSideBySideFlop under capture, from
 // kSideBySideEagerFlop otherwise.
+// Only where one of the two grids is under one round: two grids that each fill the GPU (the
+// FFN's dN, 256 tiles, beside its [dWg;dWu], 704) gain nothing from sharing it, and the
+// long blocks of the second one then start late (measured 0.363 -> 0.40 ms for that pair).
+// Grid sizes are estimated on the usual tiles: 256 x 128 for the bf16 input gradient,
+// 256 x 256 for the fp32 weight gradient.
 constexpr double kSideBySideFlop = 2.0e9;
 constexpr double kSideBySideEagerFlop = 5.0e10;
 
-Fork side_by_side(int dtype, double flop_dx, double flop_dw) {
+inline long grid_est(long rows, long cols, int bm, int bn) {
+    return ((rows + bm - 1) / bm) * ((cols + bn - 1) / bn);
+}
+
+// dx: the input gradient's output [xr x xc]; dw: the weight gradient's [wr x wc]
+Fork side_by_side(int dtype, double flop_dx, double flop_dw, long xr, long xc, long wr, long wc) {
     const double lo = std::min(flop_dx, flop_dw);
     if (dtype != GN_BF16 || lo < kSideBySideFlop) return Fork::kNever;
+    if (std::min(grid_est(xr, xc, 256, 128), grid_est(wr, wc, 256, 256)) >= 256) return Fork::kNever;
     return lo >= kSideBySideEagerFlop ? Fork::kAlways : Fork::kCaptured;
 }
 
@@ -884,7 +895,7 @@ extern "C" int gn_linear_bwd_ws(const void* dY, const void* X, const void* W, vo
         return small_linear_launch((const float*)dY, (const float*)X, (const float*)W, (float*)dX,
                                    (float*)dW, (float*)db, M, N, K, flags & GN_ACCUMULATE, s);
     const double mac = (double)M * N * K;
-    SideBySide sb(s, dX ? side_by_side(dtype, 2.0 * mac, 2.0 * mac) : Fork::kNever);
+    SideBySide sb(s, dX ? side_by_side(dtype, 2.0 * mac, 2.0 * mac, M, K, N, K) : Fork::kNever);
     // dW[N x K] = dY^T . X  (A = dY stored [M x N] = [Ks x Mout], transposed), db fused
     int rc = weight_grad(dY, N, X, K, M, N, K, dW, dW, N, (float*)db, nullptr, dtype, flags, s, ws,
                          ws_bytes);
@@ -931,7 +942,7 @@ static int glu_proj_impl(const void* gu, const void* X, const void* Wg, const vo
     const bool acc = flags & GN_ACCUMULATE;
     if (M == 0 || K == 0 || H == 0) return GN_OK;
     const double mac = 2.0 * (double)M * K * H;
-    SideBySide sb(s, dX && dWg ? side_by_side(dtype, 2.0 * mac, 2.0 * mac) : Fork::kNever);
+    SideBySide sb(s, dX && dWg ? side_by_side(dtype, 2.0 * mac, 2.0 * mac, M, K, 2L * H, K) : Fork::kNever);
     int rc = GN_OK;
     if (dWg) {
         // dWg / dWu from one GEMM over the 2H rows of gu^T X, with the bias sums fused
@@ -1008,7 +1019,7 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
     if (M == 0 || H == 0) return GN_OK;
     hipStream_t s = as_stream(stream);
     const double mac = (double)M * N * H;
-    SideBySide sb(s, dWd ? side_by_side(dtype, 2.0 * mac, 2.0 * mac) : Fork::kNever);
+    SideBySide sb(s, dWd ? side_by_side(dtype, 2.0 * mac, 2.0 * mac, M, H, N, H) : Fork::kNever);
     int rc = GN_OK;
     // frozen down projection (dWd NULL): the local gradients only
     if (dWd) rc = weight_grad(dY, N, A, H, M, N, H, dWd, dWd, N, (float*)dbd, nullptr, dtype, flags, s);
