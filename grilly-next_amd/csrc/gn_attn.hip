@@ -260,9 +260,10 @@ struct DkdvCfg {
 
 // dK, dV for 128 keys of one (batch, head): wave w owns keys 32 (w % 4) ..; loops over the
 // query tiles of 64 that can see those keys.  With NW = 4 each wave takes both 32-query
-// halves of a tile in turn; with NW = 8 waves w and w + 4 take one half each (two waves per
-// SIMD) and add their partial sums at the end.  Per query half and wave:
-//   S = Q K^T, dP = dO V^T        (A = Q / dO rows, B = K / V rows, all from LDS)
+// halves of a tile in turn (at D = 64, two blocks per CU, K / V fragments in registers); with
+// NW = 8 waves w and w + 4 take one half each (two waves per SIMD) and add their partial sums
+// at the end.  Per query half and wave:
+//   S = Q K^T, dP = dO V^T        (A = Q / dO rows, B = K / V rows, from LDS)
 //   P = exp2(S scale log2e - L log2e), dS = P (dP - D_i)    (masked on edge tiles)
 //   dV += P^T dO, dK += dS^T Q    (A = P / dS straight from the accumulators,
 //                                  B = dO / Q columns by transpose reads)
@@ -328,11 +329,22 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
     }
     issue(0);
     if (STAGES > 2 && T > 1) issue(1);
+    // four waves at D = 64: the wave's K and V fragments (8 per k-step row set, 32 registers)
+    // are read from LDS once, after the first tile's barrier, and stay in registers
+    constexpr bool KVREG = NW == 4 && D == 64;
+    bf16x8_t kr[KVREG ? KS : 1], vr[KVREG ? KS : 1];
     for (int it = 0; it < T; ++it) {
         if (STAGES > 2 && it + 1 < T) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::DMA_PER_TILE));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();  // tile `it` is in LDS for every wave; the buffer refilled next is free
         if (it + STAGES - 1 < T) issue(it + STAGES - 1);
+        if (KVREG && it == 0) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                kr[ks] = frag_rows<D>(sKb, 32 * kg, ks);
+                vr[ks] = frag_rows<D>(sVb, 32 * kg, ks);
+            }
+        }
         const int q0 = (t0 + it) * 64;
         const unsigned char* sb = smem + (it % STAGES) * C::STAGE;
         const bf16_t* sQ = reinterpret_cast<const bf16_t*>(sb);
@@ -358,18 +370,23 @@ __global__ __launch_bounds__(64 * NW) void attn_dkdv_mfma(
             bf16x8_t fa[2][2], kv[2][2];
             fa[0][0] = frag_rows<D>(sQ, 32 * i, 0);
             fa[0][1] = frag_rows<D>(sG, 32 * i, 0);
-            kv[0][0] = frag_rows<D>(sKb, 32 * kg, 0);
-            kv[0][1] = frag_rows<D>(sVb, 32 * kg, 0);
+            if (!KVREG) {
+                kv[0][0] = frag_rows<D>(sKb, 32 * kg, 0);
+                kv[0][1] = frag_rows<D>(sVb, 32 * kg, 0);
+            }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if (ks + 1 < KS) {
                     fa[(ks + 1) & 1][0] = frag_rows<D>(sQ, 32 * i, ks + 1);
                     fa[(ks + 1) & 1][1] = frag_rows<D>(sG, 32 * i, ks + 1);
-                    kv[(ks + 1) & 1][0] = frag_rows<D>(sKb, 32 * kg, ks + 1);
-                    kv[(ks + 1) & 1][1] = frag_rows<D>(sVb, 32 * kg, ks + 1);
+                    if (!KVREG) {
+                        kv[(ks + 1) & 1][0] = frag_rows<D>(sKb, 32 * kg, ks + 1);
+                        kv[(ks + 1) & 1][1] = frag_rows<D>(sVb, 32 * kg, ks + 1);
+                    }
                 }
-                s = mfma32(fa[ks & 1][0], kv[ks & 1][0], s);
-                dp = mfma32(fa[ks & 1][1], kv[ks & 1][1], dp);
+                const int kk = KVREG ? ks : 0;  // in range for the one-element arrays too
+                s = mfma32(fa[ks & 1][0], KVREG ? kr[kk] : kv[ks & 1][0], s);
+                dp = mfma32(fa[ks & 1][1], KVREG ? vr[kk] : kv[ks & 1][1], dp);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // the first transpose fragments of the dV / dK step are in flight during the exp work
@@ -1609,7 +1626,11 @@ bool allow_lds(F* fn, size_t bytes) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess;
 }
 
-constexpr int kStagesDkdv = 2, kStagesDq = 2, kWavesDkdv = 8;
+constexpr int kStagesDkdv = 2, kStagesDq = 2;
+// dK/dV waves per block: eight (two per SIMD, one block per CU) at D = 128, where the block's
+// 128 K and V rows and two stages fill the LDS; four at D = 64 (65 KB of LDS, 207 registers),
+// so two blocks share a CU and each wave keeps its K and V fragments in registers
+template <int D> constexpr int dkdv_waves() { return D == 64 ? 4 : 8; }
 
 // The eight tensors of one backward call (Q, K: un-rotated inputs).
 struct AttnIO {
@@ -1627,10 +1648,11 @@ template <int D>
 int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, const float* mask,
                     int BH, int H, int S, float scale, int causal, int rope_mode, float theta,
                     hipStream_t s) {
-    using C1 = DkdvCfg<D, kStagesDkdv, kWavesDkdv>;
+    constexpr int NWK = dkdv_waves<D>();
+    using C1 = DkdvCfg<D, kStagesDkdv, NWK>;
     using C2 = DqCfg<D, kStagesDq>;
-    static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, false>, C1::LDS) &&
-                            allow_lds(attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, true>, C1::LDS);
+    static const bool ok1 = allow_lds(attn_dkdv_mfma<D, kStagesDkdv, NWK, false>, C1::LDS) &&
+                            allow_lds(attn_dkdv_mfma<D, kStagesDkdv, NWK, true>, C1::LDS);
     static const bool ok2 = allow_lds(attn_dq_mfma<D, kStagesDq>, C2::LDS);
     if (!ok1 || !ok2) {
         set_error("gn_attn_bwd: cannot reserve LDS (%d / %d B)", C1::LDS, C2::LDS);
@@ -1655,9 +1677,9 @@ int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, const f
     const TDesc tQ = rope_mode != GN_ROPE_NONE ? bhsd(w.Qr, H, S, D) : io.Q;
     const TDesc tK = rope_mode != GN_ROPE_NONE ? bhsd(w.Kr, H, S, D) : io.K;
     const int nb = (S + 127) / 128;
-    auto dkdv = kb ? attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, true>
-                   : attn_dkdv_mfma<D, kStagesDkdv, kWavesDkdv, false>;
-    hipLaunchKernelGGL(dkdv, dim3(BH, nb), dim3(64 * kWavesDkdv), C1::LDS, s, tQ, tK, io.V,
+    auto dkdv = kb ? attn_dkdv_mfma<D, kStagesDkdv, NWK, true>
+                   : attn_dkdv_mfma<D, kStagesDkdv, NWK, false>;
+    hipLaunchKernelGGL(dkdv, dim3(BH, nb), dim3(64 * NWK), C1::LDS, s, tQ, tK, io.V,
                        io.dO, w.Lsc, w.Di, w.cs, kb, kt, io.dK, io.dV, H, S, Spad, scale, causal,
                        rope_mode);
     hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, tQ, tK,
