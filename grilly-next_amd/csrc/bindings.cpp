@@ -151,6 +151,10 @@ PYBIND11_MODULE(_grilly_core, m) {
              [](TapeContext& t, Node* loss, uint64_t g) { t.backward(loss, g); },
              py::arg("loss_node"), py::arg("grad_output_buffer"))
         .def("get_grad_buffer", &TapeContext::get_grad_buffer, py::arg("input_buffer_id"))
+        // no counterpart in the reference: the down projection's backward forms the GLU's
+        // local gradients in its epilogue (the GLU output's gradient is then not kept)
+        .def("set_glu_epilogue", &TapeContext::set_glu_epilogue, py::arg("on"))
+        .def("glu_epilogue", &TapeContext::glu_epilogue)
         .def("record_temporal_surprise",
              [](TapeContext& t, const TensorRef& input, const TensorRef& output, float coh,
                 float contra, uint32_t branches, uint32_t dt, float alpha) {

@@ -927,6 +927,15 @@ extern "C" int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, co
                          stream);
 }
 
+extern "C" int gn_glu_proj_bwd_ws(const void* gu, const void* X, const void* Wg, const void* Wu,
+                                  void* dX, void* dWg, void* dWu, void* dbg, void* dbu, int M,
+                                  int K, int H, int dtype, unsigned flags, void* ws,
+                                  size_t ws_bytes, void* stream) {
+    clear_error();
+    return glu_proj_impl(gu, X, Wg, Wu, dX, dWg, dWu, dbg, dbu, M, K, H, dtype, flags, ws,
+                         ws_bytes, stream);
+}
+
 static int glu_proj_impl(const void* gu, const void* X, const void* Wg, const void* Wu,
                          void* dX, void* dWg, void* dWu, void* dbg, void* dbu, int M, int K,
                          int H, int dtype, unsigned flags, void* ws, size_t ws_bytes,
@@ -1006,11 +1015,10 @@ extern "C" int gn_glu_linear_bwd_ws(int kind, const void* dO, const void* gate, 
 // Down projection backward with the GLU local gradient fused into the dA epilogue:
 //   gu = [dGate | dUp] of glu(gate, up) at dO = dA = dY Wd   (dA never written)
 //   dWd = dY^T A (fp32),  dbd = column sums of dY (optional).
-extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, const void* Wd,
-                                   const void* gate, const void* up, void* gu, void* dWd,
-                                   void* dbd, int M, int N, int H, int dtype, unsigned flags,
-                                   void* stream) {
-    clear_error();
+static int ffn_down_glu_impl(int kind, const void* dY, const void* A, const void* Wd,
+                             const void* gate, const void* up, void* gu, void* dWd, void* dbd,
+                             int M, int N, int H, int dtype, unsigned flags, void* ws,
+                             size_t ws_bytes, void* stream) {
     GN_REQUIRE(M >= 0 && N >= 0 && H >= 0, "gn_ffn_down_glu_bwd: negative size");
     GN_REQUIRE(dY && A && Wd && gate && up && gu, "gn_ffn_down_glu_bwd: null pointer");
     GN_REQUIRE(dWd || !dbd, "gn_ffn_down_glu_bwd: dbd without dWd");
@@ -1022,7 +1030,9 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
     SideBySide sb(s, dWd ? side_by_side(dtype, 2.0 * mac, 2.0 * mac, M, H, N, H) : Fork::kNever);
     int rc = GN_OK;
     // frozen down projection (dWd NULL): the local gradients only
-    if (dWd) rc = weight_grad(dY, N, A, H, M, N, H, dWd, dWd, N, (float*)dbd, nullptr, dtype, flags, s);
+    if (dWd)
+        rc = weight_grad(dY, N, A, H, M, N, H, dWd, dWd, N, (float*)dbd, nullptr, dtype, flags, s, ws,
+                         ws_bytes);
     if (rc == GN_OK) {
         GemmDesc d{};
         d.nseg = 1;
@@ -1035,4 +1045,23 @@ extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, cons
     }
     const int jr = sb.join();
     return rc ? rc : jr;
+}
+
+extern "C" int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, const void* Wd,
+                                   const void* gate, const void* up, void* gu, void* dWd,
+                                   void* dbd, int M, int N, int H, int dtype, unsigned flags,
+                                   void* stream) {
+    clear_error();
+    return ffn_down_glu_impl(kind, dY, A, Wd, gate, up, gu, dWd, dbd, M, N, H, dtype, flags,
+                             nullptr, 0, stream);
+}
+
+// Same, with a workspace for dWd's split-K partials: gn_linear_workspace_bytes(M, N, H, dtype).
+extern "C" int gn_ffn_down_glu_bwd_ws(int kind, const void* dY, const void* A, const void* Wd,
+                                      const void* gate, const void* up, void* gu, void* dWd,
+                                      void* dbd, int M, int N, int H, int dtype, unsigned flags,
+                                      void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    return ffn_down_glu_impl(kind, dY, A, Wd, gate, up, gu, dWd, dbd, M, N, H, dtype, flags, ws,
+                             ws_bytes, stream);
 }

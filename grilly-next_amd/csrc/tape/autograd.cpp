@@ -163,6 +163,8 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
     ws_bytes_ = 0;
     bf16_copies_.clear();
     norm_pending_.clear();
+    glu_node_ = nullptr;
+    glu_gu_ = 0;
     if (!loss_node) throw std::invalid_argument("backward: loss node is None");
     // autograd.cpp:30-31: 0 means "the loss computes its own gradient" (sentinel 1)
     loss_node->grad_output_buffer = grad_output_buffer ? grad_output_buffer : 1ULL;
@@ -192,6 +194,8 @@ void BackwardEngine::backward(TapeArena& tape, Node* loss_node, uint64_t grad_ou
                 }
             }
         }
+        // a FusedGLU whose output gradient the down projection's epilogue turned into gu
+        if (cur->grad_output_buffer == 0 && cur == glu_node_) cur->grad_output_buffer = 1;
         if (cur->grad_output_buffer == 0) continue;
         stats_.nodes_with_grad++;
         std::memset(cur->grad_input_buffers, 0, sizeof(cur->grad_input_buffers));
@@ -324,6 +328,26 @@ void BackwardEngine::bwd_linear(Node* n) {
         if (rc != GN_E_INVALID) gn_call(rc, "Linear backward (fused surprise-momentum)");
         // a shape the fused kernel does not take: the usual backward below
     }
+    if (Node* g = glu_before(n)) {
+        // x = glu(gate, up) feeds only this node: the GLU's local gradients come out of the
+        // input-gradient GEMM's epilogue for the FusedGLU node visited next (dX never formed)
+        uint64_t gu = alloc_grad((size_t)2 * M * K * 2);
+        uint64_t dW = alloc_grad((size_t)N * K * 4);
+        uint64_t db = b ? alloc_grad((size_t)N * 4) : 0;
+        const size_t wsb = gn_linear_workspace_bytes(M, N, K, dt);
+        const uint64_t ws = split_ws(wsb);
+        gn_call(gn_ffn_down_glu_bwd_ws((int)params_of<FusedGLUParams>(g).kind, gout(n),
+                                       P(x.buffer_id), P(W), P(g->saved_buffer_ids[2]),
+                                       P(g->saved_buffer_ids[3]), P(gu), P(dW), P(db), M, N, K, dt,
+                                       0, P(ws), wsb, dev_.stream()),
+                "Linear backward (GLU local gradients in the epilogue)");
+        stats_.shaders_dispatched += 2;
+        glu_node_ = g;
+        glu_gu_ = gu;
+        contribute(W, dW, 0, (size_t)N * K, true);
+        if (b) contribute(b, db, 0, (size_t)N, true);
+        return;
+    }
     uint64_t dX = x.requires_grad ? alloc_grad(x.size_bytes()) : 0;
     uint64_t dW = alloc_grad((size_t)N * K * 4);
     uint64_t db = b ? alloc_grad((size_t)N * 4) : 0;
@@ -405,6 +429,24 @@ uint64_t BackwardEngine::bf16_copy_for(Node* n, uint64_t dX) {
     const uint64_t c = alloc_grad(x.numel() * 2);
     bf16_copies_.emplace_back(dX, c);
     return c;
+}
+
+// The FusedGLU node whose output is this Linear's input, when set_glu_epilogue is on and the
+// fusion applies: bf16, the GLU recorded right before the Linear (so every other consumer of
+// its output comes later on the tape and was visited first) and no gradient of that output
+// in the table yet (no other consumer), so this node's contribution is the whole gradient.
+Node* BackwardEngine::glu_before(Node* n) const {
+    const TensorRef& x = n->inputs[0];
+    Node* g = n->prev_in_tape;
+    if (!glu_epilogue_ || !g || g->op != OpType::FusedGLU || !x.requires_grad || x.dtype != 4 /* bf16 */ ||
+        g->num_inputs < 1 || g->num_outputs < 1 || g->num_saved < 4 || !g->saved_buffer_ids[2] ||
+        !g->saved_buffer_ids[3] || g->outputs[0].buffer_id != x.buffer_id ||
+        g->inputs[0].buffer_id == x.buffer_id || g->inputs[0].dtype != 4 ||
+        g->outputs[0].numel() != x.numel() || g->outputs[0].last() != x.last() ||
+        params_of<FusedGLUParams>(g).kind > GN_GLU_REGLU_UP)
+        return nullptr;
+    const GradEntry* e = find(x.buffer_id);
+    return e && e->grad_id ? nullptr : g;
 }
 
 // saved: [0] gamma, [1] beta (or 0), [2] mean, [3] rstd (or var with stat_is_var).  x and its
@@ -672,14 +714,26 @@ void BackwardEngine::bwd_fused_glu(Node* n) {
     uint64_t dX = x.requires_grad ? alloc_grad(x.size_bytes()) : 0;
     uint64_t dWg = alloc_grad((size_t)H * K * 4), dWu = alloc_grad((size_t)H * K * 4);
     uint64_t dbg = bg ? alloc_grad((size_t)H * 4) : 0, dbu = bu ? alloc_grad((size_t)H * 4) : 0;
-    uint64_t gu = alloc_grad((size_t)2 * M * H * es);
     const size_t wsb = gn_glu_workspace_bytes(M, K, H, dt);
     const uint64_t ws = split_ws(wsb);
-    gn_call(gn_glu_linear_bwd_ws((int)params_of<FusedGLUParams>(n).kind, gout(n), P(s[2]), P(s[3]),
-                                 P(x.buffer_id), P(s[0]), P(s[1]), P(dX), P(dWg), P(dWu), P(dbg),
-                                 P(dbu), P(gu), M, K, H, dt, 0, P(ws), wsb, dev_.stream()),
-            "FusedGLU backward");
-    stats_.shaders_dispatched += 4;
+    if (n == glu_node_) {
+        // [dGate | dUp] from the down projection's epilogue (bwd_linear, set_glu_epilogue)
+        gn_call(gn_glu_proj_bwd_ws(P(glu_gu_), P(x.buffer_id), P(s[0]), P(s[1]), P(dX), P(dWg),
+                                   P(dWu), P(dbg), P(dbu), M, K, H, dt, 0, P(ws), wsb,
+                                   dev_.stream()),
+                "FusedGLU backward (projections)");
+        glu_node_ = nullptr;
+        glu_gu_ = 0;
+        stats_.shaders_dispatched += 3;
+    } else {
+        uint64_t gu = alloc_grad((size_t)2 * M * H * es);
+        gn_call(gn_glu_linear_bwd_ws((int)params_of<FusedGLUParams>(n).kind, gout(n), P(s[2]),
+                                     P(s[3]), P(x.buffer_id), P(s[0]), P(s[1]), P(dX), P(dWg),
+                                     P(dWu), P(dbg), P(dbu), P(gu), M, K, H, dt, 0, P(ws), wsb,
+                                     dev_.stream()),
+                "FusedGLU backward");
+        stats_.shaders_dispatched += 4;
+    }
     n->grad_input_buffers[0] = dX;
     contribute(s[0], dWg, 0, (size_t)H * K, true);
     contribute(s[1], dWu, 0, (size_t)H * K, true);

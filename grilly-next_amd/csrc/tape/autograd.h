@@ -167,6 +167,16 @@ public:
     void clear_fused_updates() { fused_.clear(); }
     bool fused_update_applied(uint64_t weight) const;
 
+    // A Linear whose input is the output of the FusedGLU node recorded right before it (the
+    // FFN's down projection), with no other gradient for that output: the Linear's backward
+    // writes the GLU's local gradients [dGate | dUp] in the epilogue of its input-gradient
+    // GEMM (gn_ffn_down_glu_bwd_ws) and the FusedGLU node starts from them
+    // (gn_glu_proj_bwd_ws).  The GLU output's own gradient is then never formed:
+    // get_grad_buffer() for it stays 0.  bf16 only; off by default, so every gradient the
+    // reference's engine keeps is kept unless the caller asks for the fusion.
+    void set_glu_epilogue(bool on) { glu_epilogue_ = on; }
+    bool glu_epilogue() const { return glu_epilogue_; }
+
     static constexpr size_t kGradTableSize = 8192;  // power of two
 
 private:
@@ -195,6 +205,7 @@ private:
     // output buffer of a norm's input gradient, summed with the input's existing gradient
     uint64_t norm_dx(Node* n, const void** add);
     uint64_t bf16_copy_for(Node* n, uint64_t dX);
+    Node* glu_before(Node* n) const;
 
     void bwd_linear(Node* n);
     void bwd_act(Node* n, int kind, bool uses_output);
@@ -239,6 +250,11 @@ private:
     // norm backwards whose parameter gradients are still partial rows in their workspaces,
     // summed by one gn_norm_finish at the end of the pass (or before anything reads them)
     std::vector<GnNormFinish> norm_pending_;
+    // set_glu_epilogue: [dGate | dUp] a Linear's backward wrote for the FusedGLU node visited
+    // next (bwd_linear -> bwd_fused_glu)
+    bool glu_epilogue_ = false;
+    const Node* glu_node_ = nullptr;
+    uint64_t glu_gu_ = 0;
     bool norm_pending(uint64_t buf) const;
     void flush_norms();
     FusedSlot* fused_for(uint64_t weight);
@@ -260,6 +276,8 @@ public:
     }
     void clear_fused_updates() { engine_.clear_fused_updates(); }
     bool fused_update_applied(uint64_t weight) const { return engine_.fused_update_applied(weight); }
+    void set_glu_epilogue(bool on) { engine_.set_glu_epilogue(on); }
+    bool glu_epilogue() const { return engine_.glu_epilogue(); }
     // every (tensor id, gradient buffer id) pair of the last backward pass
     std::vector<std::pair<uint64_t, uint64_t>> grads() const;
     void end();

@@ -27,8 +27,9 @@ import gn_bwd as gn
 
 class Decoder:
     def __init__(self, layers=12, d=768, heads=12, ff=3072, vocab=32000, batch=8, seq=1024,
-                 seed=5, device="cuda:0"):
+                 seed=5, device="cuda:0", glu_epilogue=True):
         self.L, self.d, self.H, self.ff, self.V = layers, d, heads, ff, vocab
+        self.glu_epilogue = glu_epilogue
         self.B, self.S, self.T = batch, seq, batch * seq
         self.dev = torch.device(device)
         g = torch.Generator(device=self.dev)
@@ -123,7 +124,10 @@ class Decoder:
                               gb.cross_entropy_params(1.0 / self.T))
 
     def backward_step(self, tape):
-        """One end-to-end backward through the tape: begin, record, backward, end."""
+        """One end-to-end backward through the tape: begin, record, backward, end.  The tape
+        runs with set_glu_epilogue(True): each down projection forms its GLU's local gradients
+        in its input-gradient GEMM (the GLU output's gradient is not kept)."""
+        tape.set_glu_epilogue(self.glu_epilogue)
         tape.begin()
         loss = self.record(tape)
         tape.backward(loss, 0)

@@ -28,7 +28,8 @@ ROPE = {"none": 0, "interleaved": 1, "half": 2}
 SYMBOLS = [
     "gn_last_error", "gn_version", "gn_linear_bwd", "gn_linear_bwd_ws", "gn_linear_workspace_bytes",
     "gn_gemm", "gn_colsum", "gn_act_bwd", "gn_glu_bwd", "gn_glu_linear_bwd", "gn_glu_linear_bwd_ws",
-    "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_ffn_down_glu_bwd", "gn_layernorm_bwd",
+    "gn_glu_workspace_bytes", "gn_glu_proj_bwd", "gn_glu_proj_bwd_ws", "gn_ffn_down_glu_bwd",
+    "gn_ffn_down_glu_bwd_ws", "gn_layernorm_bwd",
     "gn_layernorm_bwd_noalloc", "gn_layernorm_bwd_ex", "gn_layernorm_bwd_ex16", "gn_norm_finish", "gn_rmsnorm_bwd", "gn_rmsnorm_bwd_ex",
     "gn_rmsnorm_bwd_stat", "gn_norm_workspace_bytes", "gn_softmax_bwd", "gn_xent_bwd", "gn_attn_bwd",
     "gn_attn_workspace_bytes", "gn_attn_workspace_bytes_dtype", "gn_attn_bwd_bshd", "gn_attn_fwd", "gn_attn_fwd_mask",
@@ -83,6 +84,9 @@ _SIGS = {
     "gn_glu_workspace_bytes": ([_I, _I, _I, _I], _Z),
     "gn_glu_proj_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
     "gn_ffn_down_glu_bwd": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P], _I),
+    "gn_glu_proj_bwd_ws": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P, _Z, _P], _I),
+    "gn_ffn_down_glu_bwd_ws": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U, _P, _Z, _P],
+                               _I),
     "gn_layernorm_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P, _Z, _P], _I),
     "gn_layernorm_bwd_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _I, _U, _P], _I),
     "gn_rmsnorm_bwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _U, _P, _Z, _P], _I),
@@ -310,8 +314,10 @@ def glu_linear_bwd(kind, dO, gate, up, X, Wg, Wu, need_dx=True, need_db=False, g
     return dX, dWg, dWu, dbg, dbu
 
 
-def glu_proj_bwd(gu, X, Wg, Wu, need_dx=True, need_db=False):
-    """Projection half of the GLU backward from gu = [dGate | dUp] ([M, 2H])."""
+def glu_proj_bwd(gu, X, Wg, Wu, need_dx=True, need_db=False, ws=False):
+    """Projection half of the GLU backward from gu = [dGate | dUp] ([M, 2H]).  ws: False =
+    no workspace (gn_glu_proj_bwd); None = one sized by gn_glu_workspace_bytes, or a uint8
+    tensor (gn_glu_proj_bwd_ws)."""
     M, H2 = gu.shape
     H, K = H2 // 2, X.shape[1]
     dev = gu.device
@@ -320,23 +326,38 @@ def glu_proj_bwd(gu, X, Wg, Wu, need_dx=True, need_db=False):
     dWu = torch.empty((H, K), dtype=torch.float32, device=dev)
     dbg = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
     dbu = torch.empty((H,), dtype=torch.float32, device=dev) if need_db else None
-    _check(lib().gn_glu_proj_bwd(_ptr(gu), _ptr(X), _ptr(Wg), _ptr(Wu), _ptr(dX), _ptr(dWg),
-                                 _ptr(dWu), _ptr(dbg), _ptr(dbu), M, K, H, _dt(gu), 0, _stream()),
-           "gn_glu_proj_bwd")
+    args = (_ptr(gu), _ptr(X), _ptr(Wg), _ptr(Wu), _ptr(dX), _ptr(dWg), _ptr(dWu), _ptr(dbg),
+            _ptr(dbu), M, K, H, _dt(gu), 0)
+    if ws is False:
+        _check(lib().gn_glu_proj_bwd(*args, _stream()), "gn_glu_proj_bwd")
+    else:
+        if ws is None:
+            nb = glu_workspace_bytes(M, K, H, _dt(gu))
+            ws = workspace(nb, dev) if nb else None
+        wsp, wsb = (None, 0) if ws is None else (_ptr(ws), ws.numel() * ws.element_size())
+        _check(lib().gn_glu_proj_bwd_ws(*args, wsp, wsb, _stream()), "gn_glu_proj_bwd_ws")
     return dX, dWg, dWu, dbg, dbu
 
 
-def ffn_down_glu_bwd(kind, dY, A, Wd, gate, up, need_db=False, gu=None, dWd=None):
-    """Down projection backward with the GLU local gradient fused: (gu, dWd, dbd)."""
+def ffn_down_glu_bwd(kind, dY, A, Wd, gate, up, need_db=False, gu=None, dWd=None, ws=False):
+    """Down projection backward with the GLU local gradient fused: (gu, dWd, dbd).  ws as in
+    glu_proj_bwd (sized by gn_linear_workspace_bytes(M, N, H); gn_ffn_down_glu_bwd_ws)."""
     M, N = dY.shape
     H = A.shape[1]
     dev = dY.device
     gu = torch.empty((M, 2 * H), dtype=dY.dtype, device=dev) if gu is None else gu
     dWd = torch.empty((N, H), dtype=torch.float32, device=dev) if dWd is None else dWd
     dbd = torch.empty((N,), dtype=torch.float32, device=dev) if need_db else None
-    _check(lib().gn_ffn_down_glu_bwd(GLU[kind], _ptr(dY), _ptr(A), _ptr(Wd), _ptr(gate), _ptr(up),
-                                     _ptr(gu), _ptr(dWd), _ptr(dbd), M, N, H, _dt(dY), 0,
-                                     _stream()), "gn_ffn_down_glu_bwd")
+    args = (GLU[kind], _ptr(dY), _ptr(A), _ptr(Wd), _ptr(gate), _ptr(up), _ptr(gu), _ptr(dWd),
+            _ptr(dbd), M, N, H, _dt(dY), 0)
+    if ws is False:
+        _check(lib().gn_ffn_down_glu_bwd(*args, _stream()), "gn_ffn_down_glu_bwd")
+    else:
+        if ws is None:
+            nb = linear_workspace_bytes(M, N, H, _dt(dY))
+            ws = workspace(nb, dev) if nb else None
+        wsp, wsb = (None, 0) if ws is None else (_ptr(ws), ws.numel() * ws.element_size())
+        _check(lib().gn_ffn_down_glu_bwd_ws(*args, wsp, wsb, _stream()), "gn_ffn_down_glu_bwd_ws")
     return gu, dWd, dbd
 
 

@@ -171,6 +171,11 @@ size_t gn_glu_workspace_bytes(int M, int K, int H, int dtype);
 int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, const void* Wu, void* dX,
                     void* dWg, void* dWu, void* dbg, void* dbu, int M, int K, int H, int dtype,
                     unsigned flags, void* stream);
+/* gn_glu_proj_bwd with a workspace for the dWg / dWu GEMM's split-K partials, sized by
+ * gn_glu_workspace_bytes(M, K, H, dtype); semantics as gn_linear_bwd_ws. */
+int gn_glu_proj_bwd_ws(const void* gu, const void* X, const void* Wg, const void* Wu, void* dX,
+                       void* dWg, void* dWu, void* dbg, void* dbu, int M, int K, int H,
+                       int dtype, unsigned flags, void* ws, size_t ws_bytes, void* stream);
 
 /* Down-projection backward with the GLU backward fused into its epilogue (a two-node
  * fusion of backward_linear and the fused-*-backward.glsl local gradients):
@@ -182,6 +187,13 @@ int gn_glu_proj_bwd(const void* gu, const void* X, const void* Wg, const void* W
 int gn_ffn_down_glu_bwd(int kind, const void* dY, const void* A, const void* Wd,
                         const void* gate, const void* up, void* gu, void* dWd, void* dbd, int M,
                         int N, int H, int dtype, unsigned flags, void* stream);
+/* gn_ffn_down_glu_bwd with a workspace for dWd's split-K partials, sized by
+ * gn_linear_workspace_bytes(M, N, H, dtype) (dWd is the weight gradient of the Linear
+ * y = A Wd^T); semantics as gn_linear_bwd_ws. */
+int gn_ffn_down_glu_bwd_ws(int kind, const void* dY, const void* A, const void* Wd,
+                           const void* gate, const void* up, void* gu, void* dWd, void* dbd,
+                           int M, int N, int H, int dtype, unsigned flags, void* ws,
+                           size_t ws_bytes, void* stream);
 
 /* ---- normalisation ---------------------------------------------------------------- */
 /* LayerNorm backward, textbook form (autograd_core.py:591-609; fnn-layernorm-backward.glsl

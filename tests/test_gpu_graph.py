@@ -92,8 +92,9 @@ def grads_of(gb, dev, source, tensors, dtype=None):
     return out
 
 
-def eager_grads(gc, gb, dev, model, tensors, dtype=None):
+def eager_grads(gc, gb, dev, model, tensors, dtype=None, glu_epilogue=False):
     tape = gb.create_tape_context(dev)
+    tape.set_glu_epilogue(glu_epilogue)
     tape.begin()
     loss = model.record(gc, gb, tape) if isinstance(model, MLP) else model.record(tape)
     tape.backward(loss, 0)
@@ -248,10 +249,12 @@ def test_capture_errors_leave_the_device_usable(env):
     assert rel_err(want["W1"], ref["W1"]) < 1e-4
 
 
-def test_decoder_backward_graph_replays_match_eager(env):
+@pytest.mark.parametrize("glu_epilogue", [False, True])
+def test_decoder_backward_graph_replays_match_eager(env, glu_epilogue):
     """BASELINE configs[4]'s decoder at a small size (2 layers), captured once: two replays,
     with the logits and targets changed in place between them, equal the eager tape backward
-    (bit for bit; the tied embedding's gradient, which sums fp32 atomics, within 1e-6)."""
+    (bit for bit; the tied embedding's gradient, which sums fp32 atomics, within 1e-6), with
+    and without the GLU's local gradients in the down projection's epilogue."""
     gc, gb, dev = env
     import decoder_tape
     m = decoder_tape.Decoder(layers=2, d=256, heads=4, ff=512, vocab=500, batch=2, seq=128, seed=12)
@@ -262,6 +265,7 @@ def test_decoder_backward_graph_replays_match_eager(env):
                   "bg", "bu", "Wd", "bd"):
             tensors[f"{k}{i}"] = p[k]
     tape = gb.create_tape_context(dev)
+    tape.set_glu_epilogue(glu_epilogue)
     tape.begin()
     g = gc.OpGraph()
     g.capture_backward(tape, m.record(tape), 0)
@@ -278,7 +282,7 @@ def test_decoder_backward_graph_replays_match_eager(env):
         g.execute(dev)
         torch.cuda.synchronize()
         got = grads_of(gb, dev, g, tensors, gb.DTYPE_F32)
-        want = eager_grads(gc, gb, dev, m, tensors, gb.DTYPE_F32)
+        want = eager_grads(gc, gb, dev, m, tensors, gb.DTYPE_F32, glu_epilogue)
         for k in tensors:
             if k == "E":
                 assert rel_err(got[k], want[k]) < 1e-6

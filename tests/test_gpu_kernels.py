@@ -547,6 +547,35 @@ def test_ffn_down_glu_fused(gn, M, N, H, kind):
     assert rel_err(host(dbg), gG.sum(0)) < 1e-4 and rel_err(host(dbu), gU.sum(0)) < 1e-4
 
 
+def test_ffn_down_glu_and_proj_with_workspace(gn):
+    """The workspace forms (gn_ffn_down_glu_bwd_ws, gn_glu_proj_bwd_ws) at the C5 decoder's
+    FFN shapes, where the weight gradients split K over fp32 planes: the GLU-epilogue GEMM and
+    dX are bit-identical to the calls without a workspace (no split on them), the weight and
+    bias gradients agree to fp32 rounding and match float64 on sampled rows."""
+    import torch
+    M, N, H, K = 8192, 768, 3072, 768
+    g = torch.Generator(device="cuda:0").manual_seed(31)
+    b = torch.bfloat16
+    r = lambda *sh, s=1.0: (torch.randn(*sh, device="cuda:0", generator=g) * s).to(b)
+    dY, A, Wd, gate, up = r(M, N, s=0.1), r(M, H), r(N, H, s=0.02), r(M, H), r(M, H)
+    gu0, dWd0, dbd0 = gn.ffn_down_glu_bwd("geglu_up", dY, A, Wd, gate, up, need_db=True)
+    gu1, dWd1, dbd1 = gn.ffn_down_glu_bwd("geglu_up", dY, A, Wd, gate, up, need_db=True, ws=None)
+    X, Wg, Wu = r(M, K), r(H, K, s=0.02), r(H, K, s=0.02)
+    p0 = gn.glu_proj_bwd(gu0, X, Wg, Wu, need_db=True)
+    p1 = gn.glu_proj_bwd(gu0, X, Wg, Wu, need_db=True, ws=None)
+    torch.cuda.synchronize()
+    assert torch.equal(gu0, gu1) and torch.equal(p0[0], p1[0])
+    for a0, a1 in ((dWd0, dWd1), (dbd0, dbd1)) + tuple(zip(p0[1:], p1[1:])):
+        assert rel_err(a1.cpu().numpy(), a0.cpu().numpy()) < 1e-5
+    rows = torch.tensor([0, N // 2, N - 1], device="cuda:0")
+    ref = (dY.t()[rows].double() @ A.double()).cpu().numpy()
+    assert rel_err(dWd1[rows].cpu().numpy(), ref) < 1e-5
+    rows = torch.tensor([1, H - 1], device="cuda:0")
+    ref = (gu0[:, H:].t()[rows].double() @ X.double()).cpu().numpy()
+    assert rel_err(p1[2][rows].cpu().numpy(), ref) < 1e-5
+    assert rel_err(dbd1.cpu().numpy(), dY.double().sum(0).cpu().numpy()) < 1e-5
+
+
 # ---------------------------------------------------------------------------- norms
 def test_layernorm_golden_fp32(gn):
     g = golden("layernorm")

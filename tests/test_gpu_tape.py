@@ -99,8 +99,11 @@ def test_mlp_c1_through_tape(env):
     assert not tape.is_recording()
 
 
-def test_ffn_block_bf16_through_tape(env):
-    """configs[1] structure at a small size: RMSNorm -> FusedGLU(SwiGLU) -> Linear(down)."""
+@pytest.mark.parametrize("glu_epilogue", [False, True])
+def test_ffn_block_bf16_through_tape(env, glu_epilogue):
+    """configs[1] structure at a small size: RMSNorm -> FusedGLU(SwiGLU) -> Linear(down), with
+    and without the GLU's local gradients in the down projection's epilogue (then the GLU
+    output's gradient is not kept; everything upstream of it is unchanged)."""
     gc, gb, dev = env
     r = np.random.default_rng(2)
     M, Dm, Hd = 96, 256, 384
@@ -118,6 +121,7 @@ def test_ffn_block_bf16_through_tape(env):
     y = (a @ Wd.t()).contiguous()
 
     tape = gb.create_tape_context(dev)
+    tape.set_glu_epilogue(glu_epilogue)
     tape.begin()
     nn_ = tape.record_op(gc.OpType.RMSNorm, [gb.tref(x, True)], [gb.tref(n)])
     tape.save_for_backward(nn_, [w.data_ptr(), rstd.data_ptr()])
@@ -134,7 +138,10 @@ def test_ffn_block_bf16_through_tape(env):
     dN = oracle.linear_bwd(dG, h(n), h(Wg))[0] + oracle.linear_bwd(dU, h(n), h(Wu))[0]
     dWg, dWu = oracle.linear_bwd(dG, h(n), h(Wg))[1], oracle.linear_bwd(dU, h(n), h(Wu))[1]
     dx, dw = oracle.rmsnorm_bwd(dN, h(x), h(w), h(rstd))
-    assert rel_err(grad(gb, dev, tape, a), dA) < 2e-2
+    if glu_epilogue:
+        assert tape.get_grad_buffer(a.data_ptr()) == 0
+    else:
+        assert rel_err(grad(gb, dev, tape, a), dA) < 2e-2
     assert rel_err(grad(gb, dev, tape, Wd, gb.DTYPE_F32), dWd) < 2e-2
     assert rel_err(grad(gb, dev, tape, n), dN) < 2e-2
     assert rel_err(grad(gb, dev, tape, Wg, gb.DTYPE_F32), dWg) < 2e-2
@@ -405,9 +412,12 @@ def _decoder_reference(m):
     return E, params, lnf_g, lnf_b
 
 
-def test_decoder_stack_through_tape(env):
+@pytest.mark.parametrize("glu_epilogue", [False, True])
+def test_decoder_stack_through_tape(env, glu_epilogue):
     """BASELINE configs[4] at a small size: embedding, LN, fused QKV + causal attention on
-    the fused layout, residual adds, GEGLU, tied LM head and CE, all through the tape."""
+    the fused layout, residual adds, GEGLU, tied LM head and CE, all through the tape; with
+    the GLU's local gradients formed by the down projection's epilogue (set_glu_epilogue) the
+    GLU output's own gradient is not kept, and without it it is."""
     gc, gb, dev = env
     import decoder_tape
     m = decoder_tape.Decoder(layers=2, d=128, heads=2, ff=256, vocab=300, batch=2, seq=128, seed=7)
@@ -420,6 +430,8 @@ def test_decoder_stack_through_tape(env):
             p[k].copy_((0.05 * torch.randn(p[k].shape, device="cuda:0", generator=g)).bfloat16())
     m.forward()
     tape = gb.create_tape_context(dev)
+    tape.set_glu_epilogue(glu_epilogue)
+    assert tape.glu_epilogue() == glu_epilogue
     tape.begin()
     loss = m.record(tape)
     tape.backward(loss, 0)
@@ -427,6 +439,8 @@ def test_decoder_stack_through_tape(env):
     for i, p in enumerate(m.layers):
         for k in ("Wqkv", "bqkv", "Wo", "ln1_g", "ln2_b", "Wg", "Wu", "bu", "Wd"):
             got[f"{k}{i}"] = grad(gb, dev, tape, p[k], gb.DTYPE_F32)
+        kept = tape.get_grad_buffer(m.acts[i]["h"].data_ptr())
+        assert (kept == 0) == glu_epilogue, (i, kept)
     got["lnf_g"] = grad(gb, dev, tape, m.lnf_g, gb.DTYPE_F32)
     tape.end()
     E, params, lnf_g, _ = _decoder_reference(m)
@@ -449,7 +463,8 @@ def test_decoder_full_size_through_tape(env):
     largest entry is ~5 % of sum_rows |dy * xhat| at this size); with the residual stream and
     its gradient in fp32 the error that reaches it stays within the bf16 bound.  The kernel
     itself is also pinned on its own input: dgamma against the oracle's LayerNorm backward fed
-    the GPU's own upstream dy (<= 1e-4)."""
+    the GPU's own upstream dy (<= 1e-4).  The tape runs as the bench runs it, with the GLU's
+    local gradients formed in the down projection's epilogue."""
     gc, gb, dev = env
     import decoder_tape
     m = decoder_tape.Decoder(seed=9)
@@ -462,6 +477,7 @@ def test_decoder_full_size_through_tape(env):
             p[k].copy_((0.05 * torch.randn(p[k].shape, device="cuda:0", generator=g)).bfloat16())
     m.forward()
     tape = gb.create_tape_context(dev)
+    tape.set_glu_epilogue(m.glu_epilogue)
     tape.begin()
     loss = m.record(tape)
     tape.backward(loss, 0)
