@@ -1113,9 +1113,11 @@ inline TileChoice choose_tile(const GemmDesc& g, bool ta, size_t c_bytes, int ep
     // glu', 16-byte stores) overlaps the other's main loop, which the time model does not
     // describe.  Measured on MI355X, down projection 4096 x 5632 x 2048 with dWd: 225-228 us
     // against 230-236 us for the 256 x 128 / 128 x 256 / 256 x 256 shapes (interleaved runs,
-    // one process).  Short k loops (the decoder's 8192 x 3072 x 768) keep the model's choice:
-    // there the doubled block count's fixed costs weigh more.
-    if (epi == 1 && KT >= 24) return {3, 1};
+    // one process).  The same holds at 12 k-tiles: the decoder's 8192 x 3072 x 768 down
+    // projection (GEGLU in the epilogue) took the 12-layer backward step 8.55 -> 8.39 ms
+    // eager, 8.16 -> 8.09 ms replayed, against the model's 256 x 128.  Shorter k loops keep
+    // the model's choice.
+    if (epi == 1 && KT >= 12) return {3, 1};
     TileChoice best{1, 1};
     double bt = tile_cost(g, ta, c_bytes, epi, 1, 1);
     for (int i = 0; i < 4; ++i) {
