@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "gn_common.h"
+#include "gn_lane.h"
 #include "gn_mfma.h"
 
 namespace gn {
@@ -1679,14 +1680,20 @@ int launch_mfma_bwd(const AttnWs& w, const AttnIO& io, const float* LSE, const f
     const int nb = (S + 127) / 128;
     auto dkdv = kb ? attn_dkdv_mfma<D, kStagesDkdv, NWK, true>
                    : attn_dkdv_mfma<D, kStagesDkdv, NWK, false>;
+    // dQ does not depend on dK/dV: under graph capture at D = 64 it runs beside it on the
+    // device's side stream (a dK/dV and a dQ block fit one CU together, 65 + 35 KB of LDS, so
+    // dQ blocks fill the CUs dK/dV's last round leaves idle; C5 replayed 7.95 -> 7.88 ms).
+    // Eagerly the fork's host cost outweighs it (C5 8.27 -> 8.33 ms), and at D = 128 the
+    // blocks do not share a CU (C3 eager 0.365 -> 0.374 ms), so both run in issue order.
+    SideBySide sb(s, D == 64 ? Fork::kCaptured : Fork::kNever);
     hipLaunchKernelGGL(dkdv, dim3(BH, nb), dim3(64 * NWK), C1::LDS, s, tQ, tK, io.V,
                        io.dO, w.Lsc, w.Di, w.cs, kb, kt, io.dK, io.dV, H, S, Spad, scale, causal,
                        rope_mode);
-    hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, s, tQ, tK,
-                       io.V, io.dO, w.Lsc, w.Di, w.cs, kb, kt, io.dQ, H, S, Spad, scale, causal,
-                       rope_mode);
+    hipLaunchKernelGGL((attn_dq_mfma<D, kStagesDq>), dim3(BH, nb), dim3(256), C2::LDS, sb.side(),
+                       tQ, tK, io.V, io.dO, w.Lsc, w.Di, w.cs, kb, kt, io.dQ, H, S, Spad, scale,
+                       causal, rope_mode);
     GN_LAUNCH_CHECK("gn_attn_bwd (mfma)");
-    return GN_OK;
+    return sb.join();
 }
 
 // head dims of the generic MFMA path (multiples of 32 whose dK/dV column groups of <= 128
