@@ -107,7 +107,9 @@ def pmc_summary(read_dir, write_dir, call):
               128-byte ones as gfx950 documents them); an ordinary request's size is calibrated
               on the add of --calib-copy, which reads exactly 2 GiB;
       writes: TCC_EA0_WRREQ_sum, TCC_EA0_WRREQ_64B_sum (64-byte ones, the rest 32 bytes),
-              checked against the add's 1 GiB.
+              scaled by the add's 1 GiB over what the same formula counts for it (1.0 on
+              most boxes; 0.5 on those whose summed counters read every request twice, where
+              the read calibration also gives half the bytes per request).
     Each launch's per-dispatch mean is summed over the call's launches."""
     import csv
     import glob
@@ -135,13 +137,15 @@ def pmc_summary(read_dir, write_dir, call):
     plain = ca[rd[0]] - ca[rd[1]] - ca[rd[2]]
     bytes_per_req = (2.0 * CALIB_FLOATS * 4 - 32 * ca[rd[1]] - 128 * ca[rd[2]]) / plain
     rbytes = lambda c: (c[rd[0]] - c[rd[1]] - c[rd[2]]) * bytes_per_req + 32 * c[rd[1]] + 128 * c[rd[2]]
-    wbytes = lambda c: (c[wr[0]] - c[wr[1]]) * 32 + 64 * c[wr[1]]
+    wcount = lambda c: (c[wr[0]] - c[wr[1]]) * 32 + 64 * c[wr[1]]
     _, cw = mean(W, "add_kernel", None, wr)
+    wscale = CALIB_FLOATS * 4 / wcount(cw)
+    wbytes = lambda c: wcount(c) * wscale
     lines = [f"call: {call}",
              f"reads: calibration add {ca[rd[0]]:.0f} requests ({ca[rd[1]]:.0f} of 32 B, {ca[rd[2]]:.0f} "
              f"of 128 B) for 2 GiB -> {bytes_per_req:.1f} B per ordinary request",
-             f"writes: calibration add {cw[wr[0]]:.0f} requests ({cw[wr[1]]:.0f} of 64 B) -> "
-             f"{wbytes(cw) / 2**30:.4f} GiB (1 GiB written)"]
+             f"writes: calibration add {cw[wr[0]]:.0f} requests ({cw[wr[1]]:.0f} of 64 B) count "
+             f"{wcount(cw) / 2**30:.4f} GiB for the 1 GiB it writes -> write counts scaled by {wscale:.4f}"]
     total = 0.0
     for pat, grid in CALL_KERNELS[call]:
         n, c = mean(R, pat, grid, rd)
