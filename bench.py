@@ -539,7 +539,8 @@ def bench_decoder(args, torch, gn):
                 {"workload": "C5 12-layer decoder bwd: d768 H12 LN, fused QKV, causal attention, "
                              "GEGLU 3072, tied embedding 32000 + CE; B8 x S1024, bf16",
                  "tokens": m.T, "layers": m.L, "d_model": m.d, "heads": m.H, "ff": m.ff,
-                 "vocab": m.V, "parallelism": "none (1 GPU)"},
+                 "vocab": m.V, "parallelism": "none (1 GPU)",
+                 "tape": "set_glu_epilogue(True)" if m.glu_epilogue else "defaults"},
                 {"kernel": "whole step (GEMMs, attention, norms, CE, adds)", "bound": "mfma",
                  "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                  "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
