@@ -724,6 +724,7 @@ void BackwardEngine::bwd_fused_glu(Node* n) {
                 "FusedGLU backward (projections)");
         glu_node_ = nullptr;
         glu_gu_ = 0;
+        n->grad_output_buffer = 0;  // its output's gradient was never formed
         stats_.shaders_dispatched += 3;
     } else {
         uint64_t gu = alloc_grad((size_t)2 * M * H * es);

@@ -140,6 +140,7 @@ def test_ffn_block_bf16_through_tape(env, glu_epilogue):
     dx, dw = oracle.rmsnorm_bwd(dN, h(x), h(w), h(rstd))
     if glu_epilogue:
         assert tape.get_grad_buffer(a.data_ptr()) == 0
+        assert ng.grad_output_buffer == 0  # no upstream buffer: it started from [dGate | dUp]
     else:
         assert rel_err(grad(gb, dev, tape, a), dA) < 2e-2
     assert rel_err(grad(gb, dev, tape, Wd, gb.DTYPE_F32), dWd) < 2e-2
