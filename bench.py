@@ -107,9 +107,9 @@ def pmc_summary(read_dir, write_dir, call):
               128-byte ones as gfx950 documents them); an ordinary request's size is calibrated
               on the add of --calib-copy, which reads exactly 2 GiB;
       writes: TCC_EA0_WRREQ_sum, TCC_EA0_WRREQ_64B_sum (64-byte ones, the rest 32 bytes),
-              scaled by the add's 1 GiB over what the same formula counts for it (1.0 on
-              most boxes; 0.5 on those whose summed counters read every request twice, where
-              the read calibration also gives half the bytes per request).
+              scaled by the add's 1 GiB over what the same formula counts for it (1, 1/2 or
+              1/3 on the boxes seen: their summed counters read every request once, twice or
+              three times, and the read calibration scales the same way).
     Each launch's per-dispatch mean is summed over the call's launches."""
     import csv
     import glob
