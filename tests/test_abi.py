@@ -89,6 +89,23 @@ def test_invalid_arguments_rejected_without_gpu():
     assert lib.gn_vsa_unpack_project_bwd(None, None, None, None, 8, 8, 100, 4, 0, 0, None, 0, None) == -1
     assert lib.gn_attn_bwd(None, None, None, None, None, None, None, None, None, 1, 1, 8, 300,
                            1.0, 1, 1, 1e4, 4, None, 0, None) == -1
+    # the workspace forms of the two GLU halves validate like their plain forms
+    BF16, F32 = 4, 0
+    assert lib.gn_ffn_down_glu_bwd_ws(0, None, None, None, None, None, None, None, None, 8, 8, 8,
+                                      BF16, 0, None, 0, None) == -1
+    assert "null" in gn_bwd.last_error()
+    one = ctypes.c_void_p(16)  # never dereferenced: the checks below fail before any launch
+    assert lib.gn_ffn_down_glu_bwd_ws(0, one, one, one, one, one, one, one, one, 8, 8, 8, F32, 0,
+                                      None, 0, None) == -1
+    assert "bf16" in gn_bwd.last_error()
+    assert lib.gn_ffn_down_glu_bwd_ws(9, one, one, one, one, one, one, one, one, 8, 8, 8, BF16, 0,
+                                      None, 0, None) == -1
+    assert lib.gn_glu_proj_bwd_ws(None, None, None, None, None, None, None, None, None, 8, 8, 8,
+                                  BF16, 0, None, 0, None) == -1
+    assert lib.gn_glu_proj_bwd_ws(one, one, one, one, None, one, None, None, None, 8, 8, 8, BF16, 0,
+                                  None, 0, None) == -1  # dWg and dWu go together
+    assert lib.gn_glu_proj_bwd_ws(one, one, one, one, None, None, None, None, None, 0, 8, 8, BF16,
+                                  0, None, 0, None) == 0  # no rows: nothing to do
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="libgn_bwd.so not built")
