@@ -1014,9 +1014,7 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
     constexpr size_t smem3 = stage3_b > strips_b ? stage3_b : strips_b;
     constexpr bool fits3 = smem3 <= 160 * 1024;
     static_assert(smem2 <= 160 * 1024, "LDS per CU");
-    // three LDS stages pay off on long k loops; short ones keep the shorter prologue
     const int KT = (g.Ks[0] + (g.nseg > 1 ? g.Ks[1] : 0)) / BK;
-    const bool three = fits3 && KT / g.ksplit >= 48;
     // the bias-summing variant exists for weight gradients only (fp32 C, plain epilogue)
     constexpr bool CAN_BIAS = EPI == 0 && sizeof(CT) == 4;
     const bool bias = CAN_BIAS && g.bias;
@@ -1024,6 +1022,13 @@ int launch_t(const GemmDesc& g, hipStream_t s) {
     // 256 x 256's accumulators do not fit beside a second wave)
     constexpr int PR = (EPI == 0 && BM * BN <= 256 * 128) ? 4 : 0;
     constexpr int NT = 256 + 64 * PR;
+    // three LDS stages wherever they fit for producer-wave tiles (their block holds the CU
+    // alone either way, and the producers issue the extra stage's DMA off the compute waves:
+    // the decoder's short k loops, 12-42 k-tiles, took the 12-layer backward 8.37-8.39 ->
+    // 8.11-8.12 ms eager, 8.05-8.06 -> 7.89 ms replayed against two stages below 48 k-tiles);
+    // for the others three stages pay off on long k loops only (shorter prologue), and the
+    // GLU-epilogue 128 x 128 tiles keep two so that two blocks share a CU
+    const bool three = fits3 && (PR > 0 || KT / g.ksplit >= 48);
     static const bool ok2 = allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, 2, false, PR>, smem2);
     static const bool ok3 =
         fits3 ? allow_lds(gemm_core<TA, TB, CT, BM, BN, EPI, fits3 ? 3 : 2, false, PR>, smem3) : false;
